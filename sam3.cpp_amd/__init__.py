@@ -1,0 +1,191 @@
+"""Python host binding of libsam3mi355.so (the MI355X backend C-ABI of
+include/sam3_mi355.h), used by the tests, bench.py and the smoke check.
+
+The library is the product: every call here goes through its C entry
+points.  If the shared library is missing this module raises instead of
+falling back to anything else.  Device memory comes from torch tensors
+(plumbing only); their data pointers are passed to the C-ABI.
+
+The package directory is named ``sam3.cpp_amd``; load it with
+``load_package()`` from a path, e.g.::
+
+    spec = importlib.util.spec_from_file_location("sam3_cpp_amd", ".../sam3.cpp_amd/__init__.py")
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+import subprocess
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB_PATH = os.path.join(HERE, "libsam3mi355.so")
+HEADER = os.path.join(ROOT, "include", "sam3_mi355.h")
+
+F32, F16, Q4_0, Q4_1, Q8_0, Q8_1 = 0, 1, 2, 3, 8, 9
+ACT_X86, ACT_REF = 0, 1
+TYPE_SIZE = {F32: 4, F16: 2, Q4_0: 18, Q4_1: 20, Q8_0: 34, Q8_1: 36}
+BLCK = {F32: 1, F16: 1, Q4_0: 32, Q4_1: 32, Q8_0: 32, Q8_1: 32}
+
+STATUS = {-4: "INVALID_ARG", -3: "UNSUPPORTED", -2: "ALLOC_FAILED", -1: "FAILED", 0: "SUCCESS", 1: "ABORTED"}
+
+
+class Mi355Error(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"{STATUS.get(status, status)}: {msg}")
+        self.status = status
+
+
+class Tensor(C.Structure):
+    """struct mi355_tensor: the layout fields of a ggml_tensor."""
+    _fields_ = [("type", C.c_int32), ("pad_", C.c_int32), ("ne", C.c_int64 * 4),
+                ("nb", C.c_int64 * 4), ("data", C.c_void_p)]
+
+
+def build(force: bool = False) -> str:
+    """Compile the HIP sources for gfx950 (make -C sam3.cpp_amd)."""
+    args = ["make", "-s", "-C", HERE, f"-j{min(16, os.cpu_count() or 1)}"]
+    if force:
+        subprocess.run(["make", "-s", "-C", HERE, "clean"], check=True)
+    subprocess.run(args, check=True)
+    return LIB_PATH
+
+
+def header_symbols() -> list[str]:
+    """Every function the public header declares."""
+    with open(HEADER) as f:
+        txt = f.read()
+    return sorted(set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(mi355_\w+)\s*\(", txt, flags=re.M)))
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() (make -C sam3.cpp_amd)")
+    L = C.CDLL(LIB_PATH)
+    P, I, F, SZ = C.c_void_p, C.c_int, C.c_float, C.c_size_t
+    T = C.POINTER(Tensor)
+    sig = {
+        "mi355_context_create": (I, [I, P, C.POINTER(P)]),
+        "mi355_context_free": (None, [P]),
+        "mi355_synchronize": (I, [P]),
+        "mi355_status_to_string": (C.c_char_p, [I]),
+        "mi355_last_error": (C.c_char_p, [P]),
+        "mi355_reserve_workspace": (I, [P, SZ]),
+        "mi355_mul_mat_workspace_size": (SZ, [T, T]),
+        "mi355_supports_mul_mat": (I, [T, T, T]),
+        "mi355_mul_mat": (I, [P, T, T, T]),
+        "mi355_quantize_rows": (I, [P, I, I, T, P]),
+        "mi355_mul_mat_block_dots": (I, [P, T, T, P]),
+        "mi355_soft_max_ext": (I, [P, T, T, F, F, T]),
+        "mi355_flash_attn_ext": (I, [P, T, T, T, T, F, F, F, T]),
+        "mi355_profile_enable": (I, [P, I]),
+        "mi355_profile_collect": (I, [P]),
+        "mi355_profile_get": (I, [P, I, C.POINTER(C.c_char_p), C.POINTER(I), C.POINTER(C.c_double)]),
+        "mi355_profile_reset": (None, [P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def row_size(t: int, ne0: int) -> int:
+    return TYPE_SIZE[t] * (ne0 // BLCK[t])
+
+
+def make_tensor(ptr: int, t: int, ne, nb=None) -> Tensor:
+    """mi355_tensor over a device pointer, ggml ne (ne[0] contiguous); nb defaults to contiguous."""
+    ne = list(ne) + [1] * (4 - len(ne))
+    if nb is None:
+        nb = [TYPE_SIZE[t], row_size(t, ne[0])]
+        nb.append(nb[1] * ne[1])
+        nb.append(nb[2] * ne[2])
+    T = Tensor()
+    T.type = t
+    for i in range(4):
+        T.ne[i] = int(ne[i])
+        T.nb[i] = int(nb[i])
+    T.data = ptr
+    return T
+
+
+def from_torch(x, t: int, ne, nb=None) -> Tensor:
+    """mi355_tensor viewing a torch tensor's storage (ggml ne order)."""
+    T = make_tensor(x.data_ptr(), t, ne, nb)
+    T._keep = x
+    return T
+
+
+class Context:
+    """mi355_context on a device and stream (default: torch's current stream)."""
+
+    def __init__(self, device: int = 0, stream: int | None = None):
+        L = lib()
+        if stream is None:
+            import torch
+            stream = torch.cuda.current_stream(device).cuda_stream
+        h = C.c_void_p()
+        st = L.mi355_context_create(device, C.c_void_p(stream), C.byref(h))
+        if st != 0:
+            raise Mi355Error(st, L.mi355_last_error(None).decode())
+        self.h = h
+        self.L = L
+
+    def close(self):
+        if self.h:
+            self.L.mi355_context_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, st: int):
+        if st != 0:
+            raise Mi355Error(st, self.L.mi355_last_error(self.h).decode())
+
+    def synchronize(self):
+        self._check(self.L.mi355_synchronize(self.h))
+
+    def mul_mat(self, src0: Tensor, src1: Tensor, dst: Tensor):
+        self._check(self.L.mi355_mul_mat(self.h, C.byref(src0), C.byref(src1), C.byref(dst)))
+
+    def mul_mat_block_dots(self, src0: Tensor, src1: Tensor, isums_ptr: int):
+        self._check(self.L.mi355_mul_mat_block_dots(self.h, C.byref(src0), C.byref(src1), C.c_void_p(isums_ptr)))
+
+    def quantize_rows(self, t: int, variant: int, src: Tensor, dst_ptr: int):
+        self._check(self.L.mi355_quantize_rows(self.h, t, variant, C.byref(src), C.c_void_p(dst_ptr)))
+
+    def soft_max_ext(self, src: Tensor, dst: Tensor, scale: float):
+        self._check(self.L.mi355_soft_max_ext(self.h, C.byref(src), None, scale, 0.0, C.byref(dst)))
+
+    def profile(self, enable: bool):
+        self._check(self.L.mi355_profile_enable(self.h, 1 if enable else 0))
+
+    def profile_collect(self) -> dict:
+        """{kernel name: (launches, total_ms)} of the launches timed so far; resets the totals."""
+        n = self.L.mi355_profile_collect(self.h)
+        if n < 0:
+            self._check(n)
+        out = {}
+        for i in range(n):
+            name, cnt, ms = C.c_char_p(), C.c_int(), C.c_double()
+            self._check(self.L.mi355_profile_get(self.h, i, C.byref(name), C.byref(cnt), C.byref(ms)))
+            out[name.value.decode()] = (cnt.value, ms.value)
+        self.L.mi355_profile_reset(self.h)
+        return out
+
+    def flash_attn_ext(self, q: Tensor, k: Tensor, v: Tensor, dst: Tensor, scale: float):
+        self._check(self.L.mi355_flash_attn_ext(self.h, C.byref(q), C.byref(k), C.byref(v), None, scale, 0.0, 0.0,
+                                                C.byref(dst)))

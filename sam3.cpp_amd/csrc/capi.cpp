@@ -1,0 +1,449 @@
+// C-ABI of the MI355X backend (include/sam3_mi355.h): ggml-semantics checks,
+// workspace management and kernel dispatch.  Every entry point validates on
+// the host before touching the GPU and reports problems as mi355_status,
+// never by aborting (sam3.cpp returns bool/nullptr on failure, CLAUDE.md:62).
+#include "../../include/sam3_mi355.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "kernels.h"
+
+struct mi355_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    void* ws = nullptr;
+    size_t ws_size = 0;
+    std::string last_error;
+    // kernel timing
+    bool prof = false;
+    struct Pending { const char* name; hipEvent_t a, b; };
+    std::vector<Pending> pending;
+    std::vector<std::string> names;
+    std::map<std::string, std::pair<int, double>> totals;
+};
+
+namespace {
+
+using namespace mi355;
+
+thread_local std::string g_noctx_error;
+
+mi355_status fail(mi355_context* ctx, mi355_status st, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    if (ctx) ctx->last_error = buf;
+    else g_noctx_error = buf;
+    return st;
+}
+
+mi355_status hip_check(mi355_context* ctx, hipError_t e, const char* what) {
+    if (e == hipSuccess) return MI355_STATUS_SUCCESS;
+    return fail(ctx, MI355_STATUS_FAILED, "%s: %s", what, hipGetErrorString(e));
+}
+
+int64_t type_size(int t) {
+    switch (t) {
+        case T_F32: return 4;
+        case T_F16: return 2;
+        case T_Q4_0: return 18;
+        case T_Q4_1: return 20;
+        case T_Q8_0: return 34;
+        case T_Q8_1: return 36;
+        default: return 0;
+    }
+}
+int blck(int t) { return (t == T_F32 || t == T_F16) ? 1 : (type_size(t) ? 32 : 0); }
+int64_t row_size(int t, int64_t ne0) { return blck(t) ? type_size(t) * (ne0 / blck(t)) : 0; }
+int64_t nrows(const mi355_tensor* t) { return t->ne[1] * t->ne[2] * t->ne[3]; }
+
+bool dims_ok(const mi355_tensor* t) {
+    for (int i = 0; i < 4; ++i)
+        if (t->ne[i] < 0 || t->nb[i] < 0) return false;
+    return true;
+}
+
+SrcView view_of(const mi355_tensor* t) {
+    SrcView v;
+    v.data = static_cast<const char*>(t->data);
+    v.type = t->type;
+    for (int i = 0; i < 4; ++i) {
+        v.ne[i] = t->ne[i];
+        v.nb[i] = t->nb[i];
+    }
+    return v;
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+// Workspace carve-up for the quantized path: qs | d | s.
+size_t mmq_ws_bytes(int64_t M, int64_t K, int64_t Z, bool with_sum) {
+    const int64_t nb = K / 32;
+    size_t b = align_up((size_t)(Z * M * K));
+    b += align_up((size_t)(Z * nb * M) * 4);
+    if (with_sum) b += align_up((size_t)(Z * nb * M) * 4);
+    return b;
+}
+
+mi355_status ensure_ws(mi355_context* ctx, size_t bytes) {
+    if (bytes <= ctx->ws_size) return MI355_STATUS_SUCCESS;
+    if (ctx->ws) {
+        // earlier kernels may still read the old buffer
+        hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) return hip_check(ctx, e, "hipStreamSynchronize");
+        (void)hipFree(ctx->ws);
+        ctx->ws = nullptr;
+        ctx->ws_size = 0;
+    }
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return fail(ctx, MI355_STATUS_ALLOC_FAILED, "workspace hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    ctx->ws = p;
+    ctx->ws_size = bytes;
+    return MI355_STATUS_SUCCESS;
+}
+
+// Brackets one launch with events when timing is enabled.
+struct Timed {
+    mi355_context* c;
+    const char* name;
+    hipEvent_t a = nullptr;
+    Timed(mi355_context* ctx, const char* n) : c(ctx), name(n) {
+        if (c && c->prof && hipEventCreate(&a) == hipSuccess) (void)hipEventRecord(a, c->stream);
+    }
+    hipError_t done(hipError_t e) {
+        if (!a) return e;
+        hipEvent_t b = nullptr;
+        if (hipEventCreate(&b) == hipSuccess) {
+            (void)hipEventRecord(b, c->stream);
+            c->pending.push_back({name, a, b});
+        } else {
+            (void)hipEventDestroy(a);
+        }
+        a = nullptr;
+        return e;
+    }
+};
+
+// ggml_mul_mat shape rules (ggml.c ggml_can_mul_mat / ggml_compute_forward_mul_mat)
+// plus what the kernels here implement.
+mi355_status check_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi355_tensor* s1,
+                           const mi355_tensor* d) {
+    if (!s0 || !s1 || !d) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: null tensor");
+    if (!s0->data || !s1->data || !d->data) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: null data pointer");
+    if (!dims_ok(s0) || !dims_ok(s1) || !dims_ok(d)) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: negative ne/nb");
+    const int t0 = s0->type;
+    if (!(t0 == T_F16 || t0 == T_Q8_0 || t0 == T_Q4_0 || t0 == T_Q4_1))
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat: src0 type %d not supported", t0);
+    if (!(s1->type == T_F32 || (s1->type == T_F16 && t0 == T_F16)))
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat: src1 type %d with src0 type %d not supported", s1->type, t0);
+    if (d->type != T_F32) return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat: dst type %d not supported", d->type);
+    const int64_t K = s0->ne[0];
+    if (s1->ne[0] != K) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: K mismatch %lld vs %lld", (long long)K, (long long)s1->ne[0]);
+    if (K % blck(t0) != 0) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: ne0 %lld not a multiple of the block size", (long long)K);
+    if (s0->ne[2] == 0 || s0->ne[3] == 0 || s1->ne[2] % s0->ne[2] != 0 || s1->ne[3] % s0->ne[3] != 0)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: src1 batch dims not a multiple of src0's");
+    if (d->ne[0] != s0->ne[1] || d->ne[1] != s1->ne[1] || d->ne[2] != s1->ne[2] || d->ne[3] != s1->ne[3])
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: dst shape mismatch");
+    if (s0->nb[0] != type_size(t0) || s0->nb[1] < row_size(t0, K))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: src0 rows must be contiguous");
+    if (d->nb[0] != 4) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: dst nb[0] must be 4");
+    if (s1->nb[0] != type_size(s1->type) && s1->type != T_F32)
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat: strided F16 src1 elements");
+    const int64_t lim = (int64_t)1 << 30;
+    if (K >= lim || s0->ne[1] >= lim || s1->ne[1] >= lim || s1->ne[2] * s1->ne[3] > 65535)
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat: dimensions beyond kernel limits");
+    if (t0 == T_F16) {
+        if (K % 8 != 0 || s0->nb[1] % 16 != 0 || (reinterpret_cast<uintptr_t>(s0->data) & 15) ||
+            s0->nb[2] % 16 != 0 || s0->nb[3] % 16 != 0)
+            return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat f16: needs K %% 8 == 0 and 16-byte aligned rows");
+    } else {
+        if (reinterpret_cast<uintptr_t>(s0->data) & 1)
+            return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: src0 data must be 2-byte aligned");
+    }
+    return MI355_STATUS_SUCCESS;
+}
+
+// Prepare the quantized activations for src0's vec_dot_type in the workspace.
+mi355_status prep_act_q8(mi355_context* ctx, const mi355_tensor* s0, const mi355_tensor* s1, ActQ8& a) {
+    const int64_t K = s1->ne[0], M = s1->ne[1], Z = s1->ne[2] * s1->ne[3];
+    const bool with_sum = s0->type == T_Q4_1;
+    mi355_status st = ensure_ws(ctx, mmq_ws_bytes(M, K, Z, with_sum));
+    if (st != MI355_STATUS_SUCCESS) return st;
+    char* p = static_cast<char*>(ctx->ws);
+    a.M = M;
+    a.K = K;
+    a.Z = Z;
+    a.qs = reinterpret_cast<int8_t*>(p);
+    p += align_up((size_t)(Z * M * K));
+    a.d = reinterpret_cast<float*>(p);
+    p += align_up((size_t)(Z * (K / 32) * M) * 4);
+    a.s = with_sum ? reinterpret_cast<float*>(p) : nullptr;
+    Timed tm(ctx, "quantize_mmq");
+    return hip_check(ctx, tm.done(launch_quantize_mmq(view_of(s1), with_sum, a, ctx->stream)), "quantize_mmq launch");
+}
+
+MatW matw_of(const mi355_tensor* s0) {
+    MatW w;
+    w.data = static_cast<const uint8_t*>(s0->data);
+    w.type = s0->type;
+    w.nb1 = s0->nb[1];
+    w.nb2 = s0->nb[2];
+    w.nb3 = s0->nb[3];
+    w.ne2 = s0->ne[2];
+    w.ne3 = s0->ne[3];
+    return w;
+}
+MatD matd_of(const mi355_tensor* d) {
+    MatD o;
+    o.data = static_cast<float*>(d->data);
+    o.nb1 = d->nb[1];
+    o.nb2 = d->nb[2];
+    o.nb3 = d->nb[3];
+    return o;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mi355_status_to_string(mi355_status s) {
+    switch (s) {
+        case MI355_STATUS_SUCCESS: return "GGML status: success";
+        case MI355_STATUS_FAILED: return "GGML status: error (operation failed)";
+        case MI355_STATUS_ALLOC_FAILED: return "GGML status: error (failed to allocate memory)";
+        case MI355_STATUS_ABORTED: return "GGML status: warning (operation aborted)";
+        case MI355_STATUS_UNSUPPORTED: return "MI355 status: error (operation not supported)";
+        case MI355_STATUS_INVALID_ARG: return "MI355 status: error (invalid argument)";
+        default: return "MI355 status: unknown";
+    }
+}
+
+const char* mi355_last_error(const mi355_context* ctx) {
+    return ctx ? ctx->last_error.c_str() : g_noctx_error.c_str();
+}
+
+mi355_status mi355_context_create(int device, void* stream, mi355_context** out) {
+    if (!out) return fail(nullptr, MI355_STATUS_INVALID_ARG, "context_create: out is null");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) return fail(nullptr, MI355_STATUS_FAILED, "no HIP device: %s", hipGetErrorString(e));
+    if (device < 0 || device >= n) return fail(nullptr, MI355_STATUS_INVALID_ARG, "device %d out of range", device);
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return fail(nullptr, MI355_STATUS_FAILED, "hipSetDevice: %s", hipGetErrorString(e));
+    mi355_context* ctx = new mi355_context();
+    ctx->device = device;
+    ctx->stream = static_cast<hipStream_t>(stream);  // NULL: the device's default stream
+    *out = ctx;
+    return MI355_STATUS_SUCCESS;
+}
+
+void mi355_context_free(mi355_context* ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    mi355_profile_reset(ctx);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    delete ctx;
+}
+
+mi355_status mi355_synchronize(mi355_context* ctx) {
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "synchronize: null context");
+    (void)hipSetDevice(ctx->device);
+    return hip_check(ctx, hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+}
+
+mi355_status mi355_reserve_workspace(mi355_context* ctx, size_t bytes) {
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "reserve_workspace: null context");
+    (void)hipSetDevice(ctx->device);
+    return ensure_ws(ctx, bytes);
+}
+
+size_t mi355_mul_mat_workspace_size(const mi355_tensor* s0, const mi355_tensor* s1) {
+    if (!s0 || !s1) return 0;
+    const int64_t K = s1->ne[0], M = s1->ne[1], Z = s1->ne[2] * s1->ne[3];
+    if (s0->type == T_F16) {
+        if (s1->type == T_F16 && s1->nb[0] == 2) return 0;
+        return align_up((size_t)(Z * M * K) * 2);
+    }
+    return mmq_ws_bytes(M, K, Z, s0->type == T_Q4_1);
+}
+
+int mi355_supports_mul_mat(const mi355_tensor* s0, const mi355_tensor* s1, const mi355_tensor* d) {
+    return check_mul_mat(nullptr, s0, s1, d) == MI355_STATUS_SUCCESS;
+}
+
+mi355_status mi355_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi355_tensor* s1,
+                           const mi355_tensor* d) {
+    mi355_status st = check_mul_mat(ctx, s0, s1, d);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "mul_mat: null context");
+    (void)hipSetDevice(ctx->device);
+    const int64_t K = s0->ne[0], N = s0->ne[1], M = s1->ne[1];
+    if (K == 0 || N == 0 || M == 0 || s1->ne[2] * s1->ne[3] == 0) return MI355_STATUS_SUCCESS;
+    if (s0->type == T_F16) {
+        const uint16_t* a = nullptr;
+        int64_t s1e, s2e, s3e;
+        const bool direct = s1->type == T_F16 && s1->nb[0] == 2 && s1->nb[1] % 16 == 0 && s1->nb[2] % 16 == 0 &&
+                            s1->nb[3] % 16 == 0 && (reinterpret_cast<uintptr_t>(s1->data) & 15) == 0;
+        if (direct) {
+            a = static_cast<const uint16_t*>(s1->data);
+            s1e = s1->nb[1] / 2;
+            s2e = s1->nb[2] / 2;
+            s3e = s1->nb[3] / 2;
+        } else {
+            st = ensure_ws(ctx, align_up((size_t)(nrows(s1) * K) * 2));
+            if (st != MI355_STATUS_SUCCESS) return st;
+            uint16_t* buf = static_cast<uint16_t*>(ctx->ws);
+            Timed tc(ctx, "convert_f16");
+            st = hip_check(ctx, tc.done(launch_convert_f16(view_of(s1), buf, ctx->stream)), "convert_f16 launch");
+            if (st != MI355_STATUS_SUCCESS) return st;
+            a = buf;
+            s1e = K;
+            s2e = K * M;
+            s3e = K * M * s1->ne[2];
+        }
+        Timed tg(ctx, "gemm_f16");
+        return hip_check(ctx, tg.done(launch_gemm_f16(matw_of(s0), a, s1e, s2e, s3e, matd_of(d), M, N, K,
+                                                      s1->ne[2], s1->ne[3], ctx->stream)),
+                         "gemm_f16 launch");
+    }
+    ActQ8 a;
+    st = prep_act_q8(ctx, s0, s1, a);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    Timed tq(ctx, s0->type == T_Q8_0 ? "mmq_q8_0" : s0->type == T_Q4_0 ? "mmq_q4_0" : "mmq_q4_1");
+    return hip_check(ctx, tq.done(launch_mmq(matw_of(s0), a, matd_of(d), N, s1->ne[2], s1->ne[3], nullptr,
+                                             ctx->stream)),
+                     "mmq launch");
+}
+
+mi355_status mi355_mul_mat_block_dots(mi355_context* ctx, const mi355_tensor* s0, const mi355_tensor* s1,
+                                      int32_t* isums) {
+    if (!s0 || !s1 || !isums) return fail(ctx, MI355_STATUS_INVALID_ARG, "block_dots: null argument");
+    if (s0->type == T_F16) return fail(ctx, MI355_STATUS_INVALID_ARG, "block_dots: src0 must be a block type");
+    mi355_tensor d{};
+    d.type = T_F32;
+    d.ne[0] = s0->ne[1];
+    d.ne[1] = s1->ne[1];
+    d.ne[2] = s1->ne[2];
+    d.ne[3] = s1->ne[3];
+    d.nb[0] = 4;
+    d.nb[1] = 4 * d.ne[0];
+    d.nb[2] = d.nb[1] * d.ne[1];
+    d.nb[3] = d.nb[2] * d.ne[2];
+    d.data = isums;  // shape check only; the kernel writes isums
+    mi355_status st = check_mul_mat(ctx, s0, s1, &d);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "block_dots: null context");
+    (void)hipSetDevice(ctx->device);
+    ActQ8 a;
+    st = prep_act_q8(ctx, s0, s1, a);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    return hip_check(ctx, launch_mmq(matw_of(s0), a, matd_of(&d), s0->ne[1], s1->ne[2], s1->ne[3], isums,
+                                     ctx->stream),
+                     "mmq(dots) launch");
+}
+
+mi355_status mi355_quantize_rows(mi355_context* ctx, int type, int variant, const mi355_tensor* src, void* dst) {
+    if (!src || !src->data || !dst) return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_rows: null argument");
+    if (!dims_ok(src)) return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_rows: negative ne/nb");
+    if (src->type != T_F32) return fail(ctx, MI355_STATUS_UNSUPPORTED, "quantize_rows: src must be F32");
+    if (!(type == T_Q8_0 || type == T_Q8_1 || type == T_F16))
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "quantize_rows: type %d not supported", type);
+    if (variant != MI355_ACT_X86 && variant != MI355_ACT_REF)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_rows: bad variant %d", variant);
+    if (src->ne[0] % blck(type) != 0)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_rows: ne0 not a multiple of the block size");
+    if (type == T_Q8_1 && (reinterpret_cast<uintptr_t>(dst) & 3))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_rows: q8_1 dst must be 4-byte aligned");
+    if (reinterpret_cast<uintptr_t>(dst) & 1)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_rows: dst must be 2-byte aligned");
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "quantize_rows: null context");
+    (void)hipSetDevice(ctx->device);
+    Timed tq(ctx, "quantize_rows");
+    return hip_check(ctx, tq.done(launch_quantize_ggml(view_of(src), type, variant == MI355_ACT_REF, dst, ctx->stream)),
+                     "quantize launch");
+}
+
+mi355_status mi355_soft_max_ext(mi355_context* ctx, const mi355_tensor* src, const mi355_tensor* mask, float scale,
+                                float max_bias, const mi355_tensor* dst) {
+    if (!src || !dst || !src->data || !dst->data) return fail(ctx, MI355_STATUS_INVALID_ARG, "soft_max: null argument");
+    if (mask || max_bias != 0.0f) return fail(ctx, MI355_STATUS_UNSUPPORTED, "soft_max: mask/ALiBi not supported");
+    if (src->type != T_F32 || dst->type != T_F32) return fail(ctx, MI355_STATUS_UNSUPPORTED, "soft_max: F32 only");
+    for (int i = 0; i < 4; ++i)
+        if (src->ne[i] != dst->ne[i]) return fail(ctx, MI355_STATUS_INVALID_ARG, "soft_max: shape mismatch");
+    if (src->ne[0] > 8192) return fail(ctx, MI355_STATUS_UNSUPPORTED, "soft_max: rows longer than 8192");
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "soft_max: null context");
+    (void)hipSetDevice(ctx->device);
+    Timed ts(ctx, "soft_max");
+    return hip_check(ctx, ts.done(launch_soft_max(view_of(src), scale, static_cast<char*>(dst->data), dst->nb, ctx->stream)),
+                     "soft_max launch");
+}
+
+mi355_status mi355_profile_enable(mi355_context* ctx, int enable) {
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "profile_enable: null context");
+    ctx->prof = enable != 0;
+    return MI355_STATUS_SUCCESS;
+}
+
+int mi355_profile_collect(mi355_context* ctx) {
+    if (!ctx) return (int)fail(nullptr, MI355_STATUS_INVALID_ARG, "profile_collect: null context");
+    (void)hipSetDevice(ctx->device);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return (int)hip_check(ctx, e, "hipStreamSynchronize");
+    for (auto& p : ctx->pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+            auto& t = ctx->totals[p.name];
+            t.first += 1;
+            t.second += ms;
+        }
+        (void)hipEventDestroy(p.a);
+        (void)hipEventDestroy(p.b);
+    }
+    ctx->pending.clear();
+    ctx->names.clear();
+    for (auto& kv : ctx->totals) ctx->names.push_back(kv.first);
+    return (int)ctx->names.size();
+}
+
+mi355_status mi355_profile_get(mi355_context* ctx, int index, const char** name, int* launches, double* total_ms) {
+    if (!ctx || index < 0 || index >= (int)ctx->names.size())
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "profile_get: bad index %d", index);
+    const auto& t = ctx->totals[ctx->names[index]];
+    if (name) *name = ctx->names[index].c_str();
+    if (launches) *launches = t.first;
+    if (total_ms) *total_ms = t.second;
+    return MI355_STATUS_SUCCESS;
+}
+
+void mi355_profile_reset(mi355_context* ctx) {
+    if (!ctx) return;
+    for (auto& p : ctx->pending) {
+        (void)hipEventDestroy(p.a);
+        (void)hipEventDestroy(p.b);
+    }
+    ctx->pending.clear();
+    ctx->totals.clear();
+    ctx->names.clear();
+}
+
+mi355_status mi355_flash_attn_ext(mi355_context* ctx, const mi355_tensor* q, const mi355_tensor* k,
+                                  const mi355_tensor* v, const mi355_tensor* mask, float scale, float max_bias,
+                                  float logit_softcap, const mi355_tensor* dst) {
+    (void)q; (void)k; (void)v; (void)mask; (void)scale; (void)max_bias; (void)logit_softcap; (void)dst;
+    return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: not built yet");
+}
+
+}  // extern "C"

@@ -1,0 +1,187 @@
+// Activation from_float kernels: F32 -> Q8_0 / Q8_1 / F16, bit-exact with
+// ggml-cpu's quantize_row_q8_0 / q8_1 (x86 SIMD and scalar _ref variants)
+// and ggml_cpu_fp32_to_fp16.
+//
+// Work split: 8 lanes per 32-element block, 4 elements per lane, so one
+// wavefront quantizes 8 blocks.  The block's |x| max is reduced across its 8
+// lanes with a butterfly, every lane derives d and id itself (IEEE-correct
+// fp32 division), rounds its 4 values and writes 4 packed int8.
+#include "common.cuh"
+#include "kernels.h"
+
+namespace mi355 {
+
+struct RowAddr {
+    int64_t ne1, ne2;
+    int64_t nb0, nb1, nb2, nb3;
+    __device__ __forceinline__ const char* row(const char* base, int64_t r) const {
+        const int64_t i1 = r % ne1;
+        const int64_t i2 = (r / ne1) % ne2;
+        const int64_t i3 = r / (ne1 * ne2);
+        return base + i1 * nb1 + i2 * nb2 + i3 * nb3;
+    }
+};
+
+__device__ __forceinline__ float ld_elem(const char* p, int type) {
+    return type == T_F32 ? *reinterpret_cast<const float*>(p) : h2f(*reinterpret_cast<const uint16_t*>(p));
+}
+
+// Quantize one 32-block spread over 8 lanes.  Returns the 4 packed int8 of
+// this lane, the fp16 d and (when wanted) the fp16 s; all lanes of the group
+// get d and s.
+template <bool REF>
+__device__ __forceinline__ uint32_t q8_lanes(const float x[4], uint16_t& dh, float& d32, int& isum) {
+    float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+    amax = group_max<8>(amax);
+    const float d = amax / 127.0f;
+    float id;
+    if (REF) id = d != 0.0f ? 1.0f / d : 0.0f;
+    else id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    uint32_t packed = 0;
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float v = x[j] * id;
+        const int q = (int)(REF ? roundf(v) : rintf(v));
+        s += q;
+        packed |= ((uint32_t)q & 0xffu) << (8 * j);
+    }
+    isum = group_sum_i<8>(s);
+    dh = f2h(d);
+    d32 = d;
+    return packed;
+}
+
+template <int OUT, bool REF>  // OUT: T_Q8_0 or T_Q8_1 (ggml layout)
+__global__ __launch_bounds__(256) void quantize_ggml_kernel(const char* __restrict__ src, int stype, RowAddr ra,
+                                                            int64_t ne0, int64_t nblocks, uint8_t* __restrict__ dst) {
+    const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t g = gt >> 3;
+    const int t = threadIdx.x & 7;
+    const bool valid = g < nblocks;
+    const int64_t nbpr = ne0 / QK;
+    const int64_t r = valid ? g / nbpr : 0;
+    const int64_t b = valid ? g % nbpr : 0;
+    float x[4] = {0.f, 0.f, 0.f, 0.f};
+    if (valid) {
+        const char* rp = ra.row(src, r);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = ld_elem(rp + (b * QK + 4 * t + j) * ra.nb0, stype);
+    }
+    uint16_t dh;
+    float d32;
+    int isum;
+    const uint32_t packed = q8_lanes<REF>(x, dh, d32, isum);
+    if (!valid) return;
+    if (OUT == T_Q8_0) {
+        uint8_t* blk = dst + (r * nbpr + b) * (int64_t)sizeof(blk_q8_0);
+        uint16_t* q16 = reinterpret_cast<uint16_t*>(blk + 2 + 4 * t);  // 2-byte aligned
+        q16[0] = (uint16_t)(packed & 0xffffu);
+        q16[1] = (uint16_t)(packed >> 16);
+        if (t == 0) *reinterpret_cast<uint16_t*>(blk) = dh;
+    } else {
+        uint8_t* blk = dst + (r * nbpr + b) * (int64_t)sizeof(blk_q8_1);
+        *reinterpret_cast<uint32_t*>(blk + 4 + 4 * t) = packed;  // 36-byte blocks: 4-byte aligned
+        if (t == 0) {
+            reinterpret_cast<uint16_t*>(blk)[0] = dh;
+            reinterpret_cast<uint16_t*>(blk)[1] = f2h(d32 * (float)isum);
+        }
+    }
+}
+
+// Same arithmetic (x86 variant) into the MMQ layout.
+template <bool WITH_SUM>
+__global__ __launch_bounds__(256) void quantize_mmq_kernel(const char* __restrict__ src, int stype, RowAddr ra,
+                                                           int64_t ne0, int64_t nblocks, int64_t M,
+                                                           int8_t* __restrict__ qs, float* __restrict__ dout,
+                                                           float* __restrict__ sout) {
+    const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t g = gt >> 3;
+    const int t = threadIdx.x & 7;
+    const bool valid = g < nblocks;
+    const int64_t nbpr = ne0 / QK;
+    const int64_t r = valid ? g / nbpr : 0;
+    const int64_t b = valid ? g % nbpr : 0;
+    float x[4] = {0.f, 0.f, 0.f, 0.f};
+    if (valid) {
+        const char* rp = ra.row(src, r);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = ld_elem(rp + (b * QK + 4 * t + j) * ra.nb0, stype);
+    }
+    uint16_t dh;
+    float d32;
+    int isum;
+    const uint32_t packed = q8_lanes<false>(x, dh, d32, isum);
+    if (!valid) return;
+    *reinterpret_cast<uint32_t*>(qs + r * ne0 + b * QK + 4 * t) = packed;
+    if (t == 0) {
+        const int64_t z = r / M, m = r % M;
+        const int64_t si = (z * nbpr + b) * M + m;
+        dout[si] = h2f(dh);
+        if (WITH_SUM) sout[si] = h2f(f2h(d32 * (float)isum));
+    }
+}
+
+__global__ __launch_bounds__(256) void convert_f16_kernel(const char* __restrict__ src, int stype, RowAddr ra,
+                                                          int64_t ne0, int64_t n, uint16_t* __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int64_t r = i / ne0, k = i % ne0;
+    const char* p = ra.row(src, r) + k * ra.nb0;
+    dst[i] = stype == T_F32 ? f2h(*reinterpret_cast<const float*>(p)) : *reinterpret_cast<const uint16_t*>(p);
+}
+
+static RowAddr row_addr(const SrcView& s) {
+    RowAddr ra;
+    ra.ne1 = s.ne[1];
+    ra.ne2 = s.ne[2];
+    ra.nb0 = s.nb[0];
+    ra.nb1 = s.nb[1];
+    ra.nb2 = s.nb[2];
+    ra.nb3 = s.nb[3];
+    return ra;
+}
+
+hipError_t launch_quantize_ggml(const SrcView& src, int type, bool ref_variant, void* dst, hipStream_t st) {
+    const int64_t rows = src.ne[1] * src.ne[2] * src.ne[3];
+    if (type == T_F16) return launch_convert_f16(src, static_cast<uint16_t*>(dst), st);
+    const int64_t nblocks = rows * (src.ne[0] / QK);
+    if (nblocks == 0) return hipSuccess;
+    const dim3 grid((unsigned)((nblocks * 8 + 255) / 256));
+    const RowAddr ra = row_addr(src);
+    uint8_t* out = static_cast<uint8_t*>(dst);
+    if (type == T_Q8_0 && !ref_variant)
+        quantize_ggml_kernel<T_Q8_0, false><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, out);
+    else if (type == T_Q8_0)
+        quantize_ggml_kernel<T_Q8_0, true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, out);
+    else if (!ref_variant)
+        quantize_ggml_kernel<T_Q8_1, false><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, out);
+    else
+        quantize_ggml_kernel<T_Q8_1, true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_mmq(const SrcView& src, bool with_sum, const ActQ8& out, hipStream_t st) {
+    const int64_t rows = src.ne[1] * src.ne[2] * src.ne[3];
+    const int64_t nblocks = rows * (src.ne[0] / QK);
+    if (nblocks == 0) return hipSuccess;
+    const dim3 grid((unsigned)((nblocks * 8 + 255) / 256));
+    const RowAddr ra = row_addr(src);
+    if (with_sum)
+        quantize_mmq_kernel<true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, out.M, out.qs,
+                                                        out.d, out.s);
+    else
+        quantize_mmq_kernel<false><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, out.M, out.qs,
+                                                         out.d, out.s);
+    return hipGetLastError();
+}
+
+hipError_t launch_convert_f16(const SrcView& src, uint16_t* dst, hipStream_t st) {
+    const int64_t n = src.ne[0] * src.ne[1] * src.ne[2] * src.ne[3];
+    if (n == 0) return hipSuccess;
+    const dim3 grid((unsigned)((n + 255) / 256));
+    convert_f16_kernel<<<grid, 256, 0, st>>>(src.data, src.type, row_addr(src), src.ne[0], n, dst);
+    return hipGetLastError();
+}
+
+}  // namespace mi355

@@ -1,0 +1,95 @@
+"""The C-ABI library on the host: it loads, exports every entry point the
+public header declares, and rejects invalid ggml operands with the right
+status before touching the GPU (mirrors the failure modes sam3.cpp maps to
+false at sam3.cpp:1023-1028)."""
+import ctypes as C
+
+import pytest
+
+
+def test_exports_every_header_symbol(mi):
+    L = mi.lib()
+    syms = mi.header_symbols()
+    assert len(syms) >= 12
+    missing = [s for s in syms if not hasattr(L, s)]
+    assert not missing, missing
+
+
+def test_status_strings(mi):
+    L = mi.lib()
+    assert b"success" in L.mi355_status_to_string(0)
+    assert b"not supported" in L.mi355_status_to_string(-3)
+
+
+def mm(mi, t0=8, K=64, N=16, M=8, t1=0, tdst=0, ptr=0x1000):
+    s0 = mi.make_tensor(ptr, t0, [K, N])
+    s1 = mi.make_tensor(ptr, t1, [K, M])
+    d = mi.make_tensor(ptr, tdst, [N, M])
+    return s0, s1, d
+
+
+def status(mi, s0, s1, d):
+    return mi.lib().mi355_mul_mat(None, C.byref(s0), C.byref(s1), C.byref(d))
+
+
+def test_mul_mat_validation(mi):
+    L = mi.lib()
+    s0, s1, d = mm(mi)
+    assert L.mi355_supports_mul_mat(C.byref(s0), C.byref(s1), C.byref(d)) == 1
+    assert status(mi, s0, s1, d) == -4  # valid operands, null context
+    assert b"null context" in L.mi355_last_error(None)
+    # K mismatch
+    s0, s1, d = mm(mi)
+    s1.ne[0] = 96
+    assert status(mi, s0, s1, d) == -4
+    # K not a multiple of the block size
+    s0, s1, d = mm(mi, K=48)
+    assert status(mi, s0, s1, d) == -4
+    assert b"block size" in L.mi355_last_error(None)
+    # unsupported dtypes
+    assert status(mi, *mm(mi, t0=9)) == -3        # q8_1 weights
+    assert status(mi, *mm(mi, t0=8, t1=1)) == -3  # f16 src1 with q8_0 src0
+    assert status(mi, *mm(mi, tdst=1)) == -3      # f16 dst
+    # broadcast ratio
+    s0, s1, d = mm(mi)
+    s0.ne[2] = 3
+    s1.ne[2] = 4
+    d.ne[2] = 4
+    assert status(mi, s0, s1, d) == -4
+    # null data pointer
+    s0, s1, d = mm(mi)
+    s1.data = None
+    assert status(mi, s0, s1, d) == -4
+    # non-contiguous src0 rows
+    s0, s1, d = mm(mi)
+    s0.nb[1] = 10
+    assert status(mi, s0, s1, d) == -4
+    # misaligned f16 rows
+    s0, s1, d = mm(mi, t0=1, K=12)
+    assert status(mi, s0, s1, d) == -3
+
+
+def test_quantize_rows_validation(mi):
+    L = mi.lib()
+    src = mi.make_tensor(0x1000, 0, [64, 4])
+    assert L.mi355_quantize_rows(None, 8, 0, C.byref(src), C.c_void_p(0x2000)) == -4  # null context
+    assert L.mi355_quantize_rows(None, 2, 0, C.byref(src), C.c_void_p(0x2000)) == -3  # q4_0 is not an act type
+    assert L.mi355_quantize_rows(None, 8, 5, C.byref(src), C.c_void_p(0x2000)) == -4  # bad variant
+    src = mi.make_tensor(0x1000, 0, [48, 4])
+    assert L.mi355_quantize_rows(None, 8, 0, C.byref(src), C.c_void_p(0x2000)) == -4  # 48 % 32
+
+
+def test_soft_max_and_fa_validation(mi):
+    L = mi.lib()
+    a = mi.make_tensor(0x1000, 0, [64, 4])
+    b = mi.make_tensor(0x1000, 0, [64, 4])
+    assert L.mi355_soft_max_ext(None, C.byref(a), C.byref(a), 1.0, 0.0, C.byref(b)) == -3  # mask unsupported
+    assert L.mi355_soft_max_ext(None, C.byref(a), None, 1.0, 0.5, C.byref(b)) == -3       # ALiBi unsupported
+    b.ne[1] = 5
+    assert L.mi355_soft_max_ext(None, C.byref(a), None, 1.0, 0.0, C.byref(b)) == -4
+
+
+def test_workspace_size(mi):
+    s0, s1, d = mm(mi, K=1024, N=4736, M=5184)
+    n = mi.lib().mi355_mul_mat_workspace_size(C.byref(s0), C.byref(s1))
+    assert n >= 5184 * 1024 + 5184 * 32 * 4

@@ -1,0 +1,120 @@
+"""GPU mul_mat parity through the C-ABI (mi355_mul_mat) against the oracle's
+ggml-cpu restatement on identical seeded inputs.
+
+Bars (from the path's contract):
+  * integer block dots: bit-exact (mi355_mul_mat_block_dots vs numpy int64);
+  * quantized paths:   |gpu - oracle| <= 1e-5 * absterm
+  * F16:               |gpu - oracle| <= 2e-3 * absterm
+absterm = sum_b |d_w d_a| sum_j |q_w q_a| (+|m_w s_a|), the scale that bounds
+the fp32 rounding of any summation order (outputs near zero make a plain
+per-element relative error meaningless).
+"""
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import absterm, dev, rel_err, run_mul_mat
+
+pytestmark = pytest.mark.gpu
+TOL = {"q8_0": 1e-5, "q4_0": 1e-5, "q4_1": 1e-5, "f16": 2e-3}
+
+
+def check(mi, ctx, orc, tname, M, N, K, seed=0, dims=(1, 1, 1, 1), wstd=0.02, xscale=1.0, sample=None):
+    t = orc.NAME_TYPE[tname]
+    ne02, ne03, ne12, ne13 = dims
+    w = orc.normal(ne03 * ne02 * N * K, seed=seed, stream=1, std=wstd).reshape(-1, K)
+    x = orc.normal(ne13 * ne12 * M * K, seed=seed, stream=2).reshape(ne13, ne12, M, K) * np.float32(xscale)
+    wq = orc.quantize_weights(t, w)
+    out = run_mul_mat(mi, ctx, wq, t, K, N, x, dims)
+    assert np.isfinite(out).all()
+    vt = orc.VEC_DOT_TYPE[t]
+    wq4 = wq.reshape(ne03, ne02, N, -1)
+    worst = 0.0
+    for i13 in range(ne13):
+        for i12 in range(ne12):
+            rows = np.arange(M) if sample is None else sample
+            xs = x[i13, i12, rows]
+            wb = wq4[i13 // (ne13 // ne03), i12 // (ne12 // ne02)]
+            ref = orc.mul_mat(wb, t, K, N, xs[None, None])[0, 0]
+            xq = orc.from_float(vt, xs)
+            scale = absterm(orc, t, wb, K, xq)
+            e = rel_err(out[i13, i12, rows], ref, scale)
+            worst = max(worst, e)
+    assert worst <= TOL[tname], f"{tname} M={M} N={N} K={K}: rel err {worst:.3e}"
+    return worst
+
+
+@pytest.mark.parametrize("tname", ["q8_0", "q4_0", "q4_1", "f16"])
+@pytest.mark.parametrize("M,N,K", [(1, 1, 32), (77, 65, 96), (128, 128, 128), (200, 300, 1024), (33, 130, 4736)])
+def test_mul_mat_small(mi, ctx, orc, tname, M, N, K):
+    check(mi, ctx, orc, tname, M, N, K)
+
+
+@pytest.mark.parametrize("tname", ["q8_0", "q4_0", "q4_1", "f16"])
+def test_mul_mat_broadcast(mi, ctx, orc, tname):
+    # src0 [K, N, 2, 1] broadcast over src1 [K, M, 4, 3]
+    check(mi, ctx, orc, tname, 40, 72, 256, seed=3, dims=(2, 1, 4, 3))
+
+
+@pytest.mark.parametrize("tname", ["q8_0", "q4_0", "q4_1"])
+@pytest.mark.parametrize("K", [96, 1024])
+def test_block_dots_bit_exact(mi, ctx, orc, tname, K):
+    t = orc.NAME_TYPE[tname]
+    M, N = 70, 45
+    w = orc.normal(N * K, seed=4, stream=1, std=0.02).reshape(N, K)
+    x = orc.normal(M * K, seed=4, stream=2).reshape(M, K)
+    wq = orc.quantize_weights(t, w)
+    nb = K // 32
+    isums = torch.zeros(M * N * nb, dtype=torch.int32, device="cuda")
+    s0 = mi.from_torch(dev(wq), t, [K, N])
+    s1 = mi.from_torch(dev(x), mi.F32, [K, M])
+    ctx.mul_mat_block_dots(s0, s1, isums.data_ptr())
+    ctx.synchronize()
+    got = isums.cpu().numpy().reshape(M, N, nb)
+    wv, _, _ = orc.decode_blocks(t, wq, K)
+    xv, _, _ = orc.decode_blocks(orc.VEC_DOT_TYPE[t], orc.from_float(orc.VEC_DOT_TYPE[t], x), K)
+    ref = np.einsum("mbj,nbj->mnb", xv.reshape(M, nb, 32).astype(np.int64), wv.reshape(N, nb, 32).astype(np.int64))
+    assert np.array_equal(got, ref)
+
+
+def test_integer_exact_through_product_path(mi, ctx, orc):
+    """Scales of exactly 1.0 on both sides make the fp32 result an exact
+    integer: activations are integers in [-127,127] with |127| in every block
+    (d_a = 1, id = 1), weights are Q8_0 blocks with d = 1.0.  The GPU output
+    must equal sum_b isum_b bit for bit."""
+    M, N, K = 96, 80, 1024
+    rng = np.random.default_rng(11)
+    x = rng.integers(-127, 128, size=(M, K)).astype(np.float32)
+    x.reshape(M, K // 32, 32)[:, :, 5] = 127.0
+    q = rng.integers(-127, 128, size=(N, K)).astype(np.int8)
+    wq = np.zeros((N, K // 32, 34), dtype=np.uint8)
+    wq[:, :, 0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    wq[:, :, 2:] = q.reshape(N, K // 32, 32).view(np.uint8)
+    out = run_mul_mat(mi, ctx, wq.reshape(N, -1), orc.Q8_0, K, N, x[None, None])[0, 0]
+    exact = x.astype(np.int64) @ q.astype(np.int64).T
+    assert np.abs(exact).max() < 2**24
+    assert np.array_equal(out, exact.astype(np.float32))
+
+
+def test_f16_src1_direct(mi, ctx, orc):
+    """F16 src1 (the explicit attention form multiplies f16 K by f16 Q)."""
+    K, N, M = 64, 200, 150
+    w = orc.normal(N * K, seed=5, stream=1).reshape(N, K).astype(np.float16)
+    x = orc.normal(M * K, seed=5, stream=2).reshape(M, K).astype(np.float16)
+    out = run_mul_mat(mi, ctx, w.view(np.uint16), orc.F16, K, N, x[None, None])[0, 0]
+    ref = orc.mul_mat(w.view(np.uint16), orc.F16, K, N, x.view(np.uint16)[None, None], src1_type=orc.F16)[0, 0]
+    scale = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    assert rel_err(out, ref, scale) <= 2e-3
+
+
+@pytest.mark.parametrize("tname", ["q8_0", "q4_0", "q4_1", "f16"])
+@pytest.mark.parametrize("name,N,K", [("qkv", 3072, 1024), ("proj", 1024, 1024), ("fc1", 4736, 1024),
+                                      ("fc2", 1024, 4736)])
+def test_mul_mat_vit_shapes(mi, ctx, orc, tname, name, N, K):
+    """SAM3 ViT block linear set at M = 5184 tokens (72x72), weights
+    N(0,0.02), activations N(0,1), seed 0; 192 sampled token rows compared
+    against the oracle (all N columns)."""
+    sample = np.random.default_rng(0).choice(5184, size=192, replace=False)
+    sample.sort()
+    sample[0], sample[-1] = 0, 5183
+    check(mi, ctx, orc, tname, 5184, N, K, seed=0, sample=sample)
