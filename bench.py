@@ -32,6 +32,7 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 M_TOK = 5184
 LINEARS = [("qkv", 3072, 1024), ("proj", 1024, 1024), ("fc1", 4736, 1024), ("fc2", 1024, 4736)]
 TYPES = ["q8_0", "q4_0"]
+ALL_TYPES = ["q8_0", "q4_0", "q4_1", "f16"]
 
 
 def load_pkg():
@@ -53,6 +54,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--op", default=None,
+                    help="profile mode: run only TYPE/LINEAR (e.g. q8_0/fc1) --reps times and print its kernel times")
+    ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -73,7 +77,10 @@ def main():
     xs = {1024: torch.from_numpy(x1024).to(dev), 4736: torch.from_numpy(x4736).to(dev)}
     calls = []  # (tname, lname, N, K, s0, s1, d)
     host_w = {}
-    for ti, tname in enumerate(TYPES):
+    types = TYPES
+    if args.op:
+        types = [args.op.split("/")[0]]
+    for ti, tname in enumerate(types):
         t = orc.NAME_TYPE[tname]
         for li, (lname, N, K) in enumerate(LINEARS):
             w = orc.normal(N * K, seed=0, stream=10 + li, std=0.02).reshape(N, K)
@@ -85,6 +92,19 @@ def main():
             s1 = mi.from_torch(xs[K], mi.F32, [K, M_TOK])
             d = mi.from_torch(dst, mi.F32, [N, M_TOK])
             calls.append((tname, lname, N, K, s0, s1, d))
+    if args.op:
+        c = [c for c in calls if f"{c[0]}/{c[1]}" == args.op][0]
+        for _ in range(3):
+            ctx.mul_mat(c[4], c[5], c[6])
+        torch.cuda.synchronize()
+        ctx.profile(True)
+        for _ in range(args.reps):
+            ctx.mul_mat(c[4], c[5], c[6])
+        prof = ctx.profile_collect()
+        print(json.dumps({"op": args.op, "reps": args.reps,
+                          "kernel_us": {k: round(1e3 * v[1] / v[0], 2) for k, v in prof.items()}}), flush=True)
+        ctx.close()
+        return
     ops_by_type = {tn: sum(2.0 * M_TOK * N * K for (_, N, K) in LINEARS) for tn in TYPES}
     step_ops = sum(ops_by_type.values())
 

@@ -64,7 +64,6 @@ int64_t type_size(int t) {
 }
 int blck(int t) { return (t == T_F32 || t == T_F16) ? 1 : (type_size(t) ? 32 : 0); }
 int64_t row_size(int t, int64_t ne0) { return blck(t) ? type_size(t) * (ne0 / blck(t)) : 0; }
-int64_t nrows(const mi355_tensor* t) { return t->ne[1] * t->ne[2] * t->ne[3]; }
 
 bool dims_ok(const mi355_tensor* t) {
     for (int i = 0; i < 4; ++i)
@@ -86,15 +85,53 @@ SrcView view_of(const mi355_tensor* t) {
 constexpr size_t kAlign = 256;
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
-// Workspace carve-up for the quantized path: qs | d | s.
-size_t mmq_ws_bytes(int64_t M, int64_t K, int64_t Z, bool with_sum) {
-    const int64_t nb = K / 32;
-    size_t b = align_up((size_t)(Z * M * K));
-    b += align_up((size_t)(Z * nb * M) * 4);
-    if (with_sum) b += align_up((size_t)(Z * nb * M) * 4);
-    return b;
+MatW matw_of(const mi355_tensor* s0) {
+    MatW w;
+    w.data = static_cast<const uint8_t*>(s0->data);
+    w.type = s0->type;
+    w.nb1 = s0->nb[1];
+    w.nb2 = s0->nb[2];
+    w.nb3 = s0->nb[3];
+    w.ne2 = s0->ne[2];
+    w.ne3 = s0->ne[3];
+    return w;
+}
+MatD matd_of(const mi355_tensor* d) {
+    MatD o;
+    o.data = static_cast<float*>(d->data);
+    o.nb1 = d->nb[1];
+    o.nb2 = d->nb[2];
+    o.nb3 = d->nb[3];
+    return o;
 }
 
+bool f16_src1_direct(const mi355_tensor* s1) {
+    return s1->type == T_F16 && s1->nb[0] == 2 && s1->nb[1] % 16 == 0 && s1->nb[2] % 16 == 0 && s1->nb[3] % 16 == 0 &&
+           (reinterpret_cast<uintptr_t>(s1->data) & 15) == 0;
+}
+
+// Workspace carve-up of one mul_mat: activation operand (fp16 quants or an
+// F16 copy of src1) | scales | Q8_1 sums | 4-byte-pitch weight copy (only
+// for weight rows that are not 4-byte aligned).
+struct MmPlan {
+    size_t q = 0, d = 0, s = 0, align = 0;
+    size_t total() const { return q + d + s + align; }
+};
+
+MmPlan mm_plan(const mi355_tensor* s0, const mi355_tensor* s1) {
+    MmPlan pl;
+    const int64_t K = s1->ne[0], M = s1->ne[1], Z = s1->ne[2] * s1->ne[3];
+    if (s0->type == T_F16) {
+        if (!f16_src1_direct(s1)) pl.q = align_up((size_t)(Z * M * K) * 2);
+        return pl;
+    }
+    const int64_t Mp = mmq_scale_rows(M);
+    pl.q = align_up((size_t)(Z * M * K) * 2);
+    pl.d = align_up((size_t)(Z * (K / 32) * Mp) * 2);
+    if (s0->type == T_Q4_1) pl.s = pl.d;
+    pl.align = align_up(mmq_align_bytes(matw_of(s0), s0->ne[1], K));
+    return pl;
+}
 mi355_status ensure_ws(mi355_context* ctx, size_t bytes) {
     if (bytes <= ctx->ws_size) return MI355_STATUS_SUCCESS;
     if (ctx->ws) {
@@ -174,43 +211,27 @@ mi355_status check_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
     return MI355_STATUS_SUCCESS;
 }
 
-// Prepare the quantized activations for src0's vec_dot_type in the workspace.
-mi355_status prep_act_q8(mi355_context* ctx, const mi355_tensor* s0, const mi355_tensor* s1, ActQ8& a) {
-    const int64_t K = s1->ne[0], M = s1->ne[1], Z = s1->ne[2] * s1->ne[3];
+// Quantize src1 for src0's vec_dot_type into the workspace (x86 from_float).
+// The workspace must already hold mm_plan(s0, s1).total() bytes.
+mi355_status prep_act_q8(mi355_context* ctx, const mi355_tensor* s0, const mi355_tensor* s1, const MmPlan& pl,
+                         ActF16& a) {
+    const int64_t K = s1->ne[0], M = s1->ne[1];
     const bool with_sum = s0->type == T_Q4_1;
-    mi355_status st = ensure_ws(ctx, mmq_ws_bytes(M, K, Z, with_sum));
-    if (st != MI355_STATUS_SUCCESS) return st;
     char* p = static_cast<char*>(ctx->ws);
+    uint16_t* q = reinterpret_cast<uint16_t*>(p);
+    uint16_t* d = reinterpret_cast<uint16_t*>(p + pl.q);
+    uint16_t* sm = with_sum ? reinterpret_cast<uint16_t*>(p + pl.q + pl.d) : nullptr;
+    a.q = q;
+    a.s1 = K;
+    a.s2 = K * M;
+    a.s3 = K * M * s1->ne[2];
+    a.d = d;
+    a.s = sm;
     a.M = M;
     a.K = K;
-    a.Z = Z;
-    a.qs = reinterpret_cast<int8_t*>(p);
-    p += align_up((size_t)(Z * M * K));
-    a.d = reinterpret_cast<float*>(p);
-    p += align_up((size_t)(Z * (K / 32) * M) * 4);
-    a.s = with_sum ? reinterpret_cast<float*>(p) : nullptr;
     Timed tm(ctx, "quantize_mmq");
-    return hip_check(ctx, tm.done(launch_quantize_mmq(view_of(s1), with_sum, a, ctx->stream)), "quantize_mmq launch");
-}
-
-MatW matw_of(const mi355_tensor* s0) {
-    MatW w;
-    w.data = static_cast<const uint8_t*>(s0->data);
-    w.type = s0->type;
-    w.nb1 = s0->nb[1];
-    w.nb2 = s0->nb[2];
-    w.nb3 = s0->nb[3];
-    w.ne2 = s0->ne[2];
-    w.ne3 = s0->ne[3];
-    return w;
-}
-MatD matd_of(const mi355_tensor* d) {
-    MatD o;
-    o.data = static_cast<float*>(d->data);
-    o.nb1 = d->nb[1];
-    o.nb2 = d->nb[2];
-    o.nb3 = d->nb[3];
-    return o;
+    return hip_check(ctx, tm.done(launch_quantize_mmq(view_of(s1), with_sum, mmq_scale_rows(M), q, d, sm, ctx->stream)),
+                     "quantize_mmq launch");
 }
 
 }  // namespace
@@ -272,12 +293,8 @@ mi355_status mi355_reserve_workspace(mi355_context* ctx, size_t bytes) {
 
 size_t mi355_mul_mat_workspace_size(const mi355_tensor* s0, const mi355_tensor* s1) {
     if (!s0 || !s1) return 0;
-    const int64_t K = s1->ne[0], M = s1->ne[1], Z = s1->ne[2] * s1->ne[3];
-    if (s0->type == T_F16) {
-        if (s1->type == T_F16 && s1->nb[0] == 2) return 0;
-        return align_up((size_t)(Z * M * K) * 2);
-    }
-    return mmq_ws_bytes(M, K, Z, s0->type == T_Q4_1);
+    if (s0->type != T_F16 && s0->type != T_Q8_0 && s0->type != T_Q4_0 && s0->type != T_Q4_1) return 0;
+    return mm_plan(s0, s1).total();
 }
 
 int mi355_supports_mul_mat(const mi355_tensor* s0, const mi355_tensor* s1, const mi355_tensor* d) {
@@ -292,38 +309,37 @@ mi355_status mi355_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
     (void)hipSetDevice(ctx->device);
     const int64_t K = s0->ne[0], N = s0->ne[1], M = s1->ne[1];
     if (K == 0 || N == 0 || M == 0 || s1->ne[2] * s1->ne[3] == 0) return MI355_STATUS_SUCCESS;
+    const MmPlan pl = mm_plan(s0, s1);
+    st = ensure_ws(ctx, pl.total());
+    if (st != MI355_STATUS_SUCCESS) return st;
+    ActF16 a;
     if (s0->type == T_F16) {
-        const uint16_t* a = nullptr;
-        int64_t s1e, s2e, s3e;
-        const bool direct = s1->type == T_F16 && s1->nb[0] == 2 && s1->nb[1] % 16 == 0 && s1->nb[2] % 16 == 0 &&
-                            s1->nb[3] % 16 == 0 && (reinterpret_cast<uintptr_t>(s1->data) & 15) == 0;
-        if (direct) {
-            a = static_cast<const uint16_t*>(s1->data);
-            s1e = s1->nb[1] / 2;
-            s2e = s1->nb[2] / 2;
-            s3e = s1->nb[3] / 2;
+        a.M = M;
+        a.K = K;
+        a.d = a.s = nullptr;
+        if (f16_src1_direct(s1)) {
+            a.q = s1->data;
+            a.s1 = s1->nb[1] / 2;
+            a.s2 = s1->nb[2] / 2;
+            a.s3 = s1->nb[3] / 2;
         } else {
-            st = ensure_ws(ctx, align_up((size_t)(nrows(s1) * K) * 2));
-            if (st != MI355_STATUS_SUCCESS) return st;
             uint16_t* buf = static_cast<uint16_t*>(ctx->ws);
             Timed tc(ctx, "convert_f16");
             st = hip_check(ctx, tc.done(launch_convert_f16(view_of(s1), buf, ctx->stream)), "convert_f16 launch");
             if (st != MI355_STATUS_SUCCESS) return st;
-            a = buf;
-            s1e = K;
-            s2e = K * M;
-            s3e = K * M * s1->ne[2];
+            a.q = buf;
+            a.s1 = K;
+            a.s2 = K * M;
+            a.s3 = K * M * s1->ne[2];
         }
-        Timed tg(ctx, "gemm_f16");
-        return hip_check(ctx, tg.done(launch_gemm_f16(matw_of(s0), a, s1e, s2e, s3e, matd_of(d), M, N, K,
-                                                      s1->ne[2], s1->ne[3], ctx->stream)),
-                         "gemm_f16 launch");
+    } else {
+        st = prep_act_q8(ctx, s0, s1, pl, a);
+        if (st != MI355_STATUS_SUCCESS) return st;
     }
-    ActQ8 a;
-    st = prep_act_q8(ctx, s0, s1, a);
-    if (st != MI355_STATUS_SUCCESS) return st;
-    Timed tq(ctx, s0->type == T_Q8_0 ? "mmq_q8_0" : s0->type == T_Q4_0 ? "mmq_q4_0" : "mmq_q4_1");
-    return hip_check(ctx, tq.done(launch_mmq(matw_of(s0), a, matd_of(d), N, s1->ne[2], s1->ne[3], nullptr,
+    void* align_buf = pl.align ? static_cast<char*>(ctx->ws) + pl.q + pl.d + pl.s : nullptr;
+    const char* kname = s0->type == T_F16 ? "mmq_f16" : s0->type == T_Q8_0 ? "mmq_q8_0" : s0->type == T_Q4_0 ? "mmq_q4_0" : "mmq_q4_1";
+    Timed tq(ctx, kname);
+    return hip_check(ctx, tq.done(launch_mmq(matw_of(s0), a, matd_of(d), N, s1->ne[2], s1->ne[3], nullptr, align_buf,
                                              ctx->stream)),
                      "mmq launch");
 }
@@ -347,10 +363,14 @@ mi355_status mi355_mul_mat_block_dots(mi355_context* ctx, const mi355_tensor* s0
     if (st != MI355_STATUS_SUCCESS) return st;
     if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "block_dots: null context");
     (void)hipSetDevice(ctx->device);
-    ActQ8 a;
-    st = prep_act_q8(ctx, s0, s1, a);
+    const MmPlan pl = mm_plan(s0, s1);
+    st = ensure_ws(ctx, pl.total());
     if (st != MI355_STATUS_SUCCESS) return st;
-    return hip_check(ctx, launch_mmq(matw_of(s0), a, matd_of(&d), s0->ne[1], s1->ne[2], s1->ne[3], isums,
+    ActF16 a;
+    st = prep_act_q8(ctx, s0, s1, pl, a);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    void* align_buf = pl.align ? static_cast<char*>(ctx->ws) + pl.q + pl.d + pl.s : nullptr;
+    return hip_check(ctx, launch_mmq(matw_of(s0), a, matd_of(&d), s0->ne[1], s1->ne[2], s1->ne[3], isums, align_buf,
                                      ctx->stream),
                      "mmq(dots) launch");
 }

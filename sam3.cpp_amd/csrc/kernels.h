@@ -19,21 +19,28 @@ struct SrcView {
     int64_t nb[4];
 };
 
-// Quantized-activation layout consumed by the MMQ kernel: for z in
-// [0, Z), rows m in [0, M): qs[(z*M + m)*K + k] int8, scale
-// d[(z*nb + b)*M + m] fp32 (the fp16 d widened), and for Q8_1 the block sum
-// term s[(z*nb + b)*M + m] fp32 (the fp16 s widened).
-struct ActQ8 {
-    int8_t* qs;
-    float* d;
-    float* s;
-    int64_t M, K, Z;
+// Activation operand of the MFMA GEMM kernel, fp16 rows of K halves:
+// q[i12*s2 + i13*s3 + m*s1 + k] (strides in halves).  On the quantized path
+// these are the Q8 quants as exact fp16 integers, contiguous ([Z][M][K]),
+// with the per-block scale d[(z*nb + b)*Mp + m] and, for Q8_1, the block sum
+// term s[(z*nb + b)*Mp + m], both fp16 as ggml stores them; Mp =
+// mmq_scale_rows(M) pads the scale rows so every 128-row slice is a dword
+// aligned DMA.  On the F16 path q holds src1 converted to F16 (or src1
+// itself) and d, s are unused.
+struct ActF16 {
+    const void* q;
+    int64_t s1, s2, s3;
+    const void* d;
+    const void* s;
+    int64_t M, K;
 };
 
 // ggml from_float into contiguous ggml rows: type 8 (Q8_0), 9 (Q8_1), 1 (F16).
 hipError_t launch_quantize_ggml(const SrcView& src, int type, bool ref_variant, void* dst, hipStream_t st);
-// from_float into the MMQ layout (q8_0 semantics; with_sum adds the Q8_1 s).
-hipError_t launch_quantize_mmq(const SrcView& src, bool with_sum, const ActQ8& out, hipStream_t st);
+// from_float (x86 variant, Q8_0 or with_sum Q8_1 semantics) into the ActF16
+// quantized layout: q [rows][K] fp16, d and s [Z][nb][Mp] fp16, M = ne[1].
+hipError_t launch_quantize_mmq(const SrcView& src, bool with_sum, int64_t Mp, uint16_t* q, uint16_t* d, uint16_t* s,
+                               hipStream_t st);
 // F32/F16 strided rows -> contiguous F16 rows [rows][ne0] (round to nearest even).
 hipError_t launch_convert_f16(const SrcView& src, uint16_t* dst, hipStream_t st);
 
@@ -48,15 +55,16 @@ struct MatD {  // dst F32
     int64_t nb1, nb2, nb3;  // bytes
 };
 
-// dst = W^T . act for quantized W (Q8_0 / Q4_0 / Q4_1); ne12/ne13 batch dims.
-// When dots != nullptr the kernel writes the per-block int32 dots instead.
-hipError_t launch_mmq(const MatW& w, const ActQ8& a, const MatD& d, int64_t N, int64_t ne12, int64_t ne13,
-                      int32_t* dots, hipStream_t st);
-
-// dst = W^T . A for F16 W and F16 activations A (rows of K halves with
-// element strides a_nb1/a_nb2/a_nb3, in halves).
-hipError_t launch_gemm_f16(const MatW& w, const uint16_t* a, int64_t a_s1, int64_t a_s2, int64_t a_s3,
-                           const MatD& d, int64_t M, int64_t N, int64_t K, int64_t ne12, int64_t ne13, hipStream_t st);
+// dst = W^T . A on MFMA for W in Q8_0 / Q4_0 / Q4_1 (A = quantized
+// activations) or F16 (A = F16 activations); ne12/ne13 batch dims.  With
+// dots != nullptr (block types only) the kernel writes the exact per-block
+// int32 dots [z][m][n][b] instead of dst.
+hipError_t launch_mmq(const MatW& w, const ActF16& a, const MatD& d, int64_t N, int64_t ne12, int64_t ne13,
+                      int32_t* dots, void* align_buf, hipStream_t st);
+// Padded row count of the activation scale arrays.
+int64_t mmq_scale_rows(int64_t M);
+// Bytes of the 4-byte-pitch weight copy launch_mmq needs (0 when rows are aligned).
+size_t mmq_align_bytes(const MatW& w, int64_t N, int64_t K);
 
 // Row softmax of scale*x (F32, strided rows) into dst (F32, strided rows).
 hipError_t launch_soft_max(const SrcView& src, float scale, char* dst, const int64_t dnb[4], hipStream_t st);

@@ -89,12 +89,13 @@ __global__ __launch_bounds__(256) void quantize_ggml_kernel(const char* __restri
     }
 }
 
-// Same arithmetic (x86 variant) into the MMQ layout.
+// Same arithmetic (x86 variant) into the MFMA operand layout: quants as fp16
+// integers (exact), scale and Q8_1 sum as the fp16 values ggml would store.
 template <bool WITH_SUM>
 __global__ __launch_bounds__(256) void quantize_mmq_kernel(const char* __restrict__ src, int stype, RowAddr ra,
-                                                           int64_t ne0, int64_t nblocks, int64_t M,
-                                                           int8_t* __restrict__ qs, float* __restrict__ dout,
-                                                           float* __restrict__ sout) {
+                                                           int64_t ne0, int64_t nblocks, int64_t M, int64_t Mp,
+                                                           uint16_t* __restrict__ qout, uint16_t* __restrict__ dout,
+                                                           uint16_t* __restrict__ sout) {
     const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t g = gt >> 3;
     const int t = threadIdx.x & 7;
@@ -105,20 +106,32 @@ __global__ __launch_bounds__(256) void quantize_mmq_kernel(const char* __restric
     float x[4] = {0.f, 0.f, 0.f, 0.f};
     if (valid) {
         const char* rp = ra.row(src, r);
+        if (stype == T_F32 && ra.nb0 == 4 && ((reinterpret_cast<uintptr_t>(rp) & 15) == 0)) {
+            const v4f v = *reinterpret_cast<const v4f*>(rp + (b * QK + 4 * t) * 4);
+            x[0] = v[0]; x[1] = v[1]; x[2] = v[2]; x[3] = v[3];
+        } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) x[j] = ld_elem(rp + (b * QK + 4 * t + j) * ra.nb0, stype);
+            for (int j = 0; j < 4; ++j) x[j] = ld_elem(rp + (b * QK + 4 * t + j) * ra.nb0, stype);
+        }
     }
     uint16_t dh;
     float d32;
     int isum;
     const uint32_t packed = q8_lanes<false>(x, dh, d32, isum);
     if (!valid) return;
-    *reinterpret_cast<uint32_t*>(qs + r * ne0 + b * QK + 4 * t) = packed;
+    uint32_t hq[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int q0 = (int)(int8_t)((packed >> (16 * j)) & 0xffu);
+        const int q1 = (int)(int8_t)((packed >> (16 * j + 8)) & 0xffu);
+        hq[j] = (uint32_t)f2h((float)q0) | ((uint32_t)f2h((float)q1) << 16);
+    }
+    *reinterpret_cast<uint2*>(qout + r * ne0 + b * QK + 4 * t) = make_uint2(hq[0], hq[1]);
     if (t == 0) {
         const int64_t z = r / M, m = r % M;
-        const int64_t si = (z * nbpr + b) * M + m;
-        dout[si] = h2f(dh);
-        if (WITH_SUM) sout[si] = h2f(f2h(d32 * (float)isum));
+        const int64_t si = (z * nbpr + b) * Mp + m;
+        dout[si] = dh;
+        if (WITH_SUM) sout[si] = f2h(d32 * (float)isum);
     }
 }
 
@@ -161,18 +174,18 @@ hipError_t launch_quantize_ggml(const SrcView& src, int type, bool ref_variant, 
     return hipGetLastError();
 }
 
-hipError_t launch_quantize_mmq(const SrcView& src, bool with_sum, const ActQ8& out, hipStream_t st) {
+hipError_t launch_quantize_mmq(const SrcView& src, bool with_sum, int64_t Mp, uint16_t* q, uint16_t* d, uint16_t* s,
+                               hipStream_t st) {
     const int64_t rows = src.ne[1] * src.ne[2] * src.ne[3];
     const int64_t nblocks = rows * (src.ne[0] / QK);
     if (nblocks == 0) return hipSuccess;
     const dim3 grid((unsigned)((nblocks * 8 + 255) / 256));
     const RowAddr ra = row_addr(src);
     if (with_sum)
-        quantize_mmq_kernel<true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, out.M, out.qs,
-                                                        out.d, out.s);
+        quantize_mmq_kernel<true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, src.ne[1], Mp, q, d, s);
     else
-        quantize_mmq_kernel<false><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, out.M, out.qs,
-                                                         out.d, out.s);
+        quantize_mmq_kernel<false><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, src.ne[1], Mp, q, d,
+                                                         s);
     return hipGetLastError();
 }
 
