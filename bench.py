@@ -48,6 +48,47 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def _pmc_run(counter, op, kernel_sub):
+    """Average per-dispatch value (KiB) of one TCC byte counter for the
+    dispatches of kernels whose name contains kernel_sub, from a child
+    `rocprofv3 --pmc` run of this script in --op mode."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    with tempfile.TemporaryDirectory(dir="/tmp") as td:
+        cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", td, "-o", "run", "--",
+               sys.executable, os.path.abspath(__file__), "--op", op, "--reps", "5", "--op-warmup", "3"]
+        env = dict(os.environ, TMPDIR="/tmp")
+        subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                       timeout=150, check=True)
+        vals = []
+        for root, _, files in os.walk(td):
+            for f in files:
+                if f.endswith("counter_collection.csv"):
+                    for r in csv.DictReader(open(os.path.join(root, f))):
+                        if kernel_sub in r["Kernel_Name"] and r["Counter_Name"] == counter:
+                            vals.append(float(r["Counter_Value"]))
+        if not vals:
+            raise RuntimeError(f"no {counter} samples for {kernel_sub}")
+        return sum(vals) / len(vals)
+
+
+def measure_traffic(op, kernel_sub):
+    """HBM bytes per launch of the op's kernel: FETCH_SIZE and WRITE_SIZE
+    (KiB per dispatch), each scaled by what the same counter reads for a plain
+    256 MiB device copy (read 256 MiB, write 256 MiB)."""
+    copy_bytes = 256 << 20
+    f_copy = _pmc_run("FETCH_SIZE", "copy", "copyBuffer")
+    w_copy = _pmc_run("WRITE_SIZE", "copy", "copyBuffer")
+    f = _pmc_run("FETCH_SIZE", op, kernel_sub)
+    w = _pmc_run("WRITE_SIZE", op, kernel_sub)
+    fs, ws = copy_bytes / (f_copy * 1024), copy_bytes / (w_copy * 1024)
+    return {"bytes": round(f * 1024 * fs + w * 1024 * ws), "fetch_kib": round(f, 1), "write_kib": round(w, 1),
+            "fetch_scale": round(fs, 4), "write_scale": round(ws, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -57,11 +98,23 @@ def main():
     ap.add_argument("--op", default=None,
                     help="profile mode: run only TYPE/LINEAR (e.g. q8_0/fc1) --reps times and print its kernel times")
     ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--op-warmup", type=int, default=20)
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the rocprofv3 FETCH_SIZE/WRITE_SIZE child runs (roofline.traffic = null)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
               "the hot path shards trivially over tokens or frames, see DESIGN.md", file=sys.stderr)
         sys.exit(2)
+
+    traffic = None
+    if not args.op and not args.no_traffic:
+        # child profiler runs first, before this process initialises the GPU
+        log("bench: HBM traffic of mmq_q8_0 fc1 (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
+        try:
+            traffic = measure_traffic("q8_0/fc1", "mmq_kernel<8")
+        except Exception as e:  # profiler missing or failed: traffic stays unmeasured
+            log(f"bench: traffic measurement failed: {e!r}")
 
     import torch
     from oracle import oracle as orc
@@ -69,6 +122,19 @@ def main():
     mi = load_pkg()
     ctx = mi.Context(0)
     dev = torch.device("cuda:0")
+
+    if args.op == "copy":
+        # calibration for the HBM byte counters: a plain device copy of 256 MiB
+        # (reads 256 MiB, writes 256 MiB per launch)
+        n = 64 << 20
+        a = torch.empty(n, dtype=torch.float32, device=dev).uniform_()
+        b = torch.empty_like(a)
+        for _ in range(args.reps):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"op": "copy", "bytes_read": 4 * n, "bytes_written": 4 * n, "reps": args.reps}), flush=True)
+        ctx.close()
+        return
 
     # ---- inputs (host-generated with the counter RNG, then resident in HBM)
     log("bench: generating inputs")
@@ -94,7 +160,7 @@ def main():
             calls.append((tname, lname, N, K, s0, s1, d))
     if args.op:
         c = [c for c in calls if f"{c[0]}/{c[1]}" == args.op][0]
-        for _ in range(3):
+        for _ in range(args.op_warmup):
             ctx.mul_mat(c[4], c[5], c[6])
         torch.cuda.synchronize()
         ctx.profile(True)
@@ -151,9 +217,11 @@ def main():
     alg_bytes = w_bytes + a_bytes + d_bytes
     achieved = alg_bytes / (mmq_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": traffic["bytes"] if traffic else None,
                 "kernel": "mmq_q8_0 fc1 [5184x1024]x[4736x1024]", "kernel_us": round(mmq_ms * 1e3, 2),
                 "alg_bytes": alg_bytes,
+                "traffic_counters": traffic,
                 "int8_tops": round(2.0 * M_TOK * N * K / (mmq_ms * 1e-3) / 1e12, 1)}
 
     # ---- CPU baseline: the oracle's ggml-cpu restatement, same fc1 Q8_0 mul_mat

@@ -2,7 +2,7 @@
 // workspace management and kernel dispatch.  Every entry point validates on
 // the host before touching the GPU and reports problems as mi355_status,
 // never by aborting (sam3.cpp returns bool/nullptr on failure, CLAUDE.md:62).
-#include "../../include/sam3_mi355.h"
+#include "sam3_mi355.h"
 
 #include <hip/hip_runtime.h>
 

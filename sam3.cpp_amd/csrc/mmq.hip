@@ -45,10 +45,33 @@ template <> struct WInfo<T_Q8_0> { static constexpr int bytes = 34, hdr = 2; };
 template <> struct WInfo<T_Q4_0> { static constexpr int bytes = 18, hdr = 2; };
 template <> struct WInfo<T_Q4_1> { static constexpr int bytes = 20, hdr = 4; };
 
-// Raw buffer resource over [base, base + bytes): gfx9 dword3 = 0x00020000.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+// Raw buffer resource over [base, base + bytes) (stride 0, gfx9 dword3 =
+// 0x00020000): offsets at or past the end read as zero.
+__device__ __forceinline__ v4i make_rsrc(const void* base, int64_t bytes) {
     const int32_t n = bytes <= 0 ? 0 : (bytes > 0x7fffffffLL ? 0x7fffffff : (int32_t)bytes);
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    return v4i{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), n, 0x00020000};
+}
+
+// buffer_load ... lds: lane i's 4 (or 16) bytes at voffset land at LDS byte
+// address M0 + 4*i (16*i).  Issued from inline asm so the compiler's wait
+// insertion does not track them: it cannot tell one stage buffer from another
+// and would otherwise wait for every DMA in flight before the first LDS read.
+// The kernel orders them itself (vmcnt waits + barrier).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void dma_b32(v4i rsrc, const void* lds, int voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr(lds))), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma_b128(v4i rsrc, const void* lds, int voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr(lds))), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
 }
 
 __device__ __forceinline__ uint32_t h2_sub(uint32_t v, _Float16 c) {
@@ -105,15 +128,48 @@ __device__ __forceinline__ void lds_dw2(const uint32_t* row, int o, int sh, uint
     }
 }
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14, expcnt and
+// lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier without a memory fence.  __syncthreads() releases all
+// prior memory operations, which waits for every outstanding load, including
+// the DMA of later stages still in flight; here each wavefront has already
+// waited for the DMA of the stage being published, so only its own LDS reads
+// need to be done.  The "memory" clobber keeps the compiler from moving LDS
+// accesses across it.
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// One pipeline stage of operands in LDS (two K blocks = 64 halves).  The
+// kernel keeps three of these as distinct __shared__ objects so that the
+// compiler's LDS-DMA tracking can tell a read of the current stage from the
+// DMA still landing in the stage after next.
+template <int WT>
+struct Stage {
+    static constexpr bool QUANT = WT != T_F16;
+    static constexpr int SKH = QUANT ? BKH : 32;         // halves of K per stage (F16: 32, keeps 3 stages in LDS)
+    static constexpr int CH = SKH / 8;                   // 16-byte chunks per tile row
+    static constexpr int WB = WInfo<WT == T_F16 ? T_Q8_0 : WT>::bytes;
+    static constexpr int RD = (2 * WB) / 4;              // dwords of a row's 2-block stage segment
+    static constexpr int RLD = (BN * RD + NT - 1) / NT;  // raw dword DMA instructions per wavefront
+    _Float16 A[BM * SKH];                                // activation tile, swizzled 16-byte chunks
+    _Float16 Bf[QUANT ? 8 : BN * SKH];                   // F16 weight tile (same swizzle)
+    uint32_t W[QUANT ? RLD * NT : 4];                    // raw weight segments, lane-linear dwords
+    _Float16 Ad[BKB][BM];                                // activation scales of the two blocks
+    _Float16 As[WT == T_Q4_1 ? BKB : 1][BM];             // Q8_1 sums (Q4_1)
+};
 
 // Workgroup 128(m) x 128(n); wavefront w owns all 128 rows of m and the 32
 // columns n0 + 32w .. +31 (4 MFMA tiles stacked along m).  Every stage's
 // operands are DMA'd from global memory straight into LDS (buffer_load ...
-// lds): no staging registers, no LDS store instructions.  Per stage each
-// wavefront issues its share of the next stage's DMA into the other buffer
-// right after the barrier and then runs the current stage's MFMAs; one
-// vmcnt(0) + barrier per stage.
+// lds): no staging registers, no LDS store instructions.  Three stages are
+// in flight: at stage s each wavefront waits for its own DMA of stage s
+// (leaving stage s+1's outstanding), one barrier publishes everyone's, and
+// the DMA of stage s+2 goes into the buffer stage s-1 used.
 //   activation tile: 128 rows x 64 halves, unpadded; 16-byte chunk c of row r
 //     sits in slot c ^ (r & 7), so a 32-row MFMA fragment read hits 8
 //     distinct slots (no bank conflicts) while each DMA lane still writes
@@ -123,19 +179,18 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 //   activation scales (and Q8_1 sums): 128 fp16 per block, one dword per lane.
 template <int WT, bool DOTS>
 __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p) {
-    constexpr bool QUANT = WT != T_F16;
-    constexpr int QT = WT == T_F16 ? T_Q8_0 : WT;
-    constexpr int WB = WInfo<QT>::bytes, HDR = WInfo<QT>::hdr;
-    constexpr int RD = (2 * WB) / 4;             // dwords of a row's 2-block stage segment
-    constexpr int RLD = (BN * RD + NT - 1) / NT; // raw dword DMA instructions per wavefront
-    constexpr int MT = BM / 32;                  // m tiles per wavefront
-    constexpr int TH = BM * BKH;                 // halves per activation tile
-    __shared__ __attribute__((aligned(16))) _Float16 sA[2][TH];
-    __shared__ __attribute__((aligned(16))) _Float16 sBf[QUANT ? 1 : 2][QUANT ? 8 : BN * BKH];
-    __shared__ __attribute__((aligned(16))) uint32_t sW[QUANT ? 2 : 1][QUANT ? RLD * NT : 4];
-    __shared__ __attribute__((aligned(16))) _Float16 sAd[2][BKB][BM];
-    __shared__ __attribute__((aligned(16))) _Float16 sAs[WT == T_Q4_1 ? 2 : 1][BKB][BM];
-    __shared__ __attribute__((aligned(16))) _Float16 sZero[2 * BKB * BM];  // S-operand lanes 32..63
+    using St = Stage<WT>;
+    constexpr bool QUANT = St::QUANT;
+    constexpr int WB = St::WB, HDR = WInfo<WT == T_F16 ? T_Q8_0 : WT>::hdr;
+    constexpr int RD = St::RD, RLD = St::RLD, SKH = St::SKH, CH = St::CH;
+    constexpr int MT = BM / 32;       // m tiles per wavefront
+    constexpr int RPI = 64 / CH;      // tile rows per DMA instruction
+    constexpr int NI = BM / 4 / RPI;  // tile DMA instructions per wavefront
+    // per-wavefront DMA instructions of one stage (plus one scale load on some wavefronts)
+    constexpr int NL = QUANT ? NI + RLD : 2 * NI;
+    __shared__ __attribute__((aligned(16))) St st0;
+    __shared__ __attribute__((aligned(16))) St st1;
+    __shared__ __attribute__((aligned(16))) St st2;
 
     // XCD-aware tile order: workgroup id -> (xcd, slot) -> contiguous tile band per XCD
     const int T = p.tiles_m * p.tiles_n;
@@ -144,25 +199,28 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p) {
     if (t >= T) return;
     const int m0 = (t / p.tiles_n) * BM, n0 = (t % p.tiles_n) * BN;
 
-    const int tid = threadIdx.x, lane = tid & 63, wn = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wn = __builtin_amdgcn_readfirstlane(tid >> 6);  // wavefront index (uniform)
     const int z = blockIdx.y, i12 = z % p.ne12, i13 = z / p.ne12;
     const int M = p.M, N = p.N, K = p.K;
     const int nb = K / QK;
-    const int nstage = QUANT ? (nb + BKB - 1) / BKB : (K + BKH - 1) / BKH;
+    const int nstage = QUANT ? (nb + BKB - 1) / BKB : (K + SKH - 1) / SKH;
     const uint8_t* Wz = p.W + (int64_t)(i12 / p.r2) * p.w_nb2 + (int64_t)(i13 / p.r3) * p.w_nb3;
     const _Float16* Az = p.A + (int64_t)i12 * p.a_s2 + (int64_t)i13 * p.a_s3;
     const int Mp = p.Mp;
     const _Float16* Adz = QUANT ? p.Ad + (int64_t)z * nb * Mp : nullptr;
     const _Float16* Asz = WT == T_Q4_1 ? p.As + (int64_t)z * nb * Mp : nullptr;
+    // wavefronts 0, 1 load the two blocks' d; for Q4_1, 2 and 3 load the two blocks' s
+    const bool xload = QUANT && (wn < 2 || WT == T_Q4_1);
 
     // ---- DMA offsets, fixed for the whole K loop
-    // activation / F16-weight tile, instruction i of wavefront w: rows (4w+i)*8 + lane/8,
-    // slot lane%8 <- chunk (lane%8) ^ (lane/8)
-    const int trow = lane >> 3, tchunk = (lane & 7) ^ (lane >> 3);
-    int aoff[4], foff[4];
+    // activation / F16-weight tile, instruction i of wavefront w: rows (NI*w+i)*RPI + lane/CH,
+    // slot lane%CH <- chunk (lane%CH) ^ (row%CH)
+    const int trow = lane / CH, tchunk = (lane % CH) ^ (trow % CH);
+    int aoff[NI], foff[NI];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = (wn * 4 + i) * 8 + trow;
+    for (int i = 0; i < NI; ++i) {
+        const int row = (wn * NI + i) * RPI + trow;
         aoff[i] = m0 + row < M ? ((m0 + row) * (int)p.a_s1 + tchunk * 8) * 2 : OOB;
         foff[i] = !QUANT && n0 + row < N ? (n0 + row) * (int)p.w_nb1 + tchunk * 16 : OOB;
     }
@@ -173,37 +231,34 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p) {
         woff[i] = QUANT && j < BN * RD && n0 + row < N ? (n0 + row) * (int)p.w_nb1 + 4 * c : OOB;
     }
 
-    auto dma_stage = [&](int s, int buf) {
-        const int k0 = s * BKH;
-        const bool tail = k0 + BKH > K;  // chunks past K must read zeros (rows continue in memory)
+    auto dma_stage = [&](int s, St& b) {
+        const int k0 = s * SKH;
+        const bool tail = k0 + SKH > K;  // chunks past K must read zeros (rows continue in memory)
         const bool cvalid = k0 + tchunk * 8 < K;
         const auto ar = make_rsrc(Az + k0, p.a_extent - 2LL * k0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_ptr_t)&sA[buf][(wn * 4 + i) * 8 * BKH], 16,
-                                                     tail && !cvalid ? OOB : aoff[i], 0, 0, 0);
+        for (int i = 0; i < NI; ++i)
+            dma_b128(ar, &b.A[(wn * NI + i) * RPI * SKH], tail && !cvalid ? OOB : aoff[i]);
         if (QUANT) {
             const int64_t seg = (int64_t)s * BKB * WB;
             const auto wrs = make_rsrc(Wz + seg, p.w_extent - seg);
 #pragma unroll
             for (int i = 0; i < RLD; ++i)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_ptr_t)&sW[buf][NT * i + 64 * wn], 4, woff[i], 0, 0, 0);
-            // scales of blocks 2s, 2s+1: wavefronts 0, 1 (d) and, for Q8_1, 2, 3 (s)
-            const int b = wn & 1;
-            const int64_t so = (int64_t)(s * BKB + b) * Mp + m0;  // halves
+                dma_b32(wrs, &b.W[NT * i + 64 * wn], woff[i]);
+            const int bb = wn & 1;
+            const int64_t so = (int64_t)(s * BKB + bb) * Mp + m0;  // halves
             if (wn < 2) {
                 const auto dr = make_rsrc(Adz + so, 2LL * ((int64_t)nb * Mp - so));
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(dr, (lds_ptr_t)&sAd[buf][b][0], 4, lane * 4, 0, 0, 0);
+                dma_b32(dr, &b.Ad[bb][0], lane * 4);
             } else if (WT == T_Q4_1) {
                 const auto sr = make_rsrc(Asz + so, 2LL * ((int64_t)nb * Mp - so));
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (lds_ptr_t)&sAs[buf][b][0], 4, lane * 4, 0, 0, 0);
+                dma_b32(sr, &b.As[WT == T_Q4_1 ? bb : 0][0], lane * 4);
             }
         } else {
             const auto fr = make_rsrc(Wz + 2LL * k0, p.w_extent - 2LL * k0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(fr, (lds_ptr_t)&sBf[buf][(wn * 4 + i) * 8 * BKH], 16,
-                                                         tail && !cvalid ? OOB : foff[i], 0, 0, 0);
+            for (int i = 0; i < NI; ++i)
+                dma_b128(fr, &b.Bf[(wn * NI + i) * RPI * SKH], tail && !cvalid ? OOB : foff[i]);
         }
     };
 
@@ -215,93 +270,122 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p) {
     const v16f zf = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     const int lr = lane & 31, g = lane >> 5;  // fragment row, lane group
     const int wrow = wn * 32 + lr;           // this lane's weight row in the tile
-    const uint16_t* zero16 = reinterpret_cast<const uint16_t*>(&sZero[0]);
-    // S-operand activation scales: lanes 0..31 read sAd, lanes 32..63 the zero mirror
-    const uint16_t* da_src = lane < 32 ? reinterpret_cast<const uint16_t*>(&sAd[0][0][0]) : zero16;
-    const uint16_t* sa_src = lane < 32 ? reinterpret_cast<const uint16_t*>(&sAs[0][0][0]) : zero16;
-    if (QUANT) {
-        for (int i = tid; i < 2 * BKB * BM; i += NT) sZero[i] = (_Float16)0.0f;
-    }
+    const bool lo = lane < 32;
     // fragment of row r, 8-half chunk c in a swizzled tile
     auto frag = [&](const _Float16* tile, int r, int c) -> v8h {
-        return *reinterpret_cast<const v8h*>(&tile[r * BKH + ((c ^ (r & 7)) << 3)]);
+        return *reinterpret_cast<const v8h*>(&tile[r * SKH + ((c ^ (r & (CH - 1))) << 3)]);
     };
 
-    dma_stage(0, 0);
-    for (int s = 0; s < nstage; ++s) {
-        const int cur = s & 1;
-        __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): this wavefront's DMA for stage s landed
-        __syncthreads();                     // ... and everyone's; stage s-1 buffers are free
-        if (s + 1 < nstage) dma_stage(s + 1, cur ^ 1);
+    auto compute = [&](int s, const St& b) {
         if (QUANT) {
-            const uint32_t* rowp = &sW[cur][wrow * RD];
-            const uint16_t* hsrc = lane < 32 ? reinterpret_cast<const uint16_t*>(rowp) : zero16;
+            const uint32_t* rowp = &b.W[wrow * RD];
+            const uint16_t* hrow = reinterpret_cast<const uint16_t*>(rowp);
+            if (WT == T_Q4_1 && !DOTS) {
+                // acc += sum_b s_a[m][b] * m_w[n][b] over this stage's blocks (k-slots 0, 1)
+                const uint32_t m1 = s * BKB + 1 < nb ? (uint32_t)hrow[WB / 2 + 1] << 16 : 0u;
+                const v4i mwf = {lo ? (int)((uint32_t)hrow[1] | m1) : 0, 0, 0, 0};
+                const uint16_t* as0 = reinterpret_cast<const uint16_t*>(&b.As[0][0]);
+                const uint16_t* as1 = reinterpret_cast<const uint16_t*>(&b.As[WT == T_Q4_1 ? 1 : 0][0]);
 #pragma unroll
-            for (int b = 0; b < BKB; ++b) {
-                if (DOTS && s * BKB + b >= nb) break;
-                // this lane's weight fragments: row wrow, k-chunk 8g..8g+7 of each 16-wide half.
-                // A block past K (odd block count) runs with d_a = 0: S = 0 leaves acc unchanged.
+                for (int mt = 0; mt < MT; ++mt) {
+                    const int ar_ = mt * 32 + lr;
+                    v4i saf = __builtin_bit_cast(v4i, frag(b.A, ar_, g));  // finite filler
+                    saf[0] = (int)((uint32_t)as0[ar_] | ((uint32_t)as1[ar_] << 16));
+                    acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, saf),
+                                                                     __builtin_bit_cast(v8h, mwf), acc[mt], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int bk = 0; bk < BKB; ++bk) {
+                if (DOTS && s * BKB + bk >= nb) break;
+                // this lane's weight fragments: row wrow, k-chunk 8g..8g+7 of each 16-wide half
                 v8h bf[2];
                 if (WT == T_Q8_0) {
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
                         uint32_t w0, w1;
-                        lds_dw2(rowp, b * WB + HDR + 16 * h + 8 * g, (b * WB + HDR) & 3, w0, w1);
+                        lds_dw2(rowp, bk * WB + HDR + 16 * h + 8 * g, (bk * WB + HDR) & 3, w0, w1);
                         bf[h] = i8x8_to_h8(w0, w1);
                     }
                 } else {
                     uint32_t w0, w1;  // payload bytes 8g..8g+7: low nibbles = half 0, high = half 1
-                    lds_dw2(rowp, b * WB + HDR + 8 * g, (b * WB + HDR) & 3, w0, w1);
+                    lds_dw2(rowp, bk * WB + HDR + 8 * g, (bk * WB + HDR) & 3, w0, w1);
                     const _Float16 bias = WT == T_Q4_0 ? (_Float16)1032.0f : (_Float16)1024.0f;
                     bf[0] = n8_to_h8(w0 & 0x0f0f0f0fu, w1 & 0x0f0f0f0fu, bias);
                     bf[1] = n8_to_h8((w0 >> 4) & 0x0f0f0f0fu, (w1 >> 4) & 0x0f0f0f0fu, bias);
                 }
-                const v4i dwf = {(int)(uint32_t)hsrc[b * WB / 2], 0, 0, 0};
+                // S-MFMA B operand: d_w in k-slot 0 (lanes 0..31), zero in every other k-slot.
+                // A block past K (odd block count) gets d_w = 0: its raw bytes belong to the
+                // next row (or padding) and its d_a is 0, so S = 0 leaves acc unchanged.
+                const bool bvalid = s * BKB + bk < nb;
+                const v4i dwf = {lo && bvalid ? (int)(uint32_t)hrow[bk * WB / 2] : 0, 0, 0, 0};
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    const int ar_ = mt * 32 + lr;
-                    const v8h a0 = frag(sA[cur], ar_, 4 * b + g);
-                    const v8h a1 = frag(sA[cur], ar_, 4 * b + 2 + g);
-                    v16f I = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bf[0], zf, 0, 0, 0);
-                    I = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bf[1], I, 0, 0, 0);
-                    if (DOTS) {
-                        const int n = n0 + wrow;
+                for (int mp = 0; mp < MT; mp += 2) {
+                    v16f I[2], S[2];
 #pragma unroll
-                        for (int i = 0; i < 16; ++i) {
-                            const int m = m0 + mt * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-                            if (m < M && n < N) p.dots[(((int64_t)z * M + m) * N + n) * nb + s * BKB + b] = (int32_t)I[i];
+                    for (int j = 0; j < 2; ++j) {
+                        const int ar_ = (mp + j) * 32 + lr;
+                        const v8h a0 = frag(b.A, ar_, 4 * bk + g);
+                        const v8h a1 = frag(b.A, ar_, 4 * bk + 2 + g);
+                        I[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bf[0], zf, 0, 0, 0);
+                        I[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bf[1], I[j], 0, 0, 0);
+                        if (!DOTS) {
+                            // S-MFMA A operand: d_a in k-slot 0; the other k-slots keep a1's
+                            // (finite) quants, which meet B's zeros
+                            v4i daf = __builtin_bit_cast(v4i, a1);
+                            daf[0] = (int)(uint32_t) reinterpret_cast<const uint16_t*>(&b.Ad[bk][0])[ar_];
+                            S[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, daf),
+                                                                          __builtin_bit_cast(v8h, dwf), zf, 0, 0, 0);
                         }
-                        continue;
                     }
-                    const v4i daf = {(int)(uint32_t)da_src[(cur * BKB + b) * BM + ar_], 0, 0, 0};
-                    const v16f S = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                        __builtin_bit_cast(v8h, daf), __builtin_bit_cast(v8h, dwf), zf, 0, 0, 0);
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) acc[mt][i] = __builtin_fmaf(I[i], S[i], acc[mt][i]);
-                }
-            }
-            if (WT == T_Q4_1 && !DOTS) {
-                // acc += sum_b s_a[m][b] * m_w[n][b] over this stage's blocks (k-slots 0, 1)
-                const v4i mwf = {(int)((uint32_t)hsrc[1] | ((uint32_t)hsrc[WB / 2 + 1] << 16)), 0, 0, 0};
+                    for (int j = 0; j < 2; ++j) {
+                        if (DOTS) {
+                            const int n = n0 + wrow;
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    const int ar_ = mt * 32 + lr;
-                    const v4i saf = {(int)((uint32_t)sa_src[(cur * BKB) * BM + ar_] |
-                                           ((uint32_t)sa_src[(cur * BKB + 1) * BM + ar_] << 16)), 0, 0, 0};
-                    acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, saf),
-                                                                     __builtin_bit_cast(v8h, mwf), acc[mt], 0, 0, 0);
+                            for (int i = 0; i < 16; ++i) {
+                                const int m = m0 + (mp + j) * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
+                                if (m < M && n < N)
+                                    p.dots[(((int64_t)z * M + m) * N + n) * nb + s * BKB + bk] = (int32_t)I[j][i];
+                            }
+                        } else {
+#pragma unroll
+                            for (int i = 0; i < 16; ++i) acc[mp + j][i] = __builtin_fmaf(I[j][i], S[j][i], acc[mp + j][i]);
+                        }
+                    }
                 }
             }
         } else {
 #pragma unroll
-            for (int kk = 0; kk < BKH / 16; ++kk) {
-                const v8h bfr = frag(sBf[cur], wrow, 2 * kk + g);
+            for (int kk = 0; kk < SKH / 16; ++kk) {
+                const v8h bfr = frag(b.Bf, wrow, 2 * kk + g);
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
-                    acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag(sA[cur], mt * 32 + lr, 2 * kk + g), bfr,
+                    acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(frag(b.A, mt * 32 + lr, 2 * kk + g), bfr,
                                                                      acc[mt], 0, 0, 0);
             }
         }
+    };
+
+    // one pipeline step: wait for stage s, publish it, refill the oldest buffer, compute
+    auto step = [&](int s, const St& cur, St& refill) {
+        if (s + 1 < nstage) {
+            if (xload) wait_vmcnt<NL + 1>();
+            else wait_vmcnt<NL>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        stage_barrier();
+        if (s + 2 < nstage) dma_stage(s + 2, refill);
+        compute(s, cur);
+    };
+
+    dma_stage(0, st0);
+    if (nstage > 1) dma_stage(1, st1);
+    for (int s = 0; s < nstage; s += 3) {
+        step(s, st0, st2);
+        if (s + 1 < nstage) step(s + 1, st1, st0);
+        if (s + 2 < nstage) step(s + 2, st2, st1);
     }
     if (DOTS) return;
 
