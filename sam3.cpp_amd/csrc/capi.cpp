@@ -6,6 +6,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -462,8 +463,61 @@ void mi355_profile_reset(mi355_context* ctx) {
 mi355_status mi355_flash_attn_ext(mi355_context* ctx, const mi355_tensor* q, const mi355_tensor* k,
                                   const mi355_tensor* v, const mi355_tensor* mask, float scale, float max_bias,
                                   float logit_softcap, const mi355_tensor* dst) {
-    (void)q; (void)k; (void)v; (void)mask; (void)scale; (void)max_bias; (void)logit_softcap; (void)dst;
-    return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: not built yet");
+    if (!q || !k || !v || !dst || !q->data || !k->data || !v->data || !dst->data)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: null argument");
+    if (!dims_ok(q) || !dims_ok(k) || !dims_ok(v) || !dims_ok(dst))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: negative ne/nb");
+    if (mask || max_bias != 0.0f || logit_softcap != 0.0f)
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: mask, ALiBi and softcap not supported");
+    // ggml_flash_attn_ext shape rules
+    const int64_t D = q->ne[0];
+    if (k->ne[0] != D || v->ne[1] != k->ne[1] || q->ne[3] != k->ne[3] || q->ne[3] != v->ne[3])
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: q/k/v shapes do not match");
+    if (k->ne[2] <= 0 || v->ne[2] <= 0 || q->ne[2] % k->ne[2] != 0 || q->ne[2] % v->ne[2] != 0)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: heads not divisible by kv heads");
+    if (dst->type != T_F32 || dst->ne[0] != v->ne[0] || dst->ne[1] != q->ne[2] || dst->ne[2] != q->ne[1] ||
+        dst->ne[3] != q->ne[3])
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: dst must be F32 [Dv, n_head, n_q, batch]");
+    if (dst->nb[0] != 4 || dst->nb[1] != 4 * dst->ne[0] || dst->nb[2] != dst->nb[1] * dst->ne[1] ||
+        dst->nb[3] != dst->nb[2] * dst->ne[2])
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: dst must be contiguous");
+    if (v->ne[0] != D || !(D == 64 || D == 96 || D == 128))
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: head size %lld (supported: D = Dv in 64, 96, 128)",
+                    (long long)D);
+    const mi355_tensor* ops[3] = {q, k, v};
+    for (const mi355_tensor* t : ops) {
+        if (t->type != T_F32 && t->type != T_F16)
+            return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: q/k/v must be F32 or F16");
+        if (t->nb[0] != type_size(t->type))
+            return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: rows must be contiguous (nb[0] = type size)");
+        if (((reinterpret_cast<uintptr_t>(t->data) | (uintptr_t)t->nb[1] | (uintptr_t)t->nb[2] | (uintptr_t)t->nb[3]) &
+             3) != 0)
+            return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: rows must be 4-byte aligned");
+    }
+    if (k->type != v->type) return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: k and v must share a type");
+    if (q->ne[1] > INT32_MAX || k->ne[1] > INT32_MAX || q->ne[2] > 65535 || q->ne[3] > 65535)
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: sizes beyond the launch limits");
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "flash_attn_ext: null context");
+    FaArgs a;
+    a.q = static_cast<const char*>(q->data);
+    a.k = static_cast<const char*>(k->data);
+    a.v = static_cast<const char*>(v->data);
+    a.dst = static_cast<float*>(dst->data);
+    a.q_nb1 = q->nb[1]; a.q_nb2 = q->nb[2]; a.q_nb3 = q->nb[3];
+    a.k_nb1 = k->nb[1]; a.k_nb2 = k->nb[2]; a.k_nb3 = k->nb[3];
+    a.v_nb1 = v->nb[1]; a.v_nb2 = v->nb[2]; a.v_nb3 = v->nb[3];
+    a.nq = (int)q->ne[1];
+    a.nkv = (int)k->ne[1];
+    a.nh = (int)q->ne[2];
+    a.rk2 = (int)(q->ne[2] / k->ne[2]);
+    a.rv2 = (int)(q->ne[2] / v->ne[2]);
+    const float c = fabsf(scale) * 1.44269504088896340736f;
+    a.c = c > 1e-30f ? c : 1e-30f;  // keeps masked (-inf) scores at weight 0 when scale is 0
+    a.negq = scale < 0.0f;
+    (void)hipSetDevice(ctx->device);
+    Timed tf(ctx, "flash_attn_ext");
+    return hip_check(ctx, tf.done(launch_fattn(a, (int)D, q->type == T_F32, k->type == T_F32, (int)q->ne[3], ctx->stream)),
+                     "flash_attn_ext launch");
 }
 
 }  // extern "C"

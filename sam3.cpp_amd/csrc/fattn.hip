@@ -1,0 +1,255 @@
+// ggml FLASH_ATTN_EXT (mask = NULL, max_bias = 0, logit_softcap = 0) on
+// gfx950 fp16 MFMA with fp32 online softmax.
+//
+//   dst[b][iq][h][:] = sum_j softmax_j(scale * q.k_j) v_j
+//   q [D, n_q, n_head, B], k [D, n_kv, n_head_k, B], v [D, n_kv, n_head_v, B]
+//   (F32 or F16, any row strides), dst [D, n_head, n_q, B] F32 contiguous.
+//
+// Q, K and V enter the MFMAs as fp16 (round to nearest even, as ggml-cpu
+// converts Q for an F16 K); scores, the softmax statistics and the output
+// accumulate in fp32.
+//
+// Workgroup: 128 queries of one (head, batch), four wavefronts of 32
+// queries; the key/value sequence streams through LDS in tiles of 64 keys.
+//   scores:  S^T[key][q] = K Q^T (v_mfma_f32_32x32x16_f16, A = K rows from
+//            LDS, B = the wavefront's Q fragment held in registers), so each
+//            lane owns one query column and 16 keys of every 32-key block:
+//            row max / row sum are in-lane plus one exchange with lane l ^ 32.
+//   softmax: exp2 domain, c = |scale| * log2(e) folded into one FMA per score.
+//   output:  O^T[d][q] += V^T P^T.  The P registers are used directly as the
+//            B operand: MFMA k-slot j of lane group g carries key
+//            16h + 8(j/4) + 4g + j%4 of the 32-key block, and the V^T rows
+//            are read from LDS with the same key order.
+// K is staged row-major and V transposed, both with rows padded by 16 bytes
+// so the 32-row fragment reads spread over all LDS banks.  The next tile's
+// global loads go to registers before the current tile's MFMAs.
+#include "common.cuh"
+#include "kernels.h"
+
+namespace mi355 {
+
+namespace {
+constexpr int FA_BQ = 128, FA_BKV = 64, FA_NT = 256;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
+typedef v4f v4f_a4 __attribute__((aligned(4)));
+}  // namespace
+
+// 8 consecutive elements of a row as fp16 (RNE), packed in 4 dwords
+template <bool F32>
+__device__ __forceinline__ u32x4 load8_h(const char* p) {
+    if (F32) {
+        const v4f a = *reinterpret_cast<const v4f_a4*>(p);
+        const v4f b = *reinterpret_cast<const v4f_a4*>(p + 16);
+        u32x4 r;
+        r[0] = (uint32_t)f2h(a[0]) | ((uint32_t)f2h(a[1]) << 16);
+        r[1] = (uint32_t)f2h(a[2]) | ((uint32_t)f2h(a[3]) << 16);
+        r[2] = (uint32_t)f2h(b[0]) | ((uint32_t)f2h(b[1]) << 16);
+        r[3] = (uint32_t)f2h(b[2]) | ((uint32_t)f2h(b[3]) << 16);
+        return r;
+    } else {
+        return *reinterpret_cast<const u32x4_a4*>(p);
+    }
+}
+
+// value of lane l ^ 32 (the other half of the wavefront holds the same query)
+__device__ __forceinline__ float partner32(float x) {
+    const int l = (int)__lane_id();
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((l ^ 32) << 2, __builtin_bit_cast(int, x)));
+}
+__device__ __forceinline__ float xmax32(float x) { return fmaxf(x, partner32(x)); }
+__device__ __forceinline__ float xsum32(float x) { return x + partner32(x); }
+
+template <int D, bool QF32, bool KVF32>
+__global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
+    constexpr int KS = D + 8;       // K tile row stride (halves)
+    constexpr int VS = FA_BKV + 8;  // V^T tile row stride (halves)
+    constexpr int NC = D / 16;      // MFMA k-chunks of a score
+    constexpr int NDB = D / 32;     // 32-row blocks of O^T
+    constexpr int C8 = D / 8;       // 8-element chunks per key row
+    constexpr int LPT = FA_BKV * C8 / FA_NT;  // chunks per thread per tile (K and V each)
+    static_assert(FA_BKV * C8 % FA_NT == 0, "tile split");
+    __shared__ __attribute__((aligned(16))) _Float16 sK[FA_BKV * KS];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[D * VS];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lr = lane & 31, g = lane >> 5;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int qi = blockIdx.x * FA_BQ + w * 32 + lr;  // this lane's query
+    const int nkv = p.nkv;
+    const char* kb = p.k + (int64_t)(h / p.rk2) * p.k_nb2 + (int64_t)b * p.k_nb3;
+    const char* vb = p.v + (int64_t)(h / p.rv2) * p.v_nb2 + (int64_t)b * p.v_nb3;
+    constexpr int KES = KVF32 ? 4 : 2;
+
+    // Q fragment (B operand of S^T): query qi, elements 16c + 8g .. +7
+    v8h qf[NC];
+    {
+        const char* qrow = p.q + (int64_t)qi * p.q_nb1 + (int64_t)h * p.q_nb2 + (int64_t)b * p.q_nb3;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            u32x4 r = {0, 0, 0, 0};
+            if (qi < p.nq) r = load8_h<QF32>(qrow + (16 * c + 8 * g) * (QF32 ? 4 : 2));
+            if (p.negq) r ^= 0x80008000u;
+            qf[c] = __builtin_bit_cast(v8h, r);
+        }
+    }
+
+    // global -> register staging of one K/V tile.  K chunk j of thread t: key (t + 256j) / C8,
+    // column (t + 256j) % C8 (a key row's chunks on consecutive lanes); V chunk: key
+    // (t + 256j) % 64, column (t + 256j) / 64 (consecutive keys on consecutive lanes, so
+    // the transposed LDS writes of a wavefront hit consecutive halves).
+    u32x4 kreg[LPT], vreg[LPT];
+    auto load_tile = [&](int kv0) {
+#pragma unroll
+        for (int j = 0; j < LPT; ++j) {
+            const int id = tid + FA_NT * j;
+            const int kk = id / C8, kc = id % C8;
+            const int vk = id % FA_BKV, vc = id / FA_BKV;
+            kreg[j] = u32x4{0, 0, 0, 0};
+            vreg[j] = u32x4{0, 0, 0, 0};
+            if (kv0 + kk < nkv) kreg[j] = load8_h<KVF32>(kb + (int64_t)(kv0 + kk) * p.k_nb1 + kc * 8 * KES);
+            if (kv0 + vk < nkv) vreg[j] = load8_h<KVF32>(vb + (int64_t)(kv0 + vk) * p.v_nb1 + vc * 8 * KES);
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (int j = 0; j < LPT; ++j) {
+            const int id = tid + FA_NT * j;
+            const int kk = id / C8, kc = id % C8;
+            *reinterpret_cast<u32x4*>(&sK[kk * KS + kc * 8]) = kreg[j];
+            const int vk = id % FA_BKV, vc = id / FA_BKV;
+            uint16_t* col = reinterpret_cast<uint16_t*>(&sV[(vc * 8) * VS + vk]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                col[(2 * e) * VS] = (uint16_t)(vreg[j][e] & 0xffffu);
+                col[(2 * e + 1) * VS] = (uint16_t)(vreg[j][e] >> 16);
+            }
+        }
+    };
+
+    v16f O[NDB];
+#pragma unroll
+    for (int i = 0; i < NDB; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) O[i][e] = 0.0f;
+    const v16f zf = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    float m_run = -__builtin_inff(), l_run = 0.0f;
+    const float c = p.c;
+
+    const int ntile = (nkv + FA_BKV - 1) / FA_BKV;
+    load_tile(0);
+    store_tile();
+    __syncthreads();
+    for (int t = 0; t < ntile; ++t) {
+        const int kv0 = t * FA_BKV;
+        if (t + 1 < ntile) load_tile(kv0 + FA_BKV);
+
+        // S^T for the two 32-key halves
+        v16f S[2];
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+            S[kh] = zf;
+#pragma unroll
+            for (int cc = 0; cc < NC; ++cc) {
+                const v8h a = *reinterpret_cast<const v8h*>(&sK[(32 * kh + lr) * KS + 16 * cc + 8 * g]);
+                S[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[cc], S[kh], 0, 0, 0);
+            }
+        }
+        if (kv0 + FA_BKV > nkv) {  // keys past the end take no weight
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int key = kv0 + 32 * kh + 8 * (i >> 2) + 4 * g + (i & 3);
+                    if (key >= nkv) S[kh][i] = -__builtin_inff();
+                }
+        }
+        float mx = S[0][0];
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, S[kh][i]);
+        mx = xmax32(mx);
+        const float m_new = fmaxf(m_run, mx * c);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        float ls = 0.0f;
+        uint32_t P[2][8];
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int i = 0; i < 16; i += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kh][i], c, -m_new));
+                const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kh][i + 1], c, -m_new));
+                ls += p0 + p1;
+                P[kh][i >> 1] = (uint32_t)f2h(p0) | ((uint32_t)f2h(p1) << 16);
+            }
+        ls = xsum32(ls);
+        l_run = l_run * alpha + ls;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) O[db][e] *= alpha;
+
+        // O^T += V^T P^T over the 64 keys (four 16-key MFMA chunks)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+            const _Float16* vrow = &sV[(32 * db + lr) * VS];
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int k0 = 32 * kh + 16 * hh + 4 * g;
+                    const uint2 lo = *reinterpret_cast<const uint2*>(&vrow[k0]);
+                    const uint2 hi = *reinterpret_cast<const uint2*>(&vrow[k0 + 8]);
+                    const v4i av = {(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+                    const v4i bp = {(int)P[kh][4 * hh], (int)P[kh][4 * hh + 1], (int)P[kh][4 * hh + 2],
+                                    (int)P[kh][4 * hh + 3]};
+                    O[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, av),
+                                                                  __builtin_bit_cast(v8h, bp), O[db], 0, 0, 0);
+                }
+        }
+        if (t + 1 < ntile) {
+            __syncthreads();  // every wavefront is done with this tile
+            store_tile();
+            __syncthreads();
+        }
+    }
+
+    if (qi < p.nq) {
+        const float inv = l_run == 0.0f ? 0.0f : 1.0f / l_run;
+        float* orow = p.dst + (((int64_t)b * p.nq + qi) * p.nh + h) * D;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const int d = 32 * db + 8 * i4 + 4 * g;
+                v4f o = {O[db][4 * i4] * inv, O[db][4 * i4 + 1] * inv, O[db][4 * i4 + 2] * inv,
+                         O[db][4 * i4 + 3] * inv};
+                *reinterpret_cast<v4f*>(orow + d) = o;
+            }
+    }
+}
+
+template <int D>
+static void fa_launch_d(const FaArgs& a, bool qf32, bool kvf32, int B, hipStream_t st) {
+    const dim3 grid((unsigned)((a.nq + FA_BQ - 1) / FA_BQ), (unsigned)a.nh, (unsigned)B);
+    if (qf32 && kvf32) fattn_kernel<D, true, true><<<grid, FA_NT, 0, st>>>(a);
+    else if (qf32) fattn_kernel<D, true, false><<<grid, FA_NT, 0, st>>>(a);
+    else if (kvf32) fattn_kernel<D, false, true><<<grid, FA_NT, 0, st>>>(a);
+    else fattn_kernel<D, false, false><<<grid, FA_NT, 0, st>>>(a);
+}
+
+hipError_t launch_fattn(const FaArgs& a, int D, bool qf32, bool kvf32, int B, hipStream_t st) {
+    if (a.nq <= 0 || a.nkv <= 0 || a.nh <= 0 || B <= 0) return hipSuccess;
+    switch (D) {
+        case 64: fa_launch_d<64>(a, qf32, kvf32, B, st); break;
+        case 96: fa_launch_d<96>(a, qf32, kvf32, B, st); break;
+        case 128: fa_launch_d<128>(a, qf32, kvf32, B, st); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace mi355

@@ -69,4 +69,19 @@ size_t mmq_align_bytes(const MatW& w, int64_t N, int64_t K);
 // Row softmax of scale*x (F32, strided rows) into dst (F32, strided rows).
 hipError_t launch_soft_max(const SrcView& src, float scale, char* dst, const int64_t dnb[4], hipStream_t st);
 
+// FLASH_ATTN_EXT operands (byte strides; rows of D contiguous elements).
+struct FaArgs {
+    const char* q;
+    const char* k;
+    const char* v;
+    float* dst;  // [D, nh, nq, B] contiguous
+    int64_t q_nb1, q_nb2, q_nb3;
+    int64_t k_nb1, k_nb2, k_nb3;
+    int64_t v_nb1, v_nb2, v_nb3;
+    int nq, nkv, nh, rk2, rv2;  // rk2 = nh / n_head_k, rv2 = nh / n_head_v
+    float c;                    // |scale| * log2(e), at least 1e-30
+    int negq;                   // scale < 0: Q enters negated
+};
+hipError_t launch_fattn(const FaArgs& a, int D, bool qf32, bool kvf32, int B, hipStream_t st);
+
 }  // namespace mi355

@@ -88,6 +88,30 @@ def test_soft_max_and_fa_validation(mi):
     b.ne[1] = 5
     assert L.mi355_soft_max_ext(None, C.byref(a), None, 1.0, 0.0, C.byref(b)) == -4
 
+    # flash_attn_ext: q [D, nq, nh, B], k/v [D, nkv, nhk, B], dst [D, nh, nq, B]
+    def fa(D=64, nq=10, nkv=12, nh=4, nhk=2, tq=1, tk=1, tv=1, dne=None, vD=None):
+        q = mi.make_tensor(0x1000, tq, [D, nq, nh, 1])
+        k = mi.make_tensor(0x2000, tk, [D, nkv, nhk, 1])
+        v = mi.make_tensor(0x3000, tv, [vD or D, nkv, nhk, 1])
+        d = mi.make_tensor(0x4000, 0, dne or [vD or D, nh, nq, 1])
+        return q, k, v, d
+
+    def st(q, k, v, d, mask=None, bias=0.0, cap=0.0):
+        return L.mi355_flash_attn_ext(None, C.byref(q), C.byref(k), C.byref(v), mask, 0.125, bias, cap, C.byref(d))
+
+    q, k, v, d = fa()
+    assert st(q, k, v, d) == -4                       # valid, null context
+    assert b"null context" in L.mi355_last_error(None)
+    assert st(q, k, v, d, mask=C.byref(q)) == -3      # mask unsupported
+    assert st(q, k, v, d, bias=1.0) == -3             # ALiBi unsupported
+    assert st(q, k, v, d, cap=50.0) == -3             # softcap unsupported
+    assert st(*fa(D=80)) == -3                        # head size
+    assert st(*fa(vD=128)) == -3                      # Dv != D: valid ggml, not implemented
+    assert st(*fa(nhk=3)) == -4                       # 4 heads over 3 kv heads
+    assert st(*fa(dne=[64, 10, 4, 1])) == -4          # dst must be [Dv, nh, nq, B]
+    assert st(*fa(tk=1, tv=0)) == -3                  # k and v types differ
+    assert st(*fa(tq=8)) == -3                        # quantized q
+
 
 def test_workspace_size(mi):
     s0, s1, d = mm(mi, K=1024, N=4736, M=5184)
