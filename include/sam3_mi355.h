@@ -130,6 +130,78 @@ mi355_status mi355_flash_attn_ext(mi355_context* ctx, const mi355_tensor* q, con
                                   const mi355_tensor* v, const mi355_tensor* mask, float scale, float max_bias,
                                   float logit_softcap, const mi355_tensor* dst);
 
+/* ---- SAM3 ViT image encoder ----------------------------------------------
+ * The graph sam3_build_vit_graph builds (sam3.cpp:3836-3853) run on this
+ * backend: the prefix (patch embedding, tiled pos_embed, ln_pre;
+ * sam3.cpp:3810-3834) and sam3_vit_block_forward (sam3.cpp:3714-3805), with
+ * the memory-bound ggml nodes around each MUL_MAT / FLASH_ATTN_EXT fused
+ * into single passes that keep ggml's per-node fp32 rounding.
+ * Activations x are device F32 [grid*grid][E] in image token order
+ * (ggml [E, W, H, 1]).  All weight pointers are device pointers. */
+typedef struct mi355_vit_hparams {
+    int32_t embed_dim;   /* E (1024) */
+    int32_t num_heads;   /* 16; head size E / num_heads in {64, 96, 128} */
+    int32_t mlp_dim;     /* 4736 */
+    int32_t window_size; /* 24 */
+    int32_t grid;        /* tokens per image side: img_size / patch_size (72) */
+    int32_t patch_size;  /* 14 */
+    int32_t pos_grid;    /* side of pos_embed at pretrained resolution (24), tiled over the grid */
+    float eps;           /* LayerNorm eps (1e-5) */
+} mi355_vit_hparams;
+
+typedef struct mi355_vit_block {
+    /* linear weights [in, out] (ggml ne), F16 / Q8_0 / Q4_0 / Q4_1 (or F32) */
+    mi355_tensor qkv_w, proj_w, fc1_w, fc2_w;
+    const float* norm1_w;
+    const float* norm1_b;
+    const float* qkv_b;
+    const float* proj_b;
+    const float* norm2_w;
+    const float* norm2_b;
+    const float* fc1_b;
+    const float* fc2_b;
+    const float* freqs_cis; /* [N][head_dim/2][2] (cos, sin); N = window_size^2, or grid^2 if global; NULL: no RoPE */
+    int32_t is_global;      /* 0: attention inside window_size^2 windows (ggml_win_part) */
+} mi355_vit_block;
+
+/* Device bytes the encoder keeps for its activations (allocated on first use). */
+size_t mi355_vit_workspace_size(const mi355_vit_hparams* hp);
+/* x = ln_pre(conv2d_p(image) + tile(pos_embed)): image device F32 [3][H][W]
+ * with H = W = grid * patch_size; patch_w [P, P, 3, E] F32 or F16. */
+mi355_status mi355_vit_prefix(mi355_context* ctx, const mi355_vit_hparams* hp, const float* image,
+                              const mi355_tensor* patch_w, const float* pos_embed, const float* ln_pre_w,
+                              const float* ln_pre_b, float* x);
+/* x = sam3_vit_block_forward(x) in place. */
+mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams* hp, const mi355_vit_block* blk,
+                                     float* x);
+/* The whole encoder: prefix, then n_blocks blocks; x: [grid*grid][E] output. */
+mi355_status mi355_vit_encode(mi355_context* ctx, const mi355_vit_hparams* hp, const float* image,
+                              const mi355_tensor* patch_w, const float* pos_embed, const float* ln_pre_w,
+                              const float* ln_pre_b, const mi355_vit_block* blocks, int n_blocks, float* x);
+
+/* The fused node groups the encoder runs, for use by other graph builders
+ * and for testing each against ggml's node sequence:
+ * - layer_norm: y[row(r)] = ggml_add(ggml_mul(ggml_norm(x[r] (+ add[r']), eps), w), b)
+ *   (sam3_layer_norm, sam3.cpp:1041-1051); add (optional) is added first,
+ *   row r' = r, or (y%add_grid)*add_grid + x%add_grid when add_grid > 0
+ *   (ggml_repeat of pos_embed, sam3.cpp:3820-3826); row(r) is r, or its
+ *   ggml_win_part row when window > 0 (sam3.cpp:3734).  w, b may be NULL. */
+mi355_status mi355_vit_layer_norm(mi355_context* ctx, const float* x, const float* add, int add_grid, const float* w,
+                                  const float* b, float* y, int64_t rows, int E, int grid, int window, float eps);
+/* qkv [M][3E] (+ bias) -> Q, K (RoPE applied, sam3_apply_rope) and V as
+ * fp16 [M/N][NH][N][HD] (the FLASH_ATTN_EXT operand layout of
+ * sam3.cpp:3742-3778); rope [N][HD/2][2] or NULL. */
+mi355_status mi355_vit_qkv_rope(mi355_context* ctx, const float* qkv, const float* bias, const float* rope, void* q,
+                                void* k, void* v, int64_t M, int N, int n_heads, int head_dim);
+/* x[r] = x[r] + (p[row(r)] + b): proj bias, ggml_win_unpart (window > 0) and
+ * the residual add (sam3.cpp:3783-3791). */
+mi355_status mi355_vit_proj_residual(mi355_context* ctx, float* x, const float* p, const float* b, int64_t rows, int E,
+                                     int grid, int window);
+/* h = ggml_gelu_erf(h + b) over rows of n (sam3.cpp:3796-3797). */
+mi355_status mi355_vit_bias_gelu(mi355_context* ctx, float* h, const float* b, int64_t rows, int n);
+/* x = x + (f + b) over rows of n (sam3.cpp:3799-3802). */
+mi355_status mi355_vit_bias_residual(mi355_context* ctx, float* x, const float* f, const float* b, int64_t rows, int n);
+
 /* ---- Kernel timing --------------------------------------------------------
  * The device-side counterpart of the reference's timing around graph compute
  * (std::chrono, sam3.cpp:6122-6135) and of its per-op micro-bench

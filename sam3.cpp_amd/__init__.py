@@ -43,6 +43,21 @@ class Tensor(C.Structure):
                 ("nb", C.c_int64 * 4), ("data", C.c_void_p)]
 
 
+class VitHparams(C.Structure):
+    """struct mi355_vit_hparams."""
+    _fields_ = [("embed_dim", C.c_int32), ("num_heads", C.c_int32), ("mlp_dim", C.c_int32),
+                ("window_size", C.c_int32), ("grid", C.c_int32), ("patch_size", C.c_int32),
+                ("pos_grid", C.c_int32), ("eps", C.c_float)]
+
+
+class VitBlock(C.Structure):
+    """struct mi355_vit_block (device pointers)."""
+    _fields_ = [("qkv_w", Tensor), ("proj_w", Tensor), ("fc1_w", Tensor), ("fc2_w", Tensor),
+                ("norm1_w", C.c_void_p), ("norm1_b", C.c_void_p), ("qkv_b", C.c_void_p), ("proj_b", C.c_void_p),
+                ("norm2_w", C.c_void_p), ("norm2_b", C.c_void_p), ("fc1_b", C.c_void_p), ("fc2_b", C.c_void_p),
+                ("freqs_cis", C.c_void_p), ("is_global", C.c_int32)]
+
+
 def build(force: bool = False) -> str:
     """Compile the HIP sources for gfx950 (make -C sam3.cpp_amd)."""
     args = ["make", "-s", "-C", HERE, f"-j{min(16, os.cpu_count() or 1)}"]
@@ -85,6 +100,15 @@ def lib():
         "mi355_mul_mat_block_dots": (I, [P, T, T, P]),
         "mi355_soft_max_ext": (I, [P, T, T, F, F, T]),
         "mi355_flash_attn_ext": (I, [P, T, T, T, T, F, F, F, T]),
+        "mi355_vit_workspace_size": (SZ, [C.POINTER(VitHparams)]),
+        "mi355_vit_prefix": (I, [P, C.POINTER(VitHparams), P, T, P, P, P, P]),
+        "mi355_vit_block_forward": (I, [P, C.POINTER(VitHparams), C.POINTER(VitBlock), P]),
+        "mi355_vit_encode": (I, [P, C.POINTER(VitHparams), P, T, P, P, P, C.POINTER(VitBlock), I, P]),
+        "mi355_vit_layer_norm": (I, [P, P, P, I, P, P, P, C.c_int64, I, I, I, F]),
+        "mi355_vit_qkv_rope": (I, [P, P, P, P, P, P, P, C.c_int64, I, I, I]),
+        "mi355_vit_proj_residual": (I, [P, P, P, P, C.c_int64, I, I, I]),
+        "mi355_vit_bias_gelu": (I, [P, P, P, C.c_int64, I]),
+        "mi355_vit_bias_residual": (I, [P, P, P, P, C.c_int64, I]),
         "mi355_profile_enable": (I, [P, I]),
         "mi355_profile_collect": (I, [P]),
         "mi355_profile_get": (I, [P, I, C.POINTER(C.c_char_p), C.POINTER(I), C.POINTER(C.c_double)]),
@@ -185,6 +209,33 @@ class Context:
             out[name.value.decode()] = (cnt.value, ms.value)
         self.L.mi355_profile_reset(self.h)
         return out
+
+    # ---- SAM3 ViT encoder (pointers are device addresses, e.g. tensor.data_ptr())
+    def vit_layer_norm(self, x, add, add_grid, w, b, y, rows, E, grid=0, window=0, eps=1e-5):
+        self._check(self.L.mi355_vit_layer_norm(self.h, x, add, add_grid, w, b, y, rows, E, grid, window, eps))
+
+    def vit_qkv_rope(self, qkv, bias, rope, q, k, v, M, N, n_heads, head_dim):
+        self._check(self.L.mi355_vit_qkv_rope(self.h, qkv, bias, rope, q, k, v, M, N, n_heads, head_dim))
+
+    def vit_proj_residual(self, x, p, b, rows, E, grid=0, window=0):
+        self._check(self.L.mi355_vit_proj_residual(self.h, x, p, b, rows, E, grid, window))
+
+    def vit_bias_gelu(self, h, b, rows, n):
+        self._check(self.L.mi355_vit_bias_gelu(self.h, h, b, rows, n))
+
+    def vit_bias_residual(self, x, f, b, rows, n):
+        self._check(self.L.mi355_vit_bias_residual(self.h, x, f, b, rows, n))
+
+    def vit_prefix(self, hp: VitHparams, image, patch_w: Tensor, pos, ln_w, ln_b, x):
+        self._check(self.L.mi355_vit_prefix(self.h, C.byref(hp), image, C.byref(patch_w), pos, ln_w, ln_b, x))
+
+    def vit_block_forward(self, hp: VitHparams, blk: VitBlock, x):
+        self._check(self.L.mi355_vit_block_forward(self.h, C.byref(hp), C.byref(blk), x))
+
+    def vit_encode(self, hp: VitHparams, image, patch_w: Tensor, pos, ln_w, ln_b, blocks, x):
+        arr = (VitBlock * len(blocks))(*blocks)
+        self._check(self.L.mi355_vit_encode(self.h, C.byref(hp), image, C.byref(patch_w), pos, ln_w, ln_b, arr,
+                                            len(blocks), x))
 
     def flash_attn_ext(self, q: Tensor, k: Tensor, v: Tensor, dst: Tensor, scale: float):
         self._check(self.L.mi355_flash_attn_ext(self.h, C.byref(q), C.byref(k), C.byref(v), None, scale, 0.0, 0.0,

@@ -2,39 +2,16 @@
 // workspace management and kernel dispatch.  Every entry point validates on
 // the host before touching the GPU and reports problems as mi355_status,
 // never by aborting (sam3.cpp returns bool/nullptr on failure, CLAUDE.md:62).
-#include "sam3_mi355.h"
-
-#include <hip/hip_runtime.h>
-
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
-#include <map>
-#include <string>
-#include <vector>
 
-#include "kernels.h"
-
-struct mi355_context {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    void* ws = nullptr;
-    size_t ws_size = 0;
-    std::string last_error;
-    // kernel timing
-    bool prof = false;
-    struct Pending { const char* name; hipEvent_t a, b; };
-    std::vector<Pending> pending;
-    std::vector<std::string> names;
-    std::map<std::string, std::pair<int, double>> totals;
-};
-
-namespace {
-
-using namespace mi355;
+#include "context.h"
 
 thread_local std::string g_noctx_error;
+
+namespace mi355 {
 
 mi355_status fail(mi355_context* ctx, mi355_status st, const char* fmt, ...) {
     char buf[512];
@@ -86,6 +63,29 @@ SrcView view_of(const mi355_tensor* t) {
 constexpr size_t kAlign = 256;
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
+mi355_status ensure_buffer(mi355_context* ctx, void** buf, size_t* size, size_t bytes) {
+    if (bytes <= *size) return MI355_STATUS_SUCCESS;
+    if (*buf) {
+        hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) return hip_check(ctx, e, "hipStreamSynchronize");
+        (void)hipFree(*buf);
+        *buf = nullptr;
+        *size = 0;
+    }
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return fail(ctx, MI355_STATUS_ALLOC_FAILED, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    *buf = p;
+    *size = bytes;
+    return MI355_STATUS_SUCCESS;
+}
+
+}  // namespace mi355
+
+namespace {
+
+using namespace mi355;
+
 MatW matw_of(const mi355_tensor* s0) {
     MatW w;
     w.data = static_cast<const uint8_t*>(s0->data);
@@ -121,6 +121,7 @@ struct MmPlan {
 
 MmPlan mm_plan(const mi355_tensor* s0, const mi355_tensor* s1) {
     MmPlan pl;
+    if (s0->type == T_F32) return pl;
     const int64_t K = s1->ne[0], M = s1->ne[1], Z = s1->ne[2] * s1->ne[3];
     if (s0->type == T_F16) {
         if (!f16_src1_direct(s1)) pl.q = align_up((size_t)(Z * M * K) * 2);
@@ -133,45 +134,8 @@ MmPlan mm_plan(const mi355_tensor* s0, const mi355_tensor* s1) {
     pl.align = align_up(mmq_align_bytes(matw_of(s0), s0->ne[1], K));
     return pl;
 }
-mi355_status ensure_ws(mi355_context* ctx, size_t bytes) {
-    if (bytes <= ctx->ws_size) return MI355_STATUS_SUCCESS;
-    if (ctx->ws) {
-        // earlier kernels may still read the old buffer
-        hipError_t e = hipStreamSynchronize(ctx->stream);
-        if (e != hipSuccess) return hip_check(ctx, e, "hipStreamSynchronize");
-        (void)hipFree(ctx->ws);
-        ctx->ws = nullptr;
-        ctx->ws_size = 0;
-    }
-    void* p = nullptr;
-    hipError_t e = hipMalloc(&p, bytes);
-    if (e != hipSuccess) return fail(ctx, MI355_STATUS_ALLOC_FAILED, "workspace hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
-    ctx->ws = p;
-    ctx->ws_size = bytes;
-    return MI355_STATUS_SUCCESS;
-}
+mi355_status ensure_ws(mi355_context* ctx, size_t bytes) { return ensure_buffer(ctx, &ctx->ws, &ctx->ws_size, bytes); }
 
-// Brackets one launch with events when timing is enabled.
-struct Timed {
-    mi355_context* c;
-    const char* name;
-    hipEvent_t a = nullptr;
-    Timed(mi355_context* ctx, const char* n) : c(ctx), name(n) {
-        if (c && c->prof && hipEventCreate(&a) == hipSuccess) (void)hipEventRecord(a, c->stream);
-    }
-    hipError_t done(hipError_t e) {
-        if (!a) return e;
-        hipEvent_t b = nullptr;
-        if (hipEventCreate(&b) == hipSuccess) {
-            (void)hipEventRecord(b, c->stream);
-            c->pending.push_back({name, a, b});
-        } else {
-            (void)hipEventDestroy(a);
-        }
-        a = nullptr;
-        return e;
-    }
-};
 
 // ggml_mul_mat shape rules (ggml.c ggml_can_mul_mat / ggml_compute_forward_mul_mat)
 // plus what the kernels here implement.
@@ -181,7 +145,7 @@ mi355_status check_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
     if (!s0->data || !s1->data || !d->data) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: null data pointer");
     if (!dims_ok(s0) || !dims_ok(s1) || !dims_ok(d)) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: negative ne/nb");
     const int t0 = s0->type;
-    if (!(t0 == T_F16 || t0 == T_Q8_0 || t0 == T_Q4_0 || t0 == T_Q4_1))
+    if (!(t0 == T_F32 || t0 == T_F16 || t0 == T_Q8_0 || t0 == T_Q4_0 || t0 == T_Q4_1))
         return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat: src0 type %d not supported", t0);
     if (!(s1->type == T_F32 || (s1->type == T_F16 && t0 == T_F16)))
         return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat: src1 type %d with src0 type %d not supported", s1->type, t0);
@@ -201,7 +165,12 @@ mi355_status check_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
     const int64_t lim = (int64_t)1 << 30;
     if (K >= lim || s0->ne[1] >= lim || s1->ne[1] >= lim || s1->ne[2] * s1->ne[3] > 65535)
         return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat: dimensions beyond kernel limits");
-    if (t0 == T_F16) {
+    if (t0 == T_F32) {
+        if (s1->nb[0] != 4 || ((reinterpret_cast<uintptr_t>(s0->data) | (uintptr_t)s0->nb[1] | (uintptr_t)s0->nb[2] |
+                                (uintptr_t)s0->nb[3] | reinterpret_cast<uintptr_t>(s1->data) | (uintptr_t)s1->nb[1] |
+                                (uintptr_t)s1->nb[2] | (uintptr_t)s1->nb[3]) & 3))
+            return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat f32: needs contiguous, 4-byte aligned rows");
+    } else if (t0 == T_F16) {
         if (K % 8 != 0 || s0->nb[1] % 16 != 0 || (reinterpret_cast<uintptr_t>(s0->data) & 15) ||
             s0->nb[2] % 16 != 0 || s0->nb[3] % 16 != 0)
             return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat f16: needs K %% 8 == 0 and 16-byte aligned rows");
@@ -277,6 +246,7 @@ void mi355_context_free(mi355_context* ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     mi355_profile_reset(ctx);
     if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->enc) (void)hipFree(ctx->enc);
     delete ctx;
 }
 
@@ -294,7 +264,8 @@ mi355_status mi355_reserve_workspace(mi355_context* ctx, size_t bytes) {
 
 size_t mi355_mul_mat_workspace_size(const mi355_tensor* s0, const mi355_tensor* s1) {
     if (!s0 || !s1) return 0;
-    if (s0->type != T_F16 && s0->type != T_Q8_0 && s0->type != T_Q4_0 && s0->type != T_Q4_1) return 0;
+    if (s0->type != T_F32 && s0->type != T_F16 && s0->type != T_Q8_0 && s0->type != T_Q4_0 && s0->type != T_Q4_1)
+        return 0;
     return mm_plan(s0, s1).total();
 }
 
@@ -310,6 +281,21 @@ mi355_status mi355_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
     (void)hipSetDevice(ctx->device);
     const int64_t K = s0->ne[0], N = s0->ne[1], M = s1->ne[1];
     if (K == 0 || N == 0 || M == 0 || s1->ne[2] * s1->ne[3] == 0) return MI355_STATUS_SUCCESS;
+    if (s0->type == T_F32) {
+        GemmF32Args g;
+        g.W = static_cast<const float*>(s0->data);
+        g.w_nb1 = s0->nb[1]; g.w_nb2 = s0->nb[2]; g.w_nb3 = s0->nb[3];
+        g.X = static_cast<const float*>(s1->data);
+        g.x_nb1 = s1->nb[1]; g.x_nb2 = s1->nb[2]; g.x_nb3 = s1->nb[3];
+        g.D = static_cast<float*>(d->data);
+        g.d_nb1 = d->nb[1]; g.d_nb2 = d->nb[2]; g.d_nb3 = d->nb[3];
+        g.M = (int)M; g.N = (int)N; g.K = (int)K;
+        g.ne12 = (int)s1->ne[2];
+        g.r2 = (int)(s1->ne[2] / s0->ne[2]);
+        g.r3 = (int)(s1->ne[3] / s0->ne[3]);
+        Timed tg(ctx, "gemm_f32");
+        return hip_check(ctx, tg.done(launch_gemm_f32(g, (int)(s1->ne[2] * s1->ne[3]), ctx->stream)), "gemm_f32 launch");
+    }
     const MmPlan pl = mm_plan(s0, s1);
     st = ensure_ws(ctx, pl.total());
     if (st != MI355_STATUS_SUCCESS) return st;
@@ -348,7 +334,8 @@ mi355_status mi355_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
 mi355_status mi355_mul_mat_block_dots(mi355_context* ctx, const mi355_tensor* s0, const mi355_tensor* s1,
                                       int32_t* isums) {
     if (!s0 || !s1 || !isums) return fail(ctx, MI355_STATUS_INVALID_ARG, "block_dots: null argument");
-    if (s0->type == T_F16) return fail(ctx, MI355_STATUS_INVALID_ARG, "block_dots: src0 must be a block type");
+    if (s0->type == T_F16 || s0->type == T_F32)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "block_dots: src0 must be a block type");
     mi355_tensor d{};
     d.type = T_F32;
     d.ne[0] = s0->ne[1];

@@ -1,0 +1,66 @@
+// Host-side internals shared by the C-ABI translation units: the context
+// object behind mi355_context* and the validation / error / timing helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "kernels.h"
+#include "sam3_mi355.h"
+
+struct mi355_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    void* ws = nullptr;        // per-call scratch of mul_mat (activation operand, scales)
+    size_t ws_size = 0;
+    void* enc = nullptr;       // activation buffers of the image-encoder runner
+    size_t enc_size = 0;
+    std::string last_error;
+    // kernel timing
+    bool prof = false;
+    struct Pending { const char* name; hipEvent_t a, b; };
+    std::vector<Pending> pending;
+    std::vector<std::string> names;
+    std::map<std::string, std::pair<int, double>> totals;
+};
+
+namespace mi355 {
+
+mi355_status fail(mi355_context* ctx, mi355_status st, const char* fmt, ...);
+mi355_status hip_check(mi355_context* ctx, hipError_t e, const char* what);
+int64_t type_size(int t);
+int blck(int t);
+int64_t row_size(int t, int64_t ne0);
+bool dims_ok(const mi355_tensor* t);
+SrcView view_of(const mi355_tensor* t);
+size_t align_up(size_t x);
+// Grows a device buffer owned by the context to at least bytes (waits for the
+// stream first: earlier kernels may still read the old buffer).
+mi355_status ensure_buffer(mi355_context* ctx, void** buf, size_t* size, size_t bytes);
+
+// Brackets one launch with events when timing is enabled.
+struct Timed {
+    mi355_context* c;
+    const char* name;
+    hipEvent_t a = nullptr;
+    Timed(mi355_context* ctx, const char* n) : c(ctx), name(n) {
+        if (c && c->prof && hipEventCreate(&a) == hipSuccess) (void)hipEventRecord(a, c->stream);
+    }
+    hipError_t done(hipError_t e) {
+        if (!a) return e;
+        hipEvent_t b = nullptr;
+        if (hipEventCreate(&b) == hipSuccess) {
+            (void)hipEventRecord(b, c->stream);
+            c->pending.push_back({name, a, b});
+        } else {
+            (void)hipEventDestroy(a);
+        }
+        a = nullptr;
+        return e;
+    }
+};
+
+}  // namespace mi355

@@ -1,0 +1,237 @@
+// Memory-bound ops of the SAM3 ViT image encoder around the MUL_MAT and
+// FLASH_ATTN_EXT nodes, each fusing the ggml nodes that touch the same
+// tensor once.  Every ggml node rounds its result to fp32, so each fused
+// step keeps that rounding: no FMA contraction in this file.
+//   ln_kernel          ggml_norm(eps) -> mul(w) -> add(b) (sam3_layer_norm,
+//                      sam3.cpp:1041-1051), with an optional preceding add
+//                      (patch + tiled pos_embed, sam3.cpp:3820-3826) and the
+//                      ggml_win_part token order on output (sam3.cpp:3734)
+//   qkv_rope_kernel    add(qkv_b), Q/K/V split + permute (sam3.cpp:3742-3767),
+//                      sam3_apply_rope on Q and K (sam3.cpp:3671-3710); writes
+//                      fp16 Q/K/V [B][NH][N][HD] for FLASH_ATTN_EXT
+//   proj_residual_kernel  add(proj_b) -> ggml_win_unpart -> add(shortcut)
+//                      (sam3.cpp:3783-3791)
+//   bias_gelu_kernel   add(fc1_b) -> ggml_gelu_erf (sam3.cpp:3796-3797)
+//   bias_residual_kernel  add(fc2_b) -> add(shortcut) (sam3.cpp:3799-3802)
+//   im2col_kernel      ggml_conv_2d_sk_p0 input columns (sam3.cpp:3815)
+#pragma clang fp contract(off)
+#include "common.cuh"
+#include "kernels.h"
+
+namespace mi355 {
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// token r of a grid x grid image (row-major, r = y*grid + x) -> its row in
+// ggml_win_part order (window (y/ws, x/ws) row-major, then y%ws, x%ws)
+__device__ __forceinline__ int64_t win_row(int64_t r, int grid, int ws) {
+    const int y = (int)(r / grid), x = (int)(r % grid);
+    const int nwx = grid / ws;
+    return (((int64_t)(y / ws) * nwx + x / ws) * ws + y % ws) * ws + x % ws;
+}
+
+// One wavefront per row of E (E % 64 == 0, E <= 2048).
+__global__ __launch_bounds__(256) void ln_kernel(const LnArgs a) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= a.rows) return;
+    const int lane = threadIdx.x & 63, E = a.E, per = E / 64;
+    const float* xr = a.x + r * E;
+    const float* ar = nullptr;
+    if (a.add) {
+        int64_t pr = r;
+        if (a.add_grid > 0) {  // pos_embed [pg x pg] tiled over the grid x grid image
+            const int y = (int)(r / a.grid), x = (int)(r % a.grid);
+            pr = (int64_t)(y % a.add_grid) * a.add_grid + x % a.add_grid;
+        }
+        ar = a.add + pr * E;
+    }
+    float v[32];
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        if (j < per) {
+            float t = xr[j * 64 + lane];
+            if (ar) t = t + ar[j * 64 + lane];
+            v[j] = t;
+            s += (double)t;
+        }
+    }
+    s = wave_sum_d(s);
+    const float mean = (float)(s / (double)E);
+    double s2 = 0.0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        if (j < per) {
+            const float t = v[j] - mean;
+            v[j] = t;
+            s2 += (double)(t * t);
+        }
+    }
+    s2 = wave_sum_d(s2);
+    const float var = (float)(s2 / (double)E);
+    const float scale = 1.0f / sqrtf(var + a.eps);
+    const int64_t orow = a.ws > 0 ? win_row(r, a.grid, a.ws) : r;
+    float* yr = a.y + orow * E;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        if (j < per) {
+            const int e = j * 64 + lane;
+            float t = v[j] * scale;
+            if (a.w) t = t * a.w[e];
+            if (a.b) t = t + a.b[e];
+            yr[e] = t;
+        }
+    }
+}
+
+// thread per (token row m, head h, pair i): rows m of qkv are [q | k | v] of E each
+__global__ __launch_bounds__(256) void qkv_rope_kernel(const QkvArgs a) {
+    const int half = a.HD / 2;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t total = (int64_t)a.M * a.NH * half;
+    if (t >= total) return;
+    const int i = (int)(t % half);
+    const int h = (int)((t / half) % a.NH);
+    const int64_t m = t / ((int64_t)half * a.NH);
+    const int E = a.NH * a.HD;
+    const int64_t bwin = m / a.N, n = m % a.N;
+    const int e = h * a.HD + 2 * i;
+    const float* row = a.qkv + m * (int64_t)(3 * E);
+    float q0 = row[e] + a.bias[e], q1 = row[e + 1] + a.bias[e + 1];
+    float k0 = row[E + e] + a.bias[E + e], k1 = row[E + e + 1] + a.bias[E + e + 1];
+    const float v0 = row[2 * E + e] + a.bias[2 * E + e], v1 = row[2 * E + e + 1] + a.bias[2 * E + e + 1];
+    if (a.rope) {
+        const float c = a.rope[n * a.HD + 2 * i], s = a.rope[n * a.HD + 2 * i + 1];
+        const float qa = q0 * c, qb = q1 * s, qc = q0 * s, qd = q1 * c;
+        const float ka = k0 * c, kb = k1 * s, kc = k0 * s, kd = k1 * c;
+        q0 = qa - qb;
+        q1 = qc + qd;
+        k0 = ka - kb;
+        k1 = kc + kd;
+    }
+    const int64_t o = ((bwin * a.NH + h) * a.N + n) * a.HD + 2 * i;
+    *reinterpret_cast<uint32_t*>(a.q + o) = (uint32_t)f2h(q0) | ((uint32_t)f2h(q1) << 16);
+    *reinterpret_cast<uint32_t*>(a.k + o) = (uint32_t)f2h(k0) | ((uint32_t)f2h(k1) << 16);
+    *reinterpret_cast<uint32_t*>(a.v + o) = (uint32_t)f2h(v0) | ((uint32_t)f2h(v1) << 16);
+}
+
+// x[r] = x[r] + (p[row(r)] + b), 4 elements per thread; row(r) = win_part row or r
+__global__ __launch_bounds__(256) void proj_residual_kernel(float* __restrict__ x, const float* __restrict__ p,
+                                                            const float* __restrict__ b, int64_t rows, int E, int grid,
+                                                            int ws) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int E4 = E / 4;
+    if (t >= rows * E4) return;
+    const int64_t r = t / E4;
+    const int e = (int)(t % E4) * 4;
+    const int64_t pr = ws > 0 ? win_row(r, grid, ws) : r;
+    const v4f pv = *reinterpret_cast<const v4f*>(p + pr * E + e);
+    const v4f bv = *reinterpret_cast<const v4f*>(b + e);
+    v4f xv = *reinterpret_cast<const v4f*>(x + r * E + e);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float u = pv[j] + bv[j];
+        xv[j] = xv[j] + u;
+    }
+    *reinterpret_cast<v4f*>(x + r * E + e) = xv;
+}
+
+// h = gelu_erf(h + b) in place over rows of n (ggml_vec_gelu_erf_f32: 0.5*x*(1 + erf(x/sqrt(2))))
+__global__ __launch_bounds__(256) void bias_gelu_kernel(float* __restrict__ h, const float* __restrict__ b, int64_t rows,
+                                                        int n) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int n4 = n / 4;
+    if (t >= rows * n4) return;
+    const int64_t r = t / n4;
+    const int c = (int)(t % n4) * 4;
+    v4f hv = *reinterpret_cast<const v4f*>(h + r * n + c);
+    const v4f bv = *reinterpret_cast<const v4f*>(b + c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float u = hv[j] + bv[j];
+        const float hx = 0.5f * u;
+        hv[j] = hx * (1.0f + erff(u * 0.70710678118654752440f));
+    }
+    *reinterpret_cast<v4f*>(h + r * n + c) = hv;
+}
+
+// x = x + (f + b) over rows of n
+__global__ __launch_bounds__(256) void bias_residual_kernel(float* __restrict__ x, const float* __restrict__ f,
+                                                            const float* __restrict__ b, int64_t rows, int n) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int n4 = n / 4;
+    if (t >= rows * n4) return;
+    const int64_t r = t / n4;
+    const int c = (int)(t % n4) * 4;
+    v4f xv = *reinterpret_cast<const v4f*>(x + r * n + c);
+    const v4f fv = *reinterpret_cast<const v4f*>(f + r * n + c);
+    const v4f bv = *reinterpret_cast<const v4f*>(b + c);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float u = fv[j] + bv[j];
+        xv[j] = xv[j] + u;
+    }
+    *reinterpret_cast<v4f*>(x + r * n + c) = xv;
+}
+
+// cols[m][k], m = py*grid + px, k = (c*P + ky)*P + kx  <-  img[c][py*P + ky][px*P + kx]
+__global__ __launch_bounds__(256) void im2col_kernel(const float* __restrict__ img, float* __restrict__ cols, int C,
+                                                     int Himg, int Wimg, int P, int grid) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int K = C * P * P;
+    const int64_t total = (int64_t)grid * grid * K;
+    if (t >= total) return;
+    const int k = (int)(t % K);
+    const int64_t m = t / K;
+    const int kx = k % P, ky = (k / P) % P, c = k / (P * P);
+    const int px = (int)(m % grid), py = (int)(m / grid);
+    const int y = py * P + ky, x = px * P + kx;
+    cols[t] = (y < Himg && x < Wimg) ? img[((int64_t)c * Himg + y) * Wimg + x] : 0.0f;
+}
+
+static unsigned blocks_for(int64_t n, int per_block = 256) { return (unsigned)((n + per_block - 1) / per_block); }
+
+hipError_t launch_layer_norm(const LnArgs& a, hipStream_t st) {
+    if (a.rows <= 0) return hipSuccess;
+    if (a.E % 64 != 0 || a.E > 2048) return hipErrorInvalidValue;
+    ln_kernel<<<blocks_for(a.rows, 4), 256, 0, st>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t st) {
+    const int64_t total = (int64_t)a.M * a.NH * (a.HD / 2);
+    if (total <= 0) return hipSuccess;
+    qkv_rope_kernel<<<blocks_for(total), 256, 0, st>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_proj_residual(float* x, const float* p, const float* b, int64_t rows, int E, int grid, int ws,
+                                hipStream_t st) {
+    if (E % 4) return hipErrorInvalidValue;
+    proj_residual_kernel<<<blocks_for(rows * (E / 4)), 256, 0, st>>>(x, p, b, rows, E, grid, ws);
+    return hipGetLastError();
+}
+
+hipError_t launch_bias_gelu(float* h, const float* b, int64_t rows, int n, hipStream_t st) {
+    if (n % 4) return hipErrorInvalidValue;
+    bias_gelu_kernel<<<blocks_for(rows * (n / 4)), 256, 0, st>>>(h, b, rows, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_bias_residual(float* x, const float* f, const float* b, int64_t rows, int n, hipStream_t st) {
+    if (n % 4) return hipErrorInvalidValue;
+    bias_residual_kernel<<<blocks_for(rows * (n / 4)), 256, 0, st>>>(x, f, b, rows, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_im2col(const float* img, float* cols, int C, int Himg, int Wimg, int P, int grid, hipStream_t st) {
+    const int64_t total = (int64_t)grid * grid * C * P * P;
+    im2col_kernel<<<blocks_for(total), 256, 0, st>>>(img, cols, C, Himg, Wimg, P, grid);
+    return hipGetLastError();
+}
+
+}  // namespace mi355

@@ -84,4 +84,49 @@ struct FaArgs {
 };
 hipError_t launch_fattn(const FaArgs& a, int D, bool qf32, bool kvf32, int B, hipStream_t st);
 
+// F32 x F32 MUL_MAT: D[z][m][n] = sum_k X[z][m][k] W[z'][n][k] (byte strides).
+struct GemmF32Args {
+    const float* W;
+    int64_t w_nb1, w_nb2, w_nb3;
+    const float* X;
+    int64_t x_nb1, x_nb2, x_nb3;
+    float* D;
+    int64_t d_nb1, d_nb2, d_nb3;
+    int M, N, K, ne12, r2, r3;
+};
+hipError_t launch_gemm_f32(const GemmF32Args& a, int Z, hipStream_t st);
+
+// ---- SAM3 ViT glue (rows of E contiguous floats)
+struct LnArgs {
+    const float* x;     // [rows][E], image token order
+    const float* add;   // optional addend before the norm: same rows, or a tiled [add_grid^2][E] table
+    int add_grid;       // > 0: add row = (y % add_grid) * add_grid + x % add_grid
+    const float* w;     // optional affine (ggml_mul), [E]
+    const float* b;     // optional affine (ggml_add), [E]
+    float* y;           // [rows][E]; row win_row(r) when ws > 0, else r
+    int64_t rows;
+    int E;
+    int grid;           // tokens per image side (rows = grid^2 when ws > 0 or add_grid > 0)
+    int ws;             // window size of the output order (0: image order)
+    float eps;
+};
+hipError_t launch_layer_norm(const LnArgs& a, hipStream_t st);
+
+struct QkvArgs {
+    const float* qkv;   // [M][3E] (rows in attention-batch order)
+    const float* bias;  // [3E]
+    const float* rope;  // [N][HD/2][2] (cos, sin) or null
+    _Float16* q;        // [M/N][NH][N][HD] each
+    _Float16* k;
+    _Float16* v;
+    int64_t M;
+    int N, NH, HD;
+};
+hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t st);
+hipError_t launch_proj_residual(float* x, const float* p, const float* b, int64_t rows, int E, int grid, int ws,
+                                hipStream_t st);
+hipError_t launch_bias_gelu(float* h, const float* b, int64_t rows, int n, hipStream_t st);
+hipError_t launch_bias_residual(float* x, const float* f, const float* b, int64_t rows, int n, hipStream_t st);
+hipError_t launch_im2col(const float* img, float* cols, int C, int Himg, int Wimg, int P, int grid, hipStream_t st);
+
 }  // namespace mi355

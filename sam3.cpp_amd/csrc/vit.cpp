@@ -1,0 +1,302 @@
+// SAM3 ViT image encoder on the MI355X backend: the graph of
+// sam3_build_vit_graph (sam3.cpp:3836-3853) executed node group by node
+// group.  MUL_MAT and FLASH_ATTN_EXT go through the same entry points a ggml
+// graph would use; the memory-bound nodes between them run as the fused
+// passes of glue.hip.  Per block (sam3_vit_block_forward, sam3.cpp:3714-3805):
+//
+//   xn   = LN1(x)                  [window order when windowed: win_part]
+//   qkv  = mul_mat(qkv_w, xn)
+//   q,k,v = split(qkv + qkv_b), RoPE(q), RoPE(k)    -> fp16
+//   attn = flash_attn_ext(q, k, v, 1/sqrt(HD))      [E, M]
+//   p    = mul_mat(proj_w, attn)
+//   x    = x + win_unpart(p + proj_b)
+//   xn   = LN2(x)
+//   h    = gelu_erf(mul_mat(fc1_w, xn) + fc1_b)
+//   x    = x + (mul_mat(fc2_w, h) + fc2_b)
+//
+// The activation buffers live in one device allocation owned by the context
+// (mi355_vit_workspace_size); mul_mat keeps using the context's own scratch.
+#include <cmath>
+
+#include "context.h"
+
+using namespace mi355;
+
+namespace {
+
+struct EncBufs {
+    float* xn;      // [M][E]  LN output, projection output
+    float* qkv;     // [M][3E]
+    _Float16* q;    // [M][E] each, FLASH_ATTN_EXT layout
+    _Float16* k;
+    _Float16* v;
+    float* attn;    // [M][E]  attention output, fc2 output
+    float* big;     // [M][MLP] fc1 output (or im2col columns)
+};
+
+size_t enc_bytes(const mi355_vit_hparams* hp, EncBufs* b, char* base) {
+    const size_t M = (size_t)hp->grid * hp->grid, E = (size_t)hp->embed_dim;
+    const size_t kpatch = 3 * (size_t)hp->patch_size * hp->patch_size;
+    const size_t big = M * std::max((size_t)hp->mlp_dim, kpatch) * 4;
+    const size_t sz[7] = {M * E * 4, M * 3 * E * 4, M * E * 2, M * E * 2, M * E * 2, M * E * 4, big};
+    size_t off[7], o = 0;
+    for (int i = 0; i < 7; ++i) {
+        off[i] = o;
+        o += align_up(sz[i]);
+    }
+    if (b && base) {
+        b->xn = reinterpret_cast<float*>(base + off[0]);
+        b->qkv = reinterpret_cast<float*>(base + off[1]);
+        b->q = reinterpret_cast<_Float16*>(base + off[2]);
+        b->k = reinterpret_cast<_Float16*>(base + off[3]);
+        b->v = reinterpret_cast<_Float16*>(base + off[4]);
+        b->attn = reinterpret_cast<float*>(base + off[5]);
+        b->big = reinterpret_cast<float*>(base + off[6]);
+    }
+    return o;
+}
+
+mi355_status check_hp(mi355_context* ctx, const mi355_vit_hparams* hp) {
+    if (!hp) return fail(ctx, MI355_STATUS_INVALID_ARG, "vit: null hparams");
+    const int E = hp->embed_dim, NH = hp->num_heads;
+    if (E <= 0 || NH <= 0 || E % NH != 0 || hp->mlp_dim <= 0 || hp->grid <= 0 || hp->patch_size <= 0 ||
+        hp->window_size < 0 || hp->pos_grid < 0 || !(hp->eps >= 0.0f))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "vit: bad hparams");
+    const int HD = E / NH;
+    if (!(HD == 64 || HD == 96 || HD == 128))
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "vit: head size %d (supported: 64, 96, 128)", HD);
+    if (E % 64 != 0 || E > 2048) return fail(ctx, MI355_STATUS_UNSUPPORTED, "vit: embed_dim must be a multiple of 64, <= 2048");
+    if (hp->mlp_dim % 4 != 0) return fail(ctx, MI355_STATUS_UNSUPPORTED, "vit: mlp_dim must be a multiple of 4");
+    if ((int64_t)hp->grid * hp->grid * std::max(3 * E, hp->mlp_dim) >= ((int64_t)1 << 31))
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "vit: activations beyond 2^31 elements");
+    return MI355_STATUS_SUCCESS;
+}
+
+// contiguous F32 / F16 tensor over a device buffer
+mi355_tensor dev_tensor(const void* p, int type, int64_t ne0, int64_t ne1, int64_t ne2 = 1, int64_t ne3 = 1) {
+    mi355_tensor t{};
+    t.type = type;
+    t.ne[0] = ne0;
+    t.ne[1] = ne1;
+    t.ne[2] = ne2;
+    t.ne[3] = ne3;
+    t.nb[0] = type == T_F32 ? 4 : 2;
+    t.nb[1] = t.nb[0] * ne0;
+    t.nb[2] = t.nb[1] * ne1;
+    t.nb[3] = t.nb[2] * ne2;
+    t.data = const_cast<void*>(p);
+    return t;
+}
+
+mi355_status get_bufs(mi355_context* ctx, const mi355_vit_hparams* hp, EncBufs* b) {
+    const size_t need = enc_bytes(hp, nullptr, nullptr);
+    mi355_status st = ensure_buffer(ctx, &ctx->enc, &ctx->enc_size, need);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    enc_bytes(hp, b, static_cast<char*>(ctx->enc));
+    return MI355_STATUS_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mi355_vit_workspace_size(const mi355_vit_hparams* hp) {
+    if (check_hp(nullptr, hp) != MI355_STATUS_SUCCESS) return 0;
+    return enc_bytes(hp, nullptr, nullptr);
+}
+
+mi355_status mi355_vit_layer_norm(mi355_context* ctx, const float* x, const float* add, int add_grid, const float* w,
+                                  const float* b, float* y, int64_t rows, int E, int grid, int window, float eps) {
+    if (!x || !y) return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_layer_norm: null x/y");
+    if (rows < 0 || E <= 0 || add_grid < 0 || window < 0 || !(eps >= 0.0f))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_layer_norm: bad sizes");
+    if (E % 64 != 0 || E > 2048) return fail(ctx, MI355_STATUS_UNSUPPORTED, "vit_layer_norm: E must be a multiple of 64, <= 2048");
+    if ((window > 0 || (add && add_grid > 0)) && ((int64_t)grid * grid != rows || grid <= 0))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_layer_norm: rows must be grid^2 for window / tiled add");
+    if (window > 0 && grid % window != 0)
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "vit_layer_norm: grid %d not a multiple of the window %d", grid, window);
+    if (x == y && window > 0) return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_layer_norm: window reorder cannot run in place");
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "vit_layer_norm: null context");
+    LnArgs a;
+    a.x = x;
+    a.add = add;
+    a.add_grid = add ? add_grid : 0;
+    a.w = w;
+    a.b = b;
+    a.y = y;
+    a.rows = rows;
+    a.E = E;
+    a.grid = grid;
+    a.ws = window;
+    a.eps = eps;
+    (void)hipSetDevice(ctx->device);
+    Timed t(ctx, "layer_norm");
+    return hip_check(ctx, t.done(launch_layer_norm(a, ctx->stream)), "layer_norm launch");
+}
+
+mi355_status mi355_vit_qkv_rope(mi355_context* ctx, const float* qkv, const float* bias, const float* rope, void* q,
+                                void* k, void* v, int64_t M, int N, int n_heads, int head_dim) {
+    if (!qkv || !bias || !q || !k || !v) return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_qkv_rope: null pointer");
+    if (M < 0 || N <= 0 || n_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0 || M % N != 0)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_qkv_rope: bad sizes");
+    if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 3) != 0)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_qkv_rope: q/k/v must be 4-byte aligned");
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "vit_qkv_rope: null context");
+    QkvArgs a;
+    a.qkv = qkv;
+    a.bias = bias;
+    a.rope = rope;
+    a.q = static_cast<_Float16*>(q);
+    a.k = static_cast<_Float16*>(k);
+    a.v = static_cast<_Float16*>(v);
+    a.M = M;
+    a.N = N;
+    a.NH = n_heads;
+    a.HD = head_dim;
+    (void)hipSetDevice(ctx->device);
+    Timed t(ctx, "qkv_rope");
+    return hip_check(ctx, t.done(launch_qkv_rope(a, ctx->stream)), "qkv_rope launch");
+}
+
+mi355_status mi355_vit_proj_residual(mi355_context* ctx, float* x, const float* p, const float* b, int64_t rows, int E,
+                                     int grid, int window) {
+    if (!x || !p || !b) return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_proj_residual: null pointer");
+    if (rows < 0 || E <= 0 || E % 4 != 0 || window < 0) return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_proj_residual: bad sizes");
+    if (window > 0 && (grid <= 0 || (int64_t)grid * grid != rows || grid % window != 0))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_proj_residual: rows must be grid^2 with grid a multiple of the window");
+    if (window > 0 && x == p) return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_proj_residual: window reorder cannot run in place");
+    if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(b)) & 15) != 0)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_proj_residual: pointers must be 16-byte aligned");
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "vit_proj_residual: null context");
+    (void)hipSetDevice(ctx->device);
+    Timed t(ctx, "proj_residual");
+    return hip_check(ctx, t.done(launch_proj_residual(x, p, b, rows, E, grid, window, ctx->stream)), "proj_residual launch");
+}
+
+mi355_status mi355_vit_bias_gelu(mi355_context* ctx, float* h, const float* b, int64_t rows, int n) {
+    if (!h || !b) return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_bias_gelu: null pointer");
+    if (rows < 0 || n <= 0 || n % 4 != 0) return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_bias_gelu: bad sizes (n %% 4 == 0)");
+    if (((reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(b)) & 15) != 0)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_bias_gelu: pointers must be 16-byte aligned");
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "vit_bias_gelu: null context");
+    (void)hipSetDevice(ctx->device);
+    Timed t(ctx, "bias_gelu");
+    return hip_check(ctx, t.done(launch_bias_gelu(h, b, rows, n, ctx->stream)), "bias_gelu launch");
+}
+
+mi355_status mi355_vit_bias_residual(mi355_context* ctx, float* x, const float* f, const float* b, int64_t rows, int n) {
+    if (!x || !f || !b) return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_bias_residual: null pointer");
+    if (rows < 0 || n <= 0 || n % 4 != 0) return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_bias_residual: bad sizes (n %% 4 == 0)");
+    if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(f) | reinterpret_cast<uintptr_t>(b)) & 15) != 0)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_bias_residual: pointers must be 16-byte aligned");
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "vit_bias_residual: null context");
+    (void)hipSetDevice(ctx->device);
+    Timed t(ctx, "bias_residual");
+    return hip_check(ctx, t.done(launch_bias_residual(x, f, b, rows, n, ctx->stream)), "bias_residual launch");
+}
+
+mi355_status mi355_vit_prefix(mi355_context* ctx, const mi355_vit_hparams* hp, const float* image,
+                              const mi355_tensor* patch_w, const float* pos_embed, const float* ln_pre_w,
+                              const float* ln_pre_b, float* x) {
+    mi355_status st = check_hp(ctx, hp);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    if (!image || !patch_w || !pos_embed || !ln_pre_w || !ln_pre_b || !x)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_prefix: null pointer");
+    const int E = hp->embed_dim, P = hp->patch_size, G = hp->grid;
+    const int64_t K = 3LL * P * P, M = (int64_t)G * G;
+    if (patch_w->ne[0] != P || patch_w->ne[1] != P || patch_w->ne[2] != 3 || patch_w->ne[3] != E)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_prefix: patch weight must be [P, P, 3, E]");
+    if (hp->pos_grid <= 0 || G % hp->pos_grid != 0)
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "vit_prefix: grid must be a multiple of pos_grid");
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "vit_prefix: null context");
+    (void)hipSetDevice(ctx->device);
+    EncBufs b;
+    st = get_bufs(ctx, hp, &b);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    {
+        Timed t(ctx, "im2col");
+        st = hip_check(ctx, t.done(launch_im2col(image, b.big, 3, G * P, G * P, P, G, ctx->stream)), "im2col launch");
+        if (st != MI355_STATUS_SUCCESS) return st;
+    }
+    // conv weight [P, P, 3, E] viewed as ggml [K, E]
+    mi355_tensor w = *patch_w;
+    w.ne[0] = K;
+    w.ne[1] = E;
+    w.ne[2] = w.ne[3] = 1;
+    w.nb[1] = patch_w->nb[3];
+    w.nb[2] = w.nb[3] = w.nb[1] * E;
+    const mi355_tensor cols = dev_tensor(b.big, T_F32, K, M);
+    const mi355_tensor out = dev_tensor(b.xn, T_F32, E, M);
+    st = mi355_mul_mat(ctx, &w, &cols, &out);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    return mi355_vit_layer_norm(ctx, b.xn, pos_embed, hp->pos_grid, ln_pre_w, ln_pre_b, x, M, E, G, 0, hp->eps);
+}
+
+mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams* hp, const mi355_vit_block* blk,
+                                     float* x) {
+    mi355_status st = check_hp(ctx, hp);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    if (!blk || !x || !blk->norm1_w || !blk->norm1_b || !blk->qkv_b || !blk->proj_b || !blk->norm2_w || !blk->norm2_b ||
+        !blk->fc1_b || !blk->fc2_b)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_block: null pointer");
+    const int E = hp->embed_dim, NH = hp->num_heads, HD = E / NH, MLP = hp->mlp_dim, G = hp->grid;
+    const int WS = blk->is_global ? 0 : hp->window_size;
+    if (!blk->is_global && (WS <= 0 || G % WS != 0))
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "vit_block: grid %d not a multiple of the window %d", G, WS);
+    const int64_t M = (int64_t)G * G;
+    const int N = WS > 0 ? WS * WS : (int)M;  // tokens per attention batch
+    const int B = (int)(M / N);
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "vit_block: null context");
+    (void)hipSetDevice(ctx->device);
+    EncBufs b;
+    st = get_bufs(ctx, hp, &b);
+    if (st != MI355_STATUS_SUCCESS) return st;
+
+#define TRY(e)                                   \
+    do {                                         \
+        st = (e);                                \
+        if (st != MI355_STATUS_SUCCESS) return st; \
+    } while (0)
+    // attention
+    TRY(mi355_vit_layer_norm(ctx, x, nullptr, 0, blk->norm1_w, blk->norm1_b, b.xn, M, E, G, WS, hp->eps));
+    {
+        const mi355_tensor in = dev_tensor(b.xn, T_F32, E, M), out = dev_tensor(b.qkv, T_F32, 3 * E, M);
+        TRY(mi355_mul_mat(ctx, &blk->qkv_w, &in, &out));
+    }
+    TRY(mi355_vit_qkv_rope(ctx, b.qkv, blk->qkv_b, blk->freqs_cis, b.q, b.k, b.v, M, N, NH, HD));
+    {
+        const mi355_tensor q = dev_tensor(b.q, T_F16, HD, N, NH, B), k = dev_tensor(b.k, T_F16, HD, N, NH, B),
+                           v = dev_tensor(b.v, T_F16, HD, N, NH, B), o = dev_tensor(b.attn, T_F32, HD, NH, N, B);
+        TRY(mi355_flash_attn_ext(ctx, &q, &k, &v, nullptr, 1.0f / sqrtf((float)HD), 0.0f, 0.0f, &o));
+    }
+    {
+        const mi355_tensor in = dev_tensor(b.attn, T_F32, E, M), out = dev_tensor(b.xn, T_F32, E, M);
+        TRY(mi355_mul_mat(ctx, &blk->proj_w, &in, &out));
+    }
+    TRY(mi355_vit_proj_residual(ctx, x, b.xn, blk->proj_b, M, E, G, WS));
+    // MLP
+    TRY(mi355_vit_layer_norm(ctx, x, nullptr, 0, blk->norm2_w, blk->norm2_b, b.xn, M, E, G, 0, hp->eps));
+    {
+        const mi355_tensor in = dev_tensor(b.xn, T_F32, E, M), out = dev_tensor(b.big, T_F32, MLP, M);
+        TRY(mi355_mul_mat(ctx, &blk->fc1_w, &in, &out));
+    }
+    TRY(mi355_vit_bias_gelu(ctx, b.big, blk->fc1_b, M, MLP));
+    {
+        const mi355_tensor in = dev_tensor(b.big, T_F32, MLP, M), out = dev_tensor(b.attn, T_F32, E, M);
+        TRY(mi355_mul_mat(ctx, &blk->fc2_w, &in, &out));
+    }
+    TRY(mi355_vit_bias_residual(ctx, x, b.attn, blk->fc2_b, M, E));
+#undef TRY
+    return MI355_STATUS_SUCCESS;
+}
+
+mi355_status mi355_vit_encode(mi355_context* ctx, const mi355_vit_hparams* hp, const float* image,
+                              const mi355_tensor* patch_w, const float* pos_embed, const float* ln_pre_w,
+                              const float* ln_pre_b, const mi355_vit_block* blocks, int n_blocks, float* x) {
+    if (n_blocks < 0 || (n_blocks > 0 && !blocks)) return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_encode: bad blocks");
+    mi355_status st = mi355_vit_prefix(ctx, hp, image, patch_w, pos_embed, ln_pre_w, ln_pre_b, x);
+    for (int i = 0; i < n_blocks && st == MI355_STATUS_SUCCESS; ++i) st = mi355_vit_block_forward(ctx, hp, &blocks[i], x);
+    return st;
+}
+
+}  // extern "C"
