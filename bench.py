@@ -17,6 +17,7 @@ on its stream through the library's kernel-timing hook), and a CPU baseline
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
 import argparse
+import ctypes as C
 import json
 import os
 import sys
@@ -28,6 +29,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 INT8_PEAK_TOPS = 5033.0      # MI355X dense int8 MFMA (256 CU x 2.4 GHz x 8192 op/clk/CU)
+FP16_PEAK_TFLOPS = 2516.0    # MI355X dense fp16 MFMA
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 M_TOK = 5184
 LINEARS = [("qkv", 3072, 1024), ("proj", 1024, 1024), ("fc1", 4736, 1024), ("fc2", 1024, 4736)]
@@ -89,12 +91,117 @@ def measure_traffic(op, kernel_sub):
             "fetch_scale": round(fs, 4), "write_scale": round(ws, 4)}
 
 
+def bench_attention(mi, ctx, torch, dev):
+    """FLASH_ATTN_EXT at the SAM3 shapes: f16 Q/K/V N(0,1), head 64, 16 heads;
+    windowed = 9 windows of 576 tokens (batch 144), global = 5184 tokens."""
+    res = {}
+    g = torch.Generator(device=dev).manual_seed(0)
+    for name, n, B in (("windowed", 576, 9), ("global", 5184, 1)):
+        D, nh = 64, 16
+        q, k, v = (torch.randn((B, nh, n, D), generator=g, device=dev).half() for _ in range(3))
+        dst = torch.empty((B, n, nh, D), dtype=torch.float32, device=dev)
+        tq, tk, tv = (mi.from_torch(x, mi.F16, [D, n, nh, B]) for x in (q, k, v))
+        td = mi.from_torch(dst, mi.F32, [D, nh, n, B])
+        for _ in range(5):
+            ctx.flash_attn_ext(tq, tk, tv, td, 0.125)
+        torch.cuda.synchronize()
+        ctx.profile(True)
+        for _ in range(20):
+            ctx.flash_attn_ext(tq, tk, tv, td, 0.125)
+        pr = ctx.profile_collect()
+        ctx.profile(False)
+        us = 1e3 * pr["flash_attn_ext"][1] / pr["flash_attn_ext"][0]
+        flop = 4.0 * B * nh * n * n * D
+        res[name] = {"us": round(us, 2), "tflops": round(flop / us / 1e6, 1),
+                     "pct_fp16_peak": round(100 * flop / us / 1e6 / FP16_PEAK_TFLOPS, 2)}
+    return res
+
+
+def build_encoder(mi, orc, torch, dev, types, seed=0):
+    """Random-init SAM3 ViT (1008^2 image, patch 14, E 1024, 32 blocks, 16 heads,
+    MLP 4736, windows of 24 except global blocks 7/15/23/31): per type, the
+    32 blocks' linear weights quantized from the same f32 N(0,0.02) draws."""
+    E, NH, MLP, WS, G, P, PG = 1024, 16, 4736, 24, 72, 14, 24
+    HD = E // NH
+    hp = mi.VitHparams(E, NH, MLP, WS, G, P, PG, 1e-5)
+    keep = []
+
+    def up(a):
+        t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+        keep.append(t)
+        return t
+
+    def cis(end, scale):
+        out = np.empty(end * end * HD, dtype=np.float32)
+        orc.lib().orc_compute_axial_cis(out.ctypes.data, HD, end, end, C.c_float(10000.0), C.c_float(scale))
+        return up(out)
+
+    f_win, f_glob = cis(WS, 1.0), cis(G, WS / G)
+    blocks = {tn: [] for tn in types}
+    for i in range(32):
+        glob = i in (7, 15, 23, 31)
+        vec = {}
+        for j, (name, n, sc, m) in enumerate([("norm1_w", E, 0.1, 1.0), ("norm1_b", E, 0.02, 0.0),
+                                              ("qkv_b", 3 * E, 0.02, 0.0), ("proj_b", E, 0.02, 0.0),
+                                              ("norm2_w", E, 0.1, 1.0), ("norm2_b", E, 0.02, 0.0),
+                                              ("fc1_b", MLP, 0.02, 0.0), ("fc2_b", E, 0.02, 0.0)]):
+            vec[name] = up(orc.normal(n, seed + i, 200 + j) * np.float32(sc) + np.float32(m))
+        ws = {}
+        for j, (name, n, k) in enumerate([("qkv", 3 * E, E), ("proj", E, E), ("fc1", MLP, E), ("fc2", E, MLP)]):
+            ws[name] = (orc.normal(n * k, seed + i, 100 + j, std=0.02).reshape(n, k), n, k)
+        for tn in types:
+            t = orc.NAME_TYPE[tn]
+            blk = mi.VitBlock()
+            for name, (w, n, k) in ws.items():
+                setattr(blk, name + "_w", mi.from_torch(up(orc.quantize_weights(t, w)), t, [k, n]))
+            for name, tsr in vec.items():
+                setattr(blk, name, tsr.data_ptr())
+            blk.freqs_cis = (f_glob if glob else f_win).data_ptr()
+            blk.is_global = 1 if glob else 0
+            blocks[tn].append(blk)
+    image = up(orc.uniform(3 * 1008 * 1008, seed, 300).reshape(3, 1008, 1008))
+    patch_w = up(orc.normal(E * 3 * P * P, seed, 301, std=0.02))
+    pos = up(orc.normal(PG * PG * E, seed, 302, std=0.02))
+    ln_w = up(orc.normal(E, seed, 303) * np.float32(0.1) + np.float32(1.0))
+    ln_b = up(orc.normal(E, seed, 304) * np.float32(0.02))
+    pre = (image.data_ptr(), mi.from_torch(patch_w, mi.F32, [P, P, 3, E]), pos.data_ptr(), ln_w.data_ptr(),
+           ln_b.data_ptr())
+    return hp, pre, blocks, keep
+
+
+def bench_encoder(mi, ctx, torch, dev, hp, pre, blocks, frames):
+    """ms per frame of the whole encoder (prefix + 32 blocks), image resident in
+    HBM; plus one profiled frame split by kernel."""
+    x = torch.empty((hp.grid * hp.grid, hp.embed_dim), dtype=torch.float32, device=dev)
+    img, pw, pos, lw, lb = pre
+    run = lambda: ctx.vit_encode(hp, C.c_void_p(img), pw, C.c_void_p(pos), C.c_void_p(lw), C.c_void_p(lb), blocks,
+                                 C.c_void_p(x.data_ptr()))
+    run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(frames):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / frames
+    finite = bool(torch.isfinite(x).all().item())
+    ctx.profile(True)
+    run()
+    pr = ctx.profile_collect()
+    ctx.profile(False)
+    split = {k: round(v[1], 3) for k, v in sorted(pr.items(), key=lambda kv: -kv[1][1])}
+    return {"ms_per_frame": round(ms, 3), "frames": frames, "output_finite": finite, "kernel_ms_per_frame": split}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-encoder", action="store_true", help="skip the full ViT encoder ms/frame")
+    ap.add_argument("--frames", type=int, default=3, help="timed encoder frames per weight type")
     ap.add_argument("--op", default=None,
                     help="profile mode: run only TYPE/LINEAR (e.g. q8_0/fc1) --reps times and print its kernel times")
     ap.add_argument("--reps", type=int, default=20)
@@ -224,6 +331,23 @@ def main():
                 "traffic_counters": traffic,
                 "int8_tops": round(2.0 * M_TOK * N * K / (mmq_ms * 1e-3) / 1e12, 1)}
 
+    # ---- attention (FLASH_ATTN_EXT at the windowed / global SAM3 shapes)
+    log("bench: attention")
+    attn = bench_attention(mi, ctx, torch, dev)
+
+    # ---- full SAM3 ViT encoder ms/frame, Q8_0 and Q4_0 weights
+    encoder = None
+    if not args.no_encoder:
+        log("bench: encoder weights")
+        del calls
+        torch.cuda.empty_cache()
+        hp, pre, blocks, keep = build_encoder(mi, orc, torch, dev, TYPES)
+        encoder = {}
+        for tn in TYPES:
+            log(f"bench: encoder {tn}")
+            encoder[tn] = bench_encoder(mi, ctx, torch, dev, hp, pre, blocks[tn], args.frames)
+        del keep
+
     # ---- CPU baseline: the oracle's ggml-cpu restatement, same fc1 Q8_0 mul_mat
     cpu = None
     if not args.no_cpu_baseline:
@@ -265,6 +389,8 @@ def main():
         "type_tops": {k: round(v, 2) for k, v in type_tops.items()},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "vit_encoder_1008": encoder,
+        "attention": attn,
     }
     print(json.dumps(out), flush=True)
     ctx.close()
