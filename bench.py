@@ -91,12 +91,14 @@ def measure_traffic(op, kernel_sub):
             "fetch_scale": round(fs, 4), "write_scale": round(ws, 4)}
 
 
-def bench_attention(mi, ctx, torch, dev):
+def bench_attention(mi, ctx, torch, dev, only=None, reps=20):
     """FLASH_ATTN_EXT at the SAM3 shapes: f16 Q/K/V N(0,1), head 64, 16 heads;
     windowed = 9 windows of 576 tokens (batch 144), global = 5184 tokens."""
     res = {}
     g = torch.Generator(device=dev).manual_seed(0)
     for name, n, B in (("windowed", 576, 9), ("global", 5184, 1)):
+        if only and name != only:
+            continue
         D, nh = 64, 16
         q, k, v = (torch.randn((B, nh, n, D), generator=g, device=dev).half() for _ in range(3))
         dst = torch.empty((B, n, nh, D), dtype=torch.float32, device=dev)
@@ -106,7 +108,7 @@ def bench_attention(mi, ctx, torch, dev):
             ctx.flash_attn_ext(tq, tk, tv, td, 0.125)
         torch.cuda.synchronize()
         ctx.profile(True)
-        for _ in range(20):
+        for _ in range(reps):
             ctx.flash_attn_ext(tq, tk, tv, td, 0.125)
         pr = ctx.profile_collect()
         ctx.profile(False)
@@ -203,7 +205,8 @@ def main():
     ap.add_argument("--no-encoder", action="store_true", help="skip the full ViT encoder ms/frame")
     ap.add_argument("--frames", type=int, default=3, help="timed encoder frames per weight type")
     ap.add_argument("--op", default=None,
-                    help="profile mode: run only TYPE/LINEAR (e.g. q8_0/fc1) --reps times and print its kernel times")
+                    help="profile mode, one workload --reps times with its kernel times: TYPE/LINEAR (e.g. q8_0/fc1), "
+                         "attn/windowed, attn/global, vit/TYPE (encoder frames), copy (256 MiB device copy)")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--op-warmup", type=int, default=20)
     ap.add_argument("--no-traffic", action="store_true",
@@ -240,6 +243,20 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         print(json.dumps({"op": "copy", "bytes_read": 4 * n, "bytes_written": 4 * n, "reps": args.reps}), flush=True)
+        ctx.close()
+        return
+
+    if args.op and args.op.startswith("attn/"):
+        which = args.op.split("/")[1]
+        res = bench_attention(mi, ctx, torch, dev, only=which, reps=args.reps)
+        print(json.dumps({"op": args.op, "reps": args.reps, **res[which]}), flush=True)
+        ctx.close()
+        return
+    if args.op and args.op.startswith("vit/"):
+        tn = args.op.split("/")[1]
+        hp, pre, blocks, keep = build_encoder(mi, orc, torch, dev, [tn])
+        res = bench_encoder(mi, ctx, torch, dev, hp, pre, blocks[tn], args.reps)
+        print(json.dumps({"op": args.op, **res}), flush=True)
         ctx.close()
         return
 
