@@ -202,6 +202,59 @@ mi355_status mi355_vit_bias_gelu(mi355_context* ctx, float* h, const float* b, i
 /* x = x + (f + b) over rows of n (sam3.cpp:3799-3802). */
 mi355_status mi355_vit_bias_residual(mi355_context* ctx, float* x, const float* f, const float* b, int64_t rows, int n);
 
+/* ---- SAM2 Hiera image encoder ---------------------------------------------
+ * sam2_build_hiera_graph (sam3.cpp:4466-4535) on this backend: patch
+ * embedding (conv 7x7, stride 4, pad 3, + bias) + pos_embed, then the blocks
+ * of sam2_hiera_block_forward (sam3.cpp:4299-4461) with the per-block
+ * metadata of sam2_precompute_hiera_metadata (sam3.cpp:1680-1746).
+ * Activations are device F32 [S*S][C] in image token order (ggml [C, S, S]). */
+typedef struct mi355_hiera_hparams {
+    int32_t img_size;       /* 1024 */
+    int32_t embed_dim;      /* 96 for Hiera-tiny */
+    int32_t num_heads;      /* 1 */
+    int32_t stages[4];      /* blocks per stage {1, 2, 7, 2} */
+    int32_t q_pool;         /* stage transitions with Q pooling (3) */
+    int32_t window_spec[4]; /* {8, 4, 14, 7} */
+    int32_t global_idx[8];  /* blocks with global attention {5, 7, 9} */
+    int32_t n_global;
+    float eps;              /* LayerNorm eps (1e-6) */
+} mi355_hiera_hparams;
+
+typedef struct mi355_hiera_block {
+    mi355_tensor qkv_w, proj_w, fc1_w, fc2_w;
+    mi355_tensor dim_proj_w; /* data NULL for blocks that keep their width */
+    const float* norm1_w;
+    const float* norm1_b;
+    const float* qkv_b;
+    const float* proj_b;
+    const float* norm2_w;
+    const float* norm2_b;
+    const float* fc1_b;
+    const float* fc2_b;
+    const float* dim_proj_b;
+} mi355_hiera_block;
+
+/* Per-block metadata as the reference derives it: width in/out, heads,
+ * window size (0 = global) and Q pooling. */
+typedef struct mi355_hiera_block_info {
+    int32_t dim_in, dim_out, num_heads, window_size, q_stride, stage;
+} mi355_hiera_block_info;
+int mi355_hiera_n_blocks(const mi355_hiera_hparams* hp);
+mi355_status mi355_hiera_block_info_get(const mi355_hiera_hparams* hp, int block_index, mi355_hiera_block_info* out);
+/* Device bytes the encoder keeps for its activations (allocated on first use). */
+size_t mi355_hiera_workspace_size(const mi355_hiera_hparams* hp);
+/* One block: x [S*S][dim_in] -> x_out [S'*S'][dim_out], S' = S/2 with Q pooling.
+ * x_out must not overlap x. */
+mi355_status mi355_hiera_block_forward(mi355_context* ctx, const mi355_hiera_hparams* hp, int block_index,
+                                       const mi355_hiera_block* blk, const float* x, int spatial, float* x_out);
+/* The whole backbone: image device F32 [3][img][img]; patch_w [7, 7, 3, E]
+ * F32 or F16, patch_b [E], pos_embed [S0*S0][E] (S0 = img/4).  stage_out[s]
+ * (device [S_s*S_s][C_s], or NULL) receive the output of each stage's last
+ * block. */
+mi355_status mi355_hiera_encode(mi355_context* ctx, const mi355_hiera_hparams* hp, const float* image,
+                                const mi355_tensor* patch_w, const float* patch_b, const float* pos_embed,
+                                const mi355_hiera_block* blocks, int n_blocks, float* const stage_out[4]);
+
 /* ---- Kernel timing --------------------------------------------------------
  * The device-side counterpart of the reference's timing around graph compute
  * (std::chrono, sam3.cpp:6122-6135) and of its per-op micro-bench

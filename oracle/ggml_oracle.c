@@ -1013,6 +1013,73 @@ void orc_gelu_erf(const float* x, float* y, int64_t n) {
     }
 }
 
+/* ggml_gelu (tanh form), as ggml-cpu evaluates it with GGML_GELU_FP16: for
+ * x <= -10 the result is 0, for x >= 10 it is x, otherwise the fp16 table
+ * entry of f16(x): f16(gelu_f32(f16(x))) with
+ *   gelu_f32(v) = 0.5*v*(1 + tanh(sqrt(2/pi)*v*(1 + 0.044715*v*v)))
+ * evaluated left to right in fp32 (used by the Hiera MLP, sam3.cpp:4453). */
+static float gelu_tanh_f32(float v) {
+    const float c = 0.79788456080286535587989211986876f, a = 0.044715f;
+    const float inner = c * v * (1.0f + a * v * v);
+    return 0.5f * v * (1.0f + tanhf(inner));
+}
+void orc_gelu_tanh(const float* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float v = x[i];
+        if (v <= -10.0f) y[i] = 0.0f;
+        else if (v >= 10.0f) y[i] = v;
+        else y[i] = h2f(f2h(gelu_tanh_f32(h2f(f2h(v)))));
+    }
+}
+
+/* sam2_window_partition (sam3.cpp:4194-4232): x [H][W][C] (ggml [C, W, H]) zero-padded
+ * to Hp, Wp (multiples of ws) -> [nW][ws][ws][C], window n = wh + nW_h * ww (the
+ * H-major order the reshape sequence produces), token (lh, lw) at lh*ws + lw. */
+void orc_hiera_win_part(const float* x, float* y, int64_t C, int64_t W, int64_t H, int ws) {
+    const int64_t Wp = (W + ws - 1) / ws * ws, Hp = (H + ws - 1) / ws * ws;
+    const int64_t nwh = Hp / ws, nww = Wp / ws;
+    for (int64_t ww = 0; ww < nww; ++ww)
+        for (int64_t wh = 0; wh < nwh; ++wh)
+            for (int64_t lh = 0; lh < ws; ++lh)
+                for (int64_t lw = 0; lw < ws; ++lw) {
+                    const int64_t n = wh + nwh * ww;
+                    float* o = y + ((n * ws + lh) * ws + lw) * C;
+                    const int64_t h = wh * ws + lh, w = ww * ws + lw;
+                    if (h < H && w < W) memcpy(o, x + (h * W + w) * C, (size_t)C * 4);
+                    else memset(o, 0, (size_t)C * 4);
+                }
+}
+
+/* sam2_window_unpartition (sam3.cpp:4234-4281): inverse of the above for windows of ws
+ * over a padded Hp x Wp grid, cropped to H x W. */
+void orc_hiera_win_unpart(const float* x, float* y, int64_t C, int64_t W, int64_t H, int ws) {
+    const int64_t Hp = (H + ws - 1) / ws * ws;
+    const int64_t nwh = Hp / ws;
+    for (int64_t h = 0; h < H; ++h)
+        for (int64_t w = 0; w < W; ++w) {
+            const int64_t n = h / ws + nwh * (w / ws);
+            memcpy(y + (h * W + w) * C, x + ((n * ws + h % ws) * ws + w % ws) * C, (size_t)C * 4);
+        }
+}
+
+/* sam2_maxpool_2d (sam3.cpp:4286-4296): ggml_pool_2d MAX, kernel 2, stride 2, no
+ * padding, over x [B][H][W][C] -> [B][H/2][W/2][C]. */
+void orc_maxpool2(const float* x, float* y, int64_t C, int64_t W, int64_t H, int64_t B) {
+    const int64_t W2 = W / 2, H2 = H / 2;
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t h = 0; h < H2; ++h)
+            for (int64_t w = 0; w < W2; ++w)
+                for (int64_t c = 0; c < C; ++c) {
+                    const float* p = x + ((b * H + 2 * h) * W + 2 * w) * C + c;
+                    float m = p[0];
+                    const float v1 = p[C], v2 = p[W * C], v3 = p[W * C + C];
+                    if (v1 > m) m = v1;
+                    if (v2 > m) m = v2;
+                    if (v3 > m) m = v3;
+                    y[((b * H2 + h) * W2 + w) * C + c] = m;
+                }
+}
+
 /* sam3.cpp:3559-3590: freqs[i] = 1/theta^(4i/dim), i < dim/4; token idx at
  * (x = idx % end_x, y = idx / end_x) * scale_pos; pairs 0..dim/4-1 from x,
  * the next dim/4 pairs from y, each stored (cos, sin). */

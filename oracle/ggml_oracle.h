@@ -147,6 +147,10 @@ int orc_attn_exact(const orc_tensor* q, const orc_tensor* k, const orc_tensor* v
 /* ViT glue (sam3.cpp:1041-1051, 3559-3590, 3671-3710, 3714-3805). */
 void orc_norm_rows(const float* x, float* y, int64_t nrows, int64_t ne0, float eps);
 void orc_gelu_erf(const float* x, float* y, int64_t n);
+void orc_gelu_tanh(const float* x, float* y, int64_t n); /* ggml_gelu, fp16-table semantics */
+void orc_hiera_win_part(const float* x, float* y, int64_t C, int64_t W, int64_t H, int ws);
+void orc_hiera_win_unpart(const float* x, float* y, int64_t C, int64_t W, int64_t H, int ws);
+void orc_maxpool2(const float* x, float* y, int64_t C, int64_t W, int64_t H, int64_t B);
 void orc_compute_axial_cis(float* out, int dim, int end_x, int end_y, float theta, float scale_pos);
 /* x [hd, N, nh] rows; freqs [hd/2 pairs (cos,sin)] per token, [N][hd]. */
 void orc_apply_rope(float* x, const float* freqs, int64_t hd, int64_t n_tok, int64_t n_rows3);

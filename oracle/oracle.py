@@ -79,6 +79,10 @@ def lib():
             "orc_attn_exact": (I, [T, T, T, T, F, I]),
             "orc_norm_rows": (None, [P, P, I64, I64, F]),
             "orc_gelu_erf": (None, [P, P, I64]),
+            "orc_gelu_tanh": (None, [P, P, I64]),
+            "orc_hiera_win_part": (None, [P, P, I64, I64, I64, I]),
+            "orc_hiera_win_unpart": (None, [P, P, I64, I64, I64, I]),
+            "orc_maxpool2": (None, [P, P, I64, I64, I64, I64]),
             "orc_compute_axial_cis": (None, [P, I, I, I, F, F]),
             "orc_apply_rope": (None, [P, P, I64, I64, I64]),
             "orc_win_part": (None, [P, P, I64, I64, I64, I]),

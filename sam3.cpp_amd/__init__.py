@@ -58,6 +58,40 @@ class VitBlock(C.Structure):
                 ("freqs_cis", C.c_void_p), ("is_global", C.c_int32)]
 
 
+class HieraHparams(C.Structure):
+    """struct mi355_hiera_hparams."""
+    _fields_ = [("img_size", C.c_int32), ("embed_dim", C.c_int32), ("num_heads", C.c_int32),
+                ("stages", C.c_int32 * 4), ("q_pool", C.c_int32), ("window_spec", C.c_int32 * 4),
+                ("global_idx", C.c_int32 * 8), ("n_global", C.c_int32), ("eps", C.c_float)]
+
+
+class HieraBlock(C.Structure):
+    """struct mi355_hiera_block (device pointers)."""
+    _fields_ = [("qkv_w", Tensor), ("proj_w", Tensor), ("fc1_w", Tensor), ("fc2_w", Tensor), ("dim_proj_w", Tensor),
+                ("norm1_w", C.c_void_p), ("norm1_b", C.c_void_p), ("qkv_b", C.c_void_p), ("proj_b", C.c_void_p),
+                ("norm2_w", C.c_void_p), ("norm2_b", C.c_void_p), ("fc1_b", C.c_void_p), ("fc2_b", C.c_void_p),
+                ("dim_proj_b", C.c_void_p)]
+
+
+class HieraBlockInfo(C.Structure):
+    _fields_ = [("dim_in", C.c_int32), ("dim_out", C.c_int32), ("num_heads", C.c_int32),
+                ("window_size", C.c_int32), ("q_stride", C.c_int32), ("stage", C.c_int32)]
+
+
+def hiera_tiny(img_size: int = 1024) -> HieraHparams:
+    """SAM2.1 Hiera-tiny (convert_sam2_to_ggml.py:81-84)."""
+    hp = HieraHparams()
+    hp.img_size, hp.embed_dim, hp.num_heads, hp.q_pool, hp.eps = img_size, 96, 1, 3, 1e-6
+    for i, v in enumerate((1, 2, 7, 2)):
+        hp.stages[i] = v
+    for i, v in enumerate((8, 4, 14, 7)):
+        hp.window_spec[i] = v
+    for i, v in enumerate((5, 7, 9)):
+        hp.global_idx[i] = v
+    hp.n_global = 3
+    return hp
+
+
 def build(force: bool = False) -> str:
     """Compile the HIP sources for gfx950 (make -C sam3.cpp_amd)."""
     args = ["make", "-s", "-C", HERE, f"-j{min(16, os.cpu_count() or 1)}"]
@@ -109,6 +143,12 @@ def lib():
         "mi355_vit_proj_residual": (I, [P, P, P, P, C.c_int64, I, I, I]),
         "mi355_vit_bias_gelu": (I, [P, P, P, C.c_int64, I]),
         "mi355_vit_bias_residual": (I, [P, P, P, P, C.c_int64, I]),
+        "mi355_hiera_n_blocks": (I, [C.POINTER(HieraHparams)]),
+        "mi355_hiera_block_info_get": (I, [C.POINTER(HieraHparams), I, C.POINTER(HieraBlockInfo)]),
+        "mi355_hiera_workspace_size": (SZ, [C.POINTER(HieraHparams)]),
+        "mi355_hiera_block_forward": (I, [P, C.POINTER(HieraHparams), I, C.POINTER(HieraBlock), P, I, P]),
+        "mi355_hiera_encode": (I, [P, C.POINTER(HieraHparams), P, T, P, P, C.POINTER(HieraBlock), I,
+                                   C.POINTER(P)]),
         "mi355_profile_enable": (I, [P, I]),
         "mi355_profile_collect": (I, [P]),
         "mi355_profile_get": (I, [P, I, C.POINTER(C.c_char_p), C.POINTER(I), C.POINTER(C.c_double)]),
@@ -120,6 +160,14 @@ def lib():
         fn.argtypes = args
     _lib = L
     return L
+
+
+def hiera_block_info(hp: HieraHparams, index: int) -> HieraBlockInfo:
+    out = HieraBlockInfo()
+    st = lib().mi355_hiera_block_info_get(C.byref(hp), index, C.byref(out))
+    if st != 0:
+        raise Mi355Error(st, lib().mi355_last_error(None).decode())
+    return out
 
 
 def row_size(t: int, ne0: int) -> int:
@@ -236,6 +284,16 @@ class Context:
         arr = (VitBlock * len(blocks))(*blocks)
         self._check(self.L.mi355_vit_encode(self.h, C.byref(hp), image, C.byref(patch_w), pos, ln_w, ln_b, arr,
                                             len(blocks), x))
+
+    # ---- SAM2 Hiera encoder
+    def hiera_block_forward(self, hp: HieraHparams, index: int, blk: HieraBlock, x, spatial: int, x_out):
+        self._check(self.L.mi355_hiera_block_forward(self.h, C.byref(hp), index, C.byref(blk), x, spatial, x_out))
+
+    def hiera_encode(self, hp: HieraHparams, image, patch_w: Tensor, patch_b, pos, blocks, stage_out=None):
+        arr = (HieraBlock * len(blocks))(*blocks)
+        outs = (C.c_void_p * 4)(*(stage_out or [None] * 4))
+        self._check(self.L.mi355_hiera_encode(self.h, C.byref(hp), image, C.byref(patch_w), patch_b, pos, arr,
+                                              len(blocks), outs))
 
     def flash_attn_ext(self, q: Tensor, k: Tensor, v: Tensor, dst: Tensor, scale: float):
         self._check(self.L.mi355_flash_attn_ext(self.h, C.byref(q), C.byref(k), C.byref(v), None, scale, 0.0, 0.0,

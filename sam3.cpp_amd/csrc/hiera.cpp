@@ -1,0 +1,436 @@
+// SAM2 Hiera image encoder on the MI355X backend: the graph of
+// sam2_build_hiera_graph (sam3.cpp:4466-4535) node group by node group.  Per
+// block (sam2_hiera_block_forward, sam3.cpp:4299-4461):
+//
+//   xn   = LN1(x)  [window order over the zero-padded grid for windowed blocks]
+//   sc   = x | maxpool(x) | [maxpool](mul_mat(dim_proj_w, LN1(x)) + dim_proj_b)
+//   qkv  = mul_mat(qkv_w, xn)
+//   q,k,v = split(qkv + qkv_b), q max-pooled 2x2 inside each window  -> fp16
+//   attn = flash_attn_ext(q, k, v, 1/sqrt(HD))
+//   x'   = sc + window_unpartition(mul_mat(proj_w, attn) + proj_b)
+//   x'   = x' + (mul_mat(fc2_w, gelu(mul_mat(fc1_w, LN2(x')) + fc1_b)) + fc2_b)
+//
+// MUL_MAT and FLASH_ATTN_EXT go through the backend's own entry points; the
+// memory-bound steps are the fused passes of hiera.hip.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "context.h"
+
+using namespace mi355;
+
+namespace {
+
+struct Info {
+    int dim_in, dim_out, heads, ws, qs, stage;
+};
+
+// sam2_precompute_hiera_metadata (sam3.cpp:1680-1746): the window size lags a
+// block behind the stage (a stage's first block keeps the previous stage's
+// window), and Q pooling happens at the first block of stages 1..q_pool.
+bool block_infos(const mi355_hiera_hparams* hp, std::vector<Info>& out) {
+    out.clear();
+    int total = 0, ends[4];
+    for (int s = 0; s < 4; ++s) {
+        if (hp->stages[s] < 0) return false;
+        total += hp->stages[s];
+        ends[s] = total - 1;
+    }
+    std::vector<int> qpool_blocks;
+    for (int s = 0; s < 3 && (int)qpool_blocks.size() < hp->q_pool; ++s) qpool_blocks.push_back(ends[s] + 1);
+    int cur = 0, dim = hp->embed_dim, heads = hp->num_heads;
+    for (int i = 0; i < total; ++i) {
+        Info b;
+        int ws = hp->window_spec[cur];
+        for (int g = 0; g < hp->n_global && g < 8; ++g)
+            if (hp->global_idx[g] == i) ws = 0;
+        b.ws = ws;
+        int dim_out = dim;
+        if (i > 0 && i - 1 == ends[cur]) {
+            dim_out = dim * 2;
+            heads *= 2;
+            ++cur;
+        }
+        b.stage = cur;
+        b.dim_in = dim;
+        b.dim_out = dim_out;
+        b.heads = heads;
+        b.qs = std::find(qpool_blocks.begin(), qpool_blocks.end(), i) != qpool_blocks.end();
+        out.push_back(b);
+        dim = dim_out;
+    }
+    return true;
+}
+
+int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+// activation buffers of one block (or their maxima over the backbone)
+struct Sizes {
+    size_t xw = 0, xn = 0, dp = 0, sc = 0, qkv = 0, q = 0, kv = 0, att = 0, p = 0, h = 0, f = 0, x = 0, cols = 0, w32 = 0;
+    void max_with(const Sizes& o) {
+        size_t* a = &xw;
+        const size_t* b = &o.xw;
+        for (int i = 0; i < 14; ++i) a[i] = std::max(a[i], b[i]);
+    }
+};
+
+Sizes block_sizes(const Info& b, int S) {
+    Sizes z;
+    const size_t Cin = b.dim_in, Cout = b.dim_out;
+    const int S2 = b.qs ? S / 2 : S;
+    size_t rows = (size_t)S * S, nq = rows;
+    if (b.ws > 0) {
+        const size_t nw = (size_t)cdiv(S, b.ws) * cdiv(S, b.ws);
+        rows = nw * b.ws * b.ws;
+        nq = b.qs ? nw * (b.ws / 2) * (b.ws / 2) : rows;
+        z.xw = rows * Cin * 4;
+    }
+    z.xn = (size_t)S * S * std::max(Cin, Cout) * 4;
+    if (Cin != Cout) z.dp = (size_t)S * S * Cout * 4;
+    if (Cin != Cout || b.qs) z.sc = (size_t)S2 * S2 * Cout * 4;
+    z.qkv = rows * 3 * Cout * 4;
+    z.q = nq * Cout * 2;
+    z.kv = rows * Cout * 2;
+    z.att = nq * Cout * 4;
+    z.p = nq * Cout * 4;
+    z.h = (size_t)S2 * S2 * 4 * Cout * 4;
+    z.f = (size_t)S2 * S2 * Cout * 4;
+    z.x = (size_t)S * S * std::max(Cin, Cout) * 4;
+    return z;
+}
+
+struct Bufs {
+    float *xw, *xn, *dp, *sc, *qkv, *att, *p, *h, *f, *x0, *x1, *cols, *w32;
+    _Float16 *q, *k, *v;
+};
+
+size_t layout(const Sizes& z, char* base, Bufs* b) {
+    const size_t parts[16] = {z.xw, z.xn, z.dp, z.sc, z.qkv, z.att, z.p, z.h, z.f, z.x, z.x, z.cols, z.w32, z.q, z.kv, z.kv};
+    size_t off[16], o = 0;
+    for (int i = 0; i < 16; ++i) {
+        off[i] = o;
+        o += align_up(std::max(parts[i], (size_t)256));
+    }
+    if (b && base) {
+        float** fp[13] = {&b->xw, &b->xn, &b->dp, &b->sc, &b->qkv, &b->att, &b->p, &b->h, &b->f, &b->x0, &b->x1, &b->cols, &b->w32};
+        for (int i = 0; i < 13; ++i) *fp[i] = reinterpret_cast<float*>(base + off[i]);
+        b->q = reinterpret_cast<_Float16*>(base + off[13]);
+        b->k = reinterpret_cast<_Float16*>(base + off[14]);
+        b->v = reinterpret_cast<_Float16*>(base + off[15]);
+    }
+    return o;
+}
+
+mi355_status check_hp(mi355_context* ctx, const mi355_hiera_hparams* hp, std::vector<Info>& infos) {
+    if (!hp) return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera: null hparams");
+    if (hp->img_size <= 0 || hp->img_size % 4 != 0 || hp->embed_dim <= 0 || hp->num_heads <= 0 || hp->q_pool < 0 ||
+        hp->n_global < 0 || hp->n_global > 8 || !(hp->eps >= 0.0f))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera: bad hparams");
+    for (int s = 0; s < 4; ++s)
+        if (hp->window_spec[s] < 0) return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera: negative window size");
+    if (!block_infos(hp, infos) || infos.empty()) return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera: bad stage table");
+    int S = hp->img_size / 4;
+    for (size_t i = 0; i < infos.size(); ++i) {
+        const Info& b = infos[i];
+        if (b.dim_out % b.heads != 0) return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera: width not divisible by heads");
+        const int HD = b.dim_out / b.heads;
+        if (!(HD == 64 || HD == 96 || HD == 128))
+            return fail(ctx, MI355_STATUS_UNSUPPORTED, "hiera: head size %d (supported: 64, 96, 128)", HD);
+        if (b.dim_in % 4 != 0 || b.dim_out % 4 != 0 || b.dim_out > 2048)
+            return fail(ctx, MI355_STATUS_UNSUPPORTED, "hiera: widths must be multiples of 4, <= 2048");
+        if (b.qs && (S % 2 != 0 || (b.ws > 0 && b.ws % 2 != 0)))
+            return fail(ctx, MI355_STATUS_UNSUPPORTED, "hiera: Q pooling needs even grid and window");
+        if (b.qs && b.ws == 0) return fail(ctx, MI355_STATUS_UNSUPPORTED, "hiera: Q pooling in a global block");
+        if (b.qs) S /= 2;
+    }
+    return MI355_STATUS_SUCCESS;
+}
+
+Sizes all_sizes(const mi355_hiera_hparams* hp, const std::vector<Info>& infos) {
+    Sizes z;
+    int S = hp->img_size / 4;
+    for (const Info& b : infos) {
+        z.max_with(block_sizes(b, S));
+        if (b.qs) S /= 2;
+    }
+    const size_t S0 = (size_t)(hp->img_size / 4);
+    z.cols = S0 * S0 * 147 * 4;
+    z.w32 = (size_t)147 * hp->embed_dim * 4;
+    z.x = std::max(z.x, S0 * S0 * (size_t)hp->embed_dim * 4);
+    return z;
+}
+
+mi355_tensor tensor_on(const void* p, int type, int64_t ne0, int64_t ne1, int64_t ne2 = 1, int64_t ne3 = 1) {
+    mi355_tensor t{};
+    t.type = type;
+    t.ne[0] = ne0;
+    t.ne[1] = ne1;
+    t.ne[2] = ne2;
+    t.ne[3] = ne3;
+    t.nb[0] = type == T_F32 ? 4 : 2;
+    t.nb[1] = t.nb[0] * ne0;
+    t.nb[2] = t.nb[1] * ne1;
+    t.nb[3] = t.nb[2] * ne2;
+    t.data = const_cast<void*>(p);
+    return t;
+}
+
+mi355_status get_bufs(mi355_context* ctx, const mi355_hiera_hparams* hp, const std::vector<Info>& infos, Bufs* b) {
+    const Sizes z = all_sizes(hp, infos);
+    mi355_status st = ensure_buffer(ctx, &ctx->enc, &ctx->enc_size, layout(z, nullptr, nullptr));
+    if (st != MI355_STATUS_SUCCESS) return st;
+    layout(z, static_cast<char*>(ctx->enc), b);
+    return MI355_STATUS_SUCCESS;
+}
+
+#define TRY(e)                                     \
+    do {                                           \
+        mi355_status st_ = (e);                    \
+        if (st_ != MI355_STATUS_SUCCESS) return st_; \
+    } while (0)
+
+mi355_status run_block(mi355_context* ctx, const mi355_hiera_hparams* hp, const Info& bi, const mi355_hiera_block* blk,
+                       const float* x, int S, float* x_out, const Bufs& b) {
+    const int Cin = bi.dim_in, Cout = bi.dim_out, NH = bi.heads, HD = Cout / NH, ws = bi.ws;
+    const int S2 = bi.qs ? S / 2 : S;
+    const bool dimch = Cin != Cout;
+    const int nwh = ws > 0 ? cdiv(S, ws) : 1;
+    const int nW = ws > 0 ? nwh * nwh : 1;
+    const int Nkv = ws > 0 ? ws * ws : S * S;
+    const int Nq = bi.qs ? (ws / 2) * (ws / 2) : Nkv;
+    const int64_t rows = (int64_t)nW * Nkv;
+    hipStream_t st = ctx->stream;
+    if (!blk->norm1_w || !blk->norm1_b || !blk->qkv_b || !blk->proj_b || !blk->norm2_w || !blk->norm2_b || !blk->fc1_b ||
+        !blk->fc2_b || (dimch && (!blk->dim_proj_w.data || !blk->dim_proj_b)))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera block: null weight pointer");
+
+    // LN1: window order for the attention input; image order when dim_proj or
+    // global attention reads it
+    const float* att_in;
+    {
+        HieraLnArgs a{};
+        a.x = x;
+        a.w = blk->norm1_w;
+        a.b = blk->norm1_b;
+        a.C = Cin;
+        a.W = a.H = S;
+        a.eps = hp->eps;
+        if (ws > 0) {
+            a.y = b.xw;
+            a.y_img = dimch ? b.xn : nullptr;
+            a.rows_out = rows;
+            a.ws = ws;
+            a.nwh = nwh;
+            att_in = b.xw;
+        } else {
+            a.y = b.xn;
+            a.rows_out = (int64_t)S * S;
+            att_in = b.xn;
+        }
+        Timed t(ctx, "hiera_ln");
+        TRY(hip_check(ctx, t.done(launch_hiera_ln(a, st)), "hiera_ln launch"));
+    }
+    // shortcut
+    const float* sc = x;
+    if (dimch) {
+        const mi355_tensor in = tensor_on(b.xn, T_F32, Cin, (int64_t)S * S), out = tensor_on(b.dp, T_F32, Cout, (int64_t)S * S);
+        TRY(mi355_mul_mat(ctx, &blk->dim_proj_w, &in, &out));
+        Timed t(ctx, "hiera_bias_maxpool");
+        TRY(hip_check(ctx, t.done(launch_hiera_bias_maxpool(b.dp, blk->dim_proj_b, b.sc, Cout, S, S, bi.qs, st)),
+                      "bias_maxpool launch"));
+        sc = b.sc;
+    } else if (bi.qs) {
+        Timed t(ctx, "hiera_bias_maxpool");
+        TRY(hip_check(ctx, t.done(launch_hiera_bias_maxpool(x, nullptr, b.sc, Cout, S, S, true, st)), "maxpool launch"));
+        sc = b.sc;
+    }
+    // attention
+    {
+        const mi355_tensor in = tensor_on(att_in, T_F32, Cin, rows), out = tensor_on(b.qkv, T_F32, 3 * Cout, rows);
+        TRY(mi355_mul_mat(ctx, &blk->qkv_w, &in, &out));
+    }
+    {
+        HieraQkvArgs a{};
+        a.qkv = b.qkv;
+        a.bias = blk->qkv_b;
+        a.q = b.q;
+        a.k = b.k;
+        a.v = b.v;
+        a.B = nW;
+        a.Nkv = Nkv;
+        a.Nq = Nq;
+        a.NH = NH;
+        a.HD = HD;
+        a.qpool = bi.qs;
+        a.ws = ws;
+        Timed t(ctx, "hiera_qkv");
+        TRY(hip_check(ctx, t.done(launch_hiera_qkv(a, st)), "hiera_qkv launch"));
+    }
+    {
+        const mi355_tensor q = tensor_on(b.q, T_F16, HD, Nq, NH, nW), k = tensor_on(b.k, T_F16, HD, Nkv, NH, nW),
+                           v = tensor_on(b.v, T_F16, HD, Nkv, NH, nW), o = tensor_on(b.att, T_F32, HD, NH, Nq, nW);
+        TRY(mi355_flash_attn_ext(ctx, &q, &k, &v, nullptr, 1.0f / sqrtf((float)HD), 0.0f, 0.0f, &o));
+    }
+    {
+        const mi355_tensor in = tensor_on(b.att, T_F32, Cout, (int64_t)Nq * nW), out = tensor_on(b.p, T_F32, Cout, (int64_t)Nq * nW);
+        TRY(mi355_mul_mat(ctx, &blk->proj_w, &in, &out));
+    }
+    {
+        const int wso = ws > 0 ? (bi.qs ? ws / 2 : ws) : 0;
+        const int nwh_o = wso > 0 ? cdiv(S2, wso) : 1;
+        Timed t(ctx, "hiera_proj_residual");
+        TRY(hip_check(ctx, t.done(launch_hiera_proj_residual(x_out, sc, b.p, blk->proj_b, Cout, S2, S2, wso, nwh_o, st)),
+                      "proj_residual launch"));
+    }
+    // MLP
+    {
+        HieraLnArgs a{};
+        a.x = x_out;
+        a.w = blk->norm2_w;
+        a.b = blk->norm2_b;
+        a.y = b.xn;
+        a.rows_out = (int64_t)S2 * S2;
+        a.C = Cout;
+        a.W = a.H = S2;
+        a.eps = hp->eps;
+        Timed t(ctx, "hiera_ln");
+        TRY(hip_check(ctx, t.done(launch_hiera_ln(a, st)), "hiera_ln launch"));
+    }
+    const int64_t M2 = (int64_t)S2 * S2;
+    const int MLP = 4 * Cout;
+    {
+        const mi355_tensor in = tensor_on(b.xn, T_F32, Cout, M2), out = tensor_on(b.h, T_F32, MLP, M2);
+        TRY(mi355_mul_mat(ctx, &blk->fc1_w, &in, &out));
+        Timed t(ctx, "bias_gelu_tanh");
+        TRY(hip_check(ctx, t.done(launch_bias_gelu_tanh(b.h, blk->fc1_b, M2, MLP, st)), "bias_gelu_tanh launch"));
+    }
+    {
+        const mi355_tensor in = tensor_on(b.h, T_F32, MLP, M2), out = tensor_on(b.f, T_F32, Cout, M2);
+        TRY(mi355_mul_mat(ctx, &blk->fc2_w, &in, &out));
+        Timed t(ctx, "bias_residual");
+        TRY(hip_check(ctx, t.done(launch_bias_residual(x_out, b.f, blk->fc2_b, M2, Cout, st)), "bias_residual launch"));
+    }
+    return MI355_STATUS_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi355_hiera_n_blocks(const mi355_hiera_hparams* hp) {
+    std::vector<Info> infos;
+    if (!hp || !block_infos(hp, infos)) return -1;
+    return (int)infos.size();
+}
+
+mi355_status mi355_hiera_block_info_get(const mi355_hiera_hparams* hp, int block_index, mi355_hiera_block_info* out) {
+    std::vector<Info> infos;
+    if (!hp || !out || !block_infos(hp, infos)) return fail(nullptr, MI355_STATUS_INVALID_ARG, "hiera: bad hparams");
+    if (block_index < 0 || block_index >= (int)infos.size())
+        return fail(nullptr, MI355_STATUS_INVALID_ARG, "hiera: block index %d out of range", block_index);
+    const Info& b = infos[block_index];
+    out->dim_in = b.dim_in;
+    out->dim_out = b.dim_out;
+    out->num_heads = b.heads;
+    out->window_size = b.ws;
+    out->q_stride = b.qs;
+    out->stage = b.stage;
+    return MI355_STATUS_SUCCESS;
+}
+
+size_t mi355_hiera_workspace_size(const mi355_hiera_hparams* hp) {
+    std::vector<Info> infos;
+    if (check_hp(nullptr, hp, infos) != MI355_STATUS_SUCCESS) return 0;
+    return layout(all_sizes(hp, infos), nullptr, nullptr);
+}
+
+mi355_status mi355_hiera_block_forward(mi355_context* ctx, const mi355_hiera_hparams* hp, int block_index,
+                                       const mi355_hiera_block* blk, const float* x, int spatial, float* x_out) {
+    std::vector<Info> infos;
+    TRY(check_hp(ctx, hp, infos));
+    if (!blk || !x || !x_out) return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera_block: null pointer");
+    if (block_index < 0 || block_index >= (int)infos.size())
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera_block: block index %d out of range", block_index);
+    const Info& bi = infos[block_index];
+    if (spatial <= 0 || (bi.qs && spatial % 2 != 0))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera_block: bad spatial size %d", spatial);
+    if (x == x_out) return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera_block: x_out must not overlap x");
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "hiera_block: null context");
+    (void)hipSetDevice(ctx->device);
+    // buffers sized for this block at this spatial size (at least the backbone's)
+    Sizes z = all_sizes(hp, infos);
+    z.max_with(block_sizes(bi, spatial));
+    TRY(ensure_buffer(ctx, &ctx->enc, &ctx->enc_size, layout(z, nullptr, nullptr)));
+    Bufs b;
+    layout(z, static_cast<char*>(ctx->enc), &b);
+    return run_block(ctx, hp, bi, blk, x, spatial, x_out, b);
+}
+
+mi355_status mi355_hiera_encode(mi355_context* ctx, const mi355_hiera_hparams* hp, const float* image,
+                                const mi355_tensor* patch_w, const float* patch_b, const float* pos_embed,
+                                const mi355_hiera_block* blocks, int n_blocks, float* const stage_out[4]) {
+    std::vector<Info> infos;
+    TRY(check_hp(ctx, hp, infos));
+    if (!image || !patch_w || !patch_b || !pos_embed || !blocks)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera_encode: null pointer");
+    if (n_blocks != (int)infos.size())
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera_encode: %d blocks given, the stage table has %d", n_blocks,
+                    (int)infos.size());
+    const int E = hp->embed_dim, IMG = hp->img_size, S0 = IMG / 4;
+    if (patch_w->ne[0] != 7 || patch_w->ne[1] != 7 || patch_w->ne[2] != 3 || patch_w->ne[3] != E ||
+        !(patch_w->type == T_F32 || patch_w->type == T_F16) || !patch_w->data)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera_encode: patch weight must be F32/F16 [7, 7, 3, E]");
+    if (patch_w->nb[0] != (patch_w->type == T_F32 ? 4 : 2) || patch_w->nb[3] != patch_w->nb[0] * 147)
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "hiera_encode: patch weight must be contiguous");
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "hiera_encode: null context");
+    (void)hipSetDevice(ctx->device);
+    Bufs b;
+    TRY(get_bufs(ctx, hp, infos, &b));
+    hipStream_t st = ctx->stream;
+    // patch embedding: ggml_conv_2d(w, img, 4, 4, 3, 3, 1, 1) = im2col + mul_mat, + bias, + pos_embed
+    const bool w16 = patch_w->type == T_F16;
+    {
+        Timed t(ctx, "im2col");
+        TRY(hip_check(ctx, t.done(launch_im2col_pad(image, b.cols, 3, IMG, IMG, 7, 7, 4, 3, S0, S0, w16, st)),
+                      "im2col launch"));
+    }
+    const float* w32 = static_cast<const float*>(patch_w->data);
+    if (w16) {  // the F16 kernel's products are exact in fp32: F32 GEMM over fp16-valued operands
+        TRY(hip_check(ctx, launch_f16_to_f32(patch_w->data, b.w32, 147LL * E, st), "f16_to_f32 launch"));
+        w32 = b.w32;
+    }
+    {
+        const mi355_tensor w = tensor_on(w32, T_F32, 147, E), cols = tensor_on(b.cols, T_F32, 147, (int64_t)S0 * S0),
+                           out = tensor_on(b.x0, T_F32, E, (int64_t)S0 * S0);
+        TRY(mi355_mul_mat(ctx, &w, &cols, &out));
+    }
+    {
+        Timed t(ctx, "bias_add_pe");
+        TRY(hip_check(ctx, t.done(launch_bias_add_pe(b.x0, patch_b, pos_embed, (int64_t)S0 * S0, E, st)), "bias_pe launch"));
+    }
+    float* cur = b.x0;
+    float* nxt = b.x1;
+    int S = S0, stage = 0;
+    int ends[4], total = 0;
+    for (int s = 0; s < 4; ++s) {
+        total += hp->stages[s];
+        ends[s] = total - 1;
+    }
+    for (int i = 0; i < n_blocks; ++i) {
+        TRY(run_block(ctx, hp, infos[i], &blocks[i], cur, S, nxt, b));
+        std::swap(cur, nxt);
+        if (infos[i].qs) S /= 2;
+        while (stage < 4 && hp->stages[stage] == 0) ++stage;
+        if (stage < 4 && i == ends[stage]) {
+            if (stage_out && stage_out[stage])
+                TRY(hip_check(ctx, hipMemcpyAsync(stage_out[stage], cur, (size_t)S * S * infos[i].dim_out * 4,
+                                                  hipMemcpyDeviceToDevice, st),
+                              "stage output copy"));
+            ++stage;
+        }
+    }
+    return MI355_STATUS_SUCCESS;
+}
+
+}  // extern "C"

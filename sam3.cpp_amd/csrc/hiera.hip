@@ -1,0 +1,292 @@
+// Memory-bound ops of the SAM2 Hiera image encoder (sam2_hiera_block_forward,
+// sam3.cpp:4299-4461, and the patch embedding of sam2_build_hiera_graph,
+// sam3.cpp:4473-4496), each fusing the ggml nodes that touch one tensor.
+// Token layouts: image order t = h*W + w (ggml [C, W, H]); window order of
+// sam2_window_partition: window n = wh + nW_h*ww over the zero-padded grid,
+// token lh*ws + lw inside it.  Every ggml node rounds to fp32 and so does
+// each fused step: no FMA contraction in this file.
+#pragma clang fp contract(off)
+#include "common.cuh"
+#include "kernels.h"
+
+namespace mi355 {
+
+// window-order row r -> image token, or -1 for a padding token
+__device__ __forceinline__ int64_t hwin_src(int64_t r, int W, int H, int ws, int nwh) {
+    const int64_t n = r / (ws * ws);
+    const int loc = (int)(r - n * ws * ws);
+    const int lh = loc / ws, lw = loc % ws;
+    const int wh = (int)(n % nwh), ww = (int)(n / nwh);
+    const int h = wh * ws + lh, w = ww * ws + lw;
+    return (h < H && w < W) ? (int64_t)h * W + w : -1;
+}
+
+__device__ __forceinline__ double wave_sum_dh(double v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// ggml_norm(eps) -> mul(w) -> add(b) over rows of C (C <= 2048), one wavefront per
+// output row.  ws > 0: output rows in window order (padding rows zero) and,
+// when y_img is set, the same rows also in image order.
+__global__ __launch_bounds__(256) void hiera_ln_kernel(const HieraLnArgs a) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= a.rows_out) return;
+    const int lane = threadIdx.x & 63, C = a.C;
+    const int per = (C + 63) / 64;
+    const int64_t src = a.ws > 0 ? hwin_src(r, a.W, a.H, a.ws, a.nwh) : r;
+    float* yr = a.y + r * C;
+    if (src < 0) {
+        for (int e = lane; e < C; e += 64) yr[e] = 0.0f;
+        return;
+    }
+    const float* xr = a.x + src * C;
+    float v[32];
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        const int e = j * 64 + lane;
+        if (j < per && e < C) {
+            v[j] = xr[e];
+            s += (double)v[j];
+        }
+    }
+    s = wave_sum_dh(s);
+    const float mean = (float)(s / (double)C);
+    double s2 = 0.0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        const int e = j * 64 + lane;
+        if (j < per && e < C) {
+            const float t = v[j] - mean;
+            v[j] = t;
+            s2 += (double)(t * t);
+        }
+    }
+    s2 = wave_sum_dh(s2);
+    const float var = (float)(s2 / (double)C);
+    const float scale = 1.0f / sqrtf(var + a.eps);
+    float* yi = a.y_img ? a.y_img + src * C : nullptr;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        const int e = j * 64 + lane;
+        if (j < per && e < C) {
+            float t = v[j] * scale;
+            t = t * a.w[e];
+            t = t + a.b[e];
+            yr[e] = t;
+            if (yi) yi[e] = t;
+        }
+    }
+}
+
+// K, V: thread per (attention batch bw, token t, head h, element pair i)
+__global__ __launch_bounds__(256) void hiera_kv_kernel(const HieraQkvArgs a) {
+    const int half = a.HD / 2, C = a.NH * a.HD;
+    const int64_t tix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t total = (int64_t)a.B * a.Nkv * a.NH * half;
+    if (tix >= total) return;
+    const int i = (int)(tix % half);
+    const int h = (int)((tix / half) % a.NH);
+    const int64_t t = (tix / ((int64_t)half * a.NH)) % a.Nkv;
+    const int64_t bw = tix / ((int64_t)half * a.NH * a.Nkv);
+    const int e = h * a.HD + 2 * i;
+    const float* row = a.qkv + (bw * a.Nkv + t) * (int64_t)(3 * C);
+    const float k0 = row[C + e] + a.bias[C + e], k1 = row[C + e + 1] + a.bias[C + e + 1];
+    const float v0 = row[2 * C + e] + a.bias[2 * C + e], v1 = row[2 * C + e + 1] + a.bias[2 * C + e + 1];
+    const int64_t o = ((bw * a.NH + h) * a.Nkv + t) * a.HD + 2 * i;
+    *reinterpret_cast<uint32_t*>(a.k + o) = (uint32_t)f2h(k0) | ((uint32_t)f2h(k1) << 16);
+    *reinterpret_cast<uint32_t*>(a.v + o) = (uint32_t)f2h(v0) | ((uint32_t)f2h(v1) << 16);
+}
+
+// Q: thread per (bw, query tq, head h, pair i); with q_pool, the 2x2 max of the
+// window's (ws x ws) token grid (sam2_maxpool_2d inside each window)
+__global__ __launch_bounds__(256) void hiera_q_kernel(const HieraQkvArgs a) {
+    const int half = a.HD / 2, C = a.NH * a.HD;
+    const int64_t tix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t total = (int64_t)a.B * a.Nq * a.NH * half;
+    if (tix >= total) return;
+    const int i = (int)(tix % half);
+    const int h = (int)((tix / half) % a.NH);
+    const int64_t tq = (tix / ((int64_t)half * a.NH)) % a.Nq;
+    const int64_t bw = tix / ((int64_t)half * a.NH * a.Nq);
+    const int e = h * a.HD + 2 * i;
+    const float b0 = a.bias[e], b1 = a.bias[e + 1];
+    float q0, q1;
+    if (a.qpool) {
+        const int wo = a.ws / 2;
+        const int ph = (int)(tq / wo), pw = (int)(tq % wo);
+        q0 = q1 = -__builtin_inff();
+#pragma unroll
+        for (int dy = 0; dy < 2; ++dy)
+#pragma unroll
+            for (int dx = 0; dx < 2; ++dx) {
+                const int64_t t = (int64_t)(2 * ph + dy) * a.ws + 2 * pw + dx;
+                const float* row = a.qkv + (bw * a.Nkv + t) * (int64_t)(3 * C);
+                q0 = fmaxf(q0, row[e] + b0);
+                q1 = fmaxf(q1, row[e + 1] + b1);
+            }
+    } else {
+        const float* row = a.qkv + (bw * a.Nkv + tq) * (int64_t)(3 * C);
+        q0 = row[e] + b0;
+        q1 = row[e + 1] + b1;
+    }
+    const int64_t o = ((bw * a.NH + h) * a.Nq + tq) * a.HD + 2 * i;
+    *reinterpret_cast<uint32_t*>(a.q + o) = (uint32_t)f2h(q0) | ((uint32_t)f2h(q1) << 16);
+}
+
+// pool: out[h2][w2] = max over 2x2 of (p[t] (+ b)); else out[t] = p[t] (+ b); rows of C
+__global__ __launch_bounds__(256) void hiera_bias_maxpool_kernel(const float* __restrict__ p, const float* __restrict__ b,
+                                                                 float* __restrict__ out, int C, int W, int H, int pool) {
+    if (!pool) {
+        const int64_t tix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        if (tix >= (int64_t)W * H * C) return;
+        out[tix] = b ? p[tix] + b[tix % C] : p[tix];
+        return;
+    }
+    const int W2 = W / 2, H2 = H / 2;
+    const int64_t tix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tix >= (int64_t)W2 * H2 * C) return;
+    const int c = (int)(tix % C);
+    const int64_t t2 = tix / C;
+    const int w2 = (int)(t2 % W2), h2 = (int)(t2 / W2);
+    const float bc = b ? b[c] : 0.0f;
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int dy = 0; dy < 2; ++dy)
+#pragma unroll
+        for (int dx = 0; dx < 2; ++dx) {
+            float v = p[((int64_t)(2 * h2 + dy) * W + 2 * w2 + dx) * C + c];
+            if (b) v = v + bc;
+            m = fmaxf(m, v);
+        }
+    out[tix] = m;
+}
+
+// x[t] = shortcut[t] + (p[row(t)] + b) over the image grid W x H (rows of C);
+// row(t) = window-order row for windows of ws (grid padded to a multiple of
+// ws, nwh windows along H), or t when ws == 0
+__global__ __launch_bounds__(256) void hiera_proj_residual_kernel(float* x, const float* shortcut,
+                                                                  const float* __restrict__ p,
+                                                                  const float* __restrict__ b, int C, int W, int H,
+                                                                  int ws, int nwh) {
+    const int64_t tix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tix >= (int64_t)W * H * C) return;
+    const int c = (int)(tix % C);
+    const int64_t t = tix / C;
+    int64_t r = t;
+    if (ws > 0) {
+        const int w = (int)(t % W), h = (int)(t / W);
+        const int64_t n = h / ws + (int64_t)nwh * (w / ws);
+        r = (n * ws + h % ws) * ws + w % ws;
+    }
+    const float u = p[r * C + c] + b[c];
+    x[tix] = shortcut[tix] + u;
+}
+
+// h = ggml_gelu(h + b) with ggml-cpu's fp16-table semantics (GGML_GELU_FP16):
+// 0 for x <= -10, x for x >= 10, else f16(gelu_f32(f16(x))).
+__global__ __launch_bounds__(256) void bias_gelu_tanh_kernel(float* __restrict__ h, const float* __restrict__ b,
+                                                             int64_t rows, int n) {
+    const int64_t tix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tix >= rows * n) return;
+    const int c = (int)(tix % n);
+    const float u = h[tix] + b[c];
+    float y;
+    if (u <= -10.0f) {
+        y = 0.0f;
+    } else if (u >= 10.0f) {
+        y = u;
+    } else {
+        const float v = h2f(f2h(u));
+        const float inner0 = 0.79788456080286535587989211986876f * v;
+        const float av = 0.044715f * v;
+        const float avv = av * v;
+        const float inner = inner0 * (1.0f + avv);
+        const float hv = 0.5f * v;
+        y = h2f(f2h(hv * (1.0f + tanhf(inner))));
+    }
+    h[tix] = y;
+}
+
+// conv2d columns with stride / zero padding: cols[m][k], m = oy*OW + ox,
+// k = (c*KH + ky)*KW + kx; optionally rounded to fp16 (F16 kernels, ggml_im2col F16)
+__global__ __launch_bounds__(256) void im2col_pad_kernel(const float* __restrict__ img, float* __restrict__ cols, int C,
+                                                         int Hin, int Win, int KH, int KW, int stride, int pad, int OH,
+                                                         int OW, int round16) {
+    const int64_t tix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int K = C * KH * KW;
+    if (tix >= (int64_t)OH * OW * K) return;
+    const int k = (int)(tix % K);
+    const int64_t m = tix / K;
+    const int kx = k % KW, ky = (k / KW) % KH, c = k / (KW * KH);
+    const int ox = (int)(m % OW), oy = (int)(m / OW);
+    const int y = oy * stride - pad + ky, xx = ox * stride - pad + kx;
+    float v = (y >= 0 && y < Hin && xx >= 0 && xx < Win) ? img[((int64_t)c * Hin + y) * Win + xx] : 0.0f;
+    if (round16) v = h2f(f2h(v));
+    cols[tix] = v;
+}
+
+// x = (conv + b) + pe over rows of C (patch embedding bias, then pos_embed)
+__global__ __launch_bounds__(256) void bias_add_pe_kernel(float* __restrict__ x, const float* __restrict__ b,
+                                                          const float* __restrict__ pe, int64_t rows, int C) {
+    const int64_t tix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tix >= rows * C) return;
+    const float u = x[tix] + b[tix % C];
+    x[tix] = u + pe[tix];
+}
+
+__global__ __launch_bounds__(256) void f16_to_f32_kernel(const uint16_t* __restrict__ s, float* __restrict__ d, int64_t n) {
+    const int64_t tix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tix < n) d[tix] = h2f(s[tix]);
+}
+
+static unsigned nblk(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+hipError_t launch_hiera_ln(const HieraLnArgs& a, hipStream_t st) {
+    if (a.rows_out <= 0) return hipSuccess;
+    if (a.C <= 0 || a.C > 2048) return hipErrorInvalidValue;
+    hiera_ln_kernel<<<(unsigned)((a.rows_out + 3) / 4), 256, 0, st>>>(a);
+    return hipGetLastError();
+}
+hipError_t launch_hiera_qkv(const HieraQkvArgs& a, hipStream_t st) {
+    const int half = a.HD / 2;
+    const int64_t nkv = (int64_t)a.B * a.Nkv * a.NH * half, nq = (int64_t)a.B * a.Nq * a.NH * half;
+    if (nkv > 0) hiera_kv_kernel<<<nblk(nkv), 256, 0, st>>>(a);
+    if (nq > 0) hiera_q_kernel<<<nblk(nq), 256, 0, st>>>(a);
+    return hipGetLastError();
+}
+hipError_t launch_hiera_bias_maxpool(const float* p, const float* b, float* out, int C, int W, int H, bool pool,
+                                     hipStream_t st) {
+    const int64_t n = pool ? (int64_t)(W / 2) * (H / 2) * C : (int64_t)W * H * C;
+    if (n > 0) hiera_bias_maxpool_kernel<<<nblk(n), 256, 0, st>>>(p, b, out, C, W, H, pool ? 1 : 0);
+    return hipGetLastError();
+}
+hipError_t launch_hiera_proj_residual(float* x, const float* shortcut, const float* p, const float* b, int C, int W,
+                                      int H, int ws, int nwh, hipStream_t st) {
+    const int64_t n = (int64_t)W * H * C;
+    if (n > 0) hiera_proj_residual_kernel<<<nblk(n), 256, 0, st>>>(x, shortcut, p, b, C, W, H, ws, nwh);
+    return hipGetLastError();
+}
+hipError_t launch_bias_gelu_tanh(float* h, const float* b, int64_t rows, int n, hipStream_t st) {
+    if (rows * n > 0) bias_gelu_tanh_kernel<<<nblk(rows * n), 256, 0, st>>>(h, b, rows, n);
+    return hipGetLastError();
+}
+hipError_t launch_im2col_pad(const float* img, float* cols, int C, int Hin, int Win, int KH, int KW, int stride, int pad,
+                             int OH, int OW, bool round16, hipStream_t st) {
+    const int64_t n = (int64_t)OH * OW * C * KH * KW;
+    if (n > 0)
+        im2col_pad_kernel<<<nblk(n), 256, 0, st>>>(img, cols, C, Hin, Win, KH, KW, stride, pad, OH, OW, round16 ? 1 : 0);
+    return hipGetLastError();
+}
+hipError_t launch_bias_add_pe(float* x, const float* b, const float* pe, int64_t rows, int C, hipStream_t st) {
+    if (rows * C > 0) bias_add_pe_kernel<<<nblk(rows * C), 256, 0, st>>>(x, b, pe, rows, C);
+    return hipGetLastError();
+}
+hipError_t launch_f16_to_f32(const void* s, float* d, int64_t n, hipStream_t st) {
+    if (n > 0) f16_to_f32_kernel<<<nblk(n), 256, 0, st>>>(static_cast<const uint16_t*>(s), d, n);
+    return hipGetLastError();
+}
+
+}  // namespace mi355

@@ -129,4 +129,37 @@ hipError_t launch_bias_gelu(float* h, const float* b, int64_t rows, int n, hipSt
 hipError_t launch_bias_residual(float* x, const float* f, const float* b, int64_t rows, int n, hipStream_t st);
 hipError_t launch_im2col(const float* img, float* cols, int C, int Himg, int Wimg, int P, int grid, hipStream_t st);
 
+// ---- SAM2 Hiera glue
+struct HieraLnArgs {
+    const float* x;    // [H*W][C] image order
+    const float* w;    // [C]
+    const float* b;    // [C]
+    float* y;          // [rows_out][C]: window order (ws > 0, padding rows zero) or image order
+    float* y_img;      // optional image-order copy (ws > 0 only)
+    int64_t rows_out;  // nW * ws * ws, or H * W
+    int C, W, H, ws, nwh;
+    float eps;
+};
+hipError_t launch_hiera_ln(const HieraLnArgs& a, hipStream_t st);
+struct HieraQkvArgs {
+    const float* qkv;   // [B*Nkv][3C] window-order rows
+    const float* bias;  // [3C]
+    _Float16* q;        // [B][NH][Nq][HD]
+    _Float16* k;        // [B][NH][Nkv][HD]
+    _Float16* v;
+    int B, Nkv, Nq, NH, HD;
+    int qpool;          // Q is the 2x2 max over each window's ws x ws grid
+    int ws;
+};
+hipError_t launch_hiera_qkv(const HieraQkvArgs& a, hipStream_t st);
+hipError_t launch_hiera_bias_maxpool(const float* p, const float* b, float* out, int C, int W, int H, bool pool,
+                                     hipStream_t st);
+hipError_t launch_hiera_proj_residual(float* x, const float* shortcut, const float* p, const float* b, int C, int W,
+                                      int H, int ws, int nwh, hipStream_t st);
+hipError_t launch_bias_gelu_tanh(float* h, const float* b, int64_t rows, int n, hipStream_t st);
+hipError_t launch_im2col_pad(const float* img, float* cols, int C, int Hin, int Win, int KH, int KW, int stride, int pad,
+                             int OH, int OW, bool round16, hipStream_t st);
+hipError_t launch_bias_add_pe(float* x, const float* b, const float* pe, int64_t rows, int C, hipStream_t st);
+hipError_t launch_f16_to_f32(const void* s, float* d, int64_t n, hipStream_t st);
+
 }  // namespace mi355
