@@ -171,6 +171,85 @@ def build_encoder(mi, orc, torch, dev, types, seed=0):
     return hp, pre, blocks, keep
 
 
+def build_hiera(mi, orc, torch, dev, tname, seed=0):
+    """Random-init SAM2.1 Hiera-tiny (img 1024, embed 96, heads 1, stages
+    1/2/7/2, windows 8/4/14/7, global blocks 5/7/9, q_pool 3): linear weights
+    f32 N(0,0.02) quantized to tname; the patch weight is F16 under F16 weights
+    and F32 otherwise (its rows of 7 are not a multiple of 32)."""
+    t = orc.NAME_TYPE[tname]
+    hp = mi.hiera_tiny(1024)
+    keep = []
+
+    def up(a):
+        x = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+        keep.append(x)
+        return x
+
+    blocks = []
+    for i in range(mi.lib().mi355_hiera_n_blocks(hp)):
+        info = mi.hiera_block_info(hp, i)
+        cin, cout = info.dim_in, info.dim_out
+        blk = mi.HieraBlock()
+        shapes = [("qkv", 3 * cout, cin), ("proj", cout, cout), ("fc1", 4 * cout, cout), ("fc2", cout, 4 * cout)]
+        if cin != cout:
+            shapes.append(("dim_proj", cout, cin))
+        for j, (name, n, k) in enumerate(shapes):
+            w = orc.normal(n * k, seed + i, 400 + j, std=0.02).reshape(n, k)
+            setattr(blk, name + "_w", mi.from_torch(up(orc.quantize_weights(t, w)), t, [k, n]))
+        for j, (name, n, sc, m) in enumerate([("norm1_w", cin, 0.1, 1.0), ("norm1_b", cin, 0.02, 0.0),
+                                              ("qkv_b", 3 * cout, 0.02, 0.0), ("proj_b", cout, 0.02, 0.0),
+                                              ("norm2_w", cout, 0.1, 1.0), ("norm2_b", cout, 0.02, 0.0),
+                                              ("fc1_b", 4 * cout, 0.02, 0.0), ("fc2_b", cout, 0.02, 0.0),
+                                              ("dim_proj_b", cout, 0.02, 0.0)]):
+            setattr(blk, name, up(orc.normal(n, seed + i, 450 + j) * np.float32(sc) + np.float32(m)).data_ptr())
+        blocks.append(blk)
+    E, S0 = hp.embed_dim, hp.img_size // 4
+    image = up(orc.uniform(3 * hp.img_size ** 2, seed, 500).reshape(3, hp.img_size, hp.img_size))
+    pw32 = orc.normal(E * 147, seed, 501, std=0.02)
+    if t == orc.F16:
+        patch_w = mi.from_torch(up(orc.quantize_weights(orc.F16, pw32.reshape(E, 147))), mi.F16, [7, 7, 3, E])
+    else:
+        patch_w = mi.from_torch(up(pw32), mi.F32, [7, 7, 3, E])
+    patch_b = up(orc.normal(E, seed, 502) * np.float32(0.02))
+    pos = up(orc.normal(S0 * S0 * E, seed, 503, std=0.02))
+    dims, S, stage_dims = [], S0, []
+    for i in range(len(blocks)):
+        info = mi.hiera_block_info(hp, i)
+        if info.q_stride:
+            S //= 2
+        dims.append((S, info.dim_out, info.stage))
+    for st in range(4):
+        last = [d for d in dims if d[2] == st][-1]
+        stage_dims.append((last[0], last[1]))
+    outs = [torch.empty((s * s, c), dtype=torch.float32, device=dev) for s, c in stage_dims]
+    keep += outs
+    return hp, (image.data_ptr(), patch_w, patch_b.data_ptr(), pos.data_ptr()), blocks, outs, keep
+
+
+def bench_hiera(mi, ctx, torch, hp, pre, blocks, outs, frames):
+    """ms per frame of the Hiera-tiny backbone (patch embedding + 12 blocks),
+    image resident in HBM; plus one profiled frame split by kernel."""
+    img, pw, pb, pos = pre
+    ptrs = [o.data_ptr() for o in outs]
+    run = lambda: ctx.hiera_encode(hp, C.c_void_p(img), pw, C.c_void_p(pb), C.c_void_p(pos), blocks, ptrs)
+    run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(frames):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / frames
+    finite = all(bool(torch.isfinite(o).all().item()) for o in outs)
+    ctx.profile(True)
+    run()
+    pr = ctx.profile_collect()
+    ctx.profile(False)
+    split = {k: round(v[1], 3) for k, v in sorted(pr.items(), key=lambda kv: -kv[1][1])}
+    return {"ms_per_frame": round(ms, 3), "frames": frames, "output_finite": finite, "kernel_ms_per_frame": split}
+
+
 def bench_encoder(mi, ctx, torch, dev, hp, pre, blocks, frames):
     """ms per frame of the whole encoder (prefix + 32 blocks), image resident in
     HBM; plus one profiled frame split by kernel."""
@@ -206,7 +285,8 @@ def main():
     ap.add_argument("--frames", type=int, default=3, help="timed encoder frames per weight type")
     ap.add_argument("--op", default=None,
                     help="profile mode, one workload --reps times with its kernel times: TYPE/LINEAR (e.g. q8_0/fc1), "
-                         "attn/windowed, attn/global, vit/TYPE (encoder frames), copy (256 MiB device copy)")
+                         "attn/windowed, attn/global, vit/TYPE (SAM3 ViT frames), hiera/TYPE (Hiera-tiny frames), "
+                         "copy (256 MiB device copy)")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--op-warmup", type=int, default=20)
     ap.add_argument("--no-traffic", action="store_true",
@@ -250,6 +330,13 @@ def main():
         which = args.op.split("/")[1]
         res = bench_attention(mi, ctx, torch, dev, only=which, reps=args.reps)
         print(json.dumps({"op": args.op, "reps": args.reps, **res[which]}), flush=True)
+        ctx.close()
+        return
+    if args.op and args.op.startswith("hiera/"):
+        tn = args.op.split("/")[1]
+        hp, pre, blocks, outs, keep = build_hiera(mi, orc, torch, dev, tn)
+        res = bench_hiera(mi, ctx, torch, hp, pre, blocks, outs, args.reps)
+        print(json.dumps({"op": args.op, **res}), flush=True)
         ctx.close()
         return
     if args.op and args.op.startswith("vit/"):
@@ -354,6 +441,7 @@ def main():
 
     # ---- full SAM3 ViT encoder ms/frame, Q8_0 and Q4_0 weights
     encoder = None
+    hiera = None
     if not args.no_encoder:
         log("bench: encoder weights")
         del calls
@@ -364,6 +452,12 @@ def main():
             log(f"bench: encoder {tn}")
             encoder[tn] = bench_encoder(mi, ctx, torch, dev, hp, pre, blocks[tn], args.frames)
         del keep
+        hiera = {}
+        for tn in ("f16", "q4_0"):
+            log(f"bench: hiera-tiny {tn}")
+            hp_h, pre_h, blocks_h, outs_h, keep_h = build_hiera(mi, orc, torch, dev, tn)
+            hiera[tn] = bench_hiera(mi, ctx, torch, hp_h, pre_h, blocks_h, outs_h, 5)
+            del keep_h
 
     # ---- CPU baseline: the oracle's ggml-cpu restatement, same fc1 Q8_0 mul_mat
     cpu = None
@@ -407,6 +501,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "vit_encoder_1008": encoder,
+        "hiera_tiny_1024": hiera,
         "attention": attn,
     }
     print(json.dumps(out), flush=True)
