@@ -127,9 +127,8 @@ MmPlan mm_plan(const mi355_tensor* s0, const mi355_tensor* s1) {
         if (!f16_src1_direct(s1)) pl.q = align_up((size_t)(Z * M * K) * 2);
         return pl;
     }
-    const int64_t Mp = mmq_scale_rows(M);
     pl.q = align_up((size_t)(Z * M * K) * 2);
-    pl.d = align_up((size_t)(Z * (K / 32) * Mp) * 2);
+    pl.d = align_up((size_t)(Z * M * mmq_scale_pitch(K)) * 2);
     if (s0->type == T_Q4_1) pl.s = pl.d;
     pl.align = align_up(mmq_align_bytes(matw_of(s0), s0->ne[1], K));
     return pl;
@@ -197,10 +196,11 @@ mi355_status prep_act_q8(mi355_context* ctx, const mi355_tensor* s0, const mi355
     a.s3 = K * M * s1->ne[2];
     a.d = d;
     a.s = sm;
+    a.dp = mmq_scale_pitch(K);
     a.M = M;
     a.K = K;
     Timed tm(ctx, "quantize_mmq");
-    return hip_check(ctx, tm.done(launch_quantize_mmq(view_of(s1), with_sum, mmq_scale_rows(M), q, d, sm, ctx->stream)),
+    return hip_check(ctx, tm.done(launch_quantize_mmq(view_of(s1), with_sum, a.dp, q, d, sm, ctx->stream)),
                      "quantize_mmq launch");
 }
 
@@ -304,6 +304,7 @@ mi355_status mi355_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
         a.M = M;
         a.K = K;
         a.d = a.s = nullptr;
+        a.dp = 0;
         if (f16_src1_direct(s1)) {
             a.q = s1->data;
             a.s1 = s1->nb[1] / 2;

@@ -22,24 +22,26 @@ struct SrcView {
 // Activation operand of the MFMA GEMM kernel, fp16 rows of K halves:
 // q[i12*s2 + i13*s3 + m*s1 + k] (strides in halves).  On the quantized path
 // these are the Q8 quants as exact fp16 integers, contiguous ([Z][M][K]),
-// with the per-block scale d[(z*nb + b)*Mp + m] and, for Q8_1, the block sum
-// term s[(z*nb + b)*Mp + m], both fp16 as ggml stores them; Mp =
-// mmq_scale_rows(M) pads the scale rows so every 128-row slice is a dword
-// aligned DMA.  On the F16 path q holds src1 converted to F16 (or src1
-// itself) and d, s are unused.
+// with the per-block scale d[(z*M + m)*dp + b] and, for Q8_1, the block sum
+// term s[(z*M + m)*dp + b], both fp16 as ggml stores them; dp =
+// mmq_scale_pitch(K) is the block count rounded up to even (padding slot
+// zero), so a row's two scales of one K stage are one aligned dword.  On the
+// F16 path q holds src1 converted to F16 (or src1 itself) and d, s are unused.
 struct ActF16 {
     const void* q;
     int64_t s1, s2, s3;
     const void* d;
     const void* s;
+    int64_t dp;
     int64_t M, K;
 };
+inline int64_t mmq_scale_pitch(int64_t K) { return ((K / 32) + 1) & ~(int64_t)1; }
 
 // ggml from_float into contiguous ggml rows: type 8 (Q8_0), 9 (Q8_1), 1 (F16).
 hipError_t launch_quantize_ggml(const SrcView& src, int type, bool ref_variant, void* dst, hipStream_t st);
 // from_float (x86 variant, Q8_0 or with_sum Q8_1 semantics) into the ActF16
-// quantized layout: q [rows][K] fp16, d and s [Z][nb][Mp] fp16, M = ne[1].
-hipError_t launch_quantize_mmq(const SrcView& src, bool with_sum, int64_t Mp, uint16_t* q, uint16_t* d, uint16_t* s,
+// quantized layout: q [rows][K] fp16, d and s [rows][dp] fp16.
+hipError_t launch_quantize_mmq(const SrcView& src, bool with_sum, int64_t dp, uint16_t* q, uint16_t* d, uint16_t* s,
                                hipStream_t st);
 // F32/F16 strided rows -> contiguous F16 rows [rows][ne0] (round to nearest even).
 hipError_t launch_convert_f16(const SrcView& src, uint16_t* dst, hipStream_t st);
@@ -62,7 +64,6 @@ struct MatD {  // dst F32
 hipError_t launch_mmq(const MatW& w, const ActF16& a, const MatD& d, int64_t N, int64_t ne12, int64_t ne13,
                       int32_t* dots, void* align_buf, hipStream_t st);
 // Padded row count of the activation scale arrays.
-int64_t mmq_scale_rows(int64_t M);
 // Bytes of the 4-byte-pitch weight copy launch_mmq needs (0 when rows are aligned).
 size_t mmq_align_bytes(const MatW& w, int64_t N, int64_t K);
 

@@ -92,12 +92,12 @@ struct MmqArgs {
     const _Float16* A;         // activations (fp16 values), row stride a_s1 halves
     int64_t a_s1, a_s2, a_s3;
     int64_t a_extent;          // bytes of one activation slice ((M-1)*s1 + K halves)
-    const _Float16* Ad;        // [Z][nb][M] activation scales (quantized path)
-    const _Float16* As;        // [Z][nb][M] Q8_1 sums (Q4_1 path)
+    const _Float16* Ad;        // [Z][M][dp] activation scales (quantized path)
+    const _Float16* As;        // [Z][M][dp] Q8_1 sums (Q4_1 path)
     float* D;
     int64_t d_nb1, d_nb2, d_nb3;
     int32_t* dots;             // block-dot inspection output (or null)
-    int M, Mp, N, K, ne12, r2, r3, tiles_m, tiles_n;  // Mp: padded row count of the scale arrays
+    int M, dp, N, K, ne12, r2, r3, tiles_m, tiles_n;  // dp: row pitch (halves) of the scale arrays
 };
 
 // 8 consecutive int8 quants (two dwords) -> 8 fp16 (one MFMA k-chunk).
@@ -159,8 +159,8 @@ struct Stage {
     _Float16 A[BM * SKH];                                // activation tile, swizzled 16-byte chunks
     _Float16 Bf[QUANT ? 8 : BN * SKH];                   // F16 weight tile (same swizzle)
     uint32_t W[QUANT ? RLD * NT : 4];                    // raw weight segments, lane-linear dwords
-    _Float16 Ad[BKB][BM];                                // activation scales of the two blocks
-    _Float16 As[WT == T_Q4_1 ? BKB : 1][BM];             // Q8_1 sums (Q4_1)
+    _Float16 Ad[BM][BKB];                                // activation scales of the two blocks, per row
+    _Float16 As[WT == T_Q4_1 ? BM : 1][BKB];             // Q8_1 sums (Q4_1), per row
 };
 
 // Workgroup 128(m) x 128(n); wavefront w owns all 128 rows of m and the 32
@@ -207,9 +207,9 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p) {
     const int nstage = QUANT ? (nb + BKB - 1) / BKB : (K + SKH - 1) / SKH;
     const uint8_t* Wz = p.W + (int64_t)(i12 / p.r2) * p.w_nb2 + (int64_t)(i13 / p.r3) * p.w_nb3;
     const _Float16* Az = p.A + (int64_t)i12 * p.a_s2 + (int64_t)i13 * p.a_s3;
-    const int Mp = p.Mp;
-    const _Float16* Adz = QUANT ? p.Ad + (int64_t)z * nb * Mp : nullptr;
-    const _Float16* Asz = WT == T_Q4_1 ? p.As + (int64_t)z * nb * Mp : nullptr;
+    const int dp = p.dp;
+    const _Float16* Adz = QUANT ? p.Ad + (int64_t)z * M * dp : nullptr;
+    const _Float16* Asz = WT == T_Q4_1 ? p.As + (int64_t)z * M * dp : nullptr;
     // wavefronts 0, 1 load the two blocks' d; for Q4_1, 2 and 3 load the two blocks' s
     const bool xload = QUANT && (wn < 2 || WT == T_Q4_1);
 
@@ -245,14 +245,13 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p) {
 #pragma unroll
             for (int i = 0; i < RLD; ++i)
                 dma_b32(wrs, &b.W[NT * i + 64 * wn], woff[i]);
-            const int bb = wn & 1;
-            const int64_t so = (int64_t)(s * BKB + bb) * Mp + m0;  // halves
+            // row m0 + 64*(w & 1) + lane: one dword = the row's scales of blocks 2s, 2s+1
+            const int sr_ = 64 * (wn & 1) + lane;
+            const int soff = m0 + sr_ < M ? ((m0 + sr_) * dp + s * BKB) * 2 : OOB;
             if (wn < 2) {
-                const auto dr = make_rsrc(Adz + so, 2LL * ((int64_t)nb * Mp - so));
-                dma_b32(dr, &b.Ad[bb][0], lane * 4);
+                dma_b32(make_rsrc(Adz, 2LL * M * dp), &b.Ad[64 * (wn & 1)][0], soff);
             } else if (WT == T_Q4_1) {
-                const auto sr = make_rsrc(Asz + so, 2LL * ((int64_t)nb * Mp - so));
-                dma_b32(sr, &b.As[WT == T_Q4_1 ? bb : 0][0], lane * 4);
+                dma_b32(make_rsrc(Asz, 2LL * M * dp), &b.As[WT == T_Q4_1 ? 64 * (wn & 1) : 0][0], soff);
             }
         } else {
             const auto fr = make_rsrc(Wz + 2LL * k0, p.w_extent - 2LL * k0);
@@ -284,13 +283,12 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p) {
                 // acc += sum_b s_a[m][b] * m_w[n][b] over this stage's blocks (k-slots 0, 1)
                 const uint32_t m1 = s * BKB + 1 < nb ? (uint32_t)hrow[WB / 2 + 1] << 16 : 0u;
                 const v4i mwf = {lo ? (int)((uint32_t)hrow[1] | m1) : 0, 0, 0, 0};
-                const uint16_t* as0 = reinterpret_cast<const uint16_t*>(&b.As[0][0]);
-                const uint16_t* as1 = reinterpret_cast<const uint16_t*>(&b.As[WT == T_Q4_1 ? 1 : 0][0]);
+                const uint32_t* asw = reinterpret_cast<const uint32_t*>(&b.As[0][0]);  // row: s of blocks 2s, 2s+1
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
                     const int ar_ = mt * 32 + lr;
                     v4i saf = __builtin_bit_cast(v4i, frag(b.A, ar_, g));  // finite filler
-                    saf[0] = (int)((uint32_t)as0[ar_] | ((uint32_t)as1[ar_] << 16));
+                    saf[0] = (int)asw[WT == T_Q4_1 ? ar_ : 0];
                     acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, saf),
                                                                      __builtin_bit_cast(v8h, mwf), acc[mt], 0, 0, 0);
                 }
@@ -333,7 +331,7 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p) {
                             // S-MFMA A operand: d_a in k-slot 0; the other k-slots keep a1's
                             // (finite) quants, which meet B's zeros
                             v4i daf = __builtin_bit_cast(v4i, a1);
-                            daf[0] = (int)(uint32_t) reinterpret_cast<const uint16_t*>(&b.Ad[bk][0])[ar_];
+                            daf[0] = (int)(uint32_t) reinterpret_cast<const uint16_t*>(&b.Ad[0][0])[ar_ * BKB + bk];
                             S[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, daf),
                                                                           __builtin_bit_cast(v8h, dwf), zf, 0, 0, 0);
                         }
@@ -420,7 +418,6 @@ static void launch_t(const MmqArgs& a, int Z, bool dots, hipStream_t st) {
     else mmq_kernel<WT, false><<<grid, NT, 0, st>>>(a);
 }
 
-int64_t mmq_scale_rows(int64_t M) { return (M + BM - 1) / BM * BM; }
 
 // The weight DMA reads whole dwords and the buffer range check zeroes a dword
 // that straddles the end, so rows must start 4-byte aligned and span a whole
@@ -470,7 +467,7 @@ hipError_t launch_mmq(const MatW& w_in, const ActF16& a, const MatD& d, int64_t 
     p.d_nb3 = d.nb3;
     p.dots = dots;
     p.M = (int)a.M;
-    p.Mp = (int)mmq_scale_rows(a.M);
+    p.dp = (int)a.dp;
     p.N = (int)N;
     p.K = (int)a.K;
     p.ne12 = (int)ne12;
@@ -479,7 +476,7 @@ hipError_t launch_mmq(const MatW& w_in, const ActF16& a, const MatD& d, int64_t 
     p.tiles_m = (int)((a.M + BM - 1) / BM);
     p.tiles_n = (int)((N + BN - 1) / BN);
     // buffer offsets are 32-bit
-    if (p.w_extent >= OOB || p.a_extent >= OOB) return hipErrorInvalidValue;
+    if (p.w_extent >= OOB || p.a_extent >= OOB || 2 * a.M * a.dp >= OOB) return hipErrorInvalidValue;
     const int Z = (int)(ne12 * ne13);
     switch (w.type) {
         case T_Q8_0: launch_t<T_Q8_0>(p, Z, dots, st); break;

@@ -89,49 +89,58 @@ __global__ __launch_bounds__(256) void quantize_ggml_kernel(const char* __restri
     }
 }
 
-// Same arithmetic (x86 variant) into the MFMA operand layout: quants as fp16
-// integers (exact), scale and Q8_1 sum as the fp16 values ggml would store.
+// Same arithmetic (x86 variant) into the MFMA operand layout, one thread per
+// 32-element block: quants as fp16 integers (exact) [rows][K], scale and Q8_1
+// sum as the fp16 values ggml stores, [rows][dp] (dp = block count rounded up
+// to even; the padding slot is written as zero).  A wavefront covers 64
+// consecutive blocks of the flattened [rows][nb] grid, so loads (128 B per
+// thread), quant stores (64 B per thread) and scale stores are contiguous.
 template <bool WITH_SUM>
 __global__ __launch_bounds__(256) void quantize_mmq_kernel(const char* __restrict__ src, int stype, RowAddr ra,
-                                                           int64_t ne0, int64_t nblocks, int64_t M, int64_t Mp,
+                                                           int64_t ne0, int64_t nblocks, int64_t dp,
                                                            uint16_t* __restrict__ qout, uint16_t* __restrict__ dout,
                                                            uint16_t* __restrict__ sout) {
-    const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t g = gt >> 3;
-    const int t = threadIdx.x & 7;
-    const bool valid = g < nblocks;
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= nblocks) return;
     const int64_t nbpr = ne0 / QK;
-    const int64_t r = valid ? g / nbpr : 0;
-    const int64_t b = valid ? g % nbpr : 0;
-    float x[4] = {0.f, 0.f, 0.f, 0.f};
-    if (valid) {
-        const char* rp = ra.row(src, r);
-        if (stype == T_F32 && ra.nb0 == 4 && ((reinterpret_cast<uintptr_t>(rp) & 15) == 0)) {
-            const v4f v = *reinterpret_cast<const v4f*>(rp + (b * QK + 4 * t) * 4);
-            x[0] = v[0]; x[1] = v[1]; x[2] = v[2]; x[3] = v[3];
-        } else {
+    const int64_t r = g / nbpr, b = g - r * nbpr;
+    const char* rp = ra.row(src, r);
+    float x[QK];
+    if (stype == T_F32 && ra.nb0 == 4 && ((reinterpret_cast<uintptr_t>(rp) & 15) == 0)) {
+        const v4f* p4 = reinterpret_cast<const v4f*>(rp + b * QK * 4);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) x[j] = ld_elem(rp + (b * QK + 4 * t + j) * ra.nb0, stype);
+        for (int j = 0; j < QK / 4; ++j) {
+            const v4f v = p4[j];
+            x[4 * j] = v[0];
+            x[4 * j + 1] = v[1];
+            x[4 * j + 2] = v[2];
+            x[4 * j + 3] = v[3];
         }
-    }
-    uint16_t dh;
-    float d32;
-    int isum;
-    const uint32_t packed = q8_lanes<false>(x, dh, d32, isum);
-    if (!valid) return;
-    uint32_t hq[2];
+    } else {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int q0 = (int)(int8_t)((packed >> (16 * j)) & 0xffu);
-        const int q1 = (int)(int8_t)((packed >> (16 * j + 8)) & 0xffu);
+        for (int j = 0; j < QK; ++j) x[j] = ld_elem(rp + (b * QK + j) * ra.nb0, stype);
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < QK; ++j) amax = fmaxf(amax, fabsf(x[j]));
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    uint32_t hq[QK / 2];
+    int isum = 0;
+#pragma unroll
+    for (int j = 0; j < QK / 2; ++j) {
+        const int q0 = (int)rintf(x[2 * j] * id), q1 = (int)rintf(x[2 * j + 1] * id);
+        isum += q0 + q1;
         hq[j] = (uint32_t)f2h((float)q0) | ((uint32_t)f2h((float)q1) << 16);
     }
-    *reinterpret_cast<uint2*>(qout + r * ne0 + b * QK + 4 * t) = make_uint2(hq[0], hq[1]);
-    if (t == 0) {
-        const int64_t z = r / M, m = r % M;
-        const int64_t si = (z * nbpr + b) * Mp + m;
-        dout[si] = dh;
-        if (WITH_SUM) sout[si] = f2h(d32 * (float)isum);
+    uint4* qd = reinterpret_cast<uint4*>(qout + r * ne0 + b * QK);
+#pragma unroll
+    for (int j = 0; j < QK / 8; ++j) qd[j] = make_uint4(hq[4 * j], hq[4 * j + 1], hq[4 * j + 2], hq[4 * j + 3]);
+    dout[r * dp + b] = f2h(d);
+    if (WITH_SUM) sout[r * dp + b] = f2h(d * (float)isum);
+    if (b == nbpr - 1 && dp > nbpr) {
+        dout[r * dp + nbpr] = 0;
+        if (WITH_SUM) sout[r * dp + nbpr] = 0;
     }
 }
 
@@ -174,18 +183,17 @@ hipError_t launch_quantize_ggml(const SrcView& src, int type, bool ref_variant, 
     return hipGetLastError();
 }
 
-hipError_t launch_quantize_mmq(const SrcView& src, bool with_sum, int64_t Mp, uint16_t* q, uint16_t* d, uint16_t* s,
+hipError_t launch_quantize_mmq(const SrcView& src, bool with_sum, int64_t dp, uint16_t* q, uint16_t* d, uint16_t* s,
                                hipStream_t st) {
     const int64_t rows = src.ne[1] * src.ne[2] * src.ne[3];
     const int64_t nblocks = rows * (src.ne[0] / QK);
     if (nblocks == 0) return hipSuccess;
-    const dim3 grid((unsigned)((nblocks * 8 + 255) / 256));
+    const dim3 grid((unsigned)((nblocks + 255) / 256));
     const RowAddr ra = row_addr(src);
     if (with_sum)
-        quantize_mmq_kernel<true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, src.ne[1], Mp, q, d, s);
+        quantize_mmq_kernel<true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, dp, q, d, s);
     else
-        quantize_mmq_kernel<false><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, src.ne[1], Mp, q, d,
-                                                         s);
+        quantize_mmq_kernel<false><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, dp, q, d, s);
     return hipGetLastError();
 }
 
