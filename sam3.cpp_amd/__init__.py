@@ -149,6 +149,7 @@ def lib():
         "mi355_hiera_block_forward": (I, [P, C.POINTER(HieraHparams), I, C.POINTER(HieraBlock), P, I, P]),
         "mi355_hiera_encode": (I, [P, C.POINTER(HieraHparams), P, T, P, P, C.POINTER(HieraBlock), I,
                                    C.POINTER(P)]),
+        "mi355_context_set_fusion": (I, [P, I]),
         "mi355_profile_enable": (I, [P, I]),
         "mi355_profile_collect": (I, [P]),
         "mi355_profile_get": (I, [P, I, C.POINTER(C.c_char_p), C.POINTER(I), C.POINTER(C.c_double)]),
@@ -241,6 +242,10 @@ class Context:
 
     def soft_max_ext(self, src: Tensor, dst: Tensor, scale: float):
         self._check(self.L.mi355_soft_max_ext(self.h, C.byref(src), None, scale, 0.0, C.byref(dst)))
+
+    def set_fusion(self, enable: bool):
+        """Encoder runners: producer passes write the MUL_MAT operand (default) or f32 rows."""
+        self._check(self.L.mi355_context_set_fusion(self.h, 1 if enable else 0))
 
     def profile(self, enable: bool):
         self._check(self.L.mi355_profile_enable(self.h, 1 if enable else 0))

@@ -206,6 +206,53 @@ mi355_status prep_act_q8(mi355_context* ctx, const mi355_tensor* s0, const mi355
 
 }  // namespace
 
+namespace mi355 {
+
+int act_mode_for(int t) {
+    switch (t) {
+        case T_Q8_0:
+        case T_Q4_0: return ACT_Q8;
+        case T_Q4_1: return ACT_Q8S;
+        case T_F16: return ACT_F16;
+        default: return ACT_F32;
+    }
+}
+
+mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const mi355_tensor* d) {
+    if (!s0 || !a.q) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat_act: null operand");
+    const int mode = act_mode_for(s0->type);
+    if (mode == ACT_F32) return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat_act: no prequantized path for type %d", s0->type);
+    if (mode != ACT_F16 && (!a.d || (mode == ACT_Q8S && !a.s) || a.dp != mmq_scale_pitch(a.K)))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat_act: scales missing or wrong pitch");
+    // validate the weights and dst as mul_mat would see them with an F32 [K, M] src1
+    mi355_tensor s1{};
+    s1.type = T_F32;
+    s1.ne[0] = a.K;
+    s1.ne[1] = a.M;
+    s1.ne[2] = s1.ne[3] = 1;
+    s1.nb[0] = 4;
+    s1.nb[1] = 4 * a.K;
+    s1.nb[2] = s1.nb[3] = s1.nb[1] * a.M;
+    s1.data = const_cast<void*>(a.q);
+    mi355_status st = check_mul_mat(ctx, s0, &s1, d);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "mul_mat_act: null context");
+    (void)hipSetDevice(ctx->device);
+    const int64_t N = s0->ne[1];
+    const size_t align = align_up(mmq_align_bytes(matw_of(s0), N, a.K));
+    if (align) {
+        st = ensure_ws(ctx, align);
+        if (st != MI355_STATUS_SUCCESS) return st;
+    }
+    const char* kname = s0->type == T_F16 ? "mmq_f16" : s0->type == T_Q8_0 ? "mmq_q8_0" : s0->type == T_Q4_0 ? "mmq_q4_0" : "mmq_q4_1";
+    Timed tq(ctx, kname);
+    return hip_check(ctx, tq.done(launch_mmq(matw_of(s0), a, matd_of(d), N, 1, 1, nullptr, align ? ctx->ws : nullptr,
+                                             ctx->stream)),
+                     "mmq launch");
+}
+
+}  // namespace mi355
+
 extern "C" {
 
 const char* mi355_status_to_string(mi355_status s) {
@@ -398,6 +445,12 @@ mi355_status mi355_soft_max_ext(mi355_context* ctx, const mi355_tensor* src, con
     Timed ts(ctx, "soft_max");
     return hip_check(ctx, ts.done(launch_soft_max(view_of(src), scale, static_cast<char*>(dst->data), dst->nb, ctx->stream)),
                      "soft_max launch");
+}
+
+mi355_status mi355_context_set_fusion(mi355_context* ctx, int enable) {
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "set_fusion: null context");
+    ctx->fuse = enable != 0;
+    return MI355_STATUS_SUCCESS;
 }
 
 mi355_status mi355_profile_enable(mi355_context* ctx, int enable) {

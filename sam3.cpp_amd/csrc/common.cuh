@@ -64,6 +64,121 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// ---- activation producers that feed a MUL_MAT (ActOut, kernels.h)
+// ggml from_float x86 of 32-value blocks (d = amax/127, id = 127/amax, round
+// half to even), or F16 / F32 rows.  A lane holds 4 consecutive values, chunk
+// c of the row (elements 4c..4c+3); the 8 lanes holding chunks 8k..8k+7 (lanes
+// congruent to them mod 8, all active) hold one block and reduce it together.
+__device__ __forceinline__ void act_store_chunk(const ActOut& o, int64_t row, int64_t K, int64_t c, v4f x) {
+    if (o.mode == ACT_F32) {
+        *reinterpret_cast<v4f*>(o.y + row * K + 4 * c) = x;
+        return;
+    }
+    uint32_t h0, h1;
+    if (o.mode == ACT_F16) {
+        h0 = (uint32_t)f2h(x[0]) | ((uint32_t)f2h(x[1]) << 16);
+        h1 = (uint32_t)f2h(x[2]) | ((uint32_t)f2h(x[3]) << 16);
+    } else {
+        float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+        amax = group_max<8>(amax);
+        const float d = amax / 127.0f;
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        const int q0 = (int)rintf(x[0] * id), q1 = (int)rintf(x[1] * id);
+        const int q2 = (int)rintf(x[2] * id), q3 = (int)rintf(x[3] * id);
+        h0 = (uint32_t)f2h((float)q0) | ((uint32_t)f2h((float)q1) << 16);
+        h1 = (uint32_t)f2h((float)q2) | ((uint32_t)f2h((float)q3) << 16);
+        int isum = 0;
+        if (o.mode == ACT_Q8S) isum = group_sum_i<8>(q0 + q1 + q2 + q3);
+        if ((c & 7) == 0) {
+            const int64_t b = c >> 3;
+            o.d[row * o.dp + b] = f2h(d);
+            if (o.mode == ACT_Q8S) o.s[row * o.dp + b] = f2h(d * (float)isum);
+            if (b == K / 32 - 1 && o.dp > K / 32) {  // zero the even-pitch padding slot
+                o.d[row * o.dp + b + 1] = 0;
+                if (o.mode == ACT_Q8S) o.s[row * o.dp + b + 1] = 0;
+            }
+        }
+    }
+    *reinterpret_cast<uint2*>(o.q + row * K + 4 * c) = make_uint2(h0, h1);
+}
+
+// ggml_norm -> mul(w) -> add(b) of one row of C held by a group of G lanes
+// (G a power of two, aligned), lane l holding chunks v*G + l, v < V (C = 4*G*V).
+// Sums in double as ggml_float; every step rounds to fp32 (callers compile
+// without FMA contraction).
+template <int V>
+__device__ __forceinline__ void ln_group(v4f (&x)[V], int l, int G, int C, const float* w, const float* b, float eps) {
+    double s = 0.0;
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s += (double)x[v][i];
+    for (int o = G / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, G);
+    const float mean = (float)(s / (double)C);
+    double s2 = 0.0;
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float t = x[v][i] - mean;
+            x[v][i] = t;
+            s2 += (double)(t * t);
+        }
+    for (int o = G / 2; o > 0; o >>= 1) s2 += __shfl_xor(s2, o, G);
+    const float var = (float)(s2 / (double)C);
+    const float scale = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        const int c = v * G + l;
+        v4f t = x[v] * scale;
+        if (w) t = t * *reinterpret_cast<const v4f*>(w + 4 * c);
+        if (b) t = t + *reinterpret_cast<const v4f*>(b + 4 * c);
+        x[v] = t;
+    }
+}
+
+// lanes per row G (largest power of two <= 64 dividing C/4) and chunks per
+// lane V = C/(4G) for the grouped LayerNorm; V > 8 means the row does not fit
+inline void ln_shape(int C, int* G, int* V) {
+    int g = 1;
+    while (g < 64 && (C / 4) % (2 * g) == 0) g *= 2;
+    *G = g;
+    *V = C % 4 == 0 ? C / (4 * g) : 1 << 30;
+}
+
+// Lane-per-element variant for rows the grouped form does not fit: element
+// e = 32*blk + (lane & 31) of the row, the 32 lanes of a wavefront half
+// holding one block (all 64 lanes call it; valid = false lanes hold no
+// element and contribute 0).
+__device__ __forceinline__ void act_store_lane32(const ActOut& o, int64_t row, int64_t K, int e, float v, bool valid) {
+    if (o.mode == ACT_F32) {
+        if (valid) o.y[row * K + e] = v;
+        return;
+    }
+    if (o.mode == ACT_F16) {
+        if (valid) o.q[row * K + e] = f2h(v);
+        return;
+    }
+    const float amax = group_max<32>(valid ? fabsf(v) : 0.0f);
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    const int q = valid ? (int)rintf(v * id) : 0;
+    int isum = 0;
+    if (o.mode == ACT_Q8S) isum = group_sum_i<32>(q);
+    if (valid) {
+        o.q[row * K + e] = f2h((float)q);
+        if ((e & 31) == 0) {
+            const int64_t b = e / 32;
+            o.d[row * o.dp + b] = f2h(d);
+            if (o.mode == ACT_Q8S) o.s[row * o.dp + b] = f2h(d * (float)isum);
+            if (b == K / 32 - 1 && o.dp > K / 32) {
+                o.d[row * o.dp + b + 1] = 0;
+                if (o.mode == ACT_Q8S) o.s[row * o.dp + b + 1] = 0;
+            }
+        }
+    }
+}
+
 // Unaligned 2-byte-granular loads of quantized block payloads (ggml blocks
 // are 34/18/20 bytes, so qs is only 2-byte aligned in general).
 __device__ __forceinline__ uint32_t ld_u32_a2(const uint8_t* p) {

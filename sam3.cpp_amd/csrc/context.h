@@ -19,6 +19,8 @@ struct mi355_context {
     void* enc = nullptr;       // activation buffers of the image-encoder runner
     size_t enc_size = 0;
     std::string last_error;
+    // encoder runners: producer passes write the next MUL_MAT's operand
+    bool fuse = true;
     // kernel timing
     bool prof = false;
     struct Pending { const char* name; hipEvent_t a, b; };
@@ -40,6 +42,15 @@ size_t align_up(size_t x);
 // Grows a device buffer owned by the context to at least bytes (waits for the
 // stream first: earlier kernels may still read the old buffer).
 mi355_status ensure_buffer(mi355_context* ctx, void** buf, size_t* size, size_t bytes);
+
+// The activation layout a producer pass should write for weights of type t:
+// Q8 quants for Q8_0/Q4_0, Q8 with Q8_1 sums for Q4_1, F16 for F16, F32 otherwise.
+int act_mode_for(int weight_type);
+// MUL_MAT of weights s0 with an activation operand already in the layout
+// act_mode_for(s0->type) describes (a: quants or F16 rows, scales), as a
+// fused producer pass writes it; dst F32 [N][M] rows.  Same validation and
+// kernels as mi355_mul_mat minus the activation quantize.
+mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const mi355_tensor* dst);
 
 // Brackets one launch with events when timing is enabled.
 struct Timed {

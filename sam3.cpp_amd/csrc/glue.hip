@@ -34,21 +34,47 @@ __device__ __forceinline__ int64_t win_row(int64_t r, int grid, int ws) {
     return (((int64_t)(y / ws) * nwx + x / ws) * ws + y % ws) * ws + x % ws;
 }
 
-// One wavefront per row of E (E % 64 == 0, E <= 2048).
+// Row r's addend row: the same row, or the pos_embed [pg x pg] table tiled
+// over the grid x grid image
+__device__ __forceinline__ const float* ln_addend(const LnArgs& a, int64_t r) {
+    if (!a.add) return nullptr;
+    int64_t pr = r;
+    if (a.add_grid > 0) {
+        const int y = (int)(r / a.grid), x = (int)(r % a.grid);
+        pr = (int64_t)(y % a.add_grid) * a.add_grid + x % a.add_grid;
+    }
+    return a.add + pr * a.E;
+}
+
+// G lanes per row (E = 4*G*V), 256/G rows per workgroup, float4 loads
+template <int V>
+__global__ __launch_bounds__(256) void ln_group_kernel(const LnArgs a, int G) {
+    const int64_t r = (int64_t)blockIdx.x * (256 / G) + threadIdx.x / G;
+    if (r >= a.rows) return;
+    const int l = threadIdx.x & (G - 1), E = a.E;
+    const float* xr = a.x + r * E;
+    const float* ar = ln_addend(a, r);
+    v4f x[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        const int c = v * G + l;
+        x[v] = *reinterpret_cast<const v4f*>(xr + 4 * c);
+        if (ar) x[v] = x[v] + *reinterpret_cast<const v4f*>(ar + 4 * c);
+    }
+    ln_group<V>(x, l, G, E, a.w, a.b, a.eps);
+    const int64_t orow = a.ws > 0 ? win_row(r, a.grid, a.ws) : r;
+#pragma unroll
+    for (int v = 0; v < V; ++v) act_store_chunk(a.out, orow, E, v * G + l, x[v]);
+}
+
+// One wavefront per row of E (E % 64 == 0, E <= 2048): rows the grouped form
+// does not fit.
 __global__ __launch_bounds__(256) void ln_kernel(const LnArgs a) {
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= a.rows) return;
     const int lane = threadIdx.x & 63, E = a.E, per = E / 64;
     const float* xr = a.x + r * E;
-    const float* ar = nullptr;
-    if (a.add) {
-        int64_t pr = r;
-        if (a.add_grid > 0) {  // pos_embed [pg x pg] tiled over the grid x grid image
-            const int y = (int)(r / a.grid), x = (int)(r % a.grid);
-            pr = (int64_t)(y % a.add_grid) * a.add_grid + x % a.add_grid;
-        }
-        ar = a.add + pr * E;
-    }
+    const float* ar = ln_addend(a, r);
     float v[32];
     double s = 0.0;
 #pragma unroll
@@ -75,7 +101,6 @@ __global__ __launch_bounds__(256) void ln_kernel(const LnArgs a) {
     const float var = (float)(s2 / (double)E);
     const float scale = 1.0f / sqrtf(var + a.eps);
     const int64_t orow = a.ws > 0 ? win_row(r, a.grid, a.ws) : r;
-    float* yr = a.y + orow * E;
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
         if (j < per) {
@@ -83,7 +108,7 @@ __global__ __launch_bounds__(256) void ln_kernel(const LnArgs a) {
             float t = v[j] * scale;
             if (a.w) t = t * a.w[e];
             if (a.b) t = t + a.b[e];
-            yr[e] = t;
+            act_store_lane32(a.out, orow, E, e, t, true);
         }
     }
 }
@@ -159,6 +184,27 @@ __global__ __launch_bounds__(256) void bias_gelu_kernel(float* __restrict__ h, c
     *reinterpret_cast<v4f*>(h + r * n + c) = hv;
 }
 
+// h + b -> gelu_erf -> the next MUL_MAT's operand; one thread per 4 values
+// (n % 32 == 0, so the 8 threads of a block are lanes of one wavefront)
+__global__ __launch_bounds__(256) void bias_gelu_act_kernel(const float* __restrict__ h, const float* __restrict__ b,
+                                                            int64_t rows, int n, const ActOut o) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int n4 = n / 4;
+    if (t >= rows * n4) return;
+    const int64_t r = t / n4;
+    const int c = (int)(t - r * n4);
+    const v4f hv = *reinterpret_cast<const v4f*>(h + r * n + 4 * c);
+    const v4f bv = *reinterpret_cast<const v4f*>(b + 4 * c);
+    v4f x;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float u = hv[k] + bv[k];
+        const float hx = 0.5f * u;
+        x[k] = hx * (1.0f + erff(u * 0.70710678118654752440f));
+    }
+    act_store_chunk(o, r, n, c, x);
+}
+
 // x = x + (f + b) over rows of n
 __global__ __launch_bounds__(256) void bias_residual_kernel(float* __restrict__ x, const float* __restrict__ f,
                                                             const float* __restrict__ b, int64_t rows, int n) {
@@ -198,7 +244,20 @@ static unsigned blocks_for(int64_t n, int per_block = 256) { return (unsigned)((
 hipError_t launch_layer_norm(const LnArgs& a, hipStream_t st) {
     if (a.rows <= 0) return hipSuccess;
     if (a.E % 64 != 0 || a.E > 2048) return hipErrorInvalidValue;
-    ln_kernel<<<blocks_for(a.rows, 4), 256, 0, st>>>(a);
+    int G, V;  // E % 64 == 0: G >= 16, so each 32-block's 8 lanes share a row
+    ln_shape(a.E, &G, &V);
+    const unsigned nb = blocks_for(a.rows, 256 / G);
+    switch (V) {
+        case 1: ln_group_kernel<1><<<nb, 256, 0, st>>>(a, G); break;
+        case 2: ln_group_kernel<2><<<nb, 256, 0, st>>>(a, G); break;
+        case 3: ln_group_kernel<3><<<nb, 256, 0, st>>>(a, G); break;
+        case 4: ln_group_kernel<4><<<nb, 256, 0, st>>>(a, G); break;
+        case 5: ln_group_kernel<5><<<nb, 256, 0, st>>>(a, G); break;
+        case 6: ln_group_kernel<6><<<nb, 256, 0, st>>>(a, G); break;
+        case 7: ln_group_kernel<7><<<nb, 256, 0, st>>>(a, G); break;
+        case 8: ln_group_kernel<8><<<nb, 256, 0, st>>>(a, G); break;
+        default: ln_kernel<<<blocks_for(a.rows, 4), 256, 0, st>>>(a); break;
+    }
     return hipGetLastError();
 }
 
@@ -219,6 +278,12 @@ hipError_t launch_proj_residual(float* x, const float* p, const float* b, int64_
 hipError_t launch_bias_gelu(float* h, const float* b, int64_t rows, int n, hipStream_t st) {
     if (n % 4) return hipErrorInvalidValue;
     bias_gelu_kernel<<<blocks_for(rows * (n / 4)), 256, 0, st>>>(h, b, rows, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_bias_gelu_act(const float* h, const float* b, int64_t rows, int n, const ActOut& o, hipStream_t st) {
+    if (n % 32) return hipErrorInvalidValue;
+    bias_gelu_act_kernel<<<blocks_for(rows * (n / 4)), 256, 0, st>>>(h, b, rows, n, o);
     return hipGetLastError();
 }
 

@@ -11,7 +11,10 @@
 //   x'   = x' + (mul_mat(fc2_w, gelu(mul_mat(fc1_w, LN2(x')) + fc1_b)) + fc2_b)
 //
 // MUL_MAT and FLASH_ATTN_EXT go through the backend's own entry points; the
-// memory-bound steps are the fused passes of hiera.hip.
+// memory-bound steps are the fused passes of hiera.hip.  For quantized and F16
+// weights the passes feeding a MUL_MAT (LN1 -> qkv and dim_proj, LN2 -> fc1,
+// bias+GELU -> fc2) write the GEMM's activation operand (Q8 quants + scales,
+// or F16 rows) directly instead of f32 rows that MUL_MAT would quantize again.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -67,13 +70,31 @@ int cdiv(int a, int b) { return (a + b - 1) / b; }
 
 // activation buffers of one block (or their maxima over the backbone)
 struct Sizes {
-    size_t xw = 0, xn = 0, dp = 0, sc = 0, qkv = 0, q = 0, kv = 0, att = 0, p = 0, h = 0, f = 0, x = 0, cols = 0, w32 = 0;
+    size_t xw = 0, xn = 0, dp = 0, sc = 0, qkv = 0, q = 0, kv = 0, att = 0, p = 0, h = 0, f = 0, x = 0, cols = 0, w32 = 0,
+           a0 = 0, a1 = 0;
+    static constexpr int kFields = 16;
     void max_with(const Sizes& o) {
         size_t* a = &xw;
         const size_t* b = &o.xw;
-        for (int i = 0; i < 14; ++i) a[i] = std::max(a[i], b[i]);
+        for (int i = 0; i < kFields; ++i) a[i] = std::max(a[i], b[i]);
     }
 };
+
+// a GEMM activation operand of rows x K in one buffer: q [rows][K] fp16, then
+// d and s [rows][dp] fp16
+struct Operand {
+    uint16_t *q, *d, *s;
+};
+size_t operand_bytes(size_t rows, size_t K, Operand* o = nullptr, char* base = nullptr) {
+    const size_t dp = (size_t)mmq_scale_pitch((int64_t)K);
+    const size_t qb = align_up(rows * K * 2), sb = align_up(rows * dp * 2);
+    if (o && base) {
+        o->q = reinterpret_cast<uint16_t*>(base);
+        o->d = reinterpret_cast<uint16_t*>(base + qb);
+        o->s = reinterpret_cast<uint16_t*>(base + qb + sb);
+    }
+    return qb + 2 * sb;
+}
 
 Sizes block_sizes(const Info& b, int S) {
     Sizes z;
@@ -97,18 +118,27 @@ Sizes block_sizes(const Info& b, int S) {
     z.h = (size_t)S2 * S2 * 4 * Cout * 4;
     z.f = (size_t)S2 * S2 * Cout * 4;
     z.x = (size_t)S * S * std::max(Cin, Cout) * 4;
+    // a0: LN1 in attention order, LN2 and GELU operands; a1: LN1 in image order
+    z.a0 = std::max({operand_bytes(rows, Cin), operand_bytes((size_t)S2 * S2, Cout),
+                     operand_bytes((size_t)S2 * S2, 4 * Cout)});
+    if (Cin != Cout) {
+        z.a1 = operand_bytes((size_t)S * S, Cin);
+        z.xw = std::max(z.xw, (size_t)S * S * Cin * 4);  // dim_proj's f32 LN1 rows next to a fused qkv operand
+    }
     return z;
 }
 
 struct Bufs {
     float *xw, *xn, *dp, *sc, *qkv, *att, *p, *h, *f, *x0, *x1, *cols, *w32;
     _Float16 *q, *k, *v;
+    char *a0, *a1;
 };
 
 size_t layout(const Sizes& z, char* base, Bufs* b) {
-    const size_t parts[16] = {z.xw, z.xn, z.dp, z.sc, z.qkv, z.att, z.p, z.h, z.f, z.x, z.x, z.cols, z.w32, z.q, z.kv, z.kv};
-    size_t off[16], o = 0;
-    for (int i = 0; i < 16; ++i) {
+    const size_t parts[18] = {z.xw, z.xn, z.dp, z.sc, z.qkv, z.att, z.p,  z.h,  z.f,
+                              z.x,  z.x,  z.cols, z.w32, z.q, z.kv, z.kv, z.a0, z.a1};
+    size_t off[18], o = 0;
+    for (int i = 0; i < 18; ++i) {
         off[i] = o;
         o += align_up(std::max(parts[i], (size_t)256));
     }
@@ -118,6 +148,8 @@ size_t layout(const Sizes& z, char* base, Bufs* b) {
         b->q = reinterpret_cast<_Float16*>(base + off[13]);
         b->k = reinterpret_cast<_Float16*>(base + off[14]);
         b->v = reinterpret_cast<_Float16*>(base + off[15]);
+        b->a0 = base + off[16];
+        b->a1 = base + off[17];
     }
     return o;
 }
@@ -190,6 +222,32 @@ mi355_status get_bufs(mi355_context* ctx, const mi355_hiera_hparams* hp, const s
         if (st_ != MI355_STATUS_SUCCESS) return st_; \
     } while (0)
 
+// the activation mode a producer writes for a GEMM over K inputs with weights W
+int fused_mode(const mi355_context* ctx, const mi355_tensor& W, int64_t K) {
+    return ctx->fuse && K % 32 == 0 ? act_mode_for(W.type) : ACT_F32;
+}
+
+ActOut act_out(char* base, int mode, int64_t rows, int64_t K) {
+    Operand o;
+    operand_bytes((size_t)rows, (size_t)K, &o, base);
+    return ActOut{mode, nullptr, o.q, o.d, o.s, mmq_scale_pitch(K)};
+}
+
+ActF16 act_in(char* base, int mode, int64_t rows, int64_t K) {
+    Operand o;
+    operand_bytes((size_t)rows, (size_t)K, &o, base);
+    ActF16 a;
+    a.q = o.q;
+    a.s1 = K;
+    a.s2 = a.s3 = K * rows;
+    a.d = mode == ACT_F16 ? nullptr : o.d;
+    a.s = mode == ACT_Q8S ? o.s : nullptr;
+    a.dp = mmq_scale_pitch(K);
+    a.M = rows;
+    a.K = K;
+    return a;
+}
+
 mi355_status run_block(mi355_context* ctx, const mi355_hiera_hparams* hp, const Info& bi, const mi355_hiera_block* blk,
                        const float* x, int S, float* x_out, const Bufs& b) {
     const int Cin = bi.dim_in, Cout = bi.dim_out, NH = bi.heads, HD = Cout / NH, ws = bi.ws;
@@ -206,8 +264,10 @@ mi355_status run_block(mi355_context* ctx, const mi355_hiera_hparams* hp, const 
         return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera block: null weight pointer");
 
     // LN1: window order for the attention input; image order when dim_proj or
-    // global attention reads it
-    const float* att_in;
+    // global attention reads it.  Each output is the operand its GEMM takes.
+    const int64_t Mimg = (int64_t)S * S;
+    const int mq = fused_mode(ctx, blk->qkv_w, Cin);
+    const int md = dimch ? fused_mode(ctx, blk->dim_proj_w, Cin) : ACT_F32;
     {
         HieraLnArgs a{};
         a.x = x;
@@ -217,25 +277,44 @@ mi355_status run_block(mi355_context* ctx, const mi355_hiera_hparams* hp, const 
         a.W = a.H = S;
         a.eps = hp->eps;
         if (ws > 0) {
-            a.y = b.xw;
-            a.y_img = dimch ? b.xn : nullptr;
+            a.out = mq == ACT_F32 ? ActOut{ACT_F32, b.xw, nullptr, nullptr, nullptr, 0} : act_out(b.a0, mq, rows, Cin);
+            if (dimch)
+                a.out_img = md == ACT_F32 ? ActOut{ACT_F32, b.xn, nullptr, nullptr, nullptr, 0}
+                                          : act_out(b.a1, md, Mimg, Cin);
             a.rows_out = rows;
             a.ws = ws;
             a.nwh = nwh;
-            att_in = b.xw;
         } else {
-            a.y = b.xn;
-            a.rows_out = (int64_t)S * S;
-            att_in = b.xn;
+            a.out = mq == ACT_F32 ? ActOut{ACT_F32, b.xn, nullptr, nullptr, nullptr, 0} : act_out(b.a0, mq, Mimg, Cin);
+            a.rows_out = Mimg;
         }
-        Timed t(ctx, "hiera_ln");
-        TRY(hip_check(ctx, t.done(launch_hiera_ln(a, st)), "hiera_ln launch"));
+        {
+            Timed t(ctx, "hiera_ln");
+            TRY(hip_check(ctx, t.done(launch_hiera_ln(a, st)), "hiera_ln launch"));
+        }
+        if (ws == 0 && dimch && md != mq) {  // a second image-order LN for dim_proj's operand
+            a.out = md == ACT_F32 ? ActOut{ACT_F32, b.xw, nullptr, nullptr, nullptr, 0} : act_out(b.a1, md, Mimg, Cin);
+            Timed t(ctx, "hiera_ln");
+            TRY(hip_check(ctx, t.done(launch_hiera_ln(a, st)), "hiera_ln launch"));
+        }
     }
     // shortcut
     const float* sc = x;
     if (dimch) {
-        const mi355_tensor in = tensor_on(b.xn, T_F32, Cin, (int64_t)S * S), out = tensor_on(b.dp, T_F32, Cout, (int64_t)S * S);
-        TRY(mi355_mul_mat(ctx, &blk->dim_proj_w, &in, &out));
+        const mi355_tensor out = tensor_on(b.dp, T_F32, Cout, Mimg);
+        if (ws == 0 && md == mq) {  // one image-order LN output serves both GEMMs
+            if (md == ACT_F32) {
+                const mi355_tensor in = tensor_on(b.xn, T_F32, Cin, Mimg);
+                TRY(mi355_mul_mat(ctx, &blk->dim_proj_w, &in, &out));
+            } else {
+                TRY(mul_mat_act(ctx, &blk->dim_proj_w, act_in(b.a0, md, Mimg, Cin), &out));
+            }
+        } else if (md == ACT_F32) {
+            const mi355_tensor in = tensor_on(ws > 0 ? b.xn : b.xw, T_F32, Cin, Mimg);
+            TRY(mi355_mul_mat(ctx, &blk->dim_proj_w, &in, &out));
+        } else {
+            TRY(mul_mat_act(ctx, &blk->dim_proj_w, act_in(b.a1, md, Mimg, Cin), &out));
+        }
         Timed t(ctx, "hiera_bias_maxpool");
         TRY(hip_check(ctx, t.done(launch_hiera_bias_maxpool(b.dp, blk->dim_proj_b, b.sc, Cout, S, S, bi.qs, st)),
                       "bias_maxpool launch"));
@@ -247,8 +326,13 @@ mi355_status run_block(mi355_context* ctx, const mi355_hiera_hparams* hp, const 
     }
     // attention
     {
-        const mi355_tensor in = tensor_on(att_in, T_F32, Cin, rows), out = tensor_on(b.qkv, T_F32, 3 * Cout, rows);
-        TRY(mi355_mul_mat(ctx, &blk->qkv_w, &in, &out));
+        const mi355_tensor out = tensor_on(b.qkv, T_F32, 3 * Cout, rows);
+        if (mq == ACT_F32) {
+            const mi355_tensor in = tensor_on(ws > 0 ? b.xw : b.xn, T_F32, Cin, rows);
+            TRY(mi355_mul_mat(ctx, &blk->qkv_w, &in, &out));
+        } else {
+            TRY(mul_mat_act(ctx, &blk->qkv_w, act_in(b.a0, mq, rows, Cin), &out));
+        }
     }
     {
         HieraQkvArgs a{};
@@ -284,30 +368,49 @@ mi355_status run_block(mi355_context* ctx, const mi355_hiera_hparams* hp, const 
                       "proj_residual launch"));
     }
     // MLP
+    const int64_t M2 = (int64_t)S2 * S2;
+    const int MLP = 4 * Cout;
+    const int m1 = fused_mode(ctx, blk->fc1_w, Cout);
     {
         HieraLnArgs a{};
         a.x = x_out;
         a.w = blk->norm2_w;
         a.b = blk->norm2_b;
-        a.y = b.xn;
-        a.rows_out = (int64_t)S2 * S2;
+        a.out = m1 == ACT_F32 ? ActOut{ACT_F32, b.xn, nullptr, nullptr, nullptr, 0} : act_out(b.a0, m1, M2, Cout);
+        a.rows_out = M2;
         a.C = Cout;
         a.W = a.H = S2;
         a.eps = hp->eps;
         Timed t(ctx, "hiera_ln");
         TRY(hip_check(ctx, t.done(launch_hiera_ln(a, st)), "hiera_ln launch"));
     }
-    const int64_t M2 = (int64_t)S2 * S2;
-    const int MLP = 4 * Cout;
     {
-        const mi355_tensor in = tensor_on(b.xn, T_F32, Cout, M2), out = tensor_on(b.h, T_F32, MLP, M2);
-        TRY(mi355_mul_mat(ctx, &blk->fc1_w, &in, &out));
-        Timed t(ctx, "bias_gelu_tanh");
-        TRY(hip_check(ctx, t.done(launch_bias_gelu_tanh(b.h, blk->fc1_b, M2, MLP, st)), "bias_gelu_tanh launch"));
+        const mi355_tensor out = tensor_on(b.h, T_F32, MLP, M2);
+        if (m1 == ACT_F32) {
+            const mi355_tensor in = tensor_on(b.xn, T_F32, Cout, M2);
+            TRY(mi355_mul_mat(ctx, &blk->fc1_w, &in, &out));
+        } else {
+            TRY(mul_mat_act(ctx, &blk->fc1_w, act_in(b.a0, m1, M2, Cout), &out));
+        }
     }
     {
-        const mi355_tensor in = tensor_on(b.h, T_F32, MLP, M2), out = tensor_on(b.f, T_F32, Cout, M2);
-        TRY(mi355_mul_mat(ctx, &blk->fc2_w, &in, &out));
+        const int m2 = fused_mode(ctx, blk->fc2_w, MLP);
+        const mi355_tensor out = tensor_on(b.f, T_F32, Cout, M2);
+        if (m2 == ACT_F32) {
+            {
+                Timed t(ctx, "bias_gelu_tanh");
+                TRY(hip_check(ctx, t.done(launch_bias_gelu_tanh(b.h, blk->fc1_b, M2, MLP, st)), "bias_gelu_tanh launch"));
+            }
+            const mi355_tensor in = tensor_on(b.h, T_F32, MLP, M2);
+            TRY(mi355_mul_mat(ctx, &blk->fc2_w, &in, &out));
+        } else {
+            {
+                Timed t(ctx, "bias_gelu_tanh");
+                TRY(hip_check(ctx, t.done(launch_bias_gelu_tanh_act(b.h, blk->fc1_b, M2, MLP, act_out(b.a0, m2, M2, MLP), st)),
+                              "bias_gelu_tanh launch"));
+            }
+            TRY(mul_mat_act(ctx, &blk->fc2_w, act_in(b.a0, m2, M2, MLP), &out));
+        }
         Timed t(ctx, "bias_residual");
         TRY(hip_check(ctx, t.done(launch_bias_residual(x_out, b.f, blk->fc2_b, M2, Cout, st)), "bias_residual launch"));
     }

@@ -27,18 +27,48 @@ __device__ __forceinline__ double wave_sum_dh(double v) {
     return v;
 }
 
-// ggml_norm(eps) -> mul(w) -> add(b) over rows of C (C <= 2048), one wavefront per
-// output row.  ws > 0: output rows in window order (padding rows zero) and,
-// when y_img is set, the same rows also in image order.
+// ggml_norm(eps) -> mul(w) -> add(b) over rows of C, G lanes per row (C =
+// 4*G*V), float4 loads.  ws > 0: output rows in window order (padding rows
+// zero) and, when out_img is set, the same rows also in image order.
+template <int V>
+__global__ __launch_bounds__(256) void hiera_ln_group_kernel(const HieraLnArgs a, int G) {
+    const int64_t r = (int64_t)blockIdx.x * (256 / G) + threadIdx.x / G;
+    if (r >= a.rows_out) return;
+    const int l = threadIdx.x & (G - 1), C = a.C;
+    const int64_t src = a.ws > 0 ? hwin_src(r, a.W, a.H, a.ws, a.nwh) : r;
+    v4f x[V];
+    if (src < 0) {  // padding token: a zero row
+#pragma unroll
+        for (int v = 0; v < V; ++v) act_store_chunk(a.out, r, C, v * G + l, v4f{0.0f, 0.0f, 0.0f, 0.0f});
+        return;
+    }
+    const float* xr = a.x + src * C;
+#pragma unroll
+    for (int v = 0; v < V; ++v) x[v] = *reinterpret_cast<const v4f*>(xr + 4 * (v * G + l));
+    ln_group<V>(x, l, G, C, a.w, a.b, a.eps);
+    const bool img = a.ws > 0 && (a.out_img.y || a.out_img.q);
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        act_store_chunk(a.out, r, C, v * G + l, x[v]);
+        if (img) act_store_chunk(a.out_img, src, C, v * G + l, x[v]);
+    }
+}
+
+// One wavefront per output row, for rows the grouped form does not fit
+// (C <= 2048).
 __global__ __launch_bounds__(256) void hiera_ln_kernel(const HieraLnArgs a) {
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= a.rows_out) return;
     const int lane = threadIdx.x & 63, C = a.C;
     const int per = (C + 63) / 64;
     const int64_t src = a.ws > 0 ? hwin_src(r, a.W, a.H, a.ws, a.nwh) : r;
-    float* yr = a.y + r * C;
-    if (src < 0) {
-        for (int e = lane; e < C; e += 64) yr[e] = 0.0f;
+    const bool img = a.ws > 0 && src >= 0 && (a.out_img.y || a.out_img.q);
+    if (src < 0) {  // padding token: a zero row
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const int e = j * 64 + lane;
+            if (j < per) act_store_lane32(a.out, r, C, e, 0.0f, e < C);
+        }
         return;
     }
     const float* xr = a.x + src * C;
@@ -67,16 +97,19 @@ __global__ __launch_bounds__(256) void hiera_ln_kernel(const HieraLnArgs a) {
     s2 = wave_sum_dh(s2);
     const float var = (float)(s2 / (double)C);
     const float scale = 1.0f / sqrtf(var + a.eps);
-    float* yi = a.y_img ? a.y_img + src * C : nullptr;
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
-        const int e = j * 64 + lane;
-        if (j < per && e < C) {
-            float t = v[j] * scale;
-            t = t * a.w[e];
-            t = t + a.b[e];
-            yr[e] = t;
-            if (yi) yi[e] = t;
+        if (j < per) {
+            const int e = j * 64 + lane;
+            const bool valid = e < C;
+            float t = 0.0f;
+            if (valid) {
+                t = v[j] * scale;
+                t = t * a.w[e];
+                t = t + a.b[e];
+            }
+            act_store_lane32(a.out, r, C, e, t, valid);
+            if (img) act_store_lane32(a.out_img, src, C, e, t, valid);
         }
     }
 }
@@ -185,6 +218,19 @@ __global__ __launch_bounds__(256) void hiera_proj_residual_kernel(float* x, cons
     x[tix] = shortcut[tix] + u;
 }
 
+// ggml_gelu with ggml-cpu's fp16-table semantics (GGML_GELU_FP16): 0 for x <= -10, x for
+// x >= 10, else f16(gelu_f32(f16(x))), gelu_f32 evaluated left to right in fp32
+__device__ __forceinline__ float gelu_tanh_table(float u) {
+    if (u <= -10.0f) return 0.0f;
+    if (u >= 10.0f) return u;
+    const float v = h2f(f2h(u));
+    const float inner0 = 0.79788456080286535587989211986876f * v;
+    const float av = 0.044715f * v;
+    const float avv = av * v;
+    const float inner = inner0 * (1.0f + avv);
+    const float hv = 0.5f * v;
+    return h2f(f2h(hv * (1.0f + tanhf(inner))));
+}
 // h = ggml_gelu(h + b) with ggml-cpu's fp16-table semantics (GGML_GELU_FP16):
 // 0 for x <= -10, x for x >= 10, else f16(gelu_f32(f16(x))).
 __global__ __launch_bounds__(256) void bias_gelu_tanh_kernel(float* __restrict__ h, const float* __restrict__ b,
@@ -192,22 +238,25 @@ __global__ __launch_bounds__(256) void bias_gelu_tanh_kernel(float* __restrict__
     const int64_t tix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (tix >= rows * n) return;
     const int c = (int)(tix % n);
-    const float u = h[tix] + b[c];
-    float y;
-    if (u <= -10.0f) {
-        y = 0.0f;
-    } else if (u >= 10.0f) {
-        y = u;
-    } else {
-        const float v = h2f(f2h(u));
-        const float inner0 = 0.79788456080286535587989211986876f * v;
-        const float av = 0.044715f * v;
-        const float avv = av * v;
-        const float inner = inner0 * (1.0f + avv);
-        const float hv = 0.5f * v;
-        y = h2f(f2h(hv * (1.0f + tanhf(inner))));
-    }
+    const float y = gelu_tanh_table(h[tix] + b[c]);
     h[tix] = y;
+}
+
+// h + b -> ggml_gelu -> the next MUL_MAT's operand; one thread per 4 values
+// (n % 32 == 0, so the 8 threads of a block are lanes of one wavefront)
+__global__ __launch_bounds__(256) void bias_gelu_tanh_act_kernel(const float* __restrict__ h, const float* __restrict__ b,
+                                                                 int64_t rows, int n, const ActOut o) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int n4 = n / 4;
+    if (t >= rows * n4) return;
+    const int64_t r = t / n4;
+    const int c = (int)(t - r * n4);
+    const v4f hv = *reinterpret_cast<const v4f*>(h + r * n + 4 * c);
+    const v4f bv = *reinterpret_cast<const v4f*>(b + 4 * c);
+    v4f x;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) x[k] = gelu_tanh_table(hv[k] + bv[k]);
+    act_store_chunk(o, r, n, c, x);
 }
 
 // conv2d columns with stride / zero padding: cols[m][k], m = oy*OW + ox,
@@ -247,7 +296,22 @@ static unsigned nblk(int64_t n) { return (unsigned)((n + 255) / 256); }
 hipError_t launch_hiera_ln(const HieraLnArgs& a, hipStream_t st) {
     if (a.rows_out <= 0) return hipSuccess;
     if (a.C <= 0 || a.C > 2048) return hipErrorInvalidValue;
-    hiera_ln_kernel<<<(unsigned)((a.rows_out + 3) / 4), 256, 0, st>>>(a);
+    const bool q8 = a.out.mode >= ACT_Q8 || (a.ws > 0 && a.out_img.mode >= ACT_Q8 && (a.out_img.y || a.out_img.q));
+    if (q8 && a.C % 32 != 0) return hipErrorInvalidValue;
+    int G, V;
+    ln_shape(a.C, &G, &V);
+    const unsigned nb = (unsigned)((a.rows_out + 256 / G - 1) / (256 / G));
+    switch (V) {
+        case 1: hiera_ln_group_kernel<1><<<nb, 256, 0, st>>>(a, G); break;
+        case 2: hiera_ln_group_kernel<2><<<nb, 256, 0, st>>>(a, G); break;
+        case 3: hiera_ln_group_kernel<3><<<nb, 256, 0, st>>>(a, G); break;
+        case 4: hiera_ln_group_kernel<4><<<nb, 256, 0, st>>>(a, G); break;
+        case 5: hiera_ln_group_kernel<5><<<nb, 256, 0, st>>>(a, G); break;
+        case 6: hiera_ln_group_kernel<6><<<nb, 256, 0, st>>>(a, G); break;
+        case 7: hiera_ln_group_kernel<7><<<nb, 256, 0, st>>>(a, G); break;
+        case 8: hiera_ln_group_kernel<8><<<nb, 256, 0, st>>>(a, G); break;
+        default: hiera_ln_kernel<<<(unsigned)((a.rows_out + 3) / 4), 256, 0, st>>>(a); break;
+    }
     return hipGetLastError();
 }
 hipError_t launch_hiera_qkv(const HieraQkvArgs& a, hipStream_t st) {
@@ -271,6 +335,12 @@ hipError_t launch_hiera_proj_residual(float* x, const float* shortcut, const flo
 }
 hipError_t launch_bias_gelu_tanh(float* h, const float* b, int64_t rows, int n, hipStream_t st) {
     if (rows * n > 0) bias_gelu_tanh_kernel<<<nblk(rows * n), 256, 0, st>>>(h, b, rows, n);
+    return hipGetLastError();
+}
+hipError_t launch_bias_gelu_tanh_act(const float* h, const float* b, int64_t rows, int n, const ActOut& o,
+                                     hipStream_t st) {
+    if (n % 32) return hipErrorInvalidValue;
+    if (rows * (n / 4) > 0) bias_gelu_tanh_act_kernel<<<nblk(rows * (n / 4)), 256, 0, st>>>(h, b, rows, n, o);
     return hipGetLastError();
 }
 hipError_t launch_im2col_pad(const float* img, float* cols, int C, int Hin, int Win, int KH, int KW, int stride, int pad,

@@ -37,6 +37,19 @@ struct ActF16 {
 };
 inline int64_t mmq_scale_pitch(int64_t K) { return ((K / 32) + 1) & ~(int64_t)1; }
 
+// Output of a pass that feeds a MUL_MAT: F32 rows (y), F16 rows (q as fp16
+// values: the operand of F16 weights), or the quantized operand (q fp16
+// quants [rows][K], d [rows][dp], and Q8_1 sums s for Q4_1 weights).
+enum { ACT_F32 = 0, ACT_F16 = 1, ACT_Q8 = 2, ACT_Q8S = 3 };
+struct ActOut {
+    int mode;
+    float* y;
+    uint16_t* q;
+    uint16_t* d;
+    uint16_t* s;
+    int64_t dp;
+};
+
 // ggml from_float into contiguous ggml rows: type 8 (Q8_0), 9 (Q8_1), 1 (F16).
 hipError_t launch_quantize_ggml(const SrcView& src, int type, bool ref_variant, void* dst, hipStream_t st);
 // from_float (x86 variant, Q8_0 or with_sum Q8_1 semantics) into the ActF16
@@ -104,7 +117,7 @@ struct LnArgs {
     int add_grid;       // > 0: add row = (y % add_grid) * add_grid + x % add_grid
     const float* w;     // optional affine (ggml_mul), [E]
     const float* b;     // optional affine (ggml_add), [E]
-    float* y;           // [rows][E]; row win_row(r) when ws > 0, else r
+    ActOut out;         // [rows][E]; row win_row(r) when ws > 0, else r
     int64_t rows;
     int E;
     int grid;           // tokens per image side (rows = grid^2 when ws > 0 or add_grid > 0)
@@ -127,6 +140,7 @@ hipError_t launch_qkv_rope(const QkvArgs& a, hipStream_t st);
 hipError_t launch_proj_residual(float* x, const float* p, const float* b, int64_t rows, int E, int grid, int ws,
                                 hipStream_t st);
 hipError_t launch_bias_gelu(float* h, const float* b, int64_t rows, int n, hipStream_t st);
+hipError_t launch_bias_gelu_act(const float* h, const float* b, int64_t rows, int n, const ActOut& o, hipStream_t st);
 hipError_t launch_bias_residual(float* x, const float* f, const float* b, int64_t rows, int n, hipStream_t st);
 hipError_t launch_im2col(const float* img, float* cols, int C, int Himg, int Wimg, int P, int grid, hipStream_t st);
 
@@ -135,8 +149,8 @@ struct HieraLnArgs {
     const float* x;    // [H*W][C] image order
     const float* w;    // [C]
     const float* b;    // [C]
-    float* y;          // [rows_out][C]: window order (ws > 0, padding rows zero) or image order
-    float* y_img;      // optional image-order copy (ws > 0 only)
+    ActOut out;        // [rows_out][C]: window order (ws > 0, padding rows zero) or image order
+    ActOut out_img;    // optional image-order copy (ws > 0 only; out_img.y and .q null when unused)
     int64_t rows_out;  // nW * ws * ws, or H * W
     int C, W, H, ws, nwh;
     float eps;
@@ -158,6 +172,8 @@ hipError_t launch_hiera_bias_maxpool(const float* p, const float* b, float* out,
 hipError_t launch_hiera_proj_residual(float* x, const float* shortcut, const float* p, const float* b, int C, int W,
                                       int H, int ws, int nwh, hipStream_t st);
 hipError_t launch_bias_gelu_tanh(float* h, const float* b, int64_t rows, int n, hipStream_t st);
+hipError_t launch_bias_gelu_tanh_act(const float* h, const float* b, int64_t rows, int n, const ActOut& o,
+                                     hipStream_t st);
 hipError_t launch_im2col_pad(const float* img, float* cols, int C, int Hin, int Win, int KH, int KW, int stride, int pad,
                              int OH, int OW, bool round16, hipStream_t st);
 hipError_t launch_bias_add_pe(float* x, const float* b, const float* pe, int64_t rows, int C, hipStream_t st);

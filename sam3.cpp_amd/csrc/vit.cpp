@@ -14,8 +14,13 @@
 //   h    = gelu_erf(mul_mat(fc1_w, xn) + fc1_b)
 //   x    = x + (mul_mat(fc2_w, h) + fc2_b)
 //
-// The activation buffers live in one device allocation owned by the context
-// (mi355_vit_workspace_size); mul_mat keeps using the context's own scratch.
+// For quantized and F16 weights the passes that feed a MUL_MAT (LN1 -> qkv,
+// LN2 -> fc1, bias+GELU -> fc2) write the GEMM's activation operand directly
+// (Q8 quants + scales, or F16 rows), computed from the same fp32 values ggml
+// would quantize, so the separate activation quantize pass and the f32 round
+// trip disappear.  The activation buffers live in one device allocation owned
+// by the context (mi355_vit_workspace_size); mul_mat keeps using the
+// context's own scratch.
 #include <cmath>
 
 #include "context.h"
@@ -32,15 +37,21 @@ struct EncBufs {
     _Float16* v;
     float* attn;    // [M][E]  attention output, fc2 output
     float* big;     // [M][MLP] fc1 output (or im2col columns)
+    uint16_t* aq;   // [M][max(E, MLP)] activation operand: Q8 quants or F16 rows
+    uint16_t* ad;   // [M][dp] block scales
+    uint16_t* as;   // [M][dp] Q8_1 sums
 };
 
 size_t enc_bytes(const mi355_vit_hparams* hp, EncBufs* b, char* base) {
     const size_t M = (size_t)hp->grid * hp->grid, E = (size_t)hp->embed_dim;
     const size_t kpatch = 3 * (size_t)hp->patch_size * hp->patch_size;
     const size_t big = M * std::max((size_t)hp->mlp_dim, kpatch) * 4;
-    const size_t sz[7] = {M * E * 4, M * 3 * E * 4, M * E * 2, M * E * 2, M * E * 2, M * E * 4, big};
-    size_t off[7], o = 0;
-    for (int i = 0; i < 7; ++i) {
+    const size_t kmax = std::max(E, (size_t)hp->mlp_dim);
+    const size_t dpm = (size_t)mmq_scale_pitch((int64_t)kmax);
+    const size_t sz[10] = {M * E * 4, M * 3 * E * 4, M * E * 2, M * E * 2, M * E * 2, M * E * 4, big,
+                           M * kmax * 2, M * dpm * 2, M * dpm * 2};
+    size_t off[10], o = 0;
+    for (int i = 0; i < 10; ++i) {
         off[i] = o;
         o += align_up(sz[i]);
     }
@@ -52,6 +63,9 @@ size_t enc_bytes(const mi355_vit_hparams* hp, EncBufs* b, char* base) {
         b->v = reinterpret_cast<_Float16*>(base + off[4]);
         b->attn = reinterpret_cast<float*>(base + off[5]);
         b->big = reinterpret_cast<float*>(base + off[6]);
+        b->aq = reinterpret_cast<uint16_t*>(base + off[7]);
+        b->ad = reinterpret_cast<uint16_t*>(base + off[8]);
+        b->as = reinterpret_cast<uint16_t*>(base + off[9]);
     }
     return o;
 }
@@ -86,6 +100,23 @@ mi355_tensor dev_tensor(const void* p, int type, int64_t ne0, int64_t ne1, int64
     t.nb[3] = t.nb[2] * ne2;
     t.data = const_cast<void*>(p);
     return t;
+}
+
+// the activation operand in b.aq/ad/as for a GEMM with K inputs over M rows
+ActOut act_out(const EncBufs& b, int mode, int64_t K) {
+    return ActOut{mode, nullptr, b.aq, b.ad, b.as, mmq_scale_pitch(K)};
+}
+ActF16 act_in(const EncBufs& b, int mode, int64_t M, int64_t K) {
+    ActF16 a;
+    a.q = b.aq;
+    a.s1 = K;
+    a.s2 = a.s3 = K * M;
+    a.d = mode == ACT_F16 ? nullptr : b.ad;
+    a.s = mode == ACT_Q8S ? b.as : nullptr;
+    a.dp = mmq_scale_pitch(K);
+    a.M = M;
+    a.K = K;
+    return a;
 }
 
 mi355_status get_bufs(mi355_context* ctx, const mi355_vit_hparams* hp, EncBufs* b) {
@@ -123,7 +154,7 @@ mi355_status mi355_vit_layer_norm(mi355_context* ctx, const float* x, const floa
     a.add_grid = add ? add_grid : 0;
     a.w = w;
     a.b = b;
-    a.y = y;
+    a.out = ActOut{ACT_F32, y, nullptr, nullptr, nullptr, 0};
     a.rows = rows;
     a.E = E;
     a.grid = grid;
@@ -257,12 +288,38 @@ mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams
         st = (e);                                \
         if (st != MI355_STATUS_SUCCESS) return st; \
     } while (0)
+    // LN -> the GEMM's activation operand (fused) or F32 rows
+    auto ln_gemm = [&](const float* w, const float* bb, int ws, const mi355_tensor& W, float* out,
+                       int64_t N) -> mi355_status {
+        const int mode = ctx->fuse ? act_mode_for(W.type) : ACT_F32;
+        if (mode == ACT_F32) {
+            mi355_status s1 = mi355_vit_layer_norm(ctx, x, nullptr, 0, w, bb, b.xn, M, E, G, ws, hp->eps);
+            if (s1 != MI355_STATUS_SUCCESS) return s1;
+            const mi355_tensor in = dev_tensor(b.xn, T_F32, E, M), o = dev_tensor(out, T_F32, N, M);
+            return mi355_mul_mat(ctx, &W, &in, &o);
+        }
+        LnArgs a;
+        a.x = x;
+        a.add = nullptr;
+        a.add_grid = 0;
+        a.w = w;
+        a.b = bb;
+        a.out = act_out(b, mode, E);
+        a.rows = M;
+        a.E = E;
+        a.grid = G;
+        a.ws = ws;
+        a.eps = hp->eps;
+        {
+            Timed t(ctx, "layer_norm");
+            mi355_status s1 = hip_check(ctx, t.done(launch_layer_norm(a, ctx->stream)), "layer_norm launch");
+            if (s1 != MI355_STATUS_SUCCESS) return s1;
+        }
+        const mi355_tensor o = dev_tensor(out, T_F32, N, M);
+        return mul_mat_act(ctx, &W, act_in(b, mode, M, E), &o);
+    };
     // attention
-    TRY(mi355_vit_layer_norm(ctx, x, nullptr, 0, blk->norm1_w, blk->norm1_b, b.xn, M, E, G, WS, hp->eps));
-    {
-        const mi355_tensor in = dev_tensor(b.xn, T_F32, E, M), out = dev_tensor(b.qkv, T_F32, 3 * E, M);
-        TRY(mi355_mul_mat(ctx, &blk->qkv_w, &in, &out));
-    }
+    TRY(ln_gemm(blk->norm1_w, blk->norm1_b, WS, blk->qkv_w, b.qkv, 3 * E));
     TRY(mi355_vit_qkv_rope(ctx, b.qkv, blk->qkv_b, blk->freqs_cis, b.q, b.k, b.v, M, N, NH, HD));
     {
         const mi355_tensor q = dev_tensor(b.q, T_F16, HD, N, NH, B), k = dev_tensor(b.k, T_F16, HD, N, NH, B),
@@ -275,15 +332,22 @@ mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams
     }
     TRY(mi355_vit_proj_residual(ctx, x, b.xn, blk->proj_b, M, E, G, WS));
     // MLP
-    TRY(mi355_vit_layer_norm(ctx, x, nullptr, 0, blk->norm2_w, blk->norm2_b, b.xn, M, E, G, 0, hp->eps));
+    TRY(ln_gemm(blk->norm2_w, blk->norm2_b, 0, blk->fc1_w, b.big, MLP));
     {
-        const mi355_tensor in = dev_tensor(b.xn, T_F32, E, M), out = dev_tensor(b.big, T_F32, MLP, M);
-        TRY(mi355_mul_mat(ctx, &blk->fc1_w, &in, &out));
-    }
-    TRY(mi355_vit_bias_gelu(ctx, b.big, blk->fc1_b, M, MLP));
-    {
-        const mi355_tensor in = dev_tensor(b.big, T_F32, MLP, M), out = dev_tensor(b.attn, T_F32, E, M);
-        TRY(mi355_mul_mat(ctx, &blk->fc2_w, &in, &out));
+        const int mode = ctx->fuse ? act_mode_for(blk->fc2_w.type) : ACT_F32;
+        const mi355_tensor out = dev_tensor(b.attn, T_F32, E, M);
+        if (mode == ACT_F32 || MLP % 32 != 0) {
+            TRY(mi355_vit_bias_gelu(ctx, b.big, blk->fc1_b, M, MLP));
+            const mi355_tensor in = dev_tensor(b.big, T_F32, MLP, M);
+            TRY(mi355_mul_mat(ctx, &blk->fc2_w, &in, &out));
+        } else {
+            {
+                Timed t(ctx, "bias_gelu");
+                TRY(hip_check(ctx, t.done(launch_bias_gelu_act(b.big, blk->fc1_b, M, MLP, act_out(b, mode, MLP), ctx->stream)),
+                              "bias_gelu launch"));
+            }
+            TRY(mul_mat_act(ctx, &blk->fc2_w, act_in(b, mode, M, MLP), &out));
+        }
     }
     TRY(mi355_vit_bias_residual(ctx, x, b.attn, blk->fc2_b, M, E));
 #undef TRY

@@ -237,3 +237,42 @@ def test_hiera_encode_patch_and_stages(mi, ctx, orc):
     ctx.synchronize()
     for a, b in zip(outs, outs2):
         assert torch.equal(a, b)
+
+
+def _block_dev(mi, t, host, devs, vec):
+    blk = mi.HieraBlock()
+    for name in ("qkv", "proj", "fc1", "fc2", "dim_proj"):
+        if name in host:
+            _, N, K = host[name]
+            setattr(blk, name + "_w", mi.from_torch(devs[name], t, [K, N]))
+    vd = {k: dev(v) for k, v in vec.items()}
+    for k, v in vd.items():
+        setattr(blk, k, v.data_ptr())
+    return blk, vd
+
+
+@pytest.mark.parametrize("tname", ["f16", "q8_0", "q4_0", "q4_1"])
+@pytest.mark.parametrize("idx,S", CASES)
+def test_hiera_block_fusion_bit_exact(mi, ctx, orc, tname, idx, S):
+    """The fused LN / GELU producers write exactly the operand mul_mat would
+    make from their f32 rows: fused and unfused blocks agree bit for bit."""
+    t = orc.NAME_TYPE[tname]
+    hp = mi.hiera_tiny(128)
+    info = mi.hiera_block_info(hp, idx)
+    host, devs, vec = _weights(mi, orc, t, info, seed=idx + 11)
+    blk, _keep = _block_dev(mi, t, host, devs, vec)
+    x0 = orc.normal(S * S * info.dim_in, idx, 61).reshape(S * S, info.dim_in)
+    S2 = S // 2 if info.q_stride else S
+    xd = dev(x0)
+    outs = []
+    try:
+        for fuse in (False, True):
+            ctx.set_fusion(fuse)
+            out = torch.full((S2 * S2, info.dim_out), float("nan"), dtype=torch.float32, device="cuda")
+            ctx.hiera_block_forward(hp, idx, blk, _p(xd), S, _p(out))
+            ctx.synchronize()
+            outs.append(out.cpu().numpy())
+    finally:
+        ctx.set_fusion(True)
+    assert np.isfinite(outs[0]).all()
+    assert np.array_equal(outs[0], outs[1]), f"max diff {np.abs(outs[0] - outs[1]).max():.3e}"

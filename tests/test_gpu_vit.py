@@ -84,9 +84,11 @@ def gelu_ref(orc, x):
 
 
 # ---------------------------------------------------------------- fused passes
-@pytest.mark.parametrize("window,add_grid", [(0, 0), (24, 0), (0, 24)])
-def test_layer_norm(mi, ctx, orc, window, add_grid):
-    grid, E = 48, 256
+# E = 256 and 1024 take the grouped kernel (64 lanes x 1 or 4 float4 per row),
+# E = 1152 (V = 9 float4 per lane) the one-wavefront-per-row kernel
+@pytest.mark.parametrize("window,add_grid,E", [(0, 0, 256), (24, 0, 256), (0, 24, 256), (24, 0, 1024), (0, 0, 1152)])
+def test_layer_norm(mi, ctx, orc, window, add_grid, E):
+    grid = 48
     M = grid * grid
     x = orc.normal(M * E, 1, 1).reshape(M, E) * np.float32(3.0) + np.float32(0.5)
     w = orc.normal(E, 1, 2) * np.float32(0.2) + np.float32(1.0)
@@ -304,3 +306,40 @@ def test_vit_block(mi, ctx, orc, is_global, tname):
             f"rms32 {np.sqrt((d32 ** 2).mean()):.2e}"
     assert d16.max() <= 1e-2 and d32.max() <= 1e-2, stats
     assert np.sqrt((d16 ** 2).mean()) <= 5e-4 and np.sqrt((d32 ** 2).mean()) <= 1e-3, stats
+
+
+@pytest.mark.parametrize("is_global", [0, 1])
+@pytest.mark.parametrize("tname", ["f16", "q8_0", "q4_0", "q4_1"])
+def test_vit_block_fusion_bit_exact(mi, ctx, orc, is_global, tname):
+    """The fused LN / GELU producers write exactly the operand mul_mat would
+    make from their f32 rows: fused and unfused blocks agree bit for bit."""
+    t = orc.NAME_TYPE[tname]
+    E, NH, MLP, grid, ws = 256, 4, 1024, 48, 24
+    HD = E // NH
+    M = grid * grid
+    host, devs, vec = _block_weights(mi, orc, t, E, MLP, seed=17 + is_global)
+    freqs = axial_cis(orc, HD, grid, ws / grid) if is_global else axial_cis(orc, HD, ws, 1.0)
+    x0 = orc.normal(M * E, 9, 1).reshape(M, E)
+    vd = {k: dev(v) for k, v in vec.items()}
+    fd = dev(freqs)
+    blk = mi.VitBlock()
+    for name in ("qkv", "proj", "fc1", "fc2"):
+        _, N, K = host[name]
+        setattr(blk, name + "_w", mi.from_torch(devs[name], t, [K, N]))
+    for k, v in vd.items():
+        setattr(blk, k, v.data_ptr())
+    blk.freqs_cis = fd.data_ptr()
+    blk.is_global = is_global
+    hp = _hp(mi, E, NH, MLP, ws, grid)
+    outs = []
+    try:
+        for fuse in (False, True):
+            ctx.set_fusion(fuse)
+            x = dev(x0)
+            ctx.vit_block_forward(hp, blk, _p(x))
+            ctx.synchronize()
+            outs.append(x.cpu().numpy())
+    finally:
+        ctx.set_fusion(True)
+    assert np.isfinite(outs[0]).all()
+    assert np.array_equal(outs[0], outs[1]), f"max diff {np.abs(outs[0] - outs[1]).max():.3e}"
