@@ -289,6 +289,8 @@ def main():
                          "copy (256 MiB device copy)")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--op-warmup", type=int, default=20)
+    ap.add_argument("--no-fuse", action="store_true",
+                    help="encoder modes: run the unfused pass sequence (f32 activations between the ggml node groups)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the rocprofv3 FETCH_SIZE/WRITE_SIZE child runs (roofline.traffic = null)")
     args = ap.parse_args()
@@ -332,6 +334,8 @@ def main():
         print(json.dumps({"op": args.op, "reps": args.reps, **res[which]}), flush=True)
         ctx.close()
         return
+    if args.no_fuse:
+        ctx.set_fusion(False)
     if args.op and args.op.startswith("hiera/"):
         tn = args.op.split("/")[1]
         hp, pre, blocks, outs, keep = build_hiera(mi, orc, torch, dev, tn)

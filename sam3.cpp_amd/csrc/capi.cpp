@@ -218,7 +218,38 @@ int act_mode_for(int t) {
     }
 }
 
-mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const mi355_tensor* d) {
+mi355_status quantize_act(mi355_context* ctx, const mi355_tensor* x, const ActOut& o) {
+    if (!x || x->type != T_F32) return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_act: F32 rows expected");
+    if (o.mode == ACT_F16) {
+        Timed t(ctx, "convert_f16");
+        return hip_check(ctx, t.done(launch_convert_f16(view_of(x), o.q, ctx->stream)), "convert_f16 launch");
+    }
+    if (o.mode != ACT_Q8 && o.mode != ACT_Q8S) return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_act: bad mode");
+    if (x->ne[0] % 32 != 0 || o.dp != mmq_scale_pitch(x->ne[0]))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_act: row length / scale pitch");
+    Timed t(ctx, "quantize_mmq");
+    return hip_check(ctx, t.done(launch_quantize_mmq(view_of(x), o.mode == ACT_Q8S, o.dp, o.q, o.d, o.s, ctx->stream)),
+                     "quantize_mmq launch");
+}
+
+// MUL_MAT of a prequantized operand with a fused epilogue in place of dst
+// (dst [M][N] F32 is only a shape here: nothing is written to it).
+mi355_status mul_mat_epi(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const MmqEpi& e) {
+    if (!s0) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat_epi: null weights");
+    mi355_tensor d{};
+    d.type = T_F32;
+    d.ne[0] = s0->ne[1];
+    d.ne[1] = a.M;
+    d.ne[2] = d.ne[3] = 1;
+    d.nb[0] = 4;
+    d.nb[1] = 4 * d.ne[0];
+    d.nb[2] = d.nb[3] = d.nb[1] * a.M;
+    d.data = e.out;
+    return mul_mat_act(ctx, s0, a, &d, &e);
+}
+
+mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const mi355_tensor* d,
+                         const MmqEpi* epi) {
     if (!s0 || !a.q) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat_act: null operand");
     const int mode = act_mode_for(s0->type);
     if (mode == ACT_F32) return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat_act: no prequantized path for type %d", s0->type);
@@ -244,8 +275,15 @@ mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF1
         st = ensure_ws(ctx, align);
         if (st != MI355_STATUS_SUCCESS) return st;
     }
-    const char* kname = s0->type == T_F16 ? "mmq_f16" : s0->type == T_Q8_0 ? "mmq_q8_0" : s0->type == T_Q4_0 ? "mmq_q4_0" : "mmq_q4_1";
-    Timed tq(ctx, kname);
+    static const char* names[4][2] = {{"mmq_f16", "mmq_f16+residual"},
+                                      {"mmq_q8_0", "mmq_q8_0+residual"},
+                                      {"mmq_q4_0", "mmq_q4_0+residual"},
+                                      {"mmq_q4_1", "mmq_q4_1+residual"}};
+    const int ti = s0->type == T_F16 ? 0 : s0->type == T_Q8_0 ? 1 : s0->type == T_Q4_0 ? 2 : 3;
+    Timed tq(ctx, names[ti][epi ? 1 : 0]);
+    if (epi)
+        return hip_check(ctx, tq.done(launch_mmq_epi(matw_of(s0), a, N, *epi, align ? ctx->ws : nullptr, ctx->stream)),
+                         "mmq launch");
     return hip_check(ctx, tq.done(launch_mmq(matw_of(s0), a, matd_of(d), N, 1, 1, nullptr, align ? ctx->ws : nullptr,
                                              ctx->stream)),
                      "mmq launch");

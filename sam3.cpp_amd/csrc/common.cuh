@@ -179,6 +179,72 @@ __device__ __forceinline__ void act_store_lane32(const ActOut& o, int64_t row, i
     }
 }
 
+// ---- elementwise functions shared by the fused passes and GEMM epilogues
+// (each step rounds to fp32 as its ggml node does: no FMA contraction)
+
+// ggml_vec_gelu_erf_f32: 0.5*x*(1 + erf(x/sqrt(2)))
+__device__ __forceinline__ float gelu_erf(float u) {
+#pragma clang fp contract(off)
+    const float hx = 0.5f * u;
+    return hx * (1.0f + erff(u * 0.70710678118654752440f));
+}
+
+// ggml_gelu with ggml-cpu's fp16-table semantics (GGML_GELU_FP16): 0 for x <= -10, x for
+// x >= 10, else f16(gelu_f32(f16(x))), gelu_f32 evaluated left to right in fp32
+__device__ __forceinline__ float gelu_tanh_table(float u) {
+#pragma clang fp contract(off)
+    if (u <= -10.0f) return 0.0f;
+    if (u >= 10.0f) return u;
+    const float v = h2f(f2h(u));
+    const float inner0 = 0.79788456080286535587989211986876f * v;
+    const float av = 0.044715f * v;
+    const float avv = av * v;
+    const float inner = inner0 * (1.0f + avv);
+    const float hv = 0.5f * v;
+    return h2f(f2h(hv * (1.0f + tanhf(inner))));
+}
+
+// SAM2 window order (sam2_window_partition over the zero-padded grid: window
+// n = wh + nwh*ww, token lh*ws + lw inside it) row r -> image token h*W + w,
+// or -1 for a padding token
+__device__ __forceinline__ int64_t hwin_src(int64_t r, int W, int H, int ws, int nwh) {
+    const int64_t n = r / (ws * ws);
+    const int loc = (int)(r - n * ws * ws);
+    const int lh = loc / ws, lw = loc % ws;
+    const int wh = (int)(n % nwh), ww = (int)(n / nwh);
+    const int h = wh * ws + lh, w = ww * ws + lw;
+    return (h < H && w < W) ? (int64_t)h * W + w : -1;
+}
+
+// ggml_win_part order over a W x W grid (windows row-major, W % ws == 0) row r
+// -> image token y*W + x
+__device__ __forceinline__ int64_t win_unpart_row(int64_t r, int W, int ws) {
+    const int64_t n = r / (ws * ws);
+    const int loc = (int)(r - n * ws * ws);
+    const int nwx = W / ws;
+    const int y = (int)(n / nwx) * ws + loc / ws, x = (int)(n % nwx) * ws + loc % ws;
+    return (int64_t)y * W + x;
+}
+
+// map_row for rows and grids below 2^31 (32-bit index arithmetic)
+__device__ __forceinline__ int map_row32(const RowMap& rm, int r) {
+    if (rm.kind == ROWMAP_IDENTITY) return r;
+    const int w2 = rm.ws * rm.ws, n = r / w2, loc = r - n * w2, ly = loc / rm.ws, lx = loc - ly * rm.ws;
+    if (rm.kind == ROWMAP_WIN_UNPART) {
+        const int nwx = rm.W / rm.ws, wy = n / nwx, wx = n - wy * nwx;
+        return (wy * rm.ws + ly) * rm.W + wx * rm.ws + lx;
+    }
+    const int ww = n / rm.nwh, wh = n - ww * rm.nwh;  // SAM2: window n = wh + nwh*ww
+    const int h = wh * rm.ws + ly, w = ww * rm.ws + lx;
+    return (h < rm.H && w < rm.W) ? h * rm.W + w : -1;
+}
+
+__device__ __forceinline__ int64_t map_row(const RowMap& rm, int64_t r) {
+    if (rm.kind == ROWMAP_WIN_UNPART) return win_unpart_row(r, rm.W, rm.ws);
+    if (rm.kind == ROWMAP_SAM2_UNPART) return hwin_src(r, rm.W, rm.H, rm.ws, rm.nwh);
+    return r;
+}
+
 // Unaligned 2-byte-granular loads of quantized block payloads (ggml blocks
 // are 34/18/20 bytes, so qs is only 2-byte aligned in general).
 __device__ __forceinline__ uint32_t ld_u32_a2(const uint8_t* p) {

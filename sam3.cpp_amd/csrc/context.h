@@ -49,8 +49,15 @@ int act_mode_for(int weight_type);
 // MUL_MAT of weights s0 with an activation operand already in the layout
 // act_mode_for(s0->type) describes (a: quants or F16 rows, scales), as a
 // fused producer pass writes it; dst F32 [N][M] rows.  Same validation and
-// kernels as mi355_mul_mat minus the activation quantize.
-mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const mi355_tensor* dst);
+// kernels as mi355_mul_mat minus the activation quantize.  With epi the
+// epilogue replaces the dst store (dst only gives the shape).
+mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const mi355_tensor* dst,
+                         const MmqEpi* epi = nullptr);
+// F32 rows x [ne1][ne0] -> the MUL_MAT operand layout o (Q8 / Q8_1 quants +
+// scales, or F16 rows), the activation quantize of mi355_mul_mat.
+mi355_status quantize_act(mi355_context* ctx, const mi355_tensor* x, const ActOut& o);
+// mul_mat_act with the fused residual epilogue; dst [M][N] never exists.
+mi355_status mul_mat_epi(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const MmqEpi& e);
 
 // Brackets one launch with events when timing is enabled.
 struct Timed {

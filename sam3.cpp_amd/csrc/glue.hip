@@ -177,9 +177,7 @@ __global__ __launch_bounds__(256) void bias_gelu_kernel(float* __restrict__ h, c
     const v4f bv = *reinterpret_cast<const v4f*>(b + c);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const float u = hv[j] + bv[j];
-        const float hx = 0.5f * u;
-        hv[j] = hx * (1.0f + erff(u * 0.70710678118654752440f));
+        hv[j] = gelu_erf(hv[j] + bv[j]);
     }
     *reinterpret_cast<v4f*>(h + r * n + c) = hv;
 }
@@ -198,9 +196,7 @@ __global__ __launch_bounds__(256) void bias_gelu_act_kernel(const float* __restr
     v4f x;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const float u = hv[k] + bv[k];
-        const float hx = 0.5f * u;
-        x[k] = hx * (1.0f + erff(u * 0.70710678118654752440f));
+        x[k] = gelu_erf(hv[k] + bv[k]);
     }
     act_store_chunk(o, r, n, c, x);
 }

@@ -71,8 +71,8 @@ int cdiv(int a, int b) { return (a + b - 1) / b; }
 // activation buffers of one block (or their maxima over the backbone)
 struct Sizes {
     size_t xw = 0, xn = 0, dp = 0, sc = 0, qkv = 0, q = 0, kv = 0, att = 0, p = 0, h = 0, f = 0, x = 0, cols = 0, w32 = 0,
-           a0 = 0, a1 = 0;
-    static constexpr int kFields = 16;
+           a0 = 0, a1 = 0, a2 = 0;
+    static constexpr int kFields = 17;
     void max_with(const Sizes& o) {
         size_t* a = &xw;
         const size_t* b = &o.xw;
@@ -118,9 +118,11 @@ Sizes block_sizes(const Info& b, int S) {
     z.h = (size_t)S2 * S2 * 4 * Cout * 4;
     z.f = (size_t)S2 * S2 * Cout * 4;
     z.x = (size_t)S * S * std::max(Cin, Cout) * 4;
-    // a0: LN1 in attention order, LN2 and GELU operands; a1: LN1 in image order
-    z.a0 = std::max({operand_bytes(rows, Cin), operand_bytes((size_t)S2 * S2, Cout),
+    // a0: LN1 in attention order, attention output and LN2 operands;
+    // a1: LN1 in image order; a2: the GELU output (fc2's operand)
+    z.a0 = std::max({operand_bytes(rows, Cin), operand_bytes(nq, Cout), operand_bytes((size_t)S2 * S2, Cout),
                      operand_bytes((size_t)S2 * S2, 4 * Cout)});
+    z.a2 = operand_bytes((size_t)S2 * S2, 4 * Cout);
     if (Cin != Cout) {
         z.a1 = operand_bytes((size_t)S * S, Cin);
         z.xw = std::max(z.xw, (size_t)S * S * Cin * 4);  // dim_proj's f32 LN1 rows next to a fused qkv operand
@@ -131,14 +133,14 @@ Sizes block_sizes(const Info& b, int S) {
 struct Bufs {
     float *xw, *xn, *dp, *sc, *qkv, *att, *p, *h, *f, *x0, *x1, *cols, *w32;
     _Float16 *q, *k, *v;
-    char *a0, *a1;
+    char *a0, *a1, *a2;
 };
 
 size_t layout(const Sizes& z, char* base, Bufs* b) {
-    const size_t parts[18] = {z.xw, z.xn, z.dp, z.sc, z.qkv, z.att, z.p,  z.h,  z.f,
-                              z.x,  z.x,  z.cols, z.w32, z.q, z.kv, z.kv, z.a0, z.a1};
-    size_t off[18], o = 0;
-    for (int i = 0; i < 18; ++i) {
+    const size_t parts[19] = {z.xw, z.xn, z.dp, z.sc, z.qkv, z.att, z.p,  z.h,  z.f,  z.x,
+                              z.x,  z.cols, z.w32, z.q, z.kv, z.kv, z.a0, z.a1, z.a2};
+    size_t off[19], o = 0;
+    for (int i = 0; i < 19; ++i) {
         off[i] = o;
         o += align_up(std::max(parts[i], (size_t)256));
     }
@@ -150,6 +152,7 @@ size_t layout(const Sizes& z, char* base, Bufs* b) {
         b->v = reinterpret_cast<_Float16*>(base + off[15]);
         b->a0 = base + off[16];
         b->a1 = base + off[17];
+        b->a2 = base + off[18];
     }
     return o;
 }
@@ -356,16 +359,30 @@ mi355_status run_block(mi355_context* ctx, const mi355_hiera_hparams* hp, const 
                            v = tensor_on(b.v, T_F16, HD, Nkv, NH, nW), o = tensor_on(b.att, T_F32, HD, NH, Nq, nW);
         TRY(mi355_flash_attn_ext(ctx, &q, &k, &v, nullptr, 1.0f / sqrtf((float)HD), 0.0f, 0.0f, &o));
     }
+    // proj (+ bias, window unpartition with crop, shortcut): fused into the
+    // GEMM's epilogue for quantized / F16 weights
     {
-        const mi355_tensor in = tensor_on(b.att, T_F32, Cout, (int64_t)Nq * nW), out = tensor_on(b.p, T_F32, Cout, (int64_t)Nq * nW);
-        TRY(mi355_mul_mat(ctx, &blk->proj_w, &in, &out));
-    }
-    {
+        const int64_t Mo = (int64_t)Nq * nW;
         const int wso = ws > 0 ? (bi.qs ? ws / 2 : ws) : 0;
         const int nwh_o = wso > 0 ? cdiv(S2, wso) : 1;
-        Timed t(ctx, "hiera_proj_residual");
-        TRY(hip_check(ctx, t.done(launch_hiera_proj_residual(x_out, sc, b.p, blk->proj_b, Cout, S2, S2, wso, nwh_o, st)),
-                      "proj_residual launch"));
+        const int mp = fused_mode(ctx, blk->proj_w, Cout);
+        const mi355_tensor in = tensor_on(b.att, T_F32, Cout, Mo);
+        if (mp == ACT_F32) {
+            const mi355_tensor out = tensor_on(b.p, T_F32, Cout, Mo);
+            TRY(mi355_mul_mat(ctx, &blk->proj_w, &in, &out));
+            Timed t(ctx, "hiera_proj_residual");
+            TRY(hip_check(ctx, t.done(launch_hiera_proj_residual(x_out, sc, b.p, blk->proj_b, Cout, S2, S2, wso, nwh_o, st)),
+                          "proj_residual launch"));
+        } else {
+            TRY(quantize_act(ctx, &in, act_out(b.a0, mp, Mo, Cout)));
+            MmqEpi e{};
+            e.kind = MMQ_EPI_RESIDUAL;
+            e.bias = blk->proj_b;
+            e.res = sc;
+            e.out = x_out;
+            e.map = RowMap{wso > 0 ? ROWMAP_SAM2_UNPART : ROWMAP_IDENTITY, S2, S2, wso, nwh_o};
+            TRY(mul_mat_epi(ctx, &blk->proj_w, act_in(b.a0, mp, Mo, Cout), e));
+        }
     }
     // MLP
     const int64_t M2 = (int64_t)S2 * S2;
@@ -384,6 +401,8 @@ mi355_status run_block(mi355_context* ctx, const mi355_hiera_hparams* hp, const 
         Timed t(ctx, "hiera_ln");
         TRY(hip_check(ctx, t.done(launch_hiera_ln(a, st)), "hiera_ln launch"));
     }
+    // fc1, bias + GELU writing fc2's operand, fc2 (+ bias, residual: fused epilogue)
+    const int m2 = fused_mode(ctx, blk->fc2_w, MLP);
     {
         const mi355_tensor out = tensor_on(b.h, T_F32, MLP, M2);
         if (m1 == ACT_F32) {
@@ -392,27 +411,26 @@ mi355_status run_block(mi355_context* ctx, const mi355_hiera_hparams* hp, const 
         } else {
             TRY(mul_mat_act(ctx, &blk->fc1_w, act_in(b.a0, m1, M2, Cout), &out));
         }
+        Timed t(ctx, "bias_gelu_tanh");
+        if (m2 == ACT_F32)
+            TRY(hip_check(ctx, t.done(launch_bias_gelu_tanh(b.h, blk->fc1_b, M2, MLP, st)), "bias_gelu_tanh launch"));
+        else
+            TRY(hip_check(ctx, t.done(launch_bias_gelu_tanh_act(b.h, blk->fc1_b, M2, MLP, act_out(b.a2, m2, M2, MLP), st)),
+                          "bias_gelu_tanh launch"));
     }
-    {
-        const int m2 = fused_mode(ctx, blk->fc2_w, MLP);
-        const mi355_tensor out = tensor_on(b.f, T_F32, Cout, M2);
-        if (m2 == ACT_F32) {
-            {
-                Timed t(ctx, "bias_gelu_tanh");
-                TRY(hip_check(ctx, t.done(launch_bias_gelu_tanh(b.h, blk->fc1_b, M2, MLP, st)), "bias_gelu_tanh launch"));
-            }
-            const mi355_tensor in = tensor_on(b.h, T_F32, MLP, M2);
-            TRY(mi355_mul_mat(ctx, &blk->fc2_w, &in, &out));
-        } else {
-            {
-                Timed t(ctx, "bias_gelu_tanh");
-                TRY(hip_check(ctx, t.done(launch_bias_gelu_tanh_act(b.h, blk->fc1_b, M2, MLP, act_out(b.a0, m2, M2, MLP), st)),
-                              "bias_gelu_tanh launch"));
-            }
-            TRY(mul_mat_act(ctx, &blk->fc2_w, act_in(b.a0, m2, M2, MLP), &out));
-        }
+    if (m2 == ACT_F32) {
+        const mi355_tensor in = tensor_on(b.h, T_F32, MLP, M2), out = tensor_on(b.f, T_F32, Cout, M2);
+        TRY(mi355_mul_mat(ctx, &blk->fc2_w, &in, &out));
         Timed t(ctx, "bias_residual");
         TRY(hip_check(ctx, t.done(launch_bias_residual(x_out, b.f, blk->fc2_b, M2, Cout, st)), "bias_residual launch"));
+    } else {
+        MmqEpi e{};
+        e.kind = MMQ_EPI_RESIDUAL;
+        e.bias = blk->fc2_b;
+        e.res = x_out;
+        e.out = x_out;
+        e.map = RowMap{ROWMAP_IDENTITY, 0, 0, 0, 0};
+        TRY(mul_mat_epi(ctx, &blk->fc2_w, act_in(b.a2, m2, M2, MLP), e));
     }
     return MI355_STATUS_SUCCESS;
 }

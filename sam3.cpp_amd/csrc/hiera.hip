@@ -11,16 +11,6 @@
 
 namespace mi355 {
 
-// window-order row r -> image token, or -1 for a padding token
-__device__ __forceinline__ int64_t hwin_src(int64_t r, int W, int H, int ws, int nwh) {
-    const int64_t n = r / (ws * ws);
-    const int loc = (int)(r - n * ws * ws);
-    const int lh = loc / ws, lw = loc % ws;
-    const int wh = (int)(n % nwh), ww = (int)(n / nwh);
-    const int h = wh * ws + lh, w = ww * ws + lw;
-    return (h < H && w < W) ? (int64_t)h * W + w : -1;
-}
-
 __device__ __forceinline__ double wave_sum_dh(double v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
@@ -218,19 +208,6 @@ __global__ __launch_bounds__(256) void hiera_proj_residual_kernel(float* x, cons
     x[tix] = shortcut[tix] + u;
 }
 
-// ggml_gelu with ggml-cpu's fp16-table semantics (GGML_GELU_FP16): 0 for x <= -10, x for
-// x >= 10, else f16(gelu_f32(f16(x))), gelu_f32 evaluated left to right in fp32
-__device__ __forceinline__ float gelu_tanh_table(float u) {
-    if (u <= -10.0f) return 0.0f;
-    if (u >= 10.0f) return u;
-    const float v = h2f(f2h(u));
-    const float inner0 = 0.79788456080286535587989211986876f * v;
-    const float av = 0.044715f * v;
-    const float avv = av * v;
-    const float inner = inner0 * (1.0f + avv);
-    const float hv = 0.5f * v;
-    return h2f(f2h(hv * (1.0f + tanhf(inner))));
-}
 // h = ggml_gelu(h + b) with ggml-cpu's fp16-table semantics (GGML_GELU_FP16):
 // 0 for x <= -10, x for x >= 10, else f16(gelu_f32(f16(x))).
 __global__ __launch_bounds__(256) void bias_gelu_tanh_kernel(float* __restrict__ h, const float* __restrict__ b,

@@ -76,9 +76,31 @@ struct MatD {  // dst F32
 // int32 dots [z][m][n][b] instead of dst.
 hipError_t launch_mmq(const MatW& w, const ActF16& a, const MatD& d, int64_t N, int64_t ne12, int64_t ne13,
                       int32_t* dots, void* align_buf, hipStream_t st);
-// Padded row count of the activation scale arrays.
 // Bytes of the 4-byte-pitch weight copy launch_mmq needs (0 when rows are aligned).
 size_t mmq_align_bytes(const MatW& w, int64_t N, int64_t K);
+
+// GEMM row -> row of another token order, or -1 (a padding token, dropped).
+enum { ROWMAP_IDENTITY = 0, ROWMAP_WIN_UNPART = 1, ROWMAP_SAM2_UNPART = 2 };
+struct RowMap {
+    int kind;
+    int W, H;   // image grid (tokens)
+    int ws;     // window side
+    int nwh;    // SAM2: windows along H of the padded grid
+};
+
+// Fused MUL_MAT epilogue (one 2-D GEMM, dst [M][N] never written; N % 4 == 0):
+//   MMQ_EPI_RESIDUAL  out[map(m)][n] = res[map(m)][n] + (dst[m][n] + bias[n]),
+//                     rows with map(m) = -1 dropped
+enum { MMQ_EPI_STORE = 0, MMQ_EPI_RESIDUAL = 1 };
+struct MmqEpi {
+    int kind;
+    const float* bias;  // [N]
+    const float* res;   // [rows][N] (may be out)
+    float* out;         // [rows][N]
+    RowMap map;
+};
+hipError_t launch_mmq_epi(const MatW& w, const ActF16& a, int64_t N, const MmqEpi& e, void* align_buf,
+                          hipStream_t st);
 
 // Row softmax of scale*x (F32, strided rows) into dst (F32, strided rows).
 hipError_t launch_soft_max(const SrcView& src, float scale, char* dst, const int64_t dnb[4], hipStream_t st);

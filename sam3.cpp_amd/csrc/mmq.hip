@@ -85,6 +85,14 @@ __device__ __forceinline__ void bytes_to_h4(uint32_t u, _Float16 bias, uint32_t&
     h23 = h2_sub(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u), bias);
 }
 
+// 16-byte slot of chunk c of tile row r is c ^ swz(r): ds_read_b128 serves 16
+// lanes per pass from 64 banks, and the 16 consecutive rows an MFMA fragment
+// read touches per pass land in 16 distinct slots (8 within every 8 rows).
+template <int CH>
+__device__ __forceinline__ int swz(int r) {
+    return CH == 8 ? ((r & 7) ^ ((r >> 3) & 1)) : (((r >> 1) & 3) ^ ((r >> 3) & 1));
+}
+
 struct MmqArgs {
     const uint8_t* W;
     int64_t w_nb1, w_nb2, w_nb3;
@@ -171,14 +179,13 @@ struct Stage {
 // (leaving stage s+1's outstanding), one barrier publishes everyone's, and
 // the DMA of stage s+2 goes into the buffer stage s-1 used.
 //   activation tile: 128 rows x 64 halves, unpadded; 16-byte chunk c of row r
-//     sits in slot c ^ (r & 7), so a 32-row MFMA fragment read hits 8
-//     distinct slots (no bank conflicts) while each DMA lane still writes
-//     16 contiguous bytes;
+//     sits in slot c ^ swz(r), so the MFMA fragment reads are free of bank
+//     conflicts while each DMA lane still writes 16 contiguous bytes;
 //   raw weight segments: lane-linear dwords (row j / RD, dword j % RD);
 //     each wavefront decodes its own 32 weight rows' fragments on the fly;
 //   activation scales (and Q8_1 sums): 128 fp16 per block, one dword per lane.
-template <int WT, bool DOTS>
-__global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p) {
+template <int WT, bool DOTS, int EPI>
+__global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEpi e) {
     using St = Stage<WT>;
     constexpr bool QUANT = St::QUANT;
     constexpr int WB = St::WB, HDR = WInfo<WT == T_F16 ? T_Q8_0 : WT>::hdr;
@@ -216,13 +223,14 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p) {
     // ---- DMA offsets, fixed for the whole K loop
     // activation / F16-weight tile, instruction i of wavefront w: rows (NI*w+i)*RPI + lane/CH,
     // slot lane%CH <- chunk (lane%CH) ^ (row%CH)
-    const int trow = lane / CH, tchunk = (lane % CH) ^ (trow % CH);
-    int aoff[NI], foff[NI];
+    const int trow = lane / CH;
+    int aoff[NI], foff[NI], tch[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
         const int row = (wn * NI + i) * RPI + trow;
-        aoff[i] = m0 + row < M ? ((m0 + row) * (int)p.a_s1 + tchunk * 8) * 2 : OOB;
-        foff[i] = !QUANT && n0 + row < N ? (n0 + row) * (int)p.w_nb1 + tchunk * 16 : OOB;
+        tch[i] = (lane % CH) ^ swz<CH>(row);
+        aoff[i] = m0 + row < M ? ((m0 + row) * (int)p.a_s1 + tch[i] * 8) * 2 : OOB;
+        foff[i] = !QUANT && n0 + row < N ? (n0 + row) * (int)p.w_nb1 + tch[i] * 16 : OOB;
     }
     int woff[QUANT ? RLD : 1];  // raw weight dword j = NT*i + 64w + lane -> (row j / RD, dword j % RD)
 #pragma unroll
@@ -234,11 +242,10 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p) {
     auto dma_stage = [&](int s, St& b) {
         const int k0 = s * SKH;
         const bool tail = k0 + SKH > K;  // chunks past K must read zeros (rows continue in memory)
-        const bool cvalid = k0 + tchunk * 8 < K;
         const auto ar = make_rsrc(Az + k0, p.a_extent - 2LL * k0);
 #pragma unroll
         for (int i = 0; i < NI; ++i)
-            dma_b128(ar, &b.A[(wn * NI + i) * RPI * SKH], tail && !cvalid ? OOB : aoff[i]);
+            dma_b128(ar, &b.A[(wn * NI + i) * RPI * SKH], tail && k0 + tch[i] * 8 >= K ? OOB : aoff[i]);
         if (QUANT) {
             const int64_t seg = (int64_t)s * BKB * WB;
             const auto wrs = make_rsrc(Wz + seg, p.w_extent - seg);
@@ -257,7 +264,7 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p) {
             const auto fr = make_rsrc(Wz + 2LL * k0, p.w_extent - 2LL * k0);
 #pragma unroll
             for (int i = 0; i < NI; ++i)
-                dma_b128(fr, &b.Bf[(wn * NI + i) * RPI * SKH], tail && !cvalid ? OOB : foff[i]);
+                dma_b128(fr, &b.Bf[(wn * NI + i) * RPI * SKH], tail && k0 + tch[i] * 8 >= K ? OOB : foff[i]);
         }
     };
 
@@ -272,7 +279,7 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p) {
     const bool lo = lane < 32;
     // fragment of row r, 8-half chunk c in a swizzled tile
     auto frag = [&](const _Float16* tile, int r, int c) -> v8h {
-        return *reinterpret_cast<const v8h*>(&tile[r * SKH + ((c ^ (r & (CH - 1))) << 3)]);
+        return *reinterpret_cast<const v8h*>(&tile[r * SKH + ((c ^ swz<CH>(r)) << 3)]);
     };
 
     auto compute = [&](int s, const St& b) {
@@ -387,15 +394,63 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p) {
     }
     if (DOTS) return;
 
-    char* Dz = reinterpret_cast<char*>(p.D) + (int64_t)i12 * p.d_nb2 + (int64_t)i13 * p.d_nb3;
     const int n = n0 + wrow;
+    if (EPI == MMQ_EPI_STORE) {
+        char* Dz = reinterpret_cast<char*>(p.D) + (int64_t)i12 * p.d_nb2 + (int64_t)i13 * p.d_nb3;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int m = m0 + mt * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
+                if (m < M && n < N) *reinterpret_cast<float*>(Dz + (int64_t)m * p.d_nb1 + (int64_t)n * 4) = acc[mt][i];
+            }
+        return;
+    }
+    // The residual epilogue goes through LDS: the 128 x 128 result tile, 64
+    // rows at a time (32 in st0, 32 in st1), is rewritten row-major so that
+    // each thread then owns 4 consecutive columns (float4 loads and stores).
+    // out = res + (dst + bias), each add rounded to fp32 as ggml's ADD nodes.
+    constexpr int TP = BN + 4;                // row pitch (floats)
+    constexpr int CPR = BN / 4;               // float4 chunks per row
+    constexpr int IT = 64 * CPR / NT;         // rows per thread per half
+    static_assert(32 * TP * 4 <= (int)sizeof(St), "epilogue tile exceeds a stage buffer");
+    float* t0 = reinterpret_cast<float*>(&st0);
+    float* t1 = reinterpret_cast<float*>(&st1);
+    const int c = tid % CPR, nc = n0 + 4 * c;  // this thread's 4 columns, the same in every row
+    const bool cv = nc < N;                    // N % 4 == 0
+    const v4f bv = cv ? *reinterpret_cast<const v4f*>(&e.bias[nc]) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        __syncthreads();  // every wavefront is done reading the stage buffers / the previous half
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const int m = m0 + mt * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-            if (m < M && n < N) *reinterpret_cast<float*>(Dz + (int64_t)m * p.d_nb1 + (int64_t)n * 4) = acc[mt][i];
+            const int r = 8 * (i >> 2) + 4 * g + (i & 3);
+            t0[r * TP + wrow] = acc[2 * half][i];
+            t1[r * TP + wrow] = acc[2 * half + 1][i];
         }
+        __syncthreads();
+        {
+            // residual loads of four rows first, then their stores (res may be out)
+#pragma unroll
+            for (int i0 = 0; i0 < IT; i0 += 4) {
+                int rr[4];
+                v4f xs[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int m = m0 + half * 64 + (i0 + k) * (NT / CPR) + tid / CPR;
+                    rr[k] = m < M && cv ? map_row32(e.map, m) : -1;
+                    xs[k] = rr[k] >= 0 ? *reinterpret_cast<const v4f*>(&e.res[(int64_t)rr[k] * N + nc])
+                                       : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int it = i0 + k, r = it * (NT / CPR) + tid / CPR;
+                    const v4f v = *reinterpret_cast<const v4f*>(&(it < IT / 2 ? t0 : t1)[(r & 31) * TP + 4 * c]);
+                    if (rr[k] >= 0) *reinterpret_cast<v4f*>(&e.out[(int64_t)rr[k] * N + nc]) = xs[k] + (v + bv);
+                }
+            }
+        }
+    }
 }
 
 // Copies rows of row_bytes (2-byte aligned source rows) to a 4-byte pitch so
@@ -411,11 +466,13 @@ __global__ __launch_bounds__(256) void align_rows_kernel(const uint8_t* __restri
 }
 
 template <int WT>
-static void launch_t(const MmqArgs& a, int Z, bool dots, hipStream_t st) {
+static void launch_t(const MmqArgs& a, int Z, bool dots, const MmqEpi* e, hipStream_t st) {
     const int T = a.tiles_m * a.tiles_n;
     const dim3 grid((unsigned)(((T + 7) / 8) * 8), (unsigned)Z);
-    if (dots) mmq_kernel<WT, true><<<grid, NT, 0, st>>>(a);
-    else mmq_kernel<WT, false><<<grid, NT, 0, st>>>(a);
+    MmqEpi none{};
+    if (dots) mmq_kernel<WT, true, MMQ_EPI_STORE><<<grid, NT, 0, st>>>(a, none);
+    else if (!e || e->kind == MMQ_EPI_STORE) mmq_kernel<WT, false, MMQ_EPI_STORE><<<grid, NT, 0, st>>>(a, none);
+    else mmq_kernel<WT, false, MMQ_EPI_RESIDUAL><<<grid, NT, 0, st>>>(a, *e);
 }
 
 
@@ -431,8 +488,8 @@ size_t mmq_align_bytes(const MatW& w, int64_t N, int64_t K) {
     return a4 ? 0 : (size_t)(N * w.ne2 * w.ne3) * (size_t)((rowb + 3) & ~3);
 }
 
-hipError_t launch_mmq(const MatW& w_in, const ActF16& a, const MatD& d, int64_t N, int64_t ne12, int64_t ne13,
-                      int32_t* dots, void* align_buf, hipStream_t st) {
+static hipError_t run_mmq(const MatW& w_in, const ActF16& a, const MatD& d, int64_t N, int64_t ne12, int64_t ne13,
+                          int32_t* dots, const MmqEpi* epi, void* align_buf, hipStream_t st) {
     MatW w = w_in;
     int64_t rowb = w.type == T_F16 ? a.K * 2 : (a.K / QK) * (w.type == T_Q8_0 ? 34 : w.type == T_Q4_0 ? 18 : 20);
     if (mmq_align_bytes(w_in, N, a.K) != 0) {
@@ -479,13 +536,25 @@ hipError_t launch_mmq(const MatW& w_in, const ActF16& a, const MatD& d, int64_t 
     if (p.w_extent >= OOB || p.a_extent >= OOB || 2 * a.M * a.dp >= OOB) return hipErrorInvalidValue;
     const int Z = (int)(ne12 * ne13);
     switch (w.type) {
-        case T_Q8_0: launch_t<T_Q8_0>(p, Z, dots, st); break;
-        case T_Q4_0: launch_t<T_Q4_0>(p, Z, dots, st); break;
-        case T_Q4_1: launch_t<T_Q4_1>(p, Z, dots, st); break;
-        case T_F16: launch_t<T_F16>(p, Z, false, st); break;
+        case T_Q8_0: launch_t<T_Q8_0>(p, Z, dots, epi, st); break;
+        case T_Q4_0: launch_t<T_Q4_0>(p, Z, dots, epi, st); break;
+        case T_Q4_1: launch_t<T_Q4_1>(p, Z, dots, epi, st); break;
+        case T_F16: launch_t<T_F16>(p, Z, false, epi, st); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_mmq(const MatW& w, const ActF16& a, const MatD& d, int64_t N, int64_t ne12, int64_t ne13,
+                      int32_t* dots, void* align_buf, hipStream_t st) {
+    return run_mmq(w, a, d, N, ne12, ne13, dots, nullptr, align_buf, st);
+}
+
+hipError_t launch_mmq_epi(const MatW& w, const ActF16& a, int64_t N, const MmqEpi& e, void* align_buf,
+                          hipStream_t st) {
+    if (e.kind != MMQ_EPI_RESIDUAL || !e.bias || !e.res || !e.out || N % 4 != 0) return hipErrorInvalidValue;
+    const MatD none{nullptr, 0, 0, 0};
+    return run_mmq(w, a, none, N, 1, 1, nullptr, &e, align_buf, st);
 }
 
 }  // namespace mi355

@@ -37,21 +37,24 @@ struct EncBufs {
     _Float16* v;
     float* attn;    // [M][E]  attention output, fc2 output
     float* big;     // [M][MLP] fc1 output (or im2col columns)
-    uint16_t* aq;   // [M][max(E, MLP)] activation operand: Q8 quants or F16 rows
-    uint16_t* ad;   // [M][dp] block scales
-    uint16_t* as;   // [M][dp] Q8_1 sums
+    uint16_t* aq;   // [M][E] activation operand of qkv / proj / fc1: Q8 quants or F16 rows
+    uint16_t* ad;   // [M][dp(E)] block scales
+    uint16_t* as;   // [M][dp(E)] Q8_1 sums
+    uint16_t* hq;   // [M][MLP] operand of fc2 (fc1's epilogue output)
+    uint16_t* hd;
+    uint16_t* hs;
 };
 
 size_t enc_bytes(const mi355_vit_hparams* hp, EncBufs* b, char* base) {
     const size_t M = (size_t)hp->grid * hp->grid, E = (size_t)hp->embed_dim;
     const size_t kpatch = 3 * (size_t)hp->patch_size * hp->patch_size;
     const size_t big = M * std::max((size_t)hp->mlp_dim, kpatch) * 4;
-    const size_t kmax = std::max(E, (size_t)hp->mlp_dim);
-    const size_t dpm = (size_t)mmq_scale_pitch((int64_t)kmax);
-    const size_t sz[10] = {M * E * 4, M * 3 * E * 4, M * E * 2, M * E * 2, M * E * 2, M * E * 4, big,
-                           M * kmax * 2, M * dpm * 2, M * dpm * 2};
-    size_t off[10], o = 0;
-    for (int i = 0; i < 10; ++i) {
+    const size_t H = (size_t)hp->mlp_dim;
+    const size_t dpe = (size_t)mmq_scale_pitch((int64_t)E), dph = (size_t)mmq_scale_pitch((int64_t)H);
+    const size_t sz[13] = {M * E * 4, M * 3 * E * 4, M * E * 2, M * E * 2, M * E * 2,   M * E * 4,  big,
+                           M * E * 2, M * dpe * 2,   M * dpe * 2, M * H * 2, M * dph * 2, M * dph * 2};
+    size_t off[13], o = 0;
+    for (int i = 0; i < 13; ++i) {
         off[i] = o;
         o += align_up(sz[i]);
     }
@@ -66,6 +69,9 @@ size_t enc_bytes(const mi355_vit_hparams* hp, EncBufs* b, char* base) {
         b->aq = reinterpret_cast<uint16_t*>(base + off[7]);
         b->ad = reinterpret_cast<uint16_t*>(base + off[8]);
         b->as = reinterpret_cast<uint16_t*>(base + off[9]);
+        b->hq = reinterpret_cast<uint16_t*>(base + off[10]);
+        b->hd = reinterpret_cast<uint16_t*>(base + off[11]);
+        b->hs = reinterpret_cast<uint16_t*>(base + off[12]);
     }
     return o;
 }
@@ -102,17 +108,19 @@ mi355_tensor dev_tensor(const void* p, int type, int64_t ne0, int64_t ne1, int64
     return t;
 }
 
-// the activation operand in b.aq/ad/as for a GEMM with K inputs over M rows
-ActOut act_out(const EncBufs& b, int mode, int64_t K) {
-    return ActOut{mode, nullptr, b.aq, b.ad, b.as, mmq_scale_pitch(K)};
+// a GEMM activation operand (q, d, s) with K inputs over M rows: the E-wide
+// one (aq, ad, as) or fc2's (hq, hd, hs)
+ActOut act_out(const EncBufs& b, int mode, int64_t K, bool hidden = false) {
+    return hidden ? ActOut{mode, nullptr, b.hq, b.hd, b.hs, mmq_scale_pitch(K)}
+                  : ActOut{mode, nullptr, b.aq, b.ad, b.as, mmq_scale_pitch(K)};
 }
-ActF16 act_in(const EncBufs& b, int mode, int64_t M, int64_t K) {
+ActF16 act_in(const EncBufs& b, int mode, int64_t M, int64_t K, bool hidden = false) {
     ActF16 a;
-    a.q = b.aq;
+    a.q = hidden ? b.hq : b.aq;
     a.s1 = K;
     a.s2 = a.s3 = K * M;
-    a.d = mode == ACT_F16 ? nullptr : b.ad;
-    a.s = mode == ACT_Q8S ? b.as : nullptr;
+    a.d = mode == ACT_F16 ? nullptr : hidden ? b.hd : b.ad;
+    a.s = mode == ACT_Q8S ? (hidden ? b.hs : b.as) : nullptr;
     a.dp = mmq_scale_pitch(K);
     a.M = M;
     a.K = K;
@@ -326,30 +334,46 @@ mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams
                            v = dev_tensor(b.v, T_F16, HD, N, NH, B), o = dev_tensor(b.attn, T_F32, HD, NH, N, B);
         TRY(mi355_flash_attn_ext(ctx, &q, &k, &v, nullptr, 1.0f / sqrtf((float)HD), 0.0f, 0.0f, &o));
     }
-    {
+    // proj (+ bias, window unpartition, residual: fused into the GEMM's epilogue)
+    const int mp = ctx->fuse ? act_mode_for(blk->proj_w.type) : ACT_F32;
+    if (mp == ACT_F32) {
         const mi355_tensor in = dev_tensor(b.attn, T_F32, E, M), out = dev_tensor(b.xn, T_F32, E, M);
         TRY(mi355_mul_mat(ctx, &blk->proj_w, &in, &out));
+        TRY(mi355_vit_proj_residual(ctx, x, b.xn, blk->proj_b, M, E, G, WS));
+    } else {
+        const mi355_tensor in = dev_tensor(b.attn, T_F32, E, M);
+        TRY(quantize_act(ctx, &in, act_out(b, mp, E)));
+        MmqEpi e{};
+        e.kind = MMQ_EPI_RESIDUAL;
+        e.bias = blk->proj_b;
+        e.res = x;
+        e.out = x;
+        e.map = RowMap{WS > 0 ? ROWMAP_WIN_UNPART : ROWMAP_IDENTITY, G, G, WS, 0};
+        TRY(mul_mat_epi(ctx, &blk->proj_w, act_in(b, mp, M, E), e));
     }
-    TRY(mi355_vit_proj_residual(ctx, x, b.xn, blk->proj_b, M, E, G, WS));
-    // MLP
+    // MLP: fc1, bias + GELU writing fc2's operand, fc2 (+ bias, residual: fused epilogue)
+    const int m2 = ctx->fuse && MLP % 32 == 0 ? act_mode_for(blk->fc2_w.type) : ACT_F32;
     TRY(ln_gemm(blk->norm2_w, blk->norm2_b, 0, blk->fc1_w, b.big, MLP));
-    {
-        const int mode = ctx->fuse ? act_mode_for(blk->fc2_w.type) : ACT_F32;
-        const mi355_tensor out = dev_tensor(b.attn, T_F32, E, M);
-        if (mode == ACT_F32 || MLP % 32 != 0) {
-            TRY(mi355_vit_bias_gelu(ctx, b.big, blk->fc1_b, M, MLP));
-            const mi355_tensor in = dev_tensor(b.big, T_F32, MLP, M);
-            TRY(mi355_mul_mat(ctx, &blk->fc2_w, &in, &out));
-        } else {
-            {
-                Timed t(ctx, "bias_gelu");
-                TRY(hip_check(ctx, t.done(launch_bias_gelu_act(b.big, blk->fc1_b, M, MLP, act_out(b, mode, MLP), ctx->stream)),
-                              "bias_gelu launch"));
-            }
-            TRY(mul_mat_act(ctx, &blk->fc2_w, act_in(b, mode, M, MLP), &out));
-        }
+    if (m2 == ACT_F32) {
+        TRY(mi355_vit_bias_gelu(ctx, b.big, blk->fc1_b, M, MLP));
+    } else {
+        Timed t(ctx, "bias_gelu");
+        TRY(hip_check(ctx, t.done(launch_bias_gelu_act(b.big, blk->fc1_b, M, MLP, act_out(b, m2, MLP, true), ctx->stream)),
+                      "bias_gelu launch"));
     }
-    TRY(mi355_vit_bias_residual(ctx, x, b.attn, blk->fc2_b, M, E));
+    if (m2 == ACT_F32) {
+        const mi355_tensor in = dev_tensor(b.big, T_F32, MLP, M), out = dev_tensor(b.attn, T_F32, E, M);
+        TRY(mi355_mul_mat(ctx, &blk->fc2_w, &in, &out));
+        TRY(mi355_vit_bias_residual(ctx, x, b.attn, blk->fc2_b, M, E));
+    } else {
+        MmqEpi e{};
+        e.kind = MMQ_EPI_RESIDUAL;
+        e.bias = blk->fc2_b;
+        e.res = x;
+        e.out = x;
+        e.map = RowMap{ROWMAP_IDENTITY, 0, 0, 0, 0};
+        TRY(mul_mat_epi(ctx, &blk->fc2_w, act_in(b, m2, M, MLP, true), e));
+    }
 #undef TRY
     return MI355_STATUS_SUCCESS;
 }
