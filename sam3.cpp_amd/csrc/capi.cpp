@@ -218,20 +218,6 @@ int act_mode_for(int t) {
     }
 }
 
-mi355_status quantize_act(mi355_context* ctx, const mi355_tensor* x, const ActOut& o) {
-    if (!x || x->type != T_F32) return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_act: F32 rows expected");
-    if (o.mode == ACT_F16) {
-        Timed t(ctx, "convert_f16");
-        return hip_check(ctx, t.done(launch_convert_f16(view_of(x), o.q, ctx->stream)), "convert_f16 launch");
-    }
-    if (o.mode != ACT_Q8 && o.mode != ACT_Q8S) return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_act: bad mode");
-    if (x->ne[0] % 32 != 0 || o.dp != mmq_scale_pitch(x->ne[0]))
-        return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_act: row length / scale pitch");
-    Timed t(ctx, "quantize_mmq");
-    return hip_check(ctx, t.done(launch_quantize_mmq(view_of(x), o.mode == ACT_Q8S, o.dp, o.q, o.d, o.s, ctx->stream)),
-                     "quantize_mmq launch");
-}
-
 // MUL_MAT of a prequantized operand with a fused epilogue in place of dst
 // (dst [M][N] F32 is only a shape here: nothing is written to it).
 mi355_status mul_mat_epi(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const MmqEpi& e) {
@@ -287,6 +273,74 @@ mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF1
     return hip_check(ctx, tq.done(launch_mmq(matw_of(s0), a, matd_of(d), N, 1, 1, nullptr, align ? ctx->ws : nullptr,
                                              ctx->stream)),
                      "mmq launch");
+}
+
+mi355_status flash_attn_act(mi355_context* ctx, const mi355_tensor* q, const mi355_tensor* k, const mi355_tensor* v,
+                            const mi355_tensor* mask, float scale, float max_bias, float logit_softcap,
+                            const mi355_tensor* dst, const ActOut* op) {
+    if (!q || !k || !v || !dst || !q->data || !k->data || !v->data || !dst->data)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: null argument");
+    if (!dims_ok(q) || !dims_ok(k) || !dims_ok(v) || !dims_ok(dst))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: negative ne/nb");
+    if (mask || max_bias != 0.0f || logit_softcap != 0.0f)
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: mask, ALiBi and softcap not supported");
+    // ggml_flash_attn_ext shape rules
+    const int64_t D = q->ne[0];
+    if (k->ne[0] != D || v->ne[1] != k->ne[1] || q->ne[3] != k->ne[3] || q->ne[3] != v->ne[3])
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: q/k/v shapes do not match");
+    if (k->ne[2] <= 0 || v->ne[2] <= 0 || q->ne[2] % k->ne[2] != 0 || q->ne[2] % v->ne[2] != 0)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: heads not divisible by kv heads");
+    if (dst->type != T_F32 || dst->ne[0] != v->ne[0] || dst->ne[1] != q->ne[2] || dst->ne[2] != q->ne[1] ||
+        dst->ne[3] != q->ne[3])
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: dst must be F32 [Dv, n_head, n_q, batch]");
+    if (dst->nb[0] != 4 || dst->nb[1] != 4 * dst->ne[0] || dst->nb[2] != dst->nb[1] * dst->ne[1] ||
+        dst->nb[3] != dst->nb[2] * dst->ne[2])
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: dst must be contiguous");
+    if (v->ne[0] != D || !(D == 64 || D == 96 || D == 128))
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: head size %lld (supported: D = Dv in 64, 96, 128)",
+                    (long long)D);
+    const mi355_tensor* ops[3] = {q, k, v};
+    for (const mi355_tensor* t : ops) {
+        if (t->type != T_F32 && t->type != T_F16)
+            return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: q/k/v must be F32 or F16");
+        if (t->nb[0] != type_size(t->type))
+            return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: rows must be contiguous (nb[0] = type size)");
+        if (((reinterpret_cast<uintptr_t>(t->data) | (uintptr_t)t->nb[1] | (uintptr_t)t->nb[2] | (uintptr_t)t->nb[3]) &
+             3) != 0)
+            return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: rows must be 4-byte aligned");
+    }
+    if (k->type != v->type) return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: k and v must share a type");
+    if (q->ne[1] > INT32_MAX || k->ne[1] > INT32_MAX || q->ne[2] > 65535 || q->ne[3] > 65535)
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: sizes beyond the launch limits");
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "flash_attn_ext: null context");
+    FaArgs a;
+    a.q = static_cast<const char*>(q->data);
+    a.k = static_cast<const char*>(k->data);
+    a.v = static_cast<const char*>(v->data);
+    a.dst = static_cast<float*>(dst->data);
+    a.q_nb1 = q->nb[1]; a.q_nb2 = q->nb[2]; a.q_nb3 = q->nb[3];
+    a.k_nb1 = k->nb[1]; a.k_nb2 = k->nb[2]; a.k_nb3 = k->nb[3];
+    a.v_nb1 = v->nb[1]; a.v_nb2 = v->nb[2]; a.v_nb3 = v->nb[3];
+    a.nq = (int)q->ne[1];
+    a.nkv = (int)k->ne[1];
+    a.nh = (int)q->ne[2];
+    a.rk2 = (int)(q->ne[2] / k->ne[2]);
+    a.rv2 = (int)(q->ne[2] / v->ne[2]);
+    const float c = fabsf(scale) * 1.44269504088896340736f;
+    a.c = c > 1e-30f ? c : 1e-30f;  // keeps masked (-inf) scores at weight 0 when scale is 0
+    a.negq = scale < 0.0f;
+    a.out = ActOut{ACT_F32, nullptr, nullptr, nullptr, nullptr, 0};
+    if (op) {
+        const int64_t K = q->ne[2] * D;
+        if (op->mode == ACT_F32 || !op->q || (op->mode != ACT_F16 && (!op->d || (op->mode == ACT_Q8S && !op->s) ||
+                                                                    op->dp != mmq_scale_pitch(K))))
+            return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: bad operand output");
+        a.out = *op;
+    }
+    (void)hipSetDevice(ctx->device);
+    Timed tf(ctx, "flash_attn_ext");
+    return hip_check(ctx, tf.done(launch_fattn(a, (int)D, q->type == T_F32, k->type == T_F32, (int)q->ne[3], ctx->stream)),
+                     "flash_attn_ext launch");
 }
 
 }  // namespace mi355
@@ -542,61 +596,7 @@ void mi355_profile_reset(mi355_context* ctx) {
 mi355_status mi355_flash_attn_ext(mi355_context* ctx, const mi355_tensor* q, const mi355_tensor* k,
                                   const mi355_tensor* v, const mi355_tensor* mask, float scale, float max_bias,
                                   float logit_softcap, const mi355_tensor* dst) {
-    if (!q || !k || !v || !dst || !q->data || !k->data || !v->data || !dst->data)
-        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: null argument");
-    if (!dims_ok(q) || !dims_ok(k) || !dims_ok(v) || !dims_ok(dst))
-        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: negative ne/nb");
-    if (mask || max_bias != 0.0f || logit_softcap != 0.0f)
-        return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: mask, ALiBi and softcap not supported");
-    // ggml_flash_attn_ext shape rules
-    const int64_t D = q->ne[0];
-    if (k->ne[0] != D || v->ne[1] != k->ne[1] || q->ne[3] != k->ne[3] || q->ne[3] != v->ne[3])
-        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: q/k/v shapes do not match");
-    if (k->ne[2] <= 0 || v->ne[2] <= 0 || q->ne[2] % k->ne[2] != 0 || q->ne[2] % v->ne[2] != 0)
-        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: heads not divisible by kv heads");
-    if (dst->type != T_F32 || dst->ne[0] != v->ne[0] || dst->ne[1] != q->ne[2] || dst->ne[2] != q->ne[1] ||
-        dst->ne[3] != q->ne[3])
-        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: dst must be F32 [Dv, n_head, n_q, batch]");
-    if (dst->nb[0] != 4 || dst->nb[1] != 4 * dst->ne[0] || dst->nb[2] != dst->nb[1] * dst->ne[1] ||
-        dst->nb[3] != dst->nb[2] * dst->ne[2])
-        return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: dst must be contiguous");
-    if (v->ne[0] != D || !(D == 64 || D == 96 || D == 128))
-        return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: head size %lld (supported: D = Dv in 64, 96, 128)",
-                    (long long)D);
-    const mi355_tensor* ops[3] = {q, k, v};
-    for (const mi355_tensor* t : ops) {
-        if (t->type != T_F32 && t->type != T_F16)
-            return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: q/k/v must be F32 or F16");
-        if (t->nb[0] != type_size(t->type))
-            return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: rows must be contiguous (nb[0] = type size)");
-        if (((reinterpret_cast<uintptr_t>(t->data) | (uintptr_t)t->nb[1] | (uintptr_t)t->nb[2] | (uintptr_t)t->nb[3]) &
-             3) != 0)
-            return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: rows must be 4-byte aligned");
-    }
-    if (k->type != v->type) return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: k and v must share a type");
-    if (q->ne[1] > INT32_MAX || k->ne[1] > INT32_MAX || q->ne[2] > 65535 || q->ne[3] > 65535)
-        return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: sizes beyond the launch limits");
-    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "flash_attn_ext: null context");
-    FaArgs a;
-    a.q = static_cast<const char*>(q->data);
-    a.k = static_cast<const char*>(k->data);
-    a.v = static_cast<const char*>(v->data);
-    a.dst = static_cast<float*>(dst->data);
-    a.q_nb1 = q->nb[1]; a.q_nb2 = q->nb[2]; a.q_nb3 = q->nb[3];
-    a.k_nb1 = k->nb[1]; a.k_nb2 = k->nb[2]; a.k_nb3 = k->nb[3];
-    a.v_nb1 = v->nb[1]; a.v_nb2 = v->nb[2]; a.v_nb3 = v->nb[3];
-    a.nq = (int)q->ne[1];
-    a.nkv = (int)k->ne[1];
-    a.nh = (int)q->ne[2];
-    a.rk2 = (int)(q->ne[2] / k->ne[2]);
-    a.rv2 = (int)(q->ne[2] / v->ne[2]);
-    const float c = fabsf(scale) * 1.44269504088896340736f;
-    a.c = c > 1e-30f ? c : 1e-30f;  // keeps masked (-inf) scores at weight 0 when scale is 0
-    a.negq = scale < 0.0f;
-    (void)hipSetDevice(ctx->device);
-    Timed tf(ctx, "flash_attn_ext");
-    return hip_check(ctx, tf.done(launch_fattn(a, (int)D, q->type == T_F32, k->type == T_F32, (int)q->ne[3], ctx->stream)),
-                     "flash_attn_ext launch");
+    return mi355::flash_attn_act(ctx, q, k, v, mask, scale, max_bias, logit_softcap, dst, nullptr);
 }
 
 }  // extern "C"

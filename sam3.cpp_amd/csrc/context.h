@@ -53,9 +53,12 @@ int act_mode_for(int weight_type);
 // epilogue replaces the dst store (dst only gives the shape).
 mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const mi355_tensor* dst,
                          const MmqEpi* epi = nullptr);
-// F32 rows x [ne1][ne0] -> the MUL_MAT operand layout o (Q8 / Q8_1 quants +
-// scales, or F16 rows), the activation quantize of mi355_mul_mat.
-mi355_status quantize_act(mi355_context* ctx, const mi355_tensor* x, const ActOut& o);
+// FLASH_ATTN_EXT with the checks of mi355_flash_attn_ext; with op the output
+// goes to the next MUL_MAT's operand (rows b*n_q + iq, K = n_head*D) instead
+// of dst (which still gives the shape).
+mi355_status flash_attn_act(mi355_context* ctx, const mi355_tensor* q, const mi355_tensor* k, const mi355_tensor* v,
+                            const mi355_tensor* mask, float scale, float max_bias, float logit_softcap,
+                            const mi355_tensor* dst, const ActOut* op);
 // mul_mat_act with the fused residual epilogue; dst [M][N] never exists.
 mi355_status mul_mat_epi(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const MmqEpi& e);
 

@@ -219,16 +219,64 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
 
     if (qi < p.nq) {
         const float inv = l_run == 0.0f ? 0.0f : 1.0f / l_run;
-        float* orow = p.dst + (((int64_t)b * p.nq + qi) * p.nh + h) * D;
+        if (p.out.mode == ACT_F32) {
+            float* orow = p.dst + (((int64_t)b * p.nq + qi) * p.nh + h) * D;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+            for (int db = 0; db < NDB; ++db)
 #pragma unroll
-            for (int i4 = 0; i4 < 4; ++i4) {
-                const int d = 32 * db + 8 * i4 + 4 * g;
-                v4f o = {O[db][4 * i4] * inv, O[db][4 * i4 + 1] * inv, O[db][4 * i4 + 2] * inv,
-                         O[db][4 * i4 + 3] * inv};
-                *reinterpret_cast<v4f*>(orow + d) = o;
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    const int d = 32 * db + 8 * i4 + 4 * g;
+                    v4f o = {O[db][4 * i4] * inv, O[db][4 * i4 + 1] * inv, O[db][4 * i4 + 2] * inv,
+                             O[db][4 * i4 + 3] * inv};
+                    *reinterpret_cast<v4f*>(orow + d) = o;
+                }
+        } else {
+            // the projection's operand: row b*nq + qi, columns h*D + d.  Lanes l and
+            // l ^ 32 hold the two halves of each 32-value block (ggml from_float x86:
+            // d = amax/127, q = rint(x * 127/amax)).
+            const ActOut& o = p.out;
+            const int64_t K = (int64_t)p.nh * D, row = (int64_t)b * p.nq + qi;
+            uint16_t* qrow = o.q + row * K + (int64_t)h * D;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                float x[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) x[i] = O[db][i] * inv;
+                float sc = 1.0f;
+                if (o.mode != ACT_F16) {
+                    float amax = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(x[i]));
+                    amax = xmax32(amax);
+                    sc = amax != 0.0f ? 127.0f / amax : 0.0f;
+                    int isum = 0;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        x[i] = rintf(x[i] * sc);
+                        isum += (int)x[i];
+                    }
+                    if (o.mode == ACT_Q8S)
+                        isum += __builtin_amdgcn_ds_bpermute(((int)__lane_id() ^ 32) << 2, isum);
+                    if (g == 0) {
+                        const int64_t blk = ((int64_t)h * D + 32 * db) / 32;
+                        const float dd = amax / 127.0f;
+                        o.d[row * o.dp + blk] = f2h(dd);
+                        if (o.mode == ACT_Q8S) o.s[row * o.dp + blk] = f2h(dd * (float)isum);
+                        if (blk == K / 32 - 1 && o.dp > K / 32) {  // zero the even-pitch padding slot
+                            o.d[row * o.dp + blk + 1] = 0;
+                            if (o.mode == ACT_Q8S) o.s[row * o.dp + blk + 1] = 0;
+                        }
+                    }
+                }
+#pragma unroll
+                for (int i4 = 0; i4 < 4; ++i4) {
+                    const int d = 32 * db + 8 * i4 + 4 * g;
+                    const uint32_t h0 = (uint32_t)f2h(x[4 * i4]) | ((uint32_t)f2h(x[4 * i4 + 1]) << 16);
+                    const uint32_t h1 = (uint32_t)f2h(x[4 * i4 + 2]) | ((uint32_t)f2h(x[4 * i4 + 3]) << 16);
+                    *reinterpret_cast<uint2*>(qrow + d) = make_uint2(h0, h1);
+                }
             }
+        }
     }
 }
 

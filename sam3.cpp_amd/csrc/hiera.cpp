@@ -354,10 +354,14 @@ mi355_status run_block(mi355_context* ctx, const mi355_hiera_hparams* hp, const 
         Timed t(ctx, "hiera_qkv");
         TRY(hip_check(ctx, t.done(launch_hiera_qkv(a, st)), "hiera_qkv launch"));
     }
+    // attention; for quantized / F16 proj weights it writes the projection's operand
+    const int mp = fused_mode(ctx, blk->proj_w, Cout);
     {
         const mi355_tensor q = tensor_on(b.q, T_F16, HD, Nq, NH, nW), k = tensor_on(b.k, T_F16, HD, Nkv, NH, nW),
                            v = tensor_on(b.v, T_F16, HD, Nkv, NH, nW), o = tensor_on(b.att, T_F32, HD, NH, Nq, nW);
-        TRY(mi355_flash_attn_ext(ctx, &q, &k, &v, nullptr, 1.0f / sqrtf((float)HD), 0.0f, 0.0f, &o));
+        const ActOut op = act_out(b.a0, mp, (int64_t)Nq * nW, Cout);
+        TRY(flash_attn_act(ctx, &q, &k, &v, nullptr, 1.0f / sqrtf((float)HD), 0.0f, 0.0f, &o,
+                           mp == ACT_F32 ? nullptr : &op));
     }
     // proj (+ bias, window unpartition with crop, shortcut): fused into the
     // GEMM's epilogue for quantized / F16 weights
@@ -365,16 +369,13 @@ mi355_status run_block(mi355_context* ctx, const mi355_hiera_hparams* hp, const 
         const int64_t Mo = (int64_t)Nq * nW;
         const int wso = ws > 0 ? (bi.qs ? ws / 2 : ws) : 0;
         const int nwh_o = wso > 0 ? cdiv(S2, wso) : 1;
-        const int mp = fused_mode(ctx, blk->proj_w, Cout);
-        const mi355_tensor in = tensor_on(b.att, T_F32, Cout, Mo);
         if (mp == ACT_F32) {
-            const mi355_tensor out = tensor_on(b.p, T_F32, Cout, Mo);
+            const mi355_tensor in = tensor_on(b.att, T_F32, Cout, Mo), out = tensor_on(b.p, T_F32, Cout, Mo);
             TRY(mi355_mul_mat(ctx, &blk->proj_w, &in, &out));
             Timed t(ctx, "hiera_proj_residual");
             TRY(hip_check(ctx, t.done(launch_hiera_proj_residual(x_out, sc, b.p, blk->proj_b, Cout, S2, S2, wso, nwh_o, st)),
                           "proj_residual launch"));
         } else {
-            TRY(quantize_act(ctx, &in, act_out(b.a0, mp, Mo, Cout)));
             MmqEpi e{};
             e.kind = MMQ_EPI_RESIDUAL;
             e.bias = blk->proj_b;

@@ -117,6 +117,8 @@ struct FaArgs {
     int nq, nkv, nh, rk2, rv2;  // rk2 = nh / n_head_k, rv2 = nh / n_head_v
     float c;                    // |scale| * log2(e), at least 1e-30
     int negq;                   // scale < 0: Q enters negated
+    ActOut out;                 // mode ACT_F32: dst; else the next MUL_MAT's operand, rows
+                                // b*nq + iq of K = nh*D (Q8 quants + scales or F16)
 };
 hipError_t launch_fattn(const FaArgs& a, int D, bool qf32, bool kvf32, int B, hipStream_t st);
 

@@ -329,20 +329,21 @@ mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams
     // attention
     TRY(ln_gemm(blk->norm1_w, blk->norm1_b, WS, blk->qkv_w, b.qkv, 3 * E));
     TRY(mi355_vit_qkv_rope(ctx, b.qkv, blk->qkv_b, blk->freqs_cis, b.q, b.k, b.v, M, N, NH, HD));
+    // attention; for quantized / F16 proj weights it writes the projection's operand
+    const int mp = ctx->fuse ? act_mode_for(blk->proj_w.type) : ACT_F32;
     {
         const mi355_tensor q = dev_tensor(b.q, T_F16, HD, N, NH, B), k = dev_tensor(b.k, T_F16, HD, N, NH, B),
                            v = dev_tensor(b.v, T_F16, HD, N, NH, B), o = dev_tensor(b.attn, T_F32, HD, NH, N, B);
-        TRY(mi355_flash_attn_ext(ctx, &q, &k, &v, nullptr, 1.0f / sqrtf((float)HD), 0.0f, 0.0f, &o));
+        const ActOut op = act_out(b, mp, E);
+        TRY(flash_attn_act(ctx, &q, &k, &v, nullptr, 1.0f / sqrtf((float)HD), 0.0f, 0.0f, &o,
+                           mp == ACT_F32 ? nullptr : &op));
     }
     // proj (+ bias, window unpartition, residual: fused into the GEMM's epilogue)
-    const int mp = ctx->fuse ? act_mode_for(blk->proj_w.type) : ACT_F32;
     if (mp == ACT_F32) {
         const mi355_tensor in = dev_tensor(b.attn, T_F32, E, M), out = dev_tensor(b.xn, T_F32, E, M);
         TRY(mi355_mul_mat(ctx, &blk->proj_w, &in, &out));
         TRY(mi355_vit_proj_residual(ctx, x, b.xn, blk->proj_b, M, E, G, WS));
     } else {
-        const mi355_tensor in = dev_tensor(b.attn, T_F32, E, M);
-        TRY(quantize_act(ctx, &in, act_out(b, mp, E)));
         MmqEpi e{};
         e.kind = MMQ_EPI_RESIDUAL;
         e.bias = blk->proj_b;
