@@ -230,7 +230,7 @@ mi355_status mul_mat_epi(mi355_context* ctx, const mi355_tensor* s0, const ActF1
     d.nb[0] = 4;
     d.nb[1] = 4 * d.ne[0];
     d.nb[2] = d.nb[3] = d.nb[1] * a.M;
-    d.data = e.out;
+    d.data = e.kind == MMQ_EPI_RESIDUAL ? static_cast<void*>(e.out) : static_cast<void*>(e.q);
     return mul_mat_act(ctx, s0, a, &d, &e);
 }
 
@@ -261,12 +261,12 @@ mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF1
         st = ensure_ws(ctx, align);
         if (st != MI355_STATUS_SUCCESS) return st;
     }
-    static const char* names[4][2] = {{"mmq_f16", "mmq_f16+residual"},
-                                      {"mmq_q8_0", "mmq_q8_0+residual"},
-                                      {"mmq_q4_0", "mmq_q4_0+residual"},
-                                      {"mmq_q4_1", "mmq_q4_1+residual"}};
+    static const char* names[4][3] = {{"mmq_f16", "mmq_f16+residual", "mmq_f16+qkv"},
+                                      {"mmq_q8_0", "mmq_q8_0+residual", "mmq_q8_0+qkv"},
+                                      {"mmq_q4_0", "mmq_q4_0+residual", "mmq_q4_0+qkv"},
+                                      {"mmq_q4_1", "mmq_q4_1+residual", "mmq_q4_1+qkv"}};
     const int ti = s0->type == T_F16 ? 0 : s0->type == T_Q8_0 ? 1 : s0->type == T_Q4_0 ? 2 : 3;
-    Timed tq(ctx, names[ti][epi ? 1 : 0]);
+    Timed tq(ctx, names[ti][epi ? epi->kind : 0]);
     if (epi)
         return hip_check(ctx, tq.done(launch_mmq_epi(matw_of(s0), a, N, *epi, align ? ctx->ws : nullptr, ctx->stream)),
                          "mmq launch");

@@ -204,6 +204,15 @@ __device__ __forceinline__ float gelu_tanh_table(float u) {
     return h2f(f2h(hv * (1.0f + tanhf(inner))));
 }
 
+// sam3_apply_rope on one (x[2i], x[2i+1]) pair: the complex product with
+// (cos, sin), each product rounded to fp32 before the add / subtract
+__device__ __forceinline__ void rope_pair(float& x0, float& x1, float c, float s) {
+#pragma clang fp contract(off)
+    const float a = x0 * c, b = x1 * s, cc = x0 * s, d = x1 * c;
+    x0 = a - b;
+    x1 = cc + d;
+}
+
 // SAM2 window order (sam2_window_partition over the zero-padded grid: window
 // n = wh + nwh*ww, token lh*ws + lw inside it) row r -> image token h*W + w,
 // or -1 for a padding token

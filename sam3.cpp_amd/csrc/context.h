@@ -59,7 +59,8 @@ mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF1
 mi355_status flash_attn_act(mi355_context* ctx, const mi355_tensor* q, const mi355_tensor* k, const mi355_tensor* v,
                             const mi355_tensor* mask, float scale, float max_bias, float logit_softcap,
                             const mi355_tensor* dst, const ActOut* op);
-// mul_mat_act with the fused residual epilogue; dst [M][N] never exists.
+// mul_mat_act with a fused epilogue (residual or qkv split); dst [M][N] never
+// exists.
 mi355_status mul_mat_epi(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const MmqEpi& e);
 
 // Brackets one launch with events when timing is enabled.

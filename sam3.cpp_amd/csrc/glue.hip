@@ -131,12 +131,8 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(const QkvArgs a) {
     const float v0 = row[2 * E + e] + a.bias[2 * E + e], v1 = row[2 * E + e + 1] + a.bias[2 * E + e + 1];
     if (a.rope) {
         const float c = a.rope[n * a.HD + 2 * i], s = a.rope[n * a.HD + 2 * i + 1];
-        const float qa = q0 * c, qb = q1 * s, qc = q0 * s, qd = q1 * c;
-        const float ka = k0 * c, kb = k1 * s, kc = k0 * s, kd = k1 * c;
-        q0 = qa - qb;
-        q1 = qc + qd;
-        k0 = ka - kb;
-        k1 = kc + kd;
+        rope_pair(q0, q1, c, s);
+        rope_pair(k0, k1, c, s);
     }
     const int64_t o = ((bwin * a.NH + h) * a.N + n) * a.HD + 2 * i;
     *reinterpret_cast<uint32_t*>(a.q + o) = (uint32_t)f2h(q0) | ((uint32_t)f2h(q1) << 16);

@@ -88,16 +88,22 @@ struct RowMap {
     int nwh;    // SAM2: windows along H of the padded grid
 };
 
-// Fused MUL_MAT epilogue (one 2-D GEMM, dst [M][N] never written; N % 4 == 0):
+// Fused MUL_MAT epilogues (one 2-D GEMM, dst [M][N] never written; N % 4 == 0):
 //   MMQ_EPI_RESIDUAL  out[map(m)][n] = res[map(m)][n] + (dst[m][n] + bias[n]),
 //                     rows with map(m) = -1 dropped
-enum { MMQ_EPI_STORE = 0, MMQ_EPI_RESIDUAL = 1 };
+//   MMQ_EPI_QKV       the ViT qkv split: u = dst + bias over N = 3E columns
+//                     [q | k | v], RoPE on q and k (rope non-null), fp16 out to
+//                     q/k/v [M/ntok][nh][ntok][hd] (the qkv_rope pass)
+enum { MMQ_EPI_STORE = 0, MMQ_EPI_RESIDUAL = 1, MMQ_EPI_QKV = 2 };
 struct MmqEpi {
     int kind;
     const float* bias;  // [N]
     const float* res;   // [rows][N] (may be out)
     float* out;         // [rows][N]
     RowMap map;
+    const float* rope;  // [ntok][hd/2][2] (cos, sin) or null
+    _Float16 *q, *k, *v;
+    int ntok, nh, hd;
 };
 hipError_t launch_mmq_epi(const MatW& w, const ActF16& a, int64_t N, const MmqEpi& e, void* align_buf,
                           hipStream_t st);

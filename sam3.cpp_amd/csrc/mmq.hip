@@ -406,10 +406,10 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
             }
         return;
     }
-    // The residual epilogue goes through LDS: the 128 x 128 result tile, 64
-    // rows at a time (32 in st0, 32 in st1), is rewritten row-major so that
-    // each thread then owns 4 consecutive columns (float4 loads and stores).
-    // out = res + (dst + bias), each add rounded to fp32 as ggml's ADD nodes.
+    // The fused epilogues go through LDS: the 128 x 128 result tile, 64 rows
+    // at a time (32 in st0, 32 in st1), is rewritten row-major so that each
+    // thread then owns 4 consecutive columns (float4 loads and stores).
+    // u = dst + bias, each add rounded to fp32 as ggml's ADD nodes.
     constexpr int TP = BN + 4;                // row pitch (floats)
     constexpr int CPR = BN / 4;               // float4 chunks per row
     constexpr int IT = 64 * CPR / NT;         // rows per thread per half
@@ -429,7 +429,26 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
             t1[r * TP + wrow] = acc[2 * half + 1][i];
         }
         __syncthreads();
-        {
+        if (EPI == MMQ_EPI_QKV) {
+            const int E = e.nh * e.hd, which = nc / E, col = nc - which * E, hh = col / e.hd, d = col - hh * e.hd;
+            _Float16* dst = which == 0 ? e.q : which == 1 ? e.k : e.v;
+#pragma unroll
+            for (int it = 0; it < IT; ++it) {
+                const int r = it * (NT / CPR) + tid / CPR, m = m0 + half * 64 + r;
+                if (m >= M || !cv) continue;
+                const v4f uv = *reinterpret_cast<const v4f*>(&(it < IT / 2 ? t0 : t1)[(r & 31) * TP + 4 * c]) + bv;
+                float u0 = uv[0], u1 = uv[1], u2 = uv[2], u3 = uv[3];
+                const int bw = m / e.ntok, n = m - bw * e.ntok;
+                if (which < 2 && e.rope) {
+                    const v4f cs = *reinterpret_cast<const v4f*>(&e.rope[(int64_t)n * e.hd + d]);
+                    rope_pair(u0, u1, cs[0], cs[1]);
+                    rope_pair(u2, u3, cs[2], cs[3]);
+                }
+                const uint32_t h0 = (uint32_t)f2h(u0) | ((uint32_t)f2h(u1) << 16);
+                const uint32_t h1 = (uint32_t)f2h(u2) | ((uint32_t)f2h(u3) << 16);
+                *reinterpret_cast<uint2*>(&dst[(((int64_t)bw * e.nh + hh) * e.ntok + n) * e.hd + d]) = make_uint2(h0, h1);
+            }
+        } else {
             // residual loads of four rows first, then their stores (res may be out)
 #pragma unroll
             for (int i0 = 0; i0 < IT; i0 += 4) {
@@ -472,7 +491,8 @@ static void launch_t(const MmqArgs& a, int Z, bool dots, const MmqEpi* e, hipStr
     MmqEpi none{};
     if (dots) mmq_kernel<WT, true, MMQ_EPI_STORE><<<grid, NT, 0, st>>>(a, none);
     else if (!e || e->kind == MMQ_EPI_STORE) mmq_kernel<WT, false, MMQ_EPI_STORE><<<grid, NT, 0, st>>>(a, none);
-    else mmq_kernel<WT, false, MMQ_EPI_RESIDUAL><<<grid, NT, 0, st>>>(a, *e);
+    else if (e->kind == MMQ_EPI_RESIDUAL) mmq_kernel<WT, false, MMQ_EPI_RESIDUAL><<<grid, NT, 0, st>>>(a, *e);
+    else mmq_kernel<WT, false, MMQ_EPI_QKV><<<grid, NT, 0, st>>>(a, *e);
 }
 
 
@@ -552,7 +572,16 @@ hipError_t launch_mmq(const MatW& w, const ActF16& a, const MatD& d, int64_t N, 
 
 hipError_t launch_mmq_epi(const MatW& w, const ActF16& a, int64_t N, const MmqEpi& e, void* align_buf,
                           hipStream_t st) {
-    if (e.kind != MMQ_EPI_RESIDUAL || !e.bias || !e.res || !e.out || N % 4 != 0) return hipErrorInvalidValue;
+    if (!e.bias || N % 4 != 0) return hipErrorInvalidValue;
+    if (e.kind == MMQ_EPI_RESIDUAL) {
+        if (!e.res || !e.out) return hipErrorInvalidValue;
+    } else if (e.kind == MMQ_EPI_QKV) {
+        if (!e.q || !e.k || !e.v || e.ntok <= 0 || e.nh <= 0 || e.hd <= 0 || e.hd % 4 != 0 || N != 3LL * e.nh * e.hd ||
+            a.M % e.ntok != 0)
+            return hipErrorInvalidValue;
+    } else {
+        return hipErrorInvalidValue;
+    }
     const MatD none{nullptr, 0, 0, 0};
     return run_mmq(w, a, none, N, 1, 1, nullptr, &e, align_buf, st);
 }

@@ -297,9 +297,10 @@ mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams
         if (st != MI355_STATUS_SUCCESS) return st; \
     } while (0)
     // LN -> the GEMM's activation operand (fused) or F32 rows
-    auto ln_gemm = [&](const float* w, const float* bb, int ws, const mi355_tensor& W, float* out,
-                       int64_t N) -> mi355_status {
+    auto ln_gemm = [&](const float* w, const float* bb, int ws, const mi355_tensor& W, float* out, int64_t N,
+                       const MmqEpi* epi) -> mi355_status {
         const int mode = ctx->fuse ? act_mode_for(W.type) : ACT_F32;
+        if (mode == ACT_F32 && epi) return fail(ctx, MI355_STATUS_FAILED, "vit: epilogue without a fused operand");
         if (mode == ACT_F32) {
             mi355_status s1 = mi355_vit_layer_norm(ctx, x, nullptr, 0, w, bb, b.xn, M, E, G, ws, hp->eps);
             if (s1 != MI355_STATUS_SUCCESS) return s1;
@@ -323,12 +324,28 @@ mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams
             mi355_status s1 = hip_check(ctx, t.done(launch_layer_norm(a, ctx->stream)), "layer_norm launch");
             if (s1 != MI355_STATUS_SUCCESS) return s1;
         }
+        if (epi) return mul_mat_epi(ctx, &W, act_in(b, mode, M, E), *epi);
         const mi355_tensor o = dev_tensor(out, T_F32, N, M);
         return mul_mat_act(ctx, &W, act_in(b, mode, M, E), &o);
     };
     // attention
-    TRY(ln_gemm(blk->norm1_w, blk->norm1_b, WS, blk->qkv_w, b.qkv, 3 * E));
-    TRY(mi355_vit_qkv_rope(ctx, b.qkv, blk->qkv_b, blk->freqs_cis, b.q, b.k, b.v, M, N, NH, HD));
+    // LN1 -> qkv (+ bias, q/k/v split, RoPE, fp16: fused epilogue)
+    if (ctx->fuse && act_mode_for(blk->qkv_w.type) != ACT_F32) {
+        MmqEpi e{};
+        e.kind = MMQ_EPI_QKV;
+        e.bias = blk->qkv_b;
+        e.rope = blk->freqs_cis;
+        e.q = b.q;
+        e.k = b.k;
+        e.v = b.v;
+        e.ntok = N;
+        e.nh = NH;
+        e.hd = HD;
+        TRY(ln_gemm(blk->norm1_w, blk->norm1_b, WS, blk->qkv_w, nullptr, 3 * E, &e));
+    } else {
+        TRY(ln_gemm(blk->norm1_w, blk->norm1_b, WS, blk->qkv_w, b.qkv, 3 * E, nullptr));
+        TRY(mi355_vit_qkv_rope(ctx, b.qkv, blk->qkv_b, blk->freqs_cis, b.q, b.k, b.v, M, N, NH, HD));
+    }
     // attention; for quantized / F16 proj weights it writes the projection's operand
     const int mp = ctx->fuse ? act_mode_for(blk->proj_w.type) : ACT_F32;
     {
@@ -354,7 +371,7 @@ mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams
     }
     // MLP: fc1, bias + GELU writing fc2's operand, fc2 (+ bias, residual: fused epilogue)
     const int m2 = ctx->fuse && MLP % 32 == 0 ? act_mode_for(blk->fc2_w.type) : ACT_F32;
-    TRY(ln_gemm(blk->norm2_w, blk->norm2_b, 0, blk->fc1_w, b.big, MLP));
+    TRY(ln_gemm(blk->norm2_w, blk->norm2_b, 0, blk->fc1_w, b.big, MLP, nullptr));
     if (m2 == ACT_F32) {
         TRY(mi355_vit_bias_gelu(ctx, b.big, blk->fc1_b, M, MLP));
     } else {
