@@ -114,15 +114,27 @@ bool f16_src1_direct(const mi355_tensor* s1) {
 // Workspace carve-up of one mul_mat: activation operand (fp16 quants or an
 // F16 copy of src1) | scales | Q8_1 sums | 4-byte-pitch weight copy (only
 // for weight rows that are not 4-byte aligned).
+// Workspace of one MUL_MAT: activation operand (q, d, s), the 4-byte-pitch
+// weight copy, then the split-K partial sums.
 struct MmPlan {
-    size_t q = 0, d = 0, s = 0, align = 0;
-    size_t total() const { return q + d + s + align; }
+    size_t q = 0, d = 0, s = 0, align = 0, part = 0;
+    int ks = 1;
+    size_t total() const { return q + d + s + align + part; }
 };
 
-MmPlan mm_plan(const mi355_tensor* s0, const mi355_tensor* s1) {
+int device_cus(int device) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
+    return n;
+}
+
+// split = false: the caller's dst cannot take the float4 stores of the split reduction
+MmPlan mm_plan(const mi355_tensor* s0, const mi355_tensor* s1, int cus, bool split = true) {
     MmPlan pl;
     if (s0->type == T_F32) return pl;
     const int64_t K = s1->ne[0], M = s1->ne[1], Z = s1->ne[2] * s1->ne[3];
+    if (split) pl.ks = mmq_ksplit(s0->type, M, s0->ne[1], K, Z, cus);
+    if (pl.ks > 1) pl.part = align_up((size_t)pl.ks * (size_t)M * (size_t)s0->ne[1] * 4);
     if (s0->type == T_F16) {
         if (!f16_src1_direct(s1)) pl.q = align_up((size_t)(Z * M * K) * 2);
         return pl;
@@ -132,6 +144,10 @@ MmPlan mm_plan(const mi355_tensor* s0, const mi355_tensor* s1) {
     if (s0->type == T_Q4_1) pl.s = pl.d;
     pl.align = align_up(mmq_align_bytes(matw_of(s0), s0->ne[1], K));
     return pl;
+}
+
+bool dst_split_ok(const mi355_tensor* d) {
+    return d->nb[1] % 16 == 0 && (reinterpret_cast<uintptr_t>(d->data) & 15) == 0;
 }
 mi355_status ensure_ws(mi355_context* ctx, size_t bytes) { return ensure_buffer(ctx, &ctx->ws, &ctx->ws_size, bytes); }
 
@@ -257,10 +273,13 @@ mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF1
     (void)hipSetDevice(ctx->device);
     const int64_t N = s0->ne[1];
     const size_t align = align_up(mmq_align_bytes(matw_of(s0), N, a.K));
-    if (align) {
-        st = ensure_ws(ctx, align);
+    const int ks = epi || dst_split_ok(d) ? mmq_ksplit(s0->type, a.M, N, a.K, 1, ctx->cus) : 1;
+    const size_t part = ks > 1 ? align_up((size_t)ks * (size_t)a.M * (size_t)N * 4) : 0;
+    if (align + part) {
+        st = ensure_ws(ctx, align + part);
         if (st != MI355_STATUS_SUCCESS) return st;
     }
+    const MmqSplit sp{ks, ks > 1 ? reinterpret_cast<float*>(static_cast<char*>(ctx->ws) + align) : nullptr};
     static const char* names[4][3] = {{"mmq_f16", "mmq_f16+residual", "mmq_f16+qkv"},
                                       {"mmq_q8_0", "mmq_q8_0+residual", "mmq_q8_0+qkv"},
                                       {"mmq_q4_0", "mmq_q4_0+residual", "mmq_q4_0+qkv"},
@@ -268,10 +287,11 @@ mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF1
     const int ti = s0->type == T_F16 ? 0 : s0->type == T_Q8_0 ? 1 : s0->type == T_Q4_0 ? 2 : 3;
     Timed tq(ctx, names[ti][epi ? epi->kind : 0]);
     if (epi)
-        return hip_check(ctx, tq.done(launch_mmq_epi(matw_of(s0), a, N, *epi, align ? ctx->ws : nullptr, ctx->stream)),
+        return hip_check(ctx, tq.done(launch_mmq_epi(matw_of(s0), a, N, *epi, align ? ctx->ws : nullptr, sp,
+                                                     ctx->stream)),
                          "mmq launch");
     return hip_check(ctx, tq.done(launch_mmq(matw_of(s0), a, matd_of(d), N, 1, 1, nullptr, align ? ctx->ws : nullptr,
-                                             ctx->stream)),
+                                             sp, ctx->stream)),
                      "mmq launch");
 }
 
@@ -375,6 +395,7 @@ mi355_status mi355_context_create(int device, void* stream, mi355_context** out)
     mi355_context* ctx = new mi355_context();
     ctx->device = device;
     ctx->stream = static_cast<hipStream_t>(stream);  // NULL: the device's default stream
+    ctx->cus = device_cus(device);
     *out = ctx;
     return MI355_STATUS_SUCCESS;
 }
@@ -405,7 +426,9 @@ size_t mi355_mul_mat_workspace_size(const mi355_tensor* s0, const mi355_tensor* 
     if (!s0 || !s1) return 0;
     if (s0->type != T_F32 && s0->type != T_F16 && s0->type != T_Q8_0 && s0->type != T_Q4_0 && s0->type != T_Q4_1)
         return 0;
-    return mm_plan(s0, s1).total();
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    return mm_plan(s0, s1, device_cus(dev)).total();
 }
 
 int mi355_supports_mul_mat(const mi355_tensor* s0, const mi355_tensor* s1, const mi355_tensor* d) {
@@ -435,7 +458,7 @@ mi355_status mi355_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
         Timed tg(ctx, "gemm_f32");
         return hip_check(ctx, tg.done(launch_gemm_f32(g, (int)(s1->ne[2] * s1->ne[3]), ctx->stream)), "gemm_f32 launch");
     }
-    const MmPlan pl = mm_plan(s0, s1);
+    const MmPlan pl = mm_plan(s0, s1, ctx->cus, dst_split_ok(d));
     st = ensure_ws(ctx, pl.total());
     if (st != MI355_STATUS_SUCCESS) return st;
     ActF16 a;
@@ -464,10 +487,13 @@ mi355_status mi355_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
         if (st != MI355_STATUS_SUCCESS) return st;
     }
     void* align_buf = pl.align ? static_cast<char*>(ctx->ws) + pl.q + pl.d + pl.s : nullptr;
+    const MmqSplit sp{pl.ks, pl.ks > 1 ? reinterpret_cast<float*>(static_cast<char*>(ctx->ws) + pl.q + pl.d + pl.s +
+                                                                  pl.align)
+                                       : nullptr};
     const char* kname = s0->type == T_F16 ? "mmq_f16" : s0->type == T_Q8_0 ? "mmq_q8_0" : s0->type == T_Q4_0 ? "mmq_q4_0" : "mmq_q4_1";
     Timed tq(ctx, kname);
     return hip_check(ctx, tq.done(launch_mmq(matw_of(s0), a, matd_of(d), N, s1->ne[2], s1->ne[3], nullptr, align_buf,
-                                             ctx->stream)),
+                                             sp, ctx->stream)),
                      "mmq launch");
 }
 
@@ -491,7 +517,7 @@ mi355_status mi355_mul_mat_block_dots(mi355_context* ctx, const mi355_tensor* s0
     if (st != MI355_STATUS_SUCCESS) return st;
     if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "block_dots: null context");
     (void)hipSetDevice(ctx->device);
-    const MmPlan pl = mm_plan(s0, s1);
+    const MmPlan pl = mm_plan(s0, s1, ctx->cus, false);
     st = ensure_ws(ctx, pl.total());
     if (st != MI355_STATUS_SUCCESS) return st;
     ActF16 a;
@@ -499,7 +525,7 @@ mi355_status mi355_mul_mat_block_dots(mi355_context* ctx, const mi355_tensor* s0
     if (st != MI355_STATUS_SUCCESS) return st;
     void* align_buf = pl.align ? static_cast<char*>(ctx->ws) + pl.q + pl.d + pl.s : nullptr;
     return hip_check(ctx, launch_mmq(matw_of(s0), a, matd_of(&d), s0->ne[1], s1->ne[2], s1->ne[3], isums, align_buf,
-                                     ctx->stream),
+                                     MmqSplit{1, nullptr}, ctx->stream),
                      "mmq(dots) launch");
 }
 

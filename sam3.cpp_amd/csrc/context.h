@@ -13,6 +13,7 @@
 
 struct mi355_context {
     int device = 0;
+    int cus = 0;               // compute units of the device (split-K sizing)
     hipStream_t stream = nullptr;
     void* ws = nullptr;        // per-call scratch of mul_mat (activation operand, scales)
     size_t ws_size = 0;

@@ -74,8 +74,17 @@ struct MatD {  // dst F32
 // activations) or F16 (A = F16 activations); ne12/ne13 batch dims.  With
 // dots != nullptr (block types only) the kernel writes the exact per-block
 // int32 dots [z][m][n][b] instead of dst.
+// K split (split-K) of a 2-D GEMM: ks partial sums of [M][N] f32 in part
+// (ks * M * N * 4 bytes), added in split order by a reduction that also runs
+// the epilogue.  ks = 1: no split.
+struct MmqSplit {
+    int ks;
+    float* part;
+};
+// The split mmq_ksplit picks for a GEMM on a GPU with cus compute units.
+int mmq_ksplit(int type, int64_t M, int64_t N, int64_t K, int64_t Z, int cus);
 hipError_t launch_mmq(const MatW& w, const ActF16& a, const MatD& d, int64_t N, int64_t ne12, int64_t ne13,
-                      int32_t* dots, void* align_buf, hipStream_t st);
+                      int32_t* dots, void* align_buf, const MmqSplit& sp, hipStream_t st);
 // Bytes of the 4-byte-pitch weight copy launch_mmq needs (0 when rows are aligned).
 size_t mmq_align_bytes(const MatW& w, int64_t N, int64_t K);
 
@@ -106,7 +115,7 @@ struct MmqEpi {
     int ntok, nh, hd;
 };
 hipError_t launch_mmq_epi(const MatW& w, const ActF16& a, int64_t N, const MmqEpi& e, void* align_buf,
-                          hipStream_t st);
+                          const MmqSplit& sp, hipStream_t st);
 
 // Row softmax of scale*x (F32, strided rows) into dst (F32, strided rows).
 hipError_t launch_soft_max(const SrcView& src, float scale, char* dst, const int64_t dnb[4], hipStream_t st);

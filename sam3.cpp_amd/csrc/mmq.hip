@@ -106,6 +106,8 @@ struct MmqArgs {
     int64_t d_nb1, d_nb2, d_nb3;
     int32_t* dots;             // block-dot inspection output (or null)
     int M, dp, N, K, ne12, r2, r3, tiles_m, tiles_n;  // dp: row pitch (halves) of the scale arrays
+    int ksplit, sps;           // K split into ksplit ranges of sps stages; partial sums go to
+    int64_t d_split;           // D + split * d_split (bytes), summed by mmq_reduce_kernel
 };
 
 // 8 consecutive int8 quants (two dwords) -> 8 fp16 (one MFMA k-chunk).
@@ -200,23 +202,31 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
     __shared__ __attribute__((aligned(16))) St st2;
 
     // XCD-aware tile order: workgroup id -> (xcd, slot) -> contiguous tile band per XCD
-    const int T = p.tiles_m * p.tiles_n;
-    const int per_xcd = (T + 7) / 8;
-    const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    if (t >= T) return;
+    // (a K split's ranges of one tile are adjacent, so they share an XCD)
+    const int TT = p.tiles_m * p.tiles_n * p.ksplit;
+    const int per_xcd = (TT + 7) / 8;
+    const int tl = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tl >= TT) return;
+    const int t = tl / p.ksplit, split = tl - t * p.ksplit;
     const int m0 = (t / p.tiles_n) * BM, n0 = (t % p.tiles_n) * BN;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wn = __builtin_amdgcn_readfirstlane(tid >> 6);  // wavefront index (uniform)
     const int z = blockIdx.y, i12 = z % p.ne12, i13 = z / p.ne12;
-    const int M = p.M, N = p.N, K = p.K;
+    // a K split computes a plain GEMM over its range k0s .. k0s + K: shifted
+    // operand bases, the same kernel code
+    const int k0s = split * p.sps * SKH;
+    const int M = p.M, N = p.N, K = min(p.K - k0s, p.sps * SKH);
     const int nb = K / QK;
     const int nstage = QUANT ? (nb + BKB - 1) / BKB : (K + SKH - 1) / SKH;
-    const uint8_t* Wz = p.W + (int64_t)(i12 / p.r2) * p.w_nb2 + (int64_t)(i13 / p.r3) * p.w_nb3;
-    const _Float16* Az = p.A + (int64_t)i12 * p.a_s2 + (int64_t)i13 * p.a_s3;
+    const int64_t wsh = QUANT ? (int64_t)(k0s / QK) * WB : 2LL * k0s;  // weight bytes skipped per row
+    const uint8_t* Wz = p.W + (int64_t)(i12 / p.r2) * p.w_nb2 + (int64_t)(i13 / p.r3) * p.w_nb3 + wsh;
+    const int64_t w_extent = p.w_extent - wsh, a_extent = p.a_extent - 2LL * k0s;
+    const _Float16* Az = p.A + (int64_t)i12 * p.a_s2 + (int64_t)i13 * p.a_s3 + k0s;
     const int dp = p.dp;
-    const _Float16* Adz = QUANT ? p.Ad + (int64_t)z * M * dp : nullptr;
-    const _Float16* Asz = WT == T_Q4_1 ? p.As + (int64_t)z * M * dp : nullptr;
+    const int64_t sc_extent = 2LL * M * dp - 2LL * (k0s / QK);
+    const _Float16* Adz = QUANT ? p.Ad + (int64_t)z * M * dp + k0s / QK : nullptr;
+    const _Float16* Asz = WT == T_Q4_1 ? p.As + (int64_t)z * M * dp + k0s / QK : nullptr;
     // wavefronts 0, 1 load the two blocks' d; for Q4_1, 2 and 3 load the two blocks' s
     const bool xload = QUANT && (wn < 2 || WT == T_Q4_1);
 
@@ -242,13 +252,13 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
     auto dma_stage = [&](int s, St& b) {
         const int k0 = s * SKH;
         const bool tail = k0 + SKH > K;  // chunks past K must read zeros (rows continue in memory)
-        const auto ar = make_rsrc(Az + k0, p.a_extent - 2LL * k0);
+        const auto ar = make_rsrc(Az + k0, a_extent - 2LL * k0);
 #pragma unroll
         for (int i = 0; i < NI; ++i)
             dma_b128(ar, &b.A[(wn * NI + i) * RPI * SKH], tail && k0 + tch[i] * 8 >= K ? OOB : aoff[i]);
         if (QUANT) {
             const int64_t seg = (int64_t)s * BKB * WB;
-            const auto wrs = make_rsrc(Wz + seg, p.w_extent - seg);
+            const auto wrs = make_rsrc(Wz + seg, w_extent - seg);
 #pragma unroll
             for (int i = 0; i < RLD; ++i)
                 dma_b32(wrs, &b.W[NT * i + 64 * wn], woff[i]);
@@ -256,12 +266,12 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
             const int sr_ = 64 * (wn & 1) + lane;
             const int soff = m0 + sr_ < M ? ((m0 + sr_) * dp + s * BKB) * 2 : OOB;
             if (wn < 2) {
-                dma_b32(make_rsrc(Adz, 2LL * M * dp), &b.Ad[64 * (wn & 1)][0], soff);
+                dma_b32(make_rsrc(Adz, sc_extent), &b.Ad[64 * (wn & 1)][0], soff);
             } else if (WT == T_Q4_1) {
-                dma_b32(make_rsrc(Asz, 2LL * M * dp), &b.As[WT == T_Q4_1 ? 64 * (wn & 1) : 0][0], soff);
+                dma_b32(make_rsrc(Asz, sc_extent), &b.As[WT == T_Q4_1 ? 64 * (wn & 1) : 0][0], soff);
             }
         } else {
-            const auto fr = make_rsrc(Wz + 2LL * k0, p.w_extent - 2LL * k0);
+            const auto fr = make_rsrc(Wz + 2LL * k0, w_extent - 2LL * k0);
 #pragma unroll
             for (int i = 0; i < NI; ++i)
                 dma_b128(fr, &b.Bf[(wn * NI + i) * RPI * SKH], tail && k0 + tch[i] * 8 >= K ? OOB : foff[i]);
@@ -396,7 +406,7 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
 
     const int n = n0 + wrow;
     if (EPI == MMQ_EPI_STORE) {
-        char* Dz = reinterpret_cast<char*>(p.D) + (int64_t)i12 * p.d_nb2 + (int64_t)i13 * p.d_nb3;
+        char* Dz = reinterpret_cast<char*>(p.D) + (int64_t)i12 * p.d_nb2 + (int64_t)i13 * p.d_nb3 + split * p.d_split;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -484,8 +494,53 @@ __global__ __launch_bounds__(256) void align_rows_kernel(const uint8_t* __restri
     for (int i = threadIdx.x; i < pitch_halves; i += blockDim.x) dst[r * pitch_halves + i] = i < row_halves ? s[i] : 0;
 }
 
+// Split-K: dst rows (or the fused epilogue) from the ksplit partial sums,
+// added in split order; one thread per 4 columns (N % 4 == 0).
+template <int EPI>
+__global__ __launch_bounds__(256) void mmq_reduce_kernel(const float* __restrict__ part, int ksplit, int M, int N,
+                                                         char* __restrict__ D, int64_t d_nb1, const MmqEpi e) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int n4 = N / 4;
+    if (t >= (int64_t)M * n4) return;
+    const int m = (int)(t / n4), nc = (int)(t - (int64_t)m * n4) * 4;
+    const int64_t mn = (int64_t)M * N;
+    v4f f = *reinterpret_cast<const v4f*>(&part[(int64_t)m * N + nc]);
+    for (int s = 1; s < ksplit; ++s) f = f + *reinterpret_cast<const v4f*>(&part[s * mn + (int64_t)m * N + nc]);
+    if (EPI == MMQ_EPI_STORE) {
+        *reinterpret_cast<v4f*>(D + (int64_t)m * d_nb1 + (int64_t)nc * 4) = f;
+        return;
+    }
+    const v4f u = f + *reinterpret_cast<const v4f*>(&e.bias[nc]);
+    if (EPI == MMQ_EPI_RESIDUAL) {
+        const int rr = map_row32(e.map, m);
+        if (rr >= 0) {
+            const v4f x = *reinterpret_cast<const v4f*>(&e.res[(int64_t)rr * N + nc]);
+            *reinterpret_cast<v4f*>(&e.out[(int64_t)rr * N + nc]) = x + u;
+        }
+    } else {
+        const int E = e.nh * e.hd, which = nc / E, col = nc - which * E, hh = col / e.hd, d = col - hh * e.hd;
+        _Float16* dst = which == 0 ? e.q : which == 1 ? e.k : e.v;
+        float u0 = u[0], u1 = u[1], u2 = u[2], u3 = u[3];
+        const int bw = m / e.ntok, n = m - bw * e.ntok;
+        if (which < 2 && e.rope) {
+            const v4f cs = *reinterpret_cast<const v4f*>(&e.rope[(int64_t)n * e.hd + d]);
+            rope_pair(u0, u1, cs[0], cs[1]);
+            rope_pair(u2, u3, cs[2], cs[3]);
+        }
+        const uint32_t h0 = (uint32_t)f2h(u0) | ((uint32_t)f2h(u1) << 16);
+        const uint32_t h1 = (uint32_t)f2h(u2) | ((uint32_t)f2h(u3) << 16);
+        *reinterpret_cast<uint2*>(&dst[(((int64_t)bw * e.nh + hh) * e.ntok + n) * e.hd + d]) = make_uint2(h0, h1);
+    }
+}
+
 template <int WT>
 static void launch_t(const MmqArgs& a, int Z, bool dots, const MmqEpi* e, hipStream_t st) {
+    if (a.ksplit > 1) {  // partial sums (STORE into the split buffer), then the reduction with the epilogue
+        const int TT = a.tiles_m * a.tiles_n * a.ksplit;
+        MmqEpi none{};
+        mmq_kernel<WT, false, MMQ_EPI_STORE><<<dim3((unsigned)(((TT + 7) / 8) * 8)), NT, 0, st>>>(a, none);
+        return;
+    }
     const int T = a.tiles_m * a.tiles_n;
     const dim3 grid((unsigned)(((T + 7) / 8) * 8), (unsigned)Z);
     MmqEpi none{};
@@ -508,8 +563,33 @@ size_t mmq_align_bytes(const MatW& w, int64_t N, int64_t K) {
     return a4 ? 0 : (size_t)(N * w.ne2 * w.ne3) * (size_t)((rowb + 3) & ~3);
 }
 
+// K split for GEMMs with too few output tiles to fill the GPU: the fewest
+// (rounds of workgroups x stages per split) plus the partial-sum traffic
+// (written by the GEMM, read by the reduction at ~4 TB/s) and a launch.
+int mmq_ksplit(int type, int64_t M, int64_t N, int64_t K, int64_t Z, int cus) {
+    if (Z != 1 || N % 4 != 0 || cus <= 0) return 1;
+    const bool quant = type != T_F16;
+    const int64_t T = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    const int64_t nstage = quant ? ((K / QK) + BKB - 1) / BKB : (K + 31) / 32;
+    const int64_t slots = (int64_t)cus * (quant ? 2 : 3);
+    const double t_stage = quant ? 2.0 : 0.85;           // us per stage of one round of workgroups
+    const double unit = (double)M * N * 4 / 4.0e6;       // us to move one M x N f32 array
+    int best = 1;
+    double best_cost = (double)((T + slots - 1) / slots) * nstage * t_stage;
+    for (int ks = 2; ks <= 16; ++ks) {
+        const int64_t sps = (nstage + ks - 1) / ks;
+        if (sps < 2 || (ks - 1) * sps >= nstage) break;
+        const double cost = (double)((T * ks + slots - 1) / slots) * sps * t_stage + 2.0 * ks * unit + 3.0;
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = ks;
+        }
+    }
+    return best;
+}
+
 static hipError_t run_mmq(const MatW& w_in, const ActF16& a, const MatD& d, int64_t N, int64_t ne12, int64_t ne13,
-                          int32_t* dots, const MmqEpi* epi, void* align_buf, hipStream_t st) {
+                          int32_t* dots, const MmqEpi* epi, void* align_buf, const MmqSplit& sp, hipStream_t st) {
     MatW w = w_in;
     int64_t rowb = w.type == T_F16 ? a.K * 2 : (a.K / QK) * (w.type == T_Q8_0 ? 34 : w.type == T_Q4_0 ? 18 : 20);
     if (mmq_align_bytes(w_in, N, a.K) != 0) {
@@ -552,6 +632,18 @@ static hipError_t run_mmq(const MatW& w_in, const ActF16& a, const MatD& d, int6
     p.r3 = (int)(ne13 / w.ne3);
     p.tiles_m = (int)((a.M + BM - 1) / BM);
     p.tiles_n = (int)((N + BN - 1) / BN);
+    const int nstage = w.type != T_F16 ? (int)(((a.K / QK) + BKB - 1) / BKB) : (int)((a.K + 31) / 32);
+    const bool split = sp.ks > 1 && !dots && ne12 * ne13 == 1;
+    p.ksplit = split ? sp.ks : 1;
+    p.sps = split ? (nstage + sp.ks - 1) / sp.ks : nstage;
+    p.d_split = 0;
+    if (split) {
+        if (!sp.part || N % 4 != 0 || (int64_t)(sp.ks - 1) * p.sps >= nstage) return hipErrorInvalidValue;
+        p.D = sp.part;
+        p.d_nb1 = N * 4;
+        p.d_nb2 = p.d_nb3 = 0;
+        p.d_split = a.M * N * 4;
+    }
     // buffer offsets are 32-bit
     if (p.w_extent >= OOB || p.a_extent >= OOB || 2 * a.M * a.dp >= OOB) return hipErrorInvalidValue;
     const int Z = (int)(ne12 * ne13);
@@ -562,16 +654,28 @@ static hipError_t run_mmq(const MatW& w_in, const ActF16& a, const MatD& d, int6
         case T_F16: launch_t<T_F16>(p, Z, false, epi, st); break;
         default: return hipErrorInvalidValue;
     }
+    if (split) {
+        const int64_t n = a.M * (N / 4);
+        const unsigned g = (unsigned)((n + 255) / 256);
+        char* D = reinterpret_cast<char*>(d.data);
+        if (!epi || epi->kind == MMQ_EPI_STORE)
+            mmq_reduce_kernel<MMQ_EPI_STORE><<<g, 256, 0, st>>>(sp.part, sp.ks, (int)a.M, (int)N, D, d.nb1, MmqEpi{});
+        else if (epi->kind == MMQ_EPI_RESIDUAL)
+            mmq_reduce_kernel<MMQ_EPI_RESIDUAL><<<g, 256, 0, st>>>(sp.part, sp.ks, (int)a.M, (int)N, D, 0, *epi);
+        else
+            mmq_reduce_kernel<MMQ_EPI_QKV><<<g, 256, 0, st>>>(sp.part, sp.ks, (int)a.M, (int)N, D, 0, *epi);
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_mmq(const MatW& w, const ActF16& a, const MatD& d, int64_t N, int64_t ne12, int64_t ne13,
-                      int32_t* dots, void* align_buf, hipStream_t st) {
-    return run_mmq(w, a, d, N, ne12, ne13, dots, nullptr, align_buf, st);
+                      int32_t* dots, void* align_buf, const MmqSplit& sp, hipStream_t st) {
+    if (sp.ks > 1 && (d.nb1 % 16 != 0 || (reinterpret_cast<uintptr_t>(d.data) & 15) != 0)) return hipErrorInvalidValue;
+    return run_mmq(w, a, d, N, ne12, ne13, dots, nullptr, align_buf, sp, st);
 }
 
 hipError_t launch_mmq_epi(const MatW& w, const ActF16& a, int64_t N, const MmqEpi& e, void* align_buf,
-                          hipStream_t st) {
+                          const MmqSplit& sp, hipStream_t st) {
     if (!e.bias || N % 4 != 0) return hipErrorInvalidValue;
     if (e.kind == MMQ_EPI_RESIDUAL) {
         if (!e.res || !e.out) return hipErrorInvalidValue;
@@ -583,7 +687,7 @@ hipError_t launch_mmq_epi(const MatW& w, const ActF16& a, int64_t N, const MmqEp
         return hipErrorInvalidValue;
     }
     const MatD none{nullptr, 0, 0, 0};
-    return run_mmq(w, a, none, N, 1, 1, nullptr, &e, align_buf, st);
+    return run_mmq(w, a, none, N, 1, 1, nullptr, &e, align_buf, sp, st);
 }
 
 }  // namespace mi355

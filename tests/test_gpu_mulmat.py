@@ -118,3 +118,15 @@ def test_mul_mat_vit_shapes(mi, ctx, orc, tname, name, N, K):
     sample.sort()
     sample[0], sample[-1] = 0, 5183
     check(mi, ctx, orc, tname, 5184, N, K, seed=0, sample=sample)
+
+
+@pytest.mark.parametrize("tname", ["q8_0", "q4_0", "q4_1", "f16"])
+@pytest.mark.parametrize("M,N,K", [(1024, 768, 3072), (4096, 384, 1536), (96, 80, 4736)])
+def test_mul_mat_split_k(mi, ctx, orc, tname, M, N, K):
+    """Few output tiles over a long K (Hiera-tiny stage-3 fc2, stage-2 fc2, a
+    single tile): the K range is split over workgroups and the partial sums
+    are added by a reduction; same bars as every other shape."""
+    sample = np.random.default_rng(1).choice(M, size=min(M, 128), replace=False)
+    sample.sort()
+    sample[0], sample[-1] = 0, M - 1
+    check(mi, ctx, orc, tname, M, N, K, seed=3, sample=sample)
