@@ -358,6 +358,23 @@ mi355_status flash_attn_act(mi355_context* ctx, const mi355_tensor* q, const mi3
         a.out = *op;
     }
     (void)hipSetDevice(ctx->device);
+    a.kv_split = fattn_kv_split(a.nq, a.nkv, a.nh, (int)q->ne[3], ctx->cus);
+    a.kv_chunk = 0;
+    a.part = nullptr;
+    if (a.kv_split > 1) {
+        const int ntile = (a.nkv + 63) / 64, per = (ntile + a.kv_split - 1) / a.kv_split;
+        a.kv_chunk = per * 64;
+        a.kv_split = (ntile + per - 1) / per;  // no empty range
+        if (a.kv_split > 1) {
+            const mi355_status s2 = ensure_ws(ctx, fattn_part_bytes((int)D, a.nq, a.nh, (int)q->ne[3], a.kv_split));
+            if (s2 != MI355_STATUS_SUCCESS) return s2;
+            a.part = static_cast<float*>(ctx->ws);
+        }
+    }
+    if (a.kv_split <= 1) {
+        a.kv_split = 1;
+        a.kv_chunk = a.nkv;
+    }
     Timed tf(ctx, "flash_attn_ext");
     return hip_check(ctx, tf.done(launch_fattn(a, (int)D, q->type == T_F32, k->type == T_F32, (int)q->ne[3], ctx->stream)),
                      "flash_attn_ext launch");

@@ -23,6 +23,8 @@
 // K is staged row-major and V transposed, both with rows padded by 16 bytes
 // so the 32-row fragment reads spread over all LDS banks.  The next tile's
 // global loads go to registers before the current tile's MFMAs.
+#include <algorithm>
+
 #include "common.cuh"
 #include "kernels.h"
 
@@ -75,11 +77,12 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 31, g = lane >> 5;
-    const int h = blockIdx.y, b = blockIdx.z;
+    const int h = blockIdx.y, b = blockIdx.z / p.kv_split, ks = blockIdx.z - b * p.kv_split;
     const int qi = blockIdx.x * FA_BQ + w * 32 + lr;  // this lane's query
-    const int nkv = p.nkv;
-    const char* kb = p.k + (int64_t)(h / p.rk2) * p.k_nb2 + (int64_t)b * p.k_nb3;
-    const char* vb = p.v + (int64_t)(h / p.rv2) * p.v_nb2 + (int64_t)b * p.v_nb3;
+    // a key split attends to keys kbeg .. kbeg + nkv: shifted K/V bases, the same code
+    const int kbeg = ks * p.kv_chunk, nkv = min(p.nkv - kbeg, p.kv_chunk);
+    const char* kb = p.k + (int64_t)(h / p.rk2) * p.k_nb2 + (int64_t)b * p.k_nb3 + (int64_t)kbeg * p.k_nb1;
+    const char* vb = p.v + (int64_t)(h / p.rv2) * p.v_nb2 + (int64_t)b * p.v_nb3 + (int64_t)kbeg * p.v_nb1;
     constexpr int KES = KVF32 ? 4 : 2;
 
     // Q fragment (B operand of S^T): query qi, elements 16c + 8g .. +7
@@ -217,7 +220,23 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
         }
     }
 
-    if (qi < p.nq) {
+    if (qi < p.nq && p.kv_split > 1) {  // this key range's unnormalised O and (max, sum)
+        const int64_t pr = ((int64_t)ks * gridDim.z / p.kv_split * p.nh + (int64_t)b * p.nh + h) * p.nq + qi;
+        float* orow = p.part + pr * D;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const int d = 32 * db + 8 * i4 + 4 * g;
+                *reinterpret_cast<v4f*>(orow + d) = v4f{O[db][4 * i4], O[db][4 * i4 + 1], O[db][4 * i4 + 2], O[db][4 * i4 + 3]};
+            }
+        if (g == 0) {
+            const int64_t rows = (int64_t)gridDim.z / p.kv_split * p.nh * p.nq;
+            float* ml = p.part + (int64_t)p.kv_split * rows * D + pr * 2;
+            ml[0] = m_run;
+            ml[1] = l_run;
+        }
+    } else if (qi < p.nq) {
         const float inv = l_run == 0.0f ? 0.0f : 1.0f / l_run;
         if (p.out.mode == ACT_F32) {
             float* orow = p.dst + (((int64_t)b * p.nq + qi) * p.nh + h) * D;
@@ -280,17 +299,68 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
     }
 }
 
+// Key-split combine: thread per (batch, head, query, 4 outputs); m* = max of the
+// ranges' maxima, O = sum_s 2^(m_s - m*) O_s, l likewise, out = O / l.  The
+// operand output keeps 8 consecutive threads on one 32-block.
+template <int D>
+__global__ __launch_bounds__(256) void fattn_combine_kernel(const FaArgs p, int B) {
+    constexpr int CPR = D / 4;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t rows = (int64_t)B * p.nh * p.nq;
+    if (t >= rows * CPR) return;
+    const int64_t pr = t / CPR;
+    const int c = (int)(t - pr * CPR);
+    const int qi = (int)(pr % p.nq), h = (int)((pr / p.nq) % p.nh), b = (int)(pr / ((int64_t)p.nq * p.nh));
+    const float* ml = p.part + (int64_t)p.kv_split * rows * D;
+    float mx = -__builtin_inff();
+    for (int s = 0; s < p.kv_split; ++s) mx = fmaxf(mx, ml[(s * rows + pr) * 2]);
+    float l = 0.0f;
+    v4f o = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = 0; s < p.kv_split; ++s) {
+        const float wgt = __builtin_amdgcn_exp2f(ml[(s * rows + pr) * 2] - mx);
+        l = l + wgt * ml[(s * rows + pr) * 2 + 1];
+        o = o + wgt * *reinterpret_cast<const v4f*>(&p.part[(s * rows + pr) * D + 4 * c]);
+    }
+    const float inv = l == 0.0f ? 0.0f : 1.0f / l;
+    o = o * inv;
+    if (p.out.mode == ACT_F32)
+        *reinterpret_cast<v4f*>(p.dst + (((int64_t)b * p.nq + qi) * p.nh + h) * D + 4 * c) = o;
+    else
+        act_store_chunk(p.out, (int64_t)b * p.nq + qi, (int64_t)p.nh * D, ((int64_t)h * D) / 4 + c, o);
+}
+
+int fattn_kv_split(int nq, int nkv, int nh, int B, int cus) {
+    const int64_t wgs = (int64_t)((nq + FA_BQ - 1) / FA_BQ) * nh * B;
+    const int ntile = (nkv + FA_BKV - 1) / FA_BKV;
+    if (cus <= 0 || wgs >= cus || ntile < 4) return 1;
+    const int64_t want = (2LL * cus + wgs - 1) / wgs;
+    const int ks = (int)std::min<int64_t>(want, ntile / 2);
+    return ks < 2 ? 1 : std::min(ks, 16);
+}
+
+size_t fattn_part_bytes(int D, int nq, int nh, int B, int kv_split) {
+    if (kv_split <= 1) return 0;
+    return (size_t)kv_split * B * nh * nq * (D + 2) * 4;
+}
+
 template <int D>
 static void fa_launch_d(const FaArgs& a, bool qf32, bool kvf32, int B, hipStream_t st) {
-    const dim3 grid((unsigned)((a.nq + FA_BQ - 1) / FA_BQ), (unsigned)a.nh, (unsigned)B);
+    const dim3 grid((unsigned)((a.nq + FA_BQ - 1) / FA_BQ), (unsigned)a.nh, (unsigned)(B * a.kv_split));
     if (qf32 && kvf32) fattn_kernel<D, true, true><<<grid, FA_NT, 0, st>>>(a);
     else if (qf32) fattn_kernel<D, true, false><<<grid, FA_NT, 0, st>>>(a);
     else if (kvf32) fattn_kernel<D, false, true><<<grid, FA_NT, 0, st>>>(a);
     else fattn_kernel<D, false, false><<<grid, FA_NT, 0, st>>>(a);
+    if (a.kv_split > 1) {
+        const int64_t n = (int64_t)B * a.nh * a.nq * (D / 4);
+        fattn_combine_kernel<D><<<(unsigned)((n + 255) / 256), 256, 0, st>>>(a, B);
+    }
 }
 
 hipError_t launch_fattn(const FaArgs& a, int D, bool qf32, bool kvf32, int B, hipStream_t st) {
     if (a.nq <= 0 || a.nkv <= 0 || a.nh <= 0 || B <= 0) return hipSuccess;
+    if (a.kv_split < 1 || (a.kv_split > 1 && (!a.part || a.kv_chunk % FA_BKV != 0 ||
+                                              (int64_t)(a.kv_split - 1) * a.kv_chunk >= a.nkv)))
+        return hipErrorInvalidValue;
     switch (D) {
         case 64: fa_launch_d<64>(a, qf32, kvf32, B, st); break;
         case 96: fa_launch_d<96>(a, qf32, kvf32, B, st); break;

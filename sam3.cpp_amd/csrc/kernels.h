@@ -134,7 +134,13 @@ struct FaArgs {
     int negq;                   // scale < 0: Q enters negated
     ActOut out;                 // mode ACT_F32: dst; else the next MUL_MAT's operand, rows
                                 // b*nq + iq of K = nh*D (Q8 quants + scales or F16)
+    int kv_split, kv_chunk;     // keys split into kv_split ranges of kv_chunk (a multiple of 64);
+    float* part;                // > 1: per range unnormalised O [D] and (max, sum) per query,
+                                // combined by a second kernel; fattn_part_bytes() of workspace
 };
+// Key-range split for grids too small to fill the GPU (1 = none), and its workspace.
+int fattn_kv_split(int nq, int nkv, int nh, int B, int cus);
+size_t fattn_part_bytes(int D, int nq, int nh, int B, int kv_split);
 hipError_t launch_fattn(const FaArgs& a, int D, bool qf32, bool kvf32, int B, hipStream_t st);
 
 // F32 x F32 MUL_MAT: D[z][m][n] = sum_k X[z][m][k] W[z'][n][k] (byte strides).

@@ -108,6 +108,7 @@ struct MmqArgs {
     int M, dp, N, K, ne12, r2, r3, tiles_m, tiles_n;  // dp: row pitch (halves) of the scale arrays
     int ksplit, sps;           // K split into ksplit ranges of sps stages; partial sums go to
     int64_t d_split;           // D + split * d_split (bytes), summed by mmq_reduce_kernel
+    int d_v4;                  // D rows 16-byte aligned, N % 4 == 0: float4 stores through LDS
 };
 
 // 8 consecutive int8 quants (two dwords) -> 8 fp16 (one MFMA k-chunk).
@@ -407,6 +408,31 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
     const int n = n0 + wrow;
     if (EPI == MMQ_EPI_STORE) {
         char* Dz = reinterpret_cast<char*>(p.D) + (int64_t)i12 * p.d_nb2 + (int64_t)i13 * p.d_nb3 + split * p.d_split;
+        if (p.d_v4) {  // row-major through LDS: float4 stores, whole 512-byte row segments
+            constexpr int TP = BN + 4, CPR = BN / 4, IT = 64 * CPR / NT;
+            float* t0 = reinterpret_cast<float*>(&st0);
+            float* t1 = reinterpret_cast<float*>(&st1);
+            const int c = tid % CPR, nc = n0 + 4 * c;
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                __syncthreads();
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int r = 8 * (i >> 2) + 4 * g + (i & 3);
+                    t0[r * TP + wrow] = acc[2 * half][i];
+                    t1[r * TP + wrow] = acc[2 * half + 1][i];
+                }
+                __syncthreads();
+#pragma unroll
+                for (int it = 0; it < IT; ++it) {
+                    const int r = it * (NT / CPR) + tid / CPR, m = m0 + half * 64 + r;
+                    if (m >= M || nc >= N) continue;
+                    const v4f v = *reinterpret_cast<const v4f*>(&(it < IT / 2 ? t0 : t1)[(r & 31) * TP + 4 * c]);
+                    *reinterpret_cast<v4f*>(Dz + (int64_t)m * p.d_nb1 + (int64_t)nc * 4) = v;
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -647,6 +673,8 @@ static hipError_t run_mmq(const MatW& w_in, const ActF16& a, const MatD& d, int6
     // buffer offsets are 32-bit
     if (p.w_extent >= OOB || p.a_extent >= OOB || 2 * a.M * a.dp >= OOB) return hipErrorInvalidValue;
     const int Z = (int)(ne12 * ne13);
+    p.d_v4 = !dots && N % 4 == 0 && p.d_nb1 % 16 == 0 && (reinterpret_cast<uintptr_t>(p.D) & 15) == 0 &&
+             (Z == 1 || (p.d_nb2 % 16 == 0 && p.d_nb3 % 16 == 0));
     switch (w.type) {
         case T_Q8_0: launch_t<T_Q8_0>(p, Z, dots, epi, st); break;
         case T_Q4_0: launch_t<T_Q4_0>(p, Z, dots, epi, st); break;

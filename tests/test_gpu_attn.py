@@ -84,6 +84,8 @@ def _check(orc, got, q, k, v, scale, t):
     (128, 129, 65, 1, 1, 1),
     (64, 576, 576, 16, 16, 1),    # one SAM3 window, all heads
     (96, 196, 196, 4, 4, 3),      # Hiera 14x14 windows
+    (96, 1024, 1024, 4, 4, 1),    # few query tiles: keys split over workgroups, then combined
+    (64, 300, 2000, 2, 1, 1),     # uneven key ranges, grouped kv heads
 ])
 def test_flash_attn_f16(mi, ctx, orc, D, nq, nkv, nh, nhk, B):
     q, k, v = (_f16(a) for a in _inputs(orc, D, nq, nkv, nh, nhk, B))
