@@ -255,12 +255,14 @@ mi355_status mi355_hiera_encode(mi355_context* ctx, const mi355_hiera_hparams* h
                                 const mi355_tensor* patch_w, const float* patch_b, const float* pos_embed,
                                 const mi355_hiera_block* blocks, int n_blocks, float* const stage_out[4]);
 
-/* Producer fusion of the encoder runners (no counterpart in the reference,
- * whose graph always materialises f32 activations; on by default).  When on,
- * the LayerNorm and bias+GELU passes that feed a MUL_MAT with Q8_0/Q4_0/Q4_1
- * or F16 weights write its activation operand (the same from_float
- * quantization ggml applies to those f32 rows) instead of f32 rows; off gives
- * the unfused sequence of entry points, for parity checks. */
+/* Fusion in the encoder runners (no counterpart in the reference, whose graph
+ * always materialises f32 activations; on by default).  When on, the passes
+ * that feed a MUL_MAT with Q8_0/Q4_0/Q4_1 or F16 weights (LayerNorm, bias+GELU,
+ * the attention output) write its activation operand (the same from_float
+ * quantization ggml applies to those f32 rows), and the GEMMs run the
+ * following node group in their epilogue (bias + residual with the window
+ * unpartition; the ViT's qkv split + RoPE).  Off gives the unfused sequence
+ * of node groups, for parity checks: both produce the same bits. */
 mi355_status mi355_context_set_fusion(mi355_context* ctx, int enable);
 
 /* ---- Kernel timing --------------------------------------------------------
