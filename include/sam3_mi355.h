@@ -255,6 +255,56 @@ mi355_status mi355_hiera_encode(mi355_context* ctx, const mi355_hiera_hparams* h
                                 const mi355_tensor* patch_w, const float* patch_b, const float* pos_embed,
                                 const mi355_hiera_block* blocks, int n_blocks, float* const stage_out[4]);
 
+/* ---- Model files (sam3.cpp's .ggml format) ----------------------------------
+ * sam3_load_model / sam3_load_tensors (sam3.cpp:3095-3348): a header (magic
+ * "sam3" 0x73616D33 version 3, or "sam2" 0x73616D32 version 1; ftype; tensor
+ * count), the hyperparameters as int32 fields (sam3_load_hparams 1481-1524,
+ * sam2_load_hparams 1568-1630; SAM2 files with the Hiera backbone only), then
+ * per tensor: n_dims, name length, ggml type, ne[0..n_dims), name, zero
+ * padding to a 32-byte file offset, and the raw ggml rows.  Opening indexes the
+ * records; data is read when a tensor is loaded. */
+typedef struct mi355_model_file mi355_model_file;
+typedef struct mi355_model_tensor_info {
+    const char* name;   /* valid while the file is open */
+    int32_t type;       /* ggml type id: 0 F32, 1 F16, 2 Q4_0, 3 Q4_1, 8 Q8_0 */
+    int32_t n_dims;
+    int64_t ne[4];      /* ggml order, unused dims 1 */
+    uint64_t offset;    /* file offset of the data (32-byte aligned) */
+    uint64_t nbytes;    /* data bytes */
+} mi355_model_tensor_info;
+mi355_status mi355_model_file_open(const char* path, mi355_model_file** out);
+void mi355_model_file_close(mi355_model_file* f);
+/* Text of the last open/query error (the calls without a context). */
+const char* mi355_model_file_last_error(void);
+mi355_status mi355_model_file_header(const mi355_model_file* f, uint32_t* magic, int32_t* version, int32_t* ftype,
+                                     int32_t* n_tensors);
+/* The hyperparameter fields in file order; returns their count (or -1). */
+int mi355_model_file_hparams(const mi355_model_file* f, const int32_t** values);
+/* Index of the tensor called name, or -1. */
+int mi355_model_file_find(const mi355_model_file* f, const char* name);
+mi355_status mi355_model_file_tensor(const mi355_model_file* f, int index, mi355_model_tensor_info* out);
+/* Device bytes of tensor index loaded as dst_type (0 when no conversion exists):
+ * the file's own type, F32 (from F16 or by dequantizing Q8_0/Q4_0/Q4_1), or F16
+ * (from F32) - the conversions sam3_load_tensors applies (sam3.cpp:3150-3185). */
+size_t mi355_model_file_load_bytes(const mi355_model_file* f, int index, int32_t dst_type);
+/* Tensor data -> device memory dst (dst_bytes >= mi355_model_file_load_bytes),
+ * converted on the GPU when dst_type differs.  Synchronous. */
+mi355_status mi355_model_file_load(mi355_context* ctx, const mi355_model_file* f, int index, int32_t dst_type,
+                                   void* dst, size_t dst_bytes);
+
+/* A SAM3 file's ViT backbone in device memory: the tensors sam3_register_tensors
+ * declares for it (sam3.cpp:2530-2560: "vit.patch_embed.proj.weight",
+ * "vit.pos_embed", "vit.ln_pre.*", "vit.blocks.N.*"), weights in the file's
+ * weight type when their rows are whole blocks and F32 otherwise, as the
+ * reference registers them; the hyperparameters of mi355_vit_encode derived as
+ * sam3_load_hparams does.  The tables stay valid until mi355_vit_weights_free. */
+typedef struct mi355_vit_weights mi355_vit_weights;
+mi355_status mi355_vit_weights_load(mi355_context* ctx, const mi355_model_file* f, mi355_vit_weights** out);
+void mi355_vit_weights_free(mi355_vit_weights* w);
+mi355_status mi355_vit_weights_get(const mi355_vit_weights* w, mi355_vit_hparams* hp, const mi355_vit_block** blocks,
+                                   int* n_blocks, const mi355_tensor** patch_w, const float** pos_embed,
+                                   const float** ln_pre_w, const float** ln_pre_b);
+
 /* Fusion in the encoder runners (no counterpart in the reference, whose graph
  * always materialises f32 activations; on by default).  When on, the passes
  * that feed a MUL_MAT with Q8_0/Q4_0/Q4_1 or F16 weights (LayerNorm, bias+GELU,

@@ -150,6 +150,19 @@ def lib():
         "mi355_hiera_encode": (I, [P, C.POINTER(HieraHparams), P, T, P, P, C.POINTER(HieraBlock), I,
                                    C.POINTER(P)]),
         "mi355_context_set_fusion": (I, [P, I]),
+        "mi355_model_file_open": (I, [C.c_char_p, C.POINTER(P)]),
+        "mi355_model_file_close": (None, [P]),
+        "mi355_model_file_last_error": (C.c_char_p, []),
+        "mi355_model_file_header": (I, [P, C.POINTER(C.c_uint32), C.POINTER(I), C.POINTER(I), C.POINTER(I)]),
+        "mi355_model_file_hparams": (I, [P, C.POINTER(C.POINTER(C.c_int32))]),
+        "mi355_model_file_find": (I, [P, C.c_char_p]),
+        "mi355_model_file_tensor": (I, [P, I, C.POINTER(ModelTensorInfo)]),
+        "mi355_model_file_load_bytes": (SZ, [P, I, I]),
+        "mi355_model_file_load": (I, [P, P, I, I, P, SZ]),
+        "mi355_vit_weights_load": (I, [P, P, C.POINTER(P)]),
+        "mi355_vit_weights_free": (None, [P]),
+        "mi355_vit_weights_get": (I, [P, C.POINTER(VitHparams), C.POINTER(C.POINTER(VitBlock)), C.POINTER(I),
+                                      C.POINTER(C.POINTER(Tensor)), C.POINTER(P), C.POINTER(P), C.POINTER(P)]),
         "mi355_profile_enable": (I, [P, I]),
         "mi355_profile_collect": (I, [P]),
         "mi355_profile_get": (I, [P, I, C.POINTER(C.c_char_p), C.POINTER(I), C.POINTER(C.c_double)]),
@@ -161,6 +174,59 @@ def lib():
         fn.argtypes = args
     _lib = L
     return L
+
+
+class ModelTensorInfo(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("type", C.c_int32), ("n_dims", C.c_int32), ("ne", C.c_int64 * 4),
+                ("offset", C.c_uint64), ("nbytes", C.c_uint64)]
+
+
+class ModelFile:
+    """A sam3.cpp .ggml model file (header, hyperparameters, tensor index)."""
+
+    def __init__(self, path: str):
+        self.L = lib()
+        self.h = C.c_void_p()
+        st = self.L.mi355_model_file_open(os.fsencode(path), C.byref(self.h))
+        if st != 0:
+            raise Mi355Error(st, self.L.mi355_model_file_last_error().decode())
+
+    def close(self):
+        if self.h:
+            self.L.mi355_model_file_close(self.h)
+            self.h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def header(self):
+        m, v, f, n = C.c_uint32(), C.c_int(), C.c_int(), C.c_int()
+        st = self.L.mi355_model_file_header(self.h, C.byref(m), C.byref(v), C.byref(f), C.byref(n))
+        if st != 0:
+            raise Mi355Error(st, self.L.mi355_model_file_last_error().decode())
+        return m.value, v.value, f.value, n.value
+
+    def hparams(self) -> list:
+        p = C.POINTER(C.c_int32)()
+        n = self.L.mi355_model_file_hparams(self.h, C.byref(p))
+        return [p[i] for i in range(n)]
+
+    def find(self, name: str) -> int:
+        return self.L.mi355_model_file_find(self.h, name.encode())
+
+    def tensor(self, index: int) -> dict:
+        info = ModelTensorInfo()
+        st = self.L.mi355_model_file_tensor(self.h, index, C.byref(info))
+        if st != 0:
+            raise Mi355Error(st, self.L.mi355_model_file_last_error().decode())
+        return {"name": info.name.decode(), "type": info.type, "n_dims": info.n_dims, "ne": list(info.ne),
+                "offset": info.offset, "nbytes": info.nbytes}
+
+    def load_bytes(self, index: int, dst_type: int) -> int:
+        return self.L.mi355_model_file_load_bytes(self.h, index, dst_type)
 
 
 def hiera_block_info(hp: HieraHparams, index: int) -> HieraBlockInfo:
@@ -242,6 +308,25 @@ class Context:
 
     def soft_max_ext(self, src: Tensor, dst: Tensor, scale: float):
         self._check(self.L.mi355_soft_max_ext(self.h, C.byref(src), None, scale, 0.0, C.byref(dst)))
+
+    def model_file_load(self, f: "ModelFile", index: int, dst_type: int, dst_ptr: int, dst_bytes: int):
+        self._check(self.L.mi355_model_file_load(self.h, f.h, index, dst_type, C.c_void_p(dst_ptr), dst_bytes))
+
+    def vit_weights_load(self, f: "ModelFile"):
+        """(handle, hparams, blocks array, n, patch_w Tensor, pos, ln_w, ln_b) of the file's ViT."""
+        w = C.c_void_p()
+        self._check(self.L.mi355_vit_weights_load(self.h, f.h, C.byref(w)))
+        hp = VitHparams()
+        blocks = C.POINTER(VitBlock)()
+        n = C.c_int()
+        pw = C.POINTER(Tensor)()
+        pos, lw, lb = C.c_void_p(), C.c_void_p(), C.c_void_p()
+        self._check(self.L.mi355_vit_weights_get(w, C.byref(hp), C.byref(blocks), C.byref(n), C.byref(pw),
+                                                 C.byref(pos), C.byref(lw), C.byref(lb)))
+        return w, hp, blocks, n.value, pw.contents, pos.value, lw.value, lb.value
+
+    def vit_weights_free(self, w):
+        self.L.mi355_vit_weights_free(w)
 
     def set_fusion(self, enable: bool):
         """Encoder runners: producer passes write the MUL_MAT operand (default) or f32 rows."""

@@ -107,7 +107,7 @@ MatD matd_of(const mi355_tensor* d) {
 }
 
 bool f16_src1_direct(const mi355_tensor* s1) {
-    return s1->type == T_F16 && s1->nb[0] == 2 && s1->nb[1] % 16 == 0 && s1->nb[2] % 16 == 0 && s1->nb[3] % 16 == 0 &&
+    return s1->type == T_F16 && s1->ne[0] % 8 == 0 && s1->nb[0] == 2 && s1->nb[1] % 16 == 0 && s1->nb[2] % 16 == 0 && s1->nb[3] % 16 == 0 &&
            (reinterpret_cast<uintptr_t>(s1->data) & 15) == 0;
 }
 
@@ -136,7 +136,8 @@ MmPlan mm_plan(const mi355_tensor* s0, const mi355_tensor* s1, int cus, bool spl
     if (split) pl.ks = mmq_ksplit(s0->type, M, s0->ne[1], K, Z, cus);
     if (pl.ks > 1) pl.part = align_up((size_t)pl.ks * (size_t)M * (size_t)s0->ne[1] * 4);
     if (s0->type == T_F16) {
-        if (!f16_src1_direct(s1)) pl.q = align_up((size_t)(Z * M * K) * 2);
+        if (!f16_src1_direct(s1)) pl.q = align_up((size_t)(Z * M * ((K + 7) & ~7)) * 2);
+        pl.align = align_up(mmq_align_bytes(matw_of(s0), s0->ne[1], K));
         return pl;
     }
     pl.q = align_up((size_t)(Z * M * K) * 2);
@@ -186,9 +187,9 @@ mi355_status check_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
                                 (uintptr_t)s1->nb[2] | (uintptr_t)s1->nb[3]) & 3))
             return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat f32: needs contiguous, 4-byte aligned rows");
     } else if (t0 == T_F16) {
-        if (K % 8 != 0 || s0->nb[1] % 16 != 0 || (reinterpret_cast<uintptr_t>(s0->data) & 15) ||
-            s0->nb[2] % 16 != 0 || s0->nb[3] % 16 != 0)
-            return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat f16: needs K %% 8 == 0 and 16-byte aligned rows");
+        if (((reinterpret_cast<uintptr_t>(s0->data) | (uintptr_t)s0->nb[1] | (uintptr_t)s0->nb[2] |
+              (uintptr_t)s0->nb[3]) & 1))
+            return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat f16: src0 rows must be 2-byte aligned");
     } else {
         if (reinterpret_cast<uintptr_t>(s0->data) & 1)
             return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: src0 data must be 2-byte aligned");
@@ -257,6 +258,8 @@ mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF1
     if (mode == ACT_F32) return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat_act: no prequantized path for type %d", s0->type);
     if (mode != ACT_F16 && (!a.d || (mode == ACT_Q8S && !a.s) || a.dp != mmq_scale_pitch(a.K)))
         return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat_act: scales missing or wrong pitch");
+    if (mode == ACT_F16 && a.K % 8 != 0)
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat_act: F16 operands need K %% 8 == 0");
     // validate the weights and dst as mul_mat would see them with an F32 [K, M] src1
     mi355_tensor s1{};
     s1.type = T_F32;
@@ -490,14 +493,16 @@ mi355_status mi355_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
             a.s2 = s1->nb[2] / 2;
             a.s3 = s1->nb[3] / 2;
         } else {
+            // rows padded with zeros to a whole 16-byte chunk
+            const int64_t K8 = (K + 7) & ~7;
             uint16_t* buf = static_cast<uint16_t*>(ctx->ws);
             Timed tc(ctx, "convert_f16");
-            st = hip_check(ctx, tc.done(launch_convert_f16(view_of(s1), buf, ctx->stream)), "convert_f16 launch");
+            st = hip_check(ctx, tc.done(launch_convert_f16(view_of(s1), buf, K8, ctx->stream)), "convert_f16 launch");
             if (st != MI355_STATUS_SUCCESS) return st;
             a.q = buf;
-            a.s1 = K;
-            a.s2 = K * M;
-            a.s3 = K * M * s1->ne[2];
+            a.s1 = K8;
+            a.s2 = K8 * M;
+            a.s3 = K8 * M * s1->ne[2];
         }
     } else {
         st = prep_act_q8(ctx, s0, s1, pl, a);

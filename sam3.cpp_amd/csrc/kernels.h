@@ -57,7 +57,10 @@ hipError_t launch_quantize_ggml(const SrcView& src, int type, bool ref_variant, 
 hipError_t launch_quantize_mmq(const SrcView& src, bool with_sum, int64_t dp, uint16_t* q, uint16_t* d, uint16_t* s,
                                hipStream_t st);
 // F32/F16 strided rows -> contiguous F16 rows [rows][ne0] (round to nearest even).
-hipError_t launch_convert_f16(const SrcView& src, uint16_t* dst, hipStream_t st);
+hipError_t launch_convert_f16(const SrcView& src, uint16_t* dst, int64_t pitch, hipStream_t st);
+// n contiguous elements of type src_type -> dst_type: F16 -> F32, F32 -> F16
+// (RNE), Q8_0 / Q4_0 / Q4_1 -> F32 (ggml's to_float: d*q, d*(q-8), d*q + m).
+hipError_t launch_convert_weights(const void* src, int src_type, void* dst, int dst_type, int64_t n, hipStream_t st);
 
 struct MatW {  // src0 (weights), ggml layout
     const uint8_t* data;

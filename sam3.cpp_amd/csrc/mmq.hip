@@ -580,9 +580,15 @@ static void launch_t(const MmqArgs& a, int Z, bool dots, const MmqEpi* e, hipStr
 // The weight DMA reads whole dwords and the buffer range check zeroes a dword
 // that straddles the end, so rows must start 4-byte aligned and span a whole
 // number of dwords; other weights are first copied to a zero-padded 4-byte
-// pitch.
+// pitch. F16 rows are read in 16-byte chunks: rows that are not 16-byte
+// aligned or whose K is not a multiple of 8 are copied to a pitch of K
+// rounded up to 8 halves, zero-filled.
 size_t mmq_align_bytes(const MatW& w, int64_t N, int64_t K) {
-    if (w.type == T_F16) return 0;
+    if (w.type == T_F16) {
+        const bool a16 = K % 8 == 0 && ((reinterpret_cast<uintptr_t>(w.data) | (uintptr_t)w.nb1 | (uintptr_t)w.nb2 |
+                                         (uintptr_t)w.nb3) & 15) == 0;
+        return a16 ? 0 : (size_t)(N * w.ne2 * w.ne3) * (size_t)(((K + 7) & ~7) * 2);
+    }
     const int64_t rowb = (K / QK) * (w.type == T_Q8_0 ? 34 : w.type == T_Q4_0 ? 18 : 20);
     const bool a4 = ((reinterpret_cast<uintptr_t>(w.data) | (uintptr_t)w.nb1 | (uintptr_t)w.nb2 | (uintptr_t)w.nb3 |
                       (uintptr_t)rowb) & 3) == 0;
@@ -617,10 +623,14 @@ int mmq_ksplit(int type, int64_t M, int64_t N, int64_t K, int64_t Z, int cus) {
 static hipError_t run_mmq(const MatW& w_in, const ActF16& a, const MatD& d, int64_t N, int64_t ne12, int64_t ne13,
                           int32_t* dots, const MmqEpi* epi, void* align_buf, const MmqSplit& sp, hipStream_t st) {
     MatW w = w_in;
+    // F16 runs K to a whole 16-byte chunk: the weight copy below and the
+    // activation operand (a.s1 >= kk, zero from K to kk) carry zeros there
+    const int64_t kk = w.type == T_F16 ? (a.K + 7) & ~7 : a.K;
+    if (kk != a.K && a.s1 < kk) return hipErrorInvalidValue;
     int64_t rowb = w.type == T_F16 ? a.K * 2 : (a.K / QK) * (w.type == T_Q8_0 ? 34 : w.type == T_Q4_0 ? 18 : 20);
     if (mmq_align_bytes(w_in, N, a.K) != 0) {
-        // weight rows are only 2-byte aligned: copy them to a 4-byte pitch first
-        const int64_t pitch = (rowb + 3) & ~3, rows = N * w.ne2 * w.ne3;
+        // weight rows are not aligned for the DMA: copy them to a zero-padded pitch first
+        const int64_t pitch = w.type == T_F16 ? kk * 2 : (rowb + 3) & ~3, rows = N * w.ne2 * w.ne3;
         if (!align_buf) return hipErrorInvalidValue;
         align_rows_kernel<<<dim3((unsigned)rows), 64, 0, st>>>(w.data, w.nb1, w.nb2, w.nb3, N, w.ne2, rows,
                                                               (int)(rowb / 2), (int)(pitch / 2),
@@ -641,7 +651,7 @@ static hipError_t run_mmq(const MatW& w_in, const ActF16& a, const MatD& d, int6
     p.a_s1 = a.s1;
     p.a_s2 = a.s2;
     p.a_s3 = a.s3;
-    p.a_extent = ((a.M - 1) * a.s1 + a.K) * 2;
+    p.a_extent = ((a.M - 1) * a.s1 + kk) * 2;
     p.Ad = static_cast<const _Float16*>(a.d);
     p.As = static_cast<const _Float16*>(a.s);
     p.D = d.data;
@@ -652,13 +662,13 @@ static hipError_t run_mmq(const MatW& w_in, const ActF16& a, const MatD& d, int6
     p.M = (int)a.M;
     p.dp = (int)a.dp;
     p.N = (int)N;
-    p.K = (int)a.K;
+    p.K = (int)kk;
     p.ne12 = (int)ne12;
     p.r2 = (int)(ne12 / w.ne2);
     p.r3 = (int)(ne13 / w.ne3);
     p.tiles_m = (int)((a.M + BM - 1) / BM);
     p.tiles_n = (int)((N + BN - 1) / BN);
-    const int nstage = w.type != T_F16 ? (int)(((a.K / QK) + BKB - 1) / BKB) : (int)((a.K + 31) / 32);
+    const int nstage = w.type != T_F16 ? (int)(((a.K / QK) + BKB - 1) / BKB) : (int)((kk + 31) / 32);
     const bool split = sp.ks > 1 && !dots && ne12 * ne13 == 1;
     p.ksplit = split ? sp.ks : 1;
     p.sps = split ? (nstage + sp.ks - 1) / sp.ks : nstage;

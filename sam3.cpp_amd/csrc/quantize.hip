@@ -144,11 +144,17 @@ __global__ __launch_bounds__(256) void quantize_mmq_kernel(const char* __restric
     }
 }
 
+// dst rows of `pitch` halves; columns ne0..pitch are zero
 __global__ __launch_bounds__(256) void convert_f16_kernel(const char* __restrict__ src, int stype, RowAddr ra,
-                                                          int64_t ne0, int64_t n, uint16_t* __restrict__ dst) {
+                                                          int64_t ne0, int64_t pitch, int64_t n,
+                                                          uint16_t* __restrict__ dst) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    const int64_t r = i / ne0, k = i % ne0;
+    const int64_t r = i / pitch, k = i % pitch;
+    if (k >= ne0) {
+        dst[i] = 0;
+        return;
+    }
     const char* p = ra.row(src, r) + k * ra.nb0;
     dst[i] = stype == T_F32 ? f2h(*reinterpret_cast<const float*>(p)) : *reinterpret_cast<const uint16_t*>(p);
 }
@@ -166,7 +172,7 @@ static RowAddr row_addr(const SrcView& s) {
 
 hipError_t launch_quantize_ggml(const SrcView& src, int type, bool ref_variant, void* dst, hipStream_t st) {
     const int64_t rows = src.ne[1] * src.ne[2] * src.ne[3];
-    if (type == T_F16) return launch_convert_f16(src, static_cast<uint16_t*>(dst), st);
+    if (type == T_F16) return launch_convert_f16(src, static_cast<uint16_t*>(dst), src.ne[0], st);
     const int64_t nblocks = rows * (src.ne[0] / QK);
     if (nblocks == 0) return hipSuccess;
     const dim3 grid((unsigned)((nblocks * 8 + 255) / 256));
@@ -197,11 +203,68 @@ hipError_t launch_quantize_mmq(const SrcView& src, bool with_sum, int64_t dp, ui
     return hipGetLastError();
 }
 
-hipError_t launch_convert_f16(const SrcView& src, uint16_t* dst, hipStream_t st) {
-    const int64_t n = src.ne[0] * src.ne[1] * src.ne[2] * src.ne[3];
+hipError_t launch_convert_f16(const SrcView& src, uint16_t* dst, int64_t pitch, hipStream_t st) {
+    if (pitch < src.ne[0]) return hipErrorInvalidValue;
+    const int64_t n = pitch * src.ne[1] * src.ne[2] * src.ne[3];
     if (n == 0) return hipSuccess;
     const dim3 grid((unsigned)((n + 255) / 256));
-    convert_f16_kernel<<<grid, 256, 0, st>>>(src.data, src.type, row_addr(src), src.ne[0], n, dst);
+    convert_f16_kernel<<<grid, 256, 0, st>>>(src.data, src.type, row_addr(src), src.ne[0], pitch, n, dst);
+    return hipGetLastError();
+}
+
+// weight conversions for the model-file loader: one thread per 32 elements
+__global__ __launch_bounds__(256) void convert_weights_kernel(const uint8_t* __restrict__ src, int src_type,
+                                                              void* __restrict__ dst, int dst_type, int64_t n) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b * QK >= n) return;
+    const int64_t e0 = b * QK;
+    const int cnt = (int)min((int64_t)QK, n - e0);
+    float x[QK];
+    if (src_type == T_F32) {
+        const float* s = reinterpret_cast<const float*>(src) + e0;
+        for (int j = 0; j < cnt; ++j) x[j] = s[j];
+    } else if (src_type == T_F16) {
+        const uint16_t* s = reinterpret_cast<const uint16_t*>(src) + e0;
+        for (int j = 0; j < cnt; ++j) x[j] = h2f(s[j]);
+    } else if (src_type == T_Q8_0) {
+        const blk_q8_0* blk = reinterpret_cast<const blk_q8_0*>(src) + b;
+        const float d = h2f(blk->d);
+#pragma unroll
+        for (int j = 0; j < QK; ++j) x[j] = (float)blk->qs[j] * d;
+    } else if (src_type == T_Q4_0) {
+        const blk_q4_0* blk = reinterpret_cast<const blk_q4_0*>(src) + b;
+        const float d = h2f(blk->d);
+#pragma unroll
+        for (int j = 0; j < QK / 2; ++j) {
+            x[j] = (float)((blk->qs[j] & 0x0f) - 8) * d;
+            x[j + QK / 2] = (float)((blk->qs[j] >> 4) - 8) * d;
+        }
+    } else {  // Q4_1: q*d + m, each rounded (no contraction)
+        const blk_q4_1* blk = reinterpret_cast<const blk_q4_1*>(src) + b;
+        const float d = h2f(blk->d), m = h2f(blk->m);
+#pragma unroll
+        for (int j = 0; j < QK / 2; ++j) {
+            x[j] = __fadd_rn(__fmul_rn((float)(blk->qs[j] & 0x0f), d), m);
+            x[j + QK / 2] = __fadd_rn(__fmul_rn((float)(blk->qs[j] >> 4), d), m);
+        }
+    }
+    if (dst_type == T_F32) {
+        float* o = reinterpret_cast<float*>(dst) + e0;
+        for (int j = 0; j < cnt; ++j) o[j] = x[j];
+    } else {
+        uint16_t* o = reinterpret_cast<uint16_t*>(dst) + e0;
+        for (int j = 0; j < cnt; ++j) o[j] = f2h(x[j]);
+    }
+}
+
+hipError_t launch_convert_weights(const void* src, int src_type, void* dst, int dst_type, int64_t n, hipStream_t st) {
+    const bool ok = (src_type == T_F16 && dst_type == T_F32) || (src_type == T_F32 && dst_type == T_F16) ||
+                    ((src_type == T_Q8_0 || src_type == T_Q4_0 || src_type == T_Q4_1) && dst_type == T_F32 && n % QK == 0);
+    if (!ok) return hipErrorInvalidValue;
+    const int64_t nb = (n + QK - 1) / QK;
+    if (nb > 0)
+        convert_weights_kernel<<<(unsigned)((nb + 255) / 256), 256, 0, st>>>(static_cast<const uint8_t*>(src), src_type,
+                                                                             dst, dst_type, n);
     return hipGetLastError();
 }
 

@@ -64,9 +64,12 @@ def test_mul_mat_validation(mi):
     s0, s1, d = mm(mi)
     s0.nb[1] = 10
     assert status(mi, s0, s1, d) == -4
-    # misaligned f16 rows
+    # f16 rows of any K are taken (copied to a zero-padded pitch); odd addresses are not
     s0, s1, d = mm(mi, t0=1, K=12)
-    assert status(mi, s0, s1, d) == -3
+    assert mi.lib().mi355_supports_mul_mat(C.byref(s0), C.byref(s1), C.byref(d)) == 1
+    s0.data = (s0.data or 0) + 1
+    assert status(mi, s0, s1, d) == -4
+    assert b"2-byte" in mi.lib().mi355_last_error(None)
 
 
 def test_quantize_rows_validation(mi):

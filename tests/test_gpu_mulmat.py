@@ -96,9 +96,20 @@ def test_integer_exact_through_product_path(mi, ctx, orc):
     assert np.array_equal(out, exact.astype(np.float32))
 
 
-def test_f16_src1_direct(mi, ctx, orc):
-    """F16 src1 (the explicit attention form multiplies f16 K by f16 Q)."""
-    K, N, M = 64, 200, 150
+@pytest.mark.parametrize("M,N,K", [(300, 64, 588), (77, 40, 147), (5, 3, 3), (130, 200, 1004)])
+def test_mul_mat_f16_ragged_k(mi, ctx, orc, M, N, K):
+    """F16 weights whose K is not a multiple of 8 (the 14x14x3 patch-embed
+    conv, K = 588; the 7x7x3 stem, K = 147): rows are only 2-byte aligned, are
+    copied to a zero-padded pitch, and the F16 activation rows are padded
+    with zeros to the same pitch; same bar as every F16 shape."""
+    check(mi, ctx, orc, "f16", M, N, K, seed=7)
+
+
+@pytest.mark.parametrize("K", [64, 147])
+def test_f16_src1_direct(mi, ctx, orc, K):
+    """F16 src1 (the explicit attention form multiplies f16 K by f16 Q); a K
+    that is not a multiple of 8 takes the padded copy of src1."""
+    N, M = 200, 150
     w = orc.normal(N * K, seed=5, stream=1).reshape(N, K).astype(np.float16)
     x = orc.normal(M * K, seed=5, stream=2).reshape(M, K).astype(np.float16)
     out = run_mul_mat(mi, ctx, w.view(np.uint16), orc.F16, K, N, x[None, None])[0, 0]
