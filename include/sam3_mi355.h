@@ -107,6 +107,14 @@ mi355_status mi355_mul_mat(mi355_context* ctx, const mi355_tensor* src0, const m
  * dst + r*row_size.  variant selects the from_float flavour. */
 mi355_status mi355_quantize_rows(mi355_context* ctx, int type, int variant, const mi355_tensor* src, void* dst);
 
+/* ---- weight quantize (ggml_quantize_chunk(type, src, dst, 0, nrows,
+ * n_per_row, NULL), examples/quantize.cpp:244-245: the _ref row quantizers
+ * quantize_row_q8_0_ref / q4_0_ref / q4_1_ref).  Every row of the F32 or F16
+ * tensor src (F16 widened to F32 exactly first, as sam3_quantize_model does
+ * at quantize.cpp:227-237) -> dst as contiguous ggml rows of type (Q8_0, Q4_0
+ * or Q4_1), row r at dst + r*row_size; dst 2-byte aligned. */
+mi355_status mi355_quantize_weights(mi355_context* ctx, int type, const mi355_tensor* src, void* dst);
+
 /* ---- Block-dot inspection (no ggml counterpart; test hook) ---------------
  * isums[b2][b3..][m][n][blk] = exact int32 block dots of the quantized
  * operands that mi355_mul_mat would combine, computed by the same MFMA
@@ -304,6 +312,26 @@ void mi355_vit_weights_free(mi355_vit_weights* w);
 mi355_status mi355_vit_weights_get(const mi355_vit_weights* w, mi355_vit_hparams* hp, const mi355_vit_block** blocks,
                                    int* n_blocks, const mi355_tensor** patch_w, const float** pos_embed,
                                    const float** ln_pre_w, const float** ln_pre_b);
+
+/* sam3_quantize_model (examples/quantize.cpp:20-331): copies the .ggml file
+ * in_path to out_path with the header's ftype set to qtype (Q4_0, Q4_1 or
+ * Q8_0) and every tensor that the reference quantizes rewritten by
+ * mi355_quantize_weights: 2-D or higher, ne0 a multiple of 32, F32 or F16,
+ * and not one of the embedding / table names the reference keeps (token_embed,
+ * pos_embed, freqs_cis, ...).  Header, hyperparameters (SAM3; SAM2 including
+ * the EdgeTAM extension), the other tensors and any bytes after the last
+ * tensor are copied unchanged; records are re-padded to 32-byte offsets.
+ * stats (may be NULL) receives the reference's summary counts.  Errors:
+ * unknown magic / bad arguments INVALID_ARG, unsupported version or tensor type
+ * UNSUPPORTED, I/O FAILED; unlike the reference a truncated input is an error,
+ * not a silently shortened output. */
+typedef struct mi355_quantize_stats {
+    int32_t n_quantized, n_total;
+    int64_t size_org;  /* F32-equivalent bytes of every tensor */
+    int64_t size_new;  /* data bytes written */
+} mi355_quantize_stats;
+mi355_status mi355_model_quantize(mi355_context* ctx, const char* in_path, const char* out_path, int32_t qtype,
+                                  mi355_quantize_stats* stats);
 
 /* Fusion in the encoder runners (no counterpart in the reference, whose graph
  * always materialises f32 activations; on by default).  When on, the passes

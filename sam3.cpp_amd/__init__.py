@@ -131,6 +131,8 @@ def lib():
         "mi355_supports_mul_mat": (I, [T, T, T]),
         "mi355_mul_mat": (I, [P, T, T, T]),
         "mi355_quantize_rows": (I, [P, I, I, T, P]),
+        "mi355_quantize_weights": (I, [P, I, T, P]),
+        "mi355_model_quantize": (I, [P, C.c_char_p, C.c_char_p, C.c_int32, C.POINTER(QuantizeStats)]),
         "mi355_mul_mat_block_dots": (I, [P, T, T, P]),
         "mi355_soft_max_ext": (I, [P, T, T, F, F, T]),
         "mi355_flash_attn_ext": (I, [P, T, T, T, T, F, F, F, T]),
@@ -174,6 +176,12 @@ def lib():
         fn.argtypes = args
     _lib = L
     return L
+
+
+class QuantizeStats(C.Structure):
+    """mi355_quantize_stats: sam3_quantize_model's summary counts."""
+    _fields_ = [("n_quantized", C.c_int32), ("n_total", C.c_int32), ("size_org", C.c_int64),
+                ("size_new", C.c_int64)]
 
 
 class ModelTensorInfo(C.Structure):
@@ -305,6 +313,16 @@ class Context:
 
     def quantize_rows(self, t: int, variant: int, src: Tensor, dst_ptr: int):
         self._check(self.L.mi355_quantize_rows(self.h, t, variant, C.byref(src), C.c_void_p(dst_ptr)))
+
+    def quantize_weights(self, t: int, src: Tensor, dst_ptr: int):
+        self._check(self.L.mi355_quantize_weights(self.h, t, C.byref(src), C.c_void_p(dst_ptr)))
+
+    def model_quantize(self, in_path, out_path, qtype: int) -> QuantizeStats:
+        """sam3_quantize_model: in_path -> out_path with qtype weights; returns the counts."""
+        st = QuantizeStats()
+        self._check(self.L.mi355_model_quantize(self.h, os.fsencode(str(in_path)), os.fsencode(str(out_path)), qtype,
+                                                C.byref(st)))
+        return st
 
     def soft_max_ext(self, src: Tensor, dst: Tensor, scale: float):
         self._check(self.L.mi355_soft_max_ext(self.h, C.byref(src), None, scale, 0.0, C.byref(dst)))

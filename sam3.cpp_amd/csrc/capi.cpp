@@ -572,6 +572,26 @@ mi355_status mi355_quantize_rows(mi355_context* ctx, int type, int variant, cons
                      "quantize launch");
 }
 
+mi355_status mi355_quantize_weights(mi355_context* ctx, int type, const mi355_tensor* src, void* dst) {
+    if (!src || !src->data || !dst) return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_weights: null argument");
+    if (!dims_ok(src)) return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_weights: negative ne/nb");
+    if (src->type != T_F32 && src->type != T_F16)
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "quantize_weights: src must be F32 or F16");
+    if (!(type == T_Q8_0 || type == T_Q4_0 || type == T_Q4_1))
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "quantize_weights: type %d not supported", type);
+    if (src->ne[0] % 32 != 0)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_weights: ne0 not a multiple of the block size");
+    const uintptr_t sa = reinterpret_cast<uintptr_t>(src->data) | (uintptr_t)src->nb[0] | (uintptr_t)src->nb[1] |
+                         (uintptr_t)src->nb[2] | (uintptr_t)src->nb[3];
+    if ((sa & (src->type == T_F32 ? 3 : 1)) || (reinterpret_cast<uintptr_t>(dst) & 1))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_weights: src elements and dst must be naturally aligned");
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "quantize_weights: null context");
+    (void)hipSetDevice(ctx->device);
+    Timed tq(ctx, "quantize_weights");
+    return hip_check(ctx, tq.done(launch_quantize_ggml(view_of(src), type, true, dst, ctx->stream)),
+                     "quantize_weights launch");
+}
+
 mi355_status mi355_soft_max_ext(mi355_context* ctx, const mi355_tensor* src, const mi355_tensor* mask, float scale,
                                 float max_bias, const mi355_tensor* dst) {
     if (!src || !dst || !src->data || !dst->data) return fail(ctx, MI355_STATUS_INVALID_ARG, "soft_max: null argument");

@@ -394,6 +394,227 @@ mi355_status mi355_vit_weights_load(mi355_context* ctx, const mi355_model_file* 
     return MI355_STATUS_SUCCESS;
 }
 
+}  // extern "C"
+
+// ---- sam3_quantize_model (examples/quantize.cpp:20-331) with the GPU quantizer
+
+namespace {
+
+// Tensors the reference keeps unquantized by name: the embeddings, lookup
+// tables, positional encodings and special tokens that sam3_register_tensors
+// registers as F32 (quantize.cpp:195-216).
+const char* const kKeepByName[] = {
+    "token_embed", "pos_embed", "query_embed", "label_embed", "cls_embed", "point_embeddings", "not_a_point_embed",
+    "no_mask_embed", "no_mem_embed", "no_obj_embed", "presence_token.weight", "iou_token", "mask_tokens",
+    "obj_score_token", "pe_gaussian", "freqs_cis", "gamma", "tpos_enc", "no_obj_ptr", "no_mem_pos_enc",
+    "trk_mask_ds", "latents"};
+
+bool keep_by_name(const std::string& name) {
+    for (const char* k : kKeepByName)
+        if (name.find(k) != std::string::npos) return true;
+    return false;
+}
+
+struct OutFile {
+    int fd = -1;
+    uint64_t pos = 0;
+    bool write(const void* p, size_t n) {
+        const char* c = static_cast<const char*>(p);
+        while (n > 0) {
+            const ssize_t w = ::write(fd, c, n);
+            if (w <= 0) return false;
+            c += w;
+            n -= (size_t)w;
+            pos += (uint64_t)w;
+        }
+        return true;
+    }
+};
+
+// pinned host staging, freed on scope exit
+struct Pinned {
+    void* p = nullptr;
+    ~Pinned() {
+        if (p) (void)hipHostFree(p);
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+mi355_status mi355_model_quantize(mi355_context* ctx, const char* in_path, const char* out_path, int32_t qtype,
+                                  mi355_quantize_stats* stats) {
+    if (!ctx || !in_path || !out_path) return fail(ctx, MI355_STATUS_INVALID_ARG, "model_quantize: null argument");
+    if (!(qtype == T_Q4_0 || qtype == T_Q4_1 || qtype == T_Q8_0))
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "model_quantize: type %d is not q4_0, q4_1 or q8_0", qtype);
+    (void)hipSetDevice(ctx->device);
+    const int in = open(in_path, O_RDONLY);
+    if (in < 0) return fail(ctx, MI355_STATUS_FAILED, "model_quantize: cannot open '%s' for reading", in_path);
+    OutFile out;
+    out.fd = open(out_path, O_WRONLY | O_CREAT | O_TRUNC, 0644);
+    if (out.fd < 0) {
+        close(in);
+        return fail(ctx, MI355_STATUS_FAILED, "model_quantize: cannot open '%s' for writing", out_path);
+    }
+    const uint64_t in_size = (uint64_t)lseek(in, 0, SEEK_END);
+    uint64_t pos = 0;
+    mi355_quantize_stats acc{};
+    Pinned hin, hout;
+    size_t hin_cap = 0, hout_cap = 0;
+    auto finish = [&](mi355_status st) {
+        close(in);
+        close(out.fd);
+        if (st != MI355_STATUS_SUCCESS) unlink(out_path);  // no half-written model
+        else if (stats) *stats = acc;
+        return st;
+    };
+    auto rd = [&](void* dst, size_t n) {
+        if (!read_at(in, pos, dst, n)) return false;
+        pos += n;
+        return true;
+    };
+    auto pinned = [&](Pinned& b, size_t& cap, size_t n) {
+        if (cap >= n) return true;
+        if (b.p) (void)hipHostFree(b.p);
+        b.p = nullptr;
+        cap = 0;
+        if (hipHostMalloc(&b.p, n, hipHostMallocDefault) != hipSuccess) return false;
+        cap = n;
+        return true;
+    };
+    // copy n bytes from the input's current position through the staging buffer
+    auto copy_through = [&](uint64_t n) -> mi355_status {
+        constexpr size_t kChunk = 16u << 20;
+        if (n > 0 && !pinned(hin, hin_cap, (size_t)std::min<uint64_t>(n, kChunk)))
+            return fail(ctx, MI355_STATUS_ALLOC_FAILED, "model_quantize: staging allocation failed");
+        while (n > 0) {
+            const size_t c = (size_t)std::min<uint64_t>(n, hin_cap);
+            if (!rd(hin.p, c)) return fail(ctx, MI355_STATUS_FAILED, "model_quantize: '%s' is truncated", in_path);
+            if (!out.write(hin.p, c)) return fail(ctx, MI355_STATUS_FAILED, "model_quantize: write to '%s' failed", out_path);
+            n -= c;
+        }
+        return MI355_STATUS_SUCCESS;
+    };
+
+    // header: magic, version, ftype (replaced by qtype), tensor count
+    int32_t hdr[4];
+    if (!rd(hdr, sizeof(hdr))) return finish(fail(ctx, MI355_STATUS_FAILED, "model_quantize: short header"));
+    const uint32_t magic = (uint32_t)hdr[0];
+    if (magic == kMagicSam3) {
+        if (hdr[1] != kVersionSam3)
+            return finish(fail(ctx, MI355_STATUS_UNSUPPORTED, "model_quantize: unsupported SAM3 version %d", hdr[1]));
+    } else if (magic == kMagicSam2) {
+        if (hdr[1] != kVersionSam2)
+            return finish(fail(ctx, MI355_STATUS_UNSUPPORTED, "model_quantize: unsupported SAM2 version %d", hdr[1]));
+    } else {
+        return finish(fail(ctx, MI355_STATUS_INVALID_ARG, "model_quantize: unknown magic 0x%08x", magic));
+    }
+    const int32_t n_tensors = hdr[3];
+    if (n_tensors < 0) return finish(fail(ctx, MI355_STATUS_INVALID_ARG, "model_quantize: negative tensor count"));
+    hdr[2] = qtype;
+    if (!out.write(hdr, sizeof(hdr))) return finish(fail(ctx, MI355_STATUS_FAILED, "model_quantize: write failed"));
+
+    // hyperparameters, copied through: SAM3 8 + min(n_global, 4) + 27 fields;
+    // SAM2 57, plus 19 for the EdgeTAM (RepViT, backbone_type 2) extension
+    {
+        int32_t h[8];
+        const size_t first = magic == kMagicSam3 ? 8 : 2;
+        if (!rd(h, first * 4)) return finish(fail(ctx, MI355_STATUS_FAILED, "model_quantize: short hyperparameters"));
+        if (!out.write(h, first * 4)) return finish(fail(ctx, MI355_STATUS_FAILED, "model_quantize: write failed"));
+        const uint64_t rest = magic == kMagicSam3 ? (uint64_t)std::min(std::max(h[7], 0), 4) + 27
+                                                  : 55 + (h[1] == 2 ? 19 : 0);
+        const mi355_status st = copy_through(rest * 4);
+        if (st != MI355_STATUS_SUCCESS) return finish(st);
+    }
+
+    for (int t = 0; t < n_tensors; ++t) {
+        int32_t h3[3];
+        if (!rd(h3, sizeof(h3))) return finish(fail(ctx, MI355_STATUS_FAILED, "model_quantize: '%s' is truncated", in_path));
+        const int32_t n_dims = h3[0], name_len = h3[1], dtype = h3[2];
+        if (n_dims < 1 || n_dims > 4 || name_len <= 0 || name_len > 4096)
+            return finish(fail(ctx, MI355_STATUS_INVALID_ARG, "model_quantize: bad tensor record %d", t));
+        int32_t ne[4] = {1, 1, 1, 1};
+        std::string name((size_t)name_len, '\0');
+        if (!rd(ne, 4 * (size_t)n_dims) || !rd(&name[0], name.size()))
+            return finish(fail(ctx, MI355_STATUS_FAILED, "model_quantize: '%s' is truncated", in_path));
+        pos += (32 - pos % 32) % 32;
+        int64_t n_el = 1, ne64[4];
+        for (int i = 0; i < 4; ++i) {
+            if (ne[i] <= 0)
+                return finish(fail(ctx, MI355_STATUS_INVALID_ARG, "model_quantize: '%s' has a non-positive dimension",
+                                   name.c_str()));
+            ne64[i] = ne[i];
+            n_el *= ne[i];
+        }
+        uint64_t in_bytes = 0;
+        if (!data_bytes(dtype, ne64, &in_bytes))
+            return finish(fail(ctx, MI355_STATUS_UNSUPPORTED, "model_quantize: '%s' has type %d", name.c_str(), dtype));
+        const bool quantize = n_dims >= 2 && ne[0] % 32 == 0 && (dtype == T_F32 || dtype == T_F16) && !keep_by_name(name);
+        const int32_t dtype_out = quantize ? qtype : dtype;
+        // record header with the output type, padded to a 32-byte offset of the output
+        std::string rec;
+        const int32_t h3o[3] = {n_dims, name_len, dtype_out};
+        rec.append(reinterpret_cast<const char*>(h3o), sizeof(h3o));
+        rec.append(reinterpret_cast<const char*>(ne), 4 * (size_t)n_dims);
+        rec.append(name);
+        rec.append((32 - (out.pos + rec.size()) % 32) % 32, '\0');
+        if (!out.write(rec.data(), rec.size())) return finish(fail(ctx, MI355_STATUS_FAILED, "model_quantize: write failed"));
+        uint64_t out_bytes = in_bytes;
+        if (!quantize) {
+            const mi355_status st = copy_through(in_bytes);
+            if (st != MI355_STATUS_SUCCESS) return finish(st);
+        } else {
+            // whole rows per chunk: file -> pinned -> device -> quantize -> pinned -> file
+            const int64_t rows = n_el / ne[0];
+            const size_t in_row = (size_t)ne[0] * (dtype == T_F32 ? 4 : 2);
+            const size_t out_row = row_size(qtype, ne[0]);
+            const int64_t chunk_rows = std::max<int64_t>(1, (int64_t)((32u << 20) / in_row));
+            const int64_t cr = std::min(rows, chunk_rows);
+            const size_t in_dev = (size_t)cr * in_row, dev_off = (in_dev + 255) & ~(size_t)255;
+            mi355_status st = ensure_buffer(ctx, &ctx->ws, &ctx->ws_size, dev_off + (size_t)cr * out_row);
+            if (st != MI355_STATUS_SUCCESS) return finish(st);
+            if (!pinned(hin, hin_cap, in_dev) || !pinned(hout, hout_cap, (size_t)cr * out_row))
+                return finish(fail(ctx, MI355_STATUS_ALLOC_FAILED, "model_quantize: staging allocation failed"));
+            char* dsrc = static_cast<char*>(ctx->ws);
+            char* ddst = dsrc + dev_off;
+            for (int64_t r0 = 0; r0 < rows; r0 += cr) {
+                const int64_t nr = std::min(cr, rows - r0);
+                if (!rd(hin.p, (size_t)nr * in_row))
+                    return finish(fail(ctx, MI355_STATUS_FAILED, "model_quantize: '%s' is truncated", in_path));
+                st = hip_check(ctx, hipMemcpyAsync(dsrc, hin.p, (size_t)nr * in_row, hipMemcpyHostToDevice, ctx->stream),
+                               "upload");
+                mi355_tensor src{};
+                src.type = dtype;
+                src.ne[0] = ne[0];
+                src.ne[1] = nr;
+                src.ne[2] = src.ne[3] = 1;
+                src.nb[0] = dtype == T_F32 ? 4 : 2;
+                src.nb[1] = (int64_t)in_row;
+                src.nb[2] = src.nb[3] = (int64_t)in_row * nr;
+                src.data = dsrc;
+                if (st == MI355_STATUS_SUCCESS) st = mi355_quantize_weights(ctx, qtype, &src, ddst);
+                if (st == MI355_STATUS_SUCCESS)
+                    st = hip_check(ctx, hipMemcpyAsync(hout.p, ddst, (size_t)nr * out_row, hipMemcpyDeviceToHost,
+                                                       ctx->stream),
+                                   "download");
+                if (st == MI355_STATUS_SUCCESS) st = hip_check(ctx, hipStreamSynchronize(ctx->stream), "quantize");
+                if (st != MI355_STATUS_SUCCESS) return finish(st);
+                if (!out.write(hout.p, (size_t)nr * out_row))
+                    return finish(fail(ctx, MI355_STATUS_FAILED, "model_quantize: write to '%s' failed", out_path));
+            }
+            out_bytes = (uint64_t)rows * out_row;
+            ++acc.n_quantized;
+        }
+        acc.size_new += (int64_t)out_bytes;
+        acc.size_org += n_el * 4;
+        ++acc.n_total;
+    }
+    // whatever follows the last tensor (the embedded tokenizer) is copied verbatim
+    if (pos > in_size) return finish(fail(ctx, MI355_STATUS_FAILED, "model_quantize: '%s' is truncated", in_path));
+    return finish(copy_through(in_size - pos));
+}
+
 mi355_status mi355_vit_weights_get(const mi355_vit_weights* w, mi355_vit_hparams* hp, const mi355_vit_block** blocks,
                                    int* n_blocks, const mi355_tensor** patch_w, const float** pos_embed,
                                    const float** ln_pre_w, const float** ln_pre_b) {

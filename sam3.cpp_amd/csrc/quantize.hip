@@ -6,6 +6,8 @@
 // wavefront quantizes 8 blocks.  The block's |x| max is reduced across its 8
 // lanes with a butterfly, every lane derives d and id itself (IEEE-correct
 // fp32 division), rounds its 4 values and writes 4 packed int8.
+#include <cfloat>
+
 #include "common.cuh"
 #include "kernels.h"
 
@@ -86,6 +88,114 @@ __global__ __launch_bounds__(256) void quantize_ggml_kernel(const char* __restri
             reinterpret_cast<uint16_t*>(blk)[0] = dh;
             reinterpret_cast<uint16_t*>(blk)[1] = f2h(d32 * (float)isum);
         }
+    }
+}
+
+// Weight quantizers quantize_row_q4_0_ref / quantize_row_q4_1_ref (what
+// ggml_quantize_chunk runs when no importance matrix is given), 8 lanes per
+// block as above, lane t holding elements 4t..4t+3.  The serial loops keep
+// the FIRST element on equal comparisons (strict < / >), which decides the
+// sign of Q4_0's d when +a and -a are both extreme and the sign of a zero
+// Q4_1 min; the cross-lane reduction therefore breaks ties by element index.
+// No multiply-add contraction: x*id + 8.5 and (x-min)*id + 0.5 round twice,
+// as the unfused C expressions do.
+template <int OUT>  // T_Q4_0 or T_Q4_1 (ggml layout)
+__global__ __launch_bounds__(256) void quantize_q4_kernel(const char* __restrict__ src, int stype, RowAddr ra,
+                                                          int64_t ne0, int64_t nblocks, uint8_t* __restrict__ dst) {
+#pragma clang fp contract(off)
+    const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t g = gt >> 3;
+    const int t = threadIdx.x & 7;
+    const bool valid = g < nblocks;
+    const int64_t nbpr = ne0 / QK;
+    const int64_t r = valid ? g / nbpr : 0;
+    const int64_t b = valid ? g % nbpr : 0;
+    float x[4] = {0.f, 0.f, 0.f, 0.f};
+    if (valid) {
+        const char* rp = ra.row(src, r);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = ld_elem(rp + (b * QK + 4 * t + j) * ra.nb0, stype);
+    }
+    float d, id, base, add;
+    uint16_t dh, mh = 0;
+    if (OUT == T_Q4_0) {
+        // max = the x of largest |x|
+        float amax = 0.0f, mx = 0.0f;
+        int ix = QK;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (amax < fabsf(x[j])) {
+                amax = fabsf(x[j]);
+                mx = x[j];
+                ix = 4 * t + j;
+            }
+#pragma unroll
+        for (int o = 4; o > 0; o >>= 1) {
+            const float oa = __shfl_xor(amax, o, 8), om = __shfl_xor(mx, o, 8);
+            const int oi = __shfl_xor(ix, o, 8);
+            if (oa > amax || (oa == amax && oi < ix)) {
+                amax = oa;
+                mx = om;
+                ix = oi;
+            }
+        }
+        d = mx / -8.0f;
+        base = 0.0f;
+        add = 8.5f;
+    } else {
+        float mn = FLT_MAX, mx = -FLT_MAX;
+        int imn = QK, imx = QK;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (x[j] < mn) {
+                mn = x[j];
+                imn = 4 * t + j;
+            }
+            if (x[j] > mx) {
+                mx = x[j];
+                imx = 4 * t + j;
+            }
+        }
+#pragma unroll
+        for (int o = 4; o > 0; o >>= 1) {
+            const float omn = __shfl_xor(mn, o, 8), omx = __shfl_xor(mx, o, 8);
+            const int oin = __shfl_xor(imn, o, 8), oix = __shfl_xor(imx, o, 8);
+            if (omn < mn || (omn == mn && oin < imn)) {
+                mn = omn;
+                imn = oin;
+            }
+            if (omx > mx || (omx == mx && oix < imx)) {
+                mx = omx;
+                imx = oix;
+            }
+        }
+        d = (mx - mn) / 15.0f;
+        base = mn;
+        add = 0.5f;
+        mh = f2h(mn);
+    }
+    id = d != 0.0f ? 1.0f / d : 0.0f;
+    dh = f2h(d);
+    uint32_t nib = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float v = (OUT == T_Q4_0 ? x[j] : x[j] - base) * id;
+        const int q = min((int)(v + add), 15);
+        nib |= (uint32_t)q << (8 * j);
+    }
+    // element j's nibble is low, element j+16's high: lanes 0..3 take lanes 4..7's values
+    const uint32_t hi = __shfl_xor(nib, 4, 8);
+    if (!valid || t >= 4) return;
+    const uint32_t bytes = nib | (hi << 4);
+    constexpr int BB = OUT == T_Q4_0 ? (int)sizeof(blk_q4_0) : (int)sizeof(blk_q4_1);
+    constexpr int QS = OUT == T_Q4_0 ? 2 : 4;
+    uint8_t* blk = dst + (r * nbpr + b) * (int64_t)BB;
+    uint16_t* q16 = reinterpret_cast<uint16_t*>(blk + QS + 4 * t);  // 2-byte aligned
+    q16[0] = (uint16_t)(bytes & 0xffffu);
+    q16[1] = (uint16_t)(bytes >> 16);
+    if (t == 0) {
+        reinterpret_cast<uint16_t*>(blk)[0] = dh;
+        if (OUT == T_Q4_1) reinterpret_cast<uint16_t*>(blk)[1] = mh;
     }
 }
 
@@ -178,6 +288,13 @@ hipError_t launch_quantize_ggml(const SrcView& src, int type, bool ref_variant, 
     const dim3 grid((unsigned)((nblocks * 8 + 255) / 256));
     const RowAddr ra = row_addr(src);
     uint8_t* out = static_cast<uint8_t*>(dst);
+    if (type == T_Q4_0 || type == T_Q4_1) {  // one (_ref) quantizer each
+        if (type == T_Q4_0)
+            quantize_q4_kernel<T_Q4_0><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, out);
+        else
+            quantize_q4_kernel<T_Q4_1><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, out);
+        return hipGetLastError();
+    }
     if (type == T_Q8_0 && !ref_variant)
         quantize_ggml_kernel<T_Q8_0, false><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, out);
     else if (type == T_Q8_0)

@@ -28,8 +28,9 @@ def sam2_hparams(img=1024, backbone=1, rest=None):
     return [img, backbone] + (list(rest) if rest is not None else [200 + i for i in range(55)])
 
 
-def write(path, magic, version, ftype, hparams, tensors, pad_byte=0):
-    """tensors: list of (name, ggml type, ne tuple (ggml order), raw bytes)."""
+def write(path, magic, version, ftype, hparams, tensors, pad_byte=0, tail=b""):
+    """tensors: list of (name, ggml type, ne tuple (ggml order), raw bytes);
+    tail: bytes after the last tensor (where sam3.cpp files keep the tokenizer)."""
     with open(path, "wb") as f:
         f.write(struct.pack("<Iiii", magic, version, ftype, len(tensors)))
         f.write(struct.pack(f"<{len(hparams)}i", *hparams))
@@ -41,3 +42,4 @@ def write(path, magic, version, ftype, hparams, tensors, pad_byte=0):
             pos = f.tell()
             f.write(bytes([pad_byte]) * ((32 - pos % 32) % 32))
             f.write(np.ascontiguousarray(data).tobytes())
+        f.write(tail)

@@ -72,6 +72,24 @@ def test_mul_mat_validation(mi):
     assert b"2-byte" in mi.lib().mi355_last_error(None)
 
 
+def test_quantize_weights_validation(mi):
+    L = mi.lib()
+    src = mi.make_tensor(0x1000, 0, [64, 4])
+    assert L.mi355_quantize_weights(None, 2, C.byref(src), C.c_void_p(0x2000)) == -4  # valid: null context
+    assert b"null context" in L.mi355_last_error(None)
+    assert L.mi355_quantize_weights(None, 9, C.byref(src), C.c_void_p(0x2000)) == -3  # q8_1 is an act type
+    assert L.mi355_quantize_weights(None, 1, C.byref(src), C.c_void_p(0x2000)) == -3  # f16 is not a quant type
+    src16 = mi.make_tensor(0x1000, 1, [64, 4])
+    assert L.mi355_quantize_weights(None, 3, C.byref(src16), C.c_void_p(0x2000)) == -4  # f16 src accepted
+    srcq = mi.make_tensor(0x1000, 8, [64, 4])
+    assert L.mi355_quantize_weights(None, 2, C.byref(srcq), C.c_void_p(0x2000)) == -3  # quantized src
+    src48 = mi.make_tensor(0x1000, 0, [48, 4])
+    assert L.mi355_quantize_weights(None, 8, C.byref(src48), C.c_void_p(0x2000)) == -4
+    assert b"block size" in L.mi355_last_error(None)
+    assert L.mi355_quantize_weights(None, 8, C.byref(src), C.c_void_p(0x2001)) == -4  # odd dst
+    assert L.mi355_model_quantize(None, b"a", b"b", 8, None) == -4
+
+
 def test_quantize_rows_validation(mi):
     L = mi.lib()
     src = mi.make_tensor(0x1000, 0, [64, 4])

@@ -145,6 +145,31 @@ def test_q4_1_kat(orc, kat):
         assert q[4:20].tolist() == case["qs"], case["name"]
 
 
+def test_q4_first_extreme_wins(orc):
+    """quantize_row_q4_0_ref / q4_1_ref scan with strict comparisons, so the
+    FIRST of equal extremes is kept.  Hand-derived blocks:
+    Q4_0 [2, -2, 0...]: max = +2, d = 2/-8 = -0.25 (fp16 0xb400), id = -4,
+    q = (int)(x*id + 8.5): 2 -> 0, -2 -> (int)16.5 = 16 -> 15, 0 -> 8;
+    [-2, 2, 0...]: max = -2, d = +0.25 (0x3400), id = 4: the same quants.
+    Q4_1 [-0.0, 0.0, 1, 0...]: min = -0.0 (0.0 < -0.0 is false), m = 0x8000;
+    d = 1/15 (fp16 0x2c44), id = 1/d = 14.999999, 1 -> (int)15.499999 = 15;
+    [0.0, -0.0, 1, ...] keeps m = +0.0 (0x0000)."""
+    z = np.zeros(32, np.float32)
+    a = z.copy(); a[0], a[1] = 2.0, -2.0
+    q = orc.quantize_weights(orc.Q4_0, a[None])[0]
+    assert q[0:2].view(np.uint16)[0] == 0xB400
+    assert q[2:18].tolist() == [0x80, 0x8F] + [0x88] * 14
+    b = z.copy(); b[0], b[1] = -2.0, 2.0
+    q = orc.quantize_weights(orc.Q4_0, b[None])[0]
+    assert q[0:2].view(np.uint16)[0] == 0x3400
+    assert q[2:18].tolist() == [0x80, 0x8F] + [0x88] * 14
+    for first, m in ((-0.0, 0x8000), (0.0, 0x0000)):
+        c = z.copy(); c[0], c[1], c[2] = first, -first, 1.0
+        q = orc.quantize_weights(orc.Q4_1, c[None])[0]
+        assert q[0:4].view(np.uint16).tolist() == [0x2C44, m]
+        assert q[4:20].tolist() == [0, 0, 15] + [0] * 13
+
+
 def test_q4_properties(orc):
     w = orc.normal(128 * 1024, seed=0, stream=11, std=0.02).reshape(128, 1024)
     wb = w.reshape(128, 32, 32)
