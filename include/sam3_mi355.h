@@ -263,6 +263,17 @@ mi355_status mi355_hiera_encode(mi355_context* ctx, const mi355_hiera_hparams* h
                                 const mi355_tensor* patch_w, const float* patch_b, const float* pos_embed,
                                 const mi355_hiera_block* blocks, int n_blocks, float* const stage_out[4]);
 
+/* sam2_compute_pos_embed (sam3.cpp:4076-4157) on the device: the pos_embed
+ * that mi355_hiera_encode adds, out [H*W][E] token-major (ggml [E, W, H]) =
+ * bicubic(bkg -> H x W; Keys a = -0.75, half-pixel centres, border-clamped
+ * taps, as torch's bicubic with align_corners=False) + the window table tiled
+ * modulo ws.  bkg [E][bkg_h][bkg_w] and win [E][ws][ws] are device F32 in the
+ * raw byte order of "hiera.pos_embed" ([bkg_w, bkg_h, E, 1]) and
+ * "hiera.pos_embed_window" ([ws, ws, E, 1]).  For SAM2.1 Hiera at 1024:
+ * bkg 7x7, ws 8, H = W = 256. */
+mi355_status mi355_hiera_pos_embed(mi355_context* ctx, const float* bkg, int E, int bkg_h, int bkg_w, const float* win,
+                                   int ws, int H, int W, float* out);
+
 /* ---- Model files (sam3.cpp's .ggml format) ----------------------------------
  * sam3_load_model / sam3_load_tensors (sam3.cpp:3095-3348): a header (magic
  * "sam3" 0x73616D33 version 3, or "sam2" 0x73616D32 version 1; ftype; tensor

@@ -26,6 +26,9 @@
  *   ViT glue ............. numpy restatements of torch LayerNorm/erf-GELU;
  *                           RoPE tables as closed forms (tests/test_vit.cpp:
  *                           182,192,218); win_part∘win_unpart = identity
+ *   Hiera pos-embed ...... torch bicubic interpolate (align_corners=False,
+ *                           A = -0.75); identity at equal sizes; constant
+ *                           and linear inputs reproduced in the interior
  */
 #define _GNU_SOURCE
 #include "ggml_oracle.h"
@@ -1078,6 +1081,47 @@ void orc_maxpool2(const float* x, float* y, int64_t C, int64_t W, int64_t H, int
                     if (v3 > m) m = v3;
                     y[((b * H2 + h) * W2 + w) * C + c] = m;
                 }
+}
+
+/* sam2_bicubic_interpolate_cpu + sam2_compute_pos_embed (sam3.cpp:4076-4157):
+ * Keys cubic convolution (a = -0.75), half-pixel source coordinates
+ * fy = (y + 0.5) * H_in / H_out - 0.5, taps clamped to the border, summed
+ * val += wy * wx * src in tap order (rows outer), plus the window table tiled
+ * modulo ws.  bkg [E][bh][bw] and win [E][ws][ws] are CHW; out is token-major
+ * [H*W][E] (ggml [E, W, H]). */
+static float keys_cubic(float x) {
+    x = fabsf(x);
+    if (x < 1.0f) return (1.25f * x - 2.25f) * x * x + 1.0f;
+    if (x < 2.0f) return ((-0.75f * x + 3.75f) * x - 6.0f) * x + 3.0f;
+    return 0.0f;
+}
+
+void orc_sam2_pos_embed(const float* bkg, int E, int bh, int bw, const float* win, int ws, int H, int W, float* out) {
+    for (int e = 0; e < E; ++e)
+        for (int y = 0; y < H; ++y) {
+            const float fy = ((float)y + 0.5f) * (float)bh / (float)H - 0.5f;
+            const int iy = (int)floorf(fy);
+            const float dy = fy - (float)iy;
+            for (int x = 0; x < W; ++x) {
+                const float fx = ((float)x + 0.5f) * (float)bw / (float)W - 0.5f;
+                const int ix = (int)floorf(fx);
+                const float dx = fx - (float)ix;
+                float val = 0.0f;
+                for (int jj = -1; jj <= 2; ++jj) {
+                    const float wy = keys_cubic(dy - (float)jj);
+                    int sy = iy + jj;
+                    sy = sy < 0 ? 0 : sy > bh - 1 ? bh - 1 : sy;
+                    for (int ii = -1; ii <= 2; ++ii) {
+                        const float wx = keys_cubic(dx - (float)ii);
+                        int sx = ix + ii;
+                        sx = sx < 0 ? 0 : sx > bw - 1 ? bw - 1 : sx;
+                        val += wy * wx * bkg[((int64_t)e * bh + sy) * bw + sx];
+                    }
+                }
+                const float t = win[((int64_t)e * ws + y % ws) * ws + x % ws];
+                out[((int64_t)y * W + x) * E + e] = val + t;
+            }
+        }
 }
 
 /* sam3.cpp:3559-3590: freqs[i] = 1/theta^(4i/dim), i < dim/4; token idx at

@@ -151,6 +151,9 @@ void orc_gelu_tanh(const float* x, float* y, int64_t n); /* ggml_gelu, fp16-tabl
 void orc_hiera_win_part(const float* x, float* y, int64_t C, int64_t W, int64_t H, int ws);
 void orc_hiera_win_unpart(const float* x, float* y, int64_t C, int64_t W, int64_t H, int ws);
 void orc_maxpool2(const float* x, float* y, int64_t C, int64_t W, int64_t H, int64_t B);
+/* sam2_compute_pos_embed (sam3.cpp:4076-4157): bicubic(bkg) + tiled window
+ * table; bkg [E][bh][bw], win [E][ws][ws] CHW; out [H*W][E]. */
+void orc_sam2_pos_embed(const float* bkg, int E, int bh, int bw, const float* win, int ws, int H, int W, float* out);
 void orc_compute_axial_cis(float* out, int dim, int end_x, int end_y, float theta, float scale_pos);
 /* x [hd, N, nh] rows; freqs [hd/2 pairs (cos,sin)] per token, [N][hd]. */
 void orc_apply_rope(float* x, const float* freqs, int64_t hd, int64_t n_tok, int64_t n_rows3);

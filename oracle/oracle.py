@@ -84,6 +84,7 @@ def lib():
             "orc_hiera_win_unpart": (None, [P, P, I64, I64, I64, I]),
             "orc_maxpool2": (None, [P, P, I64, I64, I64, I64]),
             "orc_compute_axial_cis": (None, [P, I, I, I, F, F]),
+            "orc_sam2_pos_embed": (None, [P, I, I, I, P, I, I, I, P]),
             "orc_apply_rope": (None, [P, P, I64, I64, I64]),
             "orc_win_part": (None, [P, P, I64, I64, I64, I]),
             "orc_win_unpart": (None, [P, P, I64, I64, I64, I]),
@@ -233,6 +234,17 @@ def flash_attn_ext(q: OrcTensor, k: OrcTensor, v: OrcTensor, D_v: int, scale: fl
 
 
 # ---------------------------------------------------------------- numpy block codecs
+def sam2_pos_embed(bkg: np.ndarray, win: np.ndarray, H: int, W: int) -> np.ndarray:
+    """bkg [E][bh][bw], win [E][ws][ws] float32 -> [H*W][E] (sam3.cpp:4118-4157)."""
+    bkg = np.ascontiguousarray(bkg, dtype=np.float32)
+    win = np.ascontiguousarray(win, dtype=np.float32)
+    E, bh, bw = bkg.shape
+    ws = win.shape[1]
+    out = np.empty((H * W, E), dtype=np.float32)
+    lib().orc_sam2_pos_embed(_p(bkg), E, bh, bw, _p(win), ws, H, W, _p(out))
+    return out
+
+
 def decode_blocks(t: int, q: np.ndarray, k: int):
     """Independent numpy decoder of the block bytes: (qvals int32 [rows,k], d f32 [rows,nb],
     extra f32 [rows,nb] (m for q4_1, s for q8_1, else zeros))."""

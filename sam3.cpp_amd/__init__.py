@@ -152,6 +152,7 @@ def lib():
         "mi355_hiera_encode": (I, [P, C.POINTER(HieraHparams), P, T, P, P, C.POINTER(HieraBlock), I,
                                    C.POINTER(P)]),
         "mi355_context_set_fusion": (I, [P, I]),
+        "mi355_hiera_pos_embed": (I, [P, P, I, I, I, P, I, I, I, P]),
         "mi355_model_file_open": (I, [C.c_char_p, C.POINTER(P)]),
         "mi355_model_file_close": (None, [P]),
         "mi355_model_file_last_error": (C.c_char_p, []),
@@ -313,6 +314,11 @@ class Context:
 
     def quantize_rows(self, t: int, variant: int, src: Tensor, dst_ptr: int):
         self._check(self.L.mi355_quantize_rows(self.h, t, variant, C.byref(src), C.c_void_p(dst_ptr)))
+
+    def hiera_pos_embed(self, bkg_ptr: int, E: int, bkg_h: int, bkg_w: int, win_ptr: int, ws: int, H: int, W: int,
+                        out_ptr: int):
+        self._check(self.L.mi355_hiera_pos_embed(self.h, C.c_void_p(bkg_ptr), E, bkg_h, bkg_w, C.c_void_p(win_ptr), ws,
+                                                 H, W, C.c_void_p(out_ptr)))
 
     def quantize_weights(self, t: int, src: Tensor, dst_ptr: int):
         self._check(self.L.mi355_quantize_weights(self.h, t, C.byref(src), C.c_void_p(dst_ptr)))

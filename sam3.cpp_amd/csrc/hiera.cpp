@@ -440,6 +440,18 @@ mi355_status run_block(mi355_context* ctx, const mi355_hiera_hparams* hp, const 
 
 extern "C" {
 
+mi355_status mi355_hiera_pos_embed(mi355_context* ctx, const float* bkg, int E, int bkg_h, int bkg_w, const float* win,
+                                   int ws, int H, int W, float* out) {
+    if (!bkg || !win || !out) return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera_pos_embed: null pointer");
+    if (E <= 0 || bkg_h <= 0 || bkg_w <= 0 || ws <= 0 || H <= 0 || W <= 0 || (int64_t)H * W * E >= ((int64_t)1 << 40))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera_pos_embed: bad sizes");
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "hiera_pos_embed: null context");
+    (void)hipSetDevice(ctx->device);
+    Timed t(ctx, "hiera_pos_embed");
+    return hip_check(ctx, t.done(launch_hiera_pos_embed(bkg, E, bkg_h, bkg_w, win, ws, H, W, out, ctx->stream)),
+                     "hiera_pos_embed launch");
+}
+
 int mi355_hiera_n_blocks(const mi355_hiera_hparams* hp) {
     std::vector<Info> infos;
     if (!hp || !block_infos(hp, infos)) return -1;

@@ -331,6 +331,58 @@ hipError_t launch_bias_add_pe(float* x, const float* b, const float* pe, int64_t
     if (rows * C > 0) bias_add_pe_kernel<<<nblk(rows * C), 256, 0, st>>>(x, b, pe, rows, C);
     return hipGetLastError();
 }
+// sam2_compute_pos_embed (sam3.cpp:4076-4157): Keys cubic convolution
+// (a = -0.75) of the background table at half-pixel source coordinates, taps
+// clamped to the border and summed rows-outer as val += wy*wx*src, plus the
+// window table tiled modulo ws.  One thread per output value, channel
+// fastest, so the token-major rows are written contiguously; the source
+// tables are a few KB and stay in cache.  No contraction: the same roundings
+// as the reference's C loop.
+__device__ __forceinline__ float keys_cubic(float x) {
+#pragma clang fp contract(off)
+    x = fabsf(x);
+    if (x < 1.0f) return (1.25f * x - 2.25f) * x * x + 1.0f;
+    if (x < 2.0f) return ((-0.75f * x + 3.75f) * x - 6.0f) * x + 3.0f;
+    return 0.0f;
+}
+
+__global__ __launch_bounds__(256) void hiera_pos_embed_kernel(const float* __restrict__ bkg, int E, int bh, int bw,
+                                                              const float* __restrict__ win, int ws, int H, int W,
+                                                              float* __restrict__ out) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)H * W * E) return;
+    const int e = (int)(i % E);
+    const int64_t tok = i / E;
+    const int y = (int)(tok / W), x = (int)(tok % W);
+    const float fy = ((float)y + 0.5f) * (float)bh / (float)H - 0.5f;
+    const int iy = (int)floorf(fy);
+    const float dy = fy - (float)iy;
+    const float fx = ((float)x + 0.5f) * (float)bw / (float)W - 0.5f;
+    const int ix = (int)floorf(fx);
+    const float dx = fx - (float)ix;
+    const float* src = bkg + (int64_t)e * bh * bw;
+    float val = 0.0f;
+#pragma unroll
+    for (int jj = -1; jj <= 2; ++jj) {
+        const float wy = keys_cubic(dy - (float)jj);
+        const int sy = min(max(iy + jj, 0), bh - 1);
+#pragma unroll
+        for (int ii = -1; ii <= 2; ++ii) {
+            const float wx = keys_cubic(dx - (float)ii);
+            const int sx = min(max(ix + ii, 0), bw - 1);
+            val += wy * wx * src[sy * bw + sx];
+        }
+    }
+    out[i] = val + win[((int64_t)e * ws + y % ws) * ws + x % ws];
+}
+
+hipError_t launch_hiera_pos_embed(const float* bkg, int E, int bh, int bw, const float* win, int ws, int H, int W,
+                                  float* out, hipStream_t st) {
+    const int64_t n = (int64_t)H * W * E;
+    if (n > 0) hiera_pos_embed_kernel<<<nblk(n), 256, 0, st>>>(bkg, E, bh, bw, win, ws, H, W, out);
+    return hipGetLastError();
+}
 hipError_t launch_f16_to_f32(const void* s, float* d, int64_t n, hipStream_t st) {
     if (n > 0) f16_to_f32_kernel<<<nblk(n), 256, 0, st>>>(static_cast<const uint16_t*>(s), d, n);
     return hipGetLastError();

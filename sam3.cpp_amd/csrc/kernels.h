@@ -226,5 +226,7 @@ hipError_t launch_im2col_pad(const float* img, float* cols, int C, int Hin, int 
                              int OH, int OW, bool round16, hipStream_t st);
 hipError_t launch_bias_add_pe(float* x, const float* b, const float* pe, int64_t rows, int C, hipStream_t st);
 hipError_t launch_f16_to_f32(const void* s, float* d, int64_t n, hipStream_t st);
+hipError_t launch_hiera_pos_embed(const float* bkg, int E, int bh, int bw, const float* win, int ws, int H, int W,
+                                  float* out, hipStream_t st);
 
 }  // namespace mi355

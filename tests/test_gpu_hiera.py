@@ -276,3 +276,19 @@ def test_hiera_block_fusion_bit_exact(mi, ctx, orc, tname, idx, S):
         ctx.set_fusion(True)
     assert np.isfinite(outs[0]).all()
     assert np.array_equal(outs[0], outs[1]), f"max diff {np.abs(outs[0] - outs[1]).max():.3e}"
+
+
+@pytest.mark.parametrize("E,bh,bw,ws,H,W", [(96, 7, 7, 8, 256, 256), (144, 7, 7, 8, 64, 64), (8, 5, 9, 3, 12, 10)])
+def test_hiera_pos_embed_bit_exact(mi, ctx, orc, E, bh, bw, ws, H, W):
+    """sam2_compute_pos_embed on the GPU (bicubic background + tiled window
+    table) equals the oracle bit for bit: same taps, same rounding order, no
+    contraction.  The oracle is pinned to torch's bicubic interpolate and to
+    the hand-worked kernel weights."""
+    rng = np.random.default_rng(E)
+    bkg = rng.standard_normal((E, bh, bw)).astype(np.float32)
+    win = rng.standard_normal((E, ws, ws)).astype(np.float32)
+    b, w = dev(bkg), dev(win)
+    out = torch.full((H * W, E), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.hiera_pos_embed(b.data_ptr(), E, bh, bw, w.data_ptr(), ws, H, W, out.data_ptr())
+    ctx.synchronize()
+    assert np.array_equal(out.cpu().numpy(), orc.sam2_pos_embed(bkg, win, H, W))

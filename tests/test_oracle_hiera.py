@@ -87,3 +87,51 @@ def test_maxpool2(orc):
     orc.lib().orc_maxpool2(x.ctypes.data, out.ctypes.data, C, W, H, B)
     ref = x.reshape(B, H // 2, 2, W // 2, 2, C).max(axis=(2, 4))
     assert np.array_equal(out, ref)
+
+
+def _tile(win, H, W):
+    E, ws, _ = win.shape
+    return np.tile(win, (1, H // ws + 1, W // ws + 1))[:, :H, :W]
+
+
+@pytest.mark.parametrize("E,bh,bw,ws,H,W", [(96, 7, 7, 8, 256, 256), (8, 7, 7, 8, 64, 48), (4, 5, 9, 3, 12, 10)])
+def test_sam2_pos_embed_vs_torch_bicubic(orc, E, bh, bw, ws, H, W):
+    """sam2_bicubic_interpolate_cpu mirrors torch's bicubic upsampling
+    (align_corners=False, A = -0.75, border-clamped taps): the oracle agrees
+    with torch.nn.functional.interpolate to float rounding, plus the window
+    table tiled modulo ws."""
+    import torch
+    rng = np.random.default_rng(E + H)
+    bkg = rng.standard_normal((E, bh, bw)).astype(np.float32)
+    win = rng.standard_normal((E, ws, ws)).astype(np.float32)
+    got = orc.sam2_pos_embed(bkg, win, H, W)
+    up = torch.nn.functional.interpolate(torch.from_numpy(bkg)[None], size=(H, W), mode="bicubic",
+                                         align_corners=False)[0].numpy()
+    ref = (up + _tile(win, H, W)).reshape(E, H * W).T
+    assert np.abs(got - ref).max() <= 2e-5 * (np.abs(bkg).max() + np.abs(win).max())
+
+
+def test_sam2_pos_embed_closed_forms(orc):
+    """Equal sizes: every source coordinate is an integer, the taps weigh
+    (0, 1, 0, 0) and the output is the input bit for bit.  A constant table
+    stays constant (the four weights sum to 1).  A unit impulse at (3, 3) of a
+    7x7 table upsampled 2x gives the separable kernel: source coordinate
+    f = y/2 - 0.25, out(y, x) = w(f_y - 3) w(f_x - 3) with the Keys weights
+    (a = -0.75) worked by hand: w(0.25) = 0.87890625, w(0.75) = 0.26171875,
+    w(1.25) = -0.10546875, w(1.75) = -0.03515625, 0 beyond 2."""
+    rng = np.random.default_rng(1)
+    E, n = 6, 9
+    bkg = rng.standard_normal((E, n, n)).astype(np.float32)
+    zero = np.zeros((E, 1, 1), np.float32)
+    got = orc.sam2_pos_embed(bkg, zero, n, n)
+    assert np.array_equal(got, bkg.reshape(E, -1).T)
+    const = np.full((E, 7, 7), 0.75, np.float32)
+    got = orc.sam2_pos_embed(const, zero, 40, 24)
+    assert np.abs(got - 0.75).max() <= 1e-6
+    imp = np.zeros((1, 7, 7), np.float32)
+    imp[0, 3, 3] = 1.0
+    got = orc.sam2_pos_embed(imp, np.zeros((1, 1, 1), np.float32), 14, 14).reshape(14, 14)
+    wtab = {0.25: 0.87890625, 0.75: 0.26171875, 1.25: -0.10546875, 1.75: -0.03515625}
+    w1 = np.array([wtab.get(abs(y / 2 - 0.25 - 3), 0.0) for y in range(14)])
+    assert np.count_nonzero(w1) == 8
+    assert np.abs(got - np.outer(w1, w1)).max() <= 1e-7
