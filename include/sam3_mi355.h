@@ -274,6 +274,49 @@ mi355_status mi355_hiera_encode(mi355_context* ctx, const mi355_hiera_hparams* h
 mi355_status mi355_hiera_pos_embed(mi355_context* ctx, const float* bkg, int E, int bkg_h, int bkg_w, const float* win,
                                    int ws, int H, int W, float* out);
 
+/* ---- SAM3 SimpleFPN neck ----------------------------------------------------
+ * sam3_build_neck_graph (sam3.cpp:3867-3925) on this backend.  Activations
+ * are device F32 token-major [H*W][C] (ggml [C, W, H]): the ViT output the
+ * neck reads (vit_out [E, W, H]) and the four maps it writes (the reference's
+ * out[i] after its final cont(permute(.., 1, 2, 0, 3))) are exactly the
+ * reference's layouts.  Kernels are the registered ggml tensors
+ * (sam3.cpp:2566-2600): conv-transpose [2, 2, Cout, Cin], conv [1, 1, Cin,
+ * Cout] and [3, 3, Cin, Cout], F32 or F16 (F32 under quantized ftypes: their
+ * ne0 of 1, 2 or 3 is not a block multiple), contiguous; biases F32.
+ * Numerics per op as ggml-cpu: conv-transpose with the kernel cast to F16 and
+ * the input converted to F16; conv_2d with the activations in the kernel's
+ * type; f32 accumulation; f32 bias adds; GELU-erf after scale 0's first
+ * conv-transpose. */
+typedef struct mi355_neck_scale {
+    const mi355_tensor* deconv1_w; /* scales 0 and 1: [2, 2, C1, E] */
+    const float* deconv1_b;
+    const mi355_tensor* deconv2_w; /* scale 0: [2, 2, D, C1] */
+    const float* deconv2_b;
+    const mi355_tensor* conv1x1_w; /* [1, 1, Cin, D] */
+    const float* conv1x1_b;
+    const mi355_tensor* conv3x3_w; /* [3, 3, D, D] */
+    const float* conv3x3_b;
+} mi355_neck_scale;
+/* Device bytes the neck keeps in the context for a G x G grid of E channels. */
+size_t mi355_neck_workspace_size(int E, int G, const mi355_neck_scale scales[4]);
+/* out[0] [(4G)^2][D], out[1] [(2G)^2][D], out[2] [G^2][D], out[3] [(G/2)^2][D]
+ * from x [G^2][E]; G even.  Scale 0: conv-transpose + GELU, conv-transpose,
+ * 1x1, 3x3; scale 1: conv-transpose, 1x1, 3x3; scale 2: 1x1, 3x3; scale 3:
+ * 2x2 max-pool, 1x1, 3x3; every conv adds its bias. */
+mi355_status mi355_sam3_neck(mi355_context* ctx, const float* x, int E, int G, const mi355_neck_scale scales[4],
+                             float* const out[4]);
+/* The neck's node groups on token-major activations, for other graph builders:
+ * ggml_conv_transpose_2d_p0(w [2, 2, Cout, Cin], x, 2) + bias (+ ggml_gelu_erf
+ * when gelu): x [H*W][Cin] -> y [(2H)*(2W)][Cout]; */
+mi355_status mi355_neck_deconv(mi355_context* ctx, const mi355_tensor* w, const float* b, const float* x, int H, int W,
+                               int gelu, float* y);
+/* ggml_conv_2d_sk_p0 (w [1, 1, Cin, Cout]) or ggml_conv_2d_s1_ph (w [3, 3, Cin,
+ * Cout]) + bias: x [H*W][Cin] -> y [H*W][Cout]; */
+mi355_status mi355_neck_conv(mi355_context* ctx, const mi355_tensor* w, const float* b, const float* x, int H, int W,
+                             float* y);
+/* ggml_pool_2d(MAX, 2, 2, 2, 2, 0, 0): x [H*W][C] -> y [(H/2)*(W/2)][C]. */
+mi355_status mi355_neck_maxpool(mi355_context* ctx, const float* x, int H, int W, int C, float* y);
+
 /* ---- Model files (sam3.cpp's .ggml format) ----------------------------------
  * sam3_load_model / sam3_load_tensors (sam3.cpp:3095-3348): a header (magic
  * "sam3" 0x73616D33 version 3, or "sam2" 0x73616D32 version 1; ftype; tensor

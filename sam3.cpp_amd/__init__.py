@@ -153,6 +153,11 @@ def lib():
                                    C.POINTER(P)]),
         "mi355_context_set_fusion": (I, [P, I]),
         "mi355_hiera_pos_embed": (I, [P, P, I, I, I, P, I, I, I, P]),
+        "mi355_neck_workspace_size": (SZ, [I, I, C.POINTER(NeckScale)]),
+        "mi355_sam3_neck": (I, [P, P, I, I, C.POINTER(NeckScale), C.POINTER(P)]),
+        "mi355_neck_deconv": (I, [P, T, P, P, I, I, I, P]),
+        "mi355_neck_conv": (I, [P, T, P, P, I, I, P]),
+        "mi355_neck_maxpool": (I, [P, P, I, I, I, P]),
         "mi355_model_file_open": (I, [C.c_char_p, C.POINTER(P)]),
         "mi355_model_file_close": (None, [P]),
         "mi355_model_file_last_error": (C.c_char_p, []),
@@ -177,6 +182,13 @@ def lib():
         fn.argtypes = args
     _lib = L
     return L
+
+
+class NeckScale(C.Structure):
+    """mi355_neck_scale: one SimpleFPN scale's kernels (mi355_tensor*) and biases."""
+    _fields_ = [("deconv1_w", C.c_void_p), ("deconv1_b", C.c_void_p), ("deconv2_w", C.c_void_p),
+                ("deconv2_b", C.c_void_p), ("conv1x1_w", C.c_void_p), ("conv1x1_b", C.c_void_p),
+                ("conv3x3_w", C.c_void_p), ("conv3x3_b", C.c_void_p)]
 
 
 class QuantizeStats(C.Structure):
@@ -319,6 +331,30 @@ class Context:
                         out_ptr: int):
         self._check(self.L.mi355_hiera_pos_embed(self.h, C.c_void_p(bkg_ptr), E, bkg_h, bkg_w, C.c_void_p(win_ptr), ws,
                                                  H, W, C.c_void_p(out_ptr)))
+
+    def neck_deconv(self, w: Tensor, b_ptr: int, x_ptr: int, H: int, W: int, gelu: bool, y_ptr: int):
+        self._check(self.L.mi355_neck_deconv(self.h, C.byref(w), C.c_void_p(b_ptr), C.c_void_p(x_ptr), H, W,
+                                             1 if gelu else 0, C.c_void_p(y_ptr)))
+
+    def neck_conv(self, w: Tensor, b_ptr: int, x_ptr: int, H: int, W: int, y_ptr: int):
+        self._check(self.L.mi355_neck_conv(self.h, C.byref(w), C.c_void_p(b_ptr), C.c_void_p(x_ptr), H, W,
+                                           C.c_void_p(y_ptr)))
+
+    def neck_maxpool(self, x_ptr: int, H: int, W: int, Cc: int, y_ptr: int):
+        self._check(self.L.mi355_neck_maxpool(self.h, C.c_void_p(x_ptr), H, W, Cc, C.c_void_p(y_ptr)))
+
+    def sam3_neck(self, x_ptr: int, E: int, G: int, scales, outs):
+        """scales: 4 dicts of Tensor kernels / bias pointers; outs: 4 device pointers."""
+        arr = (NeckScale * 4)()
+        keep = []
+        for i, s in enumerate(scales):
+            for f in ("deconv1", "deconv2", "conv1x1", "conv3x3"):
+                if s.get(f + "_w") is not None:
+                    keep.append(s[f + "_w"])
+                    setattr(arr[i], f + "_w", C.addressof(s[f + "_w"]))
+                    setattr(arr[i], f + "_b", s[f + "_b"])
+        o = (C.c_void_p * 4)(*outs)
+        self._check(self.L.mi355_sam3_neck(self.h, C.c_void_p(x_ptr), E, G, arr, o))
 
     def quantize_weights(self, t: int, src: Tensor, dst_ptr: int):
         self._check(self.L.mi355_quantize_weights(self.h, t, C.byref(src), C.c_void_p(dst_ptr)))

@@ -427,6 +427,7 @@ void mi355_context_free(mi355_context* ctx) {
     mi355_profile_reset(ctx);
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->enc) (void)hipFree(ctx->enc);
+    if (ctx->neck) (void)hipFree(ctx->neck);
     delete ctx;
 }
 

@@ -19,6 +19,8 @@ struct mi355_context {
     size_t ws_size = 0;
     void* enc = nullptr;       // activation buffers of the image-encoder runner
     size_t enc_size = 0;
+    void* neck = nullptr;      // maps and scratch of the SimpleFPN neck
+    size_t neck_size = 0;
     std::string last_error;
     // encoder runners: producer passes write the next MUL_MAT's operand
     bool fuse = true;

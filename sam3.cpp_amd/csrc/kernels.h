@@ -226,6 +226,13 @@ hipError_t launch_im2col_pad(const float* img, float* cols, int C, int Hin, int 
                              int OH, int OW, bool round16, hipStream_t st);
 hipError_t launch_bias_add_pe(float* x, const float* b, const float* pe, int64_t rows, int C, hipStream_t st);
 hipError_t launch_f16_to_f32(const void* s, float* d, int64_t n, hipStream_t st);
+// SimpleFPN neck passes (neck.hip); activations token-major [H*W][C]
+hipError_t launch_deconv_pack(const void* w, int wtype, int Cin, int Cout, uint16_t* out, hipStream_t st);
+hipError_t launch_deconv_scatter(const float* D, const float* b, int H, int W, int Cout, bool gelu, float* y,
+                                 hipStream_t st);
+hipError_t launch_im2col3x3(const float* x, int H, int W, int C, bool f16, void* cols, hipStream_t st);
+hipError_t launch_bias_rows(float* y, const float* b, int64_t rows, int C, hipStream_t st);
+hipError_t launch_maxpool2(const float* x, int H, int W, int C, float* y, hipStream_t st);
 hipError_t launch_hiera_pos_embed(const float* bkg, int E, int bh, int bw, const float* win, int ws, int H, int W,
                                   float* out, hipStream_t st);
 

@@ -1,0 +1,253 @@
+// SAM3 SimpleFPN neck (sam3_build_neck_graph, sam3.cpp:3867-3925) on the
+// MI355X backend.
+//
+// The reference permutes the ViT output to channel-planar [W, H, E], runs
+// ggml's convolutions (im2col + MUL_MAT, and conv_transpose_2d), and permutes
+// each result back to [C, W, H].  Here every activation stays token-major
+// [H*W][C] (= ggml [C, W, H], the layout of its input and outputs), so each
+// convolution is a MUL_MAT over pixels with no permutes:
+//   - conv_transpose_2d_p0 (kernel 2, stride 2): the taps do not overlap, so
+//     it is one F16 MUL_MAT [pixels x Cin] x [Cin x 4*Cout] (kernel cast to F16
+//     and repacked tap-major) whose columns are scattered to the 2x map, with
+//     the bias (and the GELU of scale 0) applied in the scatter;
+//   - conv_2d_sk_p0 1x1: a MUL_MAT with the kernel rows as they are;
+//   - conv_2d_s1_ph 3x3: im2col (K ordered as ggml's, ic-major) + MUL_MAT;
+//   - pool_2d MAX 2x2 / 2.
+// Each op's numerics are ggml-cpu's: operands in the kernel's type (F16
+// rounded to nearest even, or F32), f32 accumulation, f32 bias adds.
+#include <algorithm>
+
+#include "context.h"
+
+using namespace mi355;
+
+namespace {
+
+mi355_tensor dev_t(const void* p, int type, int64_t ne0, int64_t ne1) {
+    mi355_tensor t{};
+    t.type = type;
+    t.ne[0] = ne0;
+    t.ne[1] = ne1;
+    t.ne[2] = t.ne[3] = 1;
+    t.nb[0] = type == T_F32 ? 4 : 2;
+    t.nb[1] = t.nb[0] * ne0;
+    t.nb[2] = t.nb[3] = t.nb[1] * ne1;
+    t.data = const_cast<void*>(p);
+    return t;
+}
+
+bool contiguous(const mi355_tensor* w) {
+    const int64_t ts = w->type == T_F32 ? 4 : 2;
+    return w->nb[0] == ts && w->nb[1] == ts * w->ne[0] && w->nb[2] == w->nb[1] * w->ne[1] &&
+           w->nb[3] == w->nb[2] * w->ne[2];
+}
+
+mi355_status check_kernel(mi355_context* ctx, const mi355_tensor* w, const float* b, int k, const char* what) {
+    if (!w || !w->data || !b) return fail(ctx, MI355_STATUS_INVALID_ARG, "%s: null kernel or bias", what);
+    if (w->type != T_F32 && w->type != T_F16)
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "%s: kernel type %d (F32 or F16)", what, w->type);
+    if (w->ne[0] != k || w->ne[1] != k || w->ne[2] <= 0 || w->ne[3] <= 0 || !contiguous(w))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "%s: kernel must be a contiguous [%d, %d, C, C]", what, k, k);
+    return MI355_STATUS_SUCCESS;
+}
+
+// scratch bytes of each op (the MUL_MAT's own workspace is the context's)
+size_t deconv_scratch(int64_t P, int64_t Cin, int64_t Cout) {
+    return align_up((size_t)(4 * Cout * Cin * 2)) + align_up((size_t)(P * 4 * Cout * 4));
+}
+size_t conv_scratch(int64_t P, int64_t Cin, int k, int wtype) {
+    return k == 1 ? 0 : align_up((size_t)(P * 9 * Cin * (wtype == T_F32 ? 4 : 2)));
+}
+
+// conv_transpose_2d_p0(kernel [2, 2, Cout, Cin], stride 2) + bias (+ GELU):
+// x [H*W][Cin] -> y [(2H)*(2W)][Cout]
+mi355_status deconv(mi355_context* ctx, const mi355_tensor* w, const float* b, const float* x, int H, int W, bool gelu,
+                    float* y, char* scratch) {
+    mi355_status st = check_kernel(ctx, w, b, 2, "neck_deconv");
+    if (st != MI355_STATUS_SUCCESS) return st;
+    const int Cout = (int)w->ne[2], Cin = (int)w->ne[3];
+    const int64_t P = (int64_t)H * W;
+    if (Cout % 4 != 0) return fail(ctx, MI355_STATUS_UNSUPPORTED, "neck_deconv: Cout %% 4 != 0");
+    uint16_t* packed = reinterpret_cast<uint16_t*>(scratch);
+    float* D = reinterpret_cast<float*>(scratch + align_up((size_t)(4 * Cout * Cin * 2)));
+    {
+        Timed t(ctx, "neck_deconv_pack");
+        st = hip_check(ctx, t.done(launch_deconv_pack(w->data, w->type, Cin, Cout, packed, ctx->stream)), "deconv pack");
+        if (st != MI355_STATUS_SUCCESS) return st;
+    }
+    const mi355_tensor s0 = dev_t(packed, T_F16, Cin, 4LL * Cout), s1 = dev_t(x, T_F32, Cin, P),
+                       d = dev_t(D, T_F32, 4LL * Cout, P);
+    st = mi355_mul_mat(ctx, &s0, &s1, &d);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    Timed t(ctx, "neck_deconv_scatter");
+    return hip_check(ctx, t.done(launch_deconv_scatter(D, b, H, W, Cout, gelu, y, ctx->stream)), "deconv scatter");
+}
+
+// conv_2d_sk_p0 (1x1) or conv_2d_s1_ph (3x3) + bias: x [H*W][Cin] -> y [H*W][Cout]
+mi355_status conv(mi355_context* ctx, const mi355_tensor* w, const float* b, const float* x, int H, int W, float* y,
+                  char* scratch) {
+    if (!w) return fail(ctx, MI355_STATUS_INVALID_ARG, "neck_conv: null kernel");
+    const int k = (int)w->ne[0];
+    if (k != 1 && k != 3) return fail(ctx, MI355_STATUS_UNSUPPORTED, "neck_conv: kernel size %d (1 or 3)", k);
+    mi355_status st = check_kernel(ctx, w, b, k, "neck_conv");
+    if (st != MI355_STATUS_SUCCESS) return st;
+    const int Cin = (int)w->ne[2], Cout = (int)w->ne[3];
+    const int64_t P = (int64_t)H * W, K = (int64_t)k * k * Cin;
+    if (Cout % 4 != 0) return fail(ctx, MI355_STATUS_UNSUPPORTED, "neck_conv: Cout %% 4 != 0");
+    const mi355_tensor s0 = dev_t(w->data, w->type, K, Cout), d = dev_t(y, T_F32, Cout, P);
+    mi355_tensor s1 = dev_t(x, T_F32, Cin, P);
+    if (k == 3) {
+        // im2col in the kernel's type: F16 columns feed the F16 MUL_MAT directly
+        const bool f16 = w->type == T_F16;
+        Timed t(ctx, "neck_im2col3x3");
+        st = hip_check(ctx, t.done(launch_im2col3x3(x, H, W, Cin, f16, scratch, ctx->stream)), "im2col3x3");
+        if (st != MI355_STATUS_SUCCESS) return st;
+        s1 = dev_t(scratch, f16 ? T_F16 : T_F32, K, P);
+    }
+    st = mi355_mul_mat(ctx, &s0, &s1, &d);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    Timed t(ctx, "neck_bias");
+    return hip_check(ctx, t.done(launch_bias_rows(y, b, P, Cout, ctx->stream)), "bias");
+}
+
+mi355_status pool(mi355_context* ctx, const float* x, int H, int W, int C, float* y) {
+    if (C % 4 != 0) return fail(ctx, MI355_STATUS_UNSUPPORTED, "neck_maxpool: C %% 4 != 0");
+    Timed t(ctx, "neck_maxpool");
+    return hip_check(ctx, t.done(launch_maxpool2(x, H, W, C, y, ctx->stream)), "maxpool");
+}
+
+mi355_status scratch_for(mi355_context* ctx, size_t bytes, char** p) {
+    mi355_status st = ensure_buffer(ctx, &ctx->neck, &ctx->neck_size, std::max<size_t>(bytes, 256));
+    *p = static_cast<char*>(ctx->neck);
+    return st;
+}
+
+// Buffer plan of the whole neck: two map buffers plus the largest op scratch.
+struct NeckPlan {
+    size_t map = 0, scratch = 0;
+    size_t total() const { return 2 * map + scratch; }
+};
+
+bool neck_plan(int E, int G, const mi355_neck_scale* s, NeckPlan* pl) {
+    auto ok = [](const mi355_tensor* t) { return t && t->ne[2] > 0 && t->ne[3] > 0; };
+    for (int i = 0; i < 4; ++i)
+        if (!ok(s[i].conv1x1_w) || !ok(s[i].conv3x3_w) || (i < 2 && !ok(s[i].deconv1_w)) || (i == 0 && !ok(s[0].deconv2_w)))
+            return false;
+    const int64_t G2 = (int64_t)G * G;
+    auto mapb = [&](int64_t P, int64_t C) { pl->map = std::max(pl->map, align_up((size_t)(P * C * 4))); };
+    auto scr = [&](size_t b) { pl->scratch = std::max(pl->scratch, b); };
+    // scale 0: deconv E->C1 (2G), GELU, deconv C1->D (4G), 1x1, 3x3
+    const int64_t C1 = s[0].deconv1_w->ne[2], D0 = s[0].deconv2_w->ne[2];
+    mapb(4 * G2, C1);
+    mapb(16 * G2, D0);
+    mapb(16 * G2, s[0].conv1x1_w->ne[3]);
+    scr(deconv_scratch(G2, E, C1));
+    scr(deconv_scratch(4 * G2, C1, D0));
+    scr(conv_scratch(16 * G2, s[0].conv3x3_w->ne[2], 3, s[0].conv3x3_w->type));
+    // scale 1: deconv E->C1 (2G), 1x1, 3x3
+    const int64_t C1b = s[1].deconv1_w->ne[2];
+    mapb(4 * G2, C1b);
+    mapb(4 * G2, s[1].conv1x1_w->ne[3]);
+    scr(deconv_scratch(G2, E, C1b));
+    scr(conv_scratch(4 * G2, s[1].conv3x3_w->ne[2], 3, s[1].conv3x3_w->type));
+    // scale 2: 1x1, 3x3 at G; scale 3: pool, 1x1, 3x3 at G/2
+    mapb(G2, s[2].conv1x1_w->ne[3]);
+    scr(conv_scratch(G2, s[2].conv3x3_w->ne[2], 3, s[2].conv3x3_w->type));
+    mapb(G2 / 4, E);
+    mapb(G2 / 4, s[3].conv1x1_w->ne[3]);
+    scr(conv_scratch(G2 / 4, s[3].conv3x3_w->ne[2], 3, s[3].conv3x3_w->type));
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+mi355_status mi355_neck_deconv(mi355_context* ctx, const mi355_tensor* w, const float* b, const float* x, int H, int W,
+                               int gelu, float* y) {
+    if (!ctx || !x || !y) return fail(ctx, MI355_STATUS_INVALID_ARG, "neck_deconv: null argument");
+    if (H <= 0 || W <= 0) return fail(ctx, MI355_STATUS_INVALID_ARG, "neck_deconv: bad size");
+    mi355_status st = check_kernel(ctx, w, b, 2, "neck_deconv");
+    if (st != MI355_STATUS_SUCCESS) return st;
+    (void)hipSetDevice(ctx->device);
+    char* scr = nullptr;
+    st = scratch_for(ctx, deconv_scratch((int64_t)H * W, w->ne[3], w->ne[2]), &scr);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    return deconv(ctx, w, b, x, H, W, gelu != 0, y, scr);
+}
+
+mi355_status mi355_neck_conv(mi355_context* ctx, const mi355_tensor* w, const float* b, const float* x, int H, int W,
+                             float* y) {
+    if (!ctx || !x || !y || !w) return fail(ctx, MI355_STATUS_INVALID_ARG, "neck_conv: null argument");
+    if (H <= 0 || W <= 0) return fail(ctx, MI355_STATUS_INVALID_ARG, "neck_conv: bad size");
+    (void)hipSetDevice(ctx->device);
+    char* scr = nullptr;
+    const int k = (int)w->ne[0];
+    mi355_status st = scratch_for(ctx, k == 3 ? conv_scratch((int64_t)H * W, w->ne[2], 3, w->type) : 0, &scr);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    return conv(ctx, w, b, x, H, W, y, scr);
+}
+
+mi355_status mi355_neck_maxpool(mi355_context* ctx, const float* x, int H, int W, int C, float* y) {
+    if (!ctx || !x || !y) return fail(ctx, MI355_STATUS_INVALID_ARG, "neck_maxpool: null argument");
+    if (H <= 1 || W <= 1 || C <= 0) return fail(ctx, MI355_STATUS_INVALID_ARG, "neck_maxpool: bad size");
+    (void)hipSetDevice(ctx->device);
+    return pool(ctx, x, H, W, C, y);
+}
+
+size_t mi355_neck_workspace_size(int E, int G, const mi355_neck_scale scales[4]) {
+    NeckPlan pl;
+    if (!scales || E <= 0 || G <= 0 || !neck_plan(E, G, scales, &pl)) return 0;
+    return pl.total();
+}
+
+mi355_status mi355_sam3_neck(mi355_context* ctx, const float* x, int E, int G, const mi355_neck_scale scales[4],
+                             float* const out[4]) {
+    if (!ctx || !x || !scales || !out) return fail(ctx, MI355_STATUS_INVALID_ARG, "sam3_neck: null argument");
+    for (int i = 0; i < 4; ++i)
+        if (!out[i]) return fail(ctx, MI355_STATUS_INVALID_ARG, "sam3_neck: null output %d", i);
+    if (E <= 0 || G <= 1 || G % 2 != 0) return fail(ctx, MI355_STATUS_INVALID_ARG, "sam3_neck: bad E or grid");
+    NeckPlan pl;
+    if (!neck_plan(E, G, scales, &pl)) return fail(ctx, MI355_STATUS_INVALID_ARG, "sam3_neck: missing kernels");
+    // channel chain: each op's input channels are the previous op's outputs
+    const mi355_neck_scale* s = scales;
+    if (s[0].deconv1_w->ne[3] != E || s[0].deconv2_w->ne[3] != s[0].deconv1_w->ne[2] ||
+        s[0].conv1x1_w->ne[2] != s[0].deconv2_w->ne[2] || s[1].deconv1_w->ne[3] != E ||
+        s[1].conv1x1_w->ne[2] != s[1].deconv1_w->ne[2] || s[2].conv1x1_w->ne[2] != E || s[3].conv1x1_w->ne[2] != E)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "sam3_neck: kernel channels do not chain");
+    for (int i = 0; i < 4; ++i)
+        if (s[i].conv3x3_w->ne[2] != s[i].conv1x1_w->ne[3])
+            return fail(ctx, MI355_STATUS_INVALID_ARG, "sam3_neck: scale %d 3x3 input channels", i);
+    (void)hipSetDevice(ctx->device);
+    mi355_status st = ensure_buffer(ctx, &ctx->neck, &ctx->neck_size, pl.total());
+    if (st != MI355_STATUS_SUCCESS) return st;
+    char* base = static_cast<char*>(ctx->neck);
+    float* A = reinterpret_cast<float*>(base);
+    float* B = reinterpret_cast<float*>(base + pl.map);
+    char* scr = base + 2 * pl.map;
+#define TRY(e)                                     \
+    do {                                           \
+        st = (e);                                  \
+        if (st != MI355_STATUS_SUCCESS) return st; \
+    } while (0)
+    // scale 0 (4x): deconv + GELU, deconv, 1x1, 3x3
+    TRY(deconv(ctx, s[0].deconv1_w, s[0].deconv1_b, x, G, G, true, A, scr));
+    TRY(deconv(ctx, s[0].deconv2_w, s[0].deconv2_b, A, 2 * G, 2 * G, false, B, scr));
+    TRY(conv(ctx, s[0].conv1x1_w, s[0].conv1x1_b, B, 4 * G, 4 * G, A, scr));
+    TRY(conv(ctx, s[0].conv3x3_w, s[0].conv3x3_b, A, 4 * G, 4 * G, out[0], scr));
+    // scale 1 (2x): deconv, 1x1, 3x3
+    TRY(deconv(ctx, s[1].deconv1_w, s[1].deconv1_b, x, G, G, false, A, scr));
+    TRY(conv(ctx, s[1].conv1x1_w, s[1].conv1x1_b, A, 2 * G, 2 * G, B, scr));
+    TRY(conv(ctx, s[1].conv3x3_w, s[1].conv3x3_b, B, 2 * G, 2 * G, out[1], scr));
+    // scale 2 (1x): 1x1, 3x3
+    TRY(conv(ctx, s[2].conv1x1_w, s[2].conv1x1_b, x, G, G, A, scr));
+    TRY(conv(ctx, s[2].conv3x3_w, s[2].conv3x3_b, A, G, G, out[2], scr));
+    // scale 3 (0.5x): max-pool, 1x1, 3x3
+    TRY(pool(ctx, x, G, G, E, B));
+    TRY(conv(ctx, s[3].conv1x1_w, s[3].conv1x1_b, B, G / 2, G / 2, A, scr));
+    TRY(conv(ctx, s[3].conv3x3_w, s[3].conv3x3_b, A, G / 2, G / 2, out[3], scr));
+#undef TRY
+    return MI355_STATUS_SUCCESS;
+}
+
+}  // extern "C"
