@@ -250,6 +250,81 @@ def bench_hiera(mi, ctx, torch, hp, pre, blocks, outs, frames):
     return {"ms_per_frame": round(ms, 3), "frames": frames, "output_finite": finite, "kernel_ms_per_frame": split}
 
 
+def build_neck(mi, orc, torch, dev, tname, seed=0):
+    """SAM3 SimpleFPN neck at 1008^2: ViT output [72*72][1024] N(0,1), E = 1024,
+    C1 = 512, D = 256; kernels N(0, 0.02) in F32 (their type under quantized
+    ftypes) or F16, biases N(0, 0.02)."""
+    E, C1, D, G = 1024, 512, 256, 72
+    t = orc.NAME_TYPE[tname]
+    keep = []
+
+    def up(a):
+        x = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+        keep.append(x)
+        return x
+
+    def kern(j, n_el, ne):
+        w = orc.normal(n_el, seed, 600 + j, std=0.02)
+        if t == orc.F16:
+            w = w.astype(np.float16).view(np.uint16)
+        k = mi.from_torch(up(w), t, ne)
+        keep.append(k)
+        return k
+
+    def bias(j, n):
+        return up(orc.normal(n, seed, 650 + j, std=0.02)).data_ptr()
+
+    sc = [dict(deconv1_w=kern(0, 4 * C1 * E, [2, 2, C1, E]), deconv1_b=bias(0, C1),
+               deconv2_w=kern(1, 4 * D * C1, [2, 2, D, C1]), deconv2_b=bias(1, D),
+               conv1x1_w=kern(2, D * D, [1, 1, D, D]), conv1x1_b=bias(2, D),
+               conv3x3_w=kern(3, 9 * D * D, [3, 3, D, D]), conv3x3_b=bias(3, D)),
+          dict(deconv1_w=kern(4, 4 * C1 * E, [2, 2, C1, E]), deconv1_b=bias(4, C1),
+               conv1x1_w=kern(5, D * C1, [1, 1, C1, D]), conv1x1_b=bias(5, D),
+               conv3x3_w=kern(6, 9 * D * D, [3, 3, D, D]), conv3x3_b=bias(6, D))]
+    for i in range(2):
+        sc.append(dict(conv1x1_w=kern(7 + 2 * i, D * E, [1, 1, E, D]), conv1x1_b=bias(7 + 2 * i, D),
+                       conv3x3_w=kern(8 + 2 * i, 9 * D * D, [3, 3, D, D]), conv3x3_b=bias(8 + 2 * i, D)))
+    x = up(orc.normal(G * G * E, seed, 660))
+    outs = [torch.empty((n, D), dtype=torch.float32, device=dev) for n in (16 * G * G, 4 * G * G, G * G, G * G // 4)]
+    keep += outs
+    return (E, G), sc, x, outs, keep
+
+
+def neck_flops(E=1024, C1=512, D=256, G=72):
+    """Multiply-add work of one neck (2 per MAC): conv-transposes, 1x1, 3x3."""
+    P = G * G
+    dec = 2 * (P * E * 4 * C1 + 4 * P * C1 * 4 * D + P * E * 4 * C1)
+    c1 = 2 * (16 * P * D * D + 4 * P * C1 * D + P * E * D + P // 4 * E * D)
+    c3 = 2 * 9 * D * D * (16 * P + 4 * P + P + P // 4)
+    return dec + c1 + c3
+
+
+def bench_neck(mi, ctx, torch, dims, sc, x, outs, frames):
+    """ms per SimpleFPN neck (four maps from the ViT output), inputs resident in
+    HBM; plus one profiled run split by kernel."""
+    E, G = dims
+    ptrs = [o.data_ptr() for o in outs]
+    run = lambda: ctx.sam3_neck(x.data_ptr(), E, G, sc, ptrs)
+    run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(frames):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / frames
+    finite = all(bool(torch.isfinite(o).all().item()) for o in outs)
+    ctx.profile(True)
+    run()
+    pr = ctx.profile_collect()
+    ctx.profile(False)
+    split = {k: round(v[1], 3) for k, v in sorted(pr.items(), key=lambda kv: -kv[1][1])}
+    fl = neck_flops()
+    return {"ms_per_neck": round(ms, 3), "frames": frames, "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+            "gflop": round(fl / 1e9, 1), "output_finite": finite, "kernel_ms": split}
+
+
 def bench_encoder(mi, ctx, torch, dev, hp, pre, blocks, frames):
     """ms per frame of the whole encoder (prefix + 32 blocks), image resident in
     HBM; plus one profiled frame split by kernel."""
@@ -286,6 +361,7 @@ def main():
     ap.add_argument("--op", default=None,
                     help="profile mode, one workload --reps times with its kernel times: TYPE/LINEAR (e.g. q8_0/fc1), "
                          "attn/windowed, attn/global, vit/TYPE (SAM3 ViT frames), hiera/TYPE (Hiera-tiny frames), "
+                         "neck/f32|f16 (SAM3 SimpleFPN neck), "
                          "copy (256 MiB device copy)")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--op-warmup", type=int, default=20)
@@ -340,6 +416,13 @@ def main():
         tn = args.op.split("/")[1]
         hp, pre, blocks, outs, keep = build_hiera(mi, orc, torch, dev, tn)
         res = bench_hiera(mi, ctx, torch, hp, pre, blocks, outs, args.reps)
+        print(json.dumps({"op": args.op, **res}), flush=True)
+        ctx.close()
+        return
+    if args.op and args.op.startswith("neck/"):
+        tn = args.op.split("/")[1]
+        dims, sc, x, outs, keep = build_neck(mi, orc, torch, dev, tn)
+        res = bench_neck(mi, ctx, torch, dims, sc, x, outs, args.reps)
         print(json.dumps({"op": args.op, **res}), flush=True)
         ctx.close()
         return
@@ -446,6 +529,7 @@ def main():
     # ---- full SAM3 ViT encoder ms/frame, Q8_0 and Q4_0 weights
     encoder = None
     hiera = None
+    neck_res = None
     if not args.no_encoder:
         log("bench: encoder weights")
         del calls
@@ -462,6 +546,12 @@ def main():
             hp_h, pre_h, blocks_h, outs_h, keep_h = build_hiera(mi, orc, torch, dev, tn)
             hiera[tn] = bench_hiera(mi, ctx, torch, hp_h, pre_h, blocks_h, outs_h, 5)
             del keep_h
+        neck_res = {}
+        for tn in ("f32", "f16"):
+            log(f"bench: neck {tn}")
+            dims, sc, xn, outs_n, keep_n = build_neck(mi, orc, torch, dev, tn)
+            neck_res[tn] = bench_neck(mi, ctx, torch, dims, sc, xn, outs_n, 3)
+            del keep_n
 
     # ---- CPU baseline: the oracle's ggml-cpu restatement, same fc1 Q8_0 mul_mat
     cpu = None
@@ -506,6 +596,7 @@ def main():
         "cpu_baseline": cpu,
         "vit_encoder_1008": encoder,
         "hiera_tiny_1024": hiera,
+        "sam3_neck_1008": neck_res,
         "attention": attn,
     }
     print(json.dumps(out), flush=True)

@@ -396,6 +396,13 @@ mi355_status mi355_model_quantize(mi355_context* ctx, const char* in_path, const
  * unpartition; the ViT's qkv split + RoPE).  Off gives the unfused sequence
  * of node groups, for parity checks: both produce the same bits. */
 mi355_status mi355_context_set_fusion(mi355_context* ctx, int enable);
+/* The skinny MUL_MAT kernel (no counterpart in the reference; on by default):
+ * GEMMs with K <= 128 over at least 4096 activation rows (SAM2 Hiera's stage-1
+ * projections, K = 96) run on a kernel that keeps the whole weight matrix in
+ * LDS and streams the activation rows; it computes every output with the
+ * tiled kernel's instruction sequence, so both give the same bits.  Off
+ * routes them to the tiled kernel (for comparisons). */
+mi355_status mi355_context_set_skinny(mi355_context* ctx, int enable);
 
 /* ---- Kernel timing --------------------------------------------------------
  * The device-side counterpart of the reference's timing around graph compute

@@ -152,6 +152,7 @@ def lib():
         "mi355_hiera_encode": (I, [P, C.POINTER(HieraHparams), P, T, P, P, C.POINTER(HieraBlock), I,
                                    C.POINTER(P)]),
         "mi355_context_set_fusion": (I, [P, I]),
+        "mi355_context_set_skinny": (I, [P, I]),
         "mi355_hiera_pos_embed": (I, [P, P, I, I, I, P, I, I, I, P]),
         "mi355_neck_workspace_size": (SZ, [I, I, C.POINTER(NeckScale)]),
         "mi355_sam3_neck": (I, [P, P, I, I, C.POINTER(NeckScale), C.POINTER(P)]),
@@ -391,6 +392,9 @@ class Context:
     def set_fusion(self, enable: bool):
         """Encoder runners: producer passes write the MUL_MAT operand (default) or f32 rows."""
         self._check(self.L.mi355_context_set_fusion(self.h, 1 if enable else 0))
+
+    def set_skinny(self, on: bool):
+        self._check(self.L.mi355_context_set_skinny(self.h, 1 if on else 0))
 
     def profile(self, enable: bool):
         self._check(self.L.mi355_profile_enable(self.h, 1 if enable else 0))

@@ -282,7 +282,8 @@ mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF1
         st = ensure_ws(ctx, align + part);
         if (st != MI355_STATUS_SUCCESS) return st;
     }
-    const MmqSplit sp{ks, ks > 1 ? reinterpret_cast<float*>(static_cast<char*>(ctx->ws) + align) : nullptr};
+    const MmqSplit sp{ks, ks > 1 ? reinterpret_cast<float*>(static_cast<char*>(ctx->ws) + align) : nullptr,
+                      ctx->skinny};
     static const char* names[4][3] = {{"mmq_f16", "mmq_f16+residual", "mmq_f16+qkv"},
                                       {"mmq_q8_0", "mmq_q8_0+residual", "mmq_q8_0+qkv"},
                                       {"mmq_q4_0", "mmq_q4_0+residual", "mmq_q4_0+qkv"},
@@ -512,7 +513,7 @@ mi355_status mi355_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
     void* align_buf = pl.align ? static_cast<char*>(ctx->ws) + pl.q + pl.d + pl.s : nullptr;
     const MmqSplit sp{pl.ks, pl.ks > 1 ? reinterpret_cast<float*>(static_cast<char*>(ctx->ws) + pl.q + pl.d + pl.s +
                                                                   pl.align)
-                                       : nullptr};
+                                       : nullptr, ctx->skinny};
     const char* kname = s0->type == T_F16 ? "mmq_f16" : s0->type == T_Q8_0 ? "mmq_q8_0" : s0->type == T_Q4_0 ? "mmq_q4_0" : "mmq_q4_1";
     Timed tq(ctx, kname);
     return hip_check(ctx, tq.done(launch_mmq(matw_of(s0), a, matd_of(d), N, s1->ne[2], s1->ne[3], nullptr, align_buf,
@@ -611,6 +612,12 @@ mi355_status mi355_soft_max_ext(mi355_context* ctx, const mi355_tensor* src, con
 mi355_status mi355_context_set_fusion(mi355_context* ctx, int enable) {
     if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "set_fusion: null context");
     ctx->fuse = enable != 0;
+    return MI355_STATUS_SUCCESS;
+}
+
+mi355_status mi355_context_set_skinny(mi355_context* ctx, int enable) {
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "set_skinny: null context");
+    ctx->skinny = enable != 0;
     return MI355_STATUS_SUCCESS;
 }
 

@@ -24,6 +24,8 @@ struct mi355_context {
     std::string last_error;
     // encoder runners: producer passes write the next MUL_MAT's operand
     bool fuse = true;
+    // MUL_MATs with K <= 128 at large M take the skinny kernel
+    bool skinny = true;
     // kernel timing
     bool prof = false;
     struct Pending { const char* name; hipEvent_t a, b; };

@@ -28,6 +28,8 @@
 // them (byte -> 0x64XX half -> packed f16 subtract).  Workgroups are
 // numbered so each XCD (round-robin dispatch) walks n-tiles of its own band
 // of m-tiles.
+#include <algorithm>
+
 #include "common.cuh"
 #include "kernels.h"
 
@@ -620,8 +622,301 @@ int mmq_ksplit(int type, int64_t M, int64_t N, int64_t K, int64_t Z, int cus) {
     return best;
 }
 
+// ---- Skinny GEMMs: K <= 128 at large M (the Hiera stage-1 projections, K = 96)
+//
+// Output writes dominate these (M x N f32 against an M x K fp16 operand),
+// while a 128x128 tile of mmq_kernel runs only two K stages, re-reads the
+// activations for every n-tile and spends most of its time in prologue and
+// epilogue.  Here one workgroup computes all N columns of 64 or 128
+// activation rows: it copies the whole quantized weight matrix into LDS
+// (raw rows, 16-byte loads, eight in flight per thread) while its activation
+// rows are in flight, then each wavefront walks n-tiles and writes each
+// 32x32 output tile through LDS as float4 row segments.  A workgroup holds
+// one row block and ends after its stores are issued, so the stores of one
+// overlap the loads of the next (on gfx9 a wait for loads also waits for
+// every earlier store).  A 32x32 tile is computed with mmq_kernel's
+// instructions on the same operands (integer block sums by two MFMAs, the
+// d_a (x) d_w outer product by one, acc = fma(isum, S, acc) in block order,
+// the Q4_1 offset term by MFMA per pair of blocks), so the results are
+// bit-identical to mmq_kernel's.  F16 weights stay on mmq_kernel: at 2 bytes
+// per element their LDS copy leaves one workgroup per CU, and the tiled
+// kernel is faster there.
+namespace {
+constexpr int SKMAX = 128;  // largest K
+}  // namespace
+
+struct SkinnyArgs {
+    const uint8_t* W;
+    int64_t w_nb1;             // weight row stride (bytes, even)
+    const _Float16* A;         // activation operand rows, stride a_s1 halves (16-byte aligned)
+    int64_t a_s1;
+    const _Float16* Ad;        // [M][dp] scales (quantized path)
+    const _Float16* As;        // [M][dp] Q8_1 sums (Q4_1)
+    float* D;
+    int64_t d_nb1;
+    int M, N, K, dp, npad;     // npad: N rounded up to 32
+    int wpitch;                // LDS bytes per weight row (the raw row size)
+};
+
+template <int WT, int SMT>  // SMT: 32-row MFMA tiles per workgroup (2 or 4)
+__global__ __launch_bounds__(256, 2) void mmq_skinny_kernel(const SkinnyArgs p) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int SBM = 32 * SMT;  // activation rows of this workgroup
+    constexpr int WB = WInfo<WT>::bytes, HDR = WInfo<WT>::hdr;
+    constexpr int NA = SKMAX / 8 * SBM / 256;  // activation chunks per thread (at most)
+    const int K = p.K, PA = K + 8, nb = K / QK, dp = p.dp, M = p.M, N = p.N;
+    const int CPR = K / 8;          // 16-byte chunks per activation row
+    const int ACH = SBM * CPR;      // chunks of the activation block
+    const int SCH = SBM * dp / 8;   // 16-byte chunks of its scales
+    // LDS: weights | activations [SBM][PA] | scales [SBM][dp] | sums [SBM][dp] | output staging [4][32][32]
+    uint8_t* Wl = smem;
+    _Float16* Al = reinterpret_cast<_Float16*>(smem + ((p.npad * p.wpitch + 16 + 15) & ~15));
+    uint16_t* Adl = reinterpret_cast<uint16_t*>(Al + SBM * PA);
+    uint16_t* Asl = Adl + SBM * dp;
+    float* Ol = reinterpret_cast<float*>(Asl + SBM * dp);
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool lo = lane < 32;
+    const int m0 = blockIdx.x * SBM;
+
+    // this block's activation rows and scales into registers (in flight during the weight copy)
+    uint4 ra[NA], rd = {0, 0, 0, 0}, rs = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+        const int c = tid + 256 * i;
+        const int r = c / CPR, c8 = c - r * CPR;
+        ra[i] = c < ACH && m0 + r < M ? *reinterpret_cast<const uint4*>(p.A + (int64_t)(m0 + r) * p.a_s1 + 8 * c8)
+                                      : uint4{0, 0, 0, 0};
+    }
+    if (tid < SCH) {
+        const int64_t o = (int64_t)m0 * dp + 8 * tid, end = (int64_t)M * dp;
+        if (o + 8 <= end) {
+            rd = *reinterpret_cast<const uint4*>(p.Ad + o);
+            if (WT == T_Q4_1) rs = *reinterpret_cast<const uint4*>(p.As + o);
+        } else {  // the block's last rows run past M: element loads up to the end
+            uint16_t hd[8], hs[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                hd[e] = o + e < end ? reinterpret_cast<const uint16_t*>(p.Ad)[o + e] : (uint16_t)0;
+                hs[e] = WT == T_Q4_1 && o + e < end ? reinterpret_cast<const uint16_t*>(p.As)[o + e] : (uint16_t)0;
+            }
+            rd = __builtin_bit_cast(uint4, hd);
+            rs = __builtin_bit_cast(uint4, hs);
+        }
+    }
+
+    // weights from contiguous rows (16-byte aligned base), 16-byte chunks with eight
+    // loads in flight per thread (indices clamped, stores guarded), unpadded: row n
+    // at byte n * wpitch
+    {
+        const int rowb = nb * WB;
+        const int nch = (N * rowb) / 16;
+        const uint4* src = reinterpret_cast<const uint4*>(p.W);
+        for (int c0 = 0; c0 < nch; c0 += 8 * 256) {
+            uint4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = src[min(c0 + u * 256 + tid, nch - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int c = c0 + u * 256 + tid;
+                if (c < nch) *reinterpret_cast<uint4*>(Wl + 16 * c) = v[u];
+            }
+        }
+        uint16_t* L16 = reinterpret_cast<uint16_t*>(Wl);
+        const uint16_t* W16 = reinterpret_cast<const uint16_t*>(p.W);
+        // the tail by halves, then zero rows up to npad
+        for (int h = 8 * nch + tid; h < N * rowb / 2; h += 256) L16[h] = W16[h];
+        for (int h = N * rowb / 2 + tid; h < p.npad * p.wpitch / 2; h += 256) L16[h] = 0;
+    }
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+        const int c = tid + 256 * i;
+        if (c < ACH) {
+            const int r = c / CPR, c8 = c - r * CPR;
+            *reinterpret_cast<uint4*>(&Al[r * PA + 8 * c8]) = ra[i];
+        }
+    }
+    if (tid < SCH) {
+        *reinterpret_cast<uint4*>(&Adl[8 * tid]) = rd;
+        if (WT == T_Q4_1) *reinterpret_cast<uint4*>(&Asl[8 * tid]) = rs;
+    }
+    __syncthreads();
+
+    const v16f zf = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const uint32_t* As32 = reinterpret_cast<const uint32_t*>(Asl);
+    auto fa = [&](int r, int c) { return *reinterpret_cast<const v8h*>(&Al[r * PA + 8 * c]); };
+    float* stg = Ol + wv * 32 * 32;  // this wavefront's 32x32 staging tile
+    const bool v4 = (p.d_nb1 & 15) == 0 && (reinterpret_cast<uintptr_t>(p.D) & 15) == 0;
+    for (int j = wv; j < p.npad / 32; j += 4) {
+        const int n = 32 * j + lr;  // this lane's weight row
+        v16f acc[SMT];
+#pragma unroll
+        for (int mt = 0; mt < SMT; ++mt) acc[mt] = zf;
+        {
+            // row n starts at byte n * wpitch (even): dwords are read from the LDS base, with
+            // lds_dw2 aligning a half-dword offset
+            const uint32_t* rowp = reinterpret_cast<const uint32_t*>(Wl);
+            const int rb0 = n * p.wpitch;
+            const uint16_t* hrow = reinterpret_cast<const uint16_t*>(Wl + rb0);
+            for (int s = 0; s < (nb + 1) / 2; ++s) {
+                if (WT == T_Q4_1) {
+                    const uint32_t m1 = 2 * s + 1 < nb ? (uint32_t)hrow[(2 * s + 1) * WB / 2 + 1] << 16 : 0u;
+                    const v4i mwf = {lo ? (int)((uint32_t)hrow[s * WB + 1] | m1) : 0, 0, 0, 0};
+#pragma unroll
+                    for (int mt = 0; mt < SMT; ++mt) {
+                        const int ar = mt * 32 + lr;
+                        v4i saf = __builtin_bit_cast(v4i, fa(ar, 8 * s + g));  // finite filler
+                        saf[0] = (int)As32[ar * dp / 2 + s];
+                        acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, saf),
+                                                                         __builtin_bit_cast(v8h, mwf), acc[mt], 0, 0, 0);
+                    }
+                }
+                for (int bk = 2 * s; bk < 2 * s + 2 && bk < nb; ++bk) {
+                    v8h bf[2];
+                    const int o = rb0 + bk * WB + HDR;
+                    if (WT == T_Q8_0) {
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            uint32_t w0, w1;
+                            lds_dw2(rowp, o + 16 * h + 8 * g, o & 3, w0, w1);
+                            bf[h] = i8x8_to_h8(w0, w1);
+                        }
+                    } else {
+                        uint32_t w0, w1;
+                        lds_dw2(rowp, o + 8 * g, o & 3, w0, w1);
+                        const _Float16 bias = WT == T_Q4_0 ? (_Float16)1032.0f : (_Float16)1024.0f;
+                        bf[0] = n8_to_h8(w0 & 0x0f0f0f0fu, w1 & 0x0f0f0f0fu, bias);
+                        bf[1] = n8_to_h8((w0 >> 4) & 0x0f0f0f0fu, (w1 >> 4) & 0x0f0f0f0fu, bias);
+                    }
+                    const v4i dwf = {lo ? (int)(uint32_t)hrow[bk * WB / 2] : 0, 0, 0, 0};
+#pragma unroll
+                    for (int mt = 0; mt < SMT; ++mt) {
+                        const int ar = mt * 32 + lr;
+                        const v8h a0 = fa(ar, 4 * bk + g), a1 = fa(ar, 4 * bk + 2 + g);
+                        v16f I = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bf[0], zf, 0, 0, 0);
+                        I = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bf[1], I, 0, 0, 0);
+                        v4i daf = __builtin_bit_cast(v4i, a1);
+                        daf[0] = (int)(uint32_t)Adl[ar * dp + bk];
+                        const v16f S = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, daf),
+                                                                              __builtin_bit_cast(v8h, dwf), zf, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) acc[mt][i] = __builtin_fmaf(I[i], S[i], acc[mt][i]);
+                    }
+                }
+            }
+        }
+        // 32x32 tiles through this wavefront's staging area: rows of 32 floats go out as
+        // eight float4 (one 128-byte line per row)
+        const int rr = lane >> 3, cc = 4 * (lane & 7), nc = 32 * j + cc;
+#pragma unroll
+        for (int mt = 0; mt < SMT; ++mt) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) stg[(8 * (i >> 2) + 4 * g + (i & 3)) * 32 + lr] = acc[mt][i];
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int m = m0 + mt * 32 + 8 * q + rr;
+                const v4f val = *reinterpret_cast<const v4f*>(&stg[(8 * q + rr) * 32 + cc]);
+                if (m < M) {
+                    float* dst = reinterpret_cast<float*>(reinterpret_cast<char*>(p.D) + (int64_t)m * p.d_nb1) + nc;
+                    if (v4 && nc + 4 <= N) {
+                        *reinterpret_cast<v4f*>(dst) = val;
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (nc + e < N) dst[e] = val[e];
+                    }
+                }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next tile overwrites
+        }
+    }
+}
+
+// LDS bytes of the skinny kernel with SMT row tiles, or 0 when the GEMM does not fit it.
+static size_t skinny_lds(int type, int64_t N, int64_t K, int dp, int smt, int* wpitch) {
+    if (K <= 0 || K > SKMAX || K % QK != 0 || N <= 0 || N > 1024) return 0;
+    const int64_t wp = (K / QK) * (type == T_Q8_0 ? 34 : type == T_Q4_0 ? 18 : 20);
+    const int64_t npad = (N + 31) / 32 * 32, sbm = 32 * smt;
+    // weights (+16 bytes: the last row's fragment reads run up to 12 bytes past it), rounded to 16;
+    // activations, scales and sums; four 32x32 f32 output staging tiles
+    const size_t wbytes = ((size_t)(npad * wp) + 16 + 15) & ~(size_t)15;
+    const size_t bytes = wbytes + sbm * (K + 8) * 2 + 2 * sbm * dp * 2 + 4 * 32 * 32 * 4;
+    *wpitch = (int)wp;
+    return bytes <= 150 * 1024 ? bytes : 0;
+}
+
+// Runs the GEMM on the skinny kernel when its shape fits; *done reports it.
+static hipError_t try_skinny(const MatW& w, const ActF16& a, const MatD& d, int64_t N, int64_t ne12, int64_t ne13,
+                             int32_t* dots, const MmqEpi* epi, const MmqSplit& sp, hipStream_t st, bool* done) {
+    *done = false;
+    if (!sp.skinny || dots || (epi && epi->kind != MMQ_EPI_STORE) || ne12 * ne13 != 1 || a.M < 4096) return hipSuccess;
+    // F16 weights stay on the tiled kernel: their LDS rows (2 bytes per element) leave
+    // one workgroup per CU, and the tiled kernel is faster there
+    if (w.type == T_F16 || a.dp > 4 || a.dp % 2 != 0) return hipSuccess;
+    const int dp = (int)a.dp;
+    int wpitch = 0;
+    // 128-row workgroups at large M while two fit per CU (a quarter of the weight
+    // copies per output row), 64 rows otherwise
+    int smt = 4;
+    size_t lds = skinny_lds(w.type, N, a.K, dp, smt, &wpitch);
+    if (a.M < 32768 || !lds || lds > 75 * 1024) {
+        smt = 2;
+        lds = skinny_lds(w.type, N, a.K, dp, smt, &wpitch);
+    }
+    const int64_t rowb = (a.K / QK) * (w.type == T_Q8_0 ? 34 : w.type == T_Q4_0 ? 18 : 20);
+    if (!lds || a.s1 % 8 != 0 || w.nb1 != rowb || (reinterpret_cast<uintptr_t>(w.data) & 15) ||
+        (reinterpret_cast<uintptr_t>(a.q) & 15) || (d.nb1 & 3) || (reinterpret_cast<uintptr_t>(d.data) & 3) ||
+        (reinterpret_cast<uintptr_t>(a.d) & 15) || (w.type == T_Q4_1 && (reinterpret_cast<uintptr_t>(a.s) & 15)))
+        return hipSuccess;
+    SkinnyArgs p;
+    p.W = w.data;
+    p.w_nb1 = w.nb1;
+    p.A = static_cast<const _Float16*>(a.q);
+    p.a_s1 = a.s1;
+    p.Ad = static_cast<const _Float16*>(a.d);
+    p.As = static_cast<const _Float16*>(a.s);
+    p.D = d.data;
+    p.d_nb1 = d.nb1;
+    p.M = (int)a.M;
+    p.N = (int)N;
+    p.K = (int)a.K;
+    p.dp = dp;
+    p.npad = (int)((N + 31) / 32 * 32);
+    p.wpitch = wpitch;
+    const unsigned grid = (unsigned)((a.M + 32 * smt - 1) / (32 * smt));
+    // dynamic LDS beyond 64 KB, allowed once per kernel
+    static bool attr[6] = {false, false, false, false, false, false};
+    const int ti = (w.type == T_Q8_0 ? 0 : w.type == T_Q4_0 ? 1 : 2) * 2 + (smt == 4 ? 1 : 0);
+    const void* fns[6] = {(const void*)mmq_skinny_kernel<T_Q8_0, 2>, (const void*)mmq_skinny_kernel<T_Q8_0, 4>,
+                          (const void*)mmq_skinny_kernel<T_Q4_0, 2>, (const void*)mmq_skinny_kernel<T_Q4_0, 4>,
+                          (const void*)mmq_skinny_kernel<T_Q4_1, 2>, (const void*)mmq_skinny_kernel<T_Q4_1, 4>};
+    if (!attr[ti]) {
+        if (hipFuncSetAttribute(fns[ti], hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024) != hipSuccess) {
+            (void)hipGetLastError();  // not done: the tiled kernel takes it
+            return hipSuccess;
+        }
+        attr[ti] = true;
+    }
+    switch (ti) {
+        case 0: mmq_skinny_kernel<T_Q8_0, 2><<<grid, 256, lds, st>>>(p); break;
+        case 1: mmq_skinny_kernel<T_Q8_0, 4><<<grid, 256, lds, st>>>(p); break;
+        case 2: mmq_skinny_kernel<T_Q4_0, 2><<<grid, 256, lds, st>>>(p); break;
+        case 3: mmq_skinny_kernel<T_Q4_0, 4><<<grid, 256, lds, st>>>(p); break;
+        case 4: mmq_skinny_kernel<T_Q4_1, 2><<<grid, 256, lds, st>>>(p); break;
+        default: mmq_skinny_kernel<T_Q4_1, 4><<<grid, 256, lds, st>>>(p); break;
+    }
+    *done = true;
+    return hipGetLastError();
+}
+
 static hipError_t run_mmq(const MatW& w_in, const ActF16& a, const MatD& d, int64_t N, int64_t ne12, int64_t ne13,
                           int32_t* dots, const MmqEpi* epi, void* align_buf, const MmqSplit& sp, hipStream_t st) {
+    {
+        bool done = false;
+        const hipError_t e = try_skinny(w_in, a, d, N, ne12, ne13, dots, epi, sp, st, &done);
+        if (done || e != hipSuccess) return e;
+    }
     MatW w = w_in;
     // F16 runs K to a whole 16-byte chunk: the weight copy below and the
     // activation operand (a.s1 >= kk, zero from K to kk) carry zeros there

@@ -141,3 +141,29 @@ def test_mul_mat_split_k(mi, ctx, orc, tname, M, N, K):
     sample.sort()
     sample[0], sample[-1] = 0, M - 1
     check(mi, ctx, orc, tname, M, N, K, seed=3, sample=sample)
+
+
+@pytest.mark.parametrize("tname", ["q8_0", "q4_0", "q4_1", "f16"])
+@pytest.mark.parametrize("M,N,K", [(65536, 288, 96), (5000, 100, 64), (4097, 33, 128), (8192, 384, 32),
+                                   (16384, 192, 96)])
+def test_mul_mat_skinny(mi, ctx, orc, tname, M, N, K):
+    """K <= 128 at M >= 4096 (SAM2 Hiera-tiny stage 1: 65536 tokens, K = 96,
+    qkv N = 288) with quantized weights runs on the skinny kernel:
+    bit-identical to the tiled kernel (same instruction sequence per 32x32
+    tile), and within the usual bar of the oracle on sampled rows (ragged M
+    and N included).  F16 weights stay on the tiled kernel (both calls)."""
+    t = orc.NAME_TYPE[tname]
+    w = orc.normal(N * K, seed=9, stream=1, std=0.02).reshape(N, K)
+    x = orc.normal(M * K, seed=9, stream=2).reshape(M, K)
+    wq = orc.quantize_weights(t, w)
+    got = run_mul_mat(mi, ctx, wq, t, K, N, x[None, None])[0, 0]
+    ctx.set_skinny(False)
+    try:
+        tiled = run_mul_mat(mi, ctx, wq, t, K, N, x[None, None])[0, 0]
+    finally:
+        ctx.set_skinny(True)
+    assert np.array_equal(got, tiled)
+    rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(M).choice(M, 128, replace=False)]))
+    ref = orc.mul_mat(wq, t, K, N, x[rows][None, None])[0, 0]
+    scale = absterm(orc, t, wq, K, orc.from_float(orc.VEC_DOT_TYPE[t], x[rows]))
+    assert rel_err(got[rows], ref, scale) <= TOL[tname]
