@@ -361,7 +361,8 @@ def main():
     ap.add_argument("--op", default=None,
                     help="profile mode, one workload --reps times with its kernel times: TYPE/LINEAR (e.g. q8_0/fc1), "
                          "attn/windowed, attn/global, vit/TYPE (SAM3 ViT frames), hiera/TYPE (Hiera-tiny frames), "
-                         "neck/f32|f16 (SAM3 SimpleFPN neck), "
+                         "neck/f32|f16 (SAM3 SimpleFPN neck), mm/TYPE/MxNxK (one MUL_MAT of that shape, "
+                         "e.g. mm/q4_0/65536x288x96 for the SAM2 Hiera-tiny stage-1 qkv), "
                          "copy (256 MiB device copy)")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--op-warmup", type=int, default=20)
@@ -417,6 +418,28 @@ def main():
         hp, pre, blocks, outs, keep = build_hiera(mi, orc, torch, dev, tn)
         res = bench_hiera(mi, ctx, torch, hp, pre, blocks, outs, args.reps)
         print(json.dumps({"op": args.op, **res}), flush=True)
+        ctx.close()
+        return
+    if args.op and args.op.startswith("mm/"):
+        _, tn, shape = args.op.split("/")
+        M, N, K = (int(v) for v in shape.split("x"))
+        t = orc.NAME_TYPE[tn]
+        w = orc.normal(N * K, seed=0, stream=70, std=0.02).reshape(N, K)
+        wd = torch.from_numpy(orc.quantize_weights(t, w)).to(dev)
+        xm = torch.from_numpy(orc.normal(M * K, seed=0, stream=71).reshape(M, K)).to(dev)
+        dst = torch.empty((M, N), dtype=torch.float32, device=dev)
+        s0, s1 = mi.from_torch(wd, t, [K, N]), mi.from_torch(xm, mi.F32, [K, M])
+        d = mi.from_torch(dst, mi.F32, [N, M])
+        for _ in range(args.op_warmup):
+            ctx.mul_mat(s0, s1, d)
+        torch.cuda.synchronize()
+        ctx.profile(True)
+        for _ in range(args.reps):
+            ctx.mul_mat(s0, s1, d)
+        prof = ctx.profile_collect()
+        ctx.profile(False)
+        print(json.dumps({"op": args.op, "reps": args.reps,
+                          "kernel_us": {k: round(1e3 * v[1] / v[0], 2) for k, v in prof.items()}}), flush=True)
         ctx.close()
         return
     if args.op and args.op.startswith("neck/"):
