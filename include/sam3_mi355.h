@@ -387,6 +387,21 @@ typedef struct mi355_quantize_stats {
 mi355_status mi355_model_quantize(mi355_context* ctx, const char* in_path, const char* out_path, int32_t qtype,
                                   mi355_quantize_stats* stats);
 
+/* A SAM2 file's Hiera backbone in device memory: the tensors sam3_register_tensors
+ * declares for it (sam3.cpp:1800-1840: "hiera.patch_embed.*", "hiera.pos_embed",
+ * "hiera.pos_embed_window", "hiera.blocks.N.*" with ".proj.*" at stage
+ * transitions), weights in the file's weight type when their rows are whole
+ * blocks and F32 otherwise; the hyperparameters of sam2_load_hparams
+ * (sam3.cpp:1568-1590); pos_embed [S0*S0][E] (S0 = img/4) computed by
+ * mi355_hiera_pos_embed from the two tables.  Everything mi355_hiera_encode
+ * takes besides the image; valid until mi355_hiera_weights_free. */
+typedef struct mi355_hiera_weights mi355_hiera_weights;
+mi355_status mi355_hiera_weights_load(mi355_context* ctx, const mi355_model_file* f, mi355_hiera_weights** out);
+void mi355_hiera_weights_free(mi355_hiera_weights* w);
+mi355_status mi355_hiera_weights_get(const mi355_hiera_weights* w, mi355_hiera_hparams* hp,
+                                     const mi355_hiera_block** blocks, int* n_blocks, const mi355_tensor** patch_w,
+                                     const float** patch_b, const float** pos_embed);
+
 /* Fusion in the encoder runners (no counterpart in the reference, whose graph
  * always materialises f32 activations; on by default).  When on, the passes
  * that feed a MUL_MAT with Q8_0/Q4_0/Q4_1 or F16 weights (LayerNorm, bias+GELU,

@@ -169,6 +169,10 @@ def lib():
         "mi355_model_file_load_bytes": (SZ, [P, I, I]),
         "mi355_model_file_load": (I, [P, P, I, I, P, SZ]),
         "mi355_vit_weights_load": (I, [P, P, C.POINTER(P)]),
+        "mi355_hiera_weights_load": (I, [P, P, C.POINTER(P)]),
+        "mi355_hiera_weights_free": (None, [P]),
+        "mi355_hiera_weights_get": (I, [P, C.POINTER(HieraHparams), C.POINTER(C.POINTER(HieraBlock)), C.POINTER(I),
+                                        C.POINTER(C.POINTER(Tensor)), C.POINTER(P), C.POINTER(P)]),
         "mi355_vit_weights_free": (None, [P]),
         "mi355_vit_weights_get": (I, [P, C.POINTER(VitHparams), C.POINTER(C.POINTER(VitBlock)), C.POINTER(I),
                                       C.POINTER(C.POINTER(Tensor)), C.POINTER(P), C.POINTER(P), C.POINTER(P)]),
@@ -385,6 +389,22 @@ class Context:
         self._check(self.L.mi355_vit_weights_get(w, C.byref(hp), C.byref(blocks), C.byref(n), C.byref(pw),
                                                  C.byref(pos), C.byref(lw), C.byref(lb)))
         return w, hp, blocks, n.value, pw.contents, pos.value, lw.value, lb.value
+
+    def hiera_weights_load(self, f: "ModelFile"):
+        """(handle, hparams, blocks array, n, patch_w Tensor, patch_b, pos) of the file's Hiera backbone."""
+        w = C.c_void_p()
+        self._check(self.L.mi355_hiera_weights_load(self.h, f.h, C.byref(w)))
+        hp = HieraHparams()
+        blocks = C.POINTER(HieraBlock)()
+        n = C.c_int()
+        pw = C.POINTER(Tensor)()
+        pb, pos = C.c_void_p(), C.c_void_p()
+        self._check(self.L.mi355_hiera_weights_get(w, C.byref(hp), C.byref(blocks), C.byref(n), C.byref(pw),
+                                                   C.byref(pb), C.byref(pos)))
+        return w, hp, blocks, n.value, pw.contents, pb.value, pos.value
+
+    def hiera_weights_free(self, w):
+        self.L.mi355_hiera_weights_free(w)
 
     def vit_weights_free(self, w):
         self.L.mi355_vit_weights_free(w)

@@ -281,7 +281,58 @@ mi355_status mi355_model_file_load(mi355_context* ctx, const mi355_model_file* f
                      "convert_weights launch");
 }
 
-// ---- SAM3 ViT backbone from a file (sam3_register_tensors, sam3.cpp:2530-2560)
+// ---- backbones from a file, tensors typed as sam3_register_tensors types them
+
+namespace {
+
+// Uploads named tensors of a file into fresh device buffers (kept in allocs):
+// shapes must match the registered ones, the type is the registered type.
+struct Uploader {
+    mi355_context* ctx;
+    const mi355_model_file* f;
+    std::vector<void*>* allocs;
+    const char* what;
+    mi355_status load(const std::string& name, int type, std::initializer_list<int64_t> ne, void** dptr,
+                      mi355_tensor* t) {
+        const int idx = mi355_model_file_find(f, name.c_str());
+        if (idx < 0) return fail(ctx, MI355_STATUS_INVALID_ARG, "%s: tensor '%s' missing", what, name.c_str());
+        const TensorRec& r = f->tensors[(size_t)idx];
+        int64_t want[4] = {1, 1, 1, 1};
+        int i = 0;
+        for (int64_t v : ne) want[i++] = v;
+        for (int k = 0; k < 4; ++k)
+            if (r.ne[k] != want[k])
+                return fail(ctx, MI355_STATUS_INVALID_ARG, "%s: '%s' has an unexpected shape", what, name.c_str());
+        const size_t bytes = mi355_model_file_load_bytes(f, idx, type);
+        void* d = nullptr;
+        if (bytes == 0 || hipMalloc(&d, bytes) != hipSuccess)
+            return fail(ctx, MI355_STATUS_ALLOC_FAILED, "%s: cannot place '%s'", what, name.c_str());
+        allocs->push_back(d);
+        const mi355_status st = mi355_model_file_load(ctx, f, idx, type, d, bytes);
+        if (st != MI355_STATUS_SUCCESS) return st;
+        *dptr = d;
+        if (t) {
+            *t = mi355_tensor{};
+            t->type = type;
+            for (int k = 0; k < 4; ++k) t->ne[k] = want[k];
+            t->nb[0] = type_size(type);
+            t->nb[1] = (int64_t)row_size(type, want[0]);
+            t->nb[2] = t->nb[1] * want[1];
+            t->nb[3] = t->nb[2] * want[2];
+            t->data = d;
+        }
+        return MI355_STATUS_SUCCESS;
+    }
+};
+
+// the weight type of a file's ftype (sam3_load_model's map, sam3.cpp:3246-3255)
+int weight_type(int32_t ftype) {
+    return ftype == 0 ? T_F32 : ftype == 1 ? T_F16 : ftype == 2 ? T_Q4_0 : ftype == 3 ? T_Q4_1 : T_Q8_0;
+}
+
+}  // namespace
+
+// ---- SAM3 ViT backbone (sam3_register_tensors, sam3.cpp:2530-2560)
 
 struct mi355_vit_weights {
     mi355_vit_hparams hp{};
@@ -316,45 +367,16 @@ mi355_status mi355_vit_weights_load(mi355_context* ctx, const mi355_model_file* 
     w->hp.patch_size = P;
     w->hp.pos_grid = img / P / 3;  // pos_embed at pretrained resolution, tiled 3x
     w->hp.eps = 1e-5f;
-    const int wtype = f->ftype == 0 ? T_F32 : f->ftype == 1 ? T_F16 : f->ftype == 2 ? T_Q4_0 : f->ftype == 3 ? T_Q4_1 : T_Q8_0;
+    const int wtype = weight_type(f->ftype);
     const int wblk = blck(wtype);
     auto bad = [&](mi355_status st) {
         mi355_vit_weights_free(w);
         return st;
     };
-    // upload one tensor as the reference registers it: weights (T2/T4) in the file's weight
-    // type when ne0 is a whole number of blocks, everything else F32; shapes must match
+    // weights (T2/T4) in the file's weight type when ne0 is a whole number of blocks, else F32
+    Uploader up{ctx, f, &w->allocs, "vit_weights_load"};
     auto load = [&](const std::string& name, int type, std::initializer_list<int64_t> ne, void** dptr,
-                    mi355_tensor* t) -> mi355_status {
-        const int idx = mi355_model_file_find(f, name.c_str());
-        if (idx < 0) return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_weights_load: tensor '%s' missing", name.c_str());
-        const TensorRec& r = f->tensors[(size_t)idx];
-        int64_t want[4] = {1, 1, 1, 1};
-        int i = 0;
-        for (int64_t v : ne) want[i++] = v;
-        for (int k = 0; k < 4; ++k)
-            if (r.ne[k] != want[k])
-                return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_weights_load: '%s' has an unexpected shape", name.c_str());
-        const size_t bytes = mi355_model_file_load_bytes(f, idx, type);
-        void* d = nullptr;
-        if (bytes == 0 || hipMalloc(&d, bytes) != hipSuccess)
-            return fail(ctx, MI355_STATUS_ALLOC_FAILED, "vit_weights_load: cannot place '%s'", name.c_str());
-        w->allocs.push_back(d);
-        const mi355_status st = mi355_model_file_load(ctx, f, idx, type, d, bytes);
-        if (st != MI355_STATUS_SUCCESS) return st;
-        *dptr = d;
-        if (t) {
-            *t = mi355_tensor{};
-            t->type = type;
-            for (int k = 0; k < 4; ++k) t->ne[k] = want[k];
-            t->nb[0] = type_size(type);
-            t->nb[1] = (int64_t)row_size(type, want[0]);
-            t->nb[2] = t->nb[1] * want[1];
-            t->nb[3] = t->nb[2] * want[2];
-            t->data = d;
-        }
-        return MI355_STATUS_SUCCESS;
-    };
+                    mi355_tensor* t) { return up.load(name, type, ne, dptr, t); };
     auto wt = [&](int64_t ne0) { return ne0 % wblk == 0 ? wtype : (int)T_F32; };
     const int MLP = w->hp.mlp_dim, pg = w->hp.pos_grid, G = w->hp.grid;
     void* p = nullptr;
@@ -391,6 +413,121 @@ mi355_status mi355_vit_weights_load(mi355_context* ctx, const mi355_model_file* 
         b.is_global = global ? 1 : 0;
     }
     *out = w;
+    return MI355_STATUS_SUCCESS;
+}
+
+// ---- SAM2 Hiera backbone (sam3_register_tensors' "hiera.*" names, sam3.cpp:1800-1840;
+// hyperparameters of sam2_load_hparams, sam3.cpp:1568-1590)
+
+struct mi355_hiera_weights {
+    mi355_hiera_hparams hp{};
+    std::vector<mi355_hiera_block> blocks;
+    mi355_tensor patch_w{};
+    float *patch_b = nullptr, *pos = nullptr;
+    std::vector<void*> allocs;
+};
+
+void mi355_hiera_weights_free(mi355_hiera_weights* w) {
+    if (!w) return;
+    for (void* p : w->allocs) (void)hipFree(p);
+    delete w;
+}
+
+mi355_status mi355_hiera_weights_load(mi355_context* ctx, const mi355_model_file* f, mi355_hiera_weights** out) {
+    if (!ctx || !f || !out) return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera_weights_load: null argument");
+    *out = nullptr;
+    if (f->magic != kMagicSam2 || f->hparams.size() < 25)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera_weights_load: not a SAM2 file");
+    // img_size, backbone_type, embed, heads, num_stages, stages[4], global_n, global_idx[8],
+    // q_pool, window_spec[4], pos_embed_bkg_h, pos_embed_bkg_w
+    const int32_t* h = f->hparams.data();
+    auto* w = new mi355_hiera_weights();
+    auto bad = [&](mi355_status st) {
+        mi355_hiera_weights_free(w);
+        return st;
+    };
+    mi355_hiera_hparams& hp = w->hp;
+    hp.img_size = h[0];
+    hp.embed_dim = h[2];
+    hp.num_heads = h[3];
+    for (int i = 0; i < 4; ++i) hp.stages[i] = h[5 + i];
+    hp.n_global = h[9];
+    for (int i = 0; i < 8; ++i) hp.global_idx[i] = h[10 + i];
+    hp.q_pool = h[18];
+    for (int i = 0; i < 4; ++i) hp.window_spec[i] = h[19 + i];
+    hp.eps = 1e-6f;
+    const int bkg_h = h[23], bkg_w = h[24], E = hp.embed_dim;
+    const int n = mi355_hiera_n_blocks(&hp);
+    if (h[4] != 4 || n <= 0 || hp.n_global < 0 || hp.n_global > 8 || bkg_h <= 0 || bkg_w <= 0 || hp.img_size % 4 != 0)
+        return bad(fail(ctx, MI355_STATUS_INVALID_ARG, "hiera_weights_load: bad hyperparameters"));
+    const int wtype = weight_type(f->ftype), wblk = blck(wtype);
+    auto wt = [&](int64_t ne0) { return ne0 % wblk == 0 ? wtype : (int)T_F32; };
+    Uploader up{ctx, f, &w->allocs, "hiera_weights_load"};
+    void* p = nullptr;
+    mi355_status st;
+    if ((st = up.load("hiera.patch_embed.weight", wt(7), {7, 7, 3, E}, &p, &w->patch_w)) != MI355_STATUS_SUCCESS)
+        return bad(st);
+    if ((st = up.load("hiera.patch_embed.bias", T_F32, {E}, &p, nullptr)) != MI355_STATUS_SUCCESS) return bad(st);
+    w->patch_b = static_cast<float*>(p);
+    // the positional table of the encoder's grid, built on the device from the two tables
+    // (sam2_compute_pos_embed, sam3.cpp:4118-4157)
+    const int ws0 = hp.window_spec[0], S0 = hp.img_size / 4;
+    void *bkg = nullptr, *win = nullptr;
+    if ((st = up.load("hiera.pos_embed", T_F32, {bkg_w, bkg_h, E, 1}, &bkg, nullptr)) != MI355_STATUS_SUCCESS)
+        return bad(st);
+    if ((st = up.load("hiera.pos_embed_window", T_F32, {ws0, ws0, E, 1}, &win, nullptr)) != MI355_STATUS_SUCCESS)
+        return bad(st);
+    if (hipMalloc(&p, (size_t)S0 * S0 * E * 4) != hipSuccess)
+        return bad(fail(ctx, MI355_STATUS_ALLOC_FAILED, "hiera_weights_load: pos_embed allocation failed"));
+    w->allocs.push_back(p);
+    w->pos = static_cast<float*>(p);
+    if ((st = mi355_hiera_pos_embed(ctx, static_cast<const float*>(bkg), E, bkg_h, bkg_w, static_cast<const float*>(win),
+                                    ws0, S0, S0, w->pos)) != MI355_STATUS_SUCCESS)
+        return bad(st);
+    w->blocks.resize((size_t)n);
+    for (int i = 0; i < n; ++i) {
+        mi355_hiera_block_info info;
+        if ((st = mi355_hiera_block_info_get(&hp, i, &info)) != MI355_STATUS_SUCCESS) return bad(st);
+        const int din = info.dim_in, dout = info.dim_out;
+        mi355_hiera_block& b = w->blocks[(size_t)i];
+        b = mi355_hiera_block{};
+        const std::string pre = "hiera.blocks." + std::to_string(i);
+        struct V { const char* sfx; int64_t n; const float** dst; } vecs[] = {
+            {".norm1.weight", din, &b.norm1_w}, {".norm1.bias", din, &b.norm1_b}, {".attn.qkv.bias", 3LL * dout, &b.qkv_b},
+            {".attn.proj.bias", dout, &b.proj_b}, {".norm2.weight", dout, &b.norm2_w}, {".norm2.bias", dout, &b.norm2_b},
+            {".mlp.fc1.bias", 4LL * dout, &b.fc1_b}, {".mlp.fc2.bias", dout, &b.fc2_b}};
+        for (const V& v : vecs) {
+            if ((st = up.load(pre + v.sfx, T_F32, {v.n}, &p, nullptr)) != MI355_STATUS_SUCCESS) return bad(st);
+            *v.dst = static_cast<const float*>(p);
+        }
+        if ((st = up.load(pre + ".attn.qkv.weight", wt(din), {din, 3LL * dout}, &p, &b.qkv_w)) != MI355_STATUS_SUCCESS ||
+            (st = up.load(pre + ".attn.proj.weight", wt(dout), {dout, dout}, &p, &b.proj_w)) != MI355_STATUS_SUCCESS ||
+            (st = up.load(pre + ".mlp.fc1.weight", wt(dout), {dout, 4LL * dout}, &p, &b.fc1_w)) != MI355_STATUS_SUCCESS ||
+            (st = up.load(pre + ".mlp.fc2.weight", wt(4LL * dout), {4LL * dout, dout}, &p, &b.fc2_w)) != MI355_STATUS_SUCCESS)
+            return bad(st);
+        if (din != dout) {  // dimension projection at a stage transition
+            if ((st = up.load(pre + ".proj.weight", wt(din), {din, dout}, &p, &b.dim_proj_w)) != MI355_STATUS_SUCCESS)
+                return bad(st);
+            if ((st = up.load(pre + ".proj.bias", T_F32, {dout}, &p, nullptr)) != MI355_STATUS_SUCCESS) return bad(st);
+            b.dim_proj_b = static_cast<const float*>(p);
+        }
+    }
+    if ((st = hip_check(ctx, hipStreamSynchronize(ctx->stream), "hiera_weights_load")) != MI355_STATUS_SUCCESS)
+        return bad(st);
+    *out = w;
+    return MI355_STATUS_SUCCESS;
+}
+
+mi355_status mi355_hiera_weights_get(const mi355_hiera_weights* w, mi355_hiera_hparams* hp,
+                                     const mi355_hiera_block** blocks, int* n_blocks, const mi355_tensor** patch_w,
+                                     const float** patch_b, const float** pos_embed) {
+    if (!w) return fail(nullptr, MI355_STATUS_INVALID_ARG, "hiera_weights_get: null weights");
+    if (hp) *hp = w->hp;
+    if (blocks) *blocks = w->blocks.data();
+    if (n_blocks) *n_blocks = (int)w->blocks.size();
+    if (patch_w) *patch_w = &w->patch_w;
+    if (patch_b) *patch_b = w->patch_b;
+    if (pos_embed) *pos_embed = w->pos;
     return MI355_STATUS_SUCCESS;
 }
 

@@ -137,3 +137,88 @@ def test_vit_from_file(mi, ctx, orc, tmp_path, tname, ftype):
         assert np.array_equal(a, b)
     finally:
         ctx.vit_weights_free(w)
+
+
+def test_hiera_from_file(mi, ctx, orc, tmp_path):
+    """A SAM2 Hiera-tiny file at 128x128 (Q4_0): the loader derives the
+    hyperparameters of sam2_load_hparams and builds the pos_embed table on the
+    GPU; every stage output of the encoder run from the file's tables equals,
+    bit for bit, the encoder fed the same bytes uploaded by hand with the
+    oracle's sam2_compute_pos_embed table (so the loader's table is that table)."""
+    t = orc.Q4_0
+    hpw = mi.hiera_tiny(128)
+    E, S0 = 96, 32
+    rng = np.random.default_rng(17)
+    f32 = lambda shape, s=0.05: (rng.standard_normal(shape) * s).astype(np.float32)
+    ts = [("hiera.patch_embed.weight", orc.F32, (7, 7, 3, E), f32((E, 3, 7, 7))),
+          ("hiera.patch_embed.bias", orc.F32, (E,), f32(E)),
+          ("hiera.pos_embed", orc.F32, (7, 7, E, 1), f32((E, 7, 7), 0.1)),
+          ("hiera.pos_embed_window", orc.F32, (8, 8, E, 1), f32((E, 8, 8), 0.1))]
+    infos = [mi.hiera_block_info(hpw, i) for i in range(12)]
+    for i, info in enumerate(infos):
+        din, dout = info.dim_in, info.dim_out
+        pre = f"hiera.blocks.{i}"
+        mats = [(".attn.qkv.weight", din, 3 * dout), (".attn.proj.weight", dout, dout),
+                (".mlp.fc1.weight", dout, 4 * dout), (".mlp.fc2.weight", 4 * dout, dout)]
+        if din != dout:
+            mats.append((".proj.weight", din, dout))
+        for sfx, K, N in mats:
+            ts.append((pre + sfx, t, (K, N), orc.quantize_weights(t, f32((N, K)))))
+        vecs = [(".norm1.weight", din), (".norm1.bias", din), (".attn.qkv.bias", 3 * dout), (".attn.proj.bias", dout),
+                (".norm2.weight", dout), (".norm2.bias", dout), (".mlp.fc1.bias", 4 * dout), (".mlp.fc2.bias", dout)]
+        if din != dout:
+            vecs.append((".proj.bias", dout))
+        for sfx, n in vecs:
+            ts.append((pre + sfx, orc.F32, (n,), f32(n, 0.2) + (np.float32(1) if "norm" in sfx and "weight" in sfx else 0)))
+    rest = [E, 1, 4, 1, 2, 7, 2, 3, 5, 7, 9, 0, 0, 0, 0, 0, 3, 8, 4, 14, 7, 7, 7, 1] + [300 + i for i in range(31)]
+    p = tmp_path / "hiera.ggml"
+    W.write(p, W.MAGIC_SAM2, 1, 2, W.sam2_hparams(img=128, backbone=1, rest=rest), ts)
+    f = mi.ModelFile(str(p))
+    w, hp, blocks, n, pw, pb, pos = ctx.hiera_weights_load(f)
+    try:
+        assert n == 12 and (hp.img_size, hp.embed_dim, hp.num_heads, hp.q_pool) == (128, 96, 1, 3)
+        assert list(hp.stages) == [1, 2, 7, 2] and list(hp.window_spec) == [8, 4, 14, 7]
+        assert hp.n_global == 3 and list(hp.global_idx)[:3] == [5, 7, 9]
+        by = {name: (tt, ne, data) for name, tt, ne, data in ts}
+        pe_ref = orc.sam2_pos_embed(by["hiera.pos_embed"][2], by["hiera.pos_embed_window"][2], S0, S0)
+        img = torch.from_numpy(orc.uniform(3 * 128 * 128, 9, 1).reshape(3, 128, 128)).cuda()
+        dims = [(32, 96), (16, 192), (8, 384), (4, 768)]
+        outs_f = [torch.full((s * s, c), float("nan"), dtype=torch.float32, device="cuda") for s, c in dims]
+        ctx.hiera_encode(hp, C.c_void_p(img.data_ptr()), pw, C.c_void_p(pb), C.c_void_p(pos),
+                         [blocks[i] for i in range(n)], [o.data_ptr() for o in outs_f])
+        ctx.synchronize()
+        # by hand: the same bytes, the oracle's pos_embed table
+        keep = []
+
+        def up(name):
+            d = dev(np.ascontiguousarray(by[name][2]).view(np.uint8))
+            keep.append(d)
+            return d
+
+        hb = []
+        for i, info in enumerate(infos):
+            pre = f"hiera.blocks.{i}"
+            b = mi.HieraBlock()
+            for fld, sfx in (("qkv_w", ".attn.qkv.weight"), ("proj_w", ".attn.proj.weight"),
+                             ("fc1_w", ".mlp.fc1.weight"), ("fc2_w", ".mlp.fc2.weight"), ("dim_proj_w", ".proj.weight")):
+                if pre + sfx in by:
+                    tt, ne, _ = by[pre + sfx]
+                    setattr(b, fld, mi.from_torch(up(pre + sfx), tt, list(ne)))
+            for fld, sfx in (("norm1_w", ".norm1.weight"), ("norm1_b", ".norm1.bias"), ("qkv_b", ".attn.qkv.bias"),
+                             ("proj_b", ".attn.proj.bias"), ("norm2_w", ".norm2.weight"), ("norm2_b", ".norm2.bias"),
+                             ("fc1_b", ".mlp.fc1.bias"), ("fc2_b", ".mlp.fc2.bias"), ("dim_proj_b", ".proj.bias")):
+                if pre + sfx in by:
+                    setattr(b, fld, up(pre + sfx).data_ptr())
+            hb.append(b)
+        ped = dev(pe_ref)
+        outs_h = [torch.full((s * s, c), float("nan"), dtype=torch.float32, device="cuda") for s, c in dims]
+        ctx.hiera_encode(hpw, C.c_void_p(img.data_ptr()), mi.from_torch(up("hiera.patch_embed.weight"), orc.F32,
+                                                                         [7, 7, 3, E]),
+                         C.c_void_p(up("hiera.patch_embed.bias").data_ptr()), C.c_void_p(ped.data_ptr()), hb,
+                         [o.data_ptr() for o in outs_h])
+        ctx.synchronize()
+        for a, b in zip(outs_f, outs_h):
+            assert torch.isfinite(a).all()
+            assert torch.equal(a, b)
+    finally:
+        ctx.hiera_weights_free(w)
