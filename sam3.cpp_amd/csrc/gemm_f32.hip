@@ -1,13 +1,28 @@
 // ggml MUL_MAT with F32 src0 and F32 src1 (ggml_vec_dot_f32 semantics:
 // fp32 products summed in fp32) on gfx950 fp32 MFMA.  Used by the patch
-// embedding (ggml_conv_2d_sk_p0 -> im2col + mul_mat with the F32 patch
-// weight, sam3.cpp:3815; the weight stays F32 under quantized weight types,
-// sam3.cpp:2479-2481, since its rows of 14 are not a multiple of 32).
+// embeddings (ggml_conv_2d -> im2col + mul_mat with the F32 patch weight,
+// sam3.cpp:3815, 4473; the weight stays F32 under quantized weight types,
+// sam3.cpp:2479-2481, since its rows of 7 or 14 are not a multiple of 32) and
+// by the SimpleFPN neck's F32 convolutions.
 //
-// Workgroup tile 64(m) x 64(n), four wavefronts of 32 x 32, K staged through
-// LDS 32 at a time (rows padded to 33 floats: the 32-row fragment reads of a
-// column hit 32 distinct banks); v_mfma_f32_32x32x2f32 takes one element of
-// A and one of B per lane (lane l: row/column l % 32, k = l / 32).
+// Tiled kernel (rows 16-byte aligned, K % 4 == 0): workgroup 128(m) x 128(n),
+// four wavefronts of 64 x 64 (2 x 2 v_mfma_f32_32x32x2f32 tiles), K staged 32
+// at a time, double-buffered through LDS by float4 loads held in registers
+// across the current stage's MFMAs.  The MFMA takes one A and one B element
+// per lane (lane l: row l % 32, k-slot l / 32 of a 2-wide k step), so a tile
+// row is stored parity-split, [row][k % 2][k / 2]: each lane's sixteen operand
+// values of a stage are four contiguous ds_read_b128.  Row pitch 36 floats:
+// the 16 rows one read pass touches land on distinct 4-bank groups.  Tiles
+// are walked XCD-aware (each XCD a contiguous band), so the n-tiles of one
+// m-tile read their activation rows through one L2.
+//
+// The same kernel runs a 3x3 / stride-1 / pad-1 convolution as an implicit
+// GEMM over a token-major [H*W][C] map (C % 32 == 0): a stage of 32 K values
+// lies within one tap, so each A row is one 128-byte segment of the pixel the
+// tap reaches, or zeros outside the image.  No im2col buffer exists.
+//
+// The 64 x 64 scalar-load kernel remains for rows that are not 16-byte
+// aligned or K not a multiple of 4.
 #include "common.cuh"
 #include "kernels.h"
 
@@ -15,6 +30,7 @@ namespace mi355 {
 
 namespace {
 constexpr int GT = 64, GK = 32;
+constexpr int TM = 128, TN = 128, TK = 32, TP = 36;  // tile, K stage, LDS row pitch (floats)
 }
 
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const GemmF32Args p) {
@@ -46,17 +62,152 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const GemmF32Args p) {
     }
     char* D = reinterpret_cast<char*>(p.D) + (int64_t)i12 * p.d_nb2 + (int64_t)i13 * p.d_nb3;
     const int n = n0 + wn * 32 + lr;
+    const float bn = p.bias && n < p.N ? p.bias[n] : 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int m = m0 + wm * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-        if (m < p.M && n < p.N) *reinterpret_cast<float*>(D + (int64_t)m * p.d_nb1 + 4LL * n) = acc[i];
+        if (m < p.M && n < p.N) *reinterpret_cast<float*>(D + (int64_t)m * p.d_nb1 + 4LL * n) = acc[i] + bn;
+    }
+}
+
+template <bool CONV>
+__global__ __launch_bounds__(256, 2) void gemm_f32_tiled_kernel(const GemmF32Args p) {
+    __shared__ __attribute__((aligned(16))) float sA[2][TM * TP];
+    __shared__ __attribute__((aligned(16))) float sB[2][TN * TP];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = w & 1, wn = w >> 1;  // this wavefront's 64 x 64 quadrant
+    const int lr = lane & 31, g = lane >> 5;
+    // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs, so
+    // workgroup b works tile (b % 8) * per_xcd + b / 8 and each XCD walks a contiguous
+    // band of tiles (the n-tiles of one m-tile share its activation rows in one L2)
+    const int tiles_n = (p.N + TN - 1) / TN, tiles = ((p.M + TM - 1) / TM) * tiles_n;
+    const int per_xcd = (tiles + 7) / 8;
+    const int tl = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tl >= tiles) return;
+    const int m0 = (tl / tiles_n) * TM, n0 = (tl % tiles_n) * TN;
+    const int z = blockIdx.y, i12 = z % p.ne12, i13 = z / p.ne12;
+    const char* Wb = reinterpret_cast<const char*>(p.W) + (int64_t)(i12 / p.r2) * p.w_nb2 + (int64_t)(i13 / p.r3) * p.w_nb3;
+    const char* Xb = reinterpret_cast<const char*>(p.X) + (int64_t)i12 * p.x_nb2 + (int64_t)i13 * p.x_nb3;
+
+    // loader: thread t fills row t/2 of both tiles, K values 16*(t%2) .. +15 of the stage
+    const int lrow = tid >> 1, lk = 16 * (tid & 1);
+    const int am = m0 + lrow, bn_ = n0 + lrow;
+    int oy = 0, ox = 0;
+    if (CONV) {
+        oy = am / p.Wd;
+        ox = am - oy * p.Wd;
+    }
+    v4f ra[4], rb[4];
+    auto load = [&](int k0) {
+        const v4f zero = {0, 0, 0, 0};
+        if (CONV) {  // the 32 K values of a stage lie within one tap (C % 32 == 0)
+            const int tap = k0 / p.C, c0 = k0 - tap * p.C;
+            const int iy = oy + tap / 3 - 1, ix = ox + tap % 3 - 1;
+            const bool in = am < p.M && iy >= 0 && iy < p.H && ix >= 0 && ix < p.Wd;
+            const float* src = reinterpret_cast<const float*>(Xb) + ((int64_t)iy * p.Wd + ix) * p.C + c0 + lk;
+#pragma unroll
+            for (int h = 0; h < 4; ++h) ra[h] = in ? *reinterpret_cast<const v4f*>(src + 4 * h) : zero;
+        } else {
+            const float* src = reinterpret_cast<const float*>(Xb + (int64_t)am * p.x_nb1) + k0 + lk;
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+                ra[h] = am < p.M && k0 + lk + 4 * h < p.K ? *reinterpret_cast<const v4f*>(src + 4 * h) : zero;
+        }
+        const float* wsrc = reinterpret_cast<const float*>(Wb + (int64_t)bn_ * p.w_nb1) + k0 + lk;
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+            rb[h] = bn_ < p.N && k0 + lk + 4 * h < p.K ? *reinterpret_cast<const v4f*>(wsrc + 4 * h) : zero;
+    };
+    // k = lk + 4h + j -> parity j & 1 at [row][16 * (j & 1) + k / 2]
+    auto park = [&](int buf) {
+        float* a = &sA[buf][lrow * TP];
+        float* b = &sB[buf][lrow * TP];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const int kk = (lk >> 1) + 2 * h;
+            *reinterpret_cast<v2f*>(&a[kk]) = v2f{ra[h][0], ra[h][2]};
+            *reinterpret_cast<v2f*>(&a[16 + kk]) = v2f{ra[h][1], ra[h][3]};
+            *reinterpret_cast<v2f*>(&b[kk]) = v2f{rb[h][0], rb[h][2]};
+            *reinterpret_cast<v2f*>(&b[16 + kk]) = v2f{rb[h][1], rb[h][3]};
+        }
+    };
+
+    v16f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int nst = (p.K + TK - 1) / TK;
+    load(0);
+    park(0);
+    __syncthreads();
+    for (int s = 0; s < nst; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < nst) load((s + 1) * TK);
+        v4f av[2][4], bv[2][4];  // this lane's 16 k values of its row (k-slot g), per tile
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float* a = &sA[buf][(wm * 64 + i * 32 + lr) * TP + 16 * g];
+            const float* b = &sB[buf][(wn * 64 + i * 32 + lr) * TP + 16 * g];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                av[i][q] = *reinterpret_cast<const v4f*>(a + 4 * q);
+                bv[i][q] = *reinterpret_cast<const v4f*>(b + 4 * q);
+            }
+        }
+#pragma unroll
+        for (int kk = 0; kk < TK / 2; ++kk)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][kk >> 2][kk & 3], bv[j][kk >> 2][kk & 3],
+                                                                    acc[i][j], 0, 0, 0);
+        if (s + 1 < nst) park(buf ^ 1);
+        __syncthreads();
+    }
+
+    char* D = reinterpret_cast<char*>(p.D) + (int64_t)i12 * p.d_nb2 + (int64_t)i13 * p.d_nb3;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn * 64 + j * 32 + lr;
+        if (n >= p.N) continue;
+        const float bn = p.bias ? p.bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                if (m < p.M) *reinterpret_cast<float*>(D + (int64_t)m * p.d_nb1 + 4LL * n) = acc[i][j][r] + bn;
+            }
     }
 }
 
 hipError_t launch_gemm_f32(const GemmF32Args& a, int Z, hipStream_t st) {
     if (a.M <= 0 || a.N <= 0 || Z <= 0) return hipSuccess;
-    const dim3 grid((unsigned)((a.M + GT - 1) / GT), (unsigned)((a.N + GT - 1) / GT), (unsigned)Z);
-    gemm_f32_kernel<<<grid, 256, 0, st>>>(a);
+    if (a.conv) {
+        if (a.C % TK != 0 || a.K != 9 * a.C || (int64_t)a.H * a.Wd != a.M || Z != 1 ||
+            (reinterpret_cast<uintptr_t>(a.X) & 15) || (reinterpret_cast<uintptr_t>(a.W) & 15) || (a.w_nb1 & 15))
+            return hipErrorInvalidValue;
+        const int tiles = ((a.M + TM - 1) / TM) * ((a.N + TN - 1) / TN);
+        gemm_f32_tiled_kernel<true><<<dim3((unsigned)((tiles + 7) / 8 * 8), 1), 256, 0, st>>>(a);
+        return hipGetLastError();
+    }
+    const bool tiled = a.K % 4 == 0 &&
+                       ((reinterpret_cast<uintptr_t>(a.X) | reinterpret_cast<uintptr_t>(a.W) | (uintptr_t)a.x_nb1 |
+                         (uintptr_t)a.x_nb2 | (uintptr_t)a.x_nb3 | (uintptr_t)a.w_nb1 | (uintptr_t)a.w_nb2 |
+                         (uintptr_t)a.w_nb3) & 15) == 0;
+    if (tiled) {
+        const int tiles = ((a.M + TM - 1) / TM) * ((a.N + TN - 1) / TN);
+        gemm_f32_tiled_kernel<false><<<dim3((unsigned)((tiles + 7) / 8 * 8), (unsigned)Z), 256, 0, st>>>(a);
+    } else {
+        const dim3 grid((unsigned)((a.M + GT - 1) / GT), (unsigned)((a.N + GT - 1) / GT), (unsigned)Z);
+        gemm_f32_kernel<<<grid, 256, 0, st>>>(a);
+    }
     return hipGetLastError();
 }
 

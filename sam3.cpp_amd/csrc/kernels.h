@@ -156,6 +156,10 @@ struct GemmF32Args {
     float* D;
     int64_t d_nb1, d_nb2, d_nb3;
     int M, N, K, ne12, r2, r3;
+    const float* bias = nullptr;  // [N], added to every row (or none)
+    // implicit 3x3 / stride 1 / pad 1 convolution: X is a token-major map [H*Wd][C], row m
+    // of the GEMM is output pixel m, and K = 9*C runs (tap, channel) with W rows in that order
+    int conv = 0, H = 0, Wd = 0, C = 0;
 };
 hipError_t launch_gemm_f32(const GemmF32Args& a, int Z, hipStream_t st);
 
@@ -232,6 +236,7 @@ hipError_t launch_deconv_pack(const void* w, int wtype, int Cin, int Cout, uint1
 hipError_t launch_deconv_scatter(const float* D, const float* b, int H, int W, int Cout, bool gelu, float* y,
                                  hipStream_t st);
 hipError_t launch_im2col3x3(const float* x, int H, int W, int C, bool f16, void* cols, hipStream_t st);
+hipError_t launch_conv3x3_pack(const float* w, int Cin, int Cout, float* out, hipStream_t st);
 hipError_t launch_bias_rows(float* y, const float* b, int64_t rows, int C, hipStream_t st);
 hipError_t launch_maxpool2(const float* x, int H, int W, int C, float* y, hipStream_t st);
 hipError_t launch_hiera_pos_embed(const float* bkg, int E, int bh, int bw, const float* win, int ws, int H, int W,

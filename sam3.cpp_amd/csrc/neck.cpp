@@ -10,8 +10,11 @@
 //     it is one F16 MUL_MAT [pixels x Cin] x [Cin x 4*Cout] (kernel cast to F16
 //     and repacked tap-major) whose columns are scattered to the 2x map, with
 //     the bias (and the GELU of scale 0) applied in the scatter;
-//   - conv_2d_sk_p0 1x1: a MUL_MAT with the kernel rows as they are;
-//   - conv_2d_s1_ph 3x3: im2col (K ordered as ggml's, ic-major) + MUL_MAT;
+//   - conv_2d_sk_p0 1x1: a MUL_MAT with the kernel rows as they are (F32
+//     kernels: the tiled fp32 GEMM with the bias in its epilogue);
+//   - conv_2d_s1_ph 3x3: F32 kernels as an implicit GEMM over the map (the
+//     kernel repacked to (tap, channel) rows, no im2col); F16 kernels as im2col
+//     (K ordered as ggml's, ic-major) + MUL_MAT;
 //   - pool_2d MAX 2x2 / 2.
 // Each op's numerics are ggml-cpu's: operands in the kernel's type (F16
 // rounded to nearest even, or F32), f32 accumulation, f32 bias adds.
@@ -55,8 +58,12 @@ mi355_status check_kernel(mi355_context* ctx, const mi355_tensor* w, const float
 size_t deconv_scratch(int64_t P, int64_t Cin, int64_t Cout) {
     return align_up((size_t)(4 * Cout * Cin * 2)) + align_up((size_t)(P * 4 * Cout * 4));
 }
-size_t conv_scratch(int64_t P, int64_t Cin, int k, int wtype) {
-    return k == 1 ? 0 : align_up((size_t)(P * 9 * Cin * (wtype == T_F32 ? 4 : 2)));
+// F32 3x3 with Cin % 32 == 0: the kernel repacked to (tap, channel) rows for the implicit
+// GEMM; otherwise the im2col columns in the kernel's type
+size_t conv_scratch(int64_t P, int64_t Cin, int64_t Cout, int k, int wtype) {
+    if (k == 1) return 0;
+    if (wtype == T_F32 && Cin % 32 == 0) return align_up((size_t)(9 * Cin * Cout * 4));
+    return align_up((size_t)(P * 9 * Cin * (wtype == T_F32 ? 4 : 2)));
 }
 
 // conv_transpose_2d_p0(kernel [2, 2, Cout, Cin], stride 2) + bias (+ GELU):
@@ -94,6 +101,41 @@ mi355_status conv(mi355_context* ctx, const mi355_tensor* w, const float* b, con
     const int Cin = (int)w->ne[2], Cout = (int)w->ne[3];
     const int64_t P = (int64_t)H * W, K = (int64_t)k * k * Cin;
     if (Cout % 4 != 0) return fail(ctx, MI355_STATUS_UNSUPPORTED, "neck_conv: Cout %% 4 != 0");
+    // F32 kernels: the tiled fp32 MFMA GEMM with the bias in its epilogue, the 3x3 as an
+    // implicit GEMM over the map (no im2col) with its kernel repacked to (tap, channel)
+    // rows; maps whose rows are not 16-byte aligned (or a 3x3 with Cin % 32 != 0) take
+    // im2col + MUL_MAT below
+    const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && Cin % 4 == 0;
+    if (w->type == T_F32 && aligned && (k == 1 || Cin % 32 == 0)) {
+        if (k == 3) {
+            Timed t(ctx, "neck_conv3x3_pack");
+            st = hip_check(ctx, t.done(launch_conv3x3_pack(static_cast<const float*>(w->data), Cin, Cout,
+                                                           reinterpret_cast<float*>(scratch), ctx->stream)),
+                           "conv3x3 pack");
+            if (st != MI355_STATUS_SUCCESS) return st;
+        }
+        GemmF32Args g;
+        g.W = k == 3 ? reinterpret_cast<const float*>(scratch) : static_cast<const float*>(w->data);
+        g.w_nb1 = 4 * K;
+        g.w_nb2 = g.w_nb3 = 4 * K * Cout;
+        g.X = x;
+        g.x_nb1 = 4LL * Cin;
+        g.x_nb2 = g.x_nb3 = 4LL * Cin * P;
+        g.D = y;
+        g.d_nb1 = 4LL * Cout;
+        g.d_nb2 = g.d_nb3 = 4LL * Cout * P;
+        g.M = (int)P;
+        g.N = Cout;
+        g.K = (int)K;
+        g.ne12 = g.r2 = g.r3 = 1;
+        g.bias = b;
+        g.conv = k == 3 ? 1 : 0;
+        g.H = H;
+        g.Wd = W;
+        g.C = Cin;
+        Timed t(ctx, k == 3 ? "neck_conv3x3_f32" : "neck_conv1x1_f32");
+        return hip_check(ctx, t.done(launch_gemm_f32(g, 1, ctx->stream)), "gemm_f32 launch");
+    }
     const mi355_tensor s0 = dev_t(w->data, w->type, K, Cout), d = dev_t(y, T_F32, Cout, P);
     mi355_tensor s1 = dev_t(x, T_F32, Cin, P);
     if (k == 3) {
@@ -143,19 +185,19 @@ bool neck_plan(int E, int G, const mi355_neck_scale* s, NeckPlan* pl) {
     mapb(16 * G2, s[0].conv1x1_w->ne[3]);
     scr(deconv_scratch(G2, E, C1));
     scr(deconv_scratch(4 * G2, C1, D0));
-    scr(conv_scratch(16 * G2, s[0].conv3x3_w->ne[2], 3, s[0].conv3x3_w->type));
+    scr(conv_scratch(16 * G2, s[0].conv3x3_w->ne[2], s[0].conv3x3_w->ne[3], 3, s[0].conv3x3_w->type));
     // scale 1: deconv E->C1 (2G), 1x1, 3x3
     const int64_t C1b = s[1].deconv1_w->ne[2];
     mapb(4 * G2, C1b);
     mapb(4 * G2, s[1].conv1x1_w->ne[3]);
     scr(deconv_scratch(G2, E, C1b));
-    scr(conv_scratch(4 * G2, s[1].conv3x3_w->ne[2], 3, s[1].conv3x3_w->type));
+    scr(conv_scratch(4 * G2, s[1].conv3x3_w->ne[2], s[1].conv3x3_w->ne[3], 3, s[1].conv3x3_w->type));
     // scale 2: 1x1, 3x3 at G; scale 3: pool, 1x1, 3x3 at G/2
     mapb(G2, s[2].conv1x1_w->ne[3]);
-    scr(conv_scratch(G2, s[2].conv3x3_w->ne[2], 3, s[2].conv3x3_w->type));
+    scr(conv_scratch(G2, s[2].conv3x3_w->ne[2], s[2].conv3x3_w->ne[3], 3, s[2].conv3x3_w->type));
     mapb(G2 / 4, E);
     mapb(G2 / 4, s[3].conv1x1_w->ne[3]);
-    scr(conv_scratch(G2 / 4, s[3].conv3x3_w->ne[2], 3, s[3].conv3x3_w->type));
+    scr(conv_scratch(G2 / 4, s[3].conv3x3_w->ne[2], s[3].conv3x3_w->ne[3], 3, s[3].conv3x3_w->type));
     return true;
 }
 
@@ -183,7 +225,7 @@ mi355_status mi355_neck_conv(mi355_context* ctx, const mi355_tensor* w, const fl
     (void)hipSetDevice(ctx->device);
     char* scr = nullptr;
     const int k = (int)w->ne[0];
-    mi355_status st = scratch_for(ctx, k == 3 ? conv_scratch((int64_t)H * W, w->ne[2], 3, w->type) : 0, &scr);
+    mi355_status st = scratch_for(ctx, k == 3 ? conv_scratch((int64_t)H * W, w->ne[2], w->ne[3], 3, w->type) : 0, &scr);
     if (st != MI355_STATUS_SUCCESS) return st;
     return conv(ctx, w, b, x, H, W, y, scr);
 }

@@ -3,8 +3,8 @@
 // themselves run as MUL_MATs (mmq.hip / gemm_f32.hip); these are the passes
 // around them, all HBM-bound: the conv-transpose kernel repack + F16 cast,
 // the scatter of the 2x2 / stride-2 transposed convolution with its bias
-// (and GELU), im2col of the 3x3 / pad-1 convolution, bias adds and the 2x2
-// max-pool.
+// (and GELU), the F32 3x3 kernel repack for the implicit GEMM, im2col of the
+// F16 3x3 / pad-1 convolution, bias adds and the 2x2 max-pool.
 #include "common.cuh"
 #include "kernels.h"
 
@@ -70,6 +70,18 @@ __global__ __launch_bounds__(256) void im2col3x3_kernel(const float* __restrict_
     else static_cast<float*>(cols)[i] = v;
 }
 
+// F32 3x3 kernel [Cout][Cin][3][3] (ggml [3, 3, Cin, Cout]) -> rows [Cout][tap][Cin],
+// tap = kh*3 + kw: the K order of the implicit-GEMM convolution
+__global__ __launch_bounds__(256) void conv3x3_pack_kernel(const float* __restrict__ w, int Cin, int Cout,
+                                                           float* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= 9LL * Cin * Cout) return;
+    const int ci = (int)(i % Cin);
+    const int64_t r = i / Cin;
+    const int tap = (int)(r % 9), co = (int)(r / 9);
+    out[i] = w[((int64_t)co * Cin + ci) * 9 + tap];
+}
+
 // y[r][c] += b[c], four channels per thread (C % 4 == 0)
 __global__ __launch_bounds__(256) void bias_rows_kernel(float* __restrict__ y, const float* __restrict__ b, int64_t rows,
                                                         int C) {
@@ -119,6 +131,12 @@ hipError_t launch_im2col3x3(const float* x, int H, int W, int C, bool f16, void*
     if (n <= 0) return hipSuccess;
     if (f16) im2col3x3_kernel<true><<<nblk(n), 256, 0, st>>>(x, H, W, C, cols);
     else im2col3x3_kernel<false><<<nblk(n), 256, 0, st>>>(x, H, W, C, cols);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv3x3_pack(const float* w, int Cin, int Cout, float* out, hipStream_t st) {
+    const int64_t n = 9LL * Cin * Cout;
+    if (n > 0) conv3x3_pack_kernel<<<nblk(n), 256, 0, st>>>(w, Cin, Cout, out);
     return hipGetLastError();
 }
 
