@@ -15,7 +15,10 @@
 //            LDS, B = the wavefront's Q fragment held in registers), so each
 //            lane owns one query column and 16 keys of every 32-key block:
 //            row max / row sum are in-lane plus one exchange with lane l ^ 32.
-//   softmax: exp2 domain, c = |scale| * log2(e) folded into one FMA per score.
+//   softmax: exp2 domain, c = |scale| * log2(e) folded into one FMA per score;
+//            the running max is raised lazily (only by more than 8), so most
+//            tiles skip rescaling O; P is packed to fp16 pairs by one convert
+//            and the row sum takes the same fp16 values through dot2.
 //   output:  O^T[d][q] += V^T P^T.  The P registers are used directly as the
 //            B operand: MFMA k-slot j of lane group g carries key
 //            16h + 8(j/4) + 4g + j%4 of the 32-key block, and the V^T rows
@@ -35,6 +38,7 @@ constexpr int FA_BQ = 128, FA_BKV = 64, FA_NT = 256;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
 typedef v4f v4f_a4 __attribute__((aligned(4)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 }  // namespace
 
 // 8 consecutive elements of a row as fp16 (RNE), packed in 4 dwords
@@ -174,26 +178,37 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) mx = fmaxf(mx, S[kh][i]);
         mx = xmax32(mx);
-        const float m_new = fmaxf(m_run, mx * c);
+        // the running max moves only when the tile's max exceeds it by more than 8 (in
+        // log2 units): probabilities then stay below 2^8, and the rescale of O is skipped
+        // by the whole wavefront in the tiles where no query's max moved
+        const float m_cand = fmaxf(m_run, mx * c);
+        const bool grow = m_cand > m_run + 8.0f;
+        const float m_new = grow ? m_cand : m_run;
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
         m_run = m_new;
+        // probabilities rounded to fp16 in pairs (the PV operand); the row sum adds the same
+        // rounded values (one dot2 per pair), so numerator and denominator agree
         float ls = 0.0f;
         uint32_t P[2][8];
+        const h2v ones = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
             for (int i = 0; i < 16; i += 2) {
-                const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kh][i], c, -m_new));
-                const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(S[kh][i + 1], c, -m_new));
-                ls += p0 + p1;
-                P[kh][i >> 1] = (uint32_t)f2h(p0) | ((uint32_t)f2h(p1) << 16);
+                const v2f pp = {__builtin_amdgcn_exp2f(__builtin_fmaf(S[kh][i], c, -m_new)),
+                                __builtin_amdgcn_exp2f(__builtin_fmaf(S[kh][i + 1], c, -m_new))};
+                const h2v ph = __builtin_convertvector(pp, h2v);
+                ls = __builtin_amdgcn_fdot2(ph, ones, ls, false);
+                P[kh][i >> 1] = __builtin_bit_cast(uint32_t, ph);
             }
         ls = xsum32(ls);
         l_run = l_run * alpha + ls;
+        if (__builtin_amdgcn_ballot_w64(grow)) {
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+            for (int db = 0; db < NDB; ++db)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) O[db][e] *= alpha;
+                for (int e = 0; e < 16; ++e) O[db][e] *= alpha;
+        }
 
         // O^T += V^T P^T over the 64 keys (four 16-key MFMA chunks)
 #pragma unroll
