@@ -109,6 +109,14 @@ __device__ __forceinline__ void act_store_chunk(const ActOut& o, int64_t row, in
 // without FMA contraction).
 template <int V>
 __device__ __forceinline__ void ln_group(v4f (&x)[V], int l, int G, int C, const float* w, const float* b, float eps) {
+    // the affine rows are loaded up front, so their latency overlaps the reductions
+    v4f wv[V], bv[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        const int c = v * G + l;
+        wv[v] = w ? *reinterpret_cast<const v4f*>(w + 4 * c) : v4f{1.0f, 1.0f, 1.0f, 1.0f};
+        bv[v] = b ? *reinterpret_cast<const v4f*>(b + 4 * c) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
     double s = 0.0;
 #pragma unroll
     for (int v = 0; v < V; ++v)
@@ -130,10 +138,9 @@ __device__ __forceinline__ void ln_group(v4f (&x)[V], int l, int G, int C, const
     const float scale = 1.0f / sqrtf(var + eps);
 #pragma unroll
     for (int v = 0; v < V; ++v) {
-        const int c = v * G + l;
         v4f t = x[v] * scale;
-        if (w) t = t * *reinterpret_cast<const v4f*>(w + 4 * c);
-        if (b) t = t + *reinterpret_cast<const v4f*>(b + 4 * c);
+        if (w) t = t * wv[v];
+        if (b) t = t + bv[v];
         x[v] = t;
     }
 }
