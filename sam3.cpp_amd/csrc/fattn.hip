@@ -23,9 +23,9 @@
 //            B operand: MFMA k-slot j of lane group g carries key
 //            16h + 8(j/4) + 4g + j%4 of the 32-key block, and the V^T rows
 //            are read from LDS with the same key order.
-// K is staged row-major and V transposed, both with rows padded by 16 bytes
-// so the 32-row fragment reads spread over all LDS banks.  The next tile's
-// global loads go to registers before the current tile's MFMAs.
+// K is staged row-major with rows padded by 16 bytes and V transposed with
+// rows padded by 8 bytes, so the 32-row fragment reads spread over all LDS
+// banks (no bank conflicts in rocprofv3's counters).  The next tile's// global loads go to registers before the current tile's MFMAs.
 #include <algorithm>
 
 #include "common.cuh"
@@ -69,7 +69,7 @@ __device__ __forceinline__ float xsum32(float x) { return x + partner32(x); }
 template <int D, bool QF32, bool KVF32>
 __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
     constexpr int KS = D + 8;       // K tile row stride (halves)
-    constexpr int VS = FA_BKV + 8;  // V^T tile row stride (halves)
+    constexpr int VS = FA_BKV + 4;  // V^T tile row stride (halves): 34 dwords, so the 8-byte reads of 32 rows hit distinct bank pairs
     constexpr int NC = D / 16;      // MFMA k-chunks of a score
     constexpr int NDB = D / 32;     // 32-row blocks of O^T
     constexpr int C8 = D / 8;       // 8-element chunks per key row
