@@ -25,7 +25,8 @@
 //            are read from LDS with the same key order.
 // K is staged row-major with rows padded by 16 bytes and V transposed with
 // rows padded by 8 bytes, so the 32-row fragment reads spread over all LDS
-// banks (no bank conflicts in rocprofv3's counters).  The next tile's// global loads go to registers before the current tile's MFMAs.
+// banks (no bank conflicts in rocprofv3's counters).  The next tile's
+// global loads go to registers before the current tile's MFMAs.
 #include <algorithm>
 
 #include "common.cuh"
