@@ -885,18 +885,21 @@ static hipError_t try_skinny(const MatW& w, const ActF16& a, const MatD& d, int6
     p.npad = (int)((N + 31) / 32 * 32);
     p.wpitch = wpitch;
     const unsigned grid = (unsigned)((a.M + 32 * smt - 1) / (32 * smt));
-    // dynamic LDS beyond 64 KB, allowed once per kernel
-    static bool attr[6] = {false, false, false, false, false, false};
+    // dynamic LDS beyond 64 KB, allowed once per kernel and device (the attribute is
+    // per device); concurrent first calls only repeat the same setting
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return hipSuccess;
+    static bool attr[64][6] = {};
     const int ti = (w.type == T_Q8_0 ? 0 : w.type == T_Q4_0 ? 1 : 2) * 2 + (smt == 4 ? 1 : 0);
     const void* fns[6] = {(const void*)mmq_skinny_kernel<T_Q8_0, 2>, (const void*)mmq_skinny_kernel<T_Q8_0, 4>,
                           (const void*)mmq_skinny_kernel<T_Q4_0, 2>, (const void*)mmq_skinny_kernel<T_Q4_0, 4>,
                           (const void*)mmq_skinny_kernel<T_Q4_1, 2>, (const void*)mmq_skinny_kernel<T_Q4_1, 4>};
-    if (!attr[ti]) {
+    if (!attr[dev][ti]) {
         if (hipFuncSetAttribute(fns[ti], hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024) != hipSuccess) {
             (void)hipGetLastError();  // not done: the tiled kernel takes it
             return hipSuccess;
         }
-        attr[ti] = true;
+        attr[dev][ti] = true;
     }
     switch (ti) {
         case 0: mmq_skinny_kernel<T_Q8_0, 2><<<grid, 256, lds, st>>>(p); break;
