@@ -12,9 +12,10 @@
 //     the bias (and the GELU of scale 0) applied in the scatter;
 //   - conv_2d_sk_p0 1x1: a MUL_MAT with the kernel rows as they are (F32
 //     kernels: the tiled fp32 GEMM with the bias in its epilogue);
-//   - conv_2d_s1_ph 3x3: F32 kernels as an implicit GEMM over the map (the
-//     kernel repacked to (tap, channel) rows, no im2col); F16 kernels as im2col
-//     (K ordered as ggml's, ic-major) + MUL_MAT;
+//   - conv_2d_s1_ph 3x3: an implicit GEMM over the map (the kernel repacked to
+//     (tap, channel) rows, no im2col) on fp32 MFMA (F32 kernels) or fp16 MFMA
+//     (F16 kernels, the map rounded to fp16 as it is loaded); maps with
+//     Cin % 32 != 0 take im2col (K ordered as ggml's, ic-major) + MUL_MAT;
 //   - pool_2d MAX 2x2 / 2.
 // Each op's numerics are ggml-cpu's: operands in the kernel's type (F16
 // rounded to nearest even, or F32), f32 accumulation, f32 bias adds.
@@ -58,12 +59,15 @@ mi355_status check_kernel(mi355_context* ctx, const mi355_tensor* w, const float
 size_t deconv_scratch(int64_t P, int64_t Cin, int64_t Cout) {
     return align_up((size_t)(4 * Cout * Cin * 2)) + align_up((size_t)(P * 4 * Cout * 4));
 }
-// F32 3x3 with Cin % 32 == 0: the kernel repacked to (tap, channel) rows for the implicit
-// GEMM; otherwise the im2col columns in the kernel's type
-size_t conv_scratch(int64_t P, int64_t Cin, int64_t Cout, int k, int wtype) {
+// a 3x3 runs as an implicit GEMM when its map rows are 16-byte aligned and Cin % 32 == 0
+bool implicit3x3(const float* x, int64_t Cin) { return (reinterpret_cast<uintptr_t>(x) & 15) == 0 && Cin % 32 == 0; }
+// implicit 3x3: the kernel repacked to (tap, channel) rows; otherwise the im2col
+// columns in the kernel's type (x_aligned: the map's rows are 16-byte aligned)
+size_t conv_scratch(int64_t P, int64_t Cin, int64_t Cout, int k, int wtype, bool x_aligned) {
     if (k == 1) return 0;
-    if (wtype == T_F32 && Cin % 32 == 0) return align_up((size_t)(9 * Cin * Cout * 4));
-    return align_up((size_t)(P * 9 * Cin * (wtype == T_F32 ? 4 : 2)));
+    const int64_t es = wtype == T_F32 ? 4 : 2;
+    if (x_aligned && Cin % 32 == 0) return align_up((size_t)(9 * Cin * Cout * es));
+    return align_up((size_t)(P * 9 * Cin * es));
 }
 
 // conv_transpose_2d_p0(kernel [2, 2, Cout, Cin], stride 2) + bias (+ GELU):
@@ -106,7 +110,7 @@ mi355_status conv(mi355_context* ctx, const mi355_tensor* w, const float* b, con
     // rows; maps whose rows are not 16-byte aligned (or a 3x3 with Cin % 32 != 0) take
     // im2col + MUL_MAT below
     const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && Cin % 4 == 0;
-    if (w->type == T_F32 && aligned && (k == 1 || Cin % 32 == 0)) {
+    if (w->type == T_F32 && aligned && (k == 1 || implicit3x3(x, Cin))) {
         if (k == 3) {
             Timed t(ctx, "neck_conv3x3_pack");
             st = hip_check(ctx, t.done(launch_conv3x3_pack(static_cast<const float*>(w->data), Cin, Cout,
@@ -135,6 +139,20 @@ mi355_status conv(mi355_context* ctx, const mi355_tensor* w, const float* b, con
         g.C = Cin;
         Timed t(ctx, k == 3 ? "neck_conv3x3_f32" : "neck_conv1x1_f32");
         return hip_check(ctx, t.done(launch_gemm_f32(g, 1, ctx->stream)), "gemm_f32 launch");
+    }
+    if (w->type == T_F16 && k == 3 && implicit3x3(x, Cin)) {
+        // F16 3x3 as an implicit GEMM on fp16 MFMA, bias in its epilogue
+        {
+            Timed t(ctx, "neck_conv3x3_pack");
+            st = hip_check(ctx, t.done(launch_conv3x3_pack_f16(static_cast<const uint16_t*>(w->data), Cin, Cout,
+                                                               reinterpret_cast<uint16_t*>(scratch), ctx->stream)),
+                           "conv3x3 pack");
+            if (st != MI355_STATUS_SUCCESS) return st;
+        }
+        Timed t(ctx, "neck_conv3x3_f16");
+        return hip_check(ctx, t.done(launch_conv3x3_f16(x, reinterpret_cast<const uint16_t*>(scratch), b, H, W, Cin, Cout,
+                                                        y, ctx->stream)),
+                         "conv3x3_f16 launch");
     }
     const mi355_tensor s0 = dev_t(w->data, w->type, K, Cout), d = dev_t(y, T_F32, Cout, P);
     mi355_tensor s1 = dev_t(x, T_F32, Cin, P);
@@ -185,19 +203,19 @@ bool neck_plan(int E, int G, const mi355_neck_scale* s, NeckPlan* pl) {
     mapb(16 * G2, s[0].conv1x1_w->ne[3]);
     scr(deconv_scratch(G2, E, C1));
     scr(deconv_scratch(4 * G2, C1, D0));
-    scr(conv_scratch(16 * G2, s[0].conv3x3_w->ne[2], s[0].conv3x3_w->ne[3], 3, s[0].conv3x3_w->type));
+    scr(conv_scratch(16 * G2, s[0].conv3x3_w->ne[2], s[0].conv3x3_w->ne[3], 3, s[0].conv3x3_w->type, true));
     // scale 1: deconv E->C1 (2G), 1x1, 3x3
     const int64_t C1b = s[1].deconv1_w->ne[2];
     mapb(4 * G2, C1b);
     mapb(4 * G2, s[1].conv1x1_w->ne[3]);
     scr(deconv_scratch(G2, E, C1b));
-    scr(conv_scratch(4 * G2, s[1].conv3x3_w->ne[2], s[1].conv3x3_w->ne[3], 3, s[1].conv3x3_w->type));
+    scr(conv_scratch(4 * G2, s[1].conv3x3_w->ne[2], s[1].conv3x3_w->ne[3], 3, s[1].conv3x3_w->type, true));
     // scale 2: 1x1, 3x3 at G; scale 3: pool, 1x1, 3x3 at G/2
     mapb(G2, s[2].conv1x1_w->ne[3]);
-    scr(conv_scratch(G2, s[2].conv3x3_w->ne[2], s[2].conv3x3_w->ne[3], 3, s[2].conv3x3_w->type));
+    scr(conv_scratch(G2, s[2].conv3x3_w->ne[2], s[2].conv3x3_w->ne[3], 3, s[2].conv3x3_w->type, true));
     mapb(G2 / 4, E);
     mapb(G2 / 4, s[3].conv1x1_w->ne[3]);
-    scr(conv_scratch(G2 / 4, s[3].conv3x3_w->ne[2], s[3].conv3x3_w->ne[3], 3, s[3].conv3x3_w->type));
+    scr(conv_scratch(G2 / 4, s[3].conv3x3_w->ne[2], s[3].conv3x3_w->ne[3], 3, s[3].conv3x3_w->type, true));
     return true;
 }
 
@@ -225,7 +243,8 @@ mi355_status mi355_neck_conv(mi355_context* ctx, const mi355_tensor* w, const fl
     (void)hipSetDevice(ctx->device);
     char* scr = nullptr;
     const int k = (int)w->ne[0];
-    mi355_status st = scratch_for(ctx, k == 3 ? conv_scratch((int64_t)H * W, w->ne[2], w->ne[3], 3, w->type) : 0, &scr);
+    const size_t sb = k == 3 ? conv_scratch((int64_t)H * W, w->ne[2], w->ne[3], 3, w->type, implicit3x3(x, w->ne[2])) : 0;
+    mi355_status st = scratch_for(ctx, sb, &scr);
     if (st != MI355_STATUS_SUCCESS) return st;
     return conv(ctx, w, b, x, H, W, y, scr);
 }

@@ -82,6 +82,115 @@ __global__ __launch_bounds__(256) void conv3x3_pack_kernel(const float* __restri
     out[i] = w[((int64_t)co * Cin + ci) * 9 + tap];
 }
 
+// F16 3x3 kernel [Cout][Cin][3][3] -> rows [Cout][tap][Cin] (the implicit GEMM's K order)
+__global__ __launch_bounds__(256) void conv3x3_pack_f16_kernel(const uint16_t* __restrict__ w, int Cin, int Cout,
+                                                               uint16_t* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= 9LL * Cin * Cout) return;
+    const int ci = (int)(i % Cin);
+    const int64_t r = i / Cin;
+    const int tap = (int)(r % 9), co = (int)(r / 9);
+    out[i] = w[((int64_t)co * Cin + ci) * 9 + tap];
+}
+
+// ggml_conv_2d_s1_ph with an F16 kernel as an implicit GEMM: y[p][n] = bias[n] +
+// sum_{tap, c} f16(x[p + tap offset][c]) * w[n][tap][c] over a token-major map
+// (C % 32 == 0), zero outside the image.  The activations are rounded to fp16
+// (RNE) as they are loaded, exactly as ggml's F16 im2col rounds them, so the
+// products are those of im2col + F16 MUL_MAT; fp32 accumulation.
+// Workgroup 128(m) x 128(n), four wavefronts of 64 x 64 (2 x 2
+// v_mfma_f32_32x32x16_f16 tiles), K staged 32 at a time (one tap's channel
+// slice) through two LDS buffers; rows of 32 halves at a 40-half pitch, so the
+// 16 rows one ds_read_b128 pass touches land on distinct 4-bank groups.
+namespace {
+constexpr int CT = 128, CK = 32, CP = 40;
+}
+__global__ __launch_bounds__(256, 2) void conv3x3_f16_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
+                                                             const float* __restrict__ bias, int H, int W, int C, int N,
+                                                             float* __restrict__ y) {
+    __shared__ __attribute__((aligned(16))) _Float16 sA[2][CT * CP];
+    __shared__ __attribute__((aligned(16))) _Float16 sB[2][CT * CP];
+    const int M = H * W, K = 9 * C;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wv & 1, wn = wv >> 1;
+    const int lr = lane & 31, g = lane >> 5;
+    // XCD-aware tile order (each XCD a contiguous band of tiles)
+    const int tiles_n = (N + CT - 1) / CT, tiles = ((M + CT - 1) / CT) * tiles_n;
+    const int per_xcd = (tiles + 7) / 8;
+    const int tl = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tl >= tiles) return;
+    const int m0 = (tl / tiles_n) * CT, n0 = (tl % tiles_n) * CT;
+    // loader: thread t fills row t/2 of both tiles, K values 16*(t%2) .. +15 of the stage
+    const int lrow = tid >> 1, lk = 16 * (tid & 1);
+    const int am = m0 + lrow, bn = n0 + lrow;
+    const int oy = am / W, ox = am - (am / W) * W;
+    uint4 ra[2], rb[2];
+    auto load = [&](int k0) {
+        const int tap = k0 / C, c0 = k0 - tap * C;
+        const int iy = oy + tap / 3 - 1, ix = ox + tap % 3 - 1;
+        const bool in = am < M && iy >= 0 && iy < H && ix >= 0 && ix < W;
+        const float* src = x + ((int64_t)iy * W + ix) * C + c0 + lk;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            v4f a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
+            if (in) {
+                a = *reinterpret_cast<const v4f*>(src + 8 * h);
+                b = *reinterpret_cast<const v4f*>(src + 8 * h + 4);
+            }
+            ra[h] = uint4{(uint32_t)f2h(a[0]) | ((uint32_t)f2h(a[1]) << 16), (uint32_t)f2h(a[2]) | ((uint32_t)f2h(a[3]) << 16),
+                          (uint32_t)f2h(b[0]) | ((uint32_t)f2h(b[1]) << 16), (uint32_t)f2h(b[2]) | ((uint32_t)f2h(b[3]) << 16)};
+        }
+        const uint4* ws = reinterpret_cast<const uint4*>(w + (int64_t)bn * K + k0 + lk);
+        rb[0] = bn < N ? ws[0] : uint4{0, 0, 0, 0};
+        rb[1] = bn < N ? ws[1] : uint4{0, 0, 0, 0};
+    };
+    auto park = [&](int buf) {
+        *reinterpret_cast<uint4*>(&sA[buf][lrow * CP + lk]) = ra[0];
+        *reinterpret_cast<uint4*>(&sA[buf][lrow * CP + lk + 8]) = ra[1];
+        *reinterpret_cast<uint4*>(&sB[buf][lrow * CP + lk]) = rb[0];
+        *reinterpret_cast<uint4*>(&sB[buf][lrow * CP + lk + 8]) = rb[1];
+    };
+    const v16f zf = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    v16f acc[2][2] = {{zf, zf}, {zf, zf}};
+    const int nst = K / CK;
+    load(0);
+    park(0);
+    __syncthreads();
+    for (int s = 0; s < nst; ++s) {
+        const int buf = s & 1;
+        if (s + 1 < nst) load((s + 1) * CK);
+#pragma unroll
+        for (int kk = 0; kk < CK / 16; ++kk) {
+            v8h a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                a[i] = *reinterpret_cast<const v8h*>(&sA[buf][(wm * 64 + i * 32 + lr) * CP + 16 * kk + 8 * g]);
+                b[i] = *reinterpret_cast<const v8h*>(&sB[buf][(wn * 64 + i * 32 + lr) * CP + 16 * kk + 8 * g]);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        if (s + 1 < nst) park(buf ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn * 64 + j * 32 + lr;
+        if (n >= N) continue;
+        const float bv = bias[n];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                if (m < M) y[(int64_t)m * N + n] = acc[i][j][r] + bv;
+            }
+    }
+}
+
 // y[r][c] += b[c], four channels per thread (C % 4 == 0)
 __global__ __launch_bounds__(256) void bias_rows_kernel(float* __restrict__ y, const float* __restrict__ b, int64_t rows,
                                                         int C) {
@@ -137,6 +246,23 @@ hipError_t launch_im2col3x3(const float* x, int H, int W, int C, bool f16, void*
 hipError_t launch_conv3x3_pack(const float* w, int Cin, int Cout, float* out, hipStream_t st) {
     const int64_t n = 9LL * Cin * Cout;
     if (n > 0) conv3x3_pack_kernel<<<nblk(n), 256, 0, st>>>(w, Cin, Cout, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv3x3_pack_f16(const uint16_t* w, int Cin, int Cout, uint16_t* out, hipStream_t st) {
+    const int64_t n = 9LL * Cin * Cout;
+    if (n > 0) conv3x3_pack_f16_kernel<<<nblk(n), 256, 0, st>>>(w, Cin, Cout, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv3x3_f16(const float* x, const uint16_t* w, const float* bias, int H, int W, int C, int N,
+                              float* y, hipStream_t st) {
+    if (C % CK != 0 || (reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(w) & 15))
+        return hipErrorInvalidValue;
+    const int64_t M = (int64_t)H * W;
+    if (M <= 0 || N <= 0) return hipSuccess;
+    const int tiles = (int)(((M + CT - 1) / CT) * ((N + CT - 1) / CT));
+    conv3x3_f16_kernel<<<(unsigned)((tiles + 7) / 8 * 8), 256, 0, st>>>(x, w, bias, H, W, C, N, y);
     return hipGetLastError();
 }
 

@@ -112,6 +112,33 @@ def test_neck_conv(mi, ctx, orc, wtype, k, Cin, Cout, H, W):
     check_conv(got, w, t, b, x, H, W)
 
 
+@pytest.mark.parametrize("wtype", ["f32", "f16"])
+def test_neck_conv3x3_unaligned_map(mi, orc, wtype):
+    """A 3x3 over a map whose rows are not 16-byte aligned takes im2col + MUL_MAT;
+    its scratch is sized for the columns (P * 9 * Cin), not for the repacked
+    kernel, in a fresh context whose neck scratch has not grown before."""
+    rng = np.random.default_rng(77)
+    Cout, Cin, H, W = 32, 64, 17, 15
+    t = mi.F16 if wtype == "f16" else mi.F32
+    w = rand(rng, (Cout, Cin, 3, 3), 0.05)
+    if t == mi.F16:
+        w = neck.f16r(w)
+    b, x = rand(rng, Cout, 0.1), rand(rng, (H * W, Cin))
+    c = mi.Context(0)
+    try:
+        wt = kernel_tensor(mi, w, t, [3, 3, Cin, Cout])
+        bd = dev(b)
+        xd = torch.zeros(H * W * Cin + 1, dtype=torch.float32, device="cuda")
+        xd[1:] = torch.from_numpy(x.reshape(-1)).cuda()
+        y = torch.full((H * W, Cout), float("nan"), dtype=torch.float32, device="cuda")
+        c.neck_conv(wt, bd.data_ptr(), xd.data_ptr() + 4, H, W, y.data_ptr())
+        c.synchronize()
+        got = y.cpu().numpy()
+    finally:
+        c.close()
+    check_conv(got, w, t, b, x, H, W)
+
+
 def test_neck_maxpool(mi, ctx):
     rng = np.random.default_rng(2)
     H, W, Cc = 10, 6, 12
