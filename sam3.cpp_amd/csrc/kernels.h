@@ -238,8 +238,11 @@ hipError_t launch_deconv_scatter(const float* D, const float* b, int H, int W, i
 hipError_t launch_im2col3x3(const float* x, int H, int W, int C, bool f16, void* cols, hipStream_t st);
 hipError_t launch_conv3x3_pack(const float* w, int Cin, int Cout, float* out, hipStream_t st);
 hipError_t launch_conv3x3_pack_f16(const uint16_t* w, int Cin, int Cout, uint16_t* out, hipStream_t st);
-hipError_t launch_conv3x3_f16(const float* x, const uint16_t* w, const float* bias, int H, int W, int C, int N,
-                              float* y, hipStream_t st);
+// taps: 9 (3x3, kernel packed by launch_conv3x3_pack_f16), 1 (1x1, the kernel as
+// stored) or 4 (2x2 / stride-2 conv-transpose, kernel packed by launch_deconv_pack,
+// N = 4 * Cout, y the 2x map, GELU-erf after the bias if gelu)
+hipError_t launch_conv_f16(int taps, const float* x, const uint16_t* w, const float* bias, int H, int W, int C, int N,
+                           bool gelu, float* y, hipStream_t st);
 hipError_t launch_bias_rows(float* y, const float* b, int64_t rows, int C, hipStream_t st);
 hipError_t launch_maxpool2(const float* x, int H, int W, int C, float* y, hipStream_t st);
 hipError_t launch_hiera_pos_embed(const float* bkg, int E, int bh, int bw, const float* win, int ws, int H, int W,

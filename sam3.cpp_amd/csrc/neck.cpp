@@ -7,15 +7,19 @@
 // [H*W][C] (= ggml [C, W, H], the layout of its input and outputs), so each
 // convolution is a MUL_MAT over pixels with no permutes:
 //   - conv_transpose_2d_p0 (kernel 2, stride 2): the taps do not overlap, so
-//     it is one F16 MUL_MAT [pixels x Cin] x [Cin x 4*Cout] (kernel cast to F16
+//     it is one F16 GEMM [pixels x Cin] x [Cin x 4*Cout] (kernel cast to F16
 //     and repacked tap-major) whose columns are scattered to the 2x map, with
-//     the bias (and the GELU of scale 0) applied in the scatter;
-//   - conv_2d_sk_p0 1x1: a MUL_MAT with the kernel rows as they are (F32
-//     kernels: the tiled fp32 GEMM with the bias in its epilogue);
+//     the bias (and the GELU of scale 0): in the fp16 implicit-GEMM kernel's
+//     epilogue, or (maps with Cin % 32 != 0 or unaligned rows) as a MUL_MAT
+//     and a scatter pass;
+//   - conv_2d_sk_p0 1x1: a GEMM with the kernel rows as they are, the bias in
+//     its epilogue (F32 kernels: the tiled fp32 GEMM; F16 kernels: the fp16
+//     implicit-GEMM kernel below with one tap);
 //   - conv_2d_s1_ph 3x3: an implicit GEMM over the map (the kernel repacked to
 //     (tap, channel) rows, no im2col) on fp32 MFMA (F32 kernels) or fp16 MFMA
 //     (F16 kernels, the map rounded to fp16 as it is loaded); maps with
-//     Cin % 32 != 0 take im2col (K ordered as ggml's, ic-major) + MUL_MAT;
+//     Cin % 32 != 0 or rows not 16-byte aligned take im2col (K ordered as
+//     ggml's, ic-major) or the plain map + MUL_MAT + bias;
 //   - pool_2d MAX 2x2 / 2.
 // Each op's numerics are ggml-cpu's: operands in the kernel's type (F16
 // rounded to nearest even, or F32), f32 accumulation, f32 bias adds.
@@ -55,12 +59,13 @@ mi355_status check_kernel(mi355_context* ctx, const mi355_tensor* w, const float
     return MI355_STATUS_SUCCESS;
 }
 
-// scratch bytes of each op (the MUL_MAT's own workspace is the context's)
+// scratch bytes of each op (the MUL_MAT's own workspace is the context's); the
+// conv-transpose's GEMM output D is only written when the map takes the MUL_MAT path
 size_t deconv_scratch(int64_t P, int64_t Cin, int64_t Cout) {
     return align_up((size_t)(4 * Cout * Cin * 2)) + align_up((size_t)(P * 4 * Cout * 4));
 }
-// a 3x3 runs as an implicit GEMM when its map rows are 16-byte aligned and Cin % 32 == 0
-bool implicit3x3(const float* x, int64_t Cin) { return (reinterpret_cast<uintptr_t>(x) & 15) == 0 && Cin % 32 == 0; }
+// the implicit-GEMM kernels take maps whose rows are 16-byte aligned with Cin % 32 == 0
+bool implicit_ok(const float* x, int64_t Cin) { return (reinterpret_cast<uintptr_t>(x) & 15) == 0 && Cin % 32 == 0; }
 // implicit 3x3: the kernel repacked to (tap, channel) rows; otherwise the im2col
 // columns in the kernel's type (x_aligned: the map's rows are 16-byte aligned)
 size_t conv_scratch(int64_t P, int64_t Cin, int64_t Cout, int k, int wtype, bool x_aligned) {
@@ -86,6 +91,12 @@ mi355_status deconv(mi355_context* ctx, const mi355_tensor* w, const float* b, c
         st = hip_check(ctx, t.done(launch_deconv_pack(w->data, w->type, Cin, Cout, packed, ctx->stream)), "deconv pack");
         if (st != MI355_STATUS_SUCCESS) return st;
     }
+    if (implicit_ok(x, Cin)) {
+        // one fp16-MFMA GEMM whose epilogue adds the bias (+ GELU) and scatters to the 2x map
+        Timed t(ctx, "neck_deconv_f16");
+        return hip_check(ctx, t.done(launch_conv_f16(4, x, packed, b, H, W, Cin, 4 * Cout, gelu, y, ctx->stream)),
+                         "deconv_f16 launch");
+    }
     const mi355_tensor s0 = dev_t(packed, T_F16, Cin, 4LL * Cout), s1 = dev_t(x, T_F32, Cin, P),
                        d = dev_t(D, T_F32, 4LL * Cout, P);
     st = mi355_mul_mat(ctx, &s0, &s1, &d);
@@ -110,7 +121,7 @@ mi355_status conv(mi355_context* ctx, const mi355_tensor* w, const float* b, con
     // rows; maps whose rows are not 16-byte aligned (or a 3x3 with Cin % 32 != 0) take
     // im2col + MUL_MAT below
     const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && Cin % 4 == 0;
-    if (w->type == T_F32 && aligned && (k == 1 || implicit3x3(x, Cin))) {
+    if (w->type == T_F32 && aligned && (k == 1 || implicit_ok(x, Cin))) {
         if (k == 3) {
             Timed t(ctx, "neck_conv3x3_pack");
             st = hip_check(ctx, t.done(launch_conv3x3_pack(static_cast<const float*>(w->data), Cin, Cout,
@@ -140,19 +151,20 @@ mi355_status conv(mi355_context* ctx, const mi355_tensor* w, const float* b, con
         Timed t(ctx, k == 3 ? "neck_conv3x3_f32" : "neck_conv1x1_f32");
         return hip_check(ctx, t.done(launch_gemm_f32(g, 1, ctx->stream)), "gemm_f32 launch");
     }
-    if (w->type == T_F16 && k == 3 && implicit3x3(x, Cin)) {
-        // F16 3x3 as an implicit GEMM on fp16 MFMA, bias in its epilogue
-        {
+    if (w->type == T_F16 && implicit_ok(x, Cin) && (k == 3 || (reinterpret_cast<uintptr_t>(w->data) & 15) == 0)) {
+        // F16 kernels: an implicit GEMM on fp16 MFMA (the map rounded to fp16 as it
+        // is loaded), bias in its epilogue; the 3x3 kernel repacked to (tap, channel)
+        if (k == 3) {
             Timed t(ctx, "neck_conv3x3_pack");
             st = hip_check(ctx, t.done(launch_conv3x3_pack_f16(static_cast<const uint16_t*>(w->data), Cin, Cout,
                                                                reinterpret_cast<uint16_t*>(scratch), ctx->stream)),
                            "conv3x3 pack");
             if (st != MI355_STATUS_SUCCESS) return st;
         }
-        Timed t(ctx, "neck_conv3x3_f16");
-        return hip_check(ctx, t.done(launch_conv3x3_f16(x, reinterpret_cast<const uint16_t*>(scratch), b, H, W, Cin, Cout,
-                                                        y, ctx->stream)),
-                         "conv3x3_f16 launch");
+        const uint16_t* wk = k == 3 ? reinterpret_cast<const uint16_t*>(scratch) : static_cast<const uint16_t*>(w->data);
+        Timed t(ctx, k == 3 ? "neck_conv3x3_f16" : "neck_conv1x1_f16");
+        return hip_check(ctx, t.done(launch_conv_f16(k * k, x, wk, b, H, W, Cin, Cout, false, y, ctx->stream)),
+                         "conv_f16 launch");
     }
     const mi355_tensor s0 = dev_t(w->data, w->type, K, Cout), d = dev_t(y, T_F32, Cout, P);
     mi355_tensor s1 = dev_t(x, T_F32, Cin, P);
@@ -243,7 +255,7 @@ mi355_status mi355_neck_conv(mi355_context* ctx, const mi355_tensor* w, const fl
     (void)hipSetDevice(ctx->device);
     char* scr = nullptr;
     const int k = (int)w->ne[0];
-    const size_t sb = k == 3 ? conv_scratch((int64_t)H * W, w->ne[2], w->ne[3], 3, w->type, implicit3x3(x, w->ne[2])) : 0;
+    const size_t sb = k == 3 ? conv_scratch((int64_t)H * W, w->ne[2], w->ne[3], 3, w->type, implicit_ok(x, w->ne[2])) : 0;
     mi355_status st = scratch_for(ctx, sb, &scr);
     if (st != MI355_STATUS_SUCCESS) return st;
     return conv(ctx, w, b, x, H, W, y, scr);

@@ -93,9 +93,13 @@ __global__ __launch_bounds__(256) void conv3x3_pack_f16_kernel(const uint16_t* _
     out[i] = w[((int64_t)co * Cin + ci) * 9 + tap];
 }
 
-// ggml_conv_2d_s1_ph with an F16 kernel as an implicit GEMM: y[p][n] = bias[n] +
-// sum_{tap, c} f16(x[p + tap offset][c]) * w[n][tap][c] over a token-major map
-// (C % 32 == 0), zero outside the image.  The activations are rounded to fp16
+// ggml_conv_2d_s1_ph (TAPS = 9) or ggml_conv_2d_sk_p0 1x1 (TAPS = 1) with an F16
+// kernel as an implicit GEMM: y[p][n] = bias[n] + sum_{tap, c} f16(x[p + tap
+// offset][c]) * w[n][tap][c] over a token-major map (C % 32 == 0), zero outside
+// the image.  TAPS = 4 is conv_transpose_2d_p0 (kernel 2, stride 2): the GEMM
+// of the map with the deconv_pack rows [4*Cout][C], each column n = t*Cout + co
+// stored to pixel (2py + t/2, 2px + t%2) of the 2x map as bias[co] + sum (then
+// GELU-erf if gelu), the scatter of deconv_scatter_kernel done in registers.  The activations are rounded to fp16
 // (RNE) as they are loaded, exactly as ggml's F16 im2col rounds them, so the
 // products are those of im2col + F16 MUL_MAT; fp32 accumulation.
 // Workgroup 128(m) x 128(n), four wavefronts of 64 x 64 (2 x 2
@@ -105,12 +109,13 @@ __global__ __launch_bounds__(256) void conv3x3_pack_f16_kernel(const uint16_t* _
 namespace {
 constexpr int CT = 128, CK = 32, CP = 40;
 }
-__global__ __launch_bounds__(256, 2) void conv3x3_f16_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
-                                                             const float* __restrict__ bias, int H, int W, int C, int N,
-                                                             float* __restrict__ y) {
+template <int TAPS>
+__global__ __launch_bounds__(256, 2) void conv_f16_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
+                                                          const float* __restrict__ bias, int H, int W, int C, int N,
+                                                          int gelu, float* __restrict__ y) {
     __shared__ __attribute__((aligned(16))) _Float16 sA[2][CT * CP];
     __shared__ __attribute__((aligned(16))) _Float16 sB[2][CT * CP];
-    const int M = H * W, K = 9 * C;
+    const int M = H * W, K = TAPS == 9 ? 9 * C : C;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wv & 1, wn = wv >> 1;
@@ -127,8 +132,8 @@ __global__ __launch_bounds__(256, 2) void conv3x3_f16_kernel(const float* __rest
     const int oy = am / W, ox = am - (am / W) * W;
     uint4 ra[2], rb[2];
     auto load = [&](int k0) {
-        const int tap = k0 / C, c0 = k0 - tap * C;
-        const int iy = oy + tap / 3 - 1, ix = ox + tap % 3 - 1;
+        const int tap = TAPS == 9 ? k0 / C : 0, c0 = k0 - tap * C;
+        const int iy = TAPS == 9 ? oy + tap / 3 - 1 : oy, ix = TAPS == 9 ? ox + tap % 3 - 1 : ox;
         const bool in = am < M && iy >= 0 && iy < H && ix >= 0 && ix < W;
         const float* src = x + ((int64_t)iy * W + ix) * C + c0 + lk;
 #pragma unroll
@@ -180,14 +185,30 @@ __global__ __launch_bounds__(256, 2) void conv3x3_f16_kernel(const float* __rest
     for (int j = 0; j < 2; ++j) {
         const int n = n0 + wn * 64 + j * 32 + lr;
         if (n >= N) continue;
-        const float bv = bias[n];
+        if (TAPS == 4) {
+            const int Cout = N >> 2, t = n / Cout, co = n - t * Cout;
+            const float bv = bias[co];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                if (m < M) y[(int64_t)m * N + n] = acc[i][j][r] + bv;
-            }
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (m >= M) continue;
+                    const int py = m / W, px = m - (m / W) * W;
+                    const int64_t pix = (int64_t)(2 * py + (t >> 1)) * (2 * W) + 2 * px + (t & 1);
+                    const float s = acc[i][j][r] + bv;
+                    y[pix * Cout + co] = gelu ? gelu_erf(s) : s;
+                }
+        } else {
+            const float bv = bias[n];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (m < M) y[(int64_t)m * N + n] = acc[i][j][r] + bv;
+                }
+        }
     }
 }
 
@@ -255,14 +276,22 @@ hipError_t launch_conv3x3_pack_f16(const uint16_t* w, int Cin, int Cout, uint16_
     return hipGetLastError();
 }
 
-hipError_t launch_conv3x3_f16(const float* x, const uint16_t* w, const float* bias, int H, int W, int C, int N,
-                              float* y, hipStream_t st) {
-    if (C % CK != 0 || (reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(w) & 15))
+hipError_t launch_conv_f16(int taps, const float* x, const uint16_t* w, const float* bias, int H, int W, int C, int N,
+                           bool gelu, float* y, hipStream_t st) {
+    if ((taps != 1 && taps != 4 && taps != 9) || C % CK != 0 || (reinterpret_cast<uintptr_t>(x) & 15) ||
+        (reinterpret_cast<uintptr_t>(w) & 15) || (taps == 4 && N % 4 != 0))
         return hipErrorInvalidValue;
     const int64_t M = (int64_t)H * W;
     if (M <= 0 || N <= 0) return hipSuccess;
     const int tiles = (int)(((M + CT - 1) / CT) * ((N + CT - 1) / CT));
-    conv3x3_f16_kernel<<<(unsigned)((tiles + 7) / 8 * 8), 256, 0, st>>>(x, w, bias, H, W, C, N, y);
+    const unsigned grid = (unsigned)((tiles + 7) / 8 * 8);
+    const int gl = gelu ? 1 : 0;
+    if (taps == 9)
+        conv_f16_kernel<9><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
+    else if (taps == 4)
+        conv_f16_kernel<4><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
+    else
+        conv_f16_kernel<1><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
     return hipGetLastError();
 }
 

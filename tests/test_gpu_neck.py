@@ -86,7 +86,7 @@ def check_conv(got, w, wtype, b, x, H, W, rows=None):
 
 @pytest.mark.parametrize("wtype", ["f32", "f16"])
 @pytest.mark.parametrize("gelu", [False, True])
-@pytest.mark.parametrize("Cin,Cout,H,W", [(64, 32, 6, 5), (96, 40, 3, 11)])
+@pytest.mark.parametrize("Cin,Cout,H,W", [(64, 32, 6, 5), (96, 40, 3, 11), (48, 12, 7, 3)])
 def test_neck_deconv(mi, ctx, orc, wtype, gelu, Cin, Cout, H, W):
     rng = np.random.default_rng(Cin + H)
     t = mi.F16 if wtype == "f16" else mi.F32
