@@ -29,6 +29,7 @@
 // numbered so each XCD (round-robin dispatch) walks n-tiles of its own band
 // of m-tiles.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.cuh"
 #include "kernels.h"
@@ -108,6 +109,7 @@ struct MmqArgs {
     int64_t d_nb1, d_nb2, d_nb3;
     int32_t* dots;             // block-dot inspection output (or null)
     int M, dp, N, K, ne12, r2, r3, tiles_m, tiles_n;  // dp: row pitch (halves) of the scale arrays
+    int gm;                    // m-tiles per group of the tile order
     int ksplit, sps;           // K split into ksplit ranges of sps stages; partial sums go to
     int64_t d_split;           // D + split * d_split (bytes), summed by mmq_reduce_kernel
     int d_v4;                  // D rows 16-byte aligned, N % 4 == 0: float4 stores through LDS
@@ -211,7 +213,12 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
     const int tl = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
     if (tl >= TT) return;
     const int t = tl / p.ksplit, split = tl - t * p.ksplit;
-    const int m0 = (t / p.tiles_n) * BM, n0 = (t % p.tiles_n) * BN;
+    // grouped order: gm m-tiles per group, n-major inside a group, so the
+    // workgroups resident on one XCD at a time share a few weight column
+    // tiles and activation row tiles in its L2
+    const int gsz = p.gm * p.tiles_n, grp = t / gsz, gr = t - grp * gsz;
+    const int gmr = min(p.gm, p.tiles_m - grp * p.gm);
+    const int m0 = (grp * p.gm + gr % gmr) * BM, n0 = (gr / gmr) * BN;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wn = __builtin_amdgcn_readfirstlane(tid >> 6);  // wavefront index (uniform)
@@ -385,8 +392,140 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
         }
     };
 
+    // Quantized weights (no block-dot output): each stage is 8 units (block bk,
+    // m-tile mt; mt fastest).  Unit u issues its three MFMAs (the isum in two,
+    // the scale outer product in one) into product buffer u % 2, then the fp32
+    // FMAs of unit u - 1 from the other buffer; the stage ends with unit 7's
+    // FMAs.  A wavefront's FMAs thus never wait for the MFMAs it has just
+    // issued and run while they execute (FMAs right behind their own MFMAs
+    // leave the matrix core idle while both wavefronts of a SIMD apply theirs).
+    // Every acc tile still receives its terms in block order (for Q4_1: the
+    // stage's offset term, then block 0, block 1).  Products do not live
+    // across stages: 16-register tuples carried around the K loop spill.
+    static_assert(MT == 4, "unit pipeline assumes four m-tiles per wavefront");
+    auto apply = [&](int mt, const v16f& I, const v16f& S) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[mt][i] = __builtin_fmaf(I[i], S[i], acc[mt][i]);
+    };
+    // Fragments of unit (bk, mt): the two 8-half activation chunks of row
+    // mt*32 + lr and the row's activation scale.  Unit u reads unit u + 1's
+    // while its MFMAs run, so only a stage's first unit waits on LDS.
+    struct Frag {
+        v8h a0, a1;
+        uint32_t da;
+    };
+    auto load_frag = [&](const St& b, auto bkc, auto mtc) __attribute__((always_inline)) -> Frag {
+        constexpr int bk = decltype(bkc)::value, mt = decltype(mtc)::value;
+        const int ar_ = mt * 32 + lr;
+        Frag f;
+        f.a0 = frag(b.A, ar_, 4 * bk + g);
+        f.a1 = frag(b.A, ar_, 4 * bk + 2 + g);
+        f.da = reinterpret_cast<const uint16_t*>(&b.Ad[0][0])[ar_ * BKB + bk];
+        return f;
+    };
+    // weight fragments of block bk (row wrow, k-chunk 8g..8g+7 of each 16-wide
+    // half) and the S-MFMA B operand: d_w in k-slot 0 (lanes 0..31), zero in
+    // every other k-slot.  A block past K (odd block count) gets d_w = 0: its raw
+    // bytes belong to the next row (or padding) and its d_a is 0, so S = 0.
+    struct WFrag {
+        v8h bf[2];
+        v4i dwf;
+    };
+    auto load_wfrag = [&](int s, const St& b, auto bkc) __attribute__((always_inline)) -> WFrag {
+        constexpr int bk = decltype(bkc)::value;
+        const uint32_t* rowp = &b.W[wrow * RD];
+        const uint16_t* hrow = reinterpret_cast<const uint16_t*>(rowp);
+        WFrag w;
+        if (WT == T_Q8_0) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint32_t w0, w1;
+                lds_dw2(rowp, bk * WB + HDR + 16 * h + 8 * g, (bk * WB + HDR) & 3, w0, w1);
+                w.bf[h] = i8x8_to_h8(w0, w1);
+            }
+        } else {
+            uint32_t w0, w1;  // payload bytes 8g..8g+7: low nibbles = half 0, high = half 1
+            lds_dw2(rowp, bk * WB + HDR + 8 * g, (bk * WB + HDR) & 3, w0, w1);
+            const _Float16 bias = WT == T_Q4_0 ? (_Float16)1032.0f : (_Float16)1024.0f;
+            w.bf[0] = n8_to_h8(w0 & 0x0f0f0f0fu, w1 & 0x0f0f0f0fu, bias);
+            w.bf[1] = n8_to_h8((w0 >> 4) & 0x0f0f0f0fu, (w1 >> 4) & 0x0f0f0f0fu, bias);
+        }
+        const uint32_t dw = hrow[bk * WB / 2];
+        w.dwf = v4i{lo && s * BKB + bk < nb ? (int)dw : 0, 0, 0, 0};
+        return w;
+    };
+    // unit (bk, mt): MFMAs of its fragments f into product buffer mt % 2, then the
+    // FMAs of the previous unit (m-tile mt - 1) from the other buffer, pinned
+    // here (an empty asm reads the updated accumulator) so that they are not
+    // sunk past the next units' MFMAs
+    auto unit = [&](const St& b, auto bkc, auto mtc, const Frag& f, const WFrag& w, const v4i& mwf, v16f(&PI)[2],
+                    v16f(&PS)[2]) __attribute__((always_inline)) {
+        constexpr int bk = decltype(bkc)::value, mt = decltype(mtc)::value;
+        constexpr int u2 = mt & 1, p2 = u2 ^ 1;
+        if (WT == T_Q4_1 && bk == 0) {
+            // acc += sum_b s_a[m][b] * m_w[n][b] over this stage's blocks (k-slots 0, 1)
+            v4i saf = __builtin_bit_cast(v4i, f.a0);  // finite filler
+            saf[0] = (int)reinterpret_cast<const uint32_t*>(&b.As[0][0])[WT == T_Q4_1 ? mt * 32 + lr : 0];
+            acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, saf), __builtin_bit_cast(v8h, mwf),
+                                                             acc[mt], 0, 0, 0);
+        }
+        // S-MFMA A operand: d_a in k-slot 0; the other k-slots keep a1's (finite)
+        // quants, which meet B's zeros
+        v4i daf = __builtin_bit_cast(v4i, f.a1);
+        daf[0] = (int)f.da;
+        PI[u2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a0, w.bf[0], zf, 0, 0, 0);
+        PI[u2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a1, w.bf[1], PI[u2], 0, 0, 0);
+        PS[u2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, daf), __builtin_bit_cast(v8h, w.dwf), zf,
+                                                        0, 0, 0);
+        if (bk > 0 || mt > 0) {
+            constexpr int pm = (mt + 3) & 3;
+            apply(pm, PI[p2], PS[p2]);
+            asm volatile("" : "+v"(acc[pm]));
+        }
+    };
+    auto compute_q = [&](int s, const St& b) __attribute__((always_inline)) {
+        using I0 = std::integral_constant<int, 0>;
+        using I1 = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        using I3 = std::integral_constant<int, 3>;
+        static_assert(BKB == 2, "two blocks per stage");
+        v16f PI[2], PS[2];
+        v4i mwf = {0, 0, 0, 0};
+        if (WT == T_Q4_1) {
+            const uint16_t* hrow = reinterpret_cast<const uint16_t*>(&b.W[wrow * RD]);
+            const uint32_t m1 = s * BKB + 1 < nb ? (uint32_t)hrow[WB / 2 + 1] << 16 : 0u;
+            mwf[0] = lo ? (int)((uint32_t)hrow[1] | m1) : 0;
+        }
+        const WFrag w0 = load_wfrag(s, b, I0{});
+        Frag f = load_frag(b, I0{}, I0{});
+        Frag n = load_frag(b, I0{}, I1{});
+        unit(b, I0{}, I0{}, f, w0, mwf, PI, PS);
+        __builtin_amdgcn_sched_barrier(0);
+        f = load_frag(b, I0{}, I2{});
+        unit(b, I0{}, I1{}, n, w0, mwf, PI, PS);
+        __builtin_amdgcn_sched_barrier(0);
+        n = load_frag(b, I0{}, I3{});
+        unit(b, I0{}, I2{}, f, w0, mwf, PI, PS);
+        __builtin_amdgcn_sched_barrier(0);
+        const WFrag w1 = load_wfrag(s, b, I1{});
+        f = load_frag(b, I1{}, I0{});
+        unit(b, I0{}, I3{}, n, w0, mwf, PI, PS);
+        __builtin_amdgcn_sched_barrier(0);
+        n = load_frag(b, I1{}, I1{});
+        unit(b, I1{}, I0{}, f, w1, mwf, PI, PS);
+        __builtin_amdgcn_sched_barrier(0);
+        f = load_frag(b, I1{}, I2{});
+        unit(b, I1{}, I1{}, n, w1, mwf, PI, PS);
+        __builtin_amdgcn_sched_barrier(0);
+        n = load_frag(b, I1{}, I3{});
+        unit(b, I1{}, I2{}, f, w1, mwf, PI, PS);
+        __builtin_amdgcn_sched_barrier(0);
+        unit(b, I1{}, I3{}, n, w1, mwf, PI, PS);
+        apply(3, PI[1], PS[1]);  // unit 7
+    };
+
     // one pipeline step: wait for stage s, publish it, refill the oldest buffer, compute
-    auto step = [&](int s, const St& cur, St& refill) {
+    auto step = [&](int s, const St& cur, St& refill) __attribute__((always_inline)) {
         if (s + 1 < nstage) {
             if (xload) wait_vmcnt<NL + 1>();
             else wait_vmcnt<NL>();
@@ -395,7 +534,11 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
         }
         stage_barrier();
         if (s + 2 < nstage) dma_stage(s + 2, refill);
-        compute(s, cur);
+        if (QUANT && !DOTS) {
+            compute_q(s, cur);
+        } else {
+            compute(s, cur);
+        }
     };
 
     dma_stage(0, st0);
@@ -966,6 +1109,20 @@ static hipError_t run_mmq(const MatW& w_in, const ActF16& a, const MatD& d, int6
     p.r3 = (int)(ne13 / w.ne3);
     p.tiles_m = (int)((a.M + BM - 1) / BM);
     p.tiles_n = (int)((N + BN - 1) / BN);
+    {
+        // group height: the fewest L2 bytes for the ~64 workgroups an XCD runs at once
+        // (32 CUs x 2): gm activation row tiles plus 64 / gm weight column tiles
+        const double at = (double)BM * kk * 2, wt = (double)BN * rowb;
+        double best = 0;
+        p.gm = 1;
+        for (int gm = 1; gm <= 16 && gm <= p.tiles_m; gm *= 2) {
+            const double c = gm * at + ((64 + gm - 1) / gm) * wt;
+            if (gm == 1 || c < best) {
+                best = c;
+                p.gm = gm;
+            }
+        }
+    }
     const int nstage = w.type != T_F16 ? (int)(((a.K / QK) + BKB - 1) / BKB) : (int)((kk + 31) / 32);
     const bool split = sp.ks > 1 && !dots && ne12 * ne13 == 1;
     p.ksplit = split ? sp.ks : 1;
