@@ -104,10 +104,12 @@ __global__ __launch_bounds__(256) void conv3x3_pack_f16_kernel(const uint16_t* _
 // products are those of im2col + F16 MUL_MAT; fp32 accumulation.
 // Workgroup 128(m) x 128(n), four wavefronts of 64 x 64 (2 x 2
 // v_mfma_f32_32x32x16_f16 tiles), K staged 32 at a time (one tap's channel
-// slice) through two LDS buffers; rows of 32 halves at a 40-half pitch, so the
-// 16 rows one ds_read_b128 pass touches land on distinct 4-bank groups.
+// slice) through two LDS buffers.  Tile rows are 32 halves (four 16-byte
+// chunks), unpadded; chunk c of row r sits in slot c ^ cswz(r), which spreads
+// the rows of one ds_read_b128 pass over all 64 banks.
 namespace {
-constexpr int CT = 128, CK = 32, CP = 40;
+constexpr int CT = 128, CK = 32, CP = 32;
+__device__ __forceinline__ int cswz(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
 }
 template <int TAPS>
 __global__ __launch_bounds__(256, 2) void conv_f16_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
@@ -150,11 +152,12 @@ __global__ __launch_bounds__(256, 2) void conv_f16_kernel(const float* __restric
         rb[0] = bn < N ? ws[0] : uint4{0, 0, 0, 0};
         rb[1] = bn < N ? ws[1] : uint4{0, 0, 0, 0};
     };
+    const int c0 = ((lk >> 3) ^ cswz(lrow)) << 3, c1 = (((lk >> 3) + 1) ^ cswz(lrow)) << 3;
     auto park = [&](int buf) {
-        *reinterpret_cast<uint4*>(&sA[buf][lrow * CP + lk]) = ra[0];
-        *reinterpret_cast<uint4*>(&sA[buf][lrow * CP + lk + 8]) = ra[1];
-        *reinterpret_cast<uint4*>(&sB[buf][lrow * CP + lk]) = rb[0];
-        *reinterpret_cast<uint4*>(&sB[buf][lrow * CP + lk + 8]) = rb[1];
+        *reinterpret_cast<uint4*>(&sA[buf][lrow * CP + c0]) = ra[0];
+        *reinterpret_cast<uint4*>(&sA[buf][lrow * CP + c1]) = ra[1];
+        *reinterpret_cast<uint4*>(&sB[buf][lrow * CP + c0]) = rb[0];
+        *reinterpret_cast<uint4*>(&sB[buf][lrow * CP + c1]) = rb[1];
     };
     const v16f zf = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     v16f acc[2][2] = {{zf, zf}, {zf, zf}};
@@ -170,8 +173,9 @@ __global__ __launch_bounds__(256, 2) void conv_f16_kernel(const float* __restric
             v8h a[2], b[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                a[i] = *reinterpret_cast<const v8h*>(&sA[buf][(wm * 64 + i * 32 + lr) * CP + 16 * kk + 8 * g]);
-                b[i] = *reinterpret_cast<const v8h*>(&sB[buf][(wn * 64 + i * 32 + lr) * CP + 16 * kk + 8 * g]);
+                const int ra_ = wm * 64 + i * 32 + lr, rb_ = wn * 64 + i * 32 + lr, c = 2 * kk + g;
+                a[i] = *reinterpret_cast<const v8h*>(&sA[buf][ra_ * CP + ((c ^ cswz(ra_)) << 3)]);
+                b[i] = *reinterpret_cast<const v8h*>(&sB[buf][rb_ * CP + ((c ^ cswz(rb_)) << 3)]);
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
