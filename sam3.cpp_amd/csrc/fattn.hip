@@ -65,6 +65,10 @@ __device__ __forceinline__ float partner32(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((l ^ 32) << 2, __builtin_bit_cast(int, x)));
 }
 __device__ __forceinline__ float xmax32(float x) { return fmaxf(x, partner32(x)); }
+// Workgroup barrier for LDS hazards only: waits for this wavefront's LDS accesses,
+// not for its global loads still in flight (__syncthreads() also waits for those).
+// The "memory" clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __device__ __forceinline__ float xsum32(float x) { return x + partner32(x); }
 
 template <int D, bool QF32, bool KVF32>
@@ -76,8 +80,9 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
     constexpr int C8 = D / 8;       // 8-element chunks per key row
     constexpr int LPT = FA_BKV * C8 / FA_NT;  // chunks per thread per tile (K and V each)
     static_assert(FA_BKV * C8 % FA_NT == 0, "tile split");
-    __shared__ __attribute__((aligned(16))) _Float16 sK[FA_BKV * KS];
-    __shared__ __attribute__((aligned(16))) _Float16 sV[D * VS];
+    // two K / V^T buffers: tile t + 1 is stored while tile t is computed
+    __shared__ __attribute__((aligned(16))) _Float16 sK[2][FA_BKV * KS];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[2][D * VS];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -104,34 +109,62 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
     }
 
     // global -> register staging of one K/V tile.  K chunk j of thread t: key (t + 256j) / C8,
-    // column (t + 256j) % C8 (a key row's chunks on consecutive lanes); V chunk: key
-    // (t + 256j) % 64, column (t + 256j) / 64 (consecutive keys on consecutive lanes, so
-    // the transposed LDS writes of a wavefront hit consecutive halves).
+    // column (t + 256j) % C8 (a key row's chunks on consecutive lanes).  V, when C8 % 8 == 0:
+    // thread t takes keys 2q, 2q + 1 (q = (t + 256i) % 32) of column chunk (t + 256i) / 32, so
+    // each V^T row gets the pair as one 32-bit write; otherwise V chunk j is key (t + 256j) % 64,
+    // column (t + 256j) / 64, written as 16-bit halves.
+    constexpr bool VPAIR = C8 % 8 == 0;
     u32x4 kreg[LPT], vreg[LPT];
     auto load_tile = [&](int kv0) {
 #pragma unroll
         for (int j = 0; j < LPT; ++j) {
             const int id = tid + FA_NT * j;
             const int kk = id / C8, kc = id % C8;
-            const int vk = id % FA_BKV, vc = id / FA_BKV;
             kreg[j] = u32x4{0, 0, 0, 0};
-            vreg[j] = u32x4{0, 0, 0, 0};
             if (kv0 + kk < nkv) kreg[j] = load8_h<KVF32>(kb + (int64_t)(kv0 + kk) * p.k_nb1 + kc * 8 * KES);
+            int vk, vc;
+            if (VPAIR) {
+                const int pid = tid + FA_NT * (j >> 1);
+                vk = 2 * (pid % 32) + (j & 1);
+                vc = pid / 32;
+            } else {
+                vk = id % FA_BKV;
+                vc = id / FA_BKV;
+            }
+            vreg[j] = u32x4{0, 0, 0, 0};
             if (kv0 + vk < nkv) vreg[j] = load8_h<KVF32>(vb + (int64_t)(kv0 + vk) * p.v_nb1 + vc * 8 * KES);
         }
     };
-    auto store_tile = [&]() {
+    auto store_tile = [&](int buf) {
 #pragma unroll
         for (int j = 0; j < LPT; ++j) {
             const int id = tid + FA_NT * j;
             const int kk = id / C8, kc = id % C8;
-            *reinterpret_cast<u32x4*>(&sK[kk * KS + kc * 8]) = kreg[j];
-            const int vk = id % FA_BKV, vc = id / FA_BKV;
-            uint16_t* col = reinterpret_cast<uint16_t*>(&sV[(vc * 8) * VS + vk]);
+            *reinterpret_cast<u32x4*>(&sK[buf][kk * KS + kc * 8]) = kreg[j];
+        }
+        if (VPAIR) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                col[(2 * e) * VS] = (uint16_t)(vreg[j][e] & 0xffffu);
-                col[(2 * e + 1) * VS] = (uint16_t)(vreg[j][e] >> 16);
+            for (int j = 0; j < LPT; j += 2) {
+                const int pid = tid + FA_NT * (j >> 1);
+                const int vk = 2 * (pid % 32), vc = pid / 32;
+                uint32_t* col = reinterpret_cast<uint32_t*>(&sV[buf][(vc * 8) * VS + vk]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    col[(2 * e) * (VS / 2)] = (vreg[j][e] & 0xffffu) | (vreg[j + 1][e] << 16);
+                    col[(2 * e + 1) * (VS / 2)] = (vreg[j][e] >> 16) | (vreg[j + 1][e] & 0xffff0000u);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < LPT; ++j) {
+                const int id = tid + FA_NT * j;
+                const int vk = id % FA_BKV, vc = id / FA_BKV;
+                uint16_t* col = reinterpret_cast<uint16_t*>(&sV[buf][(vc * 8) * VS + vk]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    col[(2 * e) * VS] = (uint16_t)(vreg[j][e] & 0xffffu);
+                    col[(2 * e + 1) * VS] = (uint16_t)(vreg[j][e] >> 16);
+                }
             }
         }
     };
@@ -145,13 +178,17 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
     float m_run = -__builtin_inff(), l_run = 0.0f;
     const float c = p.c;
 
+    // One LDS-only barrier per tile: it publishes tile t (stored at the end of tile
+    // t - 1) and frees the other buffer (read by tile t - 1).  After tile t's compute,
+    // tile t + 1 goes from the registers (loaded during tile t) into that buffer and
+    // tile t + 2's loads are issued, so each load has a whole tile to land.
     const int ntile = (nkv + FA_BKV - 1) / FA_BKV;
     load_tile(0);
-    store_tile();
-    __syncthreads();
+    store_tile(0);
+    if (ntile > 1) load_tile(FA_BKV);
     for (int t = 0; t < ntile; ++t) {
-        const int kv0 = t * FA_BKV;
-        if (t + 1 < ntile) load_tile(kv0 + FA_BKV);
+        const int kv0 = t * FA_BKV, cb = t & 1;
+        lds_barrier();
 
         // S^T for the two 32-key halves
         v16f S[2];
@@ -160,7 +197,7 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
             S[kh] = zf;
 #pragma unroll
             for (int cc = 0; cc < NC; ++cc) {
-                const v8h a = *reinterpret_cast<const v8h*>(&sK[(32 * kh + lr) * KS + 16 * cc + 8 * g]);
+                const v8h a = *reinterpret_cast<const v8h*>(&sK[cb][(32 * kh + lr) * KS + 16 * cc + 8 * g]);
                 S[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[cc], S[kh], 0, 0, 0);
             }
         }
@@ -214,7 +251,7 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
         // O^T += V^T P^T over the 64 keys (four 16-key MFMA chunks)
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-            const _Float16* vrow = &sV[(32 * db + lr) * VS];
+            const _Float16* vrow = &sV[cb][(32 * db + lr) * VS];
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
@@ -230,9 +267,8 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
                 }
         }
         if (t + 1 < ntile) {
-            __syncthreads();  // every wavefront is done with this tile
-            store_tile();
-            __syncthreads();
+            store_tile(cb ^ 1);
+            if (t + 2 < ntile) load_tile(kv0 + 2 * FA_BKV);
         }
     }
 
