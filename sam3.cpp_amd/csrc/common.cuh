@@ -37,7 +37,13 @@ __device__ __forceinline__ float h2f(uint16_t h) {
     __builtin_memcpy(&v, &h, 2);
     return (float)v;
 }
+// The empty asm makes f an opaque, already-rounded fp32 value: without it the
+// backend may fold a producing multiply into the conversion (v_fma_mixlo_f16,
+// one rounding of the exact product), while ggml rounds the product to fp32
+// first, e.g. the Q8_1 sum s = fp16(d * isum) differs when d * isum in fp32
+// lands on an fp16 midpoint.
 __device__ __forceinline__ uint16_t f2h(float f) {
+    asm volatile("" : "+v"(f));
     _Float16 v = (_Float16)f;
     uint16_t h;
     __builtin_memcpy(&h, &v, 2);

@@ -167,3 +167,49 @@ def test_mul_mat_skinny(mi, ctx, orc, tname, M, N, K):
     ref = orc.mul_mat(wq, t, K, N, x[rows][None, None])[0, 0]
     scale = absterm(orc, t, wq, K, orc.from_float(orc.VEC_DOT_TYPE[t], x[rows]))
     assert rel_err(got[rows], ref, scale) <= TOL[tname]
+
+
+def _sweep_shapes(tname, n=16, seed=2024):
+    """Seeded random GEMM shapes: ragged M and N, odd block counts, K up to 1280,
+    F16 with any K, and now and then a broadcast batch (src0 [K,N,2,1] over src1
+    [K,M,2,3])."""
+    rng = np.random.default_rng(seed + sum(map(ord, tname)))
+    out = []
+    for i in range(n):
+        M = int(rng.integers(1, 700))
+        N = int(rng.integers(1, 520))
+        K = int(rng.integers(1, 1281)) if tname == "f16" else 32 * int(rng.integers(1, 41))
+        dims = (2, 1, 2, 3) if i % 5 == 4 else (1, 1, 1, 1)
+        out.append((M, N, K, dims, i))
+    return out
+
+
+@pytest.mark.parametrize("tname", ["q8_0", "q4_0", "q4_1", "f16"])
+def test_mul_mat_random_shapes(mi, ctx, orc, tname):
+    for M, N, K, dims, i in _sweep_shapes(tname):
+        check(mi, ctx, orc, tname, M, N, K, seed=100 + i, dims=dims)
+
+
+def test_q8_1_sum_midpoint_rounding(mi, ctx, orc):
+    """Q4_1 weights take the Q8_1 operand, whose s = fp16(d * isum) rounds the
+    fp32 product first (ggml's from_float).  For this block (values from the
+    oracle's seeded normal stream) d * isum in fp32 is exactly an fp16 midpoint,
+    so rounding the exact product once instead of twice picks the other
+    neighbour; the GPU once did that (a fused multiply-to-fp16).  One block per
+    row makes that one-ulp s error ~1e-4 of the bar's scale."""
+    x = orc.normal(6 * 420 * 288, seed=114, stream=2).reshape(3, 2, 420, 288)[1, 0, 29, 64:96].astype(np.float32)
+    amax = np.float32(np.abs(x).max())
+    d = np.float32(amax / np.float32(127.0))
+    q = np.rint((x * (np.float32(127.0) / amax)).astype(np.float32)).astype(np.int64)
+    p = np.float32(d * np.float32(q.sum()))
+    lo = np.float16(p)
+    hi = np.nextafter(lo, np.float16(np.inf) if np.float64(lo) < np.float64(p) else np.float16(-np.inf))
+    assert np.float64(p) == (np.float64(lo) + np.float64(hi)) / 2, "not a midpoint case any more"
+    K, N = 32, 64
+    w = orc.normal(N * K, seed=7, stream=1, std=0.02).reshape(N, K)
+    wq = orc.quantize_weights(orc.Q4_1, w)
+    xs = np.tile(x, (3, 1))
+    out = run_mul_mat(mi, ctx, wq, orc.Q4_1, K, N, xs[None, None])[0, 0]
+    ref = orc.mul_mat(wq, orc.Q4_1, K, N, xs[None, None])[0, 0]
+    scale = absterm(orc, orc.Q4_1, wq, K, orc.from_float(orc.Q8_1, xs))
+    assert rel_err(out, ref, scale) <= TOL["q4_1"]
