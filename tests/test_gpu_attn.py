@@ -190,3 +190,22 @@ def test_explicit_attention_gemms(mi, ctx, orc, n, nh, nq_check):
     W = _bound_w(orc, qs, k, v, scale)[0]
     err = np.abs(got.transpose(1, 0, 2).astype(np.float64) - exact)
     assert (err <= TOL * W + 1e-6).all(), f"max err/W {(err / np.maximum(W, 1e-30)).max():.3e}"
+
+
+def test_flash_attn_random_shapes(mi, ctx, orc):
+    """Seeded random shapes against the same bars: query and key counts ragged
+    against the 128-query and 64-key tiles (some few enough that the keys are
+    split over workgroups and combined), kv-head broadcast, D in {64, 96, 128},
+    batches, and random scales."""
+    rng = np.random.default_rng(4242)
+    for i in range(14):
+        D = int(rng.choice([64, 96, 128]))
+        nq = int(rng.integers(1, 400))
+        nkv = int(rng.integers(1, 900))
+        nhk = int(rng.integers(1, 4))
+        nh = nhk * int(rng.integers(1, 3))
+        B = int(rng.integers(1, 3))
+        scale = float(rng.uniform(0.05, 0.3))
+        q, k, v = (_f16(a) for a in _inputs(orc, D, nq, nkv, nh, nhk, B, seed=200 + i))
+        got = _gpu_fa(mi, ctx, q, k, v, scale, mi.F16, mi.F16)
+        _check(orc, got, q, k, v, scale, orc.F16)
