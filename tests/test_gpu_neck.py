@@ -254,3 +254,27 @@ def test_sam3_neck_full_size_per_op(mi, ctx, orc, wtype):
     assert np.array_equal(got[0], d)
     assert np.array_equal(got[3], f)
     assert all(np.isfinite(g).all() for g in got)
+
+
+@pytest.mark.parametrize("wtype", ["f32", "f16"])
+def test_neck_random_shapes(mi, ctx, orc, wtype):
+    """Seeded random conv / conv-transpose shapes against the per-op bars: map
+    sizes ragged against the 128-pixel tiles, channel counts on both sides of
+    the implicit-GEMM condition (Cin % 32 == 0), with and without GELU."""
+    rng = np.random.default_rng(77 if wtype == "f32" else 78)
+    t = mi.F16 if wtype == "f16" else mi.F32
+    for i in range(10):
+        H, W = int(rng.integers(1, 40)), int(rng.integers(1, 40))
+        Cin = int(rng.choice([32, 64, 96, 20, 44]))
+        Cout = 4 * int(rng.integers(1, 24))
+        k = int(rng.choice([1, 3]))
+        w = rand(rng, (Cout, Cin, k, k), 0.05)
+        if t == mi.F16:
+            w = neck.f16r(w)
+        b, x = rand(rng, Cout, 0.1), rand(rng, (H * W, Cin))
+        check_conv(run_conv(mi, ctx, w, t, b, x, H, W), w, t, b, x, H, W)
+        wd = rand(rng, (Cin, Cout, 2, 2), 0.05)
+        if t == mi.F16:
+            wd = neck.f16r(wd)
+        gelu = bool(i % 2)
+        check_deconv(orc, run_deconv(mi, ctx, wd, t, b, x, H, W, gelu), wd, b, x, H, W, gelu)
