@@ -248,7 +248,7 @@ class ModelFile:
         st = self.L.mi355_model_file_tensor(self.h, index, C.byref(info))
         if st != 0:
             raise Mi355Error(st, self.L.mi355_model_file_last_error().decode())
-        return {"name": info.name.decode(), "type": info.type, "n_dims": info.n_dims, "ne": list(info.ne),
+        return {"name": info.name.decode(errors="replace"), "type": info.type, "n_dims": info.n_dims, "ne": list(info.ne),
                 "offset": info.offset, "nbytes": info.nbytes}
 
     def load_bytes(self, index: int, dst_type: int) -> int:

@@ -101,3 +101,45 @@ def test_rejections(mi, orc, tmp_path):
     p.write_bytes(data[:-10])
     _expect_error(mi, p, -1)                                        # truncated data
     _expect_error(mi, tmp_path / "absent.ggml", -1)
+
+
+def test_corrupted_files_fail_cleanly(mi, orc, tmp_path):
+    """Seeded byte mutations of a valid file (header, hyperparameters and tensor
+    records, where lengths, dims and types live): opening either succeeds with
+    a consistent index or raises the library's error; it never crashes, hangs
+    or allocates beyond the file.  Runs in a child process so that a crash
+    would fail the test instead of ending the session."""
+    import subprocess, sys, textwrap
+    p = tmp_path / "m.ggml"
+    W.write(p, W.MAGIC_SAM3, 3, 8, W.sam3_hparams(), _tensors(orc))
+    code = textwrap.dedent(f"""
+        import importlib.util, os, numpy as np, resource
+        resource.setrlimit(resource.RLIMIT_AS, (8 << 30, 8 << 30))
+        spec = importlib.util.spec_from_file_location("m", {str(mi.__file__)!r})
+        mi = importlib.util.module_from_spec(spec); spec.loader.exec_module(mi)
+        src = open({str(p)!r}, "rb").read()
+        rng = np.random.default_rng(11)
+        out = {str(tmp_path / "x.ggml")!r}
+        ok = err = 0
+        head = min(len(src), 1024)  # header, hparams and the first tensor records
+        for i in range(400):
+            b = bytearray(src)
+            for _ in range(int(rng.integers(1, 4))):
+                j = int(rng.integers(0, head))
+                b[j] = int(rng.integers(0, 256))
+            open(out, "wb").write(bytes(b))
+            try:
+                f = mi.ModelFile(out)
+                for t in range(f.header()[3]):
+                    info = f.tensor(t)
+                    assert info["offset"] + info["nbytes"] <= len(b), (info, len(b))
+                f.close()
+                ok += 1
+            except mi.Mi355Error:
+                err += 1
+        print(ok, err)
+    """)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    ok, err = map(int, r.stdout.split())
+    assert ok + err == 400 and err > 0
