@@ -138,3 +138,49 @@ def test_workspace_size(mi):
     s0, s1, d = mm(mi, K=1024, N=4736, M=5184)
     n = mi.lib().mi355_mul_mat_workspace_size(C.byref(s0), C.byref(s1))
     assert n >= 5184 * 1024 + 5184 * 32 * 4
+
+
+def test_every_entry_point_rejects_null_arguments(mi):
+    """Every entry point called with a NULL context / handle and null or zero
+    arguments returns an error status (sizes return 0; the frees and the
+    profile reset return) without touching a GPU, and a NULL-context failure
+    leaves its text in mi355_last_error(NULL).  Run in a child process so that
+    a crash fails the test instead of ending the session."""
+    import subprocess, sys, textwrap
+    code = textwrap.dedent(f"""
+        import ctypes as C, importlib.util
+        spec = importlib.util.spec_from_file_location("m", {mi.__file__!r})
+        mi = importlib.util.module_from_spec(spec); spec.loader.exec_module(mi)
+        L = mi.lib()
+        # calls that create or query state without a context (or whose null arguments are valid)
+        # are checked by their own tests: they may legitimately succeed
+        skip = {{"mi355_context_create", "mi355_status_to_string", "mi355_last_error",
+                 "mi355_model_file_last_error", "mi355_hiera_n_blocks", "mi355_supports_mul_mat"}}
+        bad = []
+        for name in sorted(mi.header_symbols()):
+            if name in skip:
+                continue
+            fn = getattr(L, name)
+            args = []
+            for t in fn.argtypes:
+                if t in (C.c_float, C.c_double):
+                    args.append(0.0)
+                elif t in (C.c_int, C.c_int32, C.c_int64, C.c_uint32, C.c_size_t):
+                    args.append(0)
+                else:
+                    args.append(None)
+            r = fn(*args)
+            if fn.restype is None:
+                continue
+            if fn.restype == C.c_size_t:
+                if r != 0: bad.append((name, r))
+            elif fn.restype == C.c_int and name.endswith(("_find", "_hparams", "_collect")):
+                if r > 0: bad.append((name, r))
+            elif fn.restype == C.c_int:
+                if r >= 0: bad.append((name, r))
+                elif not L.mi355_last_error(None): bad.append((name, "no error text"))
+        print("BAD", bad)
+    """)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-3000:]
+    assert "BAD []" in r.stdout, r.stdout
