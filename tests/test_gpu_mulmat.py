@@ -213,3 +213,57 @@ def test_q8_1_sum_midpoint_rounding(mi, ctx, orc):
     ref = orc.mul_mat(wq, orc.Q4_1, K, N, xs[None, None])[0, 0]
     scale = absterm(orc, orc.Q4_1, wq, K, orc.from_float(orc.Q8_1, xs))
     assert rel_err(out, ref, scale) <= TOL["q4_1"]
+
+
+def test_two_contexts_two_threads(mi, orc):
+    """One context per host thread and stream (the library's threading
+    contract): two threads, each with its own context on its own stream, run
+    interleaved mul_mats of different types and shapes (the skinny and tiled
+    kernels, split-K) 4 times each; every result is bit-identical to the same
+    call made alone."""
+    import threading
+    cases = [("q4_0", 65536, 96, 96), ("q8_0", 700, 520, 1024), ("q4_1", 96, 80, 4736), ("f16", 300, 64, 588)]
+    inputs = []
+    for i, (tname, M, N, K) in enumerate(cases):
+        t = orc.NAME_TYPE[tname]
+        w = orc.quantize_weights(t, orc.normal(N * K, seed=50 + i, stream=1, std=0.02).reshape(N, K))
+        x = orc.normal(M * K, seed=50 + i, stream=2).reshape(M, K)
+        inputs.append((t, torch.from_numpy(w.view(np.uint8)).cuda(), torch.from_numpy(x).cuda(), M, N, K))
+
+    def run(ctx, t, w, x, M, N, K):
+        d = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        ctx.mul_mat(mi.from_torch(w, t, [K, N]), mi.from_torch(x, mi.F32, [K, M]), mi.from_torch(d, mi.F32, [N, M]))
+        ctx.synchronize()
+        return d
+
+    solo = mi.Context(0)
+    try:
+        ref = [run(solo, *a).cpu() for a in inputs]
+    finally:
+        solo.close()
+    results, errors = {}, []
+
+    def worker(tid):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                ctx = mi.Context(0, s.cuda_stream)
+                try:
+                    for rep in range(4):
+                        for i in range(tid, tid + len(inputs)):
+                            j = i % len(inputs)
+                            results[(tid, rep, j)] = run(ctx, *inputs[j]).cpu()
+                finally:
+                    ctx.close()
+        except Exception as e:  # reported below
+            errors.append(repr(e))
+
+    th = [threading.Thread(target=worker, args=(k,)) for k in range(2)]
+    for x in th:
+        x.start()
+    for x in th:
+        x.join(timeout=120)
+    assert not errors, errors
+    assert len(results) == 2 * 4 * len(inputs)
+    for (tid, rep, j), out in results.items():
+        assert torch.equal(out, ref[j]), (tid, rep, cases[j])
