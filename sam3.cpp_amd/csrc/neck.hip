@@ -103,20 +103,27 @@ __global__ __launch_bounds__(256) void conv3x3_pack_f16_kernel(const uint16_t* _
 // (RNE) as they are loaded, exactly as ggml's F16 im2col rounds them, so the
 // products are those of im2col + F16 MUL_MAT; fp32 accumulation.
 // Workgroup 128(m) x 128(n), four wavefronts of 64 x 64 (2 x 2
-// v_mfma_f32_32x32x16_f16 tiles), K staged 32 at a time (one tap's channel
-// slice) through two LDS buffers.  Tile rows are 32 halves (four 16-byte
-// chunks), unpadded; chunk c of row r sits in slot c ^ cswz(r), which spreads
+// v_mfma_f32_32x32x16_f16 tiles), K staged KST = 32 at a time (one tap's
+// channel slice) through two LDS buffers.  The next
+// stage's map values are held raw (fp32) in registers and rounded to fp16 as
+// they are parked in LDS after the current stage's MFMAs, so their global
+// latency overlaps the MFMAs.  Tile rows are KST halves (KST / 8 16-byte
+// chunks), unpadded; chunk c of row r sits in slot c ^ csw(r), which spreads
 // the rows of one ds_read_b128 pass over all 64 banks.
 namespace {
-constexpr int CT = 128, CK = 32, CP = 32;
-__device__ __forceinline__ int cswz(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+constexpr int CT = 128;
+template <int CH>
+__device__ __forceinline__ int csw(int r) {
+    return CH == 8 ? ((r & 7) ^ ((r >> 3) & 1)) : (((r >> 1) & 3) ^ ((r >> 3) & 1));
 }
-template <int TAPS>
+}
+template <int TAPS, int KST>
 __global__ __launch_bounds__(256, 2) void conv_f16_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
                                                           const float* __restrict__ bias, int H, int W, int C, int N,
                                                           int gelu, float* __restrict__ y) {
-    __shared__ __attribute__((aligned(16))) _Float16 sA[2][CT * CP];
-    __shared__ __attribute__((aligned(16))) _Float16 sB[2][CT * CP];
+    constexpr int CH = KST / 8, HC = CH / 2;  // chunks per row; chunks per loading thread
+    __shared__ __attribute__((aligned(16))) _Float16 sA[2][CT * KST];
+    __shared__ __attribute__((aligned(16))) _Float16 sB[2][CT * KST];
     const int M = H * W, K = TAPS == 9 ? 9 * C : C;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -128,54 +135,51 @@ __global__ __launch_bounds__(256, 2) void conv_f16_kernel(const float* __restric
     const int tl = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
     if (tl >= tiles) return;
     const int m0 = (tl / tiles_n) * CT, n0 = (tl % tiles_n) * CT;
-    // loader: thread t fills row t/2 of both tiles, K values 16*(t%2) .. +15 of the stage
-    const int lrow = tid >> 1, lk = 16 * (tid & 1);
+    // loader: thread t fills row t/2 of both tiles, chunks HC*(t%2) .. +HC-1 of the stage
+    const int lrow = tid >> 1, lc = HC * (tid & 1);
     const int am = m0 + lrow, bn = n0 + lrow;
     const int oy = am / W, ox = am - (am / W) * W;
-    uint4 ra[2], rb[2];
+    v4f ra[2 * HC];
+    uint4 rb[HC];
     auto load = [&](int k0) {
         const int tap = TAPS == 9 ? k0 / C : 0, c0 = k0 - tap * C;
         const int iy = TAPS == 9 ? oy + tap / 3 - 1 : oy, ix = TAPS == 9 ? ox + tap % 3 - 1 : ox;
         const bool in = am < M && iy >= 0 && iy < H && ix >= 0 && ix < W;
-        const float* src = x + ((int64_t)iy * W + ix) * C + c0 + lk;
+        const float* src = x + ((int64_t)iy * W + ix) * C + c0 + 8 * lc;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            v4f a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
-            if (in) {
-                a = *reinterpret_cast<const v4f*>(src + 8 * h);
-                b = *reinterpret_cast<const v4f*>(src + 8 * h + 4);
-            }
-            ra[h] = uint4{(uint32_t)f2h(a[0]) | ((uint32_t)f2h(a[1]) << 16), (uint32_t)f2h(a[2]) | ((uint32_t)f2h(a[3]) << 16),
-                          (uint32_t)f2h(b[0]) | ((uint32_t)f2h(b[1]) << 16), (uint32_t)f2h(b[2]) | ((uint32_t)f2h(b[3]) << 16)};
-        }
-        const uint4* ws = reinterpret_cast<const uint4*>(w + (int64_t)bn * K + k0 + lk);
-        rb[0] = bn < N ? ws[0] : uint4{0, 0, 0, 0};
-        rb[1] = bn < N ? ws[1] : uint4{0, 0, 0, 0};
+        for (int h = 0; h < 2 * HC; ++h) ra[h] = in ? *reinterpret_cast<const v4f*>(src + 4 * h) : v4f{0, 0, 0, 0};
+        const uint4* ws = reinterpret_cast<const uint4*>(w + (int64_t)bn * K + k0 + 8 * lc);
+#pragma unroll
+        for (int h = 0; h < HC; ++h) rb[h] = bn < N ? ws[h] : uint4{0, 0, 0, 0};
     };
-    const int c0 = ((lk >> 3) ^ cswz(lrow)) << 3, c1 = (((lk >> 3) + 1) ^ cswz(lrow)) << 3;
     auto park = [&](int buf) {
-        *reinterpret_cast<uint4*>(&sA[buf][lrow * CP + c0]) = ra[0];
-        *reinterpret_cast<uint4*>(&sA[buf][lrow * CP + c1]) = ra[1];
-        *reinterpret_cast<uint4*>(&sB[buf][lrow * CP + c0]) = rb[0];
-        *reinterpret_cast<uint4*>(&sB[buf][lrow * CP + c1]) = rb[1];
+#pragma unroll
+        for (int h = 0; h < HC; ++h) {
+            const int slot = ((lc + h) ^ csw<CH>(lrow)) << 3;
+            const v4f a = ra[2 * h], b = ra[2 * h + 1];
+            const uint4 q = {(uint32_t)f2h(a[0]) | ((uint32_t)f2h(a[1]) << 16), (uint32_t)f2h(a[2]) | ((uint32_t)f2h(a[3]) << 16),
+                             (uint32_t)f2h(b[0]) | ((uint32_t)f2h(b[1]) << 16), (uint32_t)f2h(b[2]) | ((uint32_t)f2h(b[3]) << 16)};
+            *reinterpret_cast<uint4*>(&sA[buf][lrow * KST + slot]) = q;
+            *reinterpret_cast<uint4*>(&sB[buf][lrow * KST + slot]) = rb[h];
+        }
     };
     const v16f zf = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     v16f acc[2][2] = {{zf, zf}, {zf, zf}};
-    const int nst = K / CK;
+    const int nst = K / KST;
     load(0);
     park(0);
     __syncthreads();
     for (int s = 0; s < nst; ++s) {
         const int buf = s & 1;
-        if (s + 1 < nst) load((s + 1) * CK);
+        if (s + 1 < nst) load((s + 1) * KST);
 #pragma unroll
-        for (int kk = 0; kk < CK / 16; ++kk) {
+        for (int kk = 0; kk < KST / 16; ++kk) {
             v8h a[2], b[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int ra_ = wm * 64 + i * 32 + lr, rb_ = wn * 64 + i * 32 + lr, c = 2 * kk + g;
-                a[i] = *reinterpret_cast<const v8h*>(&sA[buf][ra_ * CP + ((c ^ cswz(ra_)) << 3)]);
-                b[i] = *reinterpret_cast<const v8h*>(&sB[buf][rb_ * CP + ((c ^ cswz(rb_)) << 3)]);
+                a[i] = *reinterpret_cast<const v8h*>(&sA[buf][ra_ * KST + ((c ^ csw<CH>(ra_)) << 3)]);
+                b[i] = *reinterpret_cast<const v8h*>(&sB[buf][rb_ * KST + ((c ^ csw<CH>(rb_)) << 3)]);
             }
 #pragma unroll
             for (int i = 0; i < 2; ++i)
@@ -282,7 +286,7 @@ hipError_t launch_conv3x3_pack_f16(const uint16_t* w, int Cin, int Cout, uint16_
 
 hipError_t launch_conv_f16(int taps, const float* x, const uint16_t* w, const float* bias, int H, int W, int C, int N,
                            bool gelu, float* y, hipStream_t st) {
-    if ((taps != 1 && taps != 4 && taps != 9) || C % CK != 0 || (reinterpret_cast<uintptr_t>(x) & 15) ||
+    if ((taps != 1 && taps != 4 && taps != 9) || C % 32 != 0 || (reinterpret_cast<uintptr_t>(x) & 15) ||
         (reinterpret_cast<uintptr_t>(w) & 15) || (taps == 4 && N % 4 != 0))
         return hipErrorInvalidValue;
     const int64_t M = (int64_t)H * W;
@@ -290,12 +294,13 @@ hipError_t launch_conv_f16(int taps, const float* x, const uint16_t* w, const fl
     const int tiles = (int)(((M + CT - 1) / CT) * ((N + CT - 1) / CT));
     const unsigned grid = (unsigned)((tiles + 7) / 8 * 8);
     const int gl = gelu ? 1 : 0;
+    // K step 32: a 64-deep step (64 KB of LDS, two workgroups per CU) measured slower
     if (taps == 9)
-        conv_f16_kernel<9><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
+        conv_f16_kernel<9, 32><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
     else if (taps == 4)
-        conv_f16_kernel<4><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
+        conv_f16_kernel<4, 32><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
     else
-        conv_f16_kernel<1><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
+        conv_f16_kernel<1, 32><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
     return hipGetLastError();
 }
 
