@@ -25,8 +25,10 @@
 //            are read from LDS with the same key order.
 // K is staged row-major with rows padded by 16 bytes and V transposed with
 // rows padded by 8 bytes, so the 32-row fragment reads spread over all LDS
-// banks (no bank conflicts in rocprofv3's counters).  The next tile's
-// global loads go to registers before the current tile's MFMAs.
+// banks (no bank conflicts in rocprofv3's counters).  Two K / V^T buffers:
+// after tile t's MFMAs tile t + 1 goes from registers into the free buffer
+// and tile t + 2's global loads are issued, with one LDS-only barrier per
+// tile.
 #include <algorithm>
 
 #include "common.cuh"

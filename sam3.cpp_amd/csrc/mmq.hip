@@ -16,18 +16,19 @@
 //
 // Tiling: workgroup 128(m) x 128(n), four wavefronts; wavefront w owns all
 // 128 rows and the 32 columns n0+32w..+31 (4 MFMA tiles along m).  K
-// advances two blocks (64 elements) per stage with one barrier per stage:
-// the next stage's global loads are issued into registers before the
-// current stage's MFMAs and written to the other LDS buffer after them.
-// All global traffic uses buffer loads: every per-thread offset is computed
-// once, a stage advances only the (scalar) base of the buffer resource, and
-// rows past M/N read as zeros through the resource's range check.  Weight
-// stage segments (2 blocks = 68/36/40 bytes per row) are fetched as
-// consecutive dwords across lanes (~4 rows per load instruction) and parked
-// raw in LDS; each wavefront decodes its own MFMA weight fragments from
-// them (byte -> 0x64XX half -> packed f16 subtract).  Workgroups are
-// numbered so each XCD (round-robin dispatch) walks n-tiles of its own band
-// of m-tiles.
+// advances two blocks (64 elements) per stage with one barrier per stage;
+// three stage buffers in LDS are filled by LDS DMA (buffer_load ... lds),
+// two stages ahead of the one being computed.  Every per-thread offset is
+// computed once, a stage advances only the (scalar) base of the buffer
+// resource, and rows past M/N read as zeros through the resource's range
+// check.  Weight stage segments (2 blocks = 68/36/40 bytes per row) arrive
+// as consecutive dwords across lanes (~4 rows per DMA instruction) and stay
+// raw in LDS; each wavefront decodes its own MFMA weight fragments from them
+// (byte -> 0x64XX half -> packed f16 subtract).  A stage's quantized work is
+// eight units (block x m-tile) whose combine FMAs trail their MFMAs by one
+// unit.  Workgroups are numbered so each XCD (round-robin dispatch) walks a
+// contiguous band of the tile order, which groups a few m-tiles and walks
+// n-tiles inside a group (L2 reuse of the resident workgroups' operands).
 #include <algorithm>
 #include <type_traits>
 

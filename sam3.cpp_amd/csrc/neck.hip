@@ -1,10 +1,12 @@
 // SAM3 SimpleFPN neck kernels (sam3_build_neck_graph, sam3.cpp:3867-3925) on
-// token-major activations [H*W][C] (ggml [C, W, H]).  The convolutions
-// themselves run as MUL_MATs (mmq.hip / gemm_f32.hip); these are the passes
-// around them, all HBM-bound: the conv-transpose kernel repack + F16 cast,
-// the scatter of the 2x2 / stride-2 transposed convolution with its bias
-// (and GELU), the F32 3x3 kernel repack for the implicit GEMM, im2col of the
-// F16 3x3 / pad-1 convolution, bias adds and the 2x2 max-pool.
+// token-major activations [H*W][C] (ggml [C, W, H]).  conv_f16_kernel is the
+// fp16-MFMA implicit GEMM of the F16-kernel convolutions (3x3, 1x1 and the
+// 2x2 / stride-2 conv-transpose with its scatter, bias and GELU in the
+// epilogue); F32-kernel convolutions run on gemm_f32.hip.  The rest are
+// HBM-bound passes: the conv-transpose kernel repack + F16 cast, the 3x3
+// kernel repacks for the implicit GEMMs, and, for maps the implicit GEMMs do
+// not take, im2col, the conv-transpose scatter and bias adds; the 2x2
+// max-pool.
 #include "common.cuh"
 #include "kernels.h"
 
