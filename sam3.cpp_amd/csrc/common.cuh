@@ -50,6 +50,43 @@ __device__ __forceinline__ uint16_t f2h(float f) {
     return h;
 }
 
+// Raw buffer resource over [base, base + bytes) (stride 0, gfx9 dword3 =
+// 0x00020000): offsets at or past the end read as zero.
+__device__ __forceinline__ v4i make_rsrc(const void* base, int64_t bytes) {
+    const int32_t n = bytes <= 0 ? 0 : (bytes > 0x7fffffffLL ? 0x7fffffff : (int32_t)bytes);
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    return v4i{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), n, 0x00020000};
+}
+
+// buffer_load ... lds: lane i's 4 (or 16) bytes at voffset land at LDS byte
+// address M0 + 4*i (16*i).  Issued from inline asm so the compiler's wait
+// insertion does not track them: it cannot tell one stage buffer from another
+// and would otherwise wait for every DMA in flight before the first LDS read.
+// The kernel orders them itself (vmcnt waits + barrier).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void dma_b32(v4i rsrc, const void* lds, int voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr(lds))), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma_b128(v4i rsrc, const void* lds, int voff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr(lds))), "v"(voff), "s"(rsrc)
+                 : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14, expcnt and
+// lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // Butterfly reductions across `width` consecutive lanes (width a power of
 // two <= 64) through ds_swizzle/ds_bpermute.
 template <int width>

@@ -28,7 +28,11 @@
 // banks (no bank conflicts in rocprofv3's counters).  Two K / V^T buffers:
 // after tile t's MFMAs tile t + 1 goes from registers into the free buffer
 // and tile t + 2's global loads are issued, with one LDS-only barrier per
-// tile.
+// tile.  An fp16 K with D = 64 or 128 (16-byte aligned rows) skips the
+// registers: right after the barrier that frees its buffer, tile t + 1's K
+// is copied by LDS DMA (buffer_load ... lds) into unpadded rows whose 16-byte
+// chunks are XOR-swizzled by row, and the next barrier waits for it with an
+// explicit vmcnt that leaves the V loads issued after it in flight.
 #include <algorithm>
 
 #include "common.cuh"
@@ -73,9 +77,15 @@ __device__ __forceinline__ float xmax32(float x) { return fmaxf(x, partner32(x))
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __device__ __forceinline__ float xsum32(float x) { return x + partner32(x); }
 
-template <int D, bool QF32, bool KVF32>
+// K row slot of 16-byte chunk c in row r of an unpadded fp16 K tile (DMA staging):
+// the 32-row fragment reads of one chunk then fall in distinct bank quads
+template <int D>
+__device__ __forceinline__ int kswz(int r) { return D == 64 ? ((r & 7) ^ ((r >> 3) & 1)) : (r & 15); }
+
+template <int D, bool QF32, bool KVF32, bool KDMA>
 __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
-    constexpr int KS = D + 8;       // K tile row stride (halves)
+    static_assert(!KDMA || (!KVF32 && (D == 64 || D == 128)), "K DMA staging: fp16 K, D = 64 or 128");
+    constexpr int KS = KDMA ? D : D + 8;  // K tile row stride (halves)
     constexpr int VS = FA_BKV + 4;  // V^T tile row stride (halves): 34 dwords, so the 8-byte reads of 32 rows hit distinct bank pairs
     constexpr int NC = D / 16;      // MFMA k-chunks of a score
     constexpr int NDB = D / 32;     // 32-row blocks of O^T
@@ -122,8 +132,10 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
         for (int j = 0; j < LPT; ++j) {
             const int id = tid + FA_NT * j;
             const int kk = id / C8, kc = id % C8;
-            kreg[j] = u32x4{0, 0, 0, 0};
-            if (kv0 + kk < nkv) kreg[j] = load8_h<KVF32>(kb + (int64_t)(kv0 + kk) * p.k_nb1 + kc * 8 * KES);
+            if (!KDMA) {
+                kreg[j] = u32x4{0, 0, 0, 0};
+                if (kv0 + kk < nkv) kreg[j] = load8_h<KVF32>(kb + (int64_t)(kv0 + kk) * p.k_nb1 + kc * 8 * KES);
+            }
             int vk, vc;
             if (VPAIR) {
                 const int pid = tid + FA_NT * (j >> 1);
@@ -133,13 +145,41 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
                 vk = id % FA_BKV;
                 vc = id / FA_BKV;
             }
-            vreg[j] = u32x4{0, 0, 0, 0};
-            if (kv0 + vk < nkv) vreg[j] = load8_h<KVF32>(vb + (int64_t)(kv0 + vk) * p.v_nb1 + vc * 8 * KES);
+            if (KDMA) {  // exactly LPT loads per tile (the K DMA wait counts them): rows clamped,
+                         // keys past nkv zeroed by store_tile
+                vreg[j] = load8_h<false>(vb + (int64_t)min(kv0 + vk, nkv - 1) * p.v_nb1 + vc * 16);
+            } else {
+                vreg[j] = u32x4{0, 0, 0, 0};
+                if (kv0 + vk < nkv) vreg[j] = load8_h<KVF32>(vb + (int64_t)(kv0 + vk) * p.v_nb1 + vc * 8 * KES);
+            }
         }
     };
-    auto store_tile = [&](int buf) {
+    // K tile by LDS DMA (buffer_load ... lds): wavefront w fills bytes [1024 (w KDI + j), +1024)
+    // of the tile with instruction j, lane i writing 16 bytes at + 16 i, i.e. slot s of row r;
+    // it loads the chunk s ^ kswz(r) of key kv0 + r.  Keys past nkv lie past the end of the
+    // buffer resource and read as zero.
+    constexpr int KDI = KDMA ? FA_BKV * D * 2 / 1024 / (FA_NT / 64) : 1;
+    const v4i krsrc = make_rsrc(kb, (int64_t)nkv * p.k_nb1);
+    auto dma_k = [&](int kv0, int buf) {
 #pragma unroll
-        for (int j = 0; j < LPT; ++j) {
+        for (int j = 0; j < KDI; ++j) {
+            const int base = (w * KDI + j) << 10, byte = base + 16 * lane;
+            const int r = byte / (2 * D), s = (byte % (2 * D)) / 16;
+            dma_b128(krsrc, reinterpret_cast<const char*>(sK[buf]) + base,
+                     (kv0 + r) * (int)p.k_nb1 + 16 * (s ^ kswz<D>(r)));
+        }
+    };
+    auto store_tile = [&](int buf, int kv0) {
+        if (KDMA) {
+#pragma unroll
+            for (int j = 0; j < LPT; ++j) {
+                const int id = tid + FA_NT * j, pid = tid + FA_NT * (j >> 1);
+                const int vk = VPAIR ? 2 * (pid % 32) + (j & 1) : id % FA_BKV;
+                if (kv0 + vk >= nkv) vreg[j] = u32x4{0, 0, 0, 0};
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < (KDMA ? 0 : LPT); ++j) {
             const int id = tid + FA_NT * j;
             const int kk = id / C8, kc = id % C8;
             *reinterpret_cast<u32x4*>(&sK[buf][kk * KS + kc * 8]) = kreg[j];
@@ -185,12 +225,18 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
     // tile t + 1 goes from the registers (loaded during tile t) into that buffer and
     // tile t + 2's loads are issued, so each load has a whole tile to land.
     const int ntile = (nkv + FA_BKV - 1) / FA_BKV;
+    if (KDMA) dma_k(0, 0);
     load_tile(0);
-    store_tile(0);
+    store_tile(0, 0);
     if (ntile > 1) load_tile(FA_BKV);
     for (int t = 0; t < ntile; ++t) {
         const int kv0 = t * FA_BKV, cb = t & 1;
+        if (KDMA) {  // tile t's K DMA precedes tile t + 1's LPT V loads (when issued)
+            if (t + 1 < ntile) wait_vmcnt<LPT>();
+            else wait_vmcnt<0>();
+        }
         lds_barrier();
+        if (KDMA && t + 1 < ntile) dma_k(kv0 + FA_BKV, cb ^ 1);  // buffer cb ^ 1 was freed by the barrier
 
         // S^T for the two 32-key halves
         v16f S[2];
@@ -199,7 +245,8 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
             S[kh] = zf;
 #pragma unroll
             for (int cc = 0; cc < NC; ++cc) {
-                const v8h a = *reinterpret_cast<const v8h*>(&sK[cb][(32 * kh + lr) * KS + 16 * cc + 8 * g]);
+                const int r = 32 * kh + lr, slot = KDMA ? (2 * cc + g) ^ kswz<D>(r) : 2 * cc + g;
+                const v8h a = *reinterpret_cast<const v8h*>(&sK[cb][r * KS + 8 * slot]);
                 S[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[cc], S[kh], 0, 0, 0);
             }
         }
@@ -269,7 +316,7 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
                 }
         }
         if (t + 1 < ntile) {
-            store_tile(cb ^ 1);
+            store_tile(cb ^ 1, kv0 + FA_BKV);
             if (t + 2 < ntile) load_tile(kv0 + 2 * FA_BKV);
         }
     }
@@ -400,10 +447,22 @@ size_t fattn_part_bytes(int D, int nq, int nh, int B, int kv_split) {
 template <int D>
 static void fa_launch_d(const FaArgs& a, bool qf32, bool kvf32, int B, hipStream_t st) {
     const dim3 grid((unsigned)((a.nq + FA_BQ - 1) / FA_BQ), (unsigned)a.nh, (unsigned)(B * a.kv_split));
-    if (qf32 && kvf32) fattn_kernel<D, true, true><<<grid, FA_NT, 0, st>>>(a);
-    else if (qf32) fattn_kernel<D, true, false><<<grid, FA_NT, 0, st>>>(a);
-    else if (kvf32) fattn_kernel<D, false, true><<<grid, FA_NT, 0, st>>>(a);
-    else fattn_kernel<D, false, false><<<grid, FA_NT, 0, st>>>(a);
+    bool launched = false;
+    if constexpr (D == 64 || D == 128) {
+        // fp16 K rows and bases on 16 bytes, key offsets within the 32-bit buffer offset
+        const bool kdma = !kvf32 && reinterpret_cast<uintptr_t>(a.k) % 16 == 0 && a.k_nb1 % 16 == 0 &&
+                          a.k_nb2 % 16 == 0 && a.k_nb3 % 16 == 0 && (int64_t)(a.nkv + FA_BKV) * a.k_nb1 < INT32_MAX;
+        if (kdma) {
+            if (qf32) fattn_kernel<D, true, false, true><<<grid, FA_NT, 0, st>>>(a);
+            else fattn_kernel<D, false, false, true><<<grid, FA_NT, 0, st>>>(a);
+            launched = true;
+        }
+    }
+    if (launched) {
+    } else if (qf32 && kvf32) fattn_kernel<D, true, true, false><<<grid, FA_NT, 0, st>>>(a);
+    else if (qf32) fattn_kernel<D, true, false, false><<<grid, FA_NT, 0, st>>>(a);
+    else if (kvf32) fattn_kernel<D, false, true, false><<<grid, FA_NT, 0, st>>>(a);
+    else fattn_kernel<D, false, false, false><<<grid, FA_NT, 0, st>>>(a);
     if (a.kv_split > 1) {
         const int64_t n = (int64_t)B * a.nh * a.nq * (D / 4);
         fattn_combine_kernel<D><<<(unsigned)((n + 255) / 256), 256, 0, st>>>(a, B);
