@@ -34,14 +34,15 @@ def _inputs(orc, D, nq, nkv, nh, nhk, B, seed=0):
     return q, k, v
 
 
-def _gpu_fa(mi, ctx, q, k, v, scale, qt, kvt, v_nb=None, v_ne=None):
-    """q/k/v numpy in [B, heads, n, D] order (or v given by raw buffer + ne/nb)."""
+def _gpu_fa(mi, ctx, q, k, v, scale, qt, kvt, v_nb=None, v_ne=None, k_nb=None):
+    """q/k/v numpy in [B, heads, n, D] order (or v given by raw buffer + ne/nb;
+    with k_nb, k's rows are the first D elements of its last axis)."""
     B, nh, nq, D = q.shape
     qd, kd, vd = dev(q), dev(k), dev(v)
     nkv, nhk = k.shape[2], k.shape[1]
     dst = torch.full((B, nq, nh, D), float("nan"), dtype=torch.float32, device="cuda")
     tq = mi.from_torch(qd, qt, [D, nq, nh, B])
-    tk = mi.from_torch(kd, kvt, [D, nkv, nhk, B])
+    tk = mi.from_torch(kd, kvt, [D, nkv, nhk, B], k_nb)
     tv = mi.from_torch(vd, kvt, v_ne or [D, nkv, nhk, B], v_nb)
     td = mi.from_torch(dst, mi.F32, [D, nh, nq, B])
     ctx.flash_attn_ext(tq, tk, tv, td, scale)
@@ -139,6 +140,23 @@ def test_flash_attn_mixed_types_and_scale(mi, ctx, orc):
     for scale in (-0.2, 0.0):
         got = _gpu_fa(mi, ctx, q, kh, vh, scale, mi.F32, mi.F16)
         _check(orc, got, _f16(q), kh, vh, scale, orc.F16)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_flash_attn_k_row_strides(mi, ctx, orc, D):
+    """F16 K rows inside wider rows (padding filled with NaN, never read): a row
+    stride of 3D halves keeps 16-byte rows (K staged by LDS DMA), D + 2 does not
+    (K staged through registers).  Both give output bit-identical to contiguous K."""
+    nq, nkv, nh = 150, 200, 2
+    q, k, v = (_f16(a) for a in _inputs(orc, D, nq, nkv, nh, nh, 1, seed=11))
+    scale = 1.0 / np.sqrt(D)
+    ref = _gpu_fa(mi, ctx, q, k, v, scale, mi.F16, mi.F16)
+    _check(orc, ref, q, k, v, scale, orc.F16)
+    for W in (3 * D, D + 2):
+        kbuf = np.full((1, nh, nkv, W), np.nan, np.float16)
+        kbuf[..., :D] = k
+        got = _gpu_fa(mi, ctx, q, kbuf, v, scale, mi.F16, mi.F16, k_nb=[2, 2 * W, 2 * W * nkv, 2 * W * nkv * nh])
+        assert np.array_equal(got, ref), f"row stride {W}"
 
 
 def test_flash_attn_rejects(mi, ctx, orc):
