@@ -88,6 +88,37 @@ mi355_status mi355_reserve_workspace(mi355_context* ctx, size_t bytes);
 /* Workspace bytes mul_mat needs for these operands. */
 size_t mi355_mul_mat_workspace_size(const mi355_tensor* src0, const mi355_tensor* src1);
 
+/* ---- Device buffers (the ggml-backend buffer calls around a graph) ---------
+ * A buffer is one device allocation on the context's device, owned by the
+ * caller until mi355_buffer_free.  It stands in for
+ * ggml_backend_alloc_ctx_tensors (sam3.cpp:3320, the model's weights) and for
+ * the graph allocator's buffer (ggml_gallocr_alloc_graph, sam3.cpp:6101-6115);
+ * mi355_buffer_place puts a tensor at an offset in it (ggml_tallocr_alloc),
+ * offsets being multiples of mi355_buffer_alignment().  The byte layouts are
+ * ggml's, so tensor bytes read from a .ggml file or written by ggml-cpu are
+ * used as they are. */
+typedef struct mi355_buffer mi355_buffer;
+size_t mi355_buffer_alignment(void);
+mi355_status mi355_buffer_alloc(mi355_context* ctx, size_t size, mi355_buffer** out);
+/* ggml_backend_buffer_free: waits for the device's work before freeing. */
+void mi355_buffer_free(mi355_buffer* buf);
+void* mi355_buffer_base(const mi355_buffer* buf);
+size_t mi355_buffer_size(const mi355_buffer* buf);
+/* Sets t->data = base + offset after checking that ggml_nbytes(t) bytes fit. */
+mi355_status mi355_buffer_place(const mi355_buffer* buf, size_t offset, mi355_tensor* t);
+/* ggml_nbytes of t's layout (0 for an empty tensor or an unknown type). */
+size_t mi355_tensor_nbytes(const mi355_tensor* t);
+/* ggml_backend_buffer_clear. */
+mi355_status mi355_buffer_clear(mi355_context* ctx, mi355_buffer* buf, uint8_t value);
+/* ggml_backend_tensor_set / _get / _memset (sam3.cpp:3156-3179, 6117): bytes
+ * [offset, offset + size) of the tensor's data, bounds-checked against
+ * ggml_nbytes(t); ordered after the work already on the context's stream, and
+ * returning when the host side is done (set: data may be reused; get: data
+ * has arrived). */
+mi355_status mi355_tensor_set(mi355_context* ctx, const mi355_tensor* t, const void* data, size_t offset, size_t size);
+mi355_status mi355_tensor_get(mi355_context* ctx, const mi355_tensor* t, void* data, size_t offset, size_t size);
+mi355_status mi355_tensor_memset(mi355_context* ctx, const mi355_tensor* t, uint8_t value, size_t offset, size_t size);
+
 /* ---- MUL_MAT (ggml_mul_mat, sam3.cpp:3742,3783,3796,3799) ----------------
  * dst[N, M, b2, b3] = src0[K, N, a2, a3]^T . src1[K, M, b2, b3], with
  * b2 % a2 == 0, b3 % a3 == 0 (src0 broadcast by the ratio).
@@ -96,6 +127,11 @@ size_t mi355_mul_mat_workspace_size(const mi355_tensor* src0, const mi355_tensor
  * Q8_0/Q4_0 quantize src1 to Q8_0 and Q4_1 to Q8_1 (x86 variant) exactly as
  * ggml-cpu's from_float, then combine exact int32 block dots in fp32.  F16
  * converts src1 to F16 (round to nearest even) and accumulates in fp32. */
+/* The mi355_supports_* queries are ggml_backend_supports_op for each node
+ * kind: 1 when the entry point accepts these operands (no GPU work, no
+ * context), 0 otherwise.  sam3.cpp runs each graph on a single backend
+ * (sam3.cpp:3278-3292), so a graph builder checks every node before
+ * choosing this one. */
 int mi355_supports_mul_mat(const mi355_tensor* src0, const mi355_tensor* src1, const mi355_tensor* dst);
 mi355_status mi355_mul_mat(mi355_context* ctx, const mi355_tensor* src0, const mi355_tensor* src1,
                            const mi355_tensor* dst);
@@ -125,6 +161,8 @@ mi355_status mi355_mul_mat_block_dots(mi355_context* ctx, const mi355_tensor* sr
 
 /* ---- SOFT_MAX (ggml_soft_max_ext(a, NULL, scale, 0.0f), sam3.cpp:8586) ----
  * Row-wise softmax of scale*src over ne[0]; F32 in/out, any row strides. */
+int mi355_supports_soft_max_ext(const mi355_tensor* src, const mi355_tensor* mask, float max_bias,
+                                const mi355_tensor* dst);
 mi355_status mi355_soft_max_ext(mi355_context* ctx, const mi355_tensor* src, const mi355_tensor* mask,
                                 float scale, float max_bias, const mi355_tensor* dst);
 
@@ -134,6 +172,9 @@ mi355_status mi355_soft_max_ext(mi355_context* ctx, const mi355_tensor* src, con
  * (F32 or F16, any strides: the ViT passes V as a permuted view,
  * sam3.cpp:3767); dst [Dv, n_head, n_q, B] F32 contiguous.  D = Dv in
  * {64, 96, 128}.  mask must be NULL, max_bias and logit_softcap 0. */
+int mi355_supports_flash_attn_ext(const mi355_tensor* q, const mi355_tensor* k, const mi355_tensor* v,
+                                  const mi355_tensor* mask, float max_bias, float logit_softcap,
+                                  const mi355_tensor* dst);
 mi355_status mi355_flash_attn_ext(mi355_context* ctx, const mi355_tensor* q, const mi355_tensor* k,
                                   const mi355_tensor* v, const mi355_tensor* mask, float scale, float max_bias,
                                   float logit_softcap, const mi355_tensor* dst);

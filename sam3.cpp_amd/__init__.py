@@ -129,6 +129,19 @@ def lib():
         "mi355_reserve_workspace": (I, [P, SZ]),
         "mi355_mul_mat_workspace_size": (SZ, [T, T]),
         "mi355_supports_mul_mat": (I, [T, T, T]),
+        "mi355_buffer_alignment": (SZ, []),
+        "mi355_buffer_alloc": (I, [P, SZ, C.POINTER(P)]),
+        "mi355_buffer_free": (None, [P]),
+        "mi355_buffer_base": (P, [P]),
+        "mi355_buffer_size": (SZ, [P]),
+        "mi355_buffer_place": (I, [P, SZ, T]),
+        "mi355_buffer_clear": (I, [P, P, C.c_uint8]),
+        "mi355_tensor_nbytes": (SZ, [T]),
+        "mi355_tensor_set": (I, [P, T, P, SZ, SZ]),
+        "mi355_tensor_get": (I, [P, T, P, SZ, SZ]),
+        "mi355_tensor_memset": (I, [P, T, C.c_uint8, SZ, SZ]),
+        "mi355_supports_flash_attn_ext": (I, [T, T, T, T, F, F, T]),
+        "mi355_supports_soft_max_ext": (I, [T, T, F, T]),
         "mi355_mul_mat": (I, [P, T, T, T]),
         "mi355_quantize_rows": (I, [P, I, I, T, P]),
         "mi355_quantize_weights": (I, [P, I, T, P]),

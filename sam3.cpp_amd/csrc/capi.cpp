@@ -147,6 +147,19 @@ MmPlan mm_plan(const mi355_tensor* s0, const mi355_tensor* s1, int cus, bool spl
     return pl;
 }
 
+// ggml_soft_max_ext(a, mask, scale, max_bias) shape rules plus what softmax.hip implements.
+mi355_status check_soft_max(mi355_context* ctx, const mi355_tensor* src, const mi355_tensor* mask, float max_bias,
+                            const mi355_tensor* dst) {
+    if (!src || !dst || !src->data || !dst->data) return fail(ctx, MI355_STATUS_INVALID_ARG, "soft_max: null argument");
+    if (!dims_ok(src) || !dims_ok(dst)) return fail(ctx, MI355_STATUS_INVALID_ARG, "soft_max: negative ne/nb");
+    if (mask || max_bias != 0.0f) return fail(ctx, MI355_STATUS_UNSUPPORTED, "soft_max: mask/ALiBi not supported");
+    if (src->type != T_F32 || dst->type != T_F32) return fail(ctx, MI355_STATUS_UNSUPPORTED, "soft_max: F32 only");
+    for (int i = 0; i < 4; ++i)
+        if (src->ne[i] != dst->ne[i]) return fail(ctx, MI355_STATUS_INVALID_ARG, "soft_max: shape mismatch");
+    if (src->ne[0] > 8192) return fail(ctx, MI355_STATUS_UNSUPPORTED, "soft_max: rows longer than 8192");
+    return MI355_STATUS_SUCCESS;
+}
+
 bool dst_split_ok(const mi355_tensor* d) {
     return d->nb[1] % 16 == 0 && (reinterpret_cast<uintptr_t>(d->data) & 15) == 0;
 }
@@ -200,10 +213,9 @@ mi355_status check_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
 // Quantize src1 for src0's vec_dot_type into the workspace (x86 from_float).
 // The workspace must already hold mm_plan(s0, s1).total() bytes.
 mi355_status prep_act_q8(mi355_context* ctx, const mi355_tensor* s0, const mi355_tensor* s1, const MmPlan& pl,
-                         ActF16& a) {
+                         char* p, bool timed, ActF16& a) {
     const int64_t K = s1->ne[0], M = s1->ne[1];
     const bool with_sum = s0->type == T_Q4_1;
-    char* p = static_cast<char*>(ctx->ws);
     uint16_t* q = reinterpret_cast<uint16_t*>(p);
     uint16_t* d = reinterpret_cast<uint16_t*>(p + pl.q);
     uint16_t* sm = with_sum ? reinterpret_cast<uint16_t*>(p + pl.q + pl.d) : nullptr;
@@ -216,9 +228,72 @@ mi355_status prep_act_q8(mi355_context* ctx, const mi355_tensor* s0, const mi355
     a.dp = mmq_scale_pitch(K);
     a.M = M;
     a.K = K;
-    Timed tm(ctx, "quantize_mmq");
+    Timed tm(timed ? ctx : nullptr, "quantize_mmq");
     return hip_check(ctx, tm.done(launch_quantize_mmq(view_of(s1), with_sum, a.dp, q, d, sm, ctx->stream)),
                      "quantize_mmq launch");
+}
+
+// MUL_MAT of validated operands with the workspace ws (at least
+// mm_plan(...).total() bytes): the activation conversion, then the GEMM.
+// timed = false: no timing events (the no-allocation entry point).
+mi355_status mul_mat_run(mi355_context* ctx, const mi355_tensor* s0, const mi355_tensor* s1, const mi355_tensor* d,
+                         const MmPlan& pl, char* ws, bool timed) {
+    mi355_context* tctx = timed ? ctx : nullptr;
+    const int64_t K = s0->ne[0], N = s0->ne[1], M = s1->ne[1];
+    mi355_status st;
+    ActF16 a;
+    if (s0->type == T_F16) {
+        a.M = M;
+        a.K = K;
+        a.d = a.s = nullptr;
+        a.dp = 0;
+        if (f16_src1_direct(s1)) {
+            a.q = s1->data;
+            a.s1 = s1->nb[1] / 2;
+            a.s2 = s1->nb[2] / 2;
+            a.s3 = s1->nb[3] / 2;
+        } else {
+            // rows padded with zeros to a whole 16-byte chunk
+            const int64_t K8 = (K + 7) & ~7;
+            uint16_t* buf = reinterpret_cast<uint16_t*>(ws);
+            Timed tc(tctx, "convert_f16");
+            st = hip_check(ctx, tc.done(launch_convert_f16(view_of(s1), buf, K8, ctx->stream)), "convert_f16 launch");
+            if (st != MI355_STATUS_SUCCESS) return st;
+            a.q = buf;
+            a.s1 = K8;
+            a.s2 = K8 * M;
+            a.s3 = K8 * M * s1->ne[2];
+        }
+    } else {
+        st = prep_act_q8(ctx, s0, s1, pl, ws, timed, a);
+        if (st != MI355_STATUS_SUCCESS) return st;
+    }
+    void* align_buf = pl.align ? ws + pl.q + pl.d + pl.s : nullptr;
+    const MmqSplit sp{pl.ks, pl.ks > 1 ? reinterpret_cast<float*>(ws + pl.q + pl.d + pl.s + pl.align) : nullptr,
+                      ctx->skinny};
+    const char* kname = s0->type == T_F16 ? "mmq_f16" : s0->type == T_Q8_0 ? "mmq_q8_0" : s0->type == T_Q4_0 ? "mmq_q4_0" : "mmq_q4_1";
+    Timed tq(tctx, kname);
+    return hip_check(ctx, tq.done(launch_mmq(matw_of(s0), a, matd_of(d), N, s1->ne[2], s1->ne[3], nullptr, align_buf,
+                                             sp, ctx->stream)),
+                     "mmq launch");
+}
+
+// MUL_MAT with F32 weights: the fp32 MFMA GEMM, no workspace.
+mi355_status mul_mat_f32(mi355_context* ctx, const mi355_tensor* s0, const mi355_tensor* s1, const mi355_tensor* d,
+                         bool timed) {
+    GemmF32Args g;
+    g.W = static_cast<const float*>(s0->data);
+    g.w_nb1 = s0->nb[1]; g.w_nb2 = s0->nb[2]; g.w_nb3 = s0->nb[3];
+    g.X = static_cast<const float*>(s1->data);
+    g.x_nb1 = s1->nb[1]; g.x_nb2 = s1->nb[2]; g.x_nb3 = s1->nb[3];
+    g.D = static_cast<float*>(d->data);
+    g.d_nb1 = d->nb[1]; g.d_nb2 = d->nb[2]; g.d_nb3 = d->nb[3];
+    g.M = (int)s1->ne[1]; g.N = (int)s0->ne[1]; g.K = (int)s0->ne[0];
+    g.ne12 = (int)s1->ne[2];
+    g.r2 = (int)(s1->ne[2] / s0->ne[2]);
+    g.r3 = (int)(s1->ne[3] / s0->ne[3]);
+    Timed tg(timed ? ctx : nullptr, "gemm_f32");
+    return hip_check(ctx, tg.done(launch_gemm_f32(g, (int)(s1->ne[2] * s1->ne[3]), ctx->stream)), "gemm_f32 launch");
 }
 
 }  // namespace
@@ -299,9 +374,9 @@ mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF1
                      "mmq launch");
 }
 
-mi355_status flash_attn_act(mi355_context* ctx, const mi355_tensor* q, const mi355_tensor* k, const mi355_tensor* v,
-                            const mi355_tensor* mask, float scale, float max_bias, float logit_softcap,
-                            const mi355_tensor* dst, const ActOut* op) {
+// ggml_flash_attn_ext's shape rules plus what fattn_kernel implements.
+mi355_status check_flash_attn(mi355_context* ctx, const mi355_tensor* q, const mi355_tensor* k, const mi355_tensor* v,
+                              const mi355_tensor* mask, float max_bias, float logit_softcap, const mi355_tensor* dst) {
     if (!q || !k || !v || !dst || !q->data || !k->data || !v->data || !dst->data)
         return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: null argument");
     if (!dims_ok(q) || !dims_ok(k) || !dims_ok(v) || !dims_ok(dst))
@@ -336,7 +411,16 @@ mi355_status flash_attn_act(mi355_context* ctx, const mi355_tensor* q, const mi3
     if (k->type != v->type) return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: k and v must share a type");
     if (q->ne[1] > INT32_MAX || k->ne[1] > INT32_MAX || q->ne[2] > 65535 || q->ne[3] > 65535)
         return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: sizes beyond the launch limits");
+    return MI355_STATUS_SUCCESS;
+}
+
+mi355_status flash_attn_act(mi355_context* ctx, const mi355_tensor* q, const mi355_tensor* k, const mi355_tensor* v,
+                            const mi355_tensor* mask, float scale, float max_bias, float logit_softcap,
+                            const mi355_tensor* dst, const ActOut* op) {
+    const mi355_status cs = check_flash_attn(ctx, q, k, v, mask, max_bias, logit_softcap, dst);
+    if (cs != MI355_STATUS_SUCCESS) return cs;
     if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "flash_attn_ext: null context");
+    const int64_t D = q->ne[0];
     FaArgs a;
     a.q = static_cast<const char*>(q->data);
     a.k = static_cast<const char*>(k->data);
@@ -463,62 +547,12 @@ mi355_status mi355_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
     if (st != MI355_STATUS_SUCCESS) return st;
     if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "mul_mat: null context");
     (void)hipSetDevice(ctx->device);
-    const int64_t K = s0->ne[0], N = s0->ne[1], M = s1->ne[1];
-    if (K == 0 || N == 0 || M == 0 || s1->ne[2] * s1->ne[3] == 0) return MI355_STATUS_SUCCESS;
-    if (s0->type == T_F32) {
-        GemmF32Args g;
-        g.W = static_cast<const float*>(s0->data);
-        g.w_nb1 = s0->nb[1]; g.w_nb2 = s0->nb[2]; g.w_nb3 = s0->nb[3];
-        g.X = static_cast<const float*>(s1->data);
-        g.x_nb1 = s1->nb[1]; g.x_nb2 = s1->nb[2]; g.x_nb3 = s1->nb[3];
-        g.D = static_cast<float*>(d->data);
-        g.d_nb1 = d->nb[1]; g.d_nb2 = d->nb[2]; g.d_nb3 = d->nb[3];
-        g.M = (int)M; g.N = (int)N; g.K = (int)K;
-        g.ne12 = (int)s1->ne[2];
-        g.r2 = (int)(s1->ne[2] / s0->ne[2]);
-        g.r3 = (int)(s1->ne[3] / s0->ne[3]);
-        Timed tg(ctx, "gemm_f32");
-        return hip_check(ctx, tg.done(launch_gemm_f32(g, (int)(s1->ne[2] * s1->ne[3]), ctx->stream)), "gemm_f32 launch");
-    }
+    if (s0->ne[0] == 0 || s0->ne[1] == 0 || s1->ne[1] == 0 || s1->ne[2] * s1->ne[3] == 0) return MI355_STATUS_SUCCESS;
+    if (s0->type == T_F32) return mul_mat_f32(ctx, s0, s1, d, true);
     const MmPlan pl = mm_plan(s0, s1, ctx->cus, dst_split_ok(d));
     st = ensure_ws(ctx, pl.total());
     if (st != MI355_STATUS_SUCCESS) return st;
-    ActF16 a;
-    if (s0->type == T_F16) {
-        a.M = M;
-        a.K = K;
-        a.d = a.s = nullptr;
-        a.dp = 0;
-        if (f16_src1_direct(s1)) {
-            a.q = s1->data;
-            a.s1 = s1->nb[1] / 2;
-            a.s2 = s1->nb[2] / 2;
-            a.s3 = s1->nb[3] / 2;
-        } else {
-            // rows padded with zeros to a whole 16-byte chunk
-            const int64_t K8 = (K + 7) & ~7;
-            uint16_t* buf = static_cast<uint16_t*>(ctx->ws);
-            Timed tc(ctx, "convert_f16");
-            st = hip_check(ctx, tc.done(launch_convert_f16(view_of(s1), buf, K8, ctx->stream)), "convert_f16 launch");
-            if (st != MI355_STATUS_SUCCESS) return st;
-            a.q = buf;
-            a.s1 = K8;
-            a.s2 = K8 * M;
-            a.s3 = K8 * M * s1->ne[2];
-        }
-    } else {
-        st = prep_act_q8(ctx, s0, s1, pl, a);
-        if (st != MI355_STATUS_SUCCESS) return st;
-    }
-    void* align_buf = pl.align ? static_cast<char*>(ctx->ws) + pl.q + pl.d + pl.s : nullptr;
-    const MmqSplit sp{pl.ks, pl.ks > 1 ? reinterpret_cast<float*>(static_cast<char*>(ctx->ws) + pl.q + pl.d + pl.s +
-                                                                  pl.align)
-                                       : nullptr, ctx->skinny};
-    const char* kname = s0->type == T_F16 ? "mmq_f16" : s0->type == T_Q8_0 ? "mmq_q8_0" : s0->type == T_Q4_0 ? "mmq_q4_0" : "mmq_q4_1";
-    Timed tq(ctx, kname);
-    return hip_check(ctx, tq.done(launch_mmq(matw_of(s0), a, matd_of(d), N, s1->ne[2], s1->ne[3], nullptr, align_buf,
-                                             sp, ctx->stream)),
-                     "mmq launch");
+    return mul_mat_run(ctx, s0, s1, d, pl, static_cast<char*>(ctx->ws), true);
 }
 
 mi355_status mi355_mul_mat_block_dots(mi355_context* ctx, const mi355_tensor* s0, const mi355_tensor* s1,
@@ -545,7 +579,7 @@ mi355_status mi355_mul_mat_block_dots(mi355_context* ctx, const mi355_tensor* s0
     st = ensure_ws(ctx, pl.total());
     if (st != MI355_STATUS_SUCCESS) return st;
     ActF16 a;
-    st = prep_act_q8(ctx, s0, s1, pl, a);
+    st = prep_act_q8(ctx, s0, s1, pl, static_cast<char*>(ctx->ws), true, a);
     if (st != MI355_STATUS_SUCCESS) return st;
     void* align_buf = pl.align ? static_cast<char*>(ctx->ws) + pl.q + pl.d + pl.s : nullptr;
     return hip_check(ctx, launch_mmq(matw_of(s0), a, matd_of(&d), s0->ne[1], s1->ne[2], s1->ne[3], isums, align_buf,
@@ -594,14 +628,21 @@ mi355_status mi355_quantize_weights(mi355_context* ctx, int type, const mi355_te
                      "quantize_weights launch");
 }
 
+int mi355_supports_flash_attn_ext(const mi355_tensor* q, const mi355_tensor* k, const mi355_tensor* v,
+                                  const mi355_tensor* mask, float max_bias, float logit_softcap,
+                                  const mi355_tensor* dst) {
+    return mi355::check_flash_attn(nullptr, q, k, v, mask, max_bias, logit_softcap, dst) == MI355_STATUS_SUCCESS;
+}
+
+int mi355_supports_soft_max_ext(const mi355_tensor* src, const mi355_tensor* mask, float max_bias,
+                                const mi355_tensor* dst) {
+    return check_soft_max(nullptr, src, mask, max_bias, dst) == MI355_STATUS_SUCCESS;
+}
+
 mi355_status mi355_soft_max_ext(mi355_context* ctx, const mi355_tensor* src, const mi355_tensor* mask, float scale,
                                 float max_bias, const mi355_tensor* dst) {
-    if (!src || !dst || !src->data || !dst->data) return fail(ctx, MI355_STATUS_INVALID_ARG, "soft_max: null argument");
-    if (mask || max_bias != 0.0f) return fail(ctx, MI355_STATUS_UNSUPPORTED, "soft_max: mask/ALiBi not supported");
-    if (src->type != T_F32 || dst->type != T_F32) return fail(ctx, MI355_STATUS_UNSUPPORTED, "soft_max: F32 only");
-    for (int i = 0; i < 4; ++i)
-        if (src->ne[i] != dst->ne[i]) return fail(ctx, MI355_STATUS_INVALID_ARG, "soft_max: shape mismatch");
-    if (src->ne[0] > 8192) return fail(ctx, MI355_STATUS_UNSUPPORTED, "soft_max: rows longer than 8192");
+    const mi355_status cs = check_soft_max(ctx, src, mask, max_bias, dst);
+    if (cs != MI355_STATUS_SUCCESS) return cs;
     if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "soft_max: null context");
     (void)hipSetDevice(ctx->device);
     Timed ts(ctx, "soft_max");

@@ -58,6 +58,9 @@ int act_mode_for(int weight_type);
 // epilogue replaces the dst store (dst only gives the shape).
 mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const mi355_tensor* dst,
                          const MmqEpi* epi = nullptr);
+// The host-side checks of mi355_flash_attn_ext (no launch).
+mi355_status check_flash_attn(mi355_context* ctx, const mi355_tensor* q, const mi355_tensor* k, const mi355_tensor* v,
+                              const mi355_tensor* mask, float max_bias, float logit_softcap, const mi355_tensor* dst);
 // FLASH_ATTN_EXT with the checks of mi355_flash_attn_ext; with op the output
 // goes to the next MUL_MAT's operand (rows b*n_q + iq, K = n_head*D) instead
 // of dst (which still gives the shape).

@@ -155,7 +155,7 @@ def test_every_entry_point_rejects_null_arguments(mi):
         # calls that create or query state without a context (or whose null arguments are valid)
         # are checked by their own tests: they may legitimately succeed
         skip = {{"mi355_context_create", "mi355_status_to_string", "mi355_last_error",
-                 "mi355_model_file_last_error", "mi355_hiera_n_blocks", "mi355_supports_mul_mat"}}
+                 "mi355_model_file_last_error", "mi355_hiera_n_blocks", "mi355_buffer_alignment"}}
         bad = []
         for name in sorted(mi.header_symbols()):
             if name in skip:
@@ -165,14 +165,16 @@ def test_every_entry_point_rejects_null_arguments(mi):
             for t in fn.argtypes:
                 if t in (C.c_float, C.c_double):
                     args.append(0.0)
-                elif t in (C.c_int, C.c_int32, C.c_int64, C.c_uint32, C.c_size_t):
+                elif t in (C.c_int, C.c_int32, C.c_int64, C.c_uint32, C.c_uint8, C.c_size_t):
                     args.append(0)
                 else:
                     args.append(None)
             r = fn(*args)
             if fn.restype is None:
                 continue
-            if fn.restype == C.c_size_t:
+            if name.startswith("mi355_supports_"):
+                if r != 0: bad.append((name, r))
+            elif fn.restype == C.c_size_t:
                 if r != 0: bad.append((name, r))
             elif fn.restype == C.c_int and name.endswith(("_find", "_hparams", "_collect")):
                 if r > 0: bad.append((name, r))
@@ -184,3 +186,76 @@ def test_every_entry_point_rejects_null_arguments(mi):
     r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr[-3000:]
     assert "BAD []" in r.stdout, r.stdout
+
+
+def fa_tensors(mi, D=64, n=40, nh=2, t=1, ptr=0x1000):
+    q = mi.make_tensor(ptr, t, [D, n, nh, 1])
+    k = mi.make_tensor(ptr, t, [D, n, nh, 1])
+    v = mi.make_tensor(ptr, t, [D, n, nh, 1])
+    o = mi.make_tensor(ptr, 0, [D, nh, n, 1])
+    return q, k, v, o
+
+
+def test_supports_flash_attn_and_soft_max(mi):
+    """The supports queries (ggml_backend_supports_op per node kind) answer
+    from the host checks of the entry points, with no context and no GPU."""
+    L = mi.lib()
+    q, k, v, o = fa_tensors(mi)
+    assert L.mi355_supports_flash_attn_ext(q, k, v, None, 0.0, 0.0, o) == 1
+    assert L.mi355_supports_flash_attn_ext(q, k, v, q, 0.0, 0.0, o) == 0      # a mask
+    assert L.mi355_supports_flash_attn_ext(q, k, v, None, 1.0, 0.0, o) == 0   # ALiBi
+    assert L.mi355_supports_flash_attn_ext(q, k, v, None, 0.0, 30.0, o) == 0  # softcap
+    q2, k2, v2, o2 = fa_tensors(mi, D=80)
+    assert L.mi355_supports_flash_attn_ext(q2, k2, v2, None, 0.0, 0.0, o2) == 0  # head size
+    q3, k3, v3, o3 = fa_tensors(mi)
+    o3.ne[1] = 3                                                               # dst shape
+    assert L.mi355_supports_flash_attn_ext(q3, k3, v3, None, 0.0, 0.0, o3) == 0
+    s = mi.make_tensor(0x1000, 0, [576, 576, 16, 1])
+    d = mi.make_tensor(0x2000, 0, [576, 576, 16, 1])
+    assert L.mi355_supports_soft_max_ext(s, None, 0.0, d) == 1
+    assert L.mi355_supports_soft_max_ext(s, s, 0.0, d) == 0
+    assert L.mi355_supports_soft_max_ext(s, None, 0.0, mi.make_tensor(0x2000, 1, [576, 576, 16, 1])) == 0
+    assert L.mi355_supports_soft_max_ext(mi.make_tensor(0x1000, 0, [9000, 4]), None, 0.0,
+                                         mi.make_tensor(0x2000, 0, [9000, 4])) == 0
+
+
+def test_tensor_nbytes_is_ggml_nbytes(mi):
+    L = mi.lib()
+    assert L.mi355_tensor_nbytes(mi.make_tensor(0x1000, 8, [1024, 4736])) == 4736 * 32 * 34
+    assert L.mi355_tensor_nbytes(mi.make_tensor(0x1000, 0, [64, 40, 2, 3])) == 64 * 40 * 2 * 3 * 4
+    # a permuted view: the span from the first to one past the last element
+    t = mi.make_tensor(0x1000, 0, [64, 40, 2, 1], nb=[4, 4 * 64 * 2, 4 * 64, 4 * 64 * 2 * 40])
+    assert L.mi355_tensor_nbytes(t) == 4 + 63 * 4 + 39 * 4 * 64 * 2 + 1 * 4 * 64
+    assert L.mi355_tensor_nbytes(mi.make_tensor(0x1000, 0, [64, 0])) == 0
+    assert L.mi355_tensor_nbytes(mi.make_tensor(0x1000, 7, [64, 2], nb=[4, 256, 512, 512])) == 0  # unknown type
+
+
+def test_buffer_api_host_checks(mi):
+    L = mi.lib()
+    assert L.mi355_buffer_alignment() == 256
+    out = C.c_void_p()
+    assert L.mi355_buffer_alloc(None, 1024, C.byref(out)) == -4 and not out.value
+    assert L.mi355_buffer_place(None, 0, mi.make_tensor(0, 0, [4])) == -4
+    t = mi.make_tensor(0x1000, 0, [16])
+    buf = C.create_string_buffer(64)
+    assert L.mi355_tensor_set(None, t, buf, 0, 64) == -4
+    assert L.mi355_tensor_get(None, t, buf, 0, 64) == -4
+    assert L.mi355_tensor_memset(None, t, 0, 0, 64) == -4
+    assert L.mi355_buffer_base(None) is None and L.mi355_buffer_size(None) == 0
+    L.mi355_buffer_free(None)  # no-op
+
+
+def test_capi_program_without_gpu_fails_cleanly(mi):
+    """The torch-free C++ caller (tests/native/capi_check) builds against the
+    header; where no GPU is visible it reports that and exits with 2."""
+    import os
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    subprocess.run(["make", "-s", "-C", os.path.join(root, "tests", "native")], check=True)
+    r = subprocess.run([os.path.join(root, "tests", "native", "capi_check"),
+                        os.path.join(root, "tests", "golden", "capi_fixture.bin")], capture_output=True, text=True,
+                       timeout=120)
+    if r.returncode == 0:  # a GPU is visible: the program ran its checks
+        assert "capi_check ok" in r.stdout
+    else:
+        assert r.returncode == 2 and "mi355_context_create" in r.stderr, (r.returncode, r.stdout, r.stderr)
