@@ -136,6 +136,23 @@ int mi355_supports_mul_mat(const mi355_tensor* src0, const mi355_tensor* src1, c
 mi355_status mi355_mul_mat(mi355_context* ctx, const mi355_tensor* src0, const mi355_tensor* src1,
                            const mi355_tensor* dst);
 
+/* ---- MUL_MAT without allocation (no counterpart in the reference; for
+ * callers that cannot allocate device memory: code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc) ----------------------
+ * The same operation, checks and kernels as mi355_mul_mat, with the same
+ * results.  Its scratch (the converted src1, split-K partial sums, the
+ * 4-byte-pitch weight copy) lives in a fixed device array of
+ * MI355_NOALLOC_SCRATCH_BYTES per GPU, held from library load until the
+ * process ends, instead of the context's workspace; the call allocates and
+ * frees nothing and records no timing events.  Operands needing more scratch
+ * than that (mi355_mul_mat_workspace_size) are rejected with
+ * MI355_STATUS_UNSUPPORTED.  Every call on one GPU uses that GPU's one array,
+ * so calls that overlap on a GPU (several streams, contexts or host threads)
+ * race: serialize them. */
+#define MI355_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+mi355_status mi355_mul_mat_noalloc(mi355_context* ctx, const mi355_tensor* src0, const mi355_tensor* src1,
+                                   const mi355_tensor* dst);
+
 /* ---- activation quantize (ggml-cpu type_traits[vec_dot_type].from_float,
  * the src1 conversion step of MUL_MAT; quantize_row_q8_0/q8_1, F16 convert).
  * Converts every row (ne[0] elements, rows over ne[1..3]) of the F32 tensor

@@ -143,6 +143,7 @@ def lib():
         "mi355_supports_flash_attn_ext": (I, [T, T, T, T, F, F, T]),
         "mi355_supports_soft_max_ext": (I, [T, T, F, T]),
         "mi355_mul_mat": (I, [P, T, T, T]),
+        "mi355_mul_mat_noalloc": (I, [P, T, T, T]),
         "mi355_quantize_rows": (I, [P, I, I, T, P]),
         "mi355_quantize_weights": (I, [P, I, T, P]),
         "mi355_model_quantize": (I, [P, C.c_char_p, C.c_char_p, C.c_int32, C.POINTER(QuantizeStats)]),
@@ -338,6 +339,10 @@ class Context:
 
     def mul_mat(self, src0: Tensor, src1: Tensor, dst: Tensor):
         self._check(self.L.mi355_mul_mat(self.h, C.byref(src0), C.byref(src1), C.byref(dst)))
+
+    def mul_mat_noalloc(self, src0: Tensor, src1: Tensor, dst: Tensor):
+        """mi355_mul_mat_noalloc: mi355_mul_mat with the library's fixed device scratch."""
+        self._check(self.L.mi355_mul_mat_noalloc(self.h, C.byref(src0), C.byref(src1), C.byref(dst)))
 
     def mul_mat_block_dots(self, src0: Tensor, src1: Tensor, isums_ptr: int):
         self._check(self.L.mi355_mul_mat_block_dots(self.h, C.byref(src0), C.byref(src1), C.c_void_p(isums_ptr)))

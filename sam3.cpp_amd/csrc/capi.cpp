@@ -501,6 +501,11 @@ mi355_status mi355_context_create(int device, void* stream, mi355_context** out)
     ctx->device = device;
     ctx->stream = static_cast<hipStream_t>(stream);  // NULL: the device's default stream
     ctx->cus = device_cus(device);
+    // the no-allocation entry point's fixed scratch on this device (resolved once per device)
+    if (noalloc_scratch_init(ctx) != MI355_STATUS_SUCCESS) {
+        ctx->scratch_error = ctx->last_error;
+        ctx->last_error.clear();
+    }
     *out = ctx;
     return MI355_STATUS_SUCCESS;
 }
@@ -553,6 +558,25 @@ mi355_status mi355_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
     st = ensure_ws(ctx, pl.total());
     if (st != MI355_STATUS_SUCCESS) return st;
     return mul_mat_run(ctx, s0, s1, d, pl, static_cast<char*>(ctx->ws), true);
+}
+
+mi355_status mi355_mul_mat_noalloc(mi355_context* ctx, const mi355_tensor* s0, const mi355_tensor* s1,
+                                   const mi355_tensor* d) {
+    mi355_status st = check_mul_mat(ctx, s0, s1, d);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "mul_mat_noalloc: null context");
+    (void)hipSetDevice(ctx->device);
+    if (s0->ne[0] == 0 || s0->ne[1] == 0 || s1->ne[1] == 0 || s1->ne[2] * s1->ne[3] == 0) return MI355_STATUS_SUCCESS;
+    if (s0->type == T_F32) return mul_mat_f32(ctx, s0, s1, d, false);
+    if (!ctx->scratch)
+        return fail(ctx, MI355_STATUS_FAILED, "mul_mat_noalloc: no static scratch on device %d (%s)", ctx->device,
+                    ctx->scratch_error.c_str());
+    const MmPlan pl = mm_plan(s0, s1, ctx->cus, dst_split_ok(d));
+    if (pl.total() > MI355_NOALLOC_SCRATCH_BYTES)
+        return fail(ctx, MI355_STATUS_UNSUPPORTED,
+                    "mul_mat_noalloc: these operands need %zu bytes of scratch, the static scratch holds %zu",
+                    pl.total(), (size_t)MI355_NOALLOC_SCRATCH_BYTES);
+    return mul_mat_run(ctx, s0, s1, d, pl, static_cast<char*>(ctx->scratch), false);
 }
 
 mi355_status mi355_mul_mat_block_dots(mi355_context* ctx, const mi355_tensor* s0, const mi355_tensor* s1,

@@ -21,6 +21,10 @@ struct mi355_context {
     size_t enc_size = 0;
     void* neck = nullptr;      // maps and scratch of the SimpleFPN neck
     size_t neck_size = 0;
+    // device address of the no-allocation entry point's static scratch on this
+    // context's device (null if it could not be resolved: scratch_error says why)
+    void* scratch = nullptr;
+    std::string scratch_error;
     std::string last_error;
     // encoder runners: producer passes write the next MUL_MAT's operand
     bool fuse = true;
@@ -70,6 +74,11 @@ mi355_status flash_attn_act(mi355_context* ctx, const mi355_tensor* q, const mi3
 // mul_mat_act with a fused epilogue (residual or qkv split); dst [M][N] never
 // exists.
 mi355_status mul_mat_epi(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const MmqEpi& e);
+
+// Resolves the device address of the static scratch array of
+// mi355_mul_mat_noalloc on ctx's device (current) into ctx->scratch; the
+// lookup runs once per device.
+mi355_status noalloc_scratch_init(mi355_context* ctx);
 
 // Brackets one launch with events when timing is enabled.
 struct Timed {
