@@ -477,6 +477,21 @@ mi355_status mi355_context_set_fusion(mi355_context* ctx, int enable);
  * routes them to the tiled kernel (for comparisons). */
 mi355_status mi355_context_set_skinny(mi355_context* ctx, int enable);
 
+/* The kernel behind 2-D MUL_MATs with Q8_0 / Q4_0 / Q4_1 weights (no
+ * counterpart in the reference).  All give the same bits: the exact int32
+ * block sums combined as acc = fma(isum, d_a * d_w, acc) in block order.
+ * - MI355_MMQ_F16: fp16 MFMAs over the quants as exact halves, weights used in
+ *   their ggml rows and decoded in registers;
+ * - MI355_MMQ_INT8: src1 quantized to one-byte quants, weights repacked into
+ *   int8 rows with separate scale arrays on each call, block sums on
+ *   v_mfma_i32_32x32x32_i8 (one VALU conversion per output and block more).
+ * Other MUL_MATs keep MI355_MMQ_F16. */
+typedef enum {
+    MI355_MMQ_F16 = 0,
+    MI355_MMQ_INT8 = 1,
+} mi355_mmq_kernel;
+mi355_status mi355_context_set_mmq_kernel(mi355_context* ctx, int kernel);
+
 /* ---- Kernel timing --------------------------------------------------------
  * The device-side counterpart of the reference's timing around graph compute
  * (std::chrono, sam3.cpp:6122-6135) and of its per-op micro-bench

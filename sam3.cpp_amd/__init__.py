@@ -25,6 +25,7 @@ HEADER = os.path.join(ROOT, "include", "sam3_mi355.h")
 
 F32, F16, Q4_0, Q4_1, Q8_0, Q8_1 = 0, 1, 2, 3, 8, 9
 ACT_X86, ACT_REF = 0, 1
+MMQ_F16, MMQ_INT8 = 0, 1
 TYPE_SIZE = {F32: 4, F16: 2, Q4_0: 18, Q4_1: 20, Q8_0: 34, Q8_1: 36}
 BLCK = {F32: 1, F16: 1, Q4_0: 32, Q4_1: 32, Q8_0: 32, Q8_1: 32}
 
@@ -167,6 +168,7 @@ def lib():
                                    C.POINTER(P)]),
         "mi355_context_set_fusion": (I, [P, I]),
         "mi355_context_set_skinny": (I, [P, I]),
+        "mi355_context_set_mmq_kernel": (I, [P, I]),
         "mi355_hiera_pos_embed": (I, [P, P, I, I, I, P, I, I, I, P]),
         "mi355_neck_workspace_size": (SZ, [I, I, C.POINTER(NeckScale)]),
         "mi355_sam3_neck": (I, [P, P, I, I, C.POINTER(NeckScale), C.POINTER(P)]),
@@ -430,6 +432,13 @@ class Context:
     def set_fusion(self, enable: bool):
         """Encoder runners: producer passes write the MUL_MAT operand (default) or f32 rows."""
         self._check(self.L.mi355_context_set_fusion(self.h, 1 if enable else 0))
+
+    def set_mmq_kernel(self, kernel: int):
+        """Kernel of 2-D quantized MUL_MATs: MMQ_F16 (0) or MMQ_INT8 (1); same bits."""
+        self._check(self.L.mi355_context_set_mmq_kernel(self.h, int(kernel)))
+
+    def set_mmq_int8(self, on: bool):
+        self.set_mmq_kernel(MMQ_INT8 if on else MMQ_F16)
 
     def set_skinny(self, on: bool):
         self._check(self.L.mi355_context_set_skinny(self.h, 1 if on else 0))

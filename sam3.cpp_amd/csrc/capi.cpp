@@ -111,16 +111,20 @@ bool f16_src1_direct(const mi355_tensor* s1) {
            (reinterpret_cast<uintptr_t>(s1->data) & 15) == 0;
 }
 
-// Workspace carve-up of one mul_mat: activation operand (fp16 quants or an
-// F16 copy of src1) | scales | Q8_1 sums | 4-byte-pitch weight copy (only
-// for weight rows that are not 4-byte aligned).
 // Workspace of one MUL_MAT: activation operand (q, d, s), the 4-byte-pitch
 // weight copy, then the split-K partial sums.
 struct MmPlan {
     size_t q = 0, d = 0, s = 0, align = 0, part = 0;
     int ks = 1;
+    bool i8 = false;   // int8-MFMA path: q holds int8 quants, align the repacked weights
     size_t total() const { return q + d + s + align + part; }
 };
+
+// The int8-MFMA kernel takes plain 2-D GEMMs with block-quantized weights.
+bool mm_i8_eligible(const mi355_tensor* s0, const mi355_tensor* s1) {
+    return (s0->type == T_Q8_0 || s0->type == T_Q4_0 || s0->type == T_Q4_1) && s0->ne[2] == 1 && s0->ne[3] == 1 &&
+           s1->ne[2] == 1 && s1->ne[3] == 1 && s0->ne[0] % 32 == 0;
+}
 
 int device_cus(int device) {
     int n = 0;
@@ -128,13 +132,23 @@ int device_cus(int device) {
     return n;
 }
 
-// split = false: the caller's dst cannot take the float4 stores of the split reduction
-MmPlan mm_plan(const mi355_tensor* s0, const mi355_tensor* s1, int cus, bool split = true) {
+// split = false: the caller's dst cannot take the float4 stores of the split reduction;
+// kernel: the MI355_MMQ_* route when the operands are eligible for it
+MmPlan mm_plan(const mi355_tensor* s0, const mi355_tensor* s1, int cus, bool split = true, int kernel = 0) {
+    const bool i8 = kernel == MI355_MMQ_INT8;
     MmPlan pl;
     if (s0->type == T_F32) return pl;
     const int64_t K = s1->ne[0], M = s1->ne[1], Z = s1->ne[2] * s1->ne[3];
     if (split) pl.ks = mmq_ksplit(s0->type, M, s0->ne[1], K, Z, cus);
     if (pl.ks > 1) pl.part = align_up((size_t)pl.ks * (size_t)M * (size_t)s0->ne[1] * 4);
+    if (i8 && mm_i8_eligible(s0, s1)) {
+        pl.i8 = true;
+        pl.q = align_up((size_t)(M * K));
+        pl.d = align_up((size_t)(M * mmq_scale_pitch(K)) * 4);  // dl and dh dwords
+        if (s0->type == T_Q4_1) pl.s = align_up((size_t)(M * mmq_scale_pitch(K)) * 2);
+        pl.align = align_up(wrep_bytes(s0->type, s0->ne[1], K));
+        return pl;
+    }
     if (s0->type == T_F16) {
         if (!f16_src1_direct(s1)) pl.q = align_up((size_t)(Z * M * ((K + 7) & ~7)) * 2);
         pl.align = align_up(mmq_align_bytes(matw_of(s0), s0->ne[1], K));
@@ -233,6 +247,21 @@ mi355_status prep_act_q8(mi355_context* ctx, const mi355_tensor* s0, const mi355
                      "quantize_mmq launch");
 }
 
+// The int8 activation operand's carve-up of a workspace planned with pl.i8:
+// quants [M][K], then dl and dh [M][nst], then the Q8_1 sums [M][2 nst].
+ActI8 act_i8(char* ws, const MmPlan& pl, int wtype, int64_t M, int64_t K) {
+    ActI8 a;
+    a.q = ws;
+    a.s1 = K;
+    a.nst = mmq_scale_pitch(K) / 2;
+    a.dl = reinterpret_cast<const uint32_t*>(ws + pl.q);
+    a.dh = a.dl + M * a.nst;
+    a.s = wtype == T_Q4_1 ? ws + pl.q + pl.d : nullptr;
+    a.M = M;
+    a.K = K;
+    return a;
+}
+
 // MUL_MAT of validated operands with the workspace ws (at least
 // mm_plan(...).total() bytes): the activation conversion, then the GEMM.
 // timed = false: no timing events (the no-allocation entry point).
@@ -241,6 +270,34 @@ mi355_status mul_mat_run(mi355_context* ctx, const mi355_tensor* s0, const mi355
     mi355_context* tctx = timed ? ctx : nullptr;
     const int64_t K = s0->ne[0], N = s0->ne[1], M = s1->ne[1];
     mi355_status st;
+    if (pl.i8) {
+        // weights -> int8 rows + scale arrays, src1 -> int8 quants + scales, then the int8-MFMA GEMM
+        WRep wr;
+        {
+            Timed tr(tctx, "repack_weights");
+            st = hip_check(ctx, tr.done(launch_repack_weights(matw_of(s0), N, K, ws + pl.q + pl.d + pl.s, &wr,
+                                                              ctx->stream)),
+                           "repack_weights launch");
+            if (st != MI355_STATUS_SUCCESS) return st;
+        }
+        const ActI8 a8 = act_i8(ws, pl, s0->type, M, K);
+        {
+            Timed tq8(tctx, "quantize_mmq_i8");
+            st = hip_check(ctx, tq8.done(launch_quantize_mmq_i8(view_of(s1), s0->type == T_Q4_1, K, 2 * a8.nst,
+                                                                reinterpret_cast<int8_t*>(ws),
+                                                                reinterpret_cast<uint16_t*>(ws + pl.q),
+                                                                reinterpret_cast<uint16_t*>(const_cast<void*>(a8.s)),
+                                                                ctx->stream)),
+                           "quantize_mmq_i8 launch");
+            if (st != MI355_STATUS_SUCCESS) return st;
+        }
+        if (!mmq8_supported(wr, a8)) return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat: operands beyond the int8 kernel");
+        const MmqSplit sp8{pl.ks, pl.ks > 1 ? reinterpret_cast<float*>(ws + pl.q + pl.d + pl.s + pl.align) : nullptr,
+                           false};
+        const char* kname = s0->type == T_Q8_0 ? "mmq8_q8_0" : s0->type == T_Q4_0 ? "mmq8_q4_0" : "mmq8_q4_1";
+        Timed tk(tctx, kname);
+        return hip_check(ctx, tk.done(launch_mmq8(wr, a8, matd_of(d), nullptr, sp8, ctx->stream)), "mmq8 launch");
+    }
     ActF16 a;
     if (s0->type == T_F16) {
         a.M = M;
@@ -554,7 +611,7 @@ mi355_status mi355_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
     (void)hipSetDevice(ctx->device);
     if (s0->ne[0] == 0 || s0->ne[1] == 0 || s1->ne[1] == 0 || s1->ne[2] * s1->ne[3] == 0) return MI355_STATUS_SUCCESS;
     if (s0->type == T_F32) return mul_mat_f32(ctx, s0, s1, d, true);
-    const MmPlan pl = mm_plan(s0, s1, ctx->cus, dst_split_ok(d));
+    const MmPlan pl = mm_plan(s0, s1, ctx->cus, dst_split_ok(d), ctx->mmq_kernel);
     st = ensure_ws(ctx, pl.total());
     if (st != MI355_STATUS_SUCCESS) return st;
     return mul_mat_run(ctx, s0, s1, d, pl, static_cast<char*>(ctx->ws), true);
@@ -571,7 +628,7 @@ mi355_status mi355_mul_mat_noalloc(mi355_context* ctx, const mi355_tensor* s0, c
     if (!ctx->scratch)
         return fail(ctx, MI355_STATUS_FAILED, "mul_mat_noalloc: no static scratch on device %d (%s)", ctx->device,
                     ctx->scratch_error.c_str());
-    const MmPlan pl = mm_plan(s0, s1, ctx->cus, dst_split_ok(d));
+    const MmPlan pl = mm_plan(s0, s1, ctx->cus, dst_split_ok(d), ctx->mmq_kernel);
     if (pl.total() > MI355_NOALLOC_SCRATCH_BYTES)
         return fail(ctx, MI355_STATUS_UNSUPPORTED,
                     "mul_mat_noalloc: these operands need %zu bytes of scratch, the static scratch holds %zu",
@@ -599,9 +656,26 @@ mi355_status mi355_mul_mat_block_dots(mi355_context* ctx, const mi355_tensor* s0
     if (st != MI355_STATUS_SUCCESS) return st;
     if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "block_dots: null context");
     (void)hipSetDevice(ctx->device);
-    const MmPlan pl = mm_plan(s0, s1, ctx->cus, false);
+    const MmPlan pl = mm_plan(s0, s1, ctx->cus, false, ctx->mmq_kernel);
     st = ensure_ws(ctx, pl.total());
     if (st != MI355_STATUS_SUCCESS) return st;
+    if (pl.i8) {
+        char* ws = static_cast<char*>(ctx->ws);
+        const int64_t K = s0->ne[0], M = s1->ne[1];
+        WRep wr;
+        st = hip_check(ctx, launch_repack_weights(matw_of(s0), s0->ne[1], K, ws + pl.q + pl.d + pl.s, &wr, ctx->stream),
+                       "repack_weights launch");
+        if (st != MI355_STATUS_SUCCESS) return st;
+        const ActI8 a8 = act_i8(ws, pl, s0->type, M, K);
+        st = hip_check(ctx, launch_quantize_mmq_i8(view_of(s1), s0->type == T_Q4_1, K, 2 * a8.nst, reinterpret_cast<int8_t*>(ws),
+                                                   reinterpret_cast<uint16_t*>(ws + pl.q),
+                                                   reinterpret_cast<uint16_t*>(const_cast<void*>(a8.s)), ctx->stream),
+                       "quantize_mmq_i8 launch");
+        if (st != MI355_STATUS_SUCCESS) return st;
+        return hip_check(ctx, launch_mmq8(wr, a8, MatD{nullptr, 0, 0, 0}, nullptr, MmqSplit{1, nullptr}, ctx->stream,
+                                          isums),
+                         "mmq8(dots) launch");
+    }
     ActF16 a;
     st = prep_act_q8(ctx, s0, s1, pl, static_cast<char*>(ctx->ws), true, a);
     if (st != MI355_STATUS_SUCCESS) return st;
@@ -677,6 +751,14 @@ mi355_status mi355_soft_max_ext(mi355_context* ctx, const mi355_tensor* src, con
 mi355_status mi355_context_set_fusion(mi355_context* ctx, int enable) {
     if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "set_fusion: null context");
     ctx->fuse = enable != 0;
+    return MI355_STATUS_SUCCESS;
+}
+
+mi355_status mi355_context_set_mmq_kernel(mi355_context* ctx, int kernel) {
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "set_mmq_kernel: null context");
+    if (kernel != MI355_MMQ_F16 && kernel != MI355_MMQ_INT8)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "set_mmq_kernel: unknown kernel %d", kernel);
+    ctx->mmq_kernel = kernel;
     return MI355_STATUS_SUCCESS;
 }
 

@@ -30,6 +30,8 @@ struct mi355_context {
     bool fuse = true;
     // MUL_MATs with K <= 128 at large M take the skinny kernel
     bool skinny = true;
+    // kernel of 2-D MUL_MATs with block-quantized weights (MI355_MMQ_*)
+    int mmq_kernel = 0;
     // kernel timing
     bool prof = false;
     struct Pending { const char* name; hipEvent_t a, b; };

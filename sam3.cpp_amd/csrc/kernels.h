@@ -120,6 +120,51 @@ struct MmqEpi {
 };
 hipError_t launch_mmq_epi(const MatW& w, const ActF16& a, int64_t N, const MmqEpi& e, void* align_buf,
                           const MmqSplit& sp, hipStream_t st);
+// The split-K reduction: dst rows (or the epilogue) from ks partial sums [ks][M][N] f32 in split order.
+hipError_t launch_mmq_reduce(const float* part, int ks, int M, int N, char* dst, int64_t d_nb1, const MmqEpi* epi,
+                             hipStream_t st);
+
+// ---- int8-MFMA MUL_MAT (mmq8.hip)
+// Activation operand with one-byte quants: q int8 [M][s1 bytes] (s1 a
+// multiple of 16); the scales split by block parity into the operands of the
+// kernel's scale MFMA; Q8_1 sums fp16 [M][2 nst] as ActF16's.
+struct ActI8 {
+    const void* q;        // int8 [M][s1]
+    int64_t s1;
+    const uint32_t* dl;   // [M][nst]: d of block 2s in the low half of dword s (high half zero)
+    const uint32_t* dh;   // [M][nst]: d of block 2s + 1 in the high half (low half zero)
+    const void* s;        // fp16 [M][2 nst] Q8_1 sums (Q4_1 weights)
+    int64_t nst;          // mmq_scale_pitch(K) / 2
+    int64_t M, K;
+};
+// Weights repacked for the int8 kernel: quants int8 [N][q_s1 bytes] (Q8_0 as
+// stored, Q4_0 as nibble - 8, Q4_1 as the nibble 0..15), d (and Q4_1's m) fp16
+// [N][dpw], dpw = mmq_scale_pitch(K) with a zero padding slot.
+struct WRep {
+    int type;
+    int8_t* q;
+    int64_t q_s1;
+    _Float16* d;
+    _Float16* m;
+    int dpw;
+    int64_t N, K;
+};
+// Bytes of the repacked form of N rows of K elements (0: not a repackable type).
+size_t wrep_bytes(int type, int64_t N, int64_t K);
+// Repacks the 2-D ggml weights w (rows at w.data + n * w.nb1) into dst (wrep_bytes) and describes it in *out.
+hipError_t launch_repack_weights(const MatW& w, int64_t N, int64_t K, void* dst, WRep* out, hipStream_t st);
+// Operands the int8 kernel takes (alignment, pitches, 32-bit buffer offsets).
+bool mmq8_supported(const WRep& w, const ActI8& a);
+// dst = W^T . A (2-D) on int8 MFMA, bit-identical to launch_mmq on the same
+// operands; epilogues and split-K as launch_mmq / launch_mmq_epi.
+// With dots != nullptr the kernel writes the exact int32 block sums [M][N][K/32] instead.
+hipError_t launch_mmq8(const WRep& w, const ActI8& a, const MatD& d, const MmqEpi* epi, const MmqSplit& sp,
+                       hipStream_t st, int32_t* dots = nullptr);
+// from_float (x86 variant) into the int8 operand layout: q [rows][s1] int8,
+// d -> dl [rows][dp / 2] followed by dh [rows][dp / 2] (uint32), s as ActF16's.
+hipError_t launch_quantize_mmq_i8(const SrcView& src, bool with_sum, int64_t s1, int64_t dp, int8_t* q, uint16_t* d,
+                                  uint16_t* s, hipStream_t st);
+
 
 // Row softmax of scale*x (F32, strided rows) into dst (F32, strided rows).
 hipError_t launch_soft_max(const SrcView& src, float scale, char* dst, const int64_t dnb[4], hipStream_t st);

@@ -1126,6 +1126,19 @@ static hipError_t run_mmq(const MatW& w_in, const ActF16& a, const MatD& d, int6
     return hipGetLastError();
 }
 
+hipError_t launch_mmq_reduce(const float* part, int ks, int M, int N, char* D, int64_t d_nb1, const MmqEpi* epi,
+                             hipStream_t st) {
+    const int64_t n = (int64_t)M * (N / 4);
+    const unsigned g = (unsigned)((n + 255) / 256);
+    if (!epi || epi->kind == MMQ_EPI_STORE)
+        mmq_reduce_kernel<MMQ_EPI_STORE><<<g, 256, 0, st>>>(part, ks, M, N, D, d_nb1, MmqEpi{});
+    else if (epi->kind == MMQ_EPI_RESIDUAL)
+        mmq_reduce_kernel<MMQ_EPI_RESIDUAL><<<g, 256, 0, st>>>(part, ks, M, N, D, 0, *epi);
+    else
+        mmq_reduce_kernel<MMQ_EPI_QKV><<<g, 256, 0, st>>>(part, ks, M, N, D, 0, *epi);
+    return hipGetLastError();
+}
+
 hipError_t launch_mmq(const MatW& w, const ActF16& a, const MatD& d, int64_t N, int64_t ne12, int64_t ne13,
                       int32_t* dots, void* align_buf, const MmqSplit& sp, hipStream_t st) {
     if (sp.ks > 1 && (d.nb1 % 16 != 0 || (reinterpret_cast<uintptr_t>(d.data) & 15) != 0)) return hipErrorInvalidValue;

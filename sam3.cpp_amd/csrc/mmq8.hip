@@ -1,0 +1,562 @@
+// ggml MUL_MAT on gfx950 with int8 MFMA: Q8_0 / Q4_0 / Q4_1 weights against
+// Q8_0 / Q8_1-quantized activations, both operands one byte per element.
+//
+//   dst[m][n] = sum_b fp32(d_w[n][b]) * fp32(d_a[m][b]) * isum[m][n][b]
+//               (+ sum_b fp32(m_w[n][b]) * fp32(s_a[m][b]) for Q4_1)
+//   isum[m][n][b] = sum_{j<32} q_w[n][32b+j] * q_a[m][32b+j]     (exact int32)
+//
+// One v_mfma_i32_32x32x32_i8 gives a 32x32 tile's isum of one block with
+// int32 accumulation.  The scale product d_a (x) d_w of the tile is one
+// fp16 MFMA (an outer product in k-slot 0; fp16 x fp16 is exact in fp32),
+// and the combine is acc = fma(float(isum), S, acc) in block order: the same
+// fp32 operations in the same order as mmq_kernel, whose fp16 MFMAs over
+// integer-valued halves give the same exact isum, so the two kernels' outputs
+// are bit-identical.  Q4_1's offset term is accumulated into acc by one
+// MFMA per stage before the stage's blocks, as mmq_kernel does.
+//
+// Operands (the int8 layouts, kernels.h ActI8 / WRep): activation quants
+// int8 [M][K] with fp16 scales (and Q8_1 sums) [M][dp]; weights repacked
+// once into int8 quants [N][K] (Q8_0 as stored, Q4_0 as nibble - 8, Q4_1 as
+// the nibble) with fp16 d (and m) [N][dpw].  Rows are 16-byte aligned, so
+// every stage moves by buffer_load_dwordx4 ... lds (LDS DMA): 1 KB per
+// wavefront instruction, no staging registers, no decode in the K loop.
+//
+// Tiling: workgroup 128(m) x 128(n), four wavefronts in 2 x 2, each 64 x 64
+// (2 x 2 MFMA tiles).  K advances 64 bytes (two blocks) per stage through
+// three LDS stages filled two stages ahead.  A tile row is 64 bytes = four
+// 16-byte chunks; chunk c of row r sits in slot c ^ ((r >> 2) & 3), so the 16
+// consecutive rows one ds_read_b128 pass serves cover all 64 banks.
+#include <type_traits>
+
+#include "common.cuh"
+#include "kernels.h"
+
+namespace mi355 {
+
+namespace {
+constexpr int B8M = 128, B8N = 128, SKB = 64;  // tile rows, tile columns, K bytes per stage
+constexpr int NT8 = 256;
+constexpr int OOB8 = 0x40000000;
+}  // namespace
+
+struct Mmq8Args {
+    const int8_t* A;       // [M][K] activation quants, row stride a_s1 bytes (multiple of 16)
+    int64_t a_s1;
+    const uint32_t* Adl;   // [M][nst] d_a of block 2s in the low half of dword s
+    const uint32_t* Adh;   // [M][nst] d_a of block 2s + 1 in the high half
+    const _Float16* As;    // [M][2 nst] Q8_1 sums (Q4_1)
+    const int8_t* W;       // [N][K] repacked weight quants, row stride w_s1 bytes (multiple of 16)
+    int64_t w_s1;
+    const _Float16* Wd;    // [N][2 nst] weight scales (dword s = blocks 2s, 2s+1)
+    const _Float16* Wm;    // [N][2 nst] Q4_1 minima
+    float* D;
+    int64_t d_nb1;         // bytes
+    int M, N, K, nst, tiles_m, tiles_n, gm;
+    int ksplit, sps;       // K split into ksplit ranges of sps stages (partial sums at D + split * d_split)
+    int64_t d_split;
+    int d_v4;              // float4 row stores through LDS
+    int32_t* dots;         // block-dot inspection output [M][N][nbt] (or null)
+    int nbt;               // blocks per row of the whole K
+};
+
+template <int WT>
+struct St8 {
+    static constexpr bool Q41 = WT == T_Q4_1;
+    int8_t A[B8M * SKB];
+    int8_t W[B8N * SKB];
+    uint32_t adl[B8M];         // d_a of the stage's block 0 per row (low half)
+    uint32_t adh[B8M];         // d_a of block 1 per row (high half)
+    uint32_t wd[B8N];          // d_w of blocks 0, 1 per row
+    uint32_t as[Q41 ? B8M : 1];
+    uint32_t wm[Q41 ? B8N : 1];
+    uint32_t zero[4];          // read by lanes 32..63 for the scale MFMA's B operand
+};
+
+__device__ __forceinline__ int slot8(int r, int c) { return c ^ ((r >> 2) & 3); }
+
+// Per-stage pipeline (three LDS buffers, DMA three stages ahead):
+//   units of block 0 (fragments prefetched in registers)
+//   wait for stage s+1's DMA, barrier: every wavefront has also finished
+//     reading stage s's buffer, which is refilled with stage s+3
+//   prefetch stage s+1's block-0 fragments; units of block 1;
+//   prefetch stage s+1's block-1 fragments.
+// A unit (block, m-tile, n-tile) issues its scale MFMA and isum MFMA into
+// buffer u % 2 and combines the previous unit (across stage boundaries).
+template <int WT, int EPI, bool DOTS = false>
+__global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const MmqEpi e) {
+    using St = St8<WT>;
+    constexpr bool Q41 = WT == T_Q4_1;
+    __shared__ __attribute__((aligned(16))) St st0;
+    __shared__ __attribute__((aligned(16))) St st1;
+    __shared__ __attribute__((aligned(16))) St st2;
+
+    // XCD-aware, grouped tile order (as mmq_kernel): each XCD walks a contiguous band
+    const int TT = p.tiles_m * p.tiles_n * p.ksplit;
+    const int per_xcd = (TT + 7) / 8;
+    const int tl = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tl >= TT) return;
+    const int t = tl / p.ksplit, split = tl - t * p.ksplit;
+    const int gsz = p.gm * p.tiles_n, grp = t / gsz, gr = t - grp * gsz;
+    const int gmr = min(p.gm, p.tiles_m - grp * p.gm);
+    const int m0 = (grp * p.gm + gr % gmr) * B8M, n0 = (gr / gmr) * B8N;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int M = p.M, N = p.N;
+    const int kb0 = split * p.sps * SKB;        // first K byte of this split
+    const int K = min(p.K - kb0, p.sps * SKB);  // K bytes (elements) of this split
+    const int nstage = (K / QK + 1) / 2;
+    const int so0 = kb0 / SKB;                  // first stage (scale dword) of this split
+    const int8_t* Az = p.A + kb0;
+    const int8_t* Wz = p.W + kb0;
+    const int64_t a_ext = (int64_t)(M - 1) * p.a_s1 + p.K - kb0;
+    const int64_t w_ext = (int64_t)(N - 1) * p.w_s1 + p.K - kb0;
+    const int64_t sa_ext = 4LL * M * p.nst - 4LL * so0, sw_ext = 4LL * N * p.nst - 4LL * so0;
+
+    if (tid < 4) st0.zero[tid] = st1.zero[tid] = st2.zero[tid] = 0u;
+
+    // ---- DMA offsets (fixed for the whole K loop)
+    // tile instruction i of wavefront w: rows (2w + i) * 16 + lane / 4, LDS slot lane % 4
+    int aoff[2], woff[2], tch[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int row = (2 * w + i) * 16 + (lane >> 2);
+        tch[i] = slot8(row, lane & 3);  // global chunk loaded into this lane's slot
+        aoff[i] = m0 + row < M ? (int)((int64_t)(m0 + row) * p.a_s1) + tch[i] * 16 : OOB8;
+        woff[i] = n0 + row < N ? (int)((int64_t)(n0 + row) * p.w_s1) + tch[i] * 16 : OOB8;
+    }
+    // scale dwords: wavefronts 0, 1 load d_a (both halves) of rows 64 (w & 1) + lane, 2 and 3
+    // d_w (and for Q4_1 wavefronts 0, 1 the Q8_1 sums, 2 and 3 the minima)
+    const int srow = 64 * (w & 1) + lane;
+    const bool a_side = w < 2;
+    const int soff = a_side ? (m0 + srow < M ? (int)((int64_t)(m0 + srow) * p.nst * 4) : OOB8)
+                            : (n0 + srow < N ? (int)((int64_t)(n0 + srow) * p.nst * 4) : OOB8);
+    constexpr int NLA = 4 + 2 + (Q41 ? 1 : 0), NLW = 4 + 1 + (Q41 ? 1 : 0);  // DMA instructions per stage
+
+    auto dma_stage = [&](int s, St& b) __attribute__((always_inline)) {
+        const int k0 = s * SKB;
+        const bool tail = k0 + SKB > K;
+        const auto ar = make_rsrc(Az + k0, a_ext - k0);
+        const auto wr = make_rsrc(Wz + k0, w_ext - k0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const bool past = tail && k0 + tch[i] * 16 >= K;
+            dma_b128(ar, &b.A[(2 * w + i) * 16 * SKB], past ? OOB8 : aoff[i]);
+            dma_b128(wr, &b.W[(2 * w + i) * 16 * SKB], past ? OOB8 : woff[i]);
+        }
+        const int so = soff == OOB8 ? OOB8 : soff + 4 * s;
+        if (a_side) {
+            dma_b32(make_rsrc(p.Adl + so0, sa_ext), &b.adl[64 * (w & 1)], so);
+            dma_b32(make_rsrc(p.Adh + so0, sa_ext), &b.adh[64 * (w & 1)], so);
+            if (Q41) dma_b32(make_rsrc(p.As + 2 * so0, sa_ext), &b.as[Q41 ? 64 * (w & 1) : 0], so);
+        } else {
+            dma_b32(make_rsrc(p.Wd + 2 * so0, sw_ext), &b.wd[64 * (w & 1)], so);
+            if (Q41) dma_b32(make_rsrc(p.Wm + 2 * so0, sw_ext), &b.wm[Q41 ? 64 * (w & 1) : 0], so);
+        }
+    };
+    // wait until this wavefront's DMA of all but the last `later` stages issued has landed
+    auto wait_dma = [&](int later) __attribute__((always_inline)) {
+        if (a_side) {
+            if (later >= 2) wait_vmcnt<2 * NLA>();
+            else if (later == 1) wait_vmcnt<NLA>();
+            else wait_vmcnt<0>();
+        } else {
+            if (later >= 2) wait_vmcnt<2 * NLW>();
+            else if (later == 1) wait_vmcnt<NLW>();
+            else wait_vmcnt<0>();
+        }
+    };
+
+    const int wm = w & 1, wn = w >> 1;
+    const int lr = lane & 31, g = lane >> 5;
+    const bool lo = lane < 32;
+    // per-lane LDS offsets inside a stage buffer (the same for all three)
+    int ra_off[2], rw_off[2], sda[2], sdw[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = 64 * wm + 32 * i + lr, n = 64 * wn + 32 * i + lr;
+        ra_off[i] = r * SKB;
+        rw_off[i] = n * SKB;
+        sda[i] = r * 4;
+        // lanes 32..63 carry k-slots 8..15 of the scale MFMA: a zero B operand there
+        sdw[i] = lo ? (int)offsetof(St, wd) + n * 4 : (int)offsetof(St, zero);
+    }
+    v16f acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[a][c][i] = 0.0f;
+    const v16i zi = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const v16f zf = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+
+    // fragments of one block: the lane's 16 K bytes (chunk 2 bk + g) of its A and W rows, and
+    // the scale MFMA's A operand (d_a of the block in k-slot 0 or 1; the other slots meet zeros)
+    struct FragB {
+        v4i a[2], b[2];
+        v4i da[2];
+    };
+    auto load_blk = [&](const St& b, int bk, FragB& f) __attribute__((always_inline)) {
+        const char* base = reinterpret_cast<const char*>(&b);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            f.a[i] = *reinterpret_cast<const v4i*>(&b.A[ra_off[i] + slot8(ra_off[i] / SKB, 2 * bk + g) * 16]);
+            f.b[i] = *reinterpret_cast<const v4i*>(&b.W[rw_off[i] + slot8(rw_off[i] / SKB, 2 * bk + g) * 16]);
+            f.da[i][0] = *reinterpret_cast<const int*>(base + (bk ? offsetof(St, adh) : offsetof(St, adl)) + sda[i]);
+        }
+    };
+    // scale MFMA B operands of a stage: d_w of both blocks in k-slots 0, 1 (lanes 0..31)
+    auto load_dw = [&](const St& b, v4i (&dw)[2]) __attribute__((always_inline)) {
+        const char* base = reinterpret_cast<const char*>(&b);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) dw[i][0] = *reinterpret_cast<const int*>(base + sdw[i]);
+    };
+    auto apply = [&](v16f& a, const v16i& I, const v16f& S) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) a[i] = __builtin_fmaf((float)I[i], S[i], a[i]);
+    };
+
+    FragB f0, f1;
+    v4i dw[2], dwn[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        f0.da[i] = f1.da[i] = v4i{0, 0, 0, 0};
+        dw[i] = dwn[i] = v4i{0, 0, 0, 0};
+    }
+    v16i PI[2];
+    v16f PS[2];
+    for (int i = 0; i < 2; ++i) {
+        PI[i] = zi;
+        PS[i] = zf;
+    }
+
+    // prologue: stages 0..2 in flight, stage 0 published, its fragments in registers
+    dma_stage(0, st0);
+    if (nstage > 1) dma_stage(1, st1);
+    if (nstage > 2) dma_stage(2, st2);
+    wait_dma(min(nstage - 1, 2));
+    __syncthreads();  // also publishes the zero words
+    load_blk(st0, 0, f0);
+    load_blk(st0, 1, f1);
+    load_dw(st0, dw);
+
+    // units of one block of stage s: (mt, nt) = (0,0), (0,1), (1,0), (1,1); the previous unit's
+    // combine (buffer p2) runs behind this unit's MFMAs (buffer u2)
+    auto units = [&](int s, int bk, const FragB& f, const St& b, bool first) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int mt = q >> 1, nt = q & 1;
+            const int u2 = (bk * 4 + q) & 1, p2 = u2 ^ 1;
+            if (DOTS) {
+                const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mt], f.b[nt], zi, 0, 0, 0);
+                const int n = n0 + 64 * wn + 32 * nt + lr, blk = 2 * (so0 + s) + bk;
+                if (blk < p.nbt) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int m = m0 + 64 * wm + 32 * mt + 8 * (i >> 2) + 4 * g + (i & 3);
+                        if (m < M && n < N) p.dots[((int64_t)m * N + n) * p.nbt + blk] = I[i];
+                    }
+                }
+                continue;
+            }
+            if (Q41 && bk == 0) {
+                // acc += s_a (x) m_w over the stage's two blocks, before the stage's block terms
+                const int r = 64 * wm + 32 * mt + lr, n = 64 * wn + 32 * nt + lr;
+                const v4i saf = {(int)b.as[Q41 ? r : 0], 0, 0, 0};
+                const v4i mwf = {lo ? (int)b.wm[Q41 ? n : 0] : 0, 0, 0, 0};
+                acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, saf),
+                                                                     __builtin_bit_cast(v8h, mwf), acc[mt][nt], 0, 0, 0);
+            }
+            PS[u2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, f.da[mt]),
+                                                           __builtin_bit_cast(v8h, dw[nt]), zf, 0, 0, 0);
+            PI[u2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mt], f.b[nt], zi, 0, 0, 0);
+            if (!first || bk > 0 || q > 0) {
+                // previous unit: (bk, q - 1), or block 0's last unit, or the previous stage's last
+                const int pq = (q + 3) & 3;
+                apply(acc[pq >> 1][pq & 1], PI[p2], PS[p2]);
+                asm volatile("" : "+v"(acc[pq >> 1][pq & 1]));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // one stage: cur holds stage s (already in registers), nxt stage s + 1
+    auto stage = [&](int s, St& cur, St& nxt) __attribute__((always_inline)) {
+        units(s, 0, f0, cur, s == 0);
+        if (s + 1 < nstage) {
+            wait_dma(min(nstage - 2 - s, 1));
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (s + 3 < nstage) dma_stage(s + 3, cur);
+            load_blk(nxt, 0, f0);
+            load_dw(nxt, dwn);
+        }
+        units(s, 1, f1, cur, false);
+        if (s + 1 < nstage) {
+            load_blk(nxt, 1, f1);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) dw[i] = dwn[i];
+        }
+    };
+    for (int s = 0; s < nstage; s += 3) {
+        stage(s, st0, st1);
+        if (s + 1 < nstage) stage(s + 1, st1, st2);
+        if (s + 2 < nstage) stage(s + 2, st2, st0);
+    }
+    if (!DOTS) apply(acc[1][1], PI[1], PS[1]);  // the last unit (block 1, tile (1,1))
+    if (DOTS) return;
+    // ---- epilogue: the wavefront's 64 x 64 region, 32 rows (one m-tile) at a time
+    char* Dz = reinterpret_cast<char*>(p.D) + split * p.d_split;
+    if (EPI == MMQ_EPI_STORE && !p.d_v4) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int m = m0 + 64 * wm + 32 * mt + 8 * (i >> 2) + 4 * g + (i & 3);
+                    const int n = n0 + 64 * wn + 32 * nt + lr;
+                    if (m < M && n < N) *reinterpret_cast<float*>(Dz + (int64_t)m * p.d_nb1 + (int64_t)n * 4) = acc[mt][nt][i];
+                }
+        return;
+    }
+    constexpr int TP = 68;  // staging row pitch (floats): 64 columns + 4
+    static_assert(2 * 32 * TP * 4 <= (int)sizeof(St), "epilogue staging exceeds a stage buffer");
+    __syncthreads();  // every wavefront is done with the stage buffers
+    float* stg = reinterpret_cast<float*>(w < 2 ? &st0 : &st1) + (w & 1) * 32 * TP;
+    const int c4 = lane & 15;                 // this lane's float4 column chunk
+    const int nc = n0 + 64 * wn + 4 * c4;     // its first output column
+    const bool cv = nc < N;                   // N % 4 == 0 on the float4 paths
+    v4f bv = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (EPI != MMQ_EPI_STORE && cv) bv = *reinterpret_cast<const v4f*>(&e.bias[nc]);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) stg[(8 * (i >> 2) + 4 * g + (i & 3)) * TP + 32 * nt + lr] = acc[mt][nt][i];
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's LDS writes are done
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+            const int r = it * 4 + (lane >> 4);
+            const int m = m0 + 64 * wm + 32 * mt + r;
+            const v4f v = *reinterpret_cast<const v4f*>(&stg[r * TP + 4 * c4]);
+            if (m >= M || !cv) continue;
+            if (EPI == MMQ_EPI_STORE) {
+                *reinterpret_cast<v4f*>(Dz + (int64_t)m * p.d_nb1 + (int64_t)nc * 4) = v;
+            } else if (EPI == MMQ_EPI_RESIDUAL) {
+                const int rr = map_row32(e.map, m);
+                if (rr >= 0) {
+                    const v4f x = *reinterpret_cast<const v4f*>(&e.res[(int64_t)rr * N + nc]);
+                    *reinterpret_cast<v4f*>(&e.out[(int64_t)rr * N + nc]) = x + (v + bv);
+                }
+            } else {
+                const v4f uv = v + bv;
+                const int E = e.nh * e.hd, which = nc / E, col = nc - which * E, hh = col / e.hd, d = col - hh * e.hd;
+                _Float16* dst = which == 0 ? e.q : which == 1 ? e.k : e.v;
+                float u0 = uv[0], u1 = uv[1], u2 = uv[2], u3 = uv[3];
+                const int bw = m / e.ntok, tn = m - bw * e.ntok;
+                if (which < 2 && e.rope) {
+                    const v4f cs = *reinterpret_cast<const v4f*>(&e.rope[(int64_t)tn * e.hd + d]);
+                    rope_pair(u0, u1, cs[0], cs[1]);
+                    rope_pair(u2, u3, cs[2], cs[3]);
+                }
+                const uint32_t h0 = (uint32_t)f2h(u0) | ((uint32_t)f2h(u1) << 16);
+                const uint32_t h1 = (uint32_t)f2h(u2) | ((uint32_t)f2h(u3) << 16);
+                *reinterpret_cast<uint2*>(&dst[(((int64_t)bw * e.nh + hh) * e.ntok + tn) * e.hd + d]) =
+                    make_uint2(h0, h1);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // the reads are done before the next m-tile overwrites
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+    }
+}
+
+// ---- weight repack: ggml rows -> int8 quants [N][K] + fp16 d (and m) [N][dpw]
+// One thread per 32-element block.  Q8_0 quants are copied, Q4_0 nibbles
+// become q - 8, Q4_1 nibbles stay 0..15; the padding scale slot (dpw > nb) is
+// zero.  src rows at src + r * nb1 for r < rows (2-D weights; batched
+// weights arrive as consecutive row ranges).
+template <int WT>
+__global__ __launch_bounds__(256) void repack_weights_kernel(const uint8_t* __restrict__ src, int64_t nb1, int64_t rows,
+                                                             int64_t nbr, int dpw, int8_t* __restrict__ q,
+                                                             int64_t q_s1, _Float16* __restrict__ d,
+                                                             _Float16* __restrict__ mm) {
+    const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gi >= rows * nbr) return;
+    const int64_t r = gi / nbr, b = gi - r * nbr;
+    constexpr int BS = WT == T_Q8_0 ? 34 : WT == T_Q4_0 ? 18 : 20;
+    const uint8_t* blk = src + r * nb1 + b * BS;
+    uint32_t out[8];
+    if (WT == T_Q8_0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            out[j] = (uint32_t)blk[2 + 4 * j] | ((uint32_t)blk[3 + 4 * j] << 8) | ((uint32_t)blk[4 + 4 * j] << 16) |
+                     ((uint32_t)blk[5 + 4 * j] << 24);
+    } else {
+        constexpr int HDR = WT == T_Q4_0 ? 2 : 4;
+        uint32_t raw[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            raw[j] = (uint32_t)blk[HDR + 4 * j] | ((uint32_t)blk[HDR + 1 + 4 * j] << 8) |
+                     ((uint32_t)blk[HDR + 2 + 4 * j] << 16) | ((uint32_t)blk[HDR + 3 + 4 * j] << 24);
+        // element j < 16 is the low nibble of byte j, element j + 16 its high nibble
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t lo4 = raw[j] & 0x0f0f0f0fu, hi4 = (raw[j] >> 4) & 0x0f0f0f0fu;
+            if (WT == T_Q4_0) {  // per byte (n | 0x80) - 8, then ^ 0x80: n - 8 without borrows
+                lo4 = ((lo4 | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+                hi4 = ((hi4 | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+            }
+            out[j] = lo4;
+            out[4 + j] = hi4;
+        }
+    }
+    uint4* qd = reinterpret_cast<uint4*>(q + r * q_s1 + b * QK);
+    qd[0] = make_uint4(out[0], out[1], out[2], out[3]);
+    qd[1] = make_uint4(out[4], out[5], out[6], out[7]);
+    uint16_t dh, mh = 0;
+    __builtin_memcpy(&dh, blk, 2);
+    if (WT == T_Q4_1) __builtin_memcpy(&mh, blk + 2, 2);
+    reinterpret_cast<uint16_t*>(d)[r * dpw + b] = dh;
+    if (WT == T_Q4_1) reinterpret_cast<uint16_t*>(mm)[r * dpw + b] = mh;
+    if (b == nbr - 1 && dpw > nbr) {
+        reinterpret_cast<uint16_t*>(d)[r * dpw + nbr] = 0;
+        if (WT == T_Q4_1) reinterpret_cast<uint16_t*>(mm)[r * dpw + nbr] = 0;
+    }
+}
+
+size_t wrep_bytes(int type, int64_t N, int64_t K) {
+    if (!(type == T_Q8_0 || type == T_Q4_0 || type == T_Q4_1) || K % QK != 0) return 0;
+    const size_t dpw = (size_t)mmq_scale_pitch(K);
+    const size_t q = ((size_t)N * (size_t)K + 255) & ~(size_t)255;
+    const size_t d = ((size_t)N * dpw * 2 + 255) & ~(size_t)255;
+    return q + d * (type == T_Q4_1 ? 2 : 1);
+}
+
+hipError_t launch_repack_weights(const MatW& w, int64_t N, int64_t K, void* dst, WRep* out, hipStream_t st) {
+    if (!(w.type == T_Q8_0 || w.type == T_Q4_0 || w.type == T_Q4_1) || K % QK != 0 || !dst)
+        return hipErrorInvalidValue;
+    const int64_t nbr = K / QK;
+    const int dpw = (int)mmq_scale_pitch(K);
+    const size_t q = ((size_t)N * (size_t)K + 255) & ~(size_t)255;
+    const size_t db = ((size_t)N * dpw * 2 + 255) & ~(size_t)255;
+    WRep r;
+    r.type = w.type;
+    r.q = static_cast<int8_t*>(dst);
+    r.q_s1 = K;
+    r.d = reinterpret_cast<_Float16*>(static_cast<char*>(dst) + q);
+    r.m = w.type == T_Q4_1 ? reinterpret_cast<_Float16*>(static_cast<char*>(dst) + q + db) : nullptr;
+    r.dpw = dpw;
+    r.N = N;
+    r.K = K;
+    const int64_t n = N * nbr;
+    if (n > 0) {
+        const dim3 grid((unsigned)((n + 255) / 256));
+        switch (w.type) {
+            case T_Q8_0:
+                repack_weights_kernel<T_Q8_0><<<grid, 256, 0, st>>>(w.data, w.nb1, N, nbr, dpw, r.q, r.q_s1, r.d, r.m);
+                break;
+            case T_Q4_0:
+                repack_weights_kernel<T_Q4_0><<<grid, 256, 0, st>>>(w.data, w.nb1, N, nbr, dpw, r.q, r.q_s1, r.d, r.m);
+                break;
+            default:
+                repack_weights_kernel<T_Q4_1><<<grid, 256, 0, st>>>(w.data, w.nb1, N, nbr, dpw, r.q, r.q_s1, r.d, r.m);
+                break;
+        }
+    }
+    *out = r;
+    return hipGetLastError();
+}
+
+template <int WT>
+static void launch8_t(const Mmq8Args& a, const MmqEpi* e, hipStream_t st) {
+    const int TT = a.tiles_m * a.tiles_n * a.ksplit;
+    const dim3 grid((unsigned)(((TT + 7) / 8) * 8));
+    MmqEpi none{};
+    if (a.dots) mmq8_kernel<WT, MMQ_EPI_STORE, true><<<grid, NT8, 0, st>>>(a, none);
+    else if (a.ksplit > 1 || !e || e->kind == MMQ_EPI_STORE) mmq8_kernel<WT, MMQ_EPI_STORE><<<grid, NT8, 0, st>>>(a, none);
+    else if (e->kind == MMQ_EPI_RESIDUAL) mmq8_kernel<WT, MMQ_EPI_RESIDUAL><<<grid, NT8, 0, st>>>(a, *e);
+    else mmq8_kernel<WT, MMQ_EPI_QKV><<<grid, NT8, 0, st>>>(a, *e);
+}
+
+bool mmq8_supported(const WRep& w, const ActI8& a) {
+    return (w.type == T_Q8_0 || w.type == T_Q4_0 || w.type == T_Q4_1) && a.K == w.K && a.K % QK == 0 && a.K > 0 &&
+           w.q_s1 % 16 == 0 && a.s1 % 16 == 0 && 2 * a.nst == mmq_scale_pitch(a.K) && w.dpw == 2 * a.nst &&
+           (reinterpret_cast<uintptr_t>(w.q) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.q) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(w.d) & 3) == 0 && (reinterpret_cast<uintptr_t>(a.dl) & 3) == 0 &&
+           (reinterpret_cast<uintptr_t>(a.dh) & 3) == 0 &&
+           (w.type != T_Q4_1 || (((reinterpret_cast<uintptr_t>(w.m) | reinterpret_cast<uintptr_t>(a.s)) & 3) == 0 &&
+                                 w.m && a.s)) &&
+           (int64_t)(a.M - 1) * a.s1 + a.K < OOB8 && (int64_t)(w.N - 1) * w.q_s1 + w.K < OOB8 &&
+           4LL * a.M * a.nst < OOB8 && 4LL * w.N * a.nst < OOB8;
+}
+
+hipError_t launch_mmq8(const WRep& w, const ActI8& a, const MatD& d, const MmqEpi* epi, const MmqSplit& sp,
+                       hipStream_t st, int32_t* dots) {
+    if (!mmq8_supported(w, a)) return hipErrorInvalidValue;
+    const int64_t N = w.N;
+    Mmq8Args p;
+    p.dots = dots;
+    p.nbt = (int)(a.K / QK);
+    p.A = static_cast<const int8_t*>(a.q);
+    p.a_s1 = a.s1;
+    p.Adl = a.dl;
+    p.Adh = a.dh;
+    p.As = static_cast<const _Float16*>(a.s);
+    p.W = w.q;
+    p.w_s1 = w.q_s1;
+    p.Wd = w.d;
+    p.Wm = w.m;
+    p.D = d.data;
+    p.d_nb1 = d.nb1;
+    p.M = (int)a.M;
+    p.N = (int)N;
+    p.K = (int)a.K;
+    p.nst = (int)a.nst;
+    p.tiles_m = (int)((a.M + B8M - 1) / B8M);
+    p.tiles_n = (int)((N + B8N - 1) / B8N);
+    {
+        // group height: the fewest L2 bytes for the workgroups an XCD runs at once (32 CUs x 2)
+        const double at = (double)B8M * a.K, wt = (double)B8N * a.K;
+        double best = 0;
+        p.gm = 1;
+        for (int gm = 1; gm <= 16 && gm <= p.tiles_m; gm *= 2) {
+            const double c = gm * at + ((64 + gm - 1) / gm) * wt;
+            if (gm == 1 || c < best) {
+                best = c;
+                p.gm = gm;
+            }
+        }
+    }
+    const int nstage = (int)((a.K / QK + 1) / 2);
+    const bool split = sp.ks > 1 && !dots;
+    p.ksplit = split ? sp.ks : 1;
+    p.sps = split ? (nstage + sp.ks - 1) / sp.ks : nstage;
+    p.d_split = 0;
+    if (split) {
+        if (!sp.part || N % 4 != 0 || (int64_t)(sp.ks - 1) * p.sps >= nstage) return hipErrorInvalidValue;
+        p.D = sp.part;
+        p.d_nb1 = N * 4;
+        p.d_split = a.M * N * 4;
+    } else if (epi && epi->kind != MMQ_EPI_STORE) {
+        if (N % 4 != 0 || !epi->bias) return hipErrorInvalidValue;
+    }
+    p.d_v4 = N % 4 == 0 && p.d_nb1 % 16 == 0 && (reinterpret_cast<uintptr_t>(p.D) & 15) == 0;
+    if (epi && epi->kind != MMQ_EPI_STORE && !split) p.d_v4 = 1;
+    if (!split && !dots && (!epi || epi->kind == MMQ_EPI_STORE) && !d.data) return hipErrorInvalidValue;
+    switch (w.type) {
+        case T_Q8_0: launch8_t<T_Q8_0>(p, epi, st); break;
+        case T_Q4_0: launch8_t<T_Q4_0>(p, epi, st); break;
+        default: launch8_t<T_Q4_1>(p, epi, st); break;
+    }
+    if (split) {
+        const hipError_t e0 = hipGetLastError();
+        if (e0 != hipSuccess) return e0;
+        return launch_mmq_reduce(sp.part, sp.ks, (int)a.M, (int)N, reinterpret_cast<char*>(d.data), d.nb1, epi, st);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace mi355

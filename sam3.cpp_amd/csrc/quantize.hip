@@ -205,11 +205,12 @@ __global__ __launch_bounds__(256) void quantize_q4_kernel(const char* __restrict
 // to even; the padding slot is written as zero).  A wavefront covers 64
 // consecutive blocks of the flattened [rows][nb] grid, so loads (128 B per
 // thread), quant stores (64 B per thread) and scale stores are contiguous.
-template <bool WITH_SUM>
+// I8: quants as int8 [rows][q_s1 bytes] (the int8-MFMA operand) instead of fp16 [rows][ne0].
+template <bool WITH_SUM, bool I8 = false>
 __global__ __launch_bounds__(256) void quantize_mmq_kernel(const char* __restrict__ src, int stype, RowAddr ra,
                                                            int64_t ne0, int64_t nblocks, int64_t dp,
                                                            uint16_t* __restrict__ qout, uint16_t* __restrict__ dout,
-                                                           uint16_t* __restrict__ sout) {
+                                                           uint16_t* __restrict__ sout, int64_t q_s1 = 0) {
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= nblocks) return;
     const int64_t nbpr = ne0 / QK;
@@ -235,21 +236,48 @@ __global__ __launch_bounds__(256) void quantize_mmq_kernel(const char* __restric
     for (int j = 0; j < QK; ++j) amax = fmaxf(amax, fabsf(x[j]));
     const float d = amax / 127.0f;
     const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    uint32_t hq[QK / 2];
     int isum = 0;
+    if (I8) {
+        uint32_t bq[QK / 4];
 #pragma unroll
-    for (int j = 0; j < QK / 2; ++j) {
-        const int q0 = (int)rintf(x[2 * j] * id), q1 = (int)rintf(x[2 * j + 1] * id);
-        isum += q0 + q1;
-        hq[j] = (uint32_t)f2h((float)q0) | ((uint32_t)f2h((float)q1) << 16);
+        for (int j = 0; j < QK / 4; ++j) {
+            const int q0 = (int)rintf(x[4 * j] * id), q1 = (int)rintf(x[4 * j + 1] * id);
+            const int q2 = (int)rintf(x[4 * j + 2] * id), q3 = (int)rintf(x[4 * j + 3] * id);
+            isum += q0 + q1 + q2 + q3;
+            bq[j] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+                    ((uint32_t)(q3 & 0xff) << 24);
+        }
+        uint4* qd = reinterpret_cast<uint4*>(reinterpret_cast<int8_t*>(qout) + r * q_s1 + b * QK);
+        qd[0] = make_uint4(bq[0], bq[1], bq[2], bq[3]);
+        qd[1] = make_uint4(bq[4], bq[5], bq[6], bq[7]);
+    } else {
+        uint32_t hq[QK / 2];
+#pragma unroll
+        for (int j = 0; j < QK / 2; ++j) {
+            const int q0 = (int)rintf(x[2 * j] * id), q1 = (int)rintf(x[2 * j + 1] * id);
+            isum += q0 + q1;
+            hq[j] = (uint32_t)f2h((float)q0) | ((uint32_t)f2h((float)q1) << 16);
+        }
+        uint4* qd = reinterpret_cast<uint4*>(qout + r * ne0 + b * QK);
+#pragma unroll
+        for (int j = 0; j < QK / 8; ++j) qd[j] = make_uint4(hq[4 * j], hq[4 * j + 1], hq[4 * j + 2], hq[4 * j + 3]);
     }
-    uint4* qd = reinterpret_cast<uint4*>(qout + r * ne0 + b * QK);
-#pragma unroll
-    for (int j = 0; j < QK / 8; ++j) qd[j] = make_uint4(hq[4 * j], hq[4 * j + 1], hq[4 * j + 2], hq[4 * j + 3]);
-    dout[r * dp + b] = f2h(d);
+    if (I8) {
+        // scales as the int8 kernel's scale-MFMA operands: dword [r][b / 2] of dl holds d of an
+        // even block in its low half, of dh d of an odd block in its high half (dout = dl,
+        // dh = dl + rows * nst); a missing odd block (odd count) leaves a zero dword in dh
+        const int64_t nst = dp / 2, rows = nblocks / nbpr;
+        uint32_t* dl = reinterpret_cast<uint32_t*>(dout);
+        uint32_t* dh = dl + rows * nst;
+        if ((b & 1) == 0) dl[r * nst + b / 2] = (uint32_t)f2h(d);
+        else dh[r * nst + b / 2] = (uint32_t)f2h(d) << 16;
+        if (b == nbpr - 1 && (nbpr & 1)) dh[r * nst + b / 2] = 0;
+    } else {
+        dout[r * dp + b] = f2h(d);
+    }
     if (WITH_SUM) sout[r * dp + b] = f2h(d * (float)isum);
     if (b == nbpr - 1 && dp > nbpr) {
-        dout[r * dp + nbpr] = 0;
+        if (!I8) dout[r * dp + nbpr] = 0;
         if (WITH_SUM) sout[r * dp + nbpr] = 0;
     }
 }
@@ -317,6 +345,22 @@ hipError_t launch_quantize_mmq(const SrcView& src, bool with_sum, int64_t dp, ui
         quantize_mmq_kernel<true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, dp, q, d, s);
     else
         quantize_mmq_kernel<false><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, dp, q, d, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_mmq_i8(const SrcView& src, bool with_sum, int64_t s1, int64_t dp, int8_t* q, uint16_t* d,
+                                  uint16_t* s, hipStream_t st) {
+    const int64_t rows = src.ne[1] * src.ne[2] * src.ne[3];
+    const int64_t nblocks = rows * (src.ne[0] / QK);
+    if (nblocks == 0) return hipSuccess;
+    if (s1 < src.ne[0] || s1 % 16 != 0) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((nblocks + 255) / 256));
+    const RowAddr ra = row_addr(src);
+    uint16_t* qq = reinterpret_cast<uint16_t*>(q);
+    if (with_sum)
+        quantize_mmq_kernel<true, true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, dp, qq, d, s, s1);
+    else
+        quantize_mmq_kernel<false, true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, dp, qq, d, s, s1);
     return hipGetLastError();
 }
 

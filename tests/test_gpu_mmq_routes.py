@@ -1,0 +1,104 @@
+"""The int8 MUL_MAT route (mi355_context_set_mmq_kernel(MI355_MMQ_INT8)):
+one-byte activation quants, weights repacked into int8 rows with separate
+scale arrays, exact int32 block sums on v_mfma_i32_32x32x32_i8.
+
+Bars:
+  * block sums: bit-exact against numpy int64 dot products of the oracle's
+    quants (mi355_mul_mat_block_dots on each route);
+  * outputs: |gpu - oracle| <= 1e-5 * absterm (as every quantized mul_mat),
+    and bit-identical to the MI355_MMQ_F16 route on the same operands: both
+    combine acc = fma(isum, d_a * d_w, acc) in block order, so any difference
+    is a defect of one of them.
+Shapes: the four SAM3 ViT linears at 5184 tokens, ragged M / N, an odd block
+count (K = 96, 4736 = 148 blocks), and GEMMs small enough to take split-K."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import absterm, dev, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+ROUTES = ["int8"]
+
+
+def _kernel(mi, route):
+    return {"f16": mi.MMQ_F16, "int8": mi.MMQ_INT8}[route]
+
+
+def _run(mi, ctx, wq, t, K, N, x, route):
+    M = x.shape[0]
+    w, xd = dev(wq.view(np.uint8)), dev(x)
+    dst = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.set_mmq_kernel(_kernel(mi, route))
+    try:
+        ctx.mul_mat(mi.from_torch(w, t, [K, N]), mi.from_torch(xd, mi.F32, [K, M]), mi.from_torch(dst, mi.F32, [N, M]))
+        ctx.synchronize()
+    finally:
+        ctx.set_mmq_kernel(mi.MMQ_F16)
+    return dst
+
+
+@pytest.mark.parametrize("route", ROUTES)
+@pytest.mark.parametrize("tname", ["q8_0", "q4_0", "q4_1"])
+@pytest.mark.parametrize("M,N,K", [(5184, 3072, 1024), (5184, 1024, 1024), (5184, 4736, 1024), (5184, 1024, 4736),
+                                   (77, 65, 96), (300, 200, 1024), (33, 130, 4736), (1000, 96, 160), (129, 257, 64)])
+def test_route_bit_identical(mi, ctx, orc, route, tname, M, N, K):
+    t = orc.NAME_TYPE[tname]
+    print(f"{route} route {tname} M={M} N={N} K={K}", flush=True)
+    w = orc.normal(N * K, seed=M + N, stream=1, std=0.02).reshape(N, K)
+    x = orc.normal(M * K, seed=M + N, stream=2).reshape(M, K)
+    wq = orc.quantize_weights(t, w)
+    ref16 = _run(mi, ctx, wq, t, K, N, x, "f16")
+    got8 = _run(mi, ctx, wq, t, K, N, x, route)
+    assert torch.isfinite(got8).all()
+    assert torch.equal(got8, ref16), f"max diff {(got8 - ref16).abs().max().item():.3e}"
+    rows = np.arange(M) if M <= 300 else np.linspace(0, M - 1, 97).astype(int)
+    vt = orc.VEC_DOT_TYPE[t]
+    ref = orc.mul_mat(wq, t, K, N, x[rows][None, None])[0, 0]
+    e = rel_err(got8.cpu().numpy()[rows], ref, absterm(orc, t, wq, K, orc.from_float(vt, x[rows])))
+    assert e <= 1e-5, f"rel err {e:.3e}"
+
+
+@pytest.mark.parametrize("route", ROUTES)
+@pytest.mark.parametrize("tname", ["q8_0", "q4_0", "q4_1"])
+@pytest.mark.parametrize("K", [96, 1024])
+def test_route_block_dots_bit_exact(mi, ctx, orc, route, tname, K):
+    t = orc.NAME_TYPE[tname]
+    M, N = 70, 45
+    w = orc.normal(N * K, seed=4, stream=1, std=0.02).reshape(N, K)
+    x = orc.normal(M * K, seed=4, stream=2).reshape(M, K)
+    wq = orc.quantize_weights(t, w)
+    nb = K // 32
+    isums = torch.zeros(M * N * nb, dtype=torch.int32, device="cuda")
+    ctx.set_mmq_kernel(_kernel(mi, route))
+    try:
+        ctx.mul_mat_block_dots(mi.from_torch(dev(wq), t, [K, N]), mi.from_torch(dev(x), mi.F32, [K, M]),
+                               isums.data_ptr())
+        ctx.synchronize()
+    finally:
+        ctx.set_mmq_kernel(mi.MMQ_F16)
+    got = isums.cpu().numpy().reshape(M, N, nb)
+    wv, _, _ = orc.decode_blocks(t, wq, K)
+    xv, _, _ = orc.decode_blocks(orc.VEC_DOT_TYPE[t], orc.from_float(orc.VEC_DOT_TYPE[t], x), K)
+    ref = np.einsum("mbj,nbj->mnb", xv.reshape(M, nb, 32).astype(np.int64), wv.reshape(N, nb, 32).astype(np.int64))
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("route", ROUTES)
+def test_route_integer_exact(mi, ctx, orc, route):
+    """Unit scales (d_a = d_w = 1) make the result an exact integer: each
+    route must return sum_b isum_b bit for bit, with |isum| near the int8
+    extremes (-127..127 on both sides)."""
+    M, N, K = 96, 80, 1024
+    rng = np.random.default_rng(12)
+    x = rng.integers(-127, 128, size=(M, K)).astype(np.float32)
+    x.reshape(M, K // 32, 32)[:, :, 5] = 127.0
+    q = rng.integers(-127, 128, size=(N, K)).astype(np.int8)
+    wq = np.zeros((N, K // 32, 34), dtype=np.uint8)
+    wq[:, :, 0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    wq[:, :, 2:] = q.reshape(N, K // 32, 32).view(np.uint8)
+    out = _run(mi, ctx, wq.reshape(N, -1), orc.Q8_0, K, N, x, route).cpu().numpy()
+    exact = x.astype(np.int64) @ q.astype(np.int64).T
+    assert np.array_equal(out, exact.astype(np.float32))
