@@ -59,10 +59,16 @@ typedef enum {
 } mi355_act_variant;
 
 /* The layout fields of a ggml_tensor (ggml.h struct ggml_tensor: type, ne,
- * nb, data).  data is a device pointer. */
+ * nb, data).  data is a device pointer.  layout is MI355_LAYOUT_GGML (0, the
+ * bytes ggml defines for type/ne/nb) except for a weight prepared by
+ * mi355_weight_prepare (MI355_LAYOUT_INT8). */
+typedef enum {
+    MI355_LAYOUT_GGML = 0,
+    MI355_LAYOUT_INT8 = 1,
+} mi355_layout;
 typedef struct mi355_tensor {
     int32_t type;
-    int32_t pad_;
+    int32_t layout;
     int64_t ne[4];
     int64_t nb[4];
     void* data;
@@ -106,7 +112,8 @@ void* mi355_buffer_base(const mi355_buffer* buf);
 size_t mi355_buffer_size(const mi355_buffer* buf);
 /* Sets t->data = base + offset after checking that ggml_nbytes(t) bytes fit. */
 mi355_status mi355_buffer_place(const mi355_buffer* buf, size_t offset, mi355_tensor* t);
-/* ggml_nbytes of t's layout (0 for an empty tensor or an unknown type). */
+/* ggml_nbytes of t's layout (0 for an empty tensor or an unknown type); for
+ * a prepared weight (MI355_LAYOUT_INT8) the bytes of its prepared form. */
 size_t mi355_tensor_nbytes(const mi355_tensor* t);
 /* ggml_backend_buffer_clear. */
 mi355_status mi355_buffer_clear(mi355_context* ctx, mi355_buffer* buf, uint8_t value);
@@ -135,6 +142,25 @@ mi355_status mi355_tensor_memset(mi355_context* ctx, const mi355_tensor* t, uint
 int mi355_supports_mul_mat(const mi355_tensor* src0, const mi355_tensor* src1, const mi355_tensor* dst);
 mi355_status mi355_mul_mat(mi355_context* ctx, const mi355_tensor* src0, const mi355_tensor* src1,
                            const mi355_tensor* dst);
+
+/* ---- Prepared weights (the counterpart of ggml's "extra" buffer types, such
+ * as ggml-cpu's, which repack Q4_0 weights into an interleaved layout when
+ * ggml_backend_tensor_set uploads them; sam3.cpp uploads each weight once,
+ * sam3.cpp:3156-3179).  A 2-D Q8_0 / Q4_0 / Q4_1 weight is repacked once into
+ * the int8 MUL_MAT layout (quants as int8 rows, block scales in separate
+ * arrays), so MUL_MATs with it skip the per-call repack.
+ * mi355_weight_prepared_nbytes: bytes of the prepared form of w (0: w is not
+ *   a 2-D Q8_0 / Q4_0 / Q4_1 weight with K % 32 == 0).
+ * mi355_weight_prepare: repacks w (ggml layout, device data) into dst
+ *   (256-byte aligned, dst_size >= the prepared bytes, not overlapping w) on
+ *   the context's stream, and describes the result in *out: w's type and ne,
+ *   layout MI355_LAYOUT_INT8, nb of a contiguous ggml tensor, data = dst.
+ *   mi355_mul_mat and mi355_mul_mat_noalloc take *out as src0 and give the
+ *   same bits as with w; the buffer and tensor calls copy it as bytes; every
+ *   other op rejects it (MI355_STATUS_INVALID_ARG). */
+size_t mi355_weight_prepared_nbytes(const mi355_tensor* w);
+mi355_status mi355_weight_prepare(mi355_context* ctx, const mi355_tensor* w, void* dst, size_t dst_size,
+                                  mi355_tensor* out);
 
 /* ---- MUL_MAT without allocation (no counterpart in the reference; for
  * callers that cannot allocate device memory: code under HIP graph capture,
@@ -477,18 +503,23 @@ mi355_status mi355_context_set_fusion(mi355_context* ctx, int enable);
  * routes them to the tiled kernel (for comparisons). */
 mi355_status mi355_context_set_skinny(mi355_context* ctx, int enable);
 
-/* The kernel behind 2-D MUL_MATs with Q8_0 / Q4_0 / Q4_1 weights (no
- * counterpart in the reference).  All give the same bits: the exact int32
- * block sums combined as acc = fma(isum, d_a * d_w, acc) in block order.
+/* The kernel behind 2-D MUL_MATs with Q8_0 / Q4_0 / Q4_1 weights in the
+ * ggml layout (no counterpart in the reference).  All give the same bits: the
+ * exact int32 block sums combined as acc = fma(isum, d_a * d_w, acc) in block
+ * order.
  * - MI355_MMQ_F16: fp16 MFMAs over the quants as exact halves, weights used in
  *   their ggml rows and decoded in registers;
  * - MI355_MMQ_INT8: src1 quantized to one-byte quants, weights repacked into
  *   int8 rows with separate scale arrays on each call, block sums on
- *   v_mfma_i32_32x32x32_i8 (one VALU conversion per output and block more).
- * Other MUL_MATs keep MI355_MMQ_F16. */
+ *   v_mfma_i32_32x32x32_i8;
+ * - MI355_MMQ_AUTO (the default): MI355_MMQ_INT8 for Q8_0 and Q4_0 weights,
+ *   MI355_MMQ_F16 for Q4_1 (the faster per call with the repack counted).
+ * Prepared weights always take the int8 kernel; other MUL_MATs keep their
+ * own kernels. */
 typedef enum {
     MI355_MMQ_F16 = 0,
     MI355_MMQ_INT8 = 1,
+    MI355_MMQ_AUTO = 2,
 } mi355_mmq_kernel;
 mi355_status mi355_context_set_mmq_kernel(mi355_context* ctx, int kernel);
 

@@ -25,7 +25,8 @@ HEADER = os.path.join(ROOT, "include", "sam3_mi355.h")
 
 F32, F16, Q4_0, Q4_1, Q8_0, Q8_1 = 0, 1, 2, 3, 8, 9
 ACT_X86, ACT_REF = 0, 1
-MMQ_F16, MMQ_INT8 = 0, 1
+MMQ_F16, MMQ_INT8, MMQ_AUTO = 0, 1, 2
+LAYOUT_GGML, LAYOUT_INT8 = 0, 1
 TYPE_SIZE = {F32: 4, F16: 2, Q4_0: 18, Q4_1: 20, Q8_0: 34, Q8_1: 36}
 BLCK = {F32: 1, F16: 1, Q4_0: 32, Q4_1: 32, Q8_0: 32, Q8_1: 32}
 
@@ -40,7 +41,7 @@ class Mi355Error(RuntimeError):
 
 class Tensor(C.Structure):
     """struct mi355_tensor: the layout fields of a ggml_tensor."""
-    _fields_ = [("type", C.c_int32), ("pad_", C.c_int32), ("ne", C.c_int64 * 4),
+    _fields_ = [("type", C.c_int32), ("layout", C.c_int32), ("ne", C.c_int64 * 4),
                 ("nb", C.c_int64 * 4), ("data", C.c_void_p)]
 
 
@@ -169,6 +170,8 @@ def lib():
         "mi355_context_set_fusion": (I, [P, I]),
         "mi355_context_set_skinny": (I, [P, I]),
         "mi355_context_set_mmq_kernel": (I, [P, I]),
+        "mi355_weight_prepared_nbytes": (SZ, [T]),
+        "mi355_weight_prepare": (I, [P, T, P, SZ, T]),
         "mi355_hiera_pos_embed": (I, [P, P, I, I, I, P, I, I, I, P]),
         "mi355_neck_workspace_size": (SZ, [I, I, C.POINTER(NeckScale)]),
         "mi355_sam3_neck": (I, [P, P, I, I, C.POINTER(NeckScale), C.POINTER(P)]),
@@ -297,6 +300,11 @@ def make_tensor(ptr: int, t: int, ne, nb=None) -> Tensor:
         T.nb[i] = int(nb[i])
     T.data = ptr
     return T
+
+
+def weight_prepared_nbytes(w: Tensor) -> int:
+    """mi355_weight_prepared_nbytes."""
+    return int(lib().mi355_weight_prepared_nbytes(C.byref(w)))
 
 
 def from_torch(x, t: int, ne, nb=None) -> Tensor:
@@ -434,8 +442,15 @@ class Context:
         self._check(self.L.mi355_context_set_fusion(self.h, 1 if enable else 0))
 
     def set_mmq_kernel(self, kernel: int):
-        """Kernel of 2-D quantized MUL_MATs: MMQ_F16 (0) or MMQ_INT8 (1); same bits."""
+        """Kernel of 2-D quantized MUL_MATs: MMQ_F16 (0), MMQ_INT8 (1) or MMQ_AUTO (2, the default); same bits."""
         self._check(self.L.mi355_context_set_mmq_kernel(self.h, int(kernel)))
+
+    def weight_prepare(self, w: Tensor, dst: int, size: int) -> Tensor:
+        """mi355_weight_prepare: w repacked into the device memory at dst (size bytes); the prepared tensor."""
+        out = Tensor()
+        self._check(self.L.mi355_weight_prepare(self.h, C.byref(w), C.c_void_p(dst), size, C.byref(out)))
+        out._keep = getattr(w, "_keep", None)
+        return out
 
     def set_mmq_int8(self, on: bool):
         self.set_mmq_kernel(MMQ_INT8 if on else MMQ_F16)

@@ -51,9 +51,16 @@ mi355_status fill(mi355_context* ctx, void* p, uint8_t value, size_t n) {
 
 // ggml_nbytes of the layout: the span from data to one past the last element
 // (blocks for quantized types), 0 for an empty tensor; false on overflow or an
-// unknown type.
+// unknown type or layout.  A prepared weight spans its prepared form.
 bool layout_bytes(const mi355_tensor* t, size_t* out) {
     *out = 0;
+    if (t->layout == MI355_LAYOUT_INT8) {  // a prepared weight: the bytes of its prepared form
+        if (!(t->type == T_Q8_0 || t->type == T_Q4_0 || t->type == T_Q4_1) || t->ne[0] < 0 || t->ne[1] < 0 ||
+            t->ne[2] != 1 || t->ne[3] != 1 || t->ne[0] % 32 != 0)
+            return false;
+        *out = wrep_bytes(t->type, t->ne[1], t->ne[0]);
+        return true;
+    }
     const int64_t ts = type_size(t->type), bs = blck(t->type);
     if (!ts || !bs || !dims_ok(t)) return false;
     for (int i = 0; i < 4; ++i)

@@ -44,9 +44,16 @@ int blck(int t) { return (t == T_F32 || t == T_F16) ? 1 : (type_size(t) ? 32 : 0
 int64_t row_size(int t, int64_t ne0) { return blck(t) ? type_size(t) * (ne0 / blck(t)) : 0; }
 
 bool dims_ok(const mi355_tensor* t) {
+    if (t->layout != MI355_LAYOUT_GGML) return false;
     for (int i = 0; i < 4; ++i)
         if (t->ne[i] < 0 || t->nb[i] < 0) return false;
     return true;
+}
+
+bool prepared_ok(const mi355_tensor* t) {
+    return t->layout == MI355_LAYOUT_INT8 && (t->type == T_Q8_0 || t->type == T_Q4_0 || t->type == T_Q4_1) &&
+           t->ne[0] >= 0 && t->ne[1] >= 0 && t->ne[2] == 1 && t->ne[3] == 1 && t->ne[0] % 32 == 0 &&
+           (reinterpret_cast<uintptr_t>(t->data) & 255) == 0;
 }
 
 SrcView view_of(const mi355_tensor* t) {
@@ -116,7 +123,8 @@ bool f16_src1_direct(const mi355_tensor* s1) {
 struct MmPlan {
     size_t q = 0, d = 0, s = 0, align = 0, part = 0;
     int ks = 1;
-    bool i8 = false;   // int8-MFMA path: q holds int8 quants, align the repacked weights
+    bool i8 = false;    // int8-MFMA path: q holds int8 quants, align the repacked weights
+    bool prep = false;  // src0 is a prepared weight: no repack (align empty)
     size_t total() const { return q + d + s + align + part; }
 };
 
@@ -135,7 +143,9 @@ int device_cus(int device) {
 // split = false: the caller's dst cannot take the float4 stores of the split reduction;
 // kernel: the MI355_MMQ_* route when the operands are eligible for it
 MmPlan mm_plan(const mi355_tensor* s0, const mi355_tensor* s1, int cus, bool split = true, int kernel = 0) {
-    const bool i8 = kernel == MI355_MMQ_INT8;
+    const bool prep = s0->layout == MI355_LAYOUT_INT8;
+    const bool i8 = prep || kernel == MI355_MMQ_INT8 ||
+                    (kernel == MI355_MMQ_AUTO && (s0->type == T_Q8_0 || s0->type == T_Q4_0));
     MmPlan pl;
     if (s0->type == T_F32) return pl;
     const int64_t K = s1->ne[0], M = s1->ne[1], Z = s1->ne[2] * s1->ne[3];
@@ -146,7 +156,8 @@ MmPlan mm_plan(const mi355_tensor* s0, const mi355_tensor* s1, int cus, bool spl
         pl.q = align_up((size_t)(M * K));
         pl.d = align_up((size_t)(M * mmq_scale_pitch(K)) * 4);  // dl and dh dwords
         if (s0->type == T_Q4_1) pl.s = align_up((size_t)(M * mmq_scale_pitch(K)) * 2);
-        pl.align = align_up(wrep_bytes(s0->type, s0->ne[1], K));
+        pl.prep = prep;
+        pl.align = prep ? 0 : align_up(wrep_bytes(s0->type, s0->ne[1], K));
         return pl;
     }
     if (s0->type == T_F16) {
@@ -165,7 +176,7 @@ MmPlan mm_plan(const mi355_tensor* s0, const mi355_tensor* s1, int cus, bool spl
 mi355_status check_soft_max(mi355_context* ctx, const mi355_tensor* src, const mi355_tensor* mask, float max_bias,
                             const mi355_tensor* dst) {
     if (!src || !dst || !src->data || !dst->data) return fail(ctx, MI355_STATUS_INVALID_ARG, "soft_max: null argument");
-    if (!dims_ok(src) || !dims_ok(dst)) return fail(ctx, MI355_STATUS_INVALID_ARG, "soft_max: negative ne/nb");
+    if (!dims_ok(src) || !dims_ok(dst)) return fail(ctx, MI355_STATUS_INVALID_ARG, "soft_max: negative ne/nb or not the ggml layout");
     if (mask || max_bias != 0.0f) return fail(ctx, MI355_STATUS_UNSUPPORTED, "soft_max: mask/ALiBi not supported");
     if (src->type != T_F32 || dst->type != T_F32) return fail(ctx, MI355_STATUS_UNSUPPORTED, "soft_max: F32 only");
     for (int i = 0; i < 4; ++i)
@@ -186,7 +197,10 @@ mi355_status check_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
                            const mi355_tensor* d) {
     if (!s0 || !s1 || !d) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: null tensor");
     if (!s0->data || !s1->data || !d->data) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: null data pointer");
-    if (!dims_ok(s0) || !dims_ok(s1) || !dims_ok(d)) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: negative ne/nb");
+    const bool prep = s0->layout == MI355_LAYOUT_INT8;
+    if (!dims_ok(s1) || !dims_ok(d)) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: negative ne/nb or not a ggml layout");
+    if (prep ? !prepared_ok(s0) : !dims_ok(s0))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: src0 is neither a ggml tensor nor a prepared weight");
     const int t0 = s0->type;
     if (!(t0 == T_F32 || t0 == T_F16 || t0 == T_Q8_0 || t0 == T_Q4_0 || t0 == T_Q4_1))
         return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat: src0 type %d not supported", t0);
@@ -200,8 +214,10 @@ mi355_status check_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
         return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: src1 batch dims not a multiple of src0's");
     if (d->ne[0] != s0->ne[1] || d->ne[1] != s1->ne[1] || d->ne[2] != s1->ne[2] || d->ne[3] != s1->ne[3])
         return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: dst shape mismatch");
-    if (s0->nb[0] != type_size(t0) || s0->nb[1] < row_size(t0, K))
+    if (!prep && (s0->nb[0] != type_size(t0) || s0->nb[1] < row_size(t0, K)))
         return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: src0 rows must be contiguous");
+    if (prep && (s1->ne[2] != 1 || s1->ne[3] != 1))
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat: a prepared weight takes a 2-D src1");
     if (d->nb[0] != 4) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat: dst nb[0] must be 4");
     if (s1->nb[0] != type_size(s1->type) && s1->type != T_F32)
         return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat: strided F16 src1 elements");
@@ -272,8 +288,8 @@ mi355_status mul_mat_run(mi355_context* ctx, const mi355_tensor* s0, const mi355
     mi355_status st;
     if (pl.i8) {
         // weights -> int8 rows + scale arrays, src1 -> int8 quants + scales, then the int8-MFMA GEMM
-        WRep wr;
-        {
+        WRep wr = wrep_view(s0->type, N, K, s0->data);
+        if (!pl.prep) {
             Timed tr(tctx, "repack_weights");
             st = hip_check(ctx, tr.done(launch_repack_weights(matw_of(s0), N, K, ws + pl.q + pl.d + pl.s, &wr,
                                                               ctx->stream)),
@@ -386,6 +402,8 @@ mi355_status mul_mat_epi(mi355_context* ctx, const mi355_tensor* s0, const ActF1
 mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const mi355_tensor* d,
                          const MmqEpi* epi) {
     if (!s0 || !a.q) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat_act: null operand");
+    if (s0->layout != MI355_LAYOUT_GGML)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat_act: the fused passes take weights in the ggml layout");
     const int mode = act_mode_for(s0->type);
     if (mode == ACT_F32) return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat_act: no prequantized path for type %d", s0->type);
     if (mode != ACT_F16 && (!a.d || (mode == ACT_Q8S && !a.s) || a.dp != mmq_scale_pitch(a.K)))
@@ -437,7 +455,7 @@ mi355_status check_flash_attn(mi355_context* ctx, const mi355_tensor* q, const m
     if (!q || !k || !v || !dst || !q->data || !k->data || !v->data || !dst->data)
         return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: null argument");
     if (!dims_ok(q) || !dims_ok(k) || !dims_ok(v) || !dims_ok(dst))
-        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: negative ne/nb");
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: negative ne/nb or not the ggml layout");
     if (mask || max_bias != 0.0f || logit_softcap != 0.0f)
         return fail(ctx, MI355_STATUS_UNSUPPORTED, "flash_attn_ext: mask, ALiBi and softcap not supported");
     // ggml_flash_attn_ext shape rules
@@ -599,6 +617,44 @@ size_t mi355_mul_mat_workspace_size(const mi355_tensor* s0, const mi355_tensor* 
     return mm_plan(s0, s1, device_cus(dev)).total();
 }
 
+size_t mi355_weight_prepared_nbytes(const mi355_tensor* w) {
+    if (!w || !dims_ok(w) || !(w->type == T_Q8_0 || w->type == T_Q4_0 || w->type == T_Q4_1) || w->ne[2] != 1 ||
+        w->ne[3] != 1 || w->ne[0] % 32 != 0)
+        return 0;
+    return wrep_bytes(w->type, w->ne[1], w->ne[0]);
+}
+
+mi355_status mi355_weight_prepare(mi355_context* ctx, const mi355_tensor* w, void* dst, size_t dst_size,
+                                  mi355_tensor* out) {
+    if (!w || !dst || !out) return fail(ctx, MI355_STATUS_INVALID_ARG, "weight_prepare: null argument");
+    const size_t need = mi355_weight_prepared_nbytes(w);
+    if (need == 0) return fail(ctx, MI355_STATUS_INVALID_ARG, "weight_prepare: not a 2-D Q8_0/Q4_0/Q4_1 ggml weight");
+    if (!w->data) return fail(ctx, MI355_STATUS_INVALID_ARG, "weight_prepare: null weight data");
+    if (w->nb[0] != type_size(w->type) || w->nb[1] < row_size(w->type, w->ne[0]) ||
+        (reinterpret_cast<uintptr_t>(w->data) & 1) || (w->nb[1] & 1))
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "weight_prepare: rows must be contiguous and 2-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(dst) & 255) != 0)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "weight_prepare: dst must be 256-byte aligned");
+    if (dst_size < need) return fail(ctx, MI355_STATUS_INVALID_ARG, "weight_prepare: dst holds %zu bytes, %zu needed", dst_size, need);
+    const char* wb = static_cast<const char*>(w->data);
+    const char* db = static_cast<const char*>(dst);
+    const size_t wspan = (size_t)((w->ne[1] - 1) * w->nb[1] + row_size(w->type, w->ne[0]));
+    if (w->ne[1] > 0 && db < wb + wspan && wb < db + need)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "weight_prepare: dst overlaps the weight");
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "weight_prepare: null context");
+    (void)hipSetDevice(ctx->device);
+    *out = *w;
+    out->layout = MI355_LAYOUT_INT8;
+    out->nb[1] = row_size(w->type, w->ne[0]);
+    out->nb[2] = out->nb[3] = out->nb[1] * w->ne[1];
+    out->data = dst;
+    if (w->ne[0] == 0 || w->ne[1] == 0) return MI355_STATUS_SUCCESS;
+    WRep wr;
+    Timed t(ctx, "repack_weights");
+    return hip_check(ctx, t.done(launch_repack_weights(matw_of(w), w->ne[1], w->ne[0], dst, &wr, ctx->stream)),
+                     "repack_weights launch");
+}
+
 int mi355_supports_mul_mat(const mi355_tensor* s0, const mi355_tensor* s1, const mi355_tensor* d) {
     return check_mul_mat(nullptr, s0, s1, d) == MI355_STATUS_SUCCESS;
 }
@@ -662,10 +718,13 @@ mi355_status mi355_mul_mat_block_dots(mi355_context* ctx, const mi355_tensor* s0
     if (pl.i8) {
         char* ws = static_cast<char*>(ctx->ws);
         const int64_t K = s0->ne[0], M = s1->ne[1];
-        WRep wr;
-        st = hip_check(ctx, launch_repack_weights(matw_of(s0), s0->ne[1], K, ws + pl.q + pl.d + pl.s, &wr, ctx->stream),
-                       "repack_weights launch");
-        if (st != MI355_STATUS_SUCCESS) return st;
+        WRep wr = wrep_view(s0->type, s0->ne[1], K, s0->data);
+        if (!pl.prep) {
+            st = hip_check(ctx, launch_repack_weights(matw_of(s0), s0->ne[1], K, ws + pl.q + pl.d + pl.s, &wr,
+                                                      ctx->stream),
+                           "repack_weights launch");
+            if (st != MI355_STATUS_SUCCESS) return st;
+        }
         const ActI8 a8 = act_i8(ws, pl, s0->type, M, K);
         st = hip_check(ctx, launch_quantize_mmq_i8(view_of(s1), s0->type == T_Q4_1, K, 2 * a8.nst, reinterpret_cast<int8_t*>(ws),
                                                    reinterpret_cast<uint16_t*>(ws + pl.q),
@@ -687,7 +746,7 @@ mi355_status mi355_mul_mat_block_dots(mi355_context* ctx, const mi355_tensor* s0
 
 mi355_status mi355_quantize_rows(mi355_context* ctx, int type, int variant, const mi355_tensor* src, void* dst) {
     if (!src || !src->data || !dst) return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_rows: null argument");
-    if (!dims_ok(src)) return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_rows: negative ne/nb");
+    if (!dims_ok(src)) return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_rows: negative ne/nb or not the ggml layout");
     if (src->type != T_F32) return fail(ctx, MI355_STATUS_UNSUPPORTED, "quantize_rows: src must be F32");
     if (!(type == T_Q8_0 || type == T_Q8_1 || type == T_F16))
         return fail(ctx, MI355_STATUS_UNSUPPORTED, "quantize_rows: type %d not supported", type);
@@ -708,7 +767,7 @@ mi355_status mi355_quantize_rows(mi355_context* ctx, int type, int variant, cons
 
 mi355_status mi355_quantize_weights(mi355_context* ctx, int type, const mi355_tensor* src, void* dst) {
     if (!src || !src->data || !dst) return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_weights: null argument");
-    if (!dims_ok(src)) return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_weights: negative ne/nb");
+    if (!dims_ok(src)) return fail(ctx, MI355_STATUS_INVALID_ARG, "quantize_weights: negative ne/nb or not the ggml layout");
     if (src->type != T_F32 && src->type != T_F16)
         return fail(ctx, MI355_STATUS_UNSUPPORTED, "quantize_weights: src must be F32 or F16");
     if (!(type == T_Q8_0 || type == T_Q4_0 || type == T_Q4_1))
@@ -756,7 +815,7 @@ mi355_status mi355_context_set_fusion(mi355_context* ctx, int enable) {
 
 mi355_status mi355_context_set_mmq_kernel(mi355_context* ctx, int kernel) {
     if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "set_mmq_kernel: null context");
-    if (kernel != MI355_MMQ_F16 && kernel != MI355_MMQ_INT8)
+    if (kernel != MI355_MMQ_F16 && kernel != MI355_MMQ_INT8 && kernel != MI355_MMQ_AUTO)
         return fail(ctx, MI355_STATUS_INVALID_ARG, "set_mmq_kernel: unknown kernel %d", kernel);
     ctx->mmq_kernel = kernel;
     return MI355_STATUS_SUCCESS;

@@ -29,6 +29,7 @@ typedef float v2f __attribute__((ext_vector_type(2)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 
 // fp16 <-> fp32.  v_cvt_f16_f32 rounds to nearest even under the default
 // MODE; fp16 denormals are kept (HIP's default f16/f64 denormal mode).

@@ -31,7 +31,7 @@ struct mi355_context {
     // MUL_MATs with K <= 128 at large M take the skinny kernel
     bool skinny = true;
     // kernel of 2-D MUL_MATs with block-quantized weights (MI355_MMQ_*)
-    int mmq_kernel = 0;
+    int mmq_kernel = MI355_MMQ_AUTO;
     // kernel timing
     bool prof = false;
     struct Pending { const char* name; hipEvent_t a, b; };
@@ -47,7 +47,10 @@ mi355_status hip_check(mi355_context* ctx, hipError_t e, const char* what);
 int64_t type_size(int t);
 int blck(int t);
 int64_t row_size(int t, int64_t ne0);
+// ne, nb non-negative and the ggml layout
 bool dims_ok(const mi355_tensor* t);
+// a prepared weight (mi355_weight_prepare's output): 2-D Q8_0 / Q4_0 / Q4_1, K % 32 == 0, 256-byte aligned
+bool prepared_ok(const mi355_tensor* t);
 SrcView view_of(const mi355_tensor* t);
 size_t align_up(size_t x);
 // Grows a device buffer owned by the context to at least bytes (waits for the

@@ -151,6 +151,9 @@ struct WRep {
 };
 // Bytes of the repacked form of N rows of K elements (0: not a repackable type).
 size_t wrep_bytes(int type, int64_t N, int64_t K);
+// The descriptor of a repacked form already at base (the layout launch_repack_weights writes:
+// quants, then d, then m, each part 256-byte aligned).
+WRep wrep_view(int type, int64_t N, int64_t K, void* base);
 // Repacks the 2-D ggml weights w (rows at w.data + n * w.nb1) into dst (wrep_bytes) and describes it in *out.
 hipError_t launch_repack_weights(const MatW& w, int64_t N, int64_t K, void* dst, WRep* out, hipStream_t st);
 // Operands the int8 kernel takes (alignment, pitches, 32-bit buffer offsets).

@@ -6,9 +6,13 @@
 //   isum[m][n][b] = sum_{j<32} q_w[n][32b+j] * q_a[m][32b+j]     (exact int32)
 //
 // One v_mfma_i32_32x32x32_i8 gives a 32x32 tile's isum of one block with
-// int32 accumulation.  The scale product d_a (x) d_w of the tile is one
-// fp16 MFMA (an outer product in k-slot 0; fp16 x fp16 is exact in fp32),
-// and the combine is acc = fma(float(isum), S, acc) in block order: the same
+// int32 accumulation onto the bias 0x4B400000: its result is the bit pattern
+// of the fp32 1.5 * 2^23 + isum (|isum| <= 32 * 128 * 128 < 2^22), so one
+// full-rate subtraction recovers float(isum) exactly where v_cvt_f32_i32
+// would issue at half rate.  The scale product d_a (x) d_w of the tile is one
+// v_mfma_f32_32x32x8f16 (an outer product in k-slot 0 or 1; fp16 x fp16 is
+// exact in fp32; 2-register operands), and the combine is
+// acc = fma(float(isum), S, acc) in block order: the same
 // fp32 operations in the same order as mmq_kernel, whose fp16 MFMAs over
 // integer-valued halves give the same exact isum, so the two kernels' outputs
 // are bit-identical.  Q4_1's offset term is accumulated into acc by one
@@ -37,6 +41,8 @@ namespace {
 constexpr int B8M = 128, B8N = 128, SKB = 64;  // tile rows, tile columns, K bytes per stage
 constexpr int NT8 = 256;
 constexpr int OOB8 = 0x40000000;
+constexpr int kBias = 0x4B400000;      // fp32 1.5 * 2^23 as bits
+constexpr float kBiasF = 12582912.0f;  // 1.5 * 2^23
 }  // namespace
 
 struct Mmq8Args {
@@ -192,10 +198,10 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
     const v16f zf = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
     // fragments of one block: the lane's 16 K bytes (chunk 2 bk + g) of its A and W rows, and
-    // the scale MFMA's A operand (d_a of the block in k-slot 0 or 1; the other slots meet zeros)
+    // the scale MFMA's A operand (d_a of the block in k-slot 0 or 1 of dword 0, dword 1 zero)
     struct FragB {
         v4i a[2], b[2];
-        v4i da[2];
+        v2i da[2];
     };
     auto load_blk = [&](const St& b, int bk, FragB& f) __attribute__((always_inline)) {
         const char* base = reinterpret_cast<const char*>(&b);
@@ -207,27 +213,41 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
         }
     };
     // scale MFMA B operands of a stage: d_w of both blocks in k-slots 0, 1 (lanes 0..31)
-    auto load_dw = [&](const St& b, v4i (&dw)[2]) __attribute__((always_inline)) {
+    auto load_dw = [&](const St& b, v2i (&dw)[2]) __attribute__((always_inline)) {
         const char* base = reinterpret_cast<const char*>(&b);
 #pragma unroll
         for (int i = 0; i < 2; ++i) dw[i][0] = *reinterpret_cast<const int*>(base + sdw[i]);
     };
-    auto apply = [&](v16f& a, const v16i& I, const v16f& S) __attribute__((always_inline)) {
+    // the isum MFMA's accumulator input, held in one register block for the whole loop
+    v16i kbias = {kBias, kBias, kBias, kBias, kBias, kBias, kBias, kBias,
+                  kBias, kBias, kBias, kBias, kBias, kBias, kBias, kBias};
+    asm volatile("" : "+v"(kbias));
+    // combine of elements i0 .. i0 + 7: acc += float(isum) * S
+    auto apply_half = [&](v16f& a, const v16i& I, const v16f& S, int i0) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) a[i] = __builtin_fmaf((float)I[i], S[i], a[i]);
+        for (int i = i0; i < i0 + 8; ++i) {
+            // through a scalar: this clang's __builtin_bit_cast of an ext_vector element
+            // expression reads element 0 whatever the index
+            const int bits = I[i];
+            a[i] = __builtin_fmaf(__builtin_bit_cast(float, bits) - kBiasF, S[i], a[i]);
+        }
+    };
+    auto apply = [&](v16f& a, const v16i& I, const v16f& S) __attribute__((always_inline)) {
+        apply_half(a, I, S, 0);
+        apply_half(a, I, S, 8);
     };
 
     FragB f0, f1;
-    v4i dw[2], dwn[2];
+    v2i dw[2], dwn[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        f0.da[i] = f1.da[i] = v4i{0, 0, 0, 0};
-        dw[i] = dwn[i] = v4i{0, 0, 0, 0};
+        f0.da[i] = f1.da[i] = v2i{0, 0};
+        dw[i] = dwn[i] = v2i{0, 0};
     }
     v16i PI[2];
     v16f PS[2];
     for (int i = 0; i < 2; ++i) {
-        PI[i] = zi;
+        PI[i] = kbias;
         PS[i] = zf;
     }
 
@@ -268,13 +288,19 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
                 acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, saf),
                                                                      __builtin_bit_cast(v8h, mwf), acc[mt][nt], 0, 0, 0);
             }
-            PS[u2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, f.da[mt]),
-                                                           __builtin_bit_cast(v8h, dw[nt]), zf, 0, 0, 0);
-            PI[u2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mt], f.b[nt], zi, 0, 0, 0);
-            if (!first || bk > 0 || q > 0) {
-                // previous unit: (bk, q - 1), or block 0's last unit, or the previous stage's last
-                const int pq = (q + 3) & 3;
-                apply(acc[pq >> 1][pq & 1], PI[p2], PS[p2]);
+            // the previous unit: (bk, q - 1), or block 0's last unit, or the previous stage's last;
+            // its combine is split around this unit's second MFMA so neither MFMA issue waits
+            const bool has_prev = !first || bk > 0 || q > 0;
+            const int pq = (q + 3) & 3;
+            PI[u2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mt], f.b[nt], kbias, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (has_prev) apply_half(acc[pq >> 1][pq & 1], PI[p2], PS[p2], 0);
+            __builtin_amdgcn_sched_barrier(0);
+            PS[u2] = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, f.da[mt]),
+                                                         __builtin_bit_cast(v4h, dw[nt]), zf, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (has_prev) {
+                apply_half(acc[pq >> 1][pq & 1], PI[p2], PS[p2], 8);
                 asm volatile("" : "+v"(acc[pq >> 1][pq & 1]));
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -428,11 +454,27 @@ __global__ __launch_bounds__(256) void repack_weights_kernel(const uint8_t* __re
 }
 
 size_t wrep_bytes(int type, int64_t N, int64_t K) {
-    if (!(type == T_Q8_0 || type == T_Q4_0 || type == T_Q4_1) || K % QK != 0) return 0;
+    if (!(type == T_Q8_0 || type == T_Q4_0 || type == T_Q4_1) || K % QK != 0 || N < 0 || K < 0) return 0;
     const size_t dpw = (size_t)mmq_scale_pitch(K);
     const size_t q = ((size_t)N * (size_t)K + 255) & ~(size_t)255;
     const size_t d = ((size_t)N * dpw * 2 + 255) & ~(size_t)255;
     return q + d * (type == T_Q4_1 ? 2 : 1);
+}
+
+WRep wrep_view(int type, int64_t N, int64_t K, void* base) {
+    const int dpw = (int)mmq_scale_pitch(K);
+    const size_t q = ((size_t)N * (size_t)K + 255) & ~(size_t)255;
+    const size_t db = ((size_t)N * dpw * 2 + 255) & ~(size_t)255;
+    WRep r;
+    r.type = type;
+    r.q = static_cast<int8_t*>(base);
+    r.q_s1 = K;
+    r.d = reinterpret_cast<_Float16*>(static_cast<char*>(base) + q);
+    r.m = type == T_Q4_1 ? reinterpret_cast<_Float16*>(static_cast<char*>(base) + q + db) : nullptr;
+    r.dpw = dpw;
+    r.N = N;
+    r.K = K;
+    return r;
 }
 
 hipError_t launch_repack_weights(const MatW& w, int64_t N, int64_t K, void* dst, WRep* out, hipStream_t st) {
@@ -440,17 +482,7 @@ hipError_t launch_repack_weights(const MatW& w, int64_t N, int64_t K, void* dst,
         return hipErrorInvalidValue;
     const int64_t nbr = K / QK;
     const int dpw = (int)mmq_scale_pitch(K);
-    const size_t q = ((size_t)N * (size_t)K + 255) & ~(size_t)255;
-    const size_t db = ((size_t)N * dpw * 2 + 255) & ~(size_t)255;
-    WRep r;
-    r.type = w.type;
-    r.q = static_cast<int8_t*>(dst);
-    r.q_s1 = K;
-    r.d = reinterpret_cast<_Float16*>(static_cast<char*>(dst) + q);
-    r.m = w.type == T_Q4_1 ? reinterpret_cast<_Float16*>(static_cast<char*>(dst) + q + db) : nullptr;
-    r.dpw = dpw;
-    r.N = N;
-    r.K = K;
+    const WRep r = wrep_view(w.type, N, K, dst);
     const int64_t n = N * nbr;
     if (n > 0) {
         const dim3 grid((unsigned)((n + 255) / 256));

@@ -230,6 +230,41 @@ def test_tensor_nbytes_is_ggml_nbytes(mi):
     assert L.mi355_tensor_nbytes(mi.make_tensor(0x1000, 7, [64, 2], nb=[4, 256, 512, 512])) == 0  # unknown type
 
 
+def test_prepared_weight_host_checks(mi):
+    """Prepared-weight sizes and what MUL_MAT accepts as a prepared src0 (host
+    side only: sizes, supports query)."""
+    L = mi.lib()
+    al = lambda v: (v + 255) // 256 * 256
+    for t, N, K in [(8, 4736, 1024), (2, 1024, 4736), (3, 3072, 1024), (8, 7, 96), (3, 1, 32)]:
+        dp = (K // 32 + 1) // 2 * 2
+        want = al(N * K) + al(N * dp * 2) * (2 if t == 3 else 1)
+        w = mi.make_tensor(0x1000, t, [K, N])
+        assert L.mi355_weight_prepared_nbytes(C.byref(w)) == want
+        pt = mi.make_tensor(0x1000, t, [K, N])
+        pt.layout = mi.LAYOUT_INT8
+        assert L.mi355_tensor_nbytes(C.byref(pt)) == want
+    # not preparable: F16, 3-D, K not a multiple of 32, already prepared
+    assert L.mi355_weight_prepared_nbytes(C.byref(mi.make_tensor(0x1000, 1, [64, 8]))) == 0
+    assert L.mi355_weight_prepared_nbytes(C.byref(mi.make_tensor(0x1000, 8, [64, 8, 2]))) == 0
+    w = mi.make_tensor(0x1000, 8, [64, 8])
+    w.layout = mi.LAYOUT_INT8
+    assert L.mi355_weight_prepared_nbytes(C.byref(w)) == 0
+    t = mi.make_tensor(0x1000, 0, [64, 2])
+    t.layout = 7  # unknown layout
+    assert L.mi355_tensor_nbytes(C.byref(t)) == 0
+    # MUL_MAT with a prepared src0: 2-D src1 only, 256-byte aligned data
+    s0, s1, d = mm(mi)
+    s0.layout = mi.LAYOUT_INT8
+    s0.data = 0x10000
+    assert L.mi355_supports_mul_mat(C.byref(s0), C.byref(s1), C.byref(d)) == 1
+    s0.data = 0x10010
+    assert L.mi355_supports_mul_mat(C.byref(s0), C.byref(s1), C.byref(d)) == 0
+    s0.data = 0x10000
+    s1.layout = mi.LAYOUT_INT8  # a prepared tensor is no src1
+    assert L.mi355_supports_mul_mat(C.byref(s0), C.byref(s1), C.byref(d)) == 0
+    assert status(mi, s0, s1, d) == -4
+
+
 def test_buffer_api_host_checks(mi):
     L = mi.lib()
     assert L.mi355_buffer_alignment() == 256

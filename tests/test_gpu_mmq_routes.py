@@ -1,6 +1,8 @@
-"""The int8 MUL_MAT route (mi355_context_set_mmq_kernel(MI355_MMQ_INT8)):
-one-byte activation quants, weights repacked into int8 rows with separate
-scale arrays, exact int32 block sums on v_mfma_i32_32x32x32_i8.
+"""The int8 MUL_MAT routes: mi355_context_set_mmq_kernel(MI355_MMQ_INT8)
+(one-byte activation quants, weights repacked into int8 rows with separate
+scale arrays on each call, exact int32 block sums on v_mfma_i32_32x32x32_i8),
+the default MI355_MMQ_AUTO, and weights prepared once by mi355_weight_prepare
+(the int8 kernel without the per-call repack).
 
 Bars:
   * block sums: bit-exact against numpy int64 dot products of the oracle's
@@ -20,23 +22,39 @@ from gpu_helpers import absterm, dev, rel_err
 pytestmark = pytest.mark.gpu
 
 
-ROUTES = ["int8"]
+ROUTES = ["int8", "auto", "prepared"]
 
 
 def _kernel(mi, route):
-    return {"f16": mi.MMQ_F16, "int8": mi.MMQ_INT8}[route]
+    return {"f16": mi.MMQ_F16, "int8": mi.MMQ_INT8, "auto": mi.MMQ_AUTO, "prepared": mi.MMQ_AUTO}[route]
+
+
+def _prepare(mi, ctx, wt):
+    """The prepared form of wt in a fresh 256-byte aligned device buffer."""
+    n = mi.weight_prepared_nbytes(wt)
+    assert n > 0
+    buf = torch.full((n + 256,), 0xAB, dtype=torch.uint8, device="cuda")
+    off = (-buf.data_ptr()) % 256
+    pt = ctx.weight_prepare(wt, buf.data_ptr() + off, n)
+    pt._keep = (buf, wt._keep)
+    return pt
+
+
+def _weights(mi, ctx, wq, t, K, N, route):
+    wt = mi.from_torch(dev(wq.view(np.uint8)), t, [K, N])
+    return _prepare(mi, ctx, wt) if route == "prepared" else wt
 
 
 def _run(mi, ctx, wq, t, K, N, x, route):
     M = x.shape[0]
-    w, xd = dev(wq.view(np.uint8)), dev(x)
+    s0, xd = _weights(mi, ctx, wq, t, K, N, route), dev(x)
     dst = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
     ctx.set_mmq_kernel(_kernel(mi, route))
     try:
-        ctx.mul_mat(mi.from_torch(w, t, [K, N]), mi.from_torch(xd, mi.F32, [K, M]), mi.from_torch(dst, mi.F32, [N, M]))
+        ctx.mul_mat(s0, mi.from_torch(xd, mi.F32, [K, M]), mi.from_torch(dst, mi.F32, [N, M]))
         ctx.synchronize()
     finally:
-        ctx.set_mmq_kernel(mi.MMQ_F16)
+        ctx.set_mmq_kernel(mi.MMQ_AUTO)
     return dst
 
 
@@ -72,13 +90,13 @@ def test_route_block_dots_bit_exact(mi, ctx, orc, route, tname, K):
     wq = orc.quantize_weights(t, w)
     nb = K // 32
     isums = torch.zeros(M * N * nb, dtype=torch.int32, device="cuda")
+    s0 = _weights(mi, ctx, wq, t, K, N, route)
     ctx.set_mmq_kernel(_kernel(mi, route))
     try:
-        ctx.mul_mat_block_dots(mi.from_torch(dev(wq), t, [K, N]), mi.from_torch(dev(x), mi.F32, [K, M]),
-                               isums.data_ptr())
+        ctx.mul_mat_block_dots(s0, mi.from_torch(dev(x), mi.F32, [K, M]), isums.data_ptr())
         ctx.synchronize()
     finally:
-        ctx.set_mmq_kernel(mi.MMQ_F16)
+        ctx.set_mmq_kernel(mi.MMQ_AUTO)
     got = isums.cpu().numpy().reshape(M, N, nb)
     wv, _, _ = orc.decode_blocks(t, wq, K)
     xv, _, _ = orc.decode_blocks(orc.VEC_DOT_TYPE[t], orc.from_float(orc.VEC_DOT_TYPE[t], x), K)
@@ -102,3 +120,60 @@ def test_route_integer_exact(mi, ctx, orc, route):
     out = _run(mi, ctx, wq.reshape(N, -1), orc.Q8_0, K, N, x, route).cpu().numpy()
     exact = x.astype(np.int64) @ q.astype(np.int64).T
     assert np.array_equal(out, exact.astype(np.float32))
+
+
+@pytest.mark.parametrize("tname", ["q8_0", "q4_0", "q4_1"])
+def test_prepared_layout_and_rejections(mi, ctx, orc, tname):
+    """Prepared-weight sizes (quants, then fp16 d, then Q4_1's fp16 m, each
+    part 256-byte aligned), the no-allocation entry point on a prepared
+    weight, and the calls that must refuse one."""
+    t = orc.NAME_TYPE[tname]
+    M, N, K = 200, 150, 96 + 32  # 4 blocks per row
+    w = orc.normal(N * K, seed=9, stream=1, std=0.02).reshape(N, K)
+    wq = orc.quantize_weights(t, w)
+    wt = mi.from_torch(dev(wq.view(np.uint8)), t, [K, N])
+    al = lambda v: (v + 255) // 256 * 256
+    dp = 4
+    want = al(N * K) + al(N * dp * 2) * (2 if tname == "q4_1" else 1)
+    assert mi.weight_prepared_nbytes(wt) == want
+    pt = _prepare(mi, ctx, wt)
+    assert pt.layout == mi.LAYOUT_INT8 and list(pt.ne) == [K, N, 1, 1]
+    assert mi.lib().mi355_tensor_nbytes(mi.C.byref(pt)) == want
+    # mul_mat and mul_mat_noalloc on the prepared weight: the raw weight's bits
+    x = dev(orc.normal(M * K, seed=9, stream=2).reshape(M, K))
+    outs = [torch.full((M, N), float("nan"), device="cuda") for _ in range(3)]
+    ctx.mul_mat(wt, mi.from_torch(x, mi.F32, [K, M]), mi.from_torch(outs[0], mi.F32, [N, M]))
+    ctx.mul_mat(pt, mi.from_torch(x, mi.F32, [K, M]), mi.from_torch(outs[1], mi.F32, [N, M]))
+    ctx.mul_mat_noalloc(pt, mi.from_torch(x, mi.F32, [K, M]), mi.from_torch(outs[2], mi.F32, [N, M]))
+    ctx.synchronize()
+    assert torch.equal(outs[1], outs[0]) and torch.equal(outs[2], outs[0])
+
+    def status(fn):
+        try:
+            fn()
+        except mi.Mi355Error as e:
+            return e.status
+        return 0
+
+    INVALID, UNSUP = -4, -3
+    buf = torch.empty(want + 512, dtype=torch.uint8, device="cuda")
+    base = buf.data_ptr() + (-buf.data_ptr()) % 256
+    assert status(lambda: ctx.weight_prepare(wt, base + 16, want)) == INVALID       # dst not 256-aligned
+    assert status(lambda: ctx.weight_prepare(wt, base, want - 1)) == INVALID        # dst too small
+    assert status(lambda: ctx.weight_prepare(pt, base, want)) == INVALID            # already prepared
+    w3 = mi.from_torch(dev(np.concatenate([wq, wq]).view(np.uint8)), t, [K, N, 2])  # 3-D weight
+    assert mi.weight_prepared_nbytes(w3) == 0
+    assert status(lambda: ctx.weight_prepare(w3, base, want * 2)) == INVALID
+    x3 = torch.zeros((2, M, K), device="cuda")
+    d3 = torch.zeros((2, M, N), device="cuda")
+    assert status(lambda: ctx.mul_mat(pt, mi.from_torch(x3, mi.F32, [K, M, 2]),
+                                      mi.from_torch(d3, mi.F32, [N, M, 2]))) == UNSUP
+    # a prepared tensor is not a ggml tensor for any other operand or op
+    assert status(lambda: ctx.mul_mat(wt, pt, mi.from_torch(outs[0], mi.F32, [N, M]))) == INVALID
+    assert status(lambda: ctx.quantize_rows(t, mi.ACT_X86, pt, base)) == INVALID
+    qf = torch.zeros((64, 4), dtype=torch.float16, device="cuda")
+    of = torch.zeros((4, 64), dtype=torch.float32, device="cuda")
+    qt = mi.from_torch(qf, mi.F16, [64, 4, 1, 1])
+    fake = mi.make_tensor(qf.data_ptr(), mi.F16, [64, 4, 1, 1])
+    fake.layout = mi.LAYOUT_INT8
+    assert status(lambda: ctx.flash_attn_ext(fake, qt, qt, mi.from_torch(of, mi.F32, [64, 1, 4, 1]), 0.125)) == INVALID
