@@ -3,9 +3,13 @@
 Workload ("step"): the SAM3 ViT block linear set at 72x72 = 5184 tokens --
 qkv [3072x1024], attn-out [1024x1024], fc1 [4736x1024], fc2 [1024x4736] --
 once with Q8_0 weights and once with Q4_0 weights (8 ggml mul_mat calls,
-each quantizing its f32 activations to Q8_0 and running the int8 MFMA GEMM).
-Weights are quantized from f32 N(0,0.02), activations f32 N(0,1) (seed 0);
-all inputs are resident in HBM before timing.
+each quantizing its f32 activations to one-byte Q8_0 quants and running the
+int8 MFMA GEMM).  Weights are quantized from f32 N(0,0.02) and prepared once
+at setup (mi355_weight_prepare, as a model load would); activations f32
+N(0,1) (seed 0), one buffer per call so that no call re-reads another's
+activations from the last-level cache; all inputs are resident in HBM before
+timing.  The same calls with the weights in the ggml layout (repacked on
+every call) are timed after the step and reported as raw_layout_tops.
 
 value = int8 ops of the step (2*M*N*K per GEMM) / step time, in TOPS.
 
@@ -35,6 +39,18 @@ M_TOK = 5184
 LINEARS = [("qkv", 3072, 1024), ("proj", 1024, 1024), ("fc1", 4736, 1024), ("fc2", 1024, 4736)]
 TYPES = ["q8_0", "q4_0"]
 ALL_TYPES = ["q8_0", "q4_0", "q4_1", "f16"]
+
+
+def cpu_model() -> str:
+    """The host CPU's model string (/proc/cpuinfo), or "unknown"."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def load_pkg():
@@ -381,7 +397,7 @@ def main():
         # child profiler runs first, before this process initialises the GPU
         log("bench: HBM traffic of mmq_q8_0 fc1 (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
         try:
-            traffic = measure_traffic("q8_0/fc1", "mmq_kernel<8")
+            traffic = measure_traffic("q8_0/fc1", "mmq8_kernel<8")
         except Exception as e:  # profiler missing or failed: traffic stays unmeasured
             log(f"bench: traffic measurement failed: {e!r}")
 
@@ -461,9 +477,10 @@ def main():
     log("bench: generating inputs")
     x1024 = orc.normal(M_TOK * 1024, seed=0, stream=2).reshape(M_TOK, 1024)
     x4736 = orc.normal(M_TOK * 4736, seed=0, stream=3).reshape(M_TOK, 4736)
-    xs = {1024: torch.from_numpy(x1024).to(dev), 4736: torch.from_numpy(x4736).to(dev)}
-    calls = []  # (tname, lname, N, K, s0, s1, d)
+    xhost = {1024: x1024, 4736: x4736}
+    calls = []  # (tname, lname, N, K, s0 prepared, s1, d, s0 in the ggml layout)
     host_w = {}
+    keep = []
     types = TYPES
     if args.op:
         types = [args.op.split("/")[0]]
@@ -474,11 +491,17 @@ def main():
             wq = orc.quantize_weights(t, w)
             host_w[(tname, lname)] = wq
             wd = torch.from_numpy(wq).to(dev)
+            wt = mi.from_torch(wd, t, [K, N])
+            nbw = mi.weight_prepared_nbytes(wt)
+            wbuf = torch.empty(nbw + 256, dtype=torch.uint8, device=dev)
+            s0 = ctx.weight_prepare(wt, wbuf.data_ptr() + (-wbuf.data_ptr()) % 256, nbw)
+            xd = torch.from_numpy(xhost[K]).to(dev)  # this call's own activations
             dst = torch.empty((M_TOK, N), dtype=torch.float32, device=dev)
-            s0 = mi.from_torch(wd, t, [K, N])
-            s1 = mi.from_torch(xs[K], mi.F32, [K, M_TOK])
+            s1 = mi.from_torch(xd, mi.F32, [K, M_TOK])
             d = mi.from_torch(dst, mi.F32, [N, M_TOK])
-            calls.append((tname, lname, N, K, s0, s1, d))
+            keep.append((wbuf, xd))
+            calls.append((tname, lname, N, K, s0, s1, d, wt))
+    ctx.synchronize()
     if args.op:
         c = [c for c in calls if f"{c[0]}/{c[1]}" == args.op][0]
         for _ in range(args.op_warmup):
@@ -523,24 +546,37 @@ def main():
         per_call_ms[(c[0], c[1])] = {k: v[1] / v[0] for k, v in prof.items()}
     ctx.profile(False)
     log("bench: per-call kernel times " + json.dumps({f"{a}/{b}": v for (a, b), v in per_call_ms.items()}))
+    # the same calls with the weights in the ggml layout (the int8 route repacks them on each call)
+    ctx.profile(True)
+    raw_call_ms = {}
+    for c in calls:
+        for _ in range(5):
+            ctx.mul_mat(c[7], c[5], c[6])
+        prof = ctx.profile_collect()
+        raw_call_ms[(c[0], c[1])] = {k: v[1] / v[0] for k, v in prof.items()}
+    ctx.profile(False)
+    log("bench: per-call kernel times, ggml-layout weights " +
+        json.dumps({f"{a}/{b}": v for (a, b), v in raw_call_ms.items()}))
 
-    type_tops = {}
+    type_tops, raw_tops = {}, {}
     for tname in TYPES:
         tot = sum(sum(per_call_ms[(tname, ln)].values()) for (ln, _, _) in LINEARS)
         type_tops[tname] = ops_by_type[tname] / (tot * 1e-3) / 1e12
+        tot = sum(sum(raw_call_ms[(tname, ln)].values()) for (ln, _, _) in LINEARS)
+        raw_tops[tname] = ops_by_type[tname] / (tot * 1e-3) / 1e12
 
     # ---- roofline of the dominant kernel: MMQ Q8_0 at the fc1 shape
     N, K = 4736, 1024
-    mmq_ms = per_call_ms[("q8_0", "fc1")]["mmq_q8_0"]
+    mmq_ms = per_call_ms[("q8_0", "fc1")]["mmq8_q8_0"]
     w_bytes = N * (K // 32) * 34
-    a_bytes = M_TOK * K + M_TOK * (K // 32) * 4      # int8 activations + fp32 scales
+    a_bytes = M_TOK * K + M_TOK * (K // 32) * 4      # int8 activation quants + scale dwords
     d_bytes = M_TOK * N * 4
     alg_bytes = w_bytes + a_bytes + d_bytes
     achieved = alg_bytes / (mmq_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": traffic["bytes"] if traffic else None,
-                "kernel": "mmq_q8_0 fc1 [5184x1024]x[4736x1024]", "kernel_us": round(mmq_ms * 1e3, 2),
+                "kernel": "mmq8_q8_0 fc1 [5184x1024]x[4736x1024]", "kernel_us": round(mmq_ms * 1e3, 2),
                 "alg_bytes": alg_bytes,
                 "traffic_counters": traffic,
                 "int8_tops": round(2.0 * M_TOK * N * K / (mmq_ms * 1e-3) / 1e12, 1)}
@@ -555,7 +591,7 @@ def main():
     neck_res = None
     if not args.no_encoder:
         log("bench: encoder weights")
-        del calls
+        del calls, keep
         torch.cuda.empty_cache()
         hp, pre, blocks, keep = build_encoder(mi, orc, torch, dev, TYPES)
         encoder = {}
@@ -576,26 +612,27 @@ def main():
             neck_res[tn] = bench_neck(mi, ctx, torch, dims, sc, xn, outs_n, 3)
             del keep_n
 
-    # ---- CPU baseline: the oracle's ggml-cpu restatement, same fc1 Q8_0 mul_mat
+    # ---- CPU baseline: the oracle's ggml-cpu restatement of the same fc1 Q8_0 mul_mat
+    # (from_float + vec_dot, AVX2 when the host has it), median of 5 after 2 warmups
     cpu = None
     if not args.no_cpu_baseline:
         log("bench: cpu baseline")
         wq = host_w[("q8_0", "fc1")]
         nth = orc.nthreads()
-        rows = 1296  # a quarter of the 5184 tokens per call
-        xs_cpu = np.ascontiguousarray(x1024[:rows])
-        orc.mul_mat(wq, orc.Q8_0, K, N, xs_cpu[None, None])  # warm
-        reps, t0 = 0, time.perf_counter()
-        while True:
+        xs_cpu = np.ascontiguousarray(x1024)
+        times = []
+        for i in range(7):
+            t0 = time.perf_counter()
             orc.mul_mat(wq, orc.Q8_0, K, N, xs_cpu[None, None])
-            reps += 1
-            el = time.perf_counter() - t0
-            if el > 10.0 or reps >= 50:
-                break
-        cpu_tops = reps * 2.0 * rows * N * K / el / 1e12
+            if i >= 2:
+                times.append(time.perf_counter() - t0)
+        med = float(np.median(times))
+        cpu_tops = 2.0 * M_TOK * N * K / med / 1e12
         cpu = {"value": round(cpu_tops, 4), "unit": "TOPS", "cores": nth, "kind": "port",
-               "sample": f"fc1 Q8_0 mul_mat (quantize + block dots), {rows} of 5184 tokens x 4736 x 1024, "
-                         f"{reps} reps in {el:.1f} s, isa={'avx2' if orc.lib().orc_isa_path() == 1 else 'scalar'}"}
+               "sample": f"fc1 Q8_0 mul_mat (quantize + block dots) 5184 x 4736 x 1024, median of 5 after 2 "
+                         f"warmups: {med * 1e3:.1f} ms; {nth} threads (the box's CPU share for one GPU) of "
+                         f"nproc={os.cpu_count()}, isa={'avx2' if orc.lib().orc_isa_path() == 1 else 'scalar'}, "
+                         f"cpu={cpu_model()}"}
 
     value = step_ops / (ms_step * 1e-3) / 1e12
     out = {
@@ -615,6 +652,7 @@ def main():
                    "tokens": M_TOK, "linears": [f"{n}x{k}" for (_, n, k) in LINEARS], "weight_types": TYPES},
         "pct_int8_peak": round(100.0 * value / INT8_PEAK_TOPS, 2),
         "type_tops": {k: round(v, 2) for k, v in type_tops.items()},
+        "raw_layout_tops": {k: round(v, 2) for k, v in raw_tops.items()},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "vit_encoder_1008": encoder,
