@@ -135,10 +135,19 @@ def bench_attention(mi, ctx, torch, dev, only=None, reps=20):
     return res
 
 
-def build_encoder(mi, orc, torch, dev, types, seed=0):
+def prepare_weight(mi, ctx, torch, dev, wt, keep):
+    """wt prepared once (mi355_weight_prepare) into a new device buffer, as a model load would."""
+    n = mi.weight_prepared_nbytes(wt)
+    buf = torch.empty(n + 256, dtype=torch.uint8, device=dev)
+    keep.append(buf)
+    return ctx.weight_prepare(wt, buf.data_ptr() + (-buf.data_ptr()) % 256, n)
+
+
+def build_encoder(mi, orc, torch, dev, types, seed=0, ctx=None):
     """Random-init SAM3 ViT (1008^2 image, patch 14, E 1024, 32 blocks, 16 heads,
     MLP 4736, windows of 24 except global blocks 7/15/23/31): per type, the
-    32 blocks' linear weights quantized from the same f32 N(0,0.02) draws."""
+    32 blocks' linear weights quantized from the same f32 N(0,0.02) draws and,
+    with a context, prepared for the int8 kernel."""
     E, NH, MLP, WS, G, P, PG = 1024, 16, 4736, 24, 72, 14, 24
     HD = E // NH
     hp = mi.VitHparams(E, NH, MLP, WS, G, P, PG, 1e-5)
@@ -171,7 +180,10 @@ def build_encoder(mi, orc, torch, dev, types, seed=0):
             t = orc.NAME_TYPE[tn]
             blk = mi.VitBlock()
             for name, (w, n, k) in ws.items():
-                setattr(blk, name + "_w", mi.from_torch(up(orc.quantize_weights(t, w)), t, [k, n]))
+                wt = mi.from_torch(up(orc.quantize_weights(t, w)), t, [k, n])
+                if ctx is not None and mi.weight_prepared_nbytes(wt):
+                    wt = prepare_weight(mi, ctx, torch, dev, wt, keep)
+                setattr(blk, name + "_w", wt)
             for name, tsr in vec.items():
                 setattr(blk, name, tsr.data_ptr())
             blk.freqs_cis = (f_glob if glob else f_win).data_ptr()
@@ -467,7 +479,7 @@ def main():
         return
     if args.op and args.op.startswith("vit/"):
         tn = args.op.split("/")[1]
-        hp, pre, blocks, keep = build_encoder(mi, orc, torch, dev, [tn])
+        hp, pre, blocks, keep = build_encoder(mi, orc, torch, dev, [tn], ctx=ctx)
         res = bench_encoder(mi, ctx, torch, dev, hp, pre, blocks[tn], args.reps)
         print(json.dumps({"op": args.op, **res}), flush=True)
         ctx.close()
@@ -593,7 +605,7 @@ def main():
         log("bench: encoder weights")
         del calls, keep
         torch.cuda.empty_cache()
-        hp, pre, blocks, keep = build_encoder(mi, orc, torch, dev, TYPES)
+        hp, pre, blocks, keep = build_encoder(mi, orc, torch, dev, TYPES, ctx=ctx)
         encoder = {}
         for tn in TYPES:
             log(f"bench: encoder {tn}")

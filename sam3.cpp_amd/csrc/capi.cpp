@@ -383,6 +383,11 @@ int act_mode_for(int t) {
     }
 }
 
+int act_mode_for_weight(const mi355_tensor* w) {
+    if (w->layout == MI355_LAYOUT_INT8) return w->type == T_Q4_1 ? ACT_I8S : ACT_I8;
+    return act_mode_for(w->type);
+}
+
 // MUL_MAT of a prequantized operand with a fused epilogue in place of dst
 // (dst [M][N] F32 is only a shape here: nothing is written to it).
 mi355_status mul_mat_epi(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const MmqEpi& e) {
@@ -399,11 +404,57 @@ mi355_status mul_mat_epi(mi355_context* ctx, const mi355_tensor* s0, const ActF1
     return mul_mat_act(ctx, s0, a, &d, &e);
 }
 
+// mul_mat_act for a prepared weight: the int8 kernel over an ACT_I8 / ACT_I8S operand.
+mi355_status mul_mat_act_i8(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const mi355_tensor* d,
+                            const MmqEpi* epi) {
+    const bool q41 = s0->type == T_Q4_1;
+    if (!a.d || !a.dh || (q41 && !a.s) || a.dp != mmq_scale_pitch(a.K) || a.s1 != a.K)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat_act: int8 operand scales missing or wrong pitch");
+    mi355_tensor s1{};
+    s1.type = T_F32;
+    s1.ne[0] = a.K;
+    s1.ne[1] = a.M;
+    s1.ne[2] = s1.ne[3] = 1;
+    s1.nb[0] = 4;
+    s1.nb[1] = 4 * a.K;
+    s1.nb[2] = s1.nb[3] = s1.nb[1] * a.M;
+    s1.data = const_cast<void*>(a.q);
+    mi355_status st = check_mul_mat(ctx, s0, &s1, d);
+    if (st != MI355_STATUS_SUCCESS) return st;
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "mul_mat_act: null context");
+    (void)hipSetDevice(ctx->device);
+    const int64_t N = s0->ne[1];
+    ActI8 a8;
+    a8.q = a.q;
+    a8.s1 = a.s1;
+    a8.dl = static_cast<const uint32_t*>(a.d);
+    a8.dh = static_cast<const uint32_t*>(a.dh);
+    a8.s = q41 ? a.s : nullptr;
+    a8.nst = a.dp / 2;
+    a8.M = a.M;
+    a8.K = a.K;
+    const WRep wr = wrep_view(s0->type, N, a.K, s0->data);
+    if (!mmq8_supported(wr, a8)) return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat_act: operands beyond the int8 kernel");
+    const int ks = epi || dst_split_ok(d) ? mmq_ksplit(s0->type, a.M, N, a.K, 1, ctx->cus) : 1;
+    const size_t part = ks > 1 ? align_up((size_t)ks * (size_t)a.M * (size_t)N * 4) : 0;
+    if (part) {
+        st = ensure_ws(ctx, part);
+        if (st != MI355_STATUS_SUCCESS) return st;
+    }
+    const MmqSplit sp{ks, ks > 1 ? static_cast<float*>(ctx->ws) : nullptr, false};
+    static const char* names[3][3] = {{"mmq8_q8_0", "mmq8_q8_0+residual", "mmq8_q8_0+qkv"},
+                                      {"mmq8_q4_0", "mmq8_q4_0+residual", "mmq8_q4_0+qkv"},
+                                      {"mmq8_q4_1", "mmq8_q4_1+residual", "mmq8_q4_1+qkv"}};
+    const int ti = s0->type == T_Q8_0 ? 0 : s0->type == T_Q4_0 ? 1 : 2;
+    Timed tq(ctx, names[ti][epi ? epi->kind : 0]);
+    return hip_check(ctx, tq.done(launch_mmq8(wr, a8, matd_of(d), epi, sp, ctx->stream)), "mmq8 launch");
+}
+
 mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF16& a, const mi355_tensor* d,
                          const MmqEpi* epi) {
     if (!s0 || !a.q) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat_act: null operand");
-    if (s0->layout != MI355_LAYOUT_GGML)
-        return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat_act: the fused passes take weights in the ggml layout");
+    if (s0->layout == MI355_LAYOUT_INT8) return mul_mat_act_i8(ctx, s0, a, d, epi);
+    if (s0->layout != MI355_LAYOUT_GGML) return fail(ctx, MI355_STATUS_INVALID_ARG, "mul_mat_act: unknown weight layout");
     const int mode = act_mode_for(s0->type);
     if (mode == ACT_F32) return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat_act: no prequantized path for type %d", s0->type);
     if (mode != ACT_F16 && (!a.d || (mode == ACT_Q8S && !a.s) || a.dp != mmq_scale_pitch(a.K)))
@@ -515,8 +566,9 @@ mi355_status flash_attn_act(mi355_context* ctx, const mi355_tensor* q, const mi3
     a.out = ActOut{ACT_F32, nullptr, nullptr, nullptr, nullptr, 0};
     if (op) {
         const int64_t K = q->ne[2] * D;
-        if (op->mode == ACT_F32 || !op->q || (op->mode != ACT_F16 && (!op->d || (op->mode == ACT_Q8S && !op->s) ||
-                                                                    op->dp != mmq_scale_pitch(K))))
+        if (op->mode == ACT_F32 || !op->q ||
+            (op->mode != ACT_F16 && (!op->d || (act_has_sums(op->mode) && !op->s) || (op->mode >= ACT_I8 && !op->dh) ||
+                                     op->dp != mmq_scale_pitch(K))))
             return fail(ctx, MI355_STATUS_INVALID_ARG, "flash_attn_ext: bad operand output");
         a.out = *op;
     }

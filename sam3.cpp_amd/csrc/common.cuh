@@ -114,37 +114,59 @@ __device__ __forceinline__ float group_sum(float v) {
 // half to even), or F16 / F32 rows.  A lane holds 4 consecutive values, chunk
 // c of the row (elements 4c..4c+3); the 8 lanes holding chunks 8k..8k+7 (lanes
 // congruent to them mod 8, all active) hold one block and reduce it together.
+// Scale (and Q8_1 sum) of block b of a quantized operand row, with the padding
+// slot of the last block: fp16 [row][dp] for the fp16-MFMA operand, the dl / dh
+// dword arrays for the int8 one.
+__device__ __forceinline__ void act_store_scale(const ActOut& o, int64_t row, int64_t K, int64_t b, float d, int isum) {
+    const int64_t nb = K / 32;
+    if (o.mode >= ACT_I8) {
+        uint32_t* dl = reinterpret_cast<uint32_t*>(o.d);
+        const int64_t i = row * (o.dp / 2) + b / 2;
+        if ((b & 1) == 0) dl[i] = (uint32_t)f2h(d);
+        else o.dh[i] = (uint32_t)f2h(d) << 16;
+        if (b == nb - 1 && (nb & 1)) o.dh[i] = 0;  // the missing odd block of an odd count
+    } else {
+        o.d[row * o.dp + b] = f2h(d);
+        if (b == nb - 1 && o.dp > nb) o.d[row * o.dp + b + 1] = 0;  // the even-pitch padding slot
+    }
+    if (act_has_sums(o.mode)) {
+        o.s[row * o.dp + b] = f2h(d * (float)isum);
+        if (b == nb - 1 && o.dp > nb) o.s[row * o.dp + b + 1] = 0;
+    }
+}
+
+// Four consecutive values (chunk c of a row of K) into the operand; for the
+// quantized modes the 8 lanes holding chunks 8j .. 8j + 7 are consecutive
+// lanes of one group and quantize block j together (ggml from_float, x86).
 __device__ __forceinline__ void act_store_chunk(const ActOut& o, int64_t row, int64_t K, int64_t c, v4f x) {
     if (o.mode == ACT_F32) {
         *reinterpret_cast<v4f*>(o.y + row * K + 4 * c) = x;
         return;
     }
-    uint32_t h0, h1;
     if (o.mode == ACT_F16) {
-        h0 = (uint32_t)f2h(x[0]) | ((uint32_t)f2h(x[1]) << 16);
-        h1 = (uint32_t)f2h(x[2]) | ((uint32_t)f2h(x[3]) << 16);
-    } else {
-        float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
-        amax = group_max<8>(amax);
-        const float d = amax / 127.0f;
-        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-        const int q0 = (int)rintf(x[0] * id), q1 = (int)rintf(x[1] * id);
-        const int q2 = (int)rintf(x[2] * id), q3 = (int)rintf(x[3] * id);
-        h0 = (uint32_t)f2h((float)q0) | ((uint32_t)f2h((float)q1) << 16);
-        h1 = (uint32_t)f2h((float)q2) | ((uint32_t)f2h((float)q3) << 16);
-        int isum = 0;
-        if (o.mode == ACT_Q8S) isum = group_sum_i<8>(q0 + q1 + q2 + q3);
-        if ((c & 7) == 0) {
-            const int64_t b = c >> 3;
-            o.d[row * o.dp + b] = f2h(d);
-            if (o.mode == ACT_Q8S) o.s[row * o.dp + b] = f2h(d * (float)isum);
-            if (b == K / 32 - 1 && o.dp > K / 32) {  // zero the even-pitch padding slot
-                o.d[row * o.dp + b + 1] = 0;
-                if (o.mode == ACT_Q8S) o.s[row * o.dp + b + 1] = 0;
-            }
-        }
+        const uint32_t h0 = (uint32_t)f2h(x[0]) | ((uint32_t)f2h(x[1]) << 16);
+        const uint32_t h1 = (uint32_t)f2h(x[2]) | ((uint32_t)f2h(x[3]) << 16);
+        *reinterpret_cast<uint2*>(o.q + row * K + 4 * c) = make_uint2(h0, h1);
+        return;
     }
-    *reinterpret_cast<uint2*>(o.q + row * K + 4 * c) = make_uint2(h0, h1);
+    float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+    amax = group_max<8>(amax);
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    const int q0 = (int)rintf(x[0] * id), q1 = (int)rintf(x[1] * id);
+    const int q2 = (int)rintf(x[2] * id), q3 = (int)rintf(x[3] * id);
+    int isum = 0;
+    if (act_has_sums(o.mode)) isum = group_sum_i<8>(q0 + q1 + q2 + q3);
+    if ((c & 7) == 0) act_store_scale(o, row, K, c >> 3, d, isum);
+    if (o.mode >= ACT_I8) {
+        const uint32_t b4 = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+                            ((uint32_t)(q3 & 0xff) << 24);
+        *reinterpret_cast<uint32_t*>(reinterpret_cast<int8_t*>(o.q) + row * K + 4 * c) = b4;
+    } else {
+        const uint32_t h0 = (uint32_t)f2h((float)q0) | ((uint32_t)f2h((float)q1) << 16);
+        const uint32_t h1 = (uint32_t)f2h((float)q2) | ((uint32_t)f2h((float)q3) << 16);
+        *reinterpret_cast<uint2*>(o.q + row * K + 4 * c) = make_uint2(h0, h1);
+    }
 }
 
 // ggml_norm -> mul(w) -> add(b) of one row of C held by a group of G lanes
@@ -216,18 +238,11 @@ __device__ __forceinline__ void act_store_lane32(const ActOut& o, int64_t row, i
     const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
     const int q = valid ? (int)rintf(v * id) : 0;
     int isum = 0;
-    if (o.mode == ACT_Q8S) isum = group_sum_i<32>(q);
+    if (act_has_sums(o.mode)) isum = group_sum_i<32>(q);
     if (valid) {
-        o.q[row * K + e] = f2h((float)q);
-        if ((e & 31) == 0) {
-            const int64_t b = e / 32;
-            o.d[row * o.dp + b] = f2h(d);
-            if (o.mode == ACT_Q8S) o.s[row * o.dp + b] = f2h(d * (float)isum);
-            if (b == K / 32 - 1 && o.dp > K / 32) {
-                o.d[row * o.dp + b + 1] = 0;
-                if (o.mode == ACT_Q8S) o.s[row * o.dp + b + 1] = 0;
-            }
-        }
+        if (o.mode >= ACT_I8) reinterpret_cast<int8_t*>(o.q)[row * K + e] = (int8_t)q;
+        else o.q[row * K + e] = f2h((float)q);
+        if ((e & 31) == 0) act_store_scale(o, row, K, e / 32, d, isum);
     }
 }
 

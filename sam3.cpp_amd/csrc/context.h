@@ -60,6 +60,9 @@ mi355_status ensure_buffer(mi355_context* ctx, void** buf, size_t* size, size_t 
 // The activation layout a producer pass should write for weights of type t:
 // Q8 quants for Q8_0/Q4_0, Q8 with Q8_1 sums for Q4_1, F16 for F16, F32 otherwise.
 int act_mode_for(int weight_type);
+// The same for a weight tensor: a prepared weight (MI355_LAYOUT_INT8) takes the
+// int8 operand (ACT_I8, or ACT_I8S for Q4_1).
+int act_mode_for_weight(const mi355_tensor* w);
 // MUL_MAT of weights s0 with an activation operand already in the layout
 // act_mode_for(s0->type) describes (a: quants or F16 rows, scales), as a
 // fused producer pass writes it; dst F32 [N][M] rows.  Same validation and

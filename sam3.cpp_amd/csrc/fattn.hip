@@ -375,25 +375,23 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
                         x[i] = rintf(x[i] * sc);
                         isum += (int)x[i];
                     }
-                    if (o.mode == ACT_Q8S)
+                    if (act_has_sums(o.mode))
                         isum += __builtin_amdgcn_ds_bpermute(((int)__lane_id() ^ 32) << 2, isum);
-                    if (g == 0) {
-                        const int64_t blk = ((int64_t)h * D + 32 * db) / 32;
-                        const float dd = amax / 127.0f;
-                        o.d[row * o.dp + blk] = f2h(dd);
-                        if (o.mode == ACT_Q8S) o.s[row * o.dp + blk] = f2h(dd * (float)isum);
-                        if (blk == K / 32 - 1 && o.dp > K / 32) {  // zero the even-pitch padding slot
-                            o.d[row * o.dp + blk + 1] = 0;
-                            if (o.mode == ACT_Q8S) o.s[row * o.dp + blk + 1] = 0;
-                        }
-                    }
+                    if (g == 0) act_store_scale(o, row, K, ((int64_t)h * D + 32 * db) / 32, amax / 127.0f, isum);
                 }
 #pragma unroll
                 for (int i4 = 0; i4 < 4; ++i4) {
                     const int d = 32 * db + 8 * i4 + 4 * g;
-                    const uint32_t h0 = (uint32_t)f2h(x[4 * i4]) | ((uint32_t)f2h(x[4 * i4 + 1]) << 16);
-                    const uint32_t h1 = (uint32_t)f2h(x[4 * i4 + 2]) | ((uint32_t)f2h(x[4 * i4 + 3]) << 16);
-                    *reinterpret_cast<uint2*>(qrow + d) = make_uint2(h0, h1);
+                    if (o.mode >= ACT_I8) {
+                        const uint32_t b4 = (uint32_t)((int)x[4 * i4] & 0xff) | ((uint32_t)((int)x[4 * i4 + 1] & 0xff) << 8) |
+                                            ((uint32_t)((int)x[4 * i4 + 2] & 0xff) << 16) |
+                                            ((uint32_t)((int)x[4 * i4 + 3] & 0xff) << 24);
+                        *reinterpret_cast<uint32_t*>(reinterpret_cast<int8_t*>(o.q) + row * K + (int64_t)h * D + d) = b4;
+                    } else {
+                        const uint32_t h0 = (uint32_t)f2h(x[4 * i4]) | ((uint32_t)f2h(x[4 * i4 + 1]) << 16);
+                        const uint32_t h1 = (uint32_t)f2h(x[4 * i4 + 2]) | ((uint32_t)f2h(x[4 * i4 + 3]) << 16);
+                        *reinterpret_cast<uint2*>(qrow + d) = make_uint2(h0, h1);
+                    }
                 }
             }
         }

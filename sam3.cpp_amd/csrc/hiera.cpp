@@ -80,20 +80,23 @@ struct Sizes {
     }
 };
 
-// a GEMM activation operand of rows x K in one buffer: q [rows][K] fp16, then
-// d and s [rows][dp] fp16
+// a GEMM activation operand of rows x K in one buffer: q [rows][K] fp16 (or
+// int8), then the scales (fp16 [rows][dp], or the int8 operand's dl and dh
+// dword arrays [rows][dp / 2] each), then s [rows][dp] fp16
 struct Operand {
     uint16_t *q, *d, *s;
+    uint32_t* dh;
 };
 size_t operand_bytes(size_t rows, size_t K, Operand* o = nullptr, char* base = nullptr) {
     const size_t dp = (size_t)mmq_scale_pitch((int64_t)K);
-    const size_t qb = align_up(rows * K * 2), sb = align_up(rows * dp * 2);
+    const size_t qb = align_up(rows * K * 2), db = align_up(rows * dp * 4), sb = align_up(rows * dp * 2);
     if (o && base) {
         o->q = reinterpret_cast<uint16_t*>(base);
         o->d = reinterpret_cast<uint16_t*>(base + qb);
-        o->s = reinterpret_cast<uint16_t*>(base + qb + sb);
+        o->dh = reinterpret_cast<uint32_t*>(base + qb) + rows * (dp / 2);
+        o->s = reinterpret_cast<uint16_t*>(base + qb + db);
     }
-    return qb + 2 * sb;
+    return qb + db + sb;
 }
 
 Sizes block_sizes(const Info& b, int S) {
@@ -227,13 +230,15 @@ mi355_status get_bufs(mi355_context* ctx, const mi355_hiera_hparams* hp, const s
 
 // the activation mode a producer writes for a GEMM over K inputs with weights W
 int fused_mode(const mi355_context* ctx, const mi355_tensor& W, int64_t K) {
-    return ctx->fuse && K % 32 == 0 ? act_mode_for(W.type) : ACT_F32;
+    return ctx->fuse && K % 32 == 0 ? act_mode_for_weight(&W) : ACT_F32;
 }
 
 ActOut act_out(char* base, int mode, int64_t rows, int64_t K) {
     Operand o;
     operand_bytes((size_t)rows, (size_t)K, &o, base);
-    return ActOut{mode, nullptr, o.q, o.d, o.s, mmq_scale_pitch(K)};
+    ActOut a{mode, nullptr, o.q, o.d, o.s, mmq_scale_pitch(K)};
+    if (mode >= ACT_I8) a.dh = o.dh;
+    return a;
 }
 
 ActF16 act_in(char* base, int mode, int64_t rows, int64_t K) {
@@ -244,7 +249,8 @@ ActF16 act_in(char* base, int mode, int64_t rows, int64_t K) {
     a.s1 = K;
     a.s2 = a.s3 = K * rows;
     a.d = mode == ACT_F16 ? nullptr : o.d;
-    a.s = mode == ACT_Q8S ? o.s : nullptr;
+    a.s = act_has_sums(mode) ? o.s : nullptr;
+    if (mode >= ACT_I8) a.dh = o.dh;
     a.dp = mmq_scale_pitch(K);
     a.M = rows;
     a.K = K;

@@ -34,13 +34,18 @@ struct ActF16 {
     const void* s;
     int64_t dp;
     int64_t M, K;
+    const void* dh = nullptr;  // int8 operand (ACT_I8*): q int8 [M][s1], d = dl and dh [M][dp / 2] dwords
 };
 inline int64_t mmq_scale_pitch(int64_t K) { return ((K / 32) + 1) & ~(int64_t)1; }
 
 // Output of a pass that feeds a MUL_MAT: F32 rows (y), F16 rows (q as fp16
-// values: the operand of F16 weights), or the quantized operand (q fp16
-// quants [rows][K], d [rows][dp], and Q8_1 sums s for Q4_1 weights).
-enum { ACT_F32 = 0, ACT_F16 = 1, ACT_Q8 = 2, ACT_Q8S = 3 };
+// values: the operand of F16 weights), the quantized operand of the fp16-MFMA
+// kernel (q fp16 quants [rows][K], d [rows][dp], and Q8_1 sums s for Q4_1
+// weights), or that of the int8 kernel for prepared weights (q int8 quants
+// [rows][K]; d as two dword arrays [rows][dp / 2]: d (dl) holds the scale of
+// an even block in the low half, dh that of an odd block in the high half,
+// zero for a missing odd block; s as before).
+enum { ACT_F32 = 0, ACT_F16 = 1, ACT_Q8 = 2, ACT_Q8S = 3, ACT_I8 = 4, ACT_I8S = 5 };
 struct ActOut {
     int mode;
     float* y;
@@ -48,7 +53,9 @@ struct ActOut {
     uint16_t* d;
     uint16_t* s;
     int64_t dp;
+    uint32_t* dh = nullptr;
 };
+__host__ __device__ inline bool act_has_sums(int mode) { return mode == ACT_Q8S || mode == ACT_I8S; }
 
 // ggml from_float into contiguous ggml rows: type 8 (Q8_0), 9 (Q8_1), 1 (F16).
 hipError_t launch_quantize_ggml(const SrcView& src, int type, bool ref_variant, void* dst, hipStream_t st);

@@ -51,8 +51,9 @@ size_t enc_bytes(const mi355_vit_hparams* hp, EncBufs* b, char* base) {
     const size_t big = M * std::max((size_t)hp->mlp_dim, kpatch) * 4;
     const size_t H = (size_t)hp->mlp_dim;
     const size_t dpe = (size_t)mmq_scale_pitch((int64_t)E), dph = (size_t)mmq_scale_pitch((int64_t)H);
+    // operand scales: fp16 [M][dp], or the int8 operand's dl and dh dword arrays (4 bytes per block)
     const size_t sz[13] = {M * E * 4, M * 3 * E * 4, M * E * 2, M * E * 2, M * E * 2,   M * E * 4,  big,
-                           M * E * 2, M * dpe * 2,   M * dpe * 2, M * H * 2, M * dph * 2, M * dph * 2};
+                           M * E * 2, M * dpe * 4,   M * dpe * 2, M * H * 2, M * dph * 4, M * dph * 2};
     size_t off[13], o = 0;
     for (int i = 0; i < 13; ++i) {
         off[i] = o;
@@ -109,10 +110,13 @@ mi355_tensor dev_tensor(const void* p, int type, int64_t ne0, int64_t ne1, int64
 }
 
 // a GEMM activation operand (q, d, s) with K inputs over M rows: the E-wide
-// one (aq, ad, as) or fc2's (hq, hd, hs)
-ActOut act_out(const EncBufs& b, int mode, int64_t K, bool hidden = false) {
-    return hidden ? ActOut{mode, nullptr, b.hq, b.hd, b.hs, mmq_scale_pitch(K)}
-                  : ActOut{mode, nullptr, b.aq, b.ad, b.as, mmq_scale_pitch(K)};
+// one (aq, ad, as) or fc2's (hq, hd, hs); the int8 operand's dh array follows
+// dl in the scale buffer
+ActOut act_out(const EncBufs& b, int mode, int64_t M, int64_t K, bool hidden = false) {
+    ActOut o = hidden ? ActOut{mode, nullptr, b.hq, b.hd, b.hs, mmq_scale_pitch(K)}
+                      : ActOut{mode, nullptr, b.aq, b.ad, b.as, mmq_scale_pitch(K)};
+    if (mode >= ACT_I8) o.dh = reinterpret_cast<uint32_t*>(o.d) + M * (o.dp / 2);
+    return o;
 }
 ActF16 act_in(const EncBufs& b, int mode, int64_t M, int64_t K, bool hidden = false) {
     ActF16 a;
@@ -120,10 +124,11 @@ ActF16 act_in(const EncBufs& b, int mode, int64_t M, int64_t K, bool hidden = fa
     a.s1 = K;
     a.s2 = a.s3 = K * M;
     a.d = mode == ACT_F16 ? nullptr : hidden ? b.hd : b.ad;
-    a.s = mode == ACT_Q8S ? (hidden ? b.hs : b.as) : nullptr;
+    a.s = act_has_sums(mode) ? (hidden ? b.hs : b.as) : nullptr;
     a.dp = mmq_scale_pitch(K);
     a.M = M;
     a.K = K;
+    if (mode >= ACT_I8) a.dh = reinterpret_cast<const uint32_t*>(a.d) + M * (a.dp / 2);  // after dl, as act_out puts it
     return a;
 }
 
@@ -299,7 +304,7 @@ mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams
     // LN -> the GEMM's activation operand (fused) or F32 rows
     auto ln_gemm = [&](const float* w, const float* bb, int ws, const mi355_tensor& W, float* out, int64_t N,
                        const MmqEpi* epi) -> mi355_status {
-        const int mode = ctx->fuse ? act_mode_for(W.type) : ACT_F32;
+        const int mode = ctx->fuse ? act_mode_for_weight(&W) : ACT_F32;
         if (mode == ACT_F32 && epi) return fail(ctx, MI355_STATUS_FAILED, "vit: epilogue without a fused operand");
         if (mode == ACT_F32) {
             mi355_status s1 = mi355_vit_layer_norm(ctx, x, nullptr, 0, w, bb, b.xn, M, E, G, ws, hp->eps);
@@ -313,7 +318,7 @@ mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams
         a.add_grid = 0;
         a.w = w;
         a.b = bb;
-        a.out = act_out(b, mode, E);
+        a.out = act_out(b, mode, M, E);
         a.rows = M;
         a.E = E;
         a.grid = G;
@@ -330,7 +335,7 @@ mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams
     };
     // attention
     // LN1 -> qkv (+ bias, q/k/v split, RoPE, fp16: fused epilogue)
-    if (ctx->fuse && act_mode_for(blk->qkv_w.type) != ACT_F32) {
+    if (ctx->fuse && act_mode_for_weight(&blk->qkv_w) != ACT_F32) {
         MmqEpi e{};
         e.kind = MMQ_EPI_QKV;
         e.bias = blk->qkv_b;
@@ -347,11 +352,11 @@ mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams
         TRY(mi355_vit_qkv_rope(ctx, b.qkv, blk->qkv_b, blk->freqs_cis, b.q, b.k, b.v, M, N, NH, HD));
     }
     // attention; for quantized / F16 proj weights it writes the projection's operand
-    const int mp = ctx->fuse ? act_mode_for(blk->proj_w.type) : ACT_F32;
+    const int mp = ctx->fuse ? act_mode_for_weight(&blk->proj_w) : ACT_F32;
     {
         const mi355_tensor q = dev_tensor(b.q, T_F16, HD, N, NH, B), k = dev_tensor(b.k, T_F16, HD, N, NH, B),
                            v = dev_tensor(b.v, T_F16, HD, N, NH, B), o = dev_tensor(b.attn, T_F32, HD, NH, N, B);
-        const ActOut op = act_out(b, mp, E);
+        const ActOut op = act_out(b, mp, M, E);
         TRY(flash_attn_act(ctx, &q, &k, &v, nullptr, 1.0f / sqrtf((float)HD), 0.0f, 0.0f, &o,
                            mp == ACT_F32 ? nullptr : &op));
     }
@@ -370,13 +375,13 @@ mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams
         TRY(mul_mat_epi(ctx, &blk->proj_w, act_in(b, mp, M, E), e));
     }
     // MLP: fc1, bias + GELU writing fc2's operand, fc2 (+ bias, residual: fused epilogue)
-    const int m2 = ctx->fuse && MLP % 32 == 0 ? act_mode_for(blk->fc2_w.type) : ACT_F32;
+    const int m2 = ctx->fuse && MLP % 32 == 0 ? act_mode_for_weight(&blk->fc2_w) : ACT_F32;
     TRY(ln_gemm(blk->norm2_w, blk->norm2_b, 0, blk->fc1_w, b.big, MLP, nullptr));
     if (m2 == ACT_F32) {
         TRY(mi355_vit_bias_gelu(ctx, b.big, blk->fc1_b, M, MLP));
     } else {
         Timed t(ctx, "bias_gelu");
-        TRY(hip_check(ctx, t.done(launch_bias_gelu_act(b.big, blk->fc1_b, M, MLP, act_out(b, m2, MLP, true), ctx->stream)),
+        TRY(hip_check(ctx, t.done(launch_bias_gelu_act(b.big, blk->fc1_b, M, MLP, act_out(b, m2, M, MLP, true), ctx->stream)),
                       "bias_gelu launch"));
     }
     if (m2 == ACT_F32) {
