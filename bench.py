@@ -199,7 +199,7 @@ def build_encoder(mi, orc, torch, dev, types, seed=0, ctx=None):
     return hp, pre, blocks, keep
 
 
-def build_hiera(mi, orc, torch, dev, tname, seed=0):
+def build_hiera(mi, orc, torch, dev, tname, seed=0, ctx=None):
     """Random-init SAM2.1 Hiera-tiny (img 1024, embed 96, heads 1, stages
     1/2/7/2, windows 8/4/14/7, global blocks 5/7/9, q_pool 3): linear weights
     f32 N(0,0.02) quantized to tname; the patch weight is F16 under F16 weights
@@ -223,7 +223,10 @@ def build_hiera(mi, orc, torch, dev, tname, seed=0):
             shapes.append(("dim_proj", cout, cin))
         for j, (name, n, k) in enumerate(shapes):
             w = orc.normal(n * k, seed + i, 400 + j, std=0.02).reshape(n, k)
-            setattr(blk, name + "_w", mi.from_torch(up(orc.quantize_weights(t, w)), t, [k, n]))
+            wt = mi.from_torch(up(orc.quantize_weights(t, w)), t, [k, n])
+            if ctx is not None and mi.weight_prepared_nbytes(wt):
+                wt = prepare_weight(mi, ctx, torch, dev, wt, keep)
+            setattr(blk, name + "_w", wt)
         for j, (name, n, sc, m) in enumerate([("norm1_w", cin, 0.1, 1.0), ("norm1_b", cin, 0.02, 0.0),
                                               ("qkv_b", 3 * cout, 0.02, 0.0), ("proj_b", cout, 0.02, 0.0),
                                               ("norm2_w", cout, 0.1, 1.0), ("norm2_b", cout, 0.02, 0.0),
@@ -394,6 +397,8 @@ def main():
                          "copy (256 MiB device copy)")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--op-warmup", type=int, default=20)
+    ap.add_argument("--raw-weights", action="store_true",
+                    help="encoders: quantized weights in the ggml layout (fp16 kernels) instead of prepared")
     ap.add_argument("--no-fuse", action="store_true",
                     help="encoder modes: run the unfused pass sequence (f32 activations between the ggml node groups)")
     ap.add_argument("--no-traffic", action="store_true",
@@ -443,7 +448,7 @@ def main():
         ctx.set_fusion(False)
     if args.op and args.op.startswith("hiera/"):
         tn = args.op.split("/")[1]
-        hp, pre, blocks, outs, keep = build_hiera(mi, orc, torch, dev, tn)
+        hp, pre, blocks, outs, keep = build_hiera(mi, orc, torch, dev, tn, ctx=None if args.raw_weights else ctx)
         res = bench_hiera(mi, ctx, torch, hp, pre, blocks, outs, args.reps)
         print(json.dumps({"op": args.op, **res}), flush=True)
         ctx.close()
@@ -479,7 +484,7 @@ def main():
         return
     if args.op and args.op.startswith("vit/"):
         tn = args.op.split("/")[1]
-        hp, pre, blocks, keep = build_encoder(mi, orc, torch, dev, [tn], ctx=ctx)
+        hp, pre, blocks, keep = build_encoder(mi, orc, torch, dev, [tn], ctx=None if args.raw_weights else ctx)
         res = bench_encoder(mi, ctx, torch, dev, hp, pre, blocks[tn], args.reps)
         print(json.dumps({"op": args.op, **res}), flush=True)
         ctx.close()
@@ -605,7 +610,7 @@ def main():
         log("bench: encoder weights")
         del calls, keep
         torch.cuda.empty_cache()
-        hp, pre, blocks, keep = build_encoder(mi, orc, torch, dev, TYPES, ctx=ctx)
+        hp, pre, blocks, keep = build_encoder(mi, orc, torch, dev, TYPES, ctx=None if args.raw_weights else ctx)
         encoder = {}
         for tn in TYPES:
             log(f"bench: encoder {tn}")
@@ -614,7 +619,7 @@ def main():
         hiera = {}
         for tn in ("f16", "q4_0"):
             log(f"bench: hiera-tiny {tn}")
-            hp_h, pre_h, blocks_h, outs_h, keep_h = build_hiera(mi, orc, torch, dev, tn)
+            hp_h, pre_h, blocks_h, outs_h, keep_h = build_hiera(mi, orc, torch, dev, tn, ctx=None if args.raw_weights else ctx)
             hiera[tn] = bench_hiera(mi, ctx, torch, hp_h, pre_h, blocks_h, outs_h, 5)
             del keep_h
         neck_res = {}

@@ -443,7 +443,9 @@ mi355_status mi355_model_file_load(mi355_context* ctx, const mi355_model_file* f
  * "vit.pos_embed", "vit.ln_pre.*", "vit.blocks.N.*"), weights in the file's
  * weight type when their rows are whole blocks and F32 otherwise, as the
  * reference registers them; the hyperparameters of mi355_vit_encode derived as
- * sam3_load_hparams does.  The tables stay valid until mi355_vit_weights_free. */
+ * sam3_load_hparams does.  Quantized linear weights (Q8_0 / Q4_0 / Q4_1) are
+ * handed out prepared (mi355_weight_prepare).  The tables stay valid until
+ * mi355_vit_weights_free. */
 typedef struct mi355_vit_weights mi355_vit_weights;
 mi355_status mi355_vit_weights_load(mi355_context* ctx, const mi355_model_file* f, mi355_vit_weights** out);
 void mi355_vit_weights_free(mi355_vit_weights* w);
@@ -477,8 +479,9 @@ mi355_status mi355_model_quantize(mi355_context* ctx, const char* in_path, const
  * transitions), weights in the file's weight type when their rows are whole
  * blocks and F32 otherwise; the hyperparameters of sam2_load_hparams
  * (sam3.cpp:1568-1590); pos_embed [S0*S0][E] (S0 = img/4) computed by
- * mi355_hiera_pos_embed from the two tables.  Everything mi355_hiera_encode
- * takes besides the image; valid until mi355_hiera_weights_free. */
+ * mi355_hiera_pos_embed from the two tables; quantized linear weights
+ * prepared (mi355_weight_prepare).  Everything mi355_hiera_encode takes besides
+ * the image; valid until mi355_hiera_weights_free. */
 typedef struct mi355_hiera_weights mi355_hiera_weights;
 mi355_status mi355_hiera_weights_load(mi355_context* ctx, const mi355_model_file* f, mi355_hiera_weights** out);
 void mi355_hiera_weights_free(mi355_hiera_weights* w);

@@ -292,6 +292,7 @@ struct Uploader {
     const mi355_model_file* f;
     std::vector<void*>* allocs;
     const char* what;
+    std::vector<void*> raw;  // ggml-layout weights whose prepared forms replace them
     mi355_status load(const std::string& name, int type, std::initializer_list<int64_t> ne, void** dptr,
                       mi355_tensor* t) {
         const int idx = mi355_model_file_find(f, name.c_str());
@@ -321,6 +322,39 @@ struct Uploader {
             t->nb[3] = t->nb[2] * want[2];
             t->data = d;
         }
+        return MI355_STATUS_SUCCESS;
+    }
+    // A 2-D Q8_0 / Q4_0 / Q4_1 weight is replaced by its prepared form
+    // (mi355_weight_prepare: the int8 kernel's layout); other tensors stay as loaded.
+    mi355_status prepare(mi355_tensor* t) {
+        const size_t n = mi355_weight_prepared_nbytes(t);
+        if (n == 0) return MI355_STATUS_SUCCESS;
+        void* d = nullptr;
+        if (hipMalloc(&d, n) != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(ctx, MI355_STATUS_ALLOC_FAILED, "%s: cannot place a prepared weight (%zu bytes)", what, n);
+        }
+        allocs->push_back(d);
+        mi355_tensor pt;
+        const mi355_status st = mi355_weight_prepare(ctx, t, d, n, &pt);
+        if (st != MI355_STATUS_SUCCESS) return st;
+        raw.push_back(t->data);
+        *t = pt;
+        return MI355_STATUS_SUCCESS;
+    }
+    // Waits for the repacks, then frees the ggml-layout copies they read.
+    mi355_status finish() {
+        const mi355_status st = mi355_synchronize(ctx);
+        if (st != MI355_STATUS_SUCCESS) return st;
+        for (void* p : raw) {
+            for (auto it = allocs->begin(); it != allocs->end(); ++it)
+                if (*it == p) {
+                    allocs->erase(it);
+                    break;
+                }
+            (void)hipFree(p);
+        }
+        raw.clear();
         return MI355_STATUS_SUCCESS;
     }
 };
@@ -411,7 +445,10 @@ mi355_status mi355_vit_weights_load(mi355_context* ctx, const mi355_model_file* 
             return bad(st);
         b.freqs_cis = static_cast<const float*>(p);
         b.is_global = global ? 1 : 0;
+        for (mi355_tensor* t : {&b.qkv_w, &b.proj_w, &b.fc1_w, &b.fc2_w})
+            if ((st = up.prepare(t)) != MI355_STATUS_SUCCESS) return bad(st);
     }
+    if ((st = up.finish()) != MI355_STATUS_SUCCESS) return bad(st);
     *out = w;
     return MI355_STATUS_SUCCESS;
 }
@@ -511,9 +548,10 @@ mi355_status mi355_hiera_weights_load(mi355_context* ctx, const mi355_model_file
             if ((st = up.load(pre + ".proj.bias", T_F32, {dout}, &p, nullptr)) != MI355_STATUS_SUCCESS) return bad(st);
             b.dim_proj_b = static_cast<const float*>(p);
         }
+        for (mi355_tensor* t : {&b.qkv_w, &b.proj_w, &b.fc1_w, &b.fc2_w, &b.dim_proj_w})
+            if (t->data && (st = up.prepare(t)) != MI355_STATUS_SUCCESS) return bad(st);
     }
-    if ((st = hip_check(ctx, hipStreamSynchronize(ctx->stream), "hiera_weights_load")) != MI355_STATUS_SUCCESS)
-        return bad(st);
+    if ((st = up.finish()) != MI355_STATUS_SUCCESS) return bad(st);
     *out = w;
     return MI355_STATUS_SUCCESS;
 }

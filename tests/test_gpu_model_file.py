@@ -98,6 +98,8 @@ def test_vit_from_file(mi, ctx, orc, tmp_path, tname, ftype):
         assert (hp.embed_dim, hp.num_heads, hp.mlp_dim, hp.window_size, hp.grid, hp.patch_size, hp.pos_grid) == \
             (g["E"], g["NH"], g["MLP"], g["ws"], g["G"], g["P"], g["pg"])
         assert n == 2 and blocks[0].is_global == 0 and blocks[1].is_global == 1
+        quantized = t in (orc.Q8_0, orc.Q4_0, orc.Q4_1)
+        assert blocks[0].fc1_w.layout == (mi.LAYOUT_INT8 if quantized else mi.LAYOUT_GGML)  # prepared at load
         img = torch.from_numpy(orc.uniform(3 * g["img"] ** 2, 4, 1).reshape(3, g["img"], g["img"])).cuda()
         x_file = torch.empty((g["G"] ** 2, g["E"]), dtype=torch.float32, device="cuda")
         ctx.vit_encode(hp, C.c_void_p(img.data_ptr()), pw, C.c_void_p(pos), C.c_void_p(lw), C.c_void_p(lb),
