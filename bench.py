@@ -462,6 +462,9 @@ def main():
         xm = torch.from_numpy(orc.normal(M * K, seed=0, stream=71).reshape(M, K)).to(dev)
         dst = torch.empty((M, N), dtype=torch.float32, device=dev)
         s0, s1 = mi.from_torch(wd, t, [K, N]), mi.from_torch(xm, mi.F32, [K, M])
+        keep_w = []
+        if not args.raw_weights and mi.weight_prepared_nbytes(s0):
+            s0 = prepare_weight(mi, ctx, torch, dev, s0, keep_w)  # as the bench step's weights
         d = mi.from_torch(dst, mi.F32, [N, M])
         for _ in range(args.op_warmup):
             ctx.mul_mat(s0, s1, d)
