@@ -397,6 +397,8 @@ def main():
                          "copy (256 MiB device copy)")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--op-warmup", type=int, default=20)
+    ap.add_argument("--mmq-kernel", choices=["auto", "f16", "int8"], default="auto",
+                    help="kernel of MUL_MATs with ggml-layout Q8_0/Q4_0/Q4_1 weights (mi355_context_set_mmq_kernel)")
     ap.add_argument("--raw-weights", action="store_true",
                     help="encoders: quantized weights in the ggml layout (fp16 kernels) instead of prepared")
     ap.add_argument("--no-fuse", action="store_true",
@@ -423,6 +425,7 @@ def main():
 
     mi = load_pkg()
     ctx = mi.Context(0)
+    ctx.set_mmq_kernel({"auto": mi.MMQ_AUTO, "f16": mi.MMQ_F16, "int8": mi.MMQ_INT8}[args.mmq_kernel])
     dev = torch.device("cuda:0")
 
     if args.op == "copy":
