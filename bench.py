@@ -16,7 +16,9 @@ value = int8 ops of the step (2*M*N*K per GEMM) / step time, in TOPS.
 Also reported: per-type TOPS and %% of the int8 dense MFMA peak, the
 dominant kernel's roofline (the fc1 Q8_0 MMQ kernel, timed with HIP events
 on its stream through the library's kernel-timing hook), and a CPU baseline
-(the oracle's ggml-cpu restatement of the same mul_mat, AVX2, on the host).
+(the oracle's ggml-cpu restatement of the same mul_mat, AVX2, on the host;
+beside it the SAM3 ViT encoder per frame from one windowed and one global
+block of the oracle's block composition, extrapolated x28 / x4).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -143,6 +145,56 @@ def prepare_weight(mi, ctx, torch, dev, wt, keep):
     return ctx.weight_prepare(wt, buf.data_ptr() + (-buf.data_ptr()) % 256, n)
 
 
+def vit_block_host(orc, i, seed=0):
+    """Block i's f32 vectors (LayerNorm weights near 1, biases N(0, 0.02)) and
+    f32 N(0, 0.02) linear weights [out][in], as host arrays."""
+    E, MLP = 1024, 4736
+    vec = {}
+    for j, (name, n, sc, m) in enumerate([("norm1_w", E, 0.1, 1.0), ("norm1_b", E, 0.02, 0.0),
+                                          ("qkv_b", 3 * E, 0.02, 0.0), ("proj_b", E, 0.02, 0.0),
+                                          ("norm2_w", E, 0.1, 1.0), ("norm2_b", E, 0.02, 0.0),
+                                          ("fc1_b", MLP, 0.02, 0.0), ("fc2_b", E, 0.02, 0.0)]):
+        vec[name] = orc.normal(n, seed + i, 200 + j) * np.float32(sc) + np.float32(m)
+    ws = {}
+    for j, (name, n, k) in enumerate([("qkv", 3 * E, E), ("proj", E, E), ("fc1", MLP, E), ("fc2", E, MLP)]):
+        ws[name] = (orc.normal(n * k, seed + i, 100 + j, std=0.02).reshape(n, k), n, k)
+    return vec, ws
+
+
+def cpu_encoder_baseline(orc, tname, reps, warmup):
+    """SAM3 ViT encoder time per 1008^2 frame on the host cores, from the
+    oracle's composition of sam3_vit_block_forward (ggml-cpu's algorithms:
+    quantized mul_mat with Q8_0 activations, F32 flash attention, LayerNorm,
+    RoPE, GELU-erf): one windowed block (block 0) and one global block
+    (block 7) on N(0, 1) tokens, extrapolated as 28 windowed + 4 global
+    blocks, the extrapolation of tests/test_metal_overhead.cpp:249-252.
+    Each block time is the median of reps runs after warmup runs."""
+    from oracle import blocks as ob
+    E, NH, MLP, WS, G = 1024, 16, 4736, 24, 72
+    t = orc.NAME_TYPE[tname]
+    x = orc.normal(G * G * E, 0, 310).reshape(G * G, E)
+    res = {}
+    for name, i, glob in (("windowed", 0, False), ("global", 7, True)):
+        vec, ws = vit_block_host(orc, i)
+        host = {k: (orc.quantize_weights(t, w), n, kk) for k, (w, n, kk) in ws.items()}
+        freqs = ob.axial_cis(orc, E // NH, G, WS / G) if glob else ob.axial_cis(orc, E // NH, WS, 1.0)
+        times = []
+        for r in range(warmup + reps):
+            t0 = time.perf_counter()
+            out = ob.vit_block_ref(orc, t, x, host, vec, E, NH, MLP, G, 0 if glob else WS, freqs, False)
+            if r >= warmup:
+                times.append(time.perf_counter() - t0)
+        if not np.isfinite(out).all():
+            raise RuntimeError("cpu encoder baseline: non-finite block output")
+        res[name] = float(np.median(times))
+    frame = 28 * res["windowed"] + 4 * res["global"]
+    nth = orc.nthreads()
+    return {"ms_per_frame": round(frame * 1e3, 1), "windowed_block_ms": round(res["windowed"] * 1e3, 1),
+            "global_block_ms": round(res["global"] * 1e3, 1), "cores": nth, "kind": "port",
+            "sample": f"{tname} SAM3 ViT: one windowed and one global block (median of {reps} after {warmup} "
+                      f"warmups each), x28 + x4; {nth} threads of nproc={os.cpu_count()}, cpu={cpu_model()}"}
+
+
 def build_encoder(mi, orc, torch, dev, types, seed=0, ctx=None):
     """Random-init SAM3 ViT (1008^2 image, patch 14, E 1024, 32 blocks, 16 heads,
     MLP 4736, windows of 24 except global blocks 7/15/23/31): per type, the
@@ -167,15 +219,8 @@ def build_encoder(mi, orc, torch, dev, types, seed=0, ctx=None):
     blocks = {tn: [] for tn in types}
     for i in range(32):
         glob = i in (7, 15, 23, 31)
-        vec = {}
-        for j, (name, n, sc, m) in enumerate([("norm1_w", E, 0.1, 1.0), ("norm1_b", E, 0.02, 0.0),
-                                              ("qkv_b", 3 * E, 0.02, 0.0), ("proj_b", E, 0.02, 0.0),
-                                              ("norm2_w", E, 0.1, 1.0), ("norm2_b", E, 0.02, 0.0),
-                                              ("fc1_b", MLP, 0.02, 0.0), ("fc2_b", E, 0.02, 0.0)]):
-            vec[name] = up(orc.normal(n, seed + i, 200 + j) * np.float32(sc) + np.float32(m))
-        ws = {}
-        for j, (name, n, k) in enumerate([("qkv", 3 * E, E), ("proj", E, E), ("fc1", MLP, E), ("fc2", E, MLP)]):
-            ws[name] = (orc.normal(n * k, seed + i, 100 + j, std=0.02).reshape(n, k), n, k)
+        vec_h, ws = vit_block_host(orc, i, seed)
+        vec = {name: up(a) for name, a in vec_h.items()}
         for tn in types:
             t = orc.NAME_TYPE[tn]
             blk = mi.VitBlock()
@@ -387,6 +432,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-encoder-reps", type=int, default=1,
+                    help="CPU encoder baseline: timed runs per block (median), 0 to skip")
+    ap.add_argument("--cpu-encoder-warmup", type=int, default=0, help="CPU encoder baseline: untimed runs per block")
     ap.add_argument("--no-encoder", action="store_true", help="skip the full ViT encoder ms/frame")
     ap.add_argument("--frames", type=int, default=3, help="timed encoder frames per weight type")
     ap.add_argument("--op", default=None,
@@ -656,6 +704,11 @@ def main():
                          f"warmups: {med * 1e3:.1f} ms; {nth} threads (the box's CPU share for one GPU) of "
                          f"nproc={os.cpu_count()}, isa={'avx2' if orc.lib().orc_isa_path() == 1 else 'scalar'}, "
                          f"cpu={cpu_model()}"}
+
+        if args.cpu_encoder_reps > 0 and not args.no_encoder:
+            log("bench: cpu encoder baseline (one windowed + one global Q8_0 block)")
+            cpu["vit_encoder_1008"] = cpu_encoder_baseline(orc, "q8_0", args.cpu_encoder_reps,
+                                                           args.cpu_encoder_warmup)
 
     value = step_ops / (ms_step * 1e-3) / 1e12
     out = {

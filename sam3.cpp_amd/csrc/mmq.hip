@@ -29,6 +29,7 @@
 // unit.  Workgroups are numbered so each XCD (round-robin dispatch) walks a
 // contiguous band of the tile order, which groups a few m-tiles and walks
 // n-tiles inside a group (L2 reuse of the resident workgroups' operands).
+#include <atomic>
 #include <algorithm>
 #include <type_traits>
 
@@ -994,20 +995,21 @@ static hipError_t try_skinny(const MatW& w, const ActF16& a, const MatD& d, int6
     p.wpitch = wpitch;
     const unsigned grid = (unsigned)((a.M + 32 * smt - 1) / (32 * smt));
     // dynamic LDS beyond 64 KB, allowed once per kernel and device (the attribute is
-    // per device); concurrent first calls only repeat the same setting
+    // per device); host threads making their first calls together may each set it,
+    // which repeats the same setting, and the flags are atomics so that is no data race
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return hipSuccess;
-    static bool attr[64][6] = {};
+    static std::atomic<bool> attr[64][6] = {};
     const int ti = (w.type == T_Q8_0 ? 0 : w.type == T_Q4_0 ? 1 : 2) * 2 + (smt == 4 ? 1 : 0);
     const void* fns[6] = {(const void*)mmq_skinny_kernel<T_Q8_0, 2>, (const void*)mmq_skinny_kernel<T_Q8_0, 4>,
                           (const void*)mmq_skinny_kernel<T_Q4_0, 2>, (const void*)mmq_skinny_kernel<T_Q4_0, 4>,
                           (const void*)mmq_skinny_kernel<T_Q4_1, 2>, (const void*)mmq_skinny_kernel<T_Q4_1, 4>};
-    if (!attr[dev][ti]) {
+    if (!attr[dev][ti].load(std::memory_order_acquire)) {
         if (hipFuncSetAttribute(fns[ti], hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024) != hipSuccess) {
             (void)hipGetLastError();  // not done: the tiled kernel takes it
             return hipSuccess;
         }
-        attr[dev][ti] = true;
+        attr[dev][ti].store(true, std::memory_order_release);
     }
     switch (ti) {
         case 0: mmq_skinny_kernel<T_Q8_0, 2><<<grid, 256, lds, st>>>(p); break;

@@ -77,9 +77,13 @@ bool read_at(int fd, uint64_t off, void* dst, size_t n) {
 int64_t block_bytes(int type) { return type == T_Q8_0 ? 34 : type == T_Q4_0 ? 18 : type == T_Q4_1 ? 20 : 0; }
 
 // bytes of a tensor record's data as sam3_load_tensors computes them
+// (false for an unknown type, a row not made of whole blocks, or an element
+// count whose f32 size does not fit in int64: the dequantized copy must fit too)
 bool data_bytes(int type, const int64_t ne[4], uint64_t* out) {
-    int64_t n = 1;
-    for (int i = 0; i < 4; ++i) n *= ne[i];
+    int64_t n = 1, n4 = 0;
+    for (int i = 0; i < 4; ++i)
+        if (ne[i] <= 0 || __builtin_mul_overflow(n, ne[i], &n)) return false;
+    if (__builtin_mul_overflow(n, (int64_t)4, &n4)) return false;
     if (type == T_F32) *out = (uint64_t)n * 4;
     else if (type == T_F16) *out = (uint64_t)n * 2;
     else if (block_bytes(type)) {
@@ -175,8 +179,9 @@ mi355_status mi355_model_file_open(const char* path, mi355_model_file** out) {
         if (!data_bytes(r.type, r.ne, &r.nbytes))
             return bad(MI355_STATUS_UNSUPPORTED, "model_file_open: tensor '%s' has an unsupported type or shape", r.name);
         r.offset = pos;
+        if (pos > f->size || r.nbytes > f->size - pos)
+            return bad(MI355_STATUS_FAILED, "model_file_open: tensor '%s' runs past the end", r.name);
         pos += r.nbytes;
-        if (pos > f->size) return bad(MI355_STATUS_FAILED, "model_file_open: tensor '%s' runs past the end", r.name);
         if (!f->by_name.emplace(r.name, t).second)
             return bad(MI355_STATUS_INVALID_ARG, "model_file_open: duplicate tensor '%s'", r.name);
         f->tensors.push_back(std::move(r));
@@ -714,17 +719,20 @@ mi355_status mi355_model_quantize(mi355_context* ctx, const char* in_path, const
         if (!rd(ne, 4 * (size_t)n_dims) || !rd(&name[0], name.size()))
             return finish(fail(ctx, MI355_STATUS_FAILED, "model_quantize: '%s' is truncated", in_path));
         pos += (32 - pos % 32) % 32;
-        int64_t n_el = 1, ne64[4];
+        int64_t ne64[4];
         for (int i = 0; i < 4; ++i) {
             if (ne[i] <= 0)
                 return finish(fail(ctx, MI355_STATUS_INVALID_ARG, "model_quantize: '%s' has a non-positive dimension",
                                    name.c_str()));
             ne64[i] = ne[i];
-            n_el *= ne[i];
         }
         uint64_t in_bytes = 0;
         if (!data_bytes(dtype, ne64, &in_bytes))
-            return finish(fail(ctx, MI355_STATUS_UNSUPPORTED, "model_quantize: '%s' has type %d", name.c_str(), dtype));
+            return finish(fail(ctx, MI355_STATUS_UNSUPPORTED, "model_quantize: '%s' has type %d or too many elements",
+                               name.c_str(), dtype));
+        if (pos > in_size || in_bytes > in_size - pos)
+            return finish(fail(ctx, MI355_STATUS_FAILED, "model_quantize: '%s' is truncated", in_path));
+        const int64_t n_el = ne64[0] * ne64[1] * ne64[2] * ne64[3];  // data_bytes checked 4 * n_el fits
         const bool quantize = n_dims >= 2 && ne[0] % 32 == 0 && (dtype == T_F32 || dtype == T_F16) && !keep_by_name(name);
         const int32_t dtype_out = quantize ? qtype : dtype;
         // record header with the output type, padded to a 32-byte offset of the output

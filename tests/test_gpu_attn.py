@@ -159,6 +159,27 @@ def test_flash_attn_k_row_strides(mi, ctx, orc, D):
         assert np.array_equal(got, ref), f"row stride {W}"
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_flash_attn_k_row_strides_steady_state(mi, ctx, orc, D):
+    """The same strided K through the staging loop's steady state: 2048 queries
+    x 16 heads fill 256 workgroups, so the keys are not split over workgroups
+    and each workgroup walks all 9 tiles of 576 keys (the next-but-one tile's
+    load in flight behind the current one).  A row stride of 3D halves takes
+    the K DMA staging, D + 2 the register staging; both must equal contiguous
+    K bit for bit, and contiguous K must meet the oracle on sampled queries."""
+    nq, nkv, nh = 2048, 576, 16
+    q, k, v = (_f16(a) for a in _inputs(orc, D, nq, nkv, nh, nh, 1, seed=13))
+    scale = 1.0 / np.sqrt(D)
+    ref = _gpu_fa(mi, ctx, q, k, v, scale, mi.F16, mi.F16)
+    rows = np.arange(0, nq, 97)
+    _check(orc, np.ascontiguousarray(ref[:, rows]), np.ascontiguousarray(q[:, :, rows]), k, v, scale, orc.F16)
+    for W in (3 * D, D + 2):
+        kbuf = np.full((1, nh, nkv, W), np.nan, np.float16)
+        kbuf[..., :D] = k
+        got = _gpu_fa(mi, ctx, q, kbuf, v, scale, mi.F16, mi.F16, k_nb=[2, 2 * W, 2 * W * nkv, 2 * W * nkv * nh])
+        assert np.array_equal(got, ref), f"row stride {W}"
+
+
 def test_flash_attn_rejects(mi, ctx, orc):
     D, nq, nkv = 64, 8, 8
     q, k, v = (_f16(a) for a in _inputs(orc, D, nq, nkv, 1, 1, 1))

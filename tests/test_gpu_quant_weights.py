@@ -209,3 +209,10 @@ def test_model_quantize_errors(mi, ctx, orc, tmp_path):
     W.write(p, W.MAGIC_SAM3, 3, 0, W.sam3_hparams(), good)
     assert status(p, orc.F16) == -3
     assert status(tmp_path / "missing.ggml") == -1
+    big = 2**31 - 1                                  # element count past int64
+    p = tmp_path / "huge.ggml"
+    W.write(p, W.MAGIC_SAM3, 3, 0, W.sam3_hparams(), good + [("h.weight", orc.F32, (big, big, big), np.zeros(8, np.uint8))])
+    assert status(p) == -3
+    p = tmp_path / "long.ggml"                       # 2^61 bytes claimed in a tiny file
+    W.write(p, W.MAGIC_SAM3, 3, 0, W.sam3_hparams(), good + [("l.weight", orc.F32, (2**30, 2**29), np.zeros(8, np.uint8))])
+    assert status(p) == -1

@@ -101,6 +101,13 @@ def test_rejections(mi, orc, tmp_path):
     p.write_bytes(data[:-10])
     _expect_error(mi, p, -1)                                        # truncated data
     _expect_error(mi, tmp_path / "absent.ggml", -1)
+    big = 2**31 - 1                                                 # element count past int64
+    W.write(p, W.MAGIC_SAM3, 3, 8, W.sam3_hparams(), [("huge", orc.F32, (big, big, big), np.zeros(8, np.uint8))])
+    _expect_error(mi, p, -3)
+    W.write(p, W.MAGIC_SAM3, 3, 8, W.sam3_hparams(), [("huge4", orc.F32, (big, big), np.zeros(8, np.uint8))])
+    _expect_error(mi, p, -3)                                        # 4 * count past int64
+    W.write(p, W.MAGIC_SAM3, 3, 8, W.sam3_hparams(), [("long", orc.F32, (2**30, 2**29), np.zeros(8, np.uint8))])
+    _expect_error(mi, p, -1)                                        # 2^61 bytes in a tiny file
 
 
 def test_corrupted_files_fail_cleanly(mi, orc, tmp_path):
