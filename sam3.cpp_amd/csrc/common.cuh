@@ -79,6 +79,24 @@ __device__ __forceinline__ void dma_b128(v4i rsrc, const void* lds, int voff) {
                  : "s"(__builtin_amdgcn_readfirstlane(lds_addr(lds))), "v"(voff), "s"(rsrc)
                  : "memory", "m0");
 }
+// The same with the LDS byte address already computed (m0, wave-uniform) and a
+// wave-uniform byte offset soff added in the instruction's SGPR offset field,
+// so a loop that walks K moves one SGPR instead of rebuilding descriptors.
+// Callers keep voff + soff inside the descriptor's records for every lane that
+// must load, and send a voff at or past the records (OOB) for lanes that must
+// read zero, so either range-check convention (with or without soff) agrees.
+__device__ __forceinline__ void dma_b32_so(v4i rsrc, uint32_t m0, int voff, int soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+                 :
+                 : "s"(m0), "v"(voff), "s"(rsrc), "s"(soff)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma_b128_so(v4i rsrc, uint32_t m0, int voff, int soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(m0), "v"(voff), "s"(rsrc), "s"(soff)
+                 : "memory", "m0");
+}
 
 // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt[3:0] | vmcnt[5:4] << 14, expcnt and
 // lgkmcnt left at their maxima).

@@ -131,46 +131,77 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
         aoff[i] = m0 + row < M ? (int)((int64_t)(m0 + row) * p.a_s1) + tch[i] * 16 : OOB8;
         woff[i] = n0 + row < N ? (int)((int64_t)(n0 + row) * p.w_s1) + tch[i] * 16 : OOB8;
     }
-    // scale dwords: wavefronts 0, 1 load d_a (both halves) of rows 64 (w & 1) + lane, 2 and 3
-    // d_w (and for Q4_1 wavefronts 0, 1 the Q8_1 sums, 2 and 3 the minima)
+    // scale dwords: wavefronts 0, 1 load d_a (both halves, and for Q4_1 the Q8_1 sums) of rows
+    // 64 (w & 1) + lane, 2 and 3 d_w (and for Q4_1 the minima); the d_w side loads d_w twice (the
+    // same bytes to the same LDS words) so that every wavefront issues NL DMA instructions per
+    // stage and one vmcnt wait serves both sides
     const int srow = 64 * (w & 1) + lane;
     const bool a_side = w < 2;
     const int soff = a_side ? (m0 + srow < M ? (int)((int64_t)(m0 + srow) * p.nst * 4) : OOB8)
                             : (n0 + srow < N ? (int)((int64_t)(n0 + srow) * p.nst * 4) : OOB8);
-    constexpr int NLA = 4 + 2 + (Q41 ? 1 : 0), NLW = 4 + 1 + (Q41 ? 1 : 0);  // DMA instructions per stage
+    constexpr int NS = Q41 ? 3 : 2, NL = 4 + NS;  // scale / all DMA instructions per stage and wavefront
+    // descriptors and LDS destinations, fixed for the whole K loop: stage s adds s * SKB (tiles)
+    // or 4 s (scale dwords) in the instructions' SGPR offset
+    const v4i ar = make_rsrc(Az, a_ext), wr = make_rsrc(Wz, w_ext);
+    v4i rs[NS];
+    uint32_t ls[NS];
+    {
+        const uint32_t half = 256u * (uint32_t)(w & 1);
+        if (a_side) {
+            rs[0] = make_rsrc(p.Adl + so0, sa_ext);
+            ls[0] = (uint32_t)offsetof(St, adl) + half;
+            rs[1] = make_rsrc(p.Adh + so0, sa_ext);
+            ls[1] = (uint32_t)offsetof(St, adh) + half;
+            if (Q41) {
+                rs[NS - 1] = make_rsrc(p.As + 2 * so0, sa_ext);
+                ls[NS - 1] = (uint32_t)offsetof(St, as) + half;
+            }
+        } else {
+            rs[0] = rs[1] = make_rsrc(p.Wd + 2 * so0, sw_ext);
+            ls[0] = ls[1] = (uint32_t)offsetof(St, wd) + half;
+            if (Q41) {
+                rs[NS - 1] = make_rsrc(p.Wm + 2 * so0, sw_ext);
+                ls[NS - 1] = (uint32_t)offsetof(St, wm) + half;
+            }
+        }
+    }
+    uint32_t lt[2];  // this wavefront's tile rows inside a stage buffer (A; W is SKB * B8M further)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) lt[i] = (uint32_t)offsetof(St, A) + (uint32_t)((2 * w + i) * 16 * SKB);
+    static_assert(offsetof(St, W) == offsetof(St, A) + B8M * SKB, "W follows A");
+    const uint32_t lbuf[3] = {(uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(&st0)),
+                              (uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(&st1)),
+                              (uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(&st2))};
 
-    auto dma_stage = [&](int s, St& b) __attribute__((always_inline)) {
+    // stage s into the buffer at LDS address lb; chunks past the split's K read zero
+    auto dma_stage = [&](int s, uint32_t lb) __attribute__((always_inline)) {
         const int k0 = s * SKB;
         const bool tail = k0 + SKB > K;
-        const auto ar = make_rsrc(Az + k0, a_ext - k0);
-        const auto wr = make_rsrc(Wz + k0, w_ext - k0);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const bool past = tail && k0 + tch[i] * 16 >= K;
-            dma_b128(ar, &b.A[(2 * w + i) * 16 * SKB], past ? OOB8 : aoff[i]);
-            dma_b128(wr, &b.W[(2 * w + i) * 16 * SKB], past ? OOB8 : woff[i]);
+            dma_b128_so(ar, lb + lt[i], past ? OOB8 : aoff[i], k0);
+            dma_b128_so(wr, lb + lt[i] + B8M * SKB, past ? OOB8 : woff[i], k0);
         }
-        const int so = soff == OOB8 ? OOB8 : soff + 4 * s;
-        if (a_side) {
-            dma_b32(make_rsrc(p.Adl + so0, sa_ext), &b.adl[64 * (w & 1)], so);
-            dma_b32(make_rsrc(p.Adh + so0, sa_ext), &b.adh[64 * (w & 1)], so);
-            if (Q41) dma_b32(make_rsrc(p.As + 2 * so0, sa_ext), &b.as[Q41 ? 64 * (w & 1) : 0], so);
-        } else {
-            dma_b32(make_rsrc(p.Wd + 2 * so0, sw_ext), &b.wd[64 * (w & 1)], so);
-            if (Q41) dma_b32(make_rsrc(p.Wm + 2 * so0, sw_ext), &b.wm[Q41 ? 64 * (w & 1) : 0], so);
+#pragma unroll
+        for (int j = 0; j < NS; ++j) dma_b32_so(rs[j], lb + ls[j], soff, 4 * s);
+    };
+    // the same for a stage with no chunk past K
+    auto dma_full = [&](int s, uint32_t lb) __attribute__((always_inline)) {
+        const int k0 = s * SKB;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            dma_b128_so(ar, lb + lt[i], aoff[i], k0);
+            dma_b128_so(wr, lb + lt[i] + B8M * SKB, woff[i], k0);
         }
+#pragma unroll
+        for (int j = 0; j < NS; ++j) dma_b32_so(rs[j], lb + ls[j], soff, 4 * s);
     };
     // wait until this wavefront's DMA of all but the last `later` stages issued has landed
     auto wait_dma = [&](int later) __attribute__((always_inline)) {
-        if (a_side) {
-            if (later >= 2) wait_vmcnt<2 * NLA>();
-            else if (later == 1) wait_vmcnt<NLA>();
-            else wait_vmcnt<0>();
-        } else {
-            if (later >= 2) wait_vmcnt<2 * NLW>();
-            else if (later == 1) wait_vmcnt<NLW>();
-            else wait_vmcnt<0>();
-        }
+        if (later >= 2) wait_vmcnt<2 * NL>();
+        else if (later == 1) wait_vmcnt<NL>();
+        else wait_vmcnt<0>();
     };
 
     const int wm = w & 1, wn = w >> 1;
@@ -252,9 +283,9 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
     }
 
     // prologue: stages 0..2 in flight, stage 0 published, its fragments in registers
-    dma_stage(0, st0);
-    if (nstage > 1) dma_stage(1, st1);
-    if (nstage > 2) dma_stage(2, st2);
+    dma_stage(0, lbuf[0]);
+    if (nstage > 1) dma_stage(1, lbuf[1]);
+    if (nstage > 2) dma_stage(2, lbuf[2]);
     wait_dma(min(nstage - 1, 2));
     __syncthreads();  // also publishes the zero words
     load_blk(st0, 0, f0);
@@ -307,13 +338,14 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
         }
     };
 
-    // one stage: cur holds stage s (already in registers), nxt stage s + 1
-    auto stage = [&](int s, St& cur, St& nxt) __attribute__((always_inline)) {
+    // one stage: cur (at LDS address lcur) holds stage s, whose block-0 fragments are in
+    // registers; nxt holds stage s + 1
+    auto stage = [&](int s, St& cur, St& nxt, uint32_t lcur) __attribute__((always_inline)) {
         units(s, 0, f0, cur, s == 0);
         if (s + 1 < nstage) {
             wait_dma(min(nstage - 2 - s, 1));
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            if (s + 3 < nstage) dma_stage(s + 3, cur);
+            if (s + 3 < nstage) dma_stage(s + 3, lcur);
             load_blk(nxt, 0, f0);
             load_dw(nxt, dwn);
         }
@@ -324,10 +356,38 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
             for (int i = 0; i < 2; ++i) dw[i] = dwn[i];
         }
     };
-    for (int s = 0; s < nstage; s += 3) {
-        stage(s, st0, st1);
-        if (s + 1 < nstage) stage(s + 1, st1, st2);
-        if (s + 2 < nstage) stage(s + 2, st2, st0);
+    // the steady state: 0 < s, stage s + 3 exists and has no chunk past K
+    auto stage_full = [&](int s, St& cur, St& nxt, uint32_t lcur) __attribute__((always_inline)) {
+        units(s, 0, f0, cur, false);
+        wait_vmcnt<NL>();  // stage s + 1 has landed (s + 2 may be in flight)
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        dma_full(s + 3, lcur);
+        load_blk(nxt, 0, f0);
+        load_dw(nxt, dwn);
+        units(s, 1, f1, cur, false);
+        load_blk(nxt, 1, f1);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) dw[i] = dwn[i];
+    };
+    // stages whose DMA reads no chunk past K: all, or all but a last half-filled stage
+    const int nfull = K % SKB ? nstage - 1 : nstage;
+    int s = 0;
+    // the steady state from the second group of three stages: their refills s + 3 .. s + 5 are
+    // full stages; the first group and the last (at most three) groups take the general form
+    if (5 < nfull) {
+        stage(0, st0, st1, lbuf[0]);
+        stage(1, st1, st2, lbuf[1]);
+        stage(2, st2, st0, lbuf[2]);
+        for (s = 3; s + 5 < nfull; s += 3) {
+            stage_full(s, st0, st1, lbuf[0]);
+            stage_full(s + 1, st1, st2, lbuf[1]);
+            stage_full(s + 2, st2, st0, lbuf[2]);
+        }
+    }
+    for (; s < nstage; s += 3) {
+        stage(s, st0, st1, lbuf[0]);
+        if (s + 1 < nstage) stage(s + 1, st1, st2, lbuf[1]);
+        if (s + 2 < nstage) stage(s + 2, st2, st0, lbuf[2]);
     }
     if (!DOTS) apply(acc[1][1], PI[1], PS[1]);  // the last unit (block 1, tile (1,1))
     if (DOTS) return;
