@@ -99,8 +99,17 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lr = lane & 31, g = lane >> 5;
-    const int h = blockIdx.y, b = blockIdx.z / p.kv_split, ks = blockIdx.z - b * p.kv_split;
-    const int qi = blockIdx.x * FA_BQ + w * 32 + lr;  // this lane's query
+    // XCD-aware order: workgroups go round-robin to the 8 XCDs, so workgroup g takes item
+    // (g % 8) * per_xcd + g / 8 of the (batch x key range, head, query tile) list and each
+    // XCD walks a contiguous band: the query tiles of a few heads at a time, whose K and V
+    // then stay in that XCD's L2 instead of every head's K and V passing through every L2
+    const int qtiles = (p.nq + FA_BQ - 1) / FA_BQ, items = qtiles * p.nh * p.B * p.kv_split;
+    const int per_xcd = (items + 7) / 8;
+    const int item = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (item >= items) return;
+    const int qt = item % qtiles, hz = item / qtiles, h = hz % p.nh, z = hz / p.nh;
+    const int b = z / p.kv_split, ks = z - b * p.kv_split;
+    const int qi = qt * FA_BQ + w * 32 + lr;  // this lane's query
     // a key split attends to keys kbeg .. kbeg + nkv: shifted K/V bases, the same code
     const int kbeg = ks * p.kv_chunk, nkv = min(p.nkv - kbeg, p.kv_chunk);
     const char* kb = p.k + (int64_t)(h / p.rk2) * p.k_nb2 + (int64_t)b * p.k_nb3 + (int64_t)kbeg * p.k_nb1;
@@ -322,7 +331,7 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
     }
 
     if (qi < p.nq && p.kv_split > 1) {  // this key range's unnormalised O and (max, sum)
-        const int64_t pr = ((int64_t)ks * gridDim.z / p.kv_split * p.nh + (int64_t)b * p.nh + h) * p.nq + qi;
+        const int64_t pr = ((int64_t)ks * p.B * p.nh + (int64_t)b * p.nh + h) * p.nq + qi;
         float* orow = p.part + pr * D;
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
@@ -332,7 +341,7 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
                 *reinterpret_cast<v4f*>(orow + d) = v4f{O[db][4 * i4], O[db][4 * i4 + 1], O[db][4 * i4 + 2], O[db][4 * i4 + 3]};
             }
         if (g == 0) {
-            const int64_t rows = (int64_t)gridDim.z / p.kv_split * p.nh * p.nq;
+            const int64_t rows = (int64_t)p.B * p.nh * p.nq;
             float* ml = p.part + (int64_t)p.kv_split * rows * D + pr * 2;
             ml[0] = m_run;
             ml[1] = l_run;
@@ -444,7 +453,8 @@ size_t fattn_part_bytes(int D, int nq, int nh, int B, int kv_split) {
 
 template <int D>
 static void fa_launch_d(const FaArgs& a, bool qf32, bool kvf32, int B, hipStream_t st) {
-    const dim3 grid((unsigned)((a.nq + FA_BQ - 1) / FA_BQ), (unsigned)a.nh, (unsigned)(B * a.kv_split));
+    const int64_t items = (int64_t)((a.nq + FA_BQ - 1) / FA_BQ) * a.nh * B * a.kv_split;
+    const dim3 grid((unsigned)((items + 7) / 8 * 8));
     bool launched = false;
     if constexpr (D == 64 || D == 128) {
         // fp16 K rows and bases on 16 bytes, key offsets within the 32-bit buffer offset
@@ -467,8 +477,12 @@ static void fa_launch_d(const FaArgs& a, bool qf32, bool kvf32, int B, hipStream
     }
 }
 
-hipError_t launch_fattn(const FaArgs& a, int D, bool qf32, bool kvf32, int B, hipStream_t st) {
-    if (a.nq <= 0 || a.nkv <= 0 || a.nh <= 0 || B <= 0) return hipSuccess;
+hipError_t launch_fattn(const FaArgs& a_in, int D, bool qf32, bool kvf32, int B, hipStream_t st) {
+    if (a_in.nq <= 0 || a_in.nkv <= 0 || a_in.nh <= 0 || B <= 0) return hipSuccess;
+    if ((int64_t)((a_in.nq + FA_BQ - 1) / FA_BQ) * a_in.nh * B * a_in.kv_split + 7 >= INT32_MAX)
+        return hipErrorInvalidValue;
+    FaArgs a = a_in;
+    a.B = B;
     if (a.kv_split < 1 || (a.kv_split > 1 && (!a.part || a.kv_chunk % FA_BKV != 0 ||
                                               (int64_t)(a.kv_split - 1) * a.kv_chunk >= a.nkv)))
         return hipErrorInvalidValue;

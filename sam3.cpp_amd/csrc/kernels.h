@@ -193,6 +193,7 @@ struct FaArgs {
     int negq;                   // scale < 0: Q enters negated
     ActOut out;                 // mode ACT_F32: dst; else the next MUL_MAT's operand, rows
                                 // b*nq + iq of K = nh*D (Q8 quants + scales or F16)
+    int B;                      // batch count (set by launch_fattn)
     int kv_split, kv_chunk;     // keys split into kv_split ranges of kv_chunk (a multiple of 64);
     float* part;                // > 1: per range unnormalised O [D] and (max, sum) per query,
                                 // combined by a second kernel; fattn_part_bytes() of workspace
