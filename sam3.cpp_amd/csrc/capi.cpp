@@ -308,8 +308,9 @@ mi355_status mul_mat_run(mi355_context* ctx, const mi355_tensor* s0, const mi355
             if (st != MI355_STATUS_SUCCESS) return st;
         }
         if (!mmq8_supported(wr, a8)) return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat: operands beyond the int8 kernel");
-        const MmqSplit sp8{pl.ks, pl.ks > 1 ? reinterpret_cast<float*>(ws + pl.q + pl.d + pl.s + pl.align) : nullptr,
-                           false};
+        MmqSplit sp8{pl.ks, pl.ks > 1 ? reinterpret_cast<float*>(ws + pl.q + pl.d + pl.s + pl.align) : nullptr,
+                     false};
+        sp8.cus = ctx->cus;
         const char* kname = s0->type == T_Q8_0 ? "mmq8_q8_0" : s0->type == T_Q4_0 ? "mmq8_q4_0" : "mmq8_q4_1";
         Timed tk(tctx, kname);
         return hip_check(ctx, tk.done(launch_mmq8(wr, a8, matd_of(d), nullptr, sp8, ctx->stream)), "mmq8 launch");
@@ -441,7 +442,8 @@ mi355_status mul_mat_act_i8(mi355_context* ctx, const mi355_tensor* s0, const Ac
         st = ensure_ws(ctx, part);
         if (st != MI355_STATUS_SUCCESS) return st;
     }
-    const MmqSplit sp{ks, ks > 1 ? static_cast<float*>(ctx->ws) : nullptr, false};
+    MmqSplit sp{ks, ks > 1 ? static_cast<float*>(ctx->ws) : nullptr, false};
+    sp.cus = ctx->cus;
     static const char* names[3][3] = {{"mmq8_q8_0", "mmq8_q8_0+residual", "mmq8_q8_0+qkv"},
                                       {"mmq8_q4_0", "mmq8_q4_0+residual", "mmq8_q4_0+qkv"},
                                       {"mmq8_q4_1", "mmq8_q4_1+residual", "mmq8_q4_1+qkv"}};

@@ -91,6 +91,7 @@ struct MmqSplit {
     int ks;
     float* part;
     bool skinny = true;  // K <= 128 GEMMs at large M may take the skinny kernel
+    int cus = 0;         // compute units (0: unknown); the int8 kernel sizes its tiles by it
 };
 // The split mmq_ksplit picks for a GEMM on a GPU with cus compute units.
 int mmq_ksplit(int type, int64_t M, int64_t N, int64_t K, int64_t Z, int cus);

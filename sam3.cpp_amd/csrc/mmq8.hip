@@ -65,15 +65,15 @@ struct Mmq8Args {
     int nbt;               // blocks per row of the whole K
 };
 
-template <int WT>
+template <int WT, int TM>
 struct St8 {
     static constexpr bool Q41 = WT == T_Q4_1;
-    int8_t A[B8M * SKB];
+    int8_t A[TM * SKB];
     int8_t W[B8N * SKB];
-    uint32_t adl[B8M];         // d_a of the stage's block 0 per row (low half)
-    uint32_t adh[B8M];         // d_a of block 1 per row (high half)
+    uint32_t adl[TM];          // d_a of the stage's block 0 per row (low half)
+    uint32_t adh[TM];          // d_a of block 1 per row (high half)
     uint32_t wd[B8N];          // d_w of blocks 0, 1 per row
-    uint32_t as[Q41 ? B8M : 1];
+    uint32_t as[Q41 ? TM : 1];
     uint32_t wm[Q41 ? B8N : 1];
     uint32_t zero[4];          // read by lanes 32..63 for the scale MFMA's B operand
 };
@@ -88,23 +88,30 @@ __device__ __forceinline__ int slot8(int r, int c) { return c ^ ((r >> 2) & 3); 
 //   prefetch stage s+1's block-1 fragments.
 // A unit (block, m-tile, n-tile) issues its scale MFMA and isum MFMA into
 // buffer u % 2 and combines the previous unit (across stage boundaries).
-template <int WT, int EPI, bool DOTS = false>
+// TM = 128: each wavefront computes 64 x 64 (2 x 2 MFMA tiles), two workgroups per CU.
+// TM = 64 (GEMMs whose 128-row grid leaves CUs idle): 32 x 64 per wavefront (1 x 2 tiles),
+// also two workgroups per CU (three would cap the registers at 168 and spill in the K loop).
+template <int WT, int EPI, bool DOTS = false, int TM = 128>
 __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const MmqEpi e) {
-    using St = St8<WT>;
+    using St = St8<WT, TM>;
     constexpr bool Q41 = WT == T_Q4_1;
+    constexpr int MT = TM / 64;   // 32-row MFMA tiles per wavefront
+    constexpr int WMR = 32 * MT;  // rows per wavefront (wavefronts 2 (m) x 2 (n))
+    constexpr int NU = 2 * MT;    // units (MFMA tile pairs) per block
     __shared__ __attribute__((aligned(16))) St st0;
     __shared__ __attribute__((aligned(16))) St st1;
     __shared__ __attribute__((aligned(16))) St st2;
 
-    // XCD-aware, grouped tile order (as mmq_kernel): each XCD walks a contiguous band
-    const int TT = p.tiles_m * p.tiles_n * p.ksplit;
+    // XCD-aware, grouped tile order (as mmq_kernel): each XCD walks a contiguous band. The K
+    // split is the slowest index, so the workgroups an XCD runs at once share one K range
+    const int tiles = p.tiles_m * p.tiles_n, TT = tiles * p.ksplit;
     const int per_xcd = (TT + 7) / 8;
     const int tl = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
     if (tl >= TT) return;
-    const int t = tl / p.ksplit, split = tl - t * p.ksplit;
+    const int split = tl / tiles, t = tl - split * tiles;
     const int gsz = p.gm * p.tiles_n, grp = t / gsz, gr = t - grp * gsz;
     const int gmr = min(p.gm, p.tiles_m - grp * p.gm);
-    const int m0 = (grp * p.gm + gr % gmr) * B8M, n0 = (gr / gmr) * B8N;
+    const int m0 = (grp * p.gm + gr % gmr) * TM, n0 = (gr / gmr) * B8N;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -122,24 +129,33 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
     if (tid < 4) st0.zero[tid] = st1.zero[tid] = st2.zero[tid] = 0u;
 
     // ---- DMA offsets (fixed for the whole K loop)
-    // tile instruction i of wavefront w: rows (2w + i) * 16 + lane / 4, LDS slot lane % 4
-    int aoff[2], woff[2], tch[2];
+    // A-tile instruction i of wavefront w: rows (MT w + i) * 16 + lane / 4; W-tile instruction i:
+    // rows (2w + i) * 16 + lane / 4; LDS slot lane % 4.  The global chunk a lane loads,
+    // slot8(row, lane % 4), depends on the row only through (row >> 2) & 3 = (lane >> 4) & 3.
+    const int tch = slot8(lane >> 2, lane & 3);
+    int aoff[MT], woff[2];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        const int row = (MT * w + i) * 16 + (lane >> 2);
+        aoff[i] = m0 + row < M ? (int)((int64_t)(m0 + row) * p.a_s1) + tch * 16 : OOB8;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int row = (2 * w + i) * 16 + (lane >> 2);
-        tch[i] = slot8(row, lane & 3);  // global chunk loaded into this lane's slot
-        aoff[i] = m0 + row < M ? (int)((int64_t)(m0 + row) * p.a_s1) + tch[i] * 16 : OOB8;
-        woff[i] = n0 + row < N ? (int)((int64_t)(n0 + row) * p.w_s1) + tch[i] * 16 : OOB8;
+        woff[i] = n0 + row < N ? (int)((int64_t)(n0 + row) * p.w_s1) + tch * 16 : OOB8;
     }
     // scale dwords: wavefronts 0, 1 load d_a (both halves, and for Q4_1 the Q8_1 sums) of rows
     // 64 (w & 1) + lane, 2 and 3 d_w (and for Q4_1 the minima); the d_w side loads d_w twice (the
     // same bytes to the same LDS words) so that every wavefront issues NL DMA instructions per
     // stage and one vmcnt wait serves both sides
-    const int srow = 64 * (w & 1) + lane;
+    // (TM = 64: d_a has one wavefront's worth of rows; wavefront 0 loads its low halves and
+    // wavefront 1 its high halves, Q4_1's sums loaded by both)
     const bool a_side = w < 2;
+    const int srow = (a_side && TM == 64 ? 0 : 64 * (w & 1)) + lane;
     const int soff = a_side ? (m0 + srow < M ? (int)((int64_t)(m0 + srow) * p.nst * 4) : OOB8)
                             : (n0 + srow < N ? (int)((int64_t)(n0 + srow) * p.nst * 4) : OOB8);
-    constexpr int NS = Q41 ? 3 : 2, NL = 4 + NS;  // scale / all DMA instructions per stage and wavefront
+    constexpr int NS = (TM == 128 ? 2 : 1) + (Q41 ? 1 : 0);  // scale DMA instructions per stage and wavefront
+    constexpr int NL = MT + 2 + NS;                          // all DMA instructions per stage and wavefront
     // descriptors and LDS destinations, fixed for the whole K loop: stage s adds s * SKB (tiles)
     // or 4 s (scale dwords) in the instructions' SGPR offset
     const v4i ar = make_rsrc(Az, a_ext), wr = make_rsrc(Wz, w_ext);
@@ -147,28 +163,39 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
     uint32_t ls[NS];
     {
         const uint32_t half = 256u * (uint32_t)(w & 1);
-        if (a_side) {
+        if (TM == 64 && a_side) {
+            const bool hi = w & 1;
+            rs[0] = make_rsrc(hi ? p.Adh + so0 : p.Adl + so0, sa_ext);
+            ls[0] = (uint32_t)(hi ? offsetof(St, adh) : offsetof(St, adl));
+            if (Q41) {
+                rs[NS - 1] = make_rsrc(p.As + 2 * so0, sa_ext);
+                ls[NS - 1] = (uint32_t)offsetof(St, as);
+            }
+        } else if (a_side) {
             rs[0] = make_rsrc(p.Adl + so0, sa_ext);
             ls[0] = (uint32_t)offsetof(St, adl) + half;
-            rs[1] = make_rsrc(p.Adh + so0, sa_ext);
-            ls[1] = (uint32_t)offsetof(St, adh) + half;
+            rs[NS > 1 ? 1 : 0] = make_rsrc(p.Adh + so0, sa_ext);
+            ls[NS > 1 ? 1 : 0] = (uint32_t)offsetof(St, adh) + half;
             if (Q41) {
                 rs[NS - 1] = make_rsrc(p.As + 2 * so0, sa_ext);
                 ls[NS - 1] = (uint32_t)offsetof(St, as) + half;
             }
         } else {
-            rs[0] = rs[1] = make_rsrc(p.Wd + 2 * so0, sw_ext);
-            ls[0] = ls[1] = (uint32_t)offsetof(St, wd) + half;
+            for (int j = 0; j < NS; ++j) {  // d_w (repeated up to NS, then Q4_1's minima)
+                rs[j] = make_rsrc(p.Wd + 2 * so0, sw_ext);
+                ls[j] = (uint32_t)offsetof(St, wd) + half;
+            }
             if (Q41) {
                 rs[NS - 1] = make_rsrc(p.Wm + 2 * so0, sw_ext);
                 ls[NS - 1] = (uint32_t)offsetof(St, wm) + half;
             }
         }
     }
-    uint32_t lt[2];  // this wavefront's tile rows inside a stage buffer (A; W is SKB * B8M further)
+    uint32_t lta[MT], ltw[2];  // this wavefront's tile rows inside a stage buffer
 #pragma unroll
-    for (int i = 0; i < 2; ++i) lt[i] = (uint32_t)offsetof(St, A) + (uint32_t)((2 * w + i) * 16 * SKB);
-    static_assert(offsetof(St, W) == offsetof(St, A) + B8M * SKB, "W follows A");
+    for (int i = 0; i < MT; ++i) lta[i] = (uint32_t)offsetof(St, A) + (uint32_t)((MT * w + i) * 16 * SKB);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) ltw[i] = (uint32_t)offsetof(St, W) + (uint32_t)((2 * w + i) * 16 * SKB);
     const uint32_t lbuf[3] = {(uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(&st0)),
                               (uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(&st1)),
                               (uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(&st2))};
@@ -176,13 +203,11 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
     // stage s into the buffer at LDS address lb; chunks past the split's K read zero
     auto dma_stage = [&](int s, uint32_t lb) __attribute__((always_inline)) {
         const int k0 = s * SKB;
-        const bool tail = k0 + SKB > K;
+        const bool past = k0 + SKB > K && k0 + tch * 16 >= K;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const bool past = tail && k0 + tch[i] * 16 >= K;
-            dma_b128_so(ar, lb + lt[i], past ? OOB8 : aoff[i], k0);
-            dma_b128_so(wr, lb + lt[i] + B8M * SKB, past ? OOB8 : woff[i], k0);
-        }
+        for (int i = 0; i < MT; ++i) dma_b128_so(ar, lb + lta[i], past ? OOB8 : aoff[i], k0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) dma_b128_so(wr, lb + ltw[i], past ? OOB8 : woff[i], k0);
 #pragma unroll
         for (int j = 0; j < NS; ++j) dma_b32_so(rs[j], lb + ls[j], soff, 4 * s);
     };
@@ -190,10 +215,9 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
     auto dma_full = [&](int s, uint32_t lb) __attribute__((always_inline)) {
         const int k0 = s * SKB;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            dma_b128_so(ar, lb + lt[i], aoff[i], k0);
-            dma_b128_so(wr, lb + lt[i] + B8M * SKB, woff[i], k0);
-        }
+        for (int i = 0; i < MT; ++i) dma_b128_so(ar, lb + lta[i], aoff[i], k0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) dma_b128_so(wr, lb + ltw[i], woff[i], k0);
 #pragma unroll
         for (int j = 0; j < NS; ++j) dma_b32_so(rs[j], lb + ls[j], soff, 4 * s);
     };
@@ -208,19 +232,23 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
     const int lr = lane & 31, g = lane >> 5;
     const bool lo = lane < 32;
     // per-lane LDS offsets inside a stage buffer (the same for all three)
-    int ra_off[2], rw_off[2], sda[2], sdw[2];
+    int ra_off[MT], rw_off[2], sda[MT], sdw[2];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        const int r = WMR * wm + 32 * i + lr;
+        ra_off[i] = r * SKB;
+        sda[i] = r * 4;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int r = 64 * wm + 32 * i + lr, n = 64 * wn + 32 * i + lr;
-        ra_off[i] = r * SKB;
+        const int n = 64 * wn + 32 * i + lr;
         rw_off[i] = n * SKB;
-        sda[i] = r * 4;
         // lanes 32..63 carry k-slots 8..15 of the scale MFMA: a zero B operand there
         sdw[i] = lo ? (int)offsetof(St, wd) + n * 4 : (int)offsetof(St, zero);
     }
-    v16f acc[2][2];
+    v16f acc[MT][2];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < MT; ++a)
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -231,17 +259,19 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
     // fragments of one block: the lane's 16 K bytes (chunk 2 bk + g) of its A and W rows, and
     // the scale MFMA's A operand (d_a of the block in k-slot 0 or 1 of dword 0, dword 1 zero)
     struct FragB {
-        v4i a[2], b[2];
-        v2i da[2];
+        v4i a[MT], b[2];
+        v2i da[MT];
     };
     auto load_blk = [&](const St& b, int bk, FragB& f) __attribute__((always_inline)) {
         const char* base = reinterpret_cast<const char*>(&b);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < MT; ++i) {
             f.a[i] = *reinterpret_cast<const v4i*>(&b.A[ra_off[i] + slot8(ra_off[i] / SKB, 2 * bk + g) * 16]);
-            f.b[i] = *reinterpret_cast<const v4i*>(&b.W[rw_off[i] + slot8(rw_off[i] / SKB, 2 * bk + g) * 16]);
             f.da[i][0] = *reinterpret_cast<const int*>(base + (bk ? offsetof(St, adh) : offsetof(St, adl)) + sda[i]);
         }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            f.b[i] = *reinterpret_cast<const v4i*>(&b.W[rw_off[i] + slot8(rw_off[i] / SKB, 2 * bk + g) * 16]);
     };
     // scale MFMA B operands of a stage: d_w of both blocks in k-slots 0, 1 (lanes 0..31)
     auto load_dw = [&](const St& b, v2i (&dw)[2]) __attribute__((always_inline)) {
@@ -271,10 +301,9 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
     FragB f0, f1;
     v2i dw[2], dwn[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        f0.da[i] = f1.da[i] = v2i{0, 0};
-        dw[i] = dwn[i] = v2i{0, 0};
-    }
+    for (int i = 0; i < MT; ++i) f0.da[i] = f1.da[i] = v2i{0, 0};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) dw[i] = dwn[i] = v2i{0, 0};
     v16i PI[2];
     v16f PS[2];
     for (int i = 0; i < 2; ++i) {
@@ -296,16 +325,16 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
     // combine (buffer p2) runs behind this unit's MFMAs (buffer u2)
     auto units = [&](int s, int bk, const FragB& f, const St& b, bool first) __attribute__((always_inline)) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < NU; ++q) {
             const int mt = q >> 1, nt = q & 1;
-            const int u2 = (bk * 4 + q) & 1, p2 = u2 ^ 1;
+            const int u2 = (bk * NU + q) & 1, p2 = u2 ^ 1;
             if (DOTS) {
                 const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mt], f.b[nt], zi, 0, 0, 0);
                 const int n = n0 + 64 * wn + 32 * nt + lr, blk = 2 * (so0 + s) + bk;
                 if (blk < p.nbt) {
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
-                        const int m = m0 + 64 * wm + 32 * mt + 8 * (i >> 2) + 4 * g + (i & 3);
+                        const int m = m0 + WMR * wm + 32 * mt + 8 * (i >> 2) + 4 * g + (i & 3);
                         if (m < M && n < N) p.dots[((int64_t)m * N + n) * p.nbt + blk] = I[i];
                     }
                 }
@@ -313,7 +342,7 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
             }
             if (Q41 && bk == 0) {
                 // acc += s_a (x) m_w over the stage's two blocks, before the stage's block terms
-                const int r = 64 * wm + 32 * mt + lr, n = 64 * wn + 32 * nt + lr;
+                const int r = WMR * wm + 32 * mt + lr, n = 64 * wn + 32 * nt + lr;
                 const v4i saf = {(int)b.as[Q41 ? r : 0], 0, 0, 0};
                 const v4i mwf = {lo ? (int)b.wm[Q41 ? n : 0] : 0, 0, 0, 0};
                 acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, saf),
@@ -322,7 +351,7 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
             // the previous unit: (bk, q - 1), or block 0's last unit, or the previous stage's last;
             // its combine is split around this unit's second MFMA so neither MFMA issue waits
             const bool has_prev = !first || bk > 0 || q > 0;
-            const int pq = (q + 3) & 3;
+            const int pq = (q + NU - 1) % NU;
             PI[u2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mt], f.b[nt], kbias, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             if (has_prev) apply_half(acc[pq >> 1][pq & 1], PI[p2], PS[p2], 0);
@@ -389,44 +418,49 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
         if (s + 1 < nstage) stage(s + 1, st1, st2, lbuf[1]);
         if (s + 2 < nstage) stage(s + 2, st2, st0, lbuf[2]);
     }
-    if (!DOTS) apply(acc[1][1], PI[1], PS[1]);  // the last unit (block 1, tile (1,1))
+    if (!DOTS) apply(acc[MT - 1][1], PI[1], PS[1]);  // the last unit (block 1, tile (MT - 1, 1))
     if (DOTS) return;
-    // ---- epilogue: the wavefront's 64 x 64 region, 32 rows (one m-tile) at a time
+    // ---- epilogue: the wavefront's WMR x 64 region, RP rows at a time through LDS
     char* Dz = reinterpret_cast<char*>(p.D) + split * p.d_split;
     if (EPI == MMQ_EPI_STORE && !p.d_v4) {
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
-                    const int m = m0 + 64 * wm + 32 * mt + 8 * (i >> 2) + 4 * g + (i & 3);
+                    const int m = m0 + WMR * wm + 32 * mt + 8 * (i >> 2) + 4 * g + (i & 3);
                     const int n = n0 + 64 * wn + 32 * nt + lr;
                     if (m < M && n < N) *reinterpret_cast<float*>(Dz + (int64_t)m * p.d_nb1 + (int64_t)n * 4) = acc[mt][nt][i];
                 }
         return;
     }
-    constexpr int TP = 68;  // staging row pitch (floats): 64 columns + 4
-    static_assert(2 * 32 * TP * 4 <= (int)sizeof(St), "epilogue staging exceeds a stage buffer");
+    constexpr int TP = 68;                  // staging row pitch (floats): 64 columns + 4
+    constexpr int RP = TM == 128 ? 32 : 16;  // rows per staging pass: two wavefronts per stage buffer
+    constexpr int NP = 32 / RP;              // passes per 32-row m-tile
+    static_assert(2 * RP * TP * 4 <= (int)sizeof(St), "epilogue staging exceeds a stage buffer");
     __syncthreads();  // every wavefront is done with the stage buffers
-    float* stg = reinterpret_cast<float*>(w < 2 ? &st0 : &st1) + (w & 1) * 32 * TP;
+    float* stg = reinterpret_cast<float*>(w < 2 ? &st0 : &st1) + (w & 1) * RP * TP;
     const int c4 = lane & 15;                 // this lane's float4 column chunk
     const int nc = n0 + 64 * wn + 4 * c4;     // its first output column
     const bool cv = nc < N;                   // N % 4 == 0 on the float4 paths
     v4f bv = {0.0f, 0.0f, 0.0f, 0.0f};
     if (EPI != MMQ_EPI_STORE && cv) bv = *reinterpret_cast<const v4f*>(&e.bias[nc]);
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mp = 0; mp < MT * NP; ++mp) {
+        const int mt = mp / NP, h = mp % NP;  // m-tile, and the RP-row pass inside it
+        // element i of an m-tile is row 8 (i >> 2) + 4 g + (i & 3): pass h holds i in [16 h / NP, +16 / NP)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) stg[(8 * (i >> 2) + 4 * g + (i & 3)) * TP + 32 * nt + lr] = acc[mt][nt][i];
+            for (int i = 16 * h / NP; i < 16 * (h + 1) / NP; ++i)
+                stg[(8 * (i >> 2) + 4 * g + (i & 3) - RP * h) * TP + 32 * nt + lr] = acc[mt][nt][i];
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's LDS writes are done
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int it = 0; it < 8; ++it) {
+        for (int it = 0; it < RP / 4; ++it) {
             const int r = it * 4 + (lane >> 4);
-            const int m = m0 + 64 * wm + 32 * mt + r;
+            const int m = m0 + WMR * wm + 32 * mt + RP * h + r;
             const v4f v = *reinterpret_cast<const v4f*>(&stg[r * TP + 4 * c4]);
             if (m >= M || !cv) continue;
             if (EPI == MMQ_EPI_STORE) {
@@ -454,7 +488,7 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
                     make_uint2(h0, h1);
             }
         }
-        __builtin_amdgcn_wave_barrier();  // the reads are done before the next m-tile overwrites
+        __builtin_amdgcn_wave_barrier();  // the reads are done before the next pass overwrites
         __builtin_amdgcn_s_waitcnt(0xc07f);
     }
 }
@@ -562,15 +596,15 @@ hipError_t launch_repack_weights(const MatW& w, int64_t N, int64_t K, void* dst,
     return hipGetLastError();
 }
 
-template <int WT>
+template <int WT, int TM>
 static void launch8_t(const Mmq8Args& a, const MmqEpi* e, hipStream_t st) {
     const int TT = a.tiles_m * a.tiles_n * a.ksplit;
     const dim3 grid((unsigned)(((TT + 7) / 8) * 8));
     MmqEpi none{};
-    if (a.dots) mmq8_kernel<WT, MMQ_EPI_STORE, true><<<grid, NT8, 0, st>>>(a, none);
-    else if (a.ksplit > 1 || !e || e->kind == MMQ_EPI_STORE) mmq8_kernel<WT, MMQ_EPI_STORE><<<grid, NT8, 0, st>>>(a, none);
-    else if (e->kind == MMQ_EPI_RESIDUAL) mmq8_kernel<WT, MMQ_EPI_RESIDUAL><<<grid, NT8, 0, st>>>(a, *e);
-    else mmq8_kernel<WT, MMQ_EPI_QKV><<<grid, NT8, 0, st>>>(a, *e);
+    if (a.dots) mmq8_kernel<WT, MMQ_EPI_STORE, true, TM><<<grid, NT8, 0, st>>>(a, none);
+    else if (a.ksplit > 1 || !e || e->kind == MMQ_EPI_STORE) mmq8_kernel<WT, MMQ_EPI_STORE, false, TM><<<grid, NT8, 0, st>>>(a, none);
+    else if (e->kind == MMQ_EPI_RESIDUAL) mmq8_kernel<WT, MMQ_EPI_RESIDUAL, false, TM><<<grid, NT8, 0, st>>>(a, *e);
+    else mmq8_kernel<WT, MMQ_EPI_QKV, false, TM><<<grid, NT8, 0, st>>>(a, *e);
 }
 
 bool mmq8_supported(const WRep& w, const ActI8& a) {
@@ -607,11 +641,23 @@ hipError_t launch_mmq8(const WRep& w, const ActI8& a, const MatD& d, const MmqEp
     p.N = (int)N;
     p.K = (int)a.K;
     p.nst = (int)a.nst;
-    p.tiles_m = (int)((a.M + B8M - 1) / B8M);
+    // 64-row tiles when the 128-row grid has at most 1.4 tiles per CU and no K split: twice the
+    // workgroups, half the work each, so fewer CUs idle or run two tiles while others run one
+    // (5184 x 1024 x 1024: 30.1 -> 28.1 us; 4096 x 384 x 384: 12.0 -> 9.6 us; at 1.5 tiles per
+    // CU, 4096 x 1536 x 384, the 64-row grid's second round costs more: 16.7 -> 17.2 us)
+    const bool split = sp.ks > 1 && !dots;
+    const int64_t t128 = ((a.M + B8M - 1) / B8M) * ((N + B8N - 1) / B8N);
+    const int TMv = !dots && !split && sp.cus > 0 && a.M > 64 && 5 * t128 <= 7LL * sp.cus ? 64 : B8M;
+    p.tiles_m = (int)((a.M + TMv - 1) / TMv);
     p.tiles_n = (int)((N + B8N - 1) / B8N);
+    const int nstage = (int)((a.K / QK + 1) / 2);
+    p.ksplit = split ? sp.ks : 1;
+    p.sps = split ? (nstage + sp.ks - 1) / sp.ks : nstage;
     {
-        // group height: the fewest L2 bytes for the workgroups an XCD runs at once (32 CUs x 2)
-        const double at = (double)B8M * a.K, wt = (double)B8N * a.K;
+        // group height: the fewest L2 bytes for the workgroups an XCD runs at once (32 CUs x 2),
+        // each reading one K range
+        const double kr = (double)std::min<int64_t>(a.K, (int64_t)p.sps * SKB);
+        const double at = TMv * kr, wt = B8N * kr;
         double best = 0;
         p.gm = 1;
         for (int gm = 1; gm <= 16 && gm <= p.tiles_m; gm *= 2) {
@@ -622,10 +668,6 @@ hipError_t launch_mmq8(const WRep& w, const ActI8& a, const MatD& d, const MmqEp
             }
         }
     }
-    const int nstage = (int)((a.K / QK + 1) / 2);
-    const bool split = sp.ks > 1 && !dots;
-    p.ksplit = split ? sp.ks : 1;
-    p.sps = split ? (nstage + sp.ks - 1) / sp.ks : nstage;
     p.d_split = 0;
     if (split) {
         if (!sp.part || N % 4 != 0 || (int64_t)(sp.ks - 1) * p.sps >= nstage) return hipErrorInvalidValue;
@@ -638,10 +680,13 @@ hipError_t launch_mmq8(const WRep& w, const ActI8& a, const MatD& d, const MmqEp
     p.d_v4 = N % 4 == 0 && p.d_nb1 % 16 == 0 && (reinterpret_cast<uintptr_t>(p.D) & 15) == 0;
     if (epi && epi->kind != MMQ_EPI_STORE && !split) p.d_v4 = 1;
     if (!split && !dots && (!epi || epi->kind == MMQ_EPI_STORE) && !d.data) return hipErrorInvalidValue;
-    switch (w.type) {
-        case T_Q8_0: launch8_t<T_Q8_0>(p, epi, st); break;
-        case T_Q4_0: launch8_t<T_Q4_0>(p, epi, st); break;
-        default: launch8_t<T_Q4_1>(p, epi, st); break;
+    switch (w.type * 2 + (TMv == 64 ? 1 : 0)) {
+        case T_Q8_0 * 2: launch8_t<T_Q8_0, 128>(p, epi, st); break;
+        case T_Q8_0 * 2 + 1: launch8_t<T_Q8_0, 64>(p, epi, st); break;
+        case T_Q4_0 * 2: launch8_t<T_Q4_0, 128>(p, epi, st); break;
+        case T_Q4_0 * 2 + 1: launch8_t<T_Q4_0, 64>(p, epi, st); break;
+        case T_Q4_1 * 2: launch8_t<T_Q4_1, 128>(p, epi, st); break;
+        default: launch8_t<T_Q4_1, 64>(p, epi, st); break;
     }
     if (split) {
         const hipError_t e0 = hipGetLastError();
