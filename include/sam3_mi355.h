@@ -91,7 +91,8 @@ const char* mi355_last_error(const mi355_context* ctx);
 /* Reserve the context's scratch workspace (bytes); mul_mat grows it on
  * demand otherwise.  Replaces ggml-cpu's per-graph wdata buffer. */
 mi355_status mi355_reserve_workspace(mi355_context* ctx, size_t bytes);
-/* Workspace bytes mul_mat needs for these operands. */
+/* Workspace bytes mul_mat needs for these operands: the most over the
+ * MUL_MAT routes (mi355_context_set_mmq_kernel). */
 size_t mi355_mul_mat_workspace_size(const mi355_tensor* src0, const mi355_tensor* src1);
 
 /* ---- Device buffers (the ggml-backend buffer calls around a graph) ---------

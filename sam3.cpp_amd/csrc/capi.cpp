@@ -2,6 +2,7 @@
 // workspace management and kernel dispatch.  Every entry point validates on
 // the host before touching the GPU and reports problems as mi355_status,
 // never by aborting (sam3.cpp returns bool/nullptr on failure, CLAUDE.md:62).
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -668,7 +669,11 @@ size_t mi355_mul_mat_workspace_size(const mi355_tensor* s0, const mi355_tensor* 
         return 0;
     int dev = 0;
     (void)hipGetDevice(&dev);
-    return mm_plan(s0, s1, device_cus(dev)).total();
+    // the most any MUL_MAT route (mi355_context_set_mmq_kernel) needs
+    const int cus = device_cus(dev);
+    size_t bytes = 0;
+    for (int k : {MI355_MMQ_F16, MI355_MMQ_INT8, MI355_MMQ_AUTO}) bytes = std::max(bytes, mm_plan(s0, s1, cus, true, k).total());
+    return bytes;
 }
 
 size_t mi355_weight_prepared_nbytes(const mi355_tensor* w) {

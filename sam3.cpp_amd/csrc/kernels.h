@@ -166,6 +166,11 @@ WRep wrep_view(int type, int64_t N, int64_t K, void* base);
 hipError_t launch_repack_weights(const MatW& w, int64_t N, int64_t K, void* dst, WRep* out, hipStream_t st);
 // Operands the int8 kernel takes (alignment, pitches, 32-bit buffer offsets).
 bool mmq8_supported(const WRep& w, const ActI8& a);
+// The K split (1: none) the int8 kernel runs an M x N x K GEMM with on cus compute units,
+// chosen with its tile height by a cost model fitted to kernel times.
+int mmq8_ksplit(int64_t M, int64_t N, int64_t K, int cus);
+// The int8 kernel's tile height (128 or 64 rows) for that GEMM at K split ks.
+int mmq8_tile_rows(int64_t M, int64_t N, int64_t K, int ks, int cus);
 // dst = W^T . A (2-D) on int8 MFMA, bit-identical to launch_mmq on the same
 // operands; epilogues and split-K as launch_mmq / launch_mmq_epi.
 // With dots != nullptr the kernel writes the exact int32 block sums [M][N][K/32] instead.

@@ -711,6 +711,9 @@ size_t mmq_align_bytes(const MatW& w, int64_t N, int64_t K) {
 // (written by the GEMM, read by the reduction at ~4 TB/s) and a launch.
 int mmq_ksplit(int type, int64_t M, int64_t N, int64_t K, int64_t Z, int cus) {
     if (Z != 1 || N % 4 != 0 || cus <= 0) return 1;
+    // block-quantized weights split as the int8 kernel splits them: both routes then add the
+    // same K ranges in the same order and stay bit-identical
+    if (type != T_F16 && K % QK == 0) return mmq8_ksplit(M, N, K, cus);
     const bool quant = type != T_F16;
     const int64_t T = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     const int64_t nstage = quant ? ((K / QK) + BKB - 1) / BKB : (K + 31) / 32;

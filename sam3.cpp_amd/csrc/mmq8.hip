@@ -596,6 +596,61 @@ hipError_t launch_repack_weights(const MatW& w, int64_t N, int64_t K, void* dst,
     return hipGetLastError();
 }
 
+// Modelled time (us) of the int8 kernel, plus the split reduction, at tile height tm and K split
+// ks. Two workgroups fit a CU. A grid of at most one workgroup per CU runs at the one-workgroup
+// rate; beyond that the first round spreads over the CUs and later workgroups fill freed slots
+// in pairs, the last round faster the emptier it is. The rates are fitted to the kernel times
+// of 19 GEMM shapes of the ViT and Hiera encoders at every valid tile height and split (M 1024
+// to 16384, N 192 to 4736, K 192 to 4736; 164 points, 7.7% rms error) on a 256-CU MI355X.
+static double mmq8_cost(int64_t M, int64_t N, int64_t K, int tm, int ks, int cus) {
+    const int64_t nst = (K / QK + 1) / 2, sps = (nst + ks - 1) / ks;
+    const int64_t n = ((M + tm - 1) / tm) * ((N + B8N - 1) / B8N) * ks;
+    const double pair = tm == B8M ? 1.472 : 0.734;  // us per stage, two workgroups per CU
+    const double one = tm == B8M ? 0.719 : 0.363;   // us per stage, one workgroup per CU
+    const double wg = 1.9;                          // prologue and epilogue of one workgroup
+    double t;
+    if (n <= cus) {
+        t = sps * one + wg;
+    } else {
+        const int64_t slots = 2LL * cus, rounds = (n + slots - 1) / slots;
+        const double fill = (double)(n - (rounds - 1) * slots) / slots;
+        t = (rounds - 1) * (sps * pair + wg) + sps * pair * (0.622 + 0.378 * fill) + wg;
+    }
+    if (ks > 1) t += 3.3 + (double)(ks + 1) * M * N * 4 / 6.07e6;  // reduction: ks reads and one write of M x N f32
+    return t;
+}
+
+// A split is valid when each of its ks K ranges holds at least two stages and none is empty.
+static bool mmq8_split_valid(int64_t K, int ks) {
+    const int64_t nst = (K / QK + 1) / 2, sps = (nst + ks - 1) / ks;
+    return ks == 1 || (sps >= 2 && (ks - 1) * sps < nst);
+}
+
+int mmq8_tile_rows(int64_t M, int64_t N, int64_t K, int ks, int cus) {
+    if (cus <= 0 || M <= 64) return B8M;
+    // unsplit grids of at most 1.4 128-row tiles per CU take 64-row tiles, where the model
+    // undervalues them (5184 x 1024 x 1024: 28.4 -> 27.3 us; 16384 x 192 x 768: 18.3 -> 17.2 us);
+    // at 1.5 tiles per CU the 64-row grid's second round costs more (4096 x 1536 x 384: 16.6 -> 17.2 us)
+    const int64_t t128 = ((M + B8M - 1) / B8M) * ((N + B8N - 1) / B8N);
+    if (ks == 1 && 5 * t128 <= 7LL * cus) return 64;
+    return mmq8_cost(M, N, K, 64, ks, cus) < mmq8_cost(M, N, K, B8M, ks, cus) ? 64 : B8M;
+}
+
+int mmq8_ksplit(int64_t M, int64_t N, int64_t K, int cus) {
+    if (cus <= 0 || N % 4 != 0 || M <= 0 || K < QK) return 1;
+    int best = 1;
+    double best_cost = mmq8_cost(M, N, K, mmq8_tile_rows(M, N, K, 1, cus), 1, cus);
+    for (int ks = 2; ks <= 16; ++ks) {
+        if (!mmq8_split_valid(K, ks)) continue;
+        const double c = mmq8_cost(M, N, K, mmq8_tile_rows(M, N, K, ks, cus), ks, cus);
+        if (c < best_cost) {
+            best_cost = c;
+            best = ks;
+        }
+    }
+    return best;
+}
+
 template <int WT, int TM>
 static void launch8_t(const Mmq8Args& a, const MmqEpi* e, hipStream_t st) {
     const int TT = a.tiles_m * a.tiles_n * a.ksplit;
@@ -641,13 +696,8 @@ hipError_t launch_mmq8(const WRep& w, const ActI8& a, const MatD& d, const MmqEp
     p.N = (int)N;
     p.K = (int)a.K;
     p.nst = (int)a.nst;
-    // 64-row tiles when the 128-row grid has at most 1.4 tiles per CU and no K split: twice the
-    // workgroups, half the work each, so fewer CUs idle or run two tiles while others run one
-    // (5184 x 1024 x 1024: 30.1 -> 28.1 us; 4096 x 384 x 384: 12.0 -> 9.6 us; at 1.5 tiles per
-    // CU, 4096 x 1536 x 384, the 64-row grid's second round costs more: 16.7 -> 17.2 us)
     const bool split = sp.ks > 1 && !dots;
-    const int64_t t128 = ((a.M + B8M - 1) / B8M) * ((N + B8N - 1) / B8N);
-    const int TMv = !dots && !split && sp.cus > 0 && a.M > 64 && 5 * t128 <= 7LL * sp.cus ? 64 : B8M;
+    const int TMv = dots ? B8M : mmq8_tile_rows(a.M, N, a.K, split ? sp.ks : 1, sp.cus);
     p.tiles_m = (int)((a.M + TMv - 1) / TMv);
     p.tiles_n = (int)((N + B8N - 1) / B8N);
     const int nstage = (int)((a.K / QK + 1) / 2);

@@ -138,6 +138,10 @@ def test_workspace_size(mi):
     s0, s1, d = mm(mi, K=1024, N=4736, M=5184)
     n = mi.lib().mi355_mul_mat_workspace_size(C.byref(s0), C.byref(s1))
     assert n >= 5184 * 1024 + 5184 * 32 * 4
+    # one activation row: the default (int8) route repacks the Q8_0 weights into the
+    # workspace (N * K one-byte quants), far more than the fp16 route's operand needs
+    s0, s1, d = mm(mi, K=1024, N=4736, M=1)
+    assert mi.lib().mi355_mul_mat_workspace_size(C.byref(s0), C.byref(s1)) >= 4736 * 1024
 
 
 def test_every_entry_point_rejects_null_arguments(mi):

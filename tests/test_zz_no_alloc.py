@@ -45,7 +45,7 @@ def test_mul_mat_noalloc_matches_mul_mat(mi, ctx, orc, tname):
 
 
 def test_mul_mat_noalloc_rejects_oversized(mi, ctx, orc):
-    M, N, K = 8192, 256, 4736  # the Q8 operand alone: 8192 * 4736 fp16 quants = 77.6 MB > 64 MiB
+    M, N, K = 16384, 256, 4736  # the int8 operand alone: 16384 * 4736 one-byte quants = 77.6 MB > 64 MiB
     wq = _weights(orc, orc.Q8_0, N, K, 310)
     wd = dev(wq.view(np.uint8))
     xd = torch.zeros((M, K), dtype=torch.float32, device="cuda")
