@@ -15,6 +15,8 @@
 //   bias_residual_kernel  add(fc2_b) -> add(shortcut) (sam3.cpp:3799-3802)
 //   im2col_kernel      ggml_conv_2d_sk_p0 input columns (sam3.cpp:3815)
 #pragma clang fp contract(off)
+#include <algorithm>
+
 #include "common.cuh"
 #include "kernels.h"
 
@@ -197,6 +199,92 @@ __global__ __launch_bounds__(256) void bias_gelu_act_kernel(const float* __restr
     act_store_chunk(o, r, n, c, x);
 }
 
+// h + b -> activation -> the int8 operand (ACT_I8 / ACT_I8S) of the next MUL_MAT.  Two
+// lanes per 32-value block, 16 consecutive values each: one DPP swap of the adjacent lane
+// gives the block max, the two divisions serve 16 values, and the quants leave as one
+// 16-byte store per lane.  A grid-stride loop issues the next half-block's loads before
+// this one's arithmetic, so loads stay in flight through the activation and the quantize.
+// The block's d, id and quants are those of act_store_chunk (same formulas and rounding).
+// ACT 0: gelu_erf (ggml_gelu_erf); 1: gelu_tanh_table (ggml_gelu, fp16-table semantics).
+// total = rows * n / 16 half-blocks (< 2^31, even since n % 32 == 0), lanes 2k and 2k+1
+// hold the two halves of one block and run the same iterations.
+template <int ACT>
+__global__ __launch_bounds__(256) void bias_act_i8_kernel(const float* __restrict__ h, const float* __restrict__ b,
+                                                          int rows, int n, const ActOut o) {
+    const int hb = n / 16, total = rows * hb, step = (int)(gridDim.x * blockDim.x);
+    int t = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (t >= total) return;
+    v4f hv[4], bv[4];
+    {
+        const int r = t / hb, j = t - r * hb;
+        const float* hr = h + (int64_t)r * n + 16 * j;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            hv[i] = *reinterpret_cast<const v4f*>(hr + 4 * i);
+            bv[i] = *reinterpret_cast<const v4f*>(b + 16 * j + 4 * i);
+        }
+    }
+    for (; t < total; t += step) {
+        const int r = t / hb, j = t - r * hb;
+        const int tn = t + step;
+        v4f hn[4], bn[4];
+        if (tn < total) {
+            const int rn = tn / hb, jn = tn - rn * hb;
+            const float* hr = h + (int64_t)rn * n + 16 * jn;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                hn[i] = *reinterpret_cast<const v4f*>(hr + 4 * i);
+                bn[i] = *reinterpret_cast<const v4f*>(b + 16 * jn + 4 * i);
+            }
+        }
+        float x[16], amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float u = hv[i][k] + bv[i][k];
+                x[4 * i + k] = ACT == 0 ? gelu_erf(u) : gelu_tanh_table(u);
+                amax = fmaxf(amax, fabsf(x[4 * i + k]));
+            }
+        // quad_perm [1, 0, 3, 2]: the other half of this block
+        amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0xB1, 0xF, 0xF, false)));
+        const float d = amax / 127.0f;
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        uint32_t w[4];
+        int isum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q0 = (int)rintf(x[4 * i] * id), q1 = (int)rintf(x[4 * i + 1] * id);
+            const int q2 = (int)rintf(x[4 * i + 2] * id), q3 = (int)rintf(x[4 * i + 3] * id);
+            isum += q0 + q1 + q2 + q3;
+            w[i] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+                   ((uint32_t)(q3 & 0xff) << 24);
+        }
+        if (o.mode == ACT_I8S) isum += __builtin_amdgcn_mov_dpp(isum, 0xB1, 0xF, 0xF, false);
+        *reinterpret_cast<uint4*>(reinterpret_cast<int8_t*>(o.q) + (int64_t)r * n + 16 * j) =
+            make_uint4(w[0], w[1], w[2], w[3]);
+        if ((j & 1) == 0) act_store_scale(o, r, n, j >> 1, d, isum);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            hv[i] = hn[i];
+            bv[i] = bn[i];
+        }
+    }
+}
+
+hipError_t launch_bias_act_i8(int act, const float* h, const float* b, int64_t rows, int n, const ActOut& o,
+                              hipStream_t st) {
+    if (n % 32 || o.mode < ACT_I8 || rows < 0 || rows * (n / 16) >= (int64_t)1 << 31) return hipErrorInvalidValue;
+    const int64_t total = rows * (n / 16);
+    if (total == 0) return hipSuccess;
+    // about four half-blocks per thread, but at least 1024 workgroups while there is work for them
+    const int64_t wgs = (total + 255) / 256;
+    const unsigned grid = (unsigned)std::max<int64_t>(std::min<int64_t>(wgs, 1024), (wgs + 3) / 4);
+    if (act == 0) bias_act_i8_kernel<0><<<grid, 256, 0, st>>>(h, b, (int)rows, n, o);
+    else bias_act_i8_kernel<1><<<grid, 256, 0, st>>>(h, b, (int)rows, n, o);
+    return hipGetLastError();
+}
+
 // x = x + (f + b) over rows of n
 __global__ __launch_bounds__(256) void bias_residual_kernel(float* __restrict__ x, const float* __restrict__ f,
                                                             const float* __restrict__ b, int64_t rows, int n) {
@@ -275,6 +363,7 @@ hipError_t launch_bias_gelu(float* h, const float* b, int64_t rows, int n, hipSt
 
 hipError_t launch_bias_gelu_act(const float* h, const float* b, int64_t rows, int n, const ActOut& o, hipStream_t st) {
     if (n % 32) return hipErrorInvalidValue;
+    if (o.mode >= ACT_I8 && rows * (n / 16) < (int64_t)1 << 31) return launch_bias_act_i8(0, h, b, rows, n, o, st);
     bias_gelu_act_kernel<<<blocks_for(rows * (n / 4)), 256, 0, st>>>(h, b, rows, n, o);
     return hipGetLastError();
 }
