@@ -187,17 +187,70 @@ __device__ __forceinline__ void act_store_chunk(const ActOut& o, int64_t row, in
     }
 }
 
+// Sixteen consecutive values (half-block h of a row of K: elements 16h .. 16h + 15) into
+// the operand; the lanes holding half-blocks 2k and 2k + 1 are adjacent lanes 2j, 2j + 1 of
+// one wavefront, both active, and quantize block k together: one DPP swap gives the block
+// max, d, id and the quants are act_store_chunk's (ggml from_float, x86).
+__device__ __forceinline__ void act_store_half16(const ActOut& o, int64_t row, int64_t K, int h, const float (&x)[16]) {
+    if (o.mode == ACT_F32) {
+        float* y = o.y + row * K + 16 * h;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<v4f*>(y + 4 * i) = v4f{x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]};
+        return;
+    }
+    if (o.mode == ACT_F16) {
+        uint32_t hw[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hw[i] = (uint32_t)f2h(x[2 * i]) | ((uint32_t)f2h(x[2 * i + 1]) << 16);
+        uint4* dst = reinterpret_cast<uint4*>(o.q + row * K + 16 * h);
+        dst[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        dst[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+        return;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(x[i]));
+    // quad_perm [1, 0, 3, 2]: the lane holding the other half of this block
+    amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0xB1, 0xF, 0xF, false)));
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    int q[16], isum = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        q[i] = (int)rintf(x[i] * id);
+        isum += q[i];
+    }
+    if (act_has_sums(o.mode)) isum += __builtin_amdgcn_mov_dpp(isum, 0xB1, 0xF, 0xF, false);
+    if (o.mode >= ACT_I8) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            w[i] = (uint32_t)(q[4 * i] & 0xff) | ((uint32_t)(q[4 * i + 1] & 0xff) << 8) |
+                   ((uint32_t)(q[4 * i + 2] & 0xff) << 16) | ((uint32_t)(q[4 * i + 3] & 0xff) << 24);
+        *reinterpret_cast<uint4*>(reinterpret_cast<int8_t*>(o.q) + row * K + 16 * h) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+        uint32_t hw[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hw[i] = (uint32_t)f2h((float)q[2 * i]) | ((uint32_t)f2h((float)q[2 * i + 1]) << 16);
+        uint4* dst = reinterpret_cast<uint4*>(o.q + row * K + 16 * h);
+        dst[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        dst[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+    }
+    if ((h & 1) == 0) act_store_scale(o, row, K, h >> 1, d, isum);
+}
+
 // ggml_norm -> mul(w) -> add(b) of one row of C held by a group of G lanes
-// (G a power of two, aligned), lane l holding chunks v*G + l, v < V (C = 4*G*V).
+// (G a power of two, aligned), lane l holding chunks v*G + l, v < V (C = 4*G*V),
+// or with CONTIG chunks l*V + v (4V consecutive values per lane).
 // Sums in double as ggml_float; every step rounds to fp32 (callers compile
 // without FMA contraction).
-template <int V>
+template <int V, bool CONTIG = false>
 __device__ __forceinline__ void ln_group(v4f (&x)[V], int l, int G, int C, const float* w, const float* b, float eps) {
     // the affine rows are loaded up front, so their latency overlaps the reductions
     v4f wv[V], bv[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
-        const int c = v * G + l;
+        const int c = CONTIG ? l * V + v : v * G + l;
         wv[v] = w ? *reinterpret_cast<const v4f*>(w + 4 * c) : v4f{1.0f, 1.0f, 1.0f, 1.0f};
         bv[v] = b ? *reinterpret_cast<const v4f*>(b + 4 * c) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
     }

@@ -48,6 +48,32 @@ __device__ __forceinline__ const float* ln_addend(const LnArgs& a, int64_t r) {
     return a.add + pr * a.E;
 }
 
+// ln_group_kernel at E = 1024: one wavefront per row, lane l holding the 16 consecutive
+// values 16l .. 16l + 15 (half a 32-block), so the operand's blocks are quantized by lane
+// pairs (act_store_half16) instead of groups of eight lanes
+__global__ __launch_bounds__(256) void ln1024_kernel(const LnArgs a) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= a.rows) return;
+    const int l = threadIdx.x & 63;
+    const float* xr = a.x + r * 1024;
+    const float* ar = ln_addend(a, r);
+    v4f x[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int c = l * 4 + v;
+        x[v] = *reinterpret_cast<const v4f*>(xr + 4 * c);
+        if (ar) x[v] = x[v] + *reinterpret_cast<const v4f*>(ar + 4 * c);
+    }
+    ln_group<4, true>(x, l, 64, 1024, a.w, a.b, a.eps);
+    const int64_t orow = a.ws > 0 ? win_row(r, a.grid, a.ws) : r;
+    float y[16];
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[4 * v + i] = x[v][i];
+    act_store_half16(a.out, orow, 1024, l, y);
+}
+
 // G lanes per row (E = 4*G*V), 256/G rows per workgroup, float4 loads
 template <int V>
 __global__ __launch_bounds__(256) void ln_group_kernel(const LnArgs a, int G) {
@@ -324,6 +350,10 @@ static unsigned blocks_for(int64_t n, int per_block = 256) { return (unsigned)((
 hipError_t launch_layer_norm(const LnArgs& a, hipStream_t st) {
     if (a.rows <= 0) return hipSuccess;
     if (a.E % 64 != 0 || a.E > 2048) return hipErrorInvalidValue;
+    if (a.E == 1024) {
+        ln1024_kernel<<<blocks_for(a.rows, 4), 256, 0, st>>>(a);
+        return hipGetLastError();
+    }
     int G, V;  // E % 64 == 0: G >= 16, so each 32-block's 8 lanes share a row
     ln_shape(a.E, &G, &V);
     const unsigned nb = blocks_for(a.rows, 256 / G);
