@@ -106,20 +106,74 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Butterfly reductions across `width` consecutive lanes (width a power of
-// two <= 64) through ds_swizzle/ds_bpermute.
+// Lane exchanges without the LDS pipe: step S returns the value of the lane paired with
+// this one, S = 1: lane ^ 1 and S = 2: lane ^ 2 (DPP quad_perm), S = 4: lane 7 - lane within
+// its eight (DPP row_half_mirror), S = 8: lane 15 - lane within its sixteen (DPP row_mirror),
+// S = 16: lane ^ 16 (v_permlane16_swap), S = 32: lane ^ 32 (v_permlane32_swap).  Applied in
+// the order 1, 2, 4, 8, 16, 32 they form a butterfly over aligned groups of lanes: after the
+// steps below 2^k every lane of a 2^k group holds the same value, so the mirror steps pair
+// lanes of different halves.  Every lane of a group must be active.
+template <int S>
+__device__ __forceinline__ int lane_swap(int v) {
+    if constexpr (S == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+    else if constexpr (S == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+    else if constexpr (S == 4) return __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false);
+    else if constexpr (S == 8) return __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false);
+    else if constexpr (S == 16) {
+        // odd 16-lane rows of the first operand swap with even rows of the second
+        const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (__lane_id() & 16) ? (int)p[0] : (int)p[1];
+    } else {
+        static_assert(S == 32, "lane_swap step");
+        // lanes 32..63 of the first operand swap with lanes 0..31 of the second
+        const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (__lane_id() & 32) ? (int)p[0] : (int)p[1];
+    }
+}
+template <int S>
+__device__ __forceinline__ float lane_swap_f(float v) {
+    return __int_as_float(lane_swap<S>(__float_as_int(v)));
+}
+template <int S>
+__device__ __forceinline__ double lane_swap_d(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = lane_swap<S>((int)(b & 0xffffffffLL)), hi = lane_swap<S>((int)(b >> 32));
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+
+// Butterfly max / integer sum across `width` consecutive aligned lanes (a power of two
+// <= 64); exact, so the lane order does not matter.
 template <int width>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int o = width / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, width));
+    if constexpr (width >= 2) v = fmaxf(v, lane_swap_f<1>(v));
+    if constexpr (width >= 4) v = fmaxf(v, lane_swap_f<2>(v));
+    if constexpr (width >= 8) v = fmaxf(v, lane_swap_f<4>(v));
+    if constexpr (width >= 16) v = fmaxf(v, lane_swap_f<8>(v));
+    if constexpr (width >= 32) v = fmaxf(v, lane_swap_f<16>(v));
+    if constexpr (width >= 64) v = fmaxf(v, lane_swap_f<32>(v));
     return v;
 }
 template <int width>
 __device__ __forceinline__ int group_sum_i(int v) {
-#pragma unroll
-    for (int o = width / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, width);
+    if constexpr (width >= 2) v += lane_swap<1>(v);
+    if constexpr (width >= 4) v += lane_swap<2>(v);
+    if constexpr (width >= 8) v += lane_swap<4>(v);
+    if constexpr (width >= 16) v += lane_swap<8>(v);
+    if constexpr (width >= 32) v += lane_swap<16>(v);
+    if constexpr (width >= 64) v += lane_swap<32>(v);
     return v;
 }
+// Double sum over aligned groups of G lanes (G a wavefront-uniform power of two <= 64).
+__device__ __forceinline__ double group_sum_d(double v, int G) {
+    if (G >= 2) v += lane_swap_d<1>(v);
+    if (G >= 4) v += lane_swap_d<2>(v);
+    if (G >= 8) v += lane_swap_d<4>(v);
+    if (G >= 16) v += lane_swap_d<8>(v);
+    if (G >= 32) v += lane_swap_d<16>(v);
+    if (G >= 64) v += lane_swap_d<32>(v);
+    return v;
+}
+// Float sum through ds_bpermute in a fixed order (largest distance first).
 template <int width>
 __device__ __forceinline__ float group_sum(float v) {
 #pragma unroll
@@ -211,7 +265,7 @@ __device__ __forceinline__ void act_store_half16(const ActOut& o, int64_t row, i
 #pragma unroll
     for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(x[i]));
     // quad_perm [1, 0, 3, 2]: the lane holding the other half of this block
-    amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0xB1, 0xF, 0xF, false)));
+    amax = fmaxf(amax, lane_swap_f<1>(amax));
     const float d = amax / 127.0f;
     const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
     int q[16], isum = 0;
@@ -220,7 +274,7 @@ __device__ __forceinline__ void act_store_half16(const ActOut& o, int64_t row, i
         q[i] = (int)rintf(x[i] * id);
         isum += q[i];
     }
-    if (act_has_sums(o.mode)) isum += __builtin_amdgcn_mov_dpp(isum, 0xB1, 0xF, 0xF, false);
+    if (act_has_sums(o.mode)) isum += lane_swap<1>(isum);
     if (o.mode >= ACT_I8) {
         uint32_t w[4];
 #pragma unroll
@@ -259,7 +313,7 @@ __device__ __forceinline__ void ln_group(v4f (&x)[V], int l, int G, int C, const
     for (int v = 0; v < V; ++v)
 #pragma unroll
         for (int i = 0; i < 4; ++i) s += (double)x[v][i];
-    for (int o = G / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, G);
+    s = group_sum_d(s, G);
     const float mean = (float)(s / (double)C);
     double s2 = 0.0;
 #pragma unroll
@@ -270,7 +324,7 @@ __device__ __forceinline__ void ln_group(v4f (&x)[V], int l, int G, int C, const
             x[v][i] = t;
             s2 += (double)(t * t);
         }
-    for (int o = G / 2; o > 0; o >>= 1) s2 += __shfl_xor(s2, o, G);
+    s2 = group_sum_d(s2, G);
     const float var = (float)(s2 / (double)C);
     const float scale = 1.0f / sqrtf(var + eps);
 #pragma unroll

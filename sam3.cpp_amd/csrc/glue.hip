@@ -272,8 +272,8 @@ __global__ __launch_bounds__(256) void bias_act_i8_kernel(const float* __restric
                 x[4 * i + k] = ACT == 0 ? gelu_erf(u) : gelu_tanh_table(u);
                 amax = fmaxf(amax, fabsf(x[4 * i + k]));
             }
-        // quad_perm [1, 0, 3, 2]: the other half of this block
-        amax = fmaxf(amax, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(amax), 0xB1, 0xF, 0xF, false)));
+        // the adjacent lane holds the other half of this block
+        amax = fmaxf(amax, lane_swap_f<1>(amax));
         const float d = amax / 127.0f;
         const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
         uint32_t w[4];
@@ -286,7 +286,7 @@ __global__ __launch_bounds__(256) void bias_act_i8_kernel(const float* __restric
             w[i] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
                    ((uint32_t)(q3 & 0xff) << 24);
         }
-        if (o.mode == ACT_I8S) isum += __builtin_amdgcn_mov_dpp(isum, 0xB1, 0xF, 0xF, false);
+        if (o.mode == ACT_I8S) isum += lane_swap<1>(isum);
         *reinterpret_cast<uint4*>(reinterpret_cast<int8_t*>(o.q) + (int64_t)r * n + 16 * j) =
             make_uint4(w[0], w[1], w[2], w[3]);
         if ((j & 1) == 0) act_store_scale(o, r, n, j >> 1, d, isum);
