@@ -500,11 +500,13 @@ mi355_status mi355_hiera_weights_get(const mi355_hiera_weights* w, mi355_hiera_h
  * of node groups, for parity checks: both produce the same bits. */
 mi355_status mi355_context_set_fusion(mi355_context* ctx, int enable);
 /* The skinny MUL_MAT kernel (no counterpart in the reference; on by default):
- * GEMMs with K <= 128 over at least 4096 activation rows (SAM2 Hiera's stage-1
- * projections, K = 96) run on a kernel that keeps the whole weight matrix in
- * LDS and streams the activation rows; it computes every output with the
- * tiled kernel's instruction sequence, so both give the same bits.  Off
- * routes them to the tiled kernel (for comparisons). */
+ * on the fp16 route (MI355_MMQ_F16, and ggml-layout weights behind the
+ * encoders' fused operands), quantized GEMMs with K <= 128 over at least 4096
+ * activation rows (SAM2 Hiera's stage-1 projections, K = 96) run on a kernel
+ * that keeps the whole weight matrix in LDS and streams the activation rows;
+ * it computes every output with the tiled kernel's instruction sequence, so
+ * both give the same bits.  Off routes them to the tiled kernel (for
+ * comparisons).  The int8 route serves these shapes with 64-row tiles. */
 mi355_status mi355_context_set_skinny(mi355_context* ctx, int enable);
 
 /* The kernel behind 2-D MUL_MATs with Q8_0 / Q4_0 / Q4_1 weights in the

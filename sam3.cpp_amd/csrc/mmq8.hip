@@ -30,6 +30,7 @@
 // three LDS stages filled two stages ahead.  A tile row is 64 bytes = four
 // 16-byte chunks; chunk c of row r sits in slot c ^ ((r >> 2) & 3), so the 16
 // consecutive rows one ds_read_b128 pass serves cover all 64 banks.
+#include <atomic>
 #include <type_traits>
 
 #include "common.cuh"
@@ -79,6 +80,36 @@ struct St8 {
 };
 
 __device__ __forceinline__ int slot8(int r, int c) { return c ^ ((r >> 2) & 3); }
+
+// The epilogue of one float4 of results: row m, columns nc .. nc + 3 (nc < N, N % 4 == 0):
+// stored to Dz (row pitch d_nb1 bytes), or + bias, window-unpartitioned and added to the
+// residual rows, or + bias, split into q / k / v (RoPE on q and k) as fp16.
+template <int EPI>
+__device__ __forceinline__ void epi4(char* Dz, int64_t d_nb1, const MmqEpi& e, int N, int m, int nc, v4f v, v4f bv) {
+    if (EPI == MMQ_EPI_STORE) {
+        *reinterpret_cast<v4f*>(Dz + (int64_t)m * d_nb1 + (int64_t)nc * 4) = v;
+    } else if (EPI == MMQ_EPI_RESIDUAL) {
+        const int rr = map_row32(e.map, m);
+        if (rr >= 0) {
+            const v4f x = *reinterpret_cast<const v4f*>(&e.res[(int64_t)rr * N + nc]);
+            *reinterpret_cast<v4f*>(&e.out[(int64_t)rr * N + nc]) = x + (v + bv);
+        }
+    } else {
+        const v4f uv = v + bv;
+        const int E = e.nh * e.hd, which = nc / E, col = nc - which * E, hh = col / e.hd, d = col - hh * e.hd;
+        _Float16* dst = which == 0 ? e.q : which == 1 ? e.k : e.v;
+        float u0 = uv[0], u1 = uv[1], u2 = uv[2], u3 = uv[3];
+        const int bw = m / e.ntok, tn = m - bw * e.ntok;
+        if (which < 2 && e.rope) {
+            const v4f cs = *reinterpret_cast<const v4f*>(&e.rope[(int64_t)tn * e.hd + d]);
+            rope_pair(u0, u1, cs[0], cs[1]);
+            rope_pair(u2, u3, cs[2], cs[3]);
+        }
+        const uint32_t h0 = (uint32_t)f2h(u0) | ((uint32_t)f2h(u1) << 16);
+        const uint32_t h1 = (uint32_t)f2h(u2) | ((uint32_t)f2h(u3) << 16);
+        *reinterpret_cast<uint2*>(&dst[(((int64_t)bw * e.nh + hh) * e.ntok + tn) * e.hd + d]) = make_uint2(h0, h1);
+    }
+}
 
 // Per-stage pipeline (three LDS buffers, DMA three stages ahead):
 //   units of block 0 (fragments prefetched in registers)
@@ -463,30 +494,7 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
             const int m = m0 + WMR * wm + 32 * mt + RP * h + r;
             const v4f v = *reinterpret_cast<const v4f*>(&stg[r * TP + 4 * c4]);
             if (m >= M || !cv) continue;
-            if (EPI == MMQ_EPI_STORE) {
-                *reinterpret_cast<v4f*>(Dz + (int64_t)m * p.d_nb1 + (int64_t)nc * 4) = v;
-            } else if (EPI == MMQ_EPI_RESIDUAL) {
-                const int rr = map_row32(e.map, m);
-                if (rr >= 0) {
-                    const v4f x = *reinterpret_cast<const v4f*>(&e.res[(int64_t)rr * N + nc]);
-                    *reinterpret_cast<v4f*>(&e.out[(int64_t)rr * N + nc]) = x + (v + bv);
-                }
-            } else {
-                const v4f uv = v + bv;
-                const int E = e.nh * e.hd, which = nc / E, col = nc - which * E, hh = col / e.hd, d = col - hh * e.hd;
-                _Float16* dst = which == 0 ? e.q : which == 1 ? e.k : e.v;
-                float u0 = uv[0], u1 = uv[1], u2 = uv[2], u3 = uv[3];
-                const int bw = m / e.ntok, tn = m - bw * e.ntok;
-                if (which < 2 && e.rope) {
-                    const v4f cs = *reinterpret_cast<const v4f*>(&e.rope[(int64_t)tn * e.hd + d]);
-                    rope_pair(u0, u1, cs[0], cs[1]);
-                    rope_pair(u2, u3, cs[2], cs[3]);
-                }
-                const uint32_t h0 = (uint32_t)f2h(u0) | ((uint32_t)f2h(u1) << 16);
-                const uint32_t h1 = (uint32_t)f2h(u2) | ((uint32_t)f2h(u3) << 16);
-                *reinterpret_cast<uint2*>(&dst[(((int64_t)bw * e.nh + hh) * e.ntok + tn) * e.hd + d]) =
-                    make_uint2(h0, h1);
-            }
+            epi4<EPI>(Dz, p.d_nb1, e, N, m, nc, v, bv);
         }
         __builtin_amdgcn_wave_barrier();  // the reads are done before the next pass overwrites
         __builtin_amdgcn_s_waitcnt(0xc07f);

@@ -116,3 +116,32 @@ def test_hiera_block_prepared_bit_identical(mi, ctx, orc, tname, idx, S):
         outs.append(out)
     assert torch.isfinite(outs[0]).all()
     assert torch.equal(outs[1], outs[0]), f"max diff {(outs[1] - outs[0]).abs().max().item():.3e}"
+
+
+@pytest.mark.parametrize("tname", ["q8_0", "q4_0"])
+@pytest.mark.parametrize("idx", [0, 1])
+def test_hiera_block_prepared_65536_tokens_bit_identical(mi, ctx, orc, tname, idx):
+    """Hiera-tiny blocks 0 and 1 at S = 256 (65536 tokens, K = 96 projections): on prepared
+    weights the stage-1 qkv (qkv epilogue), proj (residual epilogue), fc1 and dim_proj run on
+    the int8 kernel at 64-row tiles; on ggml-layout weights the K = 96 stores take the fp16
+    skinny kernel.  Bar: both blocks give the same bits."""
+    t = orc.NAME_TYPE[tname]
+    S = 256
+    hp = mi.hiera_tiny(1024)
+    info = mi.hiera_block_info(hp, idx)
+    host, devs, vec = th._weights(mi, orc, t, info, seed=idx + 41)
+    blk, _keep = th._block_dev(mi, t, host, devs, vec)
+    keep = []
+    pblk = _prepared_copy(mi, ctx, blk, mi.HieraBlock, ("qkv", "proj", "fc1", "fc2", "dim_proj"), keep)
+    x0 = orc.normal(S * S * info.dim_in, idx, 67).reshape(S * S, info.dim_in)
+    S2 = S // 2 if info.q_stride else S
+    xd = dev(x0)
+    print(f"hiera block {idx} S={S} {tname}: prepared vs ggml layout", flush=True)
+    outs = []
+    for b in (pblk, blk):
+        out = torch.full((S2 * S2, info.dim_out), float("nan"), dtype=torch.float32, device="cuda")
+        ctx.hiera_block_forward(hp, idx, b, th._p(xd), S, th._p(out))
+        ctx.synchronize()
+        outs.append(out)
+    assert torch.isfinite(outs[0]).all()
+    assert torch.equal(outs[0], outs[1]), f"max diff {(outs[0] - outs[1]).abs().max().item():.3e}"
