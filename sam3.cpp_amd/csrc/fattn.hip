@@ -65,11 +65,8 @@ __device__ __forceinline__ u32x4 load8_h(const char* p) {
     }
 }
 
-// value of lane l ^ 32 (the other half of the wavefront holds the same query)
-__device__ __forceinline__ float partner32(float x) {
-    const int l = (int)__lane_id();
-    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((l ^ 32) << 2, __builtin_bit_cast(int, x)));
-}
+// value of lane l ^ 32 (the other half of the wavefront holds the same query), by v_permlane32_swap
+__device__ __forceinline__ float partner32(float x) { return lane_swap_f<32>(x); }
 __device__ __forceinline__ float xmax32(float x) { return fmaxf(x, partner32(x)); }
 // Workgroup barrier for LDS hazards only: waits for this wavefront's LDS accesses,
 // not for its global loads still in flight (__syncthreads() also waits for those).
@@ -385,7 +382,7 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
                         isum += (int)x[i];
                     }
                     if (act_has_sums(o.mode))
-                        isum += __builtin_amdgcn_ds_bpermute(((int)__lane_id() ^ 32) << 2, isum);
+                        isum += lane_swap<32>(isum);
                     if (g == 0) act_store_scale(o, row, K, ((int64_t)h * D + 32 * db) / 32, amax / 127.0f, isum);
                 }
 #pragma unroll
