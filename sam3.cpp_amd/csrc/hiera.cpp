@@ -333,21 +333,30 @@ mi355_status run_block(mi355_context* ctx, const mi355_hiera_hparams* hp, const 
         TRY(hip_check(ctx, t.done(launch_hiera_bias_maxpool(x, nullptr, b.sc, Cout, S, S, true, st)), "maxpool launch"));
         sc = b.sc;
     }
-    // attention operands.  Without Q pooling, q / k / v are the qkv rows split by head with
-    // the bias added, rounded to fp16 ([window][head][token][HD]): the GEMM's qkv epilogue
-    // writes them directly (the same fp32 add and rounding as hiera_qkv, no f32 round trip)
-    if (mq != ACT_F32 && !bi.qs) {
+    // attention operands: q / k / v are the qkv rows split by head with the bias added,
+    // rounded to fp16 ([window][head][token][HD]): the GEMM's qkv epilogue writes them
+    // directly (the same fp32 add and rounding as hiera_qkv, no f32 round trip).  With Q
+    // pooling the epilogue's unpooled q goes to the (then unused) qkv buffer and
+    // hiera_qpool takes its 2x2 window max
+    if (mq != ACT_F32) {
         MmqEpi e{};
         e.kind = MMQ_EPI_QKV;
         e.bias = blk->qkv_b;
         e.rope = nullptr;
-        e.q = b.q;
+        e.q = bi.qs ? reinterpret_cast<_Float16*>(b.qkv) : b.q;
         e.k = b.k;
         e.v = b.v;
         e.ntok = Nkv;
         e.nh = NH;
         e.hd = HD;
         TRY(mul_mat_epi(ctx, &blk->qkv_w, act_in(b.a0, mq, rows, Cin), e));
+        if (bi.qs) {
+            Timed t(ctx, "hiera_qkv");
+            TRY(hip_check(ctx,
+                          t.done(launch_hiera_qpool(reinterpret_cast<const _Float16*>(b.qkv), b.q, nW, NH, Nkv, Nq,
+                                                    ws, HD, st)),
+                          "hiera_qpool launch"));
+        }
     } else {
         const mi355_tensor out = tensor_on(b.qkv, T_F32, 3 * Cout, rows);
         if (mq == ACT_F32) {

@@ -159,6 +159,33 @@ __global__ __launch_bounds__(256) void hiera_q_kernel(const HieraQkvArgs a) {
     *reinterpret_cast<uint32_t*>(a.q + o) = (uint32_t)f2h(q0) | ((uint32_t)f2h(q1) << 16);
 }
 
+// Q of a pooled block from the unpooled fp16 q [B][NH][Nkv][HD] (q + bias rounded, as the
+// GEMM's qkv epilogue writes it): the 2x2 max inside each window's ws x ws token grid
+// (sam2_maxpool_2d) into [B][NH][Nq][HD].  Rounding to fp16 is monotonic, so the max of the
+// rounded values is the rounded max: the same bits as pooling in fp32 and rounding once
+// (hiera_q_kernel).  Thread per (bw, head h, query tq, pair i).
+__global__ __launch_bounds__(256) void hiera_qpool_kernel(const _Float16* __restrict__ qf, _Float16* __restrict__ q,
+                                                          int64_t B, int NH, int Nkv, int Nq, int ws, int HD) {
+    const int half = HD / 2;
+    const int64_t tix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tix >= B * NH * Nq * half) return;
+    const int i = (int)(tix % half);
+    const int tq = (int)((tix / half) % Nq);
+    const int64_t bh = tix / ((int64_t)half * Nq);  // bw * NH + h
+    const int wo = ws / 2, ph = tq / wo, pw = tq - ph * wo;
+    float q0 = -__builtin_inff(), q1 = -__builtin_inff();
+#pragma unroll
+    for (int dy = 0; dy < 2; ++dy)
+#pragma unroll
+        for (int dx = 0; dx < 2; ++dx) {
+            const int t = (2 * ph + dy) * ws + 2 * pw + dx;
+            const uint32_t w = *reinterpret_cast<const uint32_t*>(qf + (bh * Nkv + t) * HD + 2 * i);
+            q0 = fmaxf(q0, h2f((uint16_t)(w & 0xffffu)));
+            q1 = fmaxf(q1, h2f((uint16_t)(w >> 16)));
+        }
+    *reinterpret_cast<uint32_t*>(q + (bh * Nq + tq) * HD + 2 * i) = (uint32_t)f2h(q0) | ((uint32_t)f2h(q1) << 16);
+}
+
 // pool: out[h2][w2] = max over 2x2 of (p[t] (+ b)); else out[t] = p[t] (+ b); rows of C
 __global__ __launch_bounds__(256) void hiera_bias_maxpool_kernel(const float* __restrict__ p, const float* __restrict__ b,
                                                                  float* __restrict__ out, int C, int W, int H, int pool) {
@@ -289,6 +316,13 @@ hipError_t launch_hiera_ln(const HieraLnArgs& a, hipStream_t st) {
         case 8: hiera_ln_group_kernel<8><<<nb, 256, 0, st>>>(a, G); break;
         default: hiera_ln_kernel<<<(unsigned)((a.rows_out + 3) / 4), 256, 0, st>>>(a); break;
     }
+    return hipGetLastError();
+}
+hipError_t launch_hiera_qpool(const _Float16* qf, _Float16* q, int64_t B, int NH, int Nkv, int Nq, int ws, int HD,
+                              hipStream_t st) {
+    if (HD % 2 || ws % 2 || Nkv != ws * ws || Nq * 4 != Nkv) return hipErrorInvalidValue;
+    const int64_t n = B * NH * Nq * (HD / 2);
+    if (n > 0) hiera_qpool_kernel<<<nblk(n), 256, 0, st>>>(qf, q, B, NH, Nkv, Nq, ws, HD);
     return hipGetLastError();
 }
 hipError_t launch_hiera_qkv(const HieraQkvArgs& a, hipStream_t st) {

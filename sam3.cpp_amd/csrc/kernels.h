@@ -286,6 +286,10 @@ struct HieraQkvArgs {
     int ws;
 };
 hipError_t launch_hiera_qkv(const HieraQkvArgs& a, hipStream_t st);
+// Q of a pooled block: the 2x2 window max of the unpooled fp16 q [B][NH][Nkv][HD] into
+// q [B][NH][Nq][HD] (Nkv = ws * ws, Nq = Nkv / 4).
+hipError_t launch_hiera_qpool(const _Float16* qf, _Float16* q, int64_t B, int NH, int Nkv, int Nq, int ws, int HD,
+                              hipStream_t st);
 hipError_t launch_hiera_bias_maxpool(const float* p, const float* b, float* out, int C, int W, int H, bool pool,
                                      hipStream_t st);
 hipError_t launch_hiera_proj_residual(float* x, const float* shortcut, const float* p, const float* b, int C, int W,
