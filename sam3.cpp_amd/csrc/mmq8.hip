@@ -83,9 +83,11 @@ __device__ __forceinline__ int slot8(int r, int c) { return c ^ ((r >> 2) & 3); 
 
 // The epilogue of one float4 of results: row m, columns nc .. nc + 3 (nc < N, N % 4 == 0):
 // stored to Dz (row pitch d_nb1 bytes), or + bias, window-unpartitioned and added to the
-// residual rows, or + bias, split into q / k / v (RoPE on q and k) as fp16.
+// residual rows, or + bias, split into q / k / v (RoPE on q and k by the factors cs, which
+// the caller loads from e.rope row tn, column d) as fp16.
 template <int EPI>
-__device__ __forceinline__ void epi4(char* Dz, int64_t d_nb1, const MmqEpi& e, int N, int m, int nc, v4f v, v4f bv) {
+__device__ __forceinline__ void epi4(char* Dz, int64_t d_nb1, const MmqEpi& e, int N, int m, int nc, v4f v, v4f bv,
+                                     v4f cs = v4f{0.0f, 0.0f, 0.0f, 0.0f}) {
     if (EPI == MMQ_EPI_STORE) {
         *reinterpret_cast<v4f*>(Dz + (int64_t)m * d_nb1 + (int64_t)nc * 4) = v;
     } else if (EPI == MMQ_EPI_RESIDUAL) {
@@ -101,7 +103,6 @@ __device__ __forceinline__ void epi4(char* Dz, int64_t d_nb1, const MmqEpi& e, i
         float u0 = uv[0], u1 = uv[1], u2 = uv[2], u3 = uv[3];
         const int bw = m / e.ntok, tn = m - bw * e.ntok;
         if (which < 2 && e.rope) {
-            const v4f cs = *reinterpret_cast<const v4f*>(&e.rope[(int64_t)tn * e.hd + d]);
             rope_pair(u0, u1, cs[0], cs[1]);
             rope_pair(u2, u3, cs[2], cs[3]);
         }
@@ -488,13 +489,26 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
                 stg[(8 * (i >> 2) + 4 * g + (i & 3) - RP * h) * TP + 32 * nt + lr] = acc[mt][nt][i];
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's LDS writes are done
         __builtin_amdgcn_wave_barrier();
+        // qkv with RoPE: the factors of the pass's rows are loaded before its stores, so their
+        // latency is paid once per pass instead of once per row
+        v4f csv[RP / 4];
+#pragma unroll
+        for (int it = 0; it < RP / 4; ++it) csv[it] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if (EPI == MMQ_EPI_QKV && e.rope && cv && nc < 2 * e.nh * e.hd) {
+            const int d = (nc % (e.nh * e.hd)) % e.hd;
+#pragma unroll
+            for (int it = 0; it < RP / 4; ++it) {
+                const int m = m0 + WMR * wm + 32 * mt + RP * h + it * 4 + (lane >> 4);
+                if (m < M) csv[it] = *reinterpret_cast<const v4f*>(&e.rope[(int64_t)(m % e.ntok) * e.hd + d]);
+            }
+        }
 #pragma unroll
         for (int it = 0; it < RP / 4; ++it) {
             const int r = it * 4 + (lane >> 4);
             const int m = m0 + WMR * wm + 32 * mt + RP * h + r;
             const v4f v = *reinterpret_cast<const v4f*>(&stg[r * TP + 4 * c4]);
             if (m >= M || !cv) continue;
-            epi4<EPI>(Dz, p.d_nb1, e, N, m, nc, v, bv);
+            epi4<EPI>(Dz, p.d_nb1, e, N, m, nc, v, bv, csv[it]);
         }
         __builtin_amdgcn_wave_barrier();  // the reads are done before the next pass overwrites
         __builtin_amdgcn_s_waitcnt(0xc07f);
