@@ -481,7 +481,8 @@ def main():
     PREWARM_S = args.prewarm
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
-              "the hot path shards trivially over tokens or frames, see DESIGN.md", file=sys.stderr)
+              "the hot path shards over tokens or frames, one process per GPU, with no collective "
+              "inside a MUL_MAT", file=sys.stderr)
         sys.exit(2)
 
     traffic = None
