@@ -232,7 +232,7 @@ __global__ __launch_bounds__(256) void bias_gelu_act_kernel(const float* __restr
 // this one's arithmetic, so loads stay in flight through the activation and the quantize.
 // The block's d, id and quants are those of act_store_chunk (same formulas and rounding).
 // ACT 0: gelu_erf (ggml_gelu_erf); 1: gelu_tanh_table (ggml_gelu, fp16-table semantics).
-// total = rows * n / 16 half-blocks (< 2^31, even since n % 32 == 0), lanes 2k and 2k+1
+// total = rows * n / 16 half-blocks (< 2^30, even since n % 32 == 0), lanes 2k and 2k+1
 // hold the two halves of one block and run the same iterations.
 template <int ACT>
 __global__ __launch_bounds__(256) void bias_act_i8_kernel(const float* __restrict__ h, const float* __restrict__ b,
@@ -300,7 +300,8 @@ __global__ __launch_bounds__(256) void bias_act_i8_kernel(const float* __restric
 
 hipError_t launch_bias_act_i8(int act, const float* h, const float* b, int64_t rows, int n, const ActOut& o,
                               hipStream_t st) {
-    if (n % 32 || o.mode < ACT_I8 || rows < 0 || rows * (n / 16) >= (int64_t)1 << 31) return hipErrorInvalidValue;
+    // the kernel's 32-bit index t + step stays below 2^31: total < 2^30 and step <= total / 4 + 2^18
+    if (n % 32 || o.mode < ACT_I8 || rows < 0 || rows * (n / 16) >= (int64_t)1 << 30) return hipErrorInvalidValue;
     const int64_t total = rows * (n / 16);
     if (total == 0) return hipSuccess;
     // about four half-blocks per thread, but at least 1024 workgroups while there is work for them
@@ -393,7 +394,7 @@ hipError_t launch_bias_gelu(float* h, const float* b, int64_t rows, int n, hipSt
 
 hipError_t launch_bias_gelu_act(const float* h, const float* b, int64_t rows, int n, const ActOut& o, hipStream_t st) {
     if (n % 32) return hipErrorInvalidValue;
-    if (o.mode >= ACT_I8 && rows * (n / 16) < (int64_t)1 << 31) return launch_bias_act_i8(0, h, b, rows, n, o, st);
+    if (o.mode >= ACT_I8 && rows * (n / 16) < (int64_t)1 << 30) return launch_bias_act_i8(0, h, b, rows, n, o, st);
     bias_gelu_act_kernel<<<blocks_for(rows * (n / 4)), 256, 0, st>>>(h, b, rows, n, o);
     return hipGetLastError();
 }

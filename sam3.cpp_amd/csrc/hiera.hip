@@ -351,7 +351,7 @@ hipError_t launch_bias_gelu_tanh(float* h, const float* b, int64_t rows, int n, 
 hipError_t launch_bias_gelu_tanh_act(const float* h, const float* b, int64_t rows, int n, const ActOut& o,
                                      hipStream_t st) {
     if (n % 32) return hipErrorInvalidValue;
-    if (o.mode >= ACT_I8 && rows * (n / 16) < (int64_t)1 << 31) return launch_bias_act_i8(1, h, b, rows, n, o, st);
+    if (o.mode >= ACT_I8 && rows * (n / 16) < (int64_t)1 << 30) return launch_bias_act_i8(1, h, b, rows, n, o, st);
     if (rows * (n / 4) > 0) bias_gelu_tanh_act_kernel<<<nblk(rows * (n / 4)), 256, 0, st>>>(h, b, rows, n, o);
     return hipGetLastError();
 }

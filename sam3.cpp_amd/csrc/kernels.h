@@ -257,7 +257,7 @@ hipError_t launch_proj_residual(float* x, const float* p, const float* b, int64_
 hipError_t launch_bias_gelu(float* h, const float* b, int64_t rows, int n, hipStream_t st);
 hipError_t launch_bias_gelu_act(const float* h, const float* b, int64_t rows, int n, const ActOut& o, hipStream_t st);
 // h + b -> activation (act 0: gelu_erf, 1: ggml_gelu table form) -> an int8 operand
-// (o.mode ACT_I8 / ACT_I8S; n % 32 == 0, rows * n / 16 < 2^31).
+// (o.mode ACT_I8 / ACT_I8S; n % 32 == 0, rows * n / 16 < 2^30).
 hipError_t launch_bias_act_i8(int act, const float* h, const float* b, int64_t rows, int n, const ActOut& o,
                               hipStream_t st);
 hipError_t launch_bias_residual(float* x, const float* f, const float* b, int64_t rows, int n, hipStream_t st);
