@@ -427,6 +427,50 @@ __device__ __forceinline__ int64_t win_unpart_row(int64_t r, int W, int ws) {
     return (int64_t)y * W + x;
 }
 
+// a / b, and a % b in rem, for a >= 0, b > 0, a + b < 2^31, given rb = 1.0 / b: the double
+// product a * rb lies within 2^-21 of a / b, so its truncation is the quotient or one off
+// either way, and one correction step makes it exact.  A handful of instructions against
+// the thirty-odd of a 32-bit integer division by a runtime divisor.
+__device__ __forceinline__ int div_rcp(int a, int b, double rb, int& rem) {
+    int q = (int)((double)a * rb);
+    int r = a - q * b;
+    if (r < 0) {
+        --q;
+        r += b;
+    } else if (r >= b) {
+        ++q;
+        r -= b;
+    }
+    rem = r;
+    return q;
+}
+
+// The reciprocals map_row32 divides by, computed once per thread
+struct RowMapRcp {
+    double w2, ws, nw;
+};
+__device__ __forceinline__ RowMapRcp rowmap_rcp(const RowMap& rm) {
+    RowMapRcp c{0.0, 0.0, 0.0};
+    if (rm.kind == ROWMAP_IDENTITY) return c;
+    c.w2 = 1.0 / (double)(rm.ws * rm.ws);
+    c.ws = 1.0 / (double)rm.ws;
+    c.nw = 1.0 / (double)(rm.kind == ROWMAP_WIN_UNPART ? rm.W / rm.ws : rm.nwh);
+    return c;
+}
+// map_row32 for rows below 2^30 through div_rcp (the same rows)
+__device__ __forceinline__ int map_row32(const RowMap& rm, const RowMapRcp& rc, int r) {
+    if (rm.kind == ROWMAP_IDENTITY) return r;
+    int loc, lx, sub;
+    const int n = div_rcp(r, rm.ws * rm.ws, rc.w2, loc), ly = div_rcp(loc, rm.ws, rc.ws, lx);
+    if (rm.kind == ROWMAP_WIN_UNPART) {
+        const int wy = div_rcp(n, rm.W / rm.ws, rc.nw, sub);  // sub = wx
+        return (wy * rm.ws + ly) * rm.W + sub * rm.ws + lx;
+    }
+    const int ww = div_rcp(n, rm.nwh, rc.nw, sub);  // sub = wh; SAM2: window n = wh + nwh*ww
+    const int h = sub * rm.ws + ly, w = ww * rm.ws + lx;
+    return (h < rm.H && w < rm.W) ? h * rm.W + w : -1;
+}
+
 // map_row for rows and grids below 2^31 (32-bit index arithmetic)
 __device__ __forceinline__ int map_row32(const RowMap& rm, int r) {
     if (rm.kind == ROWMAP_IDENTITY) return r;

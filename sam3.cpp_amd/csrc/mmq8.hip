@@ -82,33 +82,37 @@ struct St8 {
 __device__ __forceinline__ int slot8(int r, int c) { return c ^ ((r >> 2) & 3); }
 
 // The epilogue of one float4 of results: row m, columns nc .. nc + 3 (nc < N, N % 4 == 0):
-// stored to Dz (row pitch d_nb1 bytes), or + bias, window-unpartitioned and added to the
-// residual rows, or + bias, split into q / k / v (RoPE on q and k by the factors cs, which
-// the caller loads from e.rope row tn, column d) as fp16.
+// stored to Dz (row pitch d_nb1 bytes), or + bias, window-unpartitioned (rr = map(m)) and
+// added to the residual rows, or + bias, split into q / k / v as fp16 (RoPE on q and k by
+// the factors cs, loaded by the caller from e.rope row tn, column d).  The qkv columns
+// (destination, head, first dimension) are the lane's, fixed for the whole epilogue, and the
+// row's window bw and token tn come from the caller.
+struct QkvLane {
+    _Float16* dst;
+    int hh, d;
+    bool rope;
+};
 template <int EPI>
 __device__ __forceinline__ void epi4(char* Dz, int64_t d_nb1, const MmqEpi& e, int N, int m, int nc, v4f v, v4f bv,
-                                     v4f cs = v4f{0.0f, 0.0f, 0.0f, 0.0f}) {
+                                     int rr, const QkvLane& ql, int bw, int tn, v4f cs) {
     if (EPI == MMQ_EPI_STORE) {
         *reinterpret_cast<v4f*>(Dz + (int64_t)m * d_nb1 + (int64_t)nc * 4) = v;
     } else if (EPI == MMQ_EPI_RESIDUAL) {
-        const int rr = map_row32(e.map, m);
         if (rr >= 0) {
             const v4f x = *reinterpret_cast<const v4f*>(&e.res[(int64_t)rr * N + nc]);
             *reinterpret_cast<v4f*>(&e.out[(int64_t)rr * N + nc]) = x + (v + bv);
         }
     } else {
         const v4f uv = v + bv;
-        const int E = e.nh * e.hd, which = nc / E, col = nc - which * E, hh = col / e.hd, d = col - hh * e.hd;
-        _Float16* dst = which == 0 ? e.q : which == 1 ? e.k : e.v;
         float u0 = uv[0], u1 = uv[1], u2 = uv[2], u3 = uv[3];
-        const int bw = m / e.ntok, tn = m - bw * e.ntok;
-        if (which < 2 && e.rope) {
+        if (ql.rope) {
             rope_pair(u0, u1, cs[0], cs[1]);
             rope_pair(u2, u3, cs[2], cs[3]);
         }
         const uint32_t h0 = (uint32_t)f2h(u0) | ((uint32_t)f2h(u1) << 16);
         const uint32_t h1 = (uint32_t)f2h(u2) | ((uint32_t)f2h(u3) << 16);
-        *reinterpret_cast<uint2*>(&dst[(((int64_t)bw * e.nh + hh) * e.ntok + tn) * e.hd + d]) = make_uint2(h0, h1);
+        *reinterpret_cast<uint2*>(&ql.dst[((int64_t)bw * e.nh + ql.hh) * ((int64_t)e.ntok * e.hd) + tn * e.hd + ql.d]) =
+            make_uint2(h0, h1);
     }
 }
 
@@ -478,6 +482,20 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
     const bool cv = nc < N;                   // N % 4 == 0 on the float4 paths
     v4f bv = {0.0f, 0.0f, 0.0f, 0.0f};
     if (EPI != MMQ_EPI_STORE && cv) bv = *reinterpret_cast<const v4f*>(&e.bias[nc]);
+    // the lane's qkv columns, and the reciprocals of the row divisions (the rows of a pass are
+    // split into (window, token) or mapped through div_rcp, not by integer divisions)
+    QkvLane ql{nullptr, 0, 0, false};
+    double r_ntok = 0.0;
+    RowMapRcp rmc{0.0, 0.0, 0.0};
+    if (EPI == MMQ_EPI_QKV) {
+        const int E = e.nh * e.hd, which = nc / E, col = nc - which * E;
+        ql.hh = col / e.hd;
+        ql.d = col - ql.hh * e.hd;
+        ql.dst = which == 0 ? e.q : which == 1 ? e.k : e.v;
+        ql.rope = e.rope && which < 2;
+        r_ntok = 1.0 / (double)e.ntok;
+    }
+    if (EPI == MMQ_EPI_RESIDUAL) rmc = rowmap_rcp(e.map);
 #pragma unroll
     for (int mp = 0; mp < MT * NP; ++mp) {
         const int mt = mp / NP, h = mp % NP;  // m-tile, and the RP-row pass inside it
@@ -489,18 +507,20 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
                 stg[(8 * (i >> 2) + 4 * g + (i & 3) - RP * h) * TP + 32 * nt + lr] = acc[mt][nt][i];
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's LDS writes are done
         __builtin_amdgcn_wave_barrier();
-        // qkv with RoPE: the factors of the pass's rows are loaded before its stores, so their
-        // latency is paid once per pass instead of once per row
+        // the pass's rows: qkv (window, token) with the RoPE factors loaded before the stores, so
+        // their latency is paid once per pass instead of once per row; residual destination rows
+        int bwv[RP / 4], tnv[RP / 4], rrv[RP / 4];
         v4f csv[RP / 4];
 #pragma unroll
-        for (int it = 0; it < RP / 4; ++it) csv[it] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-        if (EPI == MMQ_EPI_QKV && e.rope && cv && nc < 2 * e.nh * e.hd) {
-            const int d = (nc % (e.nh * e.hd)) % e.hd;
-#pragma unroll
-            for (int it = 0; it < RP / 4; ++it) {
-                const int m = m0 + WMR * wm + 32 * mt + RP * h + it * 4 + (lane >> 4);
-                if (m < M) csv[it] = *reinterpret_cast<const v4f*>(&e.rope[(int64_t)(m % e.ntok) * e.hd + d]);
+        for (int it = 0; it < RP / 4; ++it) {
+            const int m = m0 + WMR * wm + 32 * mt + RP * h + it * 4 + (lane >> 4);
+            bwv[it] = tnv[it] = rrv[it] = 0;
+            csv[it] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (EPI == MMQ_EPI_QKV) {
+                bwv[it] = div_rcp(m, e.ntok, r_ntok, tnv[it]);
+                if (ql.rope && cv && m < M) csv[it] = *reinterpret_cast<const v4f*>(&e.rope[(int64_t)tnv[it] * e.hd + ql.d]);
             }
+            if (EPI == MMQ_EPI_RESIDUAL) rrv[it] = m < M && cv ? map_row32(e.map, rmc, m) : -1;
         }
 #pragma unroll
         for (int it = 0; it < RP / 4; ++it) {
@@ -508,7 +528,7 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
             const int m = m0 + WMR * wm + 32 * mt + RP * h + r;
             const v4f v = *reinterpret_cast<const v4f*>(&stg[r * TP + 4 * c4]);
             if (m >= M || !cv) continue;
-            epi4<EPI>(Dz, p.d_nb1, e, N, m, nc, v, bv, csv[it]);
+            epi4<EPI>(Dz, p.d_nb1, e, N, m, nc, v, bv, rrv[it], ql, bwv[it], tnv[it], csv[it]);
         }
         __builtin_amdgcn_wave_barrier();  // the reads are done before the next pass overwrites
         __builtin_amdgcn_s_waitcnt(0xc07f);
@@ -747,7 +767,8 @@ hipError_t launch_mmq8(const WRep& w, const ActI8& a, const MatD& d, const MmqEp
         p.d_nb1 = N * 4;
         p.d_split = a.M * N * 4;
     } else if (epi && epi->kind != MMQ_EPI_STORE) {
-        if (N % 4 != 0 || !epi->bias) return hipErrorInvalidValue;
+        // the fused epilogues split rows with div_rcp (rows below 2^30)
+        if (N % 4 != 0 || !epi->bias || a.M >= ((int64_t)1 << 30)) return hipErrorInvalidValue;
     }
     p.d_v4 = N % 4 == 0 && p.d_nb1 % 16 == 0 && (reinterpret_cast<uintptr_t>(p.D) & 15) == 0;
     if (epi && epi->kind != MMQ_EPI_STORE && !split) p.d_v4 = 1;
