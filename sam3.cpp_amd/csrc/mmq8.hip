@@ -82,11 +82,11 @@ struct St8 {
 __device__ __forceinline__ int slot8(int r, int c) { return c ^ ((r >> 2) & 3); }
 
 // The epilogue of one float4 of results: row m, columns nc .. nc + 3 (nc < N, N % 4 == 0):
-// stored to Dz (row pitch d_nb1 bytes), or + bias, window-unpartitioned (rr = map(m)) and
-// added to the residual rows, or + bias, split into q / k / v as fp16 (RoPE on q and k by
-// the factors cs, loaded by the caller from e.rope row tn, column d).  The qkv columns
-// (destination, head, first dimension) are the lane's, fixed for the whole epilogue, and the
-// row's window bw and token tn come from the caller.
+// stored to Dz (row pitch d_nb1 bytes), or + bias and added to the residual row rr = map(m)
+// (pv: that row's four values, loaded by the caller), or + bias, split into q / k / v as
+// fp16 (RoPE on q and k by the factors pv, loaded by the caller from e.rope row tn, column
+// d).  The qkv columns (destination, head, first dimension) are the lane's, fixed for the
+// whole epilogue, and the row's window bw and token tn come from the caller.
 struct QkvLane {
     _Float16* dst;
     int hh, d;
@@ -94,20 +94,17 @@ struct QkvLane {
 };
 template <int EPI>
 __device__ __forceinline__ void epi4(char* Dz, int64_t d_nb1, const MmqEpi& e, int N, int m, int nc, v4f v, v4f bv,
-                                     int rr, const QkvLane& ql, int bw, int tn, v4f cs) {
+                                     int rr, const QkvLane& ql, int bw, int tn, v4f pv) {
     if (EPI == MMQ_EPI_STORE) {
         *reinterpret_cast<v4f*>(Dz + (int64_t)m * d_nb1 + (int64_t)nc * 4) = v;
     } else if (EPI == MMQ_EPI_RESIDUAL) {
-        if (rr >= 0) {
-            const v4f x = *reinterpret_cast<const v4f*>(&e.res[(int64_t)rr * N + nc]);
-            *reinterpret_cast<v4f*>(&e.out[(int64_t)rr * N + nc]) = x + (v + bv);
-        }
+        if (rr >= 0) *reinterpret_cast<v4f*>(&e.out[(int64_t)rr * N + nc]) = pv + (v + bv);
     } else {
         const v4f uv = v + bv;
         float u0 = uv[0], u1 = uv[1], u2 = uv[2], u3 = uv[3];
         if (ql.rope) {
-            rope_pair(u0, u1, cs[0], cs[1]);
-            rope_pair(u2, u3, cs[2], cs[3]);
+            rope_pair(u0, u1, pv[0], pv[1]);
+            rope_pair(u2, u3, pv[2], pv[3]);
         }
         const uint32_t h0 = (uint32_t)f2h(u0) | ((uint32_t)f2h(u1) << 16);
         const uint32_t h1 = (uint32_t)f2h(u2) | ((uint32_t)f2h(u3) << 16);
@@ -163,6 +160,20 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
     const int64_t sa_ext = 4LL * M * p.nst - 4LL * so0, sw_ext = 4LL * N * p.nst - 4LL * so0;
 
     if (tid < 4) st0.zero[tid] = st1.zero[tid] = st2.zero[tid] = 0u;
+    // fused epilogues: where each of the tile's rows goes, worked out once per workgroup (one
+    // row per thread; published by the barrier before the K loop): residual -> the mapped row,
+    // or -1 (padding or past M); qkv -> window and token
+    __shared__ int rtab[EPI == MMQ_EPI_STORE ? 1 : 2 * TM];
+    if (EPI != MMQ_EPI_STORE && tid < TM) {
+        const int m = m0 + tid;
+        if (EPI == MMQ_EPI_RESIDUAL) {
+            rtab[tid] = m < M ? map_row32(e.map, rowmap_rcp(e.map), m) : -1;
+        } else {
+            int tn;
+            rtab[tid] = div_rcp(m, e.ntok, 1.0 / (double)e.ntok, tn);
+            rtab[TM + tid] = tn;
+        }
+    }
 
     // ---- DMA offsets (fixed for the whole K loop)
     // A-tile instruction i of wavefront w: rows (MT w + i) * 16 + lane / 4; W-tile instruction i:
@@ -482,20 +493,15 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
     const bool cv = nc < N;                   // N % 4 == 0 on the float4 paths
     v4f bv = {0.0f, 0.0f, 0.0f, 0.0f};
     if (EPI != MMQ_EPI_STORE && cv) bv = *reinterpret_cast<const v4f*>(&e.bias[nc]);
-    // the lane's qkv columns, and the reciprocals of the row divisions (the rows of a pass are
-    // split into (window, token) or mapped through div_rcp, not by integer divisions)
+    // the lane's qkv columns
     QkvLane ql{nullptr, 0, 0, false};
-    double r_ntok = 0.0;
-    RowMapRcp rmc{0.0, 0.0, 0.0};
     if (EPI == MMQ_EPI_QKV) {
         const int E = e.nh * e.hd, which = nc / E, col = nc - which * E;
         ql.hh = col / e.hd;
         ql.d = col - ql.hh * e.hd;
         ql.dst = which == 0 ? e.q : which == 1 ? e.k : e.v;
         ql.rope = e.rope && which < 2;
-        r_ntok = 1.0 / (double)e.ntok;
     }
-    if (EPI == MMQ_EPI_RESIDUAL) rmc = rowmap_rcp(e.map);
 #pragma unroll
     for (int mp = 0; mp < MT * NP; ++mp) {
         const int mt = mp / NP, h = mp % NP;  // m-tile, and the RP-row pass inside it
@@ -507,28 +513,38 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
                 stg[(8 * (i >> 2) + 4 * g + (i & 3) - RP * h) * TP + 32 * nt + lr] = acc[mt][nt][i];
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's LDS writes are done
         __builtin_amdgcn_wave_barrier();
-        // the pass's rows: qkv (window, token) with the RoPE factors loaded before the stores, so
-        // their latency is paid once per pass instead of once per row; residual destination rows
-        int bwv[RP / 4], tnv[RP / 4], rrv[RP / 4];
-        v4f csv[RP / 4];
+        // the pass's rows from the row table, and what their stores add, loaded before the stores
+        // so the latency is paid once per group of rows instead of once per row: qkv RoPE factors
+        // (the whole pass), residual rows (four at a time, which keeps 128-row tiles from
+        // spilling; each element is read and written by this lane only, so in place is fine)
+        constexpr int CH = EPI == MMQ_EPI_RESIDUAL ? 4 : RP / 4;
 #pragma unroll
-        for (int it = 0; it < RP / 4; ++it) {
-            const int m = m0 + WMR * wm + 32 * mt + RP * h + it * 4 + (lane >> 4);
-            bwv[it] = tnv[it] = rrv[it] = 0;
-            csv[it] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-            if (EPI == MMQ_EPI_QKV) {
-                bwv[it] = div_rcp(m, e.ntok, r_ntok, tnv[it]);
-                if (ql.rope && cv && m < M) csv[it] = *reinterpret_cast<const v4f*>(&e.rope[(int64_t)tnv[it] * e.hd + ql.d]);
+        for (int c0 = 0; c0 < RP / 4; c0 += CH) {
+            int bwv[CH], tnv[CH], rrv[CH];
+            v4f pvv[CH];
+#pragma unroll
+            for (int j = 0; j < CH; ++j) {
+                const int tr = WMR * wm + 32 * mt + RP * h + (c0 + j) * 4 + (lane >> 4);  // row in the tile
+                bwv[j] = tnv[j] = rrv[j] = 0;
+                pvv[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                if (EPI == MMQ_EPI_QKV) {
+                    bwv[j] = rtab[tr];
+                    tnv[j] = rtab[TM + tr];
+                    if (ql.rope && cv && m0 + tr < M) pvv[j] = *reinterpret_cast<const v4f*>(&e.rope[(int64_t)tnv[j] * e.hd + ql.d]);
+                }
+                if (EPI == MMQ_EPI_RESIDUAL) {
+                    rrv[j] = cv ? rtab[tr] : -1;
+                    if (rrv[j] >= 0) pvv[j] = *reinterpret_cast<const v4f*>(&e.res[(int64_t)rrv[j] * N + nc]);
+                }
             }
-            if (EPI == MMQ_EPI_RESIDUAL) rrv[it] = m < M && cv ? map_row32(e.map, rmc, m) : -1;
-        }
 #pragma unroll
-        for (int it = 0; it < RP / 4; ++it) {
-            const int r = it * 4 + (lane >> 4);
-            const int m = m0 + WMR * wm + 32 * mt + RP * h + r;
-            const v4f v = *reinterpret_cast<const v4f*>(&stg[r * TP + 4 * c4]);
-            if (m >= M || !cv) continue;
-            epi4<EPI>(Dz, p.d_nb1, e, N, m, nc, v, bv, rrv[it], ql, bwv[it], tnv[it], csv[it]);
+            for (int j = 0; j < CH; ++j) {
+                const int r = (c0 + j) * 4 + (lane >> 4);
+                const int m = m0 + WMR * wm + 32 * mt + RP * h + r;
+                const v4f v = *reinterpret_cast<const v4f*>(&stg[r * TP + 4 * c4]);
+                if (m >= M || !cv) continue;
+                epi4<EPI>(Dz, p.d_nb1, e, N, m, nc, v, bv, rrv[j], ql, bwv[j], tnv[j], pvv[j]);
+            }
         }
         __builtin_amdgcn_wave_barrier();  // the reads are done before the next pass overwrites
         __builtin_amdgcn_s_waitcnt(0xc07f);
