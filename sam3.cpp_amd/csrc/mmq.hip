@@ -631,15 +631,32 @@ __global__ __launch_bounds__(256) void align_rows_kernel(const uint8_t* __restri
     for (int i = threadIdx.x; i < pitch_halves; i += blockDim.x) dst[r * pitch_halves + i] = i < row_halves ? s[i] : 0;
 }
 
+// mmq_reduce_kernel's rn4
+static double reduce_rcp(int64_t M, int64_t N) {
+    const int64_t n4 = N / 4;
+    return n4 > 0 && M * n4 + n4 < ((int64_t)1 << 31) && M < ((int64_t)1 << 30) ? 1.0 / (double)n4 : 0.0;
+}
+
 // Split-K: dst rows (or the fused epilogue) from the ksplit partial sums,
-// added in split order; one thread per 4 columns (N % 4 == 0).
+// added in split order; one thread per 4 columns (N % 4 == 0).  rn4 = 4 / N when
+// M * N / 4 + N / 4 < 2^31 and M < 2^30: row, column and the epilogue's row splits then come
+// from div_rcp instead of 64- and 32-bit integer divisions; else rn4 = 0.
 template <int EPI>
 __global__ __launch_bounds__(256) void mmq_reduce_kernel(const float* __restrict__ part, int ksplit, int M, int N,
-                                                         char* __restrict__ D, int64_t d_nb1, const MmqEpi e) {
+                                                         char* __restrict__ D, int64_t d_nb1, const MmqEpi e,
+                                                         double rn4) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int n4 = N / 4;
     if (t >= (int64_t)M * n4) return;
-    const int m = (int)(t / n4), nc = (int)(t - (int64_t)m * n4) * 4;
+    const bool fast = rn4 != 0.0;
+    int m, nc;
+    if (fast) {
+        m = div_rcp((int)t, n4, rn4, nc);
+        nc *= 4;
+    } else {
+        m = (int)(t / n4);
+        nc = (int)(t - (int64_t)m * n4) * 4;
+    }
     const int64_t mn = (int64_t)M * N;
     v4f f = *reinterpret_cast<const v4f*>(&part[(int64_t)m * N + nc]);
     for (int s = 1; s < ksplit; ++s) f = f + *reinterpret_cast<const v4f*>(&part[s * mn + (int64_t)m * N + nc]);
@@ -649,7 +666,7 @@ __global__ __launch_bounds__(256) void mmq_reduce_kernel(const float* __restrict
     }
     const v4f u = f + *reinterpret_cast<const v4f*>(&e.bias[nc]);
     if (EPI == MMQ_EPI_RESIDUAL) {
-        const int rr = map_row32(e.map, m);
+        const int rr = fast ? map_row32(e.map, rowmap_rcp(e.map), m) : map_row32(e.map, m);
         if (rr >= 0) {
             const v4f x = *reinterpret_cast<const v4f*>(&e.res[(int64_t)rr * N + nc]);
             *reinterpret_cast<v4f*>(&e.out[(int64_t)rr * N + nc]) = x + u;
@@ -658,7 +675,9 @@ __global__ __launch_bounds__(256) void mmq_reduce_kernel(const float* __restrict
         const int E = e.nh * e.hd, which = nc / E, col = nc - which * E, hh = col / e.hd, d = col - hh * e.hd;
         _Float16* dst = which == 0 ? e.q : which == 1 ? e.k : e.v;
         float u0 = u[0], u1 = u[1], u2 = u[2], u3 = u[3];
-        const int bw = m / e.ntok, n = m - bw * e.ntok;
+        int n;
+        const int bw = fast ? div_rcp(m, e.ntok, 1.0 / (double)e.ntok, n) : m / e.ntok;
+        if (!fast) n = m - bw * e.ntok;
         if (which < 2 && e.rope) {
             const v4f cs = *reinterpret_cast<const v4f*>(&e.rope[(int64_t)n * e.hd + d]);
             rope_pair(u0, u1, cs[0], cs[1]);
@@ -1122,11 +1141,14 @@ static hipError_t run_mmq(const MatW& w_in, const ActF16& a, const MatD& d, int6
         const unsigned g = (unsigned)((n + 255) / 256);
         char* D = reinterpret_cast<char*>(d.data);
         if (!epi || epi->kind == MMQ_EPI_STORE)
-            mmq_reduce_kernel<MMQ_EPI_STORE><<<g, 256, 0, st>>>(sp.part, sp.ks, (int)a.M, (int)N, D, d.nb1, MmqEpi{});
+            mmq_reduce_kernel<MMQ_EPI_STORE><<<g, 256, 0, st>>>(sp.part, sp.ks, (int)a.M, (int)N, D, d.nb1, MmqEpi{},
+                                                                reduce_rcp(a.M, N));
         else if (epi->kind == MMQ_EPI_RESIDUAL)
-            mmq_reduce_kernel<MMQ_EPI_RESIDUAL><<<g, 256, 0, st>>>(sp.part, sp.ks, (int)a.M, (int)N, D, 0, *epi);
+            mmq_reduce_kernel<MMQ_EPI_RESIDUAL><<<g, 256, 0, st>>>(sp.part, sp.ks, (int)a.M, (int)N, D, 0, *epi,
+                                                                   reduce_rcp(a.M, N));
         else
-            mmq_reduce_kernel<MMQ_EPI_QKV><<<g, 256, 0, st>>>(sp.part, sp.ks, (int)a.M, (int)N, D, 0, *epi);
+            mmq_reduce_kernel<MMQ_EPI_QKV><<<g, 256, 0, st>>>(sp.part, sp.ks, (int)a.M, (int)N, D, 0, *epi,
+                                                              reduce_rcp(a.M, N));
     }
     return hipGetLastError();
 }
@@ -1136,11 +1158,11 @@ hipError_t launch_mmq_reduce(const float* part, int ks, int M, int N, char* D, i
     const int64_t n = (int64_t)M * (N / 4);
     const unsigned g = (unsigned)((n + 255) / 256);
     if (!epi || epi->kind == MMQ_EPI_STORE)
-        mmq_reduce_kernel<MMQ_EPI_STORE><<<g, 256, 0, st>>>(part, ks, M, N, D, d_nb1, MmqEpi{});
+        mmq_reduce_kernel<MMQ_EPI_STORE><<<g, 256, 0, st>>>(part, ks, M, N, D, d_nb1, MmqEpi{}, reduce_rcp(M, N));
     else if (epi->kind == MMQ_EPI_RESIDUAL)
-        mmq_reduce_kernel<MMQ_EPI_RESIDUAL><<<g, 256, 0, st>>>(part, ks, M, N, D, 0, *epi);
+        mmq_reduce_kernel<MMQ_EPI_RESIDUAL><<<g, 256, 0, st>>>(part, ks, M, N, D, 0, *epi, reduce_rcp(M, N));
     else
-        mmq_reduce_kernel<MMQ_EPI_QKV><<<g, 256, 0, st>>>(part, ks, M, N, D, 0, *epi);
+        mmq_reduce_kernel<MMQ_EPI_QKV><<<g, 256, 0, st>>>(part, ks, M, N, D, 0, *epi, reduce_rcp(M, N));
     return hipGetLastError();
 }
 

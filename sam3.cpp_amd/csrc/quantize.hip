@@ -206,16 +206,30 @@ __global__ __launch_bounds__(256) void quantize_q4_kernel(const char* __restrict
 // consecutive blocks of the flattened [rows][nb] grid, so loads (128 B per
 // thread), quant stores (64 B per thread) and scale stores are contiguous.
 // I8: quants as int8 [rows][q_s1 bytes] (the int8-MFMA operand) instead of fp16 [rows][ne0].
+// rnb = 1 / (blocks per row) when the rows lie at a fixed pitch nb1 and nblocks plus a row's
+// blocks stay below 2^31: row and block then come from div_rcp, not from 64-bit divisions
+// (whose dependent chain delayed every thread's first load); else rnb = 0.
 template <bool WITH_SUM, bool I8 = false>
 __global__ __launch_bounds__(256) void quantize_mmq_kernel(const char* __restrict__ src, int stype, RowAddr ra,
                                                            int64_t ne0, int64_t nblocks, int64_t dp,
                                                            uint16_t* __restrict__ qout, uint16_t* __restrict__ dout,
-                                                           uint16_t* __restrict__ sout, int64_t q_s1 = 0) {
+                                                           uint16_t* __restrict__ sout, double rnb, int64_t q_s1 = 0) {
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= nblocks) return;
     const int64_t nbpr = ne0 / QK;
-    const int64_t r = g / nbpr, b = g - r * nbpr;
-    const char* rp = ra.row(src, r);
+    int64_t r, b;
+    const char* rp;
+    if (rnb != 0.0) {
+        int bi;
+        const int ri = div_rcp((int)g, (int)nbpr, rnb, bi);
+        r = ri;
+        b = bi;
+        rp = src + (int64_t)ri * ra.nb1;
+    } else {
+        r = g / nbpr;
+        b = g - r * nbpr;
+        rp = ra.row(src, r);
+    }
     float x[QK];
     if (stype == T_F32 && ra.nb0 == 4 && ((reinterpret_cast<uintptr_t>(rp) & 15) == 0)) {
         const v4f* p4 = reinterpret_cast<const v4f*>(rp + b * QK * 4);
@@ -297,6 +311,13 @@ __global__ __launch_bounds__(256) void convert_f16_kernel(const char* __restrict
     dst[i] = stype == T_F32 ? f2h(*reinterpret_cast<const float*>(p)) : *reinterpret_cast<const uint16_t*>(p);
 }
 
+// 1 / (blocks per row) for quantize_mmq_kernel's fast indexing, or 0 where it does not apply
+static double blocks_rcp(const SrcView& s, int64_t nblocks) {
+    const int64_t nbpr = s.ne[0] / QK;
+    const bool flat = s.ne[2] * s.ne[3] == 1 || (s.nb[2] == s.ne[1] * s.nb[1] && (s.ne[3] == 1 || s.nb[3] == s.ne[2] * s.nb[2]));
+    return flat && nbpr > 0 && nblocks + nbpr < ((int64_t)1 << 31) ? 1.0 / (double)nbpr : 0.0;
+}
+
 static RowAddr row_addr(const SrcView& s) {
     RowAddr ra;
     ra.ne1 = s.ne[1];
@@ -342,9 +363,11 @@ hipError_t launch_quantize_mmq(const SrcView& src, bool with_sum, int64_t dp, ui
     const dim3 grid((unsigned)((nblocks + 255) / 256));
     const RowAddr ra = row_addr(src);
     if (with_sum)
-        quantize_mmq_kernel<true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, dp, q, d, s);
+        quantize_mmq_kernel<true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, dp, q, d, s,
+                                                        blocks_rcp(src, nblocks));
     else
-        quantize_mmq_kernel<false><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, dp, q, d, s);
+        quantize_mmq_kernel<false><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, dp, q, d, s,
+                                                         blocks_rcp(src, nblocks));
     return hipGetLastError();
 }
 
@@ -358,9 +381,11 @@ hipError_t launch_quantize_mmq_i8(const SrcView& src, bool with_sum, int64_t s1,
     const RowAddr ra = row_addr(src);
     uint16_t* qq = reinterpret_cast<uint16_t*>(q);
     if (with_sum)
-        quantize_mmq_kernel<true, true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, dp, qq, d, s, s1);
+        quantize_mmq_kernel<true, true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, dp, qq, d, s,
+                                                              blocks_rcp(src, nblocks), s1);
     else
-        quantize_mmq_kernel<false, true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, dp, qq, d, s, s1);
+        quantize_mmq_kernel<false, true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, dp, qq, d, s,
+                                                               blocks_rcp(src, nblocks), s1);
     return hipGetLastError();
 }
 
