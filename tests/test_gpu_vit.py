@@ -128,6 +128,34 @@ def test_bias_gelu_and_residual(mi, ctx, orc):
     assert np.array_equal(xd.cpu().numpy(), (x + (h + b).astype(np.float32)).astype(np.float32))
 
 
+def test_gelu_erf_against_exact(mi, ctx):
+    """The device GELU's erf (a fitted polynomial-and-exp2 form) against
+    0.5 u (1 + erf(u / sqrt(2))) in double, on 4M evenly spaced u in [-9, 9] and on every
+    float around the erf pieces' boundary (u = +-sqrt(2)) and clamp (u = +-4 sqrt(2)).  The
+    erf error (< 9e-8), the rounding of u / sqrt(2) (through erf's slope, < 4e-8) and the
+    rounding of 1 + erf (1.2e-7) bound |got - exact| by 1.3e-7 |u|, plus one ulp of the
+    result for its own rounding."""
+    from scipy.special import erf
+    parts = [np.linspace(-9, 9, 1 << 22, dtype=np.float32)]
+    for c in (np.sqrt(2.0), 4 * np.sqrt(2.0)):
+        m = int(np.float32(c).view(np.uint32))
+        near = np.arange(m - 100000, m + 100000, dtype=np.uint32).view(np.float32)
+        parts += [near, -near]
+    u = np.concatenate(parts)
+    n = 4096
+    u = np.concatenate([u, np.zeros((-len(u)) % n, np.float32)])
+    rows = len(u) // n
+    hd_, bd = dev(u.reshape(rows, n)), dev(np.zeros(n, np.float32))
+    ctx.vit_bias_gelu(_p(hd_), _p(bd), rows, n)
+    ctx.synchronize()
+    got = hd_.cpu().numpy().reshape(-1).astype(np.float64)
+    u64 = u.astype(np.float64)
+    exact = 0.5 * u64 * (1.0 + erf(u64 / np.sqrt(2.0)))
+    bound = 1.3e-7 * np.abs(u64) + np.spacing(np.abs(exact).astype(np.float32)).astype(np.float64)
+    err = np.abs(got - exact)
+    assert (err <= bound).all(), (float(u[np.argmax(err - bound)]), float((err - bound).max()))
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 1, 1), (70, 33, 588), (5184, 1024, 588)])
 def test_mul_mat_f32(mi, ctx, orc, M, N, K):
     """F32 x F32 mul_mat (patch embedding): |gpu - exact| <= 1e-5 * sum|w x|."""
