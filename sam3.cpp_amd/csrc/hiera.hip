@@ -6,6 +6,8 @@
 // token lh*ws + lw inside it.  Every ggml node rounds to fp32 and so does
 // each fused step: no FMA contraction in this file.
 #pragma clang fp contract(off)
+#include <algorithm>
+
 #include "common.cuh"
 #include "kernels.h"
 
@@ -264,21 +266,40 @@ __global__ __launch_bounds__(256) void bias_gelu_tanh_act_kernel(const float* __
 }
 
 // conv2d columns with stride / zero padding: cols[m][k], m = oy*OW + ox,
-// k = (c*KH + ky)*KW + kx; optionally rounded to fp16 (F16 kernels, ggml_im2col F16)
+// k = (c*KH + ky)*KW + kx; optionally rounded to fp16 (F16 kernels, ggml_im2col F16).
+// Grid-stride over the n = OH OW K elements (a workgroup per 256 elements spent its time
+// in dispatch); rc = {1/K, 1/(KH KW), 1/KW, 1/OW} when n plus the grid stays below 2^31:
+// the indices then come from div_rcp instead of 64- and 32-bit divisions; else rc.k = 0.
+struct Im2colRcp {
+    double k, kk, kw, ow;
+};
 __global__ __launch_bounds__(256) void im2col_pad_kernel(const float* __restrict__ img, float* __restrict__ cols, int C,
                                                          int Hin, int Win, int KH, int KW, int stride, int pad, int OH,
-                                                         int OW, int round16) {
-    const int64_t tix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+                                                         int OW, int round16, Im2colRcp rc) {
     const int K = C * KH * KW;
-    if (tix >= (int64_t)OH * OW * K) return;
-    const int k = (int)(tix % K);
-    const int64_t m = tix / K;
-    const int kx = k % KW, ky = (k / KW) % KH, c = k / (KW * KH);
-    const int ox = (int)(m % OW), oy = (int)(m / OW);
-    const int y = oy * stride - pad + ky, xx = ox * stride - pad + kx;
-    float v = (y >= 0 && y < Hin && xx >= 0 && xx < Win) ? img[((int64_t)c * Hin + y) * Win + xx] : 0.0f;
-    if (round16) v = h2f(f2h(v));
-    cols[tix] = v;
+    const int64_t n = (int64_t)OH * OW * K, step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t tix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; tix < n; tix += step) {
+        int k, kx, ky, c, ox, oy;
+        if (rc.k != 0.0) {
+            int r;
+            const int m = div_rcp((int)tix, K, rc.k, k);
+            c = div_rcp(k, KH * KW, rc.kk, r);
+            ky = div_rcp(r, KW, rc.kw, kx);
+            oy = div_rcp(m, OW, rc.ow, ox);
+        } else {
+            k = (int)(tix % K);
+            const int64_t m = tix / K;
+            kx = k % KW;
+            ky = (k / KW) % KH;
+            c = k / (KW * KH);
+            ox = (int)(m % OW);
+            oy = (int)(m / OW);
+        }
+        const int y = oy * stride - pad + ky, xx = ox * stride - pad + kx;
+        float v = (y >= 0 && y < Hin && xx >= 0 && xx < Win) ? img[((int64_t)c * Hin + y) * Win + xx] : 0.0f;
+        if (round16) v = h2f(f2h(v));
+        cols[tix] = v;
+    }
 }
 
 // x = (conv + b) + pe over rows of C (patch embedding bias, then pos_embed)
@@ -357,9 +378,14 @@ hipError_t launch_bias_gelu_tanh_act(const float* h, const float* b, int64_t row
 }
 hipError_t launch_im2col_pad(const float* img, float* cols, int C, int Hin, int Win, int KH, int KW, int stride, int pad,
                              int OH, int OW, bool round16, hipStream_t st) {
-    const int64_t n = (int64_t)OH * OW * C * KH * KW;
-    if (n > 0)
-        im2col_pad_kernel<<<nblk(n), 256, 0, st>>>(img, cols, C, Hin, Win, KH, KW, stride, pad, OH, OW, round16 ? 1 : 0);
+    const int64_t K = (int64_t)C * KH * KW, n = (int64_t)OH * OW * K;
+    if (n <= 0) return hipSuccess;
+    // about eight elements per thread
+    const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>(nblk(n), (nblk(n) + 7) / 8));
+    Im2colRcp rc{0.0, 0.0, 0.0, 0.0};
+    if (n + (int64_t)grid * 256 < ((int64_t)1 << 31) && K > 0 && OW > 0)
+        rc = Im2colRcp{1.0 / (double)K, 1.0 / (double)(KH * KW), 1.0 / (double)KW, 1.0 / (double)OW};
+    im2col_pad_kernel<<<grid, 256, 0, st>>>(img, cols, C, Hin, Win, KH, KW, stride, pad, OH, OW, round16 ? 1 : 0, rc);
     return hipGetLastError();
 }
 hipError_t launch_bias_add_pe(float* x, const float* b, const float* pe, int64_t rows, int C, hipStream_t st) {
