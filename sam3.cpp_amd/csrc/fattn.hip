@@ -79,19 +79,25 @@ __device__ __forceinline__ float xsum32(float x) { return x + partner32(x); }
 template <int D>
 __device__ __forceinline__ int kswz(int r) { return D == 64 ? ((r & 7) ^ ((r >> 3) & 1)) : (r & 15); }
 
-template <int D, bool QF32, bool KVF32, bool KDMA>
-__global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
+// NW wavefronts of 32 queries per workgroup (4; 1 or 2 for small windows) and NBUF K/V tile
+// buffers (2; 1 when the launcher guarantees a single key tile): a window of at most 64
+// keys and 32 or 64 queries then runs in a workgroup of its own size with half the LDS, so
+// several times more windows are in flight; the arithmetic per query is the same.
+template <int D, bool QF32, bool KVF32, bool KDMA, int NW = 4, int NBUF = 2>
+__global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void fattn_kernel(const FaArgs p) {
     static_assert(!KDMA || (!KVF32 && (D == 64 || D == 128)), "K DMA staging: fp16 K, D = 64 or 128");
+    static_assert((NW == 4 && NBUF == 2) || (!KDMA && NBUF == 1 && (NW == 1 || NW == 2)), "workgroup shape");
+    constexpr int NT = 64 * NW, BQ = 32 * NW;  // threads and queries per workgroup
     constexpr int KS = KDMA ? D : D + 8;  // K tile row stride (halves)
     constexpr int VS = FA_BKV + 4;  // V^T tile row stride (halves): 34 dwords, so the 8-byte reads of 32 rows hit distinct bank pairs
     constexpr int NC = D / 16;      // MFMA k-chunks of a score
     constexpr int NDB = D / 32;     // 32-row blocks of O^T
     constexpr int C8 = D / 8;       // 8-element chunks per key row
-    constexpr int LPT = FA_BKV * C8 / FA_NT;  // chunks per thread per tile (K and V each)
-    static_assert(FA_BKV * C8 % FA_NT == 0, "tile split");
+    constexpr int LPT = FA_BKV * C8 / NT;  // chunks per thread per tile (K and V each)
+    static_assert(FA_BKV * C8 % NT == 0, "tile split");
     // two K / V^T buffers: tile t + 1 is stored while tile t is computed
-    __shared__ __attribute__((aligned(16))) _Float16 sK[2][FA_BKV * KS];
-    __shared__ __attribute__((aligned(16))) _Float16 sV[2][D * VS];
+    __shared__ __attribute__((aligned(16))) _Float16 sK[NBUF][FA_BKV * KS];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[NBUF][D * VS];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -100,13 +106,13 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
     // (g % 8) * per_xcd + g / 8 of the (batch x key range, head, query tile) list and each
     // XCD walks a contiguous band: the query tiles of a few heads at a time, whose K and V
     // then stay in that XCD's L2 instead of every head's K and V passing through every L2
-    const int qtiles = (p.nq + FA_BQ - 1) / FA_BQ, items = qtiles * p.nh * p.B * p.kv_split;
+    const int qtiles = (p.nq + BQ - 1) / BQ, items = qtiles * p.nh * p.B * p.kv_split;
     const int per_xcd = (items + 7) / 8;
     const int item = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
     if (item >= items) return;
     const int qt = item % qtiles, hz = item / qtiles, h = hz % p.nh, z = hz / p.nh;
     const int b = z / p.kv_split, ks = z - b * p.kv_split;
-    const int qi = qt * FA_BQ + w * 32 + lr;  // this lane's query
+    const int qi = qt * BQ + w * 32 + lr;  // this lane's query
     // a key split attends to keys kbeg .. kbeg + nkv: shifted K/V bases, the same code
     const int kbeg = ks * p.kv_chunk, nkv = min(p.nkv - kbeg, p.kv_chunk);
     const char* kb = p.k + (int64_t)(h / p.rk2) * p.k_nb2 + (int64_t)b * p.k_nb3 + (int64_t)kbeg * p.k_nb1;
@@ -136,7 +142,7 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
     auto load_tile = [&](int kv0) {
 #pragma unroll
         for (int j = 0; j < LPT; ++j) {
-            const int id = tid + FA_NT * j;
+            const int id = tid + NT * j;
             const int kk = id / C8, kc = id % C8;
             if (!KDMA) {
                 kreg[j] = u32x4{0, 0, 0, 0};
@@ -144,7 +150,7 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
             }
             int vk, vc;
             if (VPAIR) {
-                const int pid = tid + FA_NT * (j >> 1);
+                const int pid = tid + NT * (j >> 1);
                 vk = 2 * (pid % 32) + (j & 1);
                 vc = pid / 32;
             } else {
@@ -164,7 +170,7 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
     // of the tile with instruction j, lane i writing 16 bytes at + 16 i, i.e. slot s of row r;
     // it loads the chunk s ^ kswz(r) of key kv0 + r.  Keys past nkv lie past the end of the
     // buffer resource and read as zero.
-    constexpr int KDI = KDMA ? FA_BKV * D * 2 / 1024 / (FA_NT / 64) : 1;
+    constexpr int KDI = KDMA ? FA_BKV * D * 2 / 1024 / (NT / 64) : 1;
     const v4i krsrc = make_rsrc(kb, (int64_t)nkv * p.k_nb1);
     auto dma_k = [&](int kv0, int buf) {
 #pragma unroll
@@ -179,21 +185,21 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
         if (KDMA) {
 #pragma unroll
             for (int j = 0; j < LPT; ++j) {
-                const int id = tid + FA_NT * j, pid = tid + FA_NT * (j >> 1);
+                const int id = tid + NT * j, pid = tid + NT * (j >> 1);
                 const int vk = VPAIR ? 2 * (pid % 32) + (j & 1) : id % FA_BKV;
                 if (kv0 + vk >= nkv) vreg[j] = u32x4{0, 0, 0, 0};
             }
         }
 #pragma unroll
         for (int j = 0; j < (KDMA ? 0 : LPT); ++j) {
-            const int id = tid + FA_NT * j;
+            const int id = tid + NT * j;
             const int kk = id / C8, kc = id % C8;
             *reinterpret_cast<u32x4*>(&sK[buf][kk * KS + kc * 8]) = kreg[j];
         }
         if (VPAIR) {
 #pragma unroll
             for (int j = 0; j < LPT; j += 2) {
-                const int pid = tid + FA_NT * (j >> 1);
+                const int pid = tid + NT * (j >> 1);
                 const int vk = 2 * (pid % 32), vc = pid / 32;
                 uint32_t* col = reinterpret_cast<uint32_t*>(&sV[buf][(vc * 8) * VS + vk]);
 #pragma unroll
@@ -205,7 +211,7 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
         } else {
 #pragma unroll
             for (int j = 0; j < LPT; ++j) {
-                const int id = tid + FA_NT * j;
+                const int id = tid + NT * j;
                 const int vk = id % FA_BKV, vc = id / FA_BKV;
                 uint16_t* col = reinterpret_cast<uint16_t*>(&sV[buf][(vc * 8) * VS + vk]);
 #pragma unroll
@@ -231,12 +237,13 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
     // tile t + 1 goes from the registers (loaded during tile t) into that buffer and
     // tile t + 2's loads are issued, so each load has a whole tile to land.
     const int ntile = (nkv + FA_BKV - 1) / FA_BKV;
+    if (NBUF == 1 && ntile > 1) return;  // one buffer holds one tile (the launcher's condition)
     if (KDMA) dma_k(0, 0);
     load_tile(0);
     store_tile(0, 0);
     if (ntile > 1) load_tile(FA_BKV);
     for (int t = 0; t < ntile; ++t) {
-        const int kv0 = t * FA_BKV, cb = t & 1;
+        const int kv0 = t * FA_BKV, cb = NBUF == 1 ? 0 : (t & 1);
         if (KDMA) {  // tile t's K DMA precedes tile t + 1's LPT V loads (when issued)
             if (t + 1 < ntile) wait_vmcnt<LPT>();
             else wait_vmcnt<0>();
@@ -321,7 +328,7 @@ __global__ __launch_bounds__(FA_NT, 2) void fattn_kernel(const FaArgs p) {
                                                                   __builtin_bit_cast(v8h, bp), O[db], 0, 0, 0);
                 }
         }
-        if (t + 1 < ntile) {
+        if (NBUF == 2 && t + 1 < ntile) {
             store_tile(cb ^ 1, kv0 + FA_BKV);
             if (t + 2 < ntile) load_tile(kv0 + 2 * FA_BKV);
         }
@@ -464,6 +471,17 @@ static void fa_launch_d(const FaArgs& a, bool qf32, bool kvf32, int B, hipStream
             else fattn_kernel<D, false, false, true><<<grid, FA_NT, 0, st>>>(a);
             launched = true;
         }
+    }
+    // windows of at most one key tile and 64 queries, fp16 operands, no key split: one or two
+    // wavefronts per workgroup and one K/V buffer
+    const int nw = a.nq <= 32 ? 1 : 2;
+    const bool small = !launched && !qf32 && !kvf32 && a.kv_split == 1 && a.nkv <= FA_BKV && a.nq <= 64;
+    if (small) {
+        const int64_t sitems = (int64_t)((a.nq + 32 * nw - 1) / (32 * nw)) * a.nh * B;
+        const dim3 sgrid((unsigned)((sitems + 7) / 8 * 8));
+        if (nw == 1) fattn_kernel<D, false, false, false, 1, 1><<<sgrid, 64, 0, st>>>(a);
+        else fattn_kernel<D, false, false, false, 2, 1><<<sgrid, 128, 0, st>>>(a);
+        launched = true;
     }
     if (launched) {
     } else if (qf32 && kvf32) fattn_kernel<D, true, true, false><<<grid, FA_NT, 0, st>>>(a);

@@ -87,6 +87,13 @@ def _check(orc, got, q, k, v, scale, t):
     (96, 196, 196, 4, 4, 3),      # Hiera 14x14 windows
     (96, 1024, 1024, 4, 4, 1),    # few query tiles: keys split over workgroups, then combined
     (64, 300, 2000, 2, 1, 1),     # uneven key ranges, grouped kv heads
+    # at most 64 keys and 64 queries: one- and two-wavefront workgroups, one K/V buffer
+    (96, 1, 1, 1, 1, 1),
+    (96, 16, 16, 2, 2, 64),       # Hiera-tiny stage 1 (4x4 windows)
+    (96, 4, 16, 4, 4, 64),        # the pooled stage-1 -> 2 block (4 queries per window)
+    (96, 64, 64, 1, 1, 32),       # stage 0 (8x8 windows)
+    (96, 49, 49, 8, 8, 25),       # stage 3 (7x7 windows)
+    (96, 33, 64, 2, 1, 3),        # two wavefronts, grouped kv heads
 ])
 def test_flash_attn_f16(mi, ctx, orc, D, nq, nkv, nh, nhk, B):
     q, k, v = (_f16(a) for a in _inputs(orc, D, nq, nkv, nh, nhk, B))
