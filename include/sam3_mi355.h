@@ -343,7 +343,8 @@ mi355_status mi355_hiera_block_forward(mi355_context* ctx, const mi355_hiera_hpa
 /* The whole backbone: image device F32 [3][img][img]; patch_w [7, 7, 3, E]
  * F32 or F16, patch_b [E], pos_embed [S0*S0][E] (S0 = img/4).  stage_out[s]
  * (device [S_s*S_s][C_s], or NULL) receive the output of each stage's last
- * block. */
+ * block, which writes it there directly; the next stage reads it from there, so
+ * the maps must not overlap one another. */
 mi355_status mi355_hiera_encode(mi355_context* ctx, const mi355_hiera_hparams* hp, const float* image,
                                 const mi355_tensor* patch_w, const float* patch_b, const float* pos_embed,
                                 const mi355_hiera_block* blocks, int n_blocks, float* const stage_out[4]);

@@ -578,18 +578,18 @@ mi355_status mi355_hiera_encode(mi355_context* ctx, const mi355_hiera_hparams* h
         total += hp->stages[s];
         ends[s] = total - 1;
     }
+    // a stage's last block writes its output straight into the caller's stage map, which the
+    // next block then reads (run_block only reads its input); the internal pair x0 / x1 takes
+    // every other output, the one that is not the current input
     for (int i = 0; i < n_blocks; ++i) {
-        TRY(run_block(ctx, hp, infos[i], &blocks[i], cur, S, nxt, b));
-        std::swap(cur, nxt);
-        if (infos[i].qs) S /= 2;
         while (stage < 4 && hp->stages[stage] == 0) ++stage;
-        if (stage < 4 && i == ends[stage]) {
-            if (stage_out && stage_out[stage])
-                TRY(hip_check(ctx, hipMemcpyAsync(stage_out[stage], cur, (size_t)S * S * infos[i].dim_out * 4,
-                                                  hipMemcpyDeviceToDevice, st),
-                              "stage output copy"));
-            ++stage;
-        }
+        const bool last = stage < 4 && i == ends[stage];
+        float* dst = last && stage_out && stage_out[stage] ? stage_out[stage] : nxt;
+        TRY(run_block(ctx, hp, infos[i], &blocks[i], cur, S, dst, b));
+        cur = dst;
+        nxt = cur == b.x0 ? b.x1 : b.x0;
+        if (infos[i].qs) S /= 2;
+        if (last) ++stage;
     }
     return MI355_STATUS_SUCCESS;
 }
