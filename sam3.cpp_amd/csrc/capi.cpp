@@ -488,6 +488,8 @@ mi355_status mul_mat_act(mi355_context* ctx, const mi355_tensor* s0, const ActF1
     }
     const MmqSplit sp{ks, ks > 1 ? reinterpret_cast<float*>(static_cast<char*>(ctx->ws) + align) : nullptr,
                       ctx->skinny};
+    if (epi && epi->ln_next)
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat_act: a LayerNorm hand-off needs int8-layout weights");
     static const char* names[4][3] = {{"mmq_f16", "mmq_f16+residual", "mmq_f16+qkv"},
                                       {"mmq_q8_0", "mmq_q8_0+residual", "mmq_q8_0+qkv"},
                                       {"mmq_q4_0", "mmq_q4_0+residual", "mmq_q4_0+qkv"},

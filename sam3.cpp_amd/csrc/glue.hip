@@ -74,6 +74,49 @@ __global__ __launch_bounds__(256) void ln1024_kernel(const LnArgs a) {
     act_store_half16(a.out, orow, 1024, l, y);
 }
 
+// The K-split reduction of a 1024-wide residual GEMM followed by the next LayerNorm, in one
+// pass: one wavefront per row, lane l holding columns 16l .. 16l + 15.  x = x + ((p_0 + ... +
+// p_{ks-1}) + bias) with mmq_reduce_kernel's adds in its order, written back, then that row's
+// LayerNorm into a.out as ln1024_kernel computes it (a.x is this x, no addend): the bits of
+// the two passes, without reading x back.
+template <int KS>
+__global__ __launch_bounds__(256) void reduce_residual_ln1024_kernel(const float* __restrict__ part,
+                                                                     const float* __restrict__ bias, float* x,
+                                                                     const LnArgs a) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= a.rows) return;
+    const int l = threadIdx.x & 63;
+    const int64_t mn = a.rows * 1024;
+    float* xr = x + r * 1024;
+    // every load of the row issued before the first add
+    v4f pv[KS][4], bv[4], xv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int c = 4 * (l * 4 + v);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) pv[s][v] = *reinterpret_cast<const v4f*>(part + s * mn + r * 1024 + c);
+        bv[v] = *reinterpret_cast<const v4f*>(bias + c);
+        xv[v] = *reinterpret_cast<const v4f*>(xr + c);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        v4f f = pv[0][v];
+#pragma unroll
+        for (int s = 1; s < KS; ++s) f = f + pv[s][v];
+        const v4f u = f + bv[v];
+        xv[v] = xv[v] + u;
+        *reinterpret_cast<v4f*>(xr + 4 * (l * 4 + v)) = xv[v];
+    }
+    ln_group<4, true>(xv, l, 64, 1024, a.w, a.b, a.eps);
+    const int64_t orow = a.ws > 0 ? win_row(r, a.grid, a.ws) : r;
+    float y[16];
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[4 * v + i] = xv[v][i];
+    act_store_half16(a.out, orow, 1024, l, y);
+}
+
 // G lanes per row (E = 4*G*V), 256/G rows per workgroup, float4 loads
 template <int V>
 __global__ __launch_bounds__(256) void ln_group_kernel(const LnArgs a, int G) {
@@ -347,6 +390,17 @@ __global__ __launch_bounds__(256) void im2col_kernel(const float* __restrict__ i
 }
 
 static unsigned blocks_for(int64_t n, int per_block = 256) { return (unsigned)((n + per_block - 1) / per_block); }
+
+hipError_t launch_reduce_residual_ln1024(const float* part, int ks, const float* bias, float* x, const LnArgs& a,
+                                        hipStream_t st) {
+    if (a.rows <= 0) return hipSuccess;
+    if (a.E != 1024 || a.x != x || a.add || ks < 2 || ks > 4 || !part || !bias) return hipErrorInvalidValue;
+    const unsigned g = blocks_for(a.rows, 4);
+    if (ks == 2) reduce_residual_ln1024_kernel<2><<<g, 256, 0, st>>>(part, bias, x, a);
+    else if (ks == 3) reduce_residual_ln1024_kernel<3><<<g, 256, 0, st>>>(part, bias, x, a);
+    else reduce_residual_ln1024_kernel<4><<<g, 256, 0, st>>>(part, bias, x, a);
+    return hipGetLastError();
+}
 
 hipError_t launch_layer_norm(const LnArgs& a, hipStream_t st) {
     if (a.rows <= 0) return hipSuccess;

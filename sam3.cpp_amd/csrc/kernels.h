@@ -116,6 +116,7 @@ struct RowMap {
 //                     [q | k | v], RoPE on q and k (rope non-null), fp16 out to
 //                     q/k/v [M/ntok][nh][ntok][hd] (the qkv_rope pass)
 enum { MMQ_EPI_STORE = 0, MMQ_EPI_RESIDUAL = 1, MMQ_EPI_QKV = 2 };
+struct LnArgs;
 struct MmqEpi {
     int kind;
     const float* bias;  // [N]
@@ -125,6 +126,9 @@ struct MmqEpi {
     const float* rope;  // [ntok][hd/2][2] (cos, sin) or null
     _Float16 *q, *k, *v;
     int ntok, nh, hd;
+    // int8 route, MMQ_EPI_RESIDUAL: the LayerNorm to run on `out` afterwards (the next
+    // block's first), fused into the K-split reduction where the shape allows; else null
+    const LnArgs* ln_next;
 };
 hipError_t launch_mmq_epi(const MatW& w, const ActF16& a, int64_t N, const MmqEpi& e, void* align_buf,
                           const MmqSplit& sp, hipStream_t st);
@@ -240,6 +244,10 @@ struct LnArgs {
     float eps;
 };
 hipError_t launch_layer_norm(const LnArgs& a, hipStream_t st);
+// x = x + (sum of ks partial sums [ks][rows][1024] in order + bias), then the LayerNorm a of
+// that x (a.x == x, E = 1024, no addend): the K-split reduction and the next LayerNorm in one pass
+hipError_t launch_reduce_residual_ln1024(const float* part, int ks, const float* bias, float* x, const LnArgs& a,
+                                        hipStream_t st);
 
 struct QkvArgs {
     const float* qkv;   // [M][3E] (rows in attention-batch order)

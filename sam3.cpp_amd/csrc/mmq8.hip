@@ -797,12 +797,18 @@ hipError_t launch_mmq8(const WRep& w, const ActI8& a, const MatD& d, const MmqEp
         case T_Q4_1 * 2: launch8_t<T_Q4_1, 128>(p, epi, st); break;
         default: launch8_t<T_Q4_1, 64>(p, epi, st); break;
     }
+    hipError_t e0 = hipGetLastError();
+    if (e0 != hipSuccess) return e0;
+    const LnArgs* ln = epi && epi->kind == MMQ_EPI_RESIDUAL ? epi->ln_next : nullptr;
     if (split) {
-        const hipError_t e0 = hipGetLastError();
+        // a 1024-wide residual into its own rows: the reduction and the next LayerNorm in one pass
+        if (ln && N == 1024 && sp.ks <= 4 && epi->map.kind == ROWMAP_IDENTITY && epi->res == epi->out &&
+            ln->x == epi->out && ln->rows == a.M && !ln->add)
+            return launch_reduce_residual_ln1024(sp.part, sp.ks, epi->bias, epi->out, *ln, st);
+        e0 = launch_mmq_reduce(sp.part, sp.ks, (int)a.M, (int)N, reinterpret_cast<char*>(d.data), d.nb1, epi, st);
         if (e0 != hipSuccess) return e0;
-        return launch_mmq_reduce(sp.part, sp.ks, (int)a.M, (int)N, reinterpret_cast<char*>(d.data), d.nb1, epi, st);
     }
-    return hipGetLastError();
+    return ln ? launch_layer_norm(*ln, st) : hipSuccess;
 }
 
 }  // namespace mi355

@@ -276,8 +276,12 @@ mi355_status mi355_vit_prefix(mi355_context* ctx, const mi355_vit_hparams* hp, c
     return mi355_vit_layer_norm(ctx, b.xn, pos_embed, hp->pos_grid, ln_pre_w, ln_pre_b, x, M, E, G, 0, hp->eps);
 }
 
-mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams* hp, const mi355_vit_block* blk,
-                                     float* x) {
+// One block.  next: the block that follows (or null); when it is given and the shapes allow,
+// this block's fc2 also runs next's LN1 into the qkv operand (fused into the K-split
+// reduction at E = 1024) and sets *ln_next_done.  ln1_ready: this block's LN1 already ran so.
+static mi355_status block_forward(mi355_context* ctx, const mi355_vit_hparams* hp, const mi355_vit_block* blk, float* x,
+                                  const mi355_vit_block* next, bool ln1_ready, bool* ln_next_done) {
+    if (ln_next_done) *ln_next_done = false;
     mi355_status st = check_hp(ctx, hp);
     if (st != MI355_STATUS_SUCCESS) return st;
     if (!blk || !x || !blk->norm1_w || !blk->norm1_b || !blk->qkv_b || !blk->proj_b || !blk->norm2_w || !blk->norm2_b ||
@@ -303,9 +307,10 @@ mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams
     } while (0)
     // LN -> the GEMM's activation operand (fused) or F32 rows
     auto ln_gemm = [&](const float* w, const float* bb, int ws, const mi355_tensor& W, float* out, int64_t N,
-                       const MmqEpi* epi) -> mi355_status {
+                       const MmqEpi* epi, bool ready = false) -> mi355_status {
         const int mode = ctx->fuse ? act_mode_for_weight(&W) : ACT_F32;
         if (mode == ACT_F32 && epi) return fail(ctx, MI355_STATUS_FAILED, "vit: epilogue without a fused operand");
+        if (mode == ACT_F32 && ready) return fail(ctx, MI355_STATUS_FAILED, "vit: LayerNorm handed over without an operand");
         if (mode == ACT_F32) {
             mi355_status s1 = mi355_vit_layer_norm(ctx, x, nullptr, 0, w, bb, b.xn, M, E, G, ws, hp->eps);
             if (s1 != MI355_STATUS_SUCCESS) return s1;
@@ -324,7 +329,7 @@ mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams
         a.grid = G;
         a.ws = ws;
         a.eps = hp->eps;
-        {
+        if (!ready) {
             Timed t(ctx, "layer_norm");
             mi355_status s1 = hip_check(ctx, t.done(launch_layer_norm(a, ctx->stream)), "layer_norm launch");
             if (s1 != MI355_STATUS_SUCCESS) return s1;
@@ -346,9 +351,9 @@ mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams
         e.ntok = N;
         e.nh = NH;
         e.hd = HD;
-        TRY(ln_gemm(blk->norm1_w, blk->norm1_b, WS, blk->qkv_w, nullptr, 3 * E, &e));
+        TRY(ln_gemm(blk->norm1_w, blk->norm1_b, WS, blk->qkv_w, nullptr, 3 * E, &e, ln1_ready));
     } else {
-        TRY(ln_gemm(blk->norm1_w, blk->norm1_b, WS, blk->qkv_w, b.qkv, 3 * E, nullptr));
+        TRY(ln_gemm(blk->norm1_w, blk->norm1_b, WS, blk->qkv_w, b.qkv, 3 * E, nullptr, ln1_ready));
         TRY(mi355_vit_qkv_rope(ctx, b.qkv, blk->qkv_b, blk->freqs_cis, b.q, b.k, b.v, M, N, NH, HD));
     }
     // attention; for quantized / F16 proj weights it writes the projection's operand
@@ -395,10 +400,35 @@ mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams
         e.res = x;
         e.out = x;
         e.map = RowMap{ROWMAP_IDENTITY, 0, 0, 0, 0};
+        // the next block's LN1 (its qkv operand) handed to the int8 route with this residual
+        const int WSn = next ? (next->is_global ? 0 : hp->window_size) : 0;
+        const int mn = next && ctx->fuse ? act_mode_for_weight(&next->qkv_w) : ACT_F32;
+        LnArgs la;
+        if (ln_next_done && mn != ACT_F32 && blk->fc2_w.layout == MI355_LAYOUT_INT8 && next->norm1_w &&
+            next->norm1_b && (WSn == 0 || (WSn > 0 && G % WSn == 0))) {
+            la.x = x;
+            la.add = nullptr;
+            la.add_grid = 0;
+            la.w = next->norm1_w;
+            la.b = next->norm1_b;
+            la.out = act_out(b, mn, M, E);
+            la.rows = M;
+            la.E = E;
+            la.grid = G;
+            la.ws = WSn;
+            la.eps = hp->eps;
+            e.ln_next = &la;
+        }
         TRY(mul_mat_epi(ctx, &blk->fc2_w, act_in(b, m2, M, MLP, true), e));
+        if (e.ln_next) *ln_next_done = true;
     }
 #undef TRY
     return MI355_STATUS_SUCCESS;
+}
+
+mi355_status mi355_vit_block_forward(mi355_context* ctx, const mi355_vit_hparams* hp, const mi355_vit_block* blk,
+                                     float* x) {
+    return block_forward(ctx, hp, blk, x, nullptr, false, nullptr);
 }
 
 mi355_status mi355_vit_encode(mi355_context* ctx, const mi355_vit_hparams* hp, const float* image,
@@ -406,7 +436,12 @@ mi355_status mi355_vit_encode(mi355_context* ctx, const mi355_vit_hparams* hp, c
                               const float* ln_pre_b, const mi355_vit_block* blocks, int n_blocks, float* x) {
     if (n_blocks < 0 || (n_blocks > 0 && !blocks)) return fail(ctx, MI355_STATUS_INVALID_ARG, "vit_encode: bad blocks");
     mi355_status st = mi355_vit_prefix(ctx, hp, image, patch_w, pos_embed, ln_pre_w, ln_pre_b, x);
-    for (int i = 0; i < n_blocks && st == MI355_STATUS_SUCCESS; ++i) st = mi355_vit_block_forward(ctx, hp, &blocks[i], x);
+    bool ready = false;  // block i's LN1 already ran in block i - 1's fc2
+    for (int i = 0; i < n_blocks && st == MI355_STATUS_SUCCESS; ++i) {
+        bool done = false;
+        st = block_forward(ctx, hp, &blocks[i], x, i + 1 < n_blocks ? &blocks[i + 1] : nullptr, ready, &done);
+        ready = done;
+    }
     return st;
 }
 

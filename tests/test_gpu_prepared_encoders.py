@@ -95,6 +95,46 @@ def test_vit_block_full_prepared_bit_identical(mi, ctx, orc, is_global, tname):
     assert torch.equal(got, ref), f"max diff {(got - ref).abs().max().item():.3e}"
 
 
+@pytest.mark.parametrize("tname", ["q8_0", "q4_0"])
+def test_vit_encode_prepared_layernorm_handoff(mi, ctx, orc, tname):
+    """On prepared weights mi355_vit_encode gives each block's fc2 the next block's LN1 (at
+    E = 1024 in one pass with fc2's K-split reduction, into the window or image order the
+    next block needs): the encoder equals the prefix plus mi355_vit_block_forward block by
+    block, and the encoder on the ggml-layout weights, bit for bit.  Four blocks at the real
+    SAM3 width: windowed, global, windowed, windowed."""
+    t = orc.NAME_TYPE[tname]
+    S = full.GRID * full.P
+    img = orc.uniform(3 * S * S, 95, 1).reshape(3, S, S)
+    pw = orc.normal(full.E * 3 * full.P * full.P, 95, 2, std=0.02).reshape(full.E, 3, full.P, full.P)
+    pos = orc.normal(full.PG * full.PG * full.E, 95, 3).reshape(full.PG * full.PG, full.E)
+    lw = orc.normal(full.E, 95, 4) * np.float32(0.2) + np.float32(1.0)
+    lb = orc.normal(full.E, 95, 5) * np.float32(0.1)
+    fw, fg = dev(full._freqs(orc, 0)), dev(full._freqs(orc, 1))
+    raw, prep, keep = [], [], []
+    for i, g in enumerate((0, 1, 0, 0)):
+        blk, _host, _vec, k = full._vit_block_weights(mi, orc, t, 130 + i, g, fg if g else fw)
+        keep.append(k)
+        raw.append(blk)
+        prep.append(_prepared_copy(mi, ctx, blk, mi.VitBlock, ("qkv", "proj", "fc1", "fc2"), keep))
+    hp = full._hp(mi)
+    imgd, pwd, posd, lwd, lbd = dev(img), dev(pw), dev(pos), dev(lw), dev(lb)
+    patch = mi.from_torch(pwd, mi.F32, [full.P, full.P, 3, full.E])
+    print(f"vit encode {tname}: 4 blocks at E={full.E}, prepared and ggml layout", flush=True)
+    outs = {}
+    for name, blocks in (("prepared", prep), ("ggml", raw)):
+        x = torch.empty((full.GRID * full.GRID, full.E), dtype=torch.float32, device="cuda")
+        ctx.vit_encode(hp, tv._p(imgd), patch, tv._p(posd), tv._p(lwd), tv._p(lbd), blocks, tv._p(x))
+        outs[name] = x
+    x = torch.empty_like(outs["prepared"])
+    ctx.vit_prefix(hp, tv._p(imgd), patch, tv._p(posd), tv._p(lwd), tv._p(lbd), tv._p(x))
+    for blk in prep:
+        ctx.vit_block_forward(hp, blk, tv._p(x))
+    ctx.synchronize()
+    assert torch.isfinite(x).all()
+    assert torch.equal(outs["prepared"], x), f"max diff {(outs['prepared'] - x).abs().max().item():.3e}"
+    assert torch.equal(outs["ggml"], x), f"max diff {(outs['ggml'] - x).abs().max().item():.3e}"
+
+
 @pytest.mark.parametrize("tname", ["q8_0", "q4_0", "q4_1"])
 @pytest.mark.parametrize("idx,S", th.CASES)
 def test_hiera_block_prepared_bit_identical(mi, ctx, orc, tname, idx, S):
