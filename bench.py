@@ -730,7 +730,7 @@ def main():
         cpu_tops = 2.0 * M_TOK * N * K / med / 1e12
         cpu = {"value": round(cpu_tops, 4), "unit": "TOPS", "cores": nth, "kind": "port",
                "sample": f"fc1 Q8_0 mul_mat (quantize + block dots) 5184 x 4736 x 1024, median of 5 after 2 "
-                         f"warmups: {med * 1e3:.1f} ms; {nth} threads (the box's CPU share for one GPU) of "
+                         f"warmups: {med * 1e3:.1f} ms; {nth} threads (the host CPU share of one GPU) of "
                          f"nproc={os.cpu_count()}, isa={'avx2' if orc.lib().orc_isa_path() == 1 else 'scalar'}, "
                          f"cpu={cpu_model()}"}
 

@@ -100,7 +100,7 @@ def lib():
 
 
 def nthreads() -> int:
-    """Host threads for oracle work (capped at 16, the GPU box's CPU share)."""
+    """Host threads for oracle work (capped at 16: the host CPU share of one GPU)."""
     return max(1, min(16, os.cpu_count() or 1))
 
 
