@@ -192,9 +192,8 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
         woff[i] = n0 + row < N ? (int)((int64_t)(n0 + row) * p.w_s1) + tch * 16 : OOB8;
     }
     // scale dwords: wavefronts 0, 1 load d_a (both halves, and for Q4_1 the Q8_1 sums) of rows
-    // 64 (w & 1) + lane, 2 and 3 d_w (and for Q4_1 the minima); the d_w side loads d_w twice (the
-    // same bytes to the same LDS words) so that every wavefront issues NL DMA instructions per
-    // stage and one vmcnt wait serves both sides
+    // 64 (w & 1) + lane, 2 and 3 d_w (and for Q4_1 the minima); at 128 rows the d_w side issues
+    // one scale DMA fewer than the d_a side (NL - 1 per stage), and each side waits on its own count
     // (TM = 64: d_a has one wavefront's worth of rows; wavefront 0 loads its low halves and
     // wavefront 1 its high halves, Q4_1's sums loaded by both)
     const bool a_side = w < 2;
@@ -202,7 +201,9 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
     const int soff = a_side ? (m0 + srow < M ? (int)((int64_t)(m0 + srow) * p.nst * 4) : OOB8)
                             : (n0 + srow < N ? (int)((int64_t)(n0 + srow) * p.nst * 4) : OOB8);
     constexpr int NS = (TM == 128 ? 2 : 1) + (Q41 ? 1 : 0);  // scale DMA instructions per stage and wavefront
-    constexpr int NL = MT + 2 + NS;                          // all DMA instructions per stage and wavefront
+    constexpr int NL = MT + 2 + NS;                          // all DMA instructions per stage, d_a side
+    // the d_w side at 128 rows: rs[0] and rs[1] would both be d_w; it loads it once (NL - 1 instructions)
+    const bool wdup = TM == 128 && !a_side;
     // descriptors and LDS destinations, fixed for the whole K loop: stage s adds s * SKB (tiles)
     // or 4 s (scale dwords) in the instructions' SGPR offset
     const v4i ar = make_rsrc(Az, a_ext), wr = make_rsrc(Wz, w_ext);
@@ -228,7 +229,7 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
                 ls[NS - 1] = (uint32_t)offsetof(St, as) + half;
             }
         } else {
-            for (int j = 0; j < NS; ++j) {  // d_w (repeated up to NS, then Q4_1's minima)
+            for (int j = 0; j < NS; ++j) {  // d_w (twice at 128 rows, the first skipped; then Q4_1's minima)
                 rs[j] = make_rsrc(p.Wd + 2 * so0, sw_ext);
                 ls[j] = (uint32_t)offsetof(St, wd) + half;
             }
@@ -256,23 +257,33 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
 #pragma unroll
         for (int i = 0; i < 2; ++i) dma_b128_so(wr, lb + ltw[i], past ? OOB8 : woff[i], k0);
 #pragma unroll
-        for (int j = 0; j < NS; ++j) dma_b32_so(rs[j], lb + ls[j], soff, 4 * s);
+        for (int j = 0; j < NS; ++j)
+            if (j > 0 || !wdup) dma_b32_so(rs[j], lb + ls[j], soff, 4 * s);
     };
-    // the same for a stage with no chunk past K
-    auto dma_full = [&](int s, uint32_t lb) __attribute__((always_inline)) {
+    // DMA instruction i (< NL) of stage s into the buffer at lb: the A-tile rows, the W-tile rows,
+    // then the scale dwords (the d_w side's duplicate skipped)
+    auto dma_one = [&](int i, int s, uint32_t lb) __attribute__((always_inline)) {
         const int k0 = s * SKB;
-#pragma unroll
-        for (int i = 0; i < MT; ++i) dma_b128_so(ar, lb + lta[i], aoff[i], k0);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) dma_b128_so(wr, lb + ltw[i], woff[i], k0);
-#pragma unroll
-        for (int j = 0; j < NS; ++j) dma_b32_so(rs[j], lb + ls[j], soff, 4 * s);
+        if (i < MT) {
+            dma_b128_so(ar, lb + lta[i < MT ? i : 0], aoff[i < MT ? i : 0], k0);
+        } else if (i < MT + 2) {
+            dma_b128_so(wr, lb + ltw[i - MT < 2 ? i - MT : 0], woff[i - MT < 2 ? i - MT : 0], k0);
+        } else {
+            const int j = i - MT - 2 < NS ? i - MT - 2 : 0;
+            if (j > 0 || !wdup) dma_b32_so(rs[j], lb + ls[j], soff, 4 * s);
+        }
     };
     // wait until this wavefront's DMA of all but the last `later` stages issued has landed
     auto wait_dma = [&](int later) __attribute__((always_inline)) {
-        if (later >= 2) wait_vmcnt<2 * NL>();
-        else if (later == 1) wait_vmcnt<NL>();
-        else wait_vmcnt<0>();
+        if (wdup) {
+            if (later >= 2) wait_vmcnt<2 * (NL - 1)>();
+            else if (later == 1) wait_vmcnt<NL - 1>();
+            else wait_vmcnt<0>();
+        } else {
+            if (later >= 2) wait_vmcnt<2 * NL>();
+            else if (later == 1) wait_vmcnt<NL>();
+            else wait_vmcnt<0>();
+        }
     };
 
     const int wm = w & 1, wn = w >> 1;
@@ -370,7 +381,10 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
 
     // units of one block of stage s: (mt, nt) = (0,0), (0,1), (1,0), (1,1); the previous unit's
     // combine (buffer p2) runs behind this unit's MFMAs (buffer u2)
-    auto units = [&](int s, int bk, const FragB& f, const St& b, bool first) __attribute__((always_inline)) {
+    // s3 >= 0: unit q also issues DMA instructions [q NL / NU, (q + 1) NL / NU) of stage s3 into the
+    // buffer at lb3, right after its isum MFMA, so the refill is spread over the block's units
+    auto units = [&](int s, int bk, const FragB& f, const St& b, bool first, int s3 = -1, uint32_t lb3 = 0)
+                     __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < NU; ++q) {
             const int mt = q >> 1, nt = q & 1;
@@ -400,6 +414,10 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
             const bool has_prev = !first || bk > 0 || q > 0;
             const int pq = (q + NU - 1) % NU;
             PI[u2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f.a[mt], f.b[nt], kbias, 0, 0, 0);
+            if (s3 >= 0) {
+#pragma unroll
+                for (int i = q * NL / NU; i < (q + 1) * NL / NU; ++i) dma_one(i, s3, lb3);
+            }
             __builtin_amdgcn_sched_barrier(0);
             if (has_prev) apply_half(acc[pq >> 1][pq & 1], PI[p2], PS[p2], 0);
             __builtin_amdgcn_sched_barrier(0);
@@ -432,15 +450,15 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
             for (int i = 0; i < 2; ++i) dw[i] = dwn[i];
         }
     };
-    // the steady state: 0 < s, stage s + 3 exists and has no chunk past K
+    // the steady state: 0 < s, stage s + 3 exists and has no chunk past K; its refill is spread
+    // over block 1's units (the fragments of block 1 are already in registers)
     auto stage_full = [&](int s, St& cur, St& nxt, uint32_t lcur) __attribute__((always_inline)) {
         units(s, 0, f0, cur, false);
-        wait_vmcnt<NL>();  // stage s + 1 has landed (s + 2 may be in flight)
+        wait_dma(1);  // stage s + 1 has landed (s + 2 may be in flight)
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        dma_full(s + 3, lcur);
         load_blk(nxt, 0, f0);
         load_dw(nxt, dwn);
-        units(s, 1, f1, cur, false);
+        units(s, 1, f1, cur, false, s + 3, lcur);
         load_blk(nxt, 1, f1);
 #pragma unroll
         for (int i = 0; i < 2; ++i) dw[i] = dwn[i];

@@ -296,6 +296,25 @@ __global__ __launch_bounds__(256) void quantize_mmq_kernel(const char* __restric
     }
 }
 
+// Flat F32 rows (row r at src + r * nb1, elements contiguous, base and nb1 16-byte aligned) ->
+// F16 rows of `pitch` halves, 8 elements per thread (two 16-byte loads, one 16-byte store) with
+// the row from div_rcp; ne0 % 8 == 0, pitch == ne0.
+__global__ __launch_bounds__(256) void convert_f16_flat_kernel(const char* __restrict__ src, int64_t nb1, int cpr,
+                                                               int nchunks, double rcpr, uint16_t* __restrict__ dst) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nchunks) return;
+    int k;
+    const int r = div_rcp(i, cpr, rcpr, k);
+    const v4f* p = reinterpret_cast<const v4f*>(src + (int64_t)r * nb1 + (int64_t)k * 32);
+    const v4f a = p[0], b = p[1];
+    uint4 o;
+    o.x = (uint32_t)f2h(a[0]) | ((uint32_t)f2h(a[1]) << 16);
+    o.y = (uint32_t)f2h(a[2]) | ((uint32_t)f2h(a[3]) << 16);
+    o.z = (uint32_t)f2h(b[0]) | ((uint32_t)f2h(b[1]) << 16);
+    o.w = (uint32_t)f2h(b[2]) | ((uint32_t)f2h(b[3]) << 16);
+    *reinterpret_cast<uint4*>(dst + (int64_t)i * 8) = o;
+}
+
 // dst rows of `pitch` halves; columns ne0..pitch are zero
 __global__ __launch_bounds__(256) void convert_f16_kernel(const char* __restrict__ src, int stype, RowAddr ra,
                                                           int64_t ne0, int64_t pitch, int64_t n,
@@ -316,6 +335,15 @@ static double blocks_rcp(const SrcView& s, int64_t nblocks) {
     const int64_t nbpr = s.ne[0] / QK;
     const bool flat = s.ne[2] * s.ne[3] == 1 || (s.nb[2] == s.ne[1] * s.nb[1] && (s.ne[3] == 1 || s.nb[3] == s.ne[2] * s.nb[2]));
     return flat && nbpr > 0 && nblocks + nbpr < ((int64_t)1 << 31) ? 1.0 / (double)nbpr : 0.0;
+}
+
+// F32 rows at one pitch nb[1] (the batch dims folded in), elements contiguous, base and pitch
+// 16-byte aligned, and n units (blocks or chunks) plus a row's units below 2^31: the layout
+// convert_f16_flat_kernel takes
+static bool flat_f32(const SrcView& s, int64_t n) {
+    const bool flat = s.ne[2] * s.ne[3] == 1 || (s.nb[2] == s.ne[1] * s.nb[1] && (s.ne[3] == 1 || s.nb[3] == s.ne[2] * s.nb[2]));
+    return s.type == T_F32 && s.nb[0] == 4 && flat && s.ne[0] >= QK && ((reinterpret_cast<uintptr_t>(s.data) | (uintptr_t)s.nb[1]) & 15) == 0 &&
+           n + s.ne[0] < ((int64_t)1 << 31) && s.ne[1] * s.ne[2] * s.ne[3] * s.nb[1] < ((int64_t)1 << 40);
 }
 
 static RowAddr row_addr(const SrcView& s) {
@@ -377,9 +405,9 @@ hipError_t launch_quantize_mmq_i8(const SrcView& src, bool with_sum, int64_t s1,
     const int64_t nblocks = rows * (src.ne[0] / QK);
     if (nblocks == 0) return hipSuccess;
     if (s1 < src.ne[0] || s1 % 16 != 0) return hipErrorInvalidValue;
+    uint16_t* qq = reinterpret_cast<uint16_t*>(q);
     const dim3 grid((unsigned)((nblocks + 255) / 256));
     const RowAddr ra = row_addr(src);
-    uint16_t* qq = reinterpret_cast<uint16_t*>(q);
     if (with_sum)
         quantize_mmq_kernel<true, true><<<grid, 256, 0, st>>>(src.data, src.type, ra, src.ne[0], nblocks, dp, qq, d, s,
                                                               blocks_rcp(src, nblocks), s1);
@@ -393,6 +421,12 @@ hipError_t launch_convert_f16(const SrcView& src, uint16_t* dst, int64_t pitch, 
     if (pitch < src.ne[0]) return hipErrorInvalidValue;
     const int64_t n = pitch * src.ne[1] * src.ne[2] * src.ne[3];
     if (n == 0) return hipSuccess;
+    if (pitch == src.ne[0] && src.ne[0] % 8 == 0 && flat_f32(src, n / 8) && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+        const int64_t cpr = src.ne[0] / 8, nch = n / 8;
+        convert_f16_flat_kernel<<<(unsigned)((nch + 255) / 256), 256, 0, st>>>(src.data, src.nb[1], (int)cpr, (int)nch,
+                                                                               1.0 / (double)cpr, dst);
+        return hipGetLastError();
+    }
     const dim3 grid((unsigned)((n + 255) / 256));
     convert_f16_kernel<<<grid, 256, 0, st>>>(src.data, src.type, row_addr(src), src.ne[0], pitch, n, dst);
     return hipGetLastError();

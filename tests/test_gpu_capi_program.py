@@ -53,8 +53,6 @@ def test_buffer_api(mi, ctx):
             ctx._check(L.mi355_tensor_get(ctx.h, t, got.ctypes.data, 0, 28000))
             assert np.array_equal(got, ref), (off, n, val)
         # the bytes around the tensor keep the clear value
-        whole = mi.make_tensor(L.mi355_buffer_base(buf), 2, [1 << 20])  # u8-sized view via Q4_0? no: raw bytes below
-        del whole
         pre = mi.make_tensor(L.mi355_buffer_base(buf), mi.F32, [128])
         got = np.empty(512, dtype=np.uint8)
         ctx._check(L.mi355_tensor_get(ctx.h, pre, got.ctypes.data, 0, 512))

@@ -177,3 +177,37 @@ def test_prepared_layout_and_rejections(mi, ctx, orc, tname):
     fake = mi.make_tensor(qf.data_ptr(), mi.F16, [64, 4, 1, 1])
     fake.layout = mi.LAYOUT_INT8
     assert status(lambda: ctx.flash_attn_ext(fake, qt, qt, mi.from_torch(of, mi.F32, [64, 1, 4, 1]), 0.125)) == INVALID
+
+
+@pytest.mark.parametrize("route,tname", [("f16", "q8_0"), ("f16", "q4_1"), ("f16", "f16"), ("int8", "q8_0"),
+                                         ("int8", "q4_1")])
+@pytest.mark.parametrize("M,K", [(5184, 1024), (77, 96), (301, 4736)])
+def test_flat_and_strided_activations_bit_identical(mi, ctx, orc, route, tname, M, K):
+    """src1 rows at a 16-byte aligned pitch take the vector-load paths of the
+    activation conversions (quantize_mmq_kernel's float4 loads,
+    convert_f16_flat_kernel), rows at an odd pitch the element-wise ones; both
+    are ggml's from_float, so the products must be equal bit for bit (F16
+    weights have no int8 route)."""
+    t = orc.NAME_TYPE[tname]
+    N = 96
+    print(f"flat vs strided src1 {route} {tname} M={M} K={K}", flush=True)
+    w = orc.normal(N * K, seed=K + M, stream=1, std=0.02).reshape(N, K)
+    x = orc.normal(M * K, seed=K + M, stream=2).reshape(M, K)
+    wq = orc.quantize_weights(t, w) if t != orc.F16 else w.astype(np.float16).view(np.uint16)
+    s0 = mi.from_torch(dev(wq.view(np.uint8)), t, [K, N])
+    flat = dev(x)
+    wide = torch.zeros((M, K + 1), dtype=torch.float32, device="cuda")
+    wide[:, :K] = flat
+    outs = []
+    ctx.set_mmq_kernel(_kernel(mi, route))
+    try:
+        for src, nb1 in ((flat, 4 * K), (wide, 4 * (K + 1))):
+            dst = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+            s1 = mi.from_torch(src, mi.F32, [K, M], nb=[4, nb1, nb1 * M, nb1 * M])
+            ctx.mul_mat(s0, s1, mi.from_torch(dst, mi.F32, [N, M]))
+            ctx.synchronize()
+            outs.append(dst)
+    finally:
+        ctx.set_mmq_kernel(mi.MMQ_AUTO)
+    assert torch.isfinite(outs[0]).all()
+    assert torch.equal(outs[0], outs[1]), f"max diff {(outs[0] - outs[1]).abs().max().item():.3e}"
