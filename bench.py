@@ -16,7 +16,7 @@ value = int8 ops of the step (2*M*N*K per GEMM) / step time, in TOPS.
 Also reported: per-type TOPS and %% of the int8 dense MFMA peak, the
 dominant kernel's roofline (the fc1 Q8_0 MMQ kernel, timed with HIP events
 on its stream through the library's kernel-timing hook), and a CPU baseline
-(the oracle's ggml-cpu restatement of the same mul_mat, AVX2, on the host;
+(the oracle's ggml-cpu restatement of the same mul_mat, AVX2 or AVX512-VNNI, on the host;
 beside it the SAM3 ViT encoder per frame from one windowed and one global
 block of the oracle's block composition, extrapolated x28 / x4).
 
@@ -40,8 +40,12 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 M_TOK = 5184
 LINEARS = [("qkv", 3072, 1024), ("proj", 1024, 1024), ("fc1", 4736, 1024), ("fc2", 1024, 4736)]
 TYPES = ["q8_0", "q4_0"]
+CONFIG2_TYPES = ["q4_1", "f16"]  # config 2's other weight types, reported beside the step
 ALL_TYPES = ["q8_0", "q4_0", "q4_1", "f16"]
 
+
+# the oracle's dot-product paths (orc_isa_path): AVX2, or AVX2 with AVX512-VNNI for the quantized dots
+ISA_NAMES = {0: "scalar", 1: "avx2", 2: "avx512vnni"}
 
 PREWARM_S = 0.5  # seconds of back-to-back work before each timed section (--prewarm)
 
@@ -209,7 +213,8 @@ def cpu_encoder_baseline(orc, tname, reps, warmup):
     return {"ms_per_frame": round(frame * 1e3, 1), "windowed_block_ms": round(res["windowed"] * 1e3, 1),
             "global_block_ms": round(res["global"] * 1e3, 1), "cores": nth, "kind": "port",
             "sample": f"{tname} SAM3 ViT: one windowed and one global block (median of {reps} after {warmup} "
-                      f"warmups each), x28 + x4; {nth} threads of nproc={os.cpu_count()}, cpu={cpu_model()}"}
+                      f"warmups each), x28 + x4; {nth} threads of nproc={os.cpu_count()}, "
+                      f"isa={ISA_NAMES.get(orc.lib().orc_isa_path(), 'scalar')}, cpu={cpu_model()}"}
 
 
 def build_encoder(mi, orc, torch, dev, types, seed=0, ctx=None):
@@ -453,9 +458,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-encoder-reps", type=int, default=1,
+    ap.add_argument("--cpu-encoder-reps", type=int, default=3,
                     help="CPU encoder baseline: timed runs per block (median), 0 to skip")
-    ap.add_argument("--cpu-encoder-warmup", type=int, default=0, help="CPU encoder baseline: untimed runs per block")
+    ap.add_argument("--cpu-encoder-warmup", type=int, default=1, help="CPU encoder baseline: untimed runs per block")
     ap.add_argument("--no-encoder", action="store_true", help="skip the full ViT encoder ms/frame")
     ap.add_argument("--frames", type=int, default=3, help="timed encoder frames per weight type")
     ap.add_argument("--op", default=None,
@@ -579,7 +584,7 @@ def main():
     calls = []  # (tname, lname, N, K, s0 prepared, s1, d, s0 in the ggml layout)
     host_w = {}
     keep = []
-    types = TYPES
+    types = TYPES + CONFIG2_TYPES  # the step's types, then config 2's Q4_1 / F16 (timed per call only)
     if args.op:
         types = [args.op.split("/")[0]]
     for ti, tname in enumerate(types):
@@ -590,9 +595,10 @@ def main():
             host_w[(tname, lname)] = wq
             wd = torch.from_numpy(wq).to(dev)
             wt = mi.from_torch(wd, t, [K, N])
-            nbw = mi.weight_prepared_nbytes(wt)
+            nbw = mi.weight_prepared_nbytes(wt)  # 0 for F16 weights: those run as given
             wbuf = torch.empty(nbw + 256, dtype=torch.uint8, device=dev)
-            s0 = ctx.weight_prepare(wt, wbuf.data_ptr() + (-wbuf.data_ptr()) % 256, nbw)
+            s0 = ctx.weight_prepare(wt, wbuf.data_ptr() + (-wbuf.data_ptr()) % 256, nbw) if nbw else wt
+            wbuf = (wbuf, wd)
             xd = torch.from_numpy(xhost[K]).to(dev)  # this call's own activations
             dst = torch.empty((M_TOK, N), dtype=torch.float32, device=dev)
             s1 = mi.from_torch(xd, mi.F32, [K, M_TOK])
@@ -614,8 +620,10 @@ def main():
                           "kernel_us": {k: round(1e3 * v[1] / v[0], 2) for k, v in prof.items()}}), flush=True)
         ctx.close()
         return
-    ops_by_type = {tn: sum(2.0 * M_TOK * N * K for (_, N, K) in LINEARS) for tn in TYPES}
-    step_ops = sum(ops_by_type.values())
+    ops_by_type = {tn: sum(2.0 * M_TOK * N * K for (_, N, K) in LINEARS) for tn in TYPES + CONFIG2_TYPES}
+    step_ops = sum(ops_by_type[tn] for tn in TYPES)
+    extra_calls = [c for c in calls if c[0] in CONFIG2_TYPES]
+    calls = [c for c in calls if c[0] in TYPES]
 
     def step():
         for c in calls:
@@ -658,6 +666,25 @@ def main():
     log("bench: per-call kernel times, ggml-layout weights " +
         json.dumps({f"{a}/{b}": v for (a, b), v in raw_call_ms.items()}))
 
+    # config 2's other weight types over the same linear set: Q4_1 (prepared, int8 kernel) and F16
+    # (fp16 MFMA kernel), per-call kernel times after a pre-warm
+    cfg2 = {}
+    for tname in CONFIG2_TYPES:
+        tc = [c for c in extra_calls if c[0] == tname]
+        prewarm(lambda: [ctx.mul_mat(c[4], c[5], c[6]) for c in tc], torch)
+        ctx.profile(True)
+        per = {}
+        for c in tc:
+            for _ in range(5):
+                ctx.mul_mat(c[4], c[5], c[6])
+            prof = ctx.profile_collect()
+            per[c[1]] = {k: round(1e3 * v[1] / v[0], 2) for k, v in prof.items()}
+        ctx.profile(False)
+        tot_ms = sum(sum(v.values()) for v in per.values()) * 1e-3
+        cfg2[tname] = {"tops": round(ops_by_type[tname] / (tot_ms * 1e-3) / 1e12, 2), "kernel_us": per,
+                       "weights": "prepared" if tname != "f16" else "as given (F16)"}
+    log("bench: config 2 Q4_1 / F16 " + json.dumps(cfg2))
+
     type_tops, raw_tops = {}, {}
     for tname in TYPES:
         tot = sum(sum(per_call_ms[(tname, ln)].values()) for (ln, _, _) in LINEARS)
@@ -691,7 +718,7 @@ def main():
     neck_res = None
     if not args.no_encoder:
         log("bench: encoder weights")
-        del calls, keep
+        del calls, extra_calls, keep
         torch.cuda.empty_cache()
         hp, pre, blocks, keep = build_encoder(mi, orc, torch, dev, TYPES, ctx=None if args.raw_weights else ctx)
         encoder = {}
@@ -713,7 +740,7 @@ def main():
             del keep_n
 
     # ---- CPU baseline: the oracle's ggml-cpu restatement of the same fc1 Q8_0 mul_mat
-    # (from_float + vec_dot, AVX2 when the host has it), median of 5 after 2 warmups
+    # (from_float + vec_dot; AVX2, or AVX512-VNNI where the host has it), median of 5 after 2 warmups
     cpu = None
     if not args.no_cpu_baseline:
         log("bench: cpu baseline")
@@ -731,7 +758,7 @@ def main():
         cpu = {"value": round(cpu_tops, 4), "unit": "TOPS", "cores": nth, "kind": "port",
                "sample": f"fc1 Q8_0 mul_mat (quantize + block dots) 5184 x 4736 x 1024, median of 5 after 2 "
                          f"warmups: {med * 1e3:.1f} ms; {nth} threads (the host CPU share of one GPU) of "
-                         f"nproc={os.cpu_count()}, isa={'avx2' if orc.lib().orc_isa_path() == 1 else 'scalar'}, "
+                         f"nproc={os.cpu_count()}, isa={ISA_NAMES.get(orc.lib().orc_isa_path(), 'scalar')}, "
                          f"cpu={cpu_model()}"}
 
         if args.cpu_encoder_reps > 0 and not args.no_encoder:
@@ -756,8 +783,11 @@ def main():
         "config": {"workload": "SAM3 ViT block linear set (qkv, proj, fc1, fc2) at 5184 tokens, Q8_0 and Q4_0 weights",
                    "tokens": M_TOK, "linears": [f"{n}x{k}" for (_, n, k) in LINEARS], "weight_types": TYPES},
         "pct_int8_peak": round(100.0 * value / INT8_PEAK_TOPS, 2),
+        "weights": "prepared once at setup (mi355_weight_prepare, as a model load does); raw_layout_tops: "
+                   "the same calls on ggml-layout weights, repacked on every call",
         "type_tops": {k: round(v, 2) for k, v in type_tops.items()},
         "raw_layout_tops": {k: round(v, 2) for k, v in raw_tops.items()},
+        "config2_type_tops": cfg2,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "vit_encoder_1008": encoder,

@@ -58,10 +58,18 @@ typedef enum {
     MI355_ACT_REF = 1,
 } mi355_act_variant;
 
+/* Version of this interface: 2 added the layout field of mi355_tensor (the
+ * former padding word, which callers must now set to 0, e.g. by
+ * zero-initializing the struct) and prepared weights.  A binding compiled
+ * against one version checks mi355_abi_version() at load. */
+#define MI355_ABI_VERSION 2
+int mi355_abi_version(void);
+
 /* The layout fields of a ggml_tensor (ggml.h struct ggml_tensor: type, ne,
  * nb, data).  data is a device pointer.  layout is MI355_LAYOUT_GGML (0, the
  * bytes ggml defines for type/ne/nb) except for a weight prepared by
- * mi355_weight_prepare (MI355_LAYOUT_INT8). */
+ * mi355_weight_prepare (MI355_LAYOUT_INT8); any other value is rejected
+ * (MI355_STATUS_INVALID_ARG) by every entry point. */
 typedef enum {
     MI355_LAYOUT_GGML = 0,
     MI355_LAYOUT_INT8 = 1,
@@ -171,11 +179,16 @@ mi355_status mi355_weight_prepare(mi355_context* ctx, const mi355_tensor* w, voi
  * 4-byte-pitch weight copy) lives in a fixed device array of
  * MI355_NOALLOC_SCRATCH_BYTES per GPU, held from library load until the
  * process ends, instead of the context's workspace; the call allocates and
- * frees nothing and records no timing events.  Operands needing more scratch
- * than that (mi355_mul_mat_workspace_size) are rejected with
- * MI355_STATUS_UNSUPPORTED.  Every call on one GPU uses that GPU's one array,
- * so calls that overlap on a GPU (several streams, contexts or host threads)
- * race: serialize them. */
+ * frees nothing and records no timing events.  Operands whose plan on the
+ * context's current route (mi355_context_set_mmq_kernel) needs more scratch
+ * than that are rejected with MI355_STATUS_UNSUPPORTED; the most any route
+ * needs, mi355_mul_mat_workspace_size, bounds it from above.  Every call on
+ * one GPU uses that GPU's one array: calls through one context serialize on
+ * its stream, and a call through another context first makes its stream
+ * wait on an event the device's previous call recorded (each context creates
+ * its event when it is created).  Under stream capture no event is waited on
+ * or recorded: the caller orders the launches of captured graphs.  Host
+ * threads sharing one context must serialize their calls. */
 #define MI355_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 mi355_status mi355_mul_mat_noalloc(mi355_context* ctx, const mi355_tensor* src0, const mi355_tensor* src1,
                                    const mi355_tensor* dst);

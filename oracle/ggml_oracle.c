@@ -18,7 +18,8 @@
  *   block isums .......... brute-force integer dot over dequantized blocks
  *   vec_dot / mul_mat .... long-double brute force of ggml's block formula;
  *                           numpy float64 matmul of dequantized operands;
- *                           AVX2 path bit-identical to the scalar order
+ *                           AVX2 and AVX512-VNNI paths bit-identical to the
+ *                           scalar order
  *   soft_max ............. rows sum to 1; numpy/scipy softmax
  *   flash_attn_ext ....... long-double textbook attention; key-permutation
  *                           equivariance; strided V == contiguous V bit-exact
@@ -571,6 +572,58 @@ static float dot_q8_avx2(int type, int64_t nb, const void* vx, const void* vy) {
     return hsum8(a) + summs;
 }
 
+/* The same dot with AVX512-VNNI: ggml's mul_sum_us8_pairs_float takes _mm256_dpbusd_epi32
+ * when __AVX512VNNI__ and __AVX512VL__ are defined, which sums the four u8 x s8 products of
+ * each 32-bit lane into int32 exactly as maddubs + madd(ones) do for |q| <= 127 (no 16-bit
+ * saturation is reachable), so the eight lanes, their float conversion and the fmadd
+ * order are those of dot_q8_avx2 and the result is bit-identical. */
+__attribute__((target("avx2,fma,f16c,avx512f,avx512vl,avx512vnni")))
+static float dot_q8_vnni(int type, int64_t nb, const void* vx, const void* vy) {
+    __m256 acc = _mm256_setzero_ps();
+    float summs = 0.0f;
+    const __m256i zero = _mm256_setzero_si256();
+    for (int64_t b = 0; b < nb; ++b) {
+        __m256i qx, qy;
+        float dx, dy;
+        if (type == ORC_TYPE_Q8_0) {
+            const blk_q8_0* x = (const blk_q8_0*)vx + b;
+            qx = _mm256_loadu_si256((const __m256i*)x->qs);
+            dx = h2f(x->d);
+        } else {
+            const uint8_t* qs;
+            if (type == ORC_TYPE_Q4_0) {
+                const blk_q4_0* x = (const blk_q4_0*)vx + b;
+                qs = x->qs; dx = h2f(x->d);
+            } else {
+                const blk_q4_1* x = (const blk_q4_1*)vx + b;
+                qs = x->qs; dx = h2f(x->d);
+            }
+            const __m128i t = _mm_loadu_si128((const __m128i*)qs);
+            const __m256i both = _mm256_insertf128_si256(_mm256_castsi128_si256(t), _mm_srli_epi16(t, 4), 1);
+            qx = _mm256_and_si256(both, _mm256_set1_epi8(0x0f));
+            if (type == ORC_TYPE_Q4_0) qx = _mm256_sub_epi8(qx, _mm256_set1_epi8(8));
+        }
+        if (type == ORC_TYPE_Q4_1) {
+            const blk_q8_1* y = (const blk_q8_1*)vy + b;
+            qy = _mm256_loadu_si256((const __m256i*)y->qs);
+            dy = h2f(y->d);
+            const float t = h2f(((const blk_q4_1*)vx + b)->m) * h2f(y->s);
+            summs = summs + t;
+        } else {
+            const blk_q8_0* y = (const blk_q8_0*)vy + b;
+            qy = _mm256_loadu_si256((const __m256i*)y->qs);
+            dy = h2f(y->d);
+        }
+        const __m256i ax = _mm256_sign_epi8(qx, qx);
+        const __m256i sy = _mm256_sign_epi8(qy, qx);
+        const __m256i p32 = _mm256_dpbusd_epi32(zero, ax, sy);
+        acc = _mm256_fmadd_ps(_mm256_set1_ps(dx * dy), _mm256_cvtepi32_ps(p32), acc);
+    }
+    float a[8];
+    _mm256_storeu_ps(a, acc);
+    return hsum8(a) + summs;
+}
+
 __attribute__((target("avx2,fma,f16c")))
 static float dot_f16_avx2(int64_t n, const uint16_t* x, const uint16_t* y) {
     __m256 acc = _mm256_setzero_ps();
@@ -585,35 +638,42 @@ static float dot_f16_avx2(int64_t n, const uint16_t* x, const uint16_t* y) {
 }
 #endif
 
+/* 0 scalar, 1 AVX2 + FMA, 2 AVX2 + FMA with AVX512-VNNI/VL for the quantized dots (the
+ * F16 and F32 dots keep their AVX2 / scalar forms on path 2). */
 static int g_isa = -1;
-int orc_isa_path(void) {
-    if (g_isa < 0) {
+static int isa_detect(void) {
 #if defined(__x86_64__)
-        __builtin_cpu_init();
-        g_isa = (__builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma")) ? 1 : 0;
+    __builtin_cpu_init();
+    if (!(__builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma"))) return 0;
+    if (__builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512vl") &&
+        __builtin_cpu_supports("avx512vnni"))
+        return 2;
+    return 1;
 #else
-        g_isa = 0;
+    return 0;
 #endif
-    }
+}
+int orc_isa_path(void) {
+    if (g_isa < 0) g_isa = isa_detect();
     return g_isa;
 }
-/* path < 0 re-detects; 0 forces scalar; 1 forces AVX2 (only if supported). */
+/* path < 0 re-detects; otherwise the requested path, or the best supported one below it. */
 void orc_set_isa(int path) {
-    g_isa = -1;
-    const int have = orc_isa_path();
-    if (path >= 0) g_isa = (path == 1 && have != 1) ? 0 : path;
+    const int have = isa_detect();
+    g_isa = path < 0 ? have : (path < have ? path : have);
 }
 
 float orc_vec_dot(int type, int64_t n, const void* x, const void* y, int order) {
     switch (type) {
         case ORC_TYPE_Q8_0: case ORC_TYPE_Q4_0: case ORC_TYPE_Q4_1:
 #if defined(__x86_64__)
+            if (order == ORC_ORDER_X86 && orc_isa_path() == 2) return dot_q8_vnni(type, n / ORC_QK, x, y);
             if (order == ORC_ORDER_X86 && orc_isa_path() == 1) return dot_q8_avx2(type, n / ORC_QK, x, y);
 #endif
             return dot_q8_scalar(type, n / ORC_QK, x, y, order);
         case ORC_TYPE_F16:
 #if defined(__x86_64__)
-            if (order == ORC_ORDER_X86 && n % 8 == 0 && orc_isa_path() == 1)
+            if (order == ORC_ORDER_X86 && n % 8 == 0 && orc_isa_path() >= 1)
                 return dot_f16_avx2(n, (const uint16_t*)x, (const uint16_t*)y);
 #endif
             return dot_f16_scalar(n, (const uint16_t*)x, (const uint16_t*)y, order);

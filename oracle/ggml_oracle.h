@@ -160,7 +160,8 @@ void orc_apply_rope(float* x, const float* freqs, int64_t hd, int64_t n_tok, int
 void orc_win_part(const float* src, float* dst, int64_t C, int64_t W, int64_t H, int w);
 void orc_win_unpart(const float* src, float* dst, int64_t C, int64_t W, int64_t H, int w);
 
-/* Host ISA path used by the fast dot kernels: 0 scalar, 1 AVX2. */
+/* Host ISA path used by the fast dot kernels: 0 scalar, 1 AVX2, 2 AVX2 with AVX512-VNNI
+ * for the quantized dots (bit-identical to 1 and to the scalar x86 order). */
 int orc_isa_path(void);
 void orc_set_isa(int path);
 

@@ -123,6 +123,7 @@ def lib():
     P, I, F, SZ = C.c_void_p, C.c_int, C.c_float, C.c_size_t
     T = C.POINTER(Tensor)
     sig = {
+        "mi355_abi_version": (I, []),
         "mi355_context_create": (I, [I, P, C.POINTER(P)]),
         "mi355_context_free": (None, [P]),
         "mi355_synchronize": (I, [P]),

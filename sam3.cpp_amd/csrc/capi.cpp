@@ -135,6 +135,21 @@ bool mm_i8_eligible(const mi355_tensor* s0, const mi355_tensor* s1) {
            s1->ne[2] == 1 && s1->ne[3] == 1 && s0->ne[0] % 32 == 0;
 }
 
+// The MUL_MAT kernels address their operands with 32-bit buffer offsets below 2^30 bytes
+// (OOB8 / OOB mark lanes past the end): the int8 route's quants and scale dwords, the fp16
+// route's weight slice, fp16 activation slice and scales.
+constexpr int64_t kExtent = (int64_t)1 << 30;
+bool i8_extents_ok(const mi355_tensor* s0, const mi355_tensor* s1) {
+    const int64_t K = s0->ne[0], N = s0->ne[1], M = s1->ne[1], nst = mmq_scale_pitch(K) / 2;
+    return M * K < kExtent && N * K < kExtent && 4 * M * nst < kExtent && 4 * N * nst < kExtent;
+}
+bool f16_extents_ok(const mi355_tensor* s0, const mi355_tensor* s1) {
+    const int64_t K = s0->ne[0], N = s0->ne[1], M = s1->ne[1];
+    const int64_t s1h = f16_src1_direct(s1) ? s1->nb[1] / 2 : (s0->type == T_F16 ? (K + 7) & ~(int64_t)7 : K);
+    return (N - 1) * s0->nb[1] + row_size(s0->type, K) < kExtent && ((M - 1) * s1h + K) * 2 < kExtent &&
+           2 * M * mmq_scale_pitch(K) < kExtent;
+}
+
 int device_cus(int device) {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
@@ -152,7 +167,7 @@ MmPlan mm_plan(const mi355_tensor* s0, const mi355_tensor* s1, int cus, bool spl
     const int64_t K = s1->ne[0], M = s1->ne[1], Z = s1->ne[2] * s1->ne[3];
     if (split) pl.ks = mmq_ksplit(s0->type, M, s0->ne[1], K, Z, cus);
     if (pl.ks > 1) pl.part = align_up((size_t)pl.ks * (size_t)M * (size_t)s0->ne[1] * 4);
-    if (i8 && mm_i8_eligible(s0, s1)) {
+    if (i8 && mm_i8_eligible(s0, s1) && i8_extents_ok(s0, s1)) {
         pl.i8 = true;
         pl.q = align_up((size_t)(M * K));
         pl.d = align_up((size_t)(M * mmq_scale_pitch(K)) * 4);  // dl and dh dwords
@@ -225,6 +240,9 @@ mi355_status check_mul_mat(mi355_context* ctx, const mi355_tensor* s0, const mi3
     const int64_t lim = (int64_t)1 << 30;
     if (K >= lim || s0->ne[1] >= lim || s1->ne[1] >= lim || s1->ne[2] * s1->ne[3] > 65535)
         return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat: dimensions beyond kernel limits");
+    if (prep ? !i8_extents_ok(s0, s1)
+             : t0 != T_F32 && !(mm_i8_eligible(s0, s1) && i8_extents_ok(s0, s1)) && !f16_extents_ok(s0, s1))
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat: operands beyond the kernels' 1 GiB buffer extents");
     if (t0 == T_F32) {
         if (s1->nb[0] != 4 || ((reinterpret_cast<uintptr_t>(s0->data) | (uintptr_t)s0->nb[1] | (uintptr_t)s0->nb[2] |
                                 (uintptr_t)s0->nb[3] | reinterpret_cast<uintptr_t>(s1->data) | (uintptr_t)s1->nb[1] |
@@ -620,6 +638,8 @@ const char* mi355_last_error(const mi355_context* ctx) {
     return ctx ? ctx->last_error.c_str() : g_noctx_error.c_str();
 }
 
+int mi355_abi_version(void) { return MI355_ABI_VERSION; }
+
 mi355_status mi355_context_create(int device, void* stream, mi355_context** out) {
     if (!out) return fail(nullptr, MI355_STATUS_INVALID_ARG, "context_create: out is null");
     *out = nullptr;
@@ -646,6 +666,7 @@ void mi355_context_free(mi355_context* ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
+    noalloc_release(ctx);
     mi355_profile_reset(ctx);
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->enc) (void)hipFree(ctx->enc);
@@ -750,7 +771,7 @@ mi355_status mi355_mul_mat_noalloc(mi355_context* ctx, const mi355_tensor* s0, c
         return fail(ctx, MI355_STATUS_UNSUPPORTED,
                     "mul_mat_noalloc: these operands need %zu bytes of scratch, the static scratch holds %zu",
                     pl.total(), (size_t)MI355_NOALLOC_SCRATCH_BYTES);
-    return mul_mat_run(ctx, s0, s1, d, pl, static_cast<char*>(ctx->scratch), false);
+    return noalloc_run(ctx, [&] { return mul_mat_run(ctx, s0, s1, d, pl, static_cast<char*>(ctx->scratch), false); });
 }
 
 mi355_status mi355_mul_mat_block_dots(mi355_context* ctx, const mi355_tensor* s0, const mi355_tensor* s1,

@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <functional>
 #include <map>
 #include <string>
 #include <vector>
@@ -25,10 +26,12 @@ struct mi355_context {
     // context's device (null if it could not be resolved: scratch_error says why)
     void* scratch = nullptr;
     std::string scratch_error;
+    hipEvent_t scratch_done = nullptr;  // recorded after this context's last no-allocation call
     std::string last_error;
     // encoder runners: producer passes write the next MUL_MAT's operand
     bool fuse = true;
-    // MUL_MATs with K <= 128 at large M take the skinny kernel
+    // fp16-route MUL_MATs (F16 weights, ggml-layout Q4_1 under MI355_MMQ_AUTO, MI355_MMQ_F16)
+    // with K <= 128 at large M take the skinny kernel; the int8 route has none
     bool skinny = true;
     // kernel of 2-D MUL_MATs with block-quantized weights (MI355_MMQ_*)
     int mmq_kernel = MI355_MMQ_AUTO;
@@ -87,6 +90,13 @@ mi355_status mul_mat_epi(mi355_context* ctx, const mi355_tensor* s0, const ActF1
 // mi355_mul_mat_noalloc on ctx's device (current) into ctx->scratch; the
 // lookup runs once per device.
 mi355_status noalloc_scratch_init(mi355_context* ctx);
+// Runs work (launches on ctx's stream that use the static scratch) ordered after the device's
+// previous no-allocation call from another context, and records ctx's scratch event after it;
+// not under stream capture.  The launches are asynchronous: the host lock is held only while
+// they are issued.
+mi355_status noalloc_run(mi355_context* ctx, const std::function<mi355_status()>& work);
+// The context's scratch event, before the context is freed (its stream synchronized).
+void noalloc_release(mi355_context* ctx);
 
 // Brackets one launch with events when timing is enabled.
 struct Timed {

@@ -15,6 +15,14 @@ def test_exports_every_header_symbol(mi):
     assert not missing, missing
 
 
+def test_abi_version(mi):
+    """The header's MI355_ABI_VERSION is what the library reports."""
+    import re
+    with open(mi.HEADER) as f:
+        want = int(re.search(r"#define MI355_ABI_VERSION (\d+)", f.read()).group(1))
+    assert mi.lib().mi355_abi_version() == want == 2
+
+
 def test_status_strings(mi):
     L = mi.lib()
     assert b"success" in L.mi355_status_to_string(0)
@@ -159,7 +167,8 @@ def test_every_entry_point_rejects_null_arguments(mi):
         # calls that create or query state without a context (or whose null arguments are valid)
         # are checked by their own tests: they may legitimately succeed
         skip = {{"mi355_context_create", "mi355_status_to_string", "mi355_last_error",
-                 "mi355_model_file_last_error", "mi355_hiera_n_blocks", "mi355_buffer_alignment"}}
+                 "mi355_model_file_last_error", "mi355_hiera_n_blocks", "mi355_buffer_alignment",
+                 "mi355_abi_version"}}
         bad = []
         for name in sorted(mi.header_symbols()):
             if name in skip:
@@ -298,3 +307,30 @@ def test_capi_program_without_gpu_fails_cleanly(mi):
         assert "capi_check ok" in r.stdout
     else:
         assert r.returncode == 2 and "mi355_context_create" in r.stderr, (r.returncode, r.stdout, r.stderr)
+
+
+def test_supports_mul_mat_buffer_extents(mi):
+    """The kernels address operands with 32-bit buffer offsets below 2^30 bytes: the
+    supports query (host-only, dummy pointers) accepts the largest activation the
+    int8 route holds (M * K just below 2^30 one-byte quants) and rejects one row
+    more, for ggml-layout Q8_0 weights (whose fp16 route would need twice the
+    bytes) and for a prepared weight; an F16 weight's fp16 route has half the room."""
+    L = mi.lib()
+    K, N = 4096, 64
+    m_max = ((1 << 30) - 1) // K  # M * K < 2^30
+    for t0, layout in ((8, 0), (8, 1), (2, 1)):
+        for M, want in ((m_max, 1), (m_max + 1, 0)):
+            s0, s1, d = mm(mi, t0=t0, K=K, N=N, M=M)
+            if layout:
+                s0.layout = mi.LAYOUT_INT8
+                s0.nb[1] = K
+                s0.nb[2] = s0.nb[3] = K * N
+            assert L.mi355_supports_mul_mat(C.byref(s0), C.byref(s1), C.byref(d)) == want, (t0, layout, M)
+    # F16 weights: ((M - 1) * K + K) * 2 < 2^30
+    m_f16 = ((1 << 29) - 1) // K
+    for M, want in ((m_f16, 1), (m_f16 + 1, 0)):
+        s0, s1, d = mm(mi, t0=1, K=K, N=N, M=M)
+        assert L.mi355_supports_mul_mat(C.byref(s0), C.byref(s1), C.byref(d)) == want, M
+    s0, s1, d = mm(mi, t0=8, K=K, N=N, M=m_max + 1)
+    assert status(mi, s0, s1, d) == -3
+    assert b"extents" in L.mi355_last_error(None)

@@ -257,8 +257,8 @@ def test_block_isums_bruteforce(orc, t):
 @pytest.mark.parametrize("t", ["q8_0", "q4_0", "q4_1", "f16"])
 def test_vec_dot_orders_and_isa(orc, t):
     """Both summation orders stay within 1e-6 of the absolute-term sum of the
-    long-double block formula, and the AVX2 kernels are bit-identical to the
-    scalar x86-order restatement."""
+    long-double block formula, and the AVX2 and AVX512-VNNI kernels (those the
+    host has) are bit-identical to the scalar x86-order restatement."""
     t = orc.NAME_TYPE[t]
     K = 4736
     w = orc.normal(8 * K, seed=2, stream=1, std=0.02).reshape(8, K)
@@ -266,7 +266,8 @@ def test_vec_dot_orders_and_isa(orc, t):
     wq = orc.quantize_weights(t, w)
     xq = orc.from_float(orc.VEC_DOT_TYPE[t], x)
     L = orc.lib()
-    have_avx2 = L.orc_isa_path() == 1
+    L.orc_set_isa(-1)
+    best = L.orc_isa_path()
     for i in range(8):
         for j in range(8):
             pw, px = wq[i].ctypes.data, xq[j].ctypes.data
@@ -278,6 +279,39 @@ def test_vec_dot_orders_and_isa(orc, t):
             L.orc_set_isa(-1)
             assert abs(s_x86 - ex) <= 1e-6 * ab
             assert abs(s_seq - ex) <= 1e-6 * ab
-            if have_avx2:
-                s_avx = L.orc_vec_dot(t, K, pw, px, orc.ORDER_X86)
-                assert np.float32(s_avx).view(np.uint32) == np.float32(s_x86).view(np.uint32)
+            for path in range(1, best + 1):  # AVX2, then AVX512-VNNI where the host has them
+                L.orc_set_isa(path)
+                s_simd = L.orc_vec_dot(t, K, pw, px, orc.ORDER_X86)
+                L.orc_set_isa(-1)
+                assert np.float32(s_simd).view(np.uint32) == np.float32(s_x86).view(np.uint32), path
+
+
+@pytest.mark.parametrize("t", ["q8_0", "q4_0", "q4_1"])
+def test_vec_dot_simd_extremes(orc, t):
+    """The SIMD dots on saturating operands: every quant at +-127 (Q8_0 both sides,
+    the activation side for Q4) and the Q4 nibble extremes, random scales; each ISA
+    path the host has returns the scalar x86-order bits."""
+    t = orc.NAME_TYPE[t]
+    K = 1024
+    rng = np.random.default_rng(17)
+    vt = orc.VEC_DOT_TYPE[t]
+    L = orc.lib()
+    L.orc_set_isa(-1)
+    best = L.orc_isa_path()
+    for trial in range(12):
+        signs_w = rng.choice([-1.0, 1.0], size=K).astype(np.float32)
+        signs_x = rng.choice([-1.0, 1.0], size=K).astype(np.float32)
+        scale = np.float32(10.0 ** rng.uniform(-3, 2))
+        w = (signs_w * scale).reshape(1, K)  # every block at +-amax: quants +-127 / nibble ends
+        x = (signs_x * np.float32(rng.uniform(0.5, 4.0))).reshape(1, K)
+        if trial % 3 == 1:
+            x[0, ::7] = 0.0
+        wq, xq = orc.quantize_weights(t, w), orc.from_float(vt, x)
+        pw, px = wq[0].ctypes.data, xq[0].ctypes.data
+        L.orc_set_isa(0)
+        ref = L.orc_vec_dot(t, K, pw, px, orc.ORDER_X86)
+        for path in range(1, best + 1):
+            L.orc_set_isa(path)
+            got = L.orc_vec_dot(t, K, pw, px, orc.ORDER_X86)
+            assert np.float32(got).view(np.uint32) == np.float32(ref).view(np.uint32), (trial, path)
+        L.orc_set_isa(-1)

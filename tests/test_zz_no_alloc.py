@@ -57,3 +57,43 @@ def test_mul_mat_noalloc_rejects_oversized(mi, ctx, orc):
     assert ei.value.status == -3 and "scratch" in str(ei.value)
     ctx.synchronize()
     assert not out.any()
+
+
+def test_mul_mat_noalloc_ordered_across_streams(mi, orc):
+    """Two contexts on two streams share the GPU's one scratch array: each call
+    waits on the event the other context's previous call recorded, so calls
+    issued back to back with no host synchronization in between still give
+    mi355_mul_mat's results (the first, a split-K GEMM, is the longest, so an
+    unordered second call would overwrite its operand while it runs)."""
+    s_a, s_b = torch.cuda.Stream(), torch.cuda.Stream()  # default priority
+    ca, cb = mi.Context(0, s_a.cuda_stream), mi.Context(0, s_b.cuda_stream)
+    try:
+        shapes = [(1024, 1024, 4736), (2048, 512, 1024), (1024, 1024, 4736), (300, 200, 1024)]
+        jobs = []
+        for i, (M, N, K) in enumerate(shapes):
+            wq = _weights(orc, orc.Q8_0, N, K, 320 + i)
+            x = orc.normal(M * K, 321 + i, 2).reshape(M, K)
+            wd, xd = dev(wq.view(np.uint8)), dev(x)
+            s0, s1 = mi.from_torch(wd, mi.Q8_0, [K, N]), mi.from_torch(xd, mi.F32, [K, M])
+            ref = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+            got = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+            jobs.append((s0, s1, ref, got, wd, xd))
+        ctx_ref = mi.Context(0)
+        try:
+            for s0, s1, ref, got, _, _ in jobs:
+                ctx_ref.mul_mat(s0, s1, mi.from_torch(ref, mi.F32, [ref.shape[1], ref.shape[0]]))
+            ctx_ref.synchronize()
+        finally:
+            ctx_ref.close()
+        torch.cuda.synchronize()
+        for i, (s0, s1, ref, got, _, _) in enumerate(jobs):
+            print(f"noalloc across streams: call {i} on context {'ab'[i % 2]}", flush=True)
+            (ca if i % 2 == 0 else cb).mul_mat_noalloc(s0, s1, mi.from_torch(got, mi.F32, [got.shape[1], got.shape[0]]))
+        ca.synchronize()
+        cb.synchronize()
+        for i, (_, _, ref, got, _, _) in enumerate(jobs):
+            assert torch.isfinite(ref).all()
+            assert torch.equal(got, ref), f"call {i}: max diff {(got - ref).abs().max().item():.3e}"
+    finally:
+        ca.close()
+        cb.close()
