@@ -65,39 +65,67 @@ __device__ __forceinline__ u32x4 load8_h(const char* p) {
     }
 }
 
-// value of lane l ^ 32 (the other half of the wavefront holds the same query), by v_permlane32_swap
-__device__ __forceinline__ float partner32(float x) { return lane_swap_f<32>(x); }
-__device__ __forceinline__ float xmax32(float x) { return fmaxf(x, partner32(x)); }
+// max / sum over lanes l and l ^ 32 (the two halves of the wavefront hold the same
+// queries): v_permlane32_swap of x with itself leaves x_l and x_(l^32) in its two
+// results, in an order that depends on the half, and both operations are commutative
+__device__ __forceinline__ float xmax32(float x) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    return fmaxf(__int_as_float((int)p[0]), __int_as_float((int)p[1]));
+}
 // Workgroup barrier for LDS hazards only: waits for this wavefront's LDS accesses,
 // not for its global loads still in flight (__syncthreads() also waits for those).
 // The "memory" clobber keeps the compiler from moving LDS accesses across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-__device__ __forceinline__ float xsum32(float x) { return x + partner32(x); }
+__device__ __forceinline__ float xsum32(float x) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    return __int_as_float((int)p[0]) + __int_as_float((int)p[1]);
+}
 
 // K row slot of 16-byte chunk c in row r of an unpadded fp16 K tile (DMA staging):
 // the 32-row fragment reads of one chunk then fall in distinct bank quads
 template <int D>
 __device__ __forceinline__ int kswz(int r) { return D == 64 ? ((r & 7) ^ ((r >> 3) & 1)) : (r & 15); }
+// V row slot of 16-byte chunk c in row r of an unpadded fp16 V tile (DMA staging): slot
+// c ^ vswz(r), vswz a permutation of 0..7 over any 8 aligned rows whose first four values
+// also reach both halves of the slots, so the transposing reads of 4 or 8 consecutive rows
+// spread over all banks
+__device__ __forceinline__ int vswz(int r) { return ((r & 1) << 2) | ((r >> 1) & 3); }
+
+// 4 fp16 of LDS by the transposing read of gfx950 (ds_read_b64_tr_b16): within each group
+// of 16 lanes, lane i receives element i % 4 of the 8 bytes addressed by lanes i / 4,
+// 4 + i / 4, 8 + i / 4 and 12 + i / 4 of its group, in that order
+__device__ __forceinline__ uint2 lds_read_tr16(const void* a) {
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(a));
+    return __builtin_bit_cast(uint2, r);
+}
 
 // NW wavefronts of 32 queries per workgroup (4; 1 or 2 for small windows) and NBUF K/V tile
 // buffers (2; 1 when the launcher guarantees a single key tile): a window of at most 64
 // keys and 32 or 64 queries then runs in a workgroup of its own size with half the LDS, so
 // several times more windows are in flight; the arithmetic per query is the same.
+// KDMA: fp16 K and V with 16-byte rows reach LDS by DMA (buffer_load ... lds) and the loop
+// is software-pipelined; otherwise they pass through registers.
 template <int D, bool QF32, bool KVF32, bool KDMA, int NW = 4, int NBUF = 2>
 __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void fattn_kernel(const FaArgs p) {
-    static_assert(!KDMA || (!KVF32 && (D == 64 || D == 128)), "K DMA staging: fp16 K, D = 64 or 128");
+    static_assert(!KDMA || (!KVF32 && (D == 64 || D == 128)), "K/V DMA staging: fp16 K and V, D = 64 or 128");
     static_assert((NW == 4 && NBUF == 2) || (!KDMA && NBUF == 1 && (NW == 1 || NW == 2)), "workgroup shape");
     constexpr int NT = 64 * NW, BQ = 32 * NW;  // threads and queries per workgroup
     constexpr int KS = KDMA ? D : D + 8;  // K tile row stride (halves)
     constexpr int VS = FA_BKV + 4;  // V^T tile row stride (halves): 34 dwords, so the 8-byte reads of 32 rows hit distinct bank pairs
+    constexpr int VTILE = KDMA ? FA_BKV * D : D * VS;  // V tile (halves): rows of keys (DMA) or of V^T
     constexpr int NC = D / 16;      // MFMA k-chunks of a score
     constexpr int NDB = D / 32;     // 32-row blocks of O^T
     constexpr int C8 = D / 8;       // 8-element chunks per key row
     constexpr int LPT = FA_BKV * C8 / NT;  // chunks per thread per tile (K and V each)
     static_assert(FA_BKV * C8 % NT == 0, "tile split");
-    // two K / V^T buffers: tile t + 1 is stored while tile t is computed
+    // two K / V buffers: tile t + 1 is stored while tile t is computed
     __shared__ __attribute__((aligned(16))) _Float16 sK[NBUF][FA_BKV * KS];
-    __shared__ __attribute__((aligned(16))) _Float16 sV[NBUF][D * VS];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[NBUF][VTILE];
+    // the pipelined loop (K DMA) needs two tiles of scores in registers and keeps each
+    // lane's Q fragment in LDS instead: slot (w, c, lane), written and read by that lane only
+    constexpr bool QLDS = KDMA;
+    __shared__ __attribute__((aligned(16))) u32x4 sQ[QLDS ? NW * NC * 64 : 1];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -128,26 +156,25 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void fattn_kernel(const F
             u32x4 r = {0, 0, 0, 0};
             if (qi < p.nq) r = load8_h<QF32>(qrow + (16 * c + 8 * g) * (QF32 ? 4 : 2));
             if (p.negq) r ^= 0x80008000u;
-            qf[c] = __builtin_bit_cast(v8h, r);
+            if (QLDS) sQ[(w * NC + c) * 64 + lane] = r;
+            else qf[c] = __builtin_bit_cast(v8h, r);
         }
     }
 
-    // global -> register staging of one K/V tile.  K chunk j of thread t: key (t + 256j) / C8,
-    // column (t + 256j) % C8 (a key row's chunks on consecutive lanes).  V, when C8 % 8 == 0:
-    // thread t takes keys 2q, 2q + 1 (q = (t + 256i) % 32) of column chunk (t + 256i) / 32, so
-    // each V^T row gets the pair as one 32-bit write; otherwise V chunk j is key (t + 256j) % 64,
-    // column (t + 256j) / 64, written as 16-bit halves.
+    // global -> register staging of one K/V tile (the non-DMA path).  K chunk j of thread t:
+    // key (t + 256j) / C8, column (t + 256j) % C8 (a key row's chunks on consecutive lanes).
+    // V, when C8 % 8 == 0: thread t takes keys 2q, 2q + 1 (q = (t + 256i) % 32) of column
+    // chunk (t + 256i) / 32, so each V^T row gets the pair as one 32-bit write; otherwise V
+    // chunk j is key (t + 256j) % 64, column (t + 256j) / 64, written as 16-bit halves.
     constexpr bool VPAIR = C8 % 8 == 0;
-    u32x4 kreg[LPT], vreg[LPT];
+    u32x4 kreg[KDMA ? 1 : LPT], vreg[KDMA ? 1 : LPT];
     auto load_tile = [&](int kv0) {
 #pragma unroll
-        for (int j = 0; j < LPT; ++j) {
+        for (int j = 0; j < (KDMA ? 0 : LPT); ++j) {
             const int id = tid + NT * j;
             const int kk = id / C8, kc = id % C8;
-            if (!KDMA) {
-                kreg[j] = u32x4{0, 0, 0, 0};
-                if (kv0 + kk < nkv) kreg[j] = load8_h<KVF32>(kb + (int64_t)(kv0 + kk) * p.k_nb1 + kc * 8 * KES);
-            }
+            kreg[j] = u32x4{0, 0, 0, 0};
+            if (kv0 + kk < nkv) kreg[j] = load8_h<KVF32>(kb + (int64_t)(kv0 + kk) * p.k_nb1 + kc * 8 * KES);
             int vk, vc;
             if (VPAIR) {
                 const int pid = tid + NT * (j >> 1);
@@ -157,46 +184,19 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void fattn_kernel(const F
                 vk = id % FA_BKV;
                 vc = id / FA_BKV;
             }
-            if (KDMA) {  // exactly LPT loads per tile (the K DMA wait counts them): rows clamped,
-                         // keys past nkv zeroed by store_tile
-                vreg[j] = load8_h<false>(vb + (int64_t)min(kv0 + vk, nkv - 1) * p.v_nb1 + vc * 16);
-            } else {
-                vreg[j] = u32x4{0, 0, 0, 0};
-                if (kv0 + vk < nkv) vreg[j] = load8_h<KVF32>(vb + (int64_t)(kv0 + vk) * p.v_nb1 + vc * 8 * KES);
-            }
+            vreg[j] = u32x4{0, 0, 0, 0};
+            if (kv0 + vk < nkv) vreg[j] = load8_h<KVF32>(vb + (int64_t)(kv0 + vk) * p.v_nb1 + vc * 8 * KES);
         }
     };
-    // K tile by LDS DMA (buffer_load ... lds): wavefront w fills bytes [1024 (w KDI + j), +1024)
-    // of the tile with instruction j, lane i writing 16 bytes at + 16 i, i.e. slot s of row r;
-    // it loads the chunk s ^ kswz(r) of key kv0 + r.  Keys past nkv lie past the end of the
-    // buffer resource and read as zero.
-    constexpr int KDI = KDMA ? FA_BKV * D * 2 / 1024 / (NT / 64) : 1;
-    const v4i krsrc = make_rsrc(kb, (int64_t)nkv * p.k_nb1);
-    auto dma_k = [&](int kv0, int buf) {
-#pragma unroll
-        for (int j = 0; j < KDI; ++j) {
-            const int base = (w * KDI + j) << 10, byte = base + 16 * lane;
-            const int r = byte / (2 * D), s = (byte % (2 * D)) / 16;
-            dma_b128(krsrc, reinterpret_cast<const char*>(sK[buf]) + base,
-                     (kv0 + r) * (int)p.k_nb1 + 16 * (s ^ kswz<D>(r)));
-        }
-    };
-    auto store_tile = [&](int buf, int kv0) {
-        if (KDMA) {
-#pragma unroll
-            for (int j = 0; j < LPT; ++j) {
-                const int id = tid + NT * j, pid = tid + NT * (j >> 1);
-                const int vk = VPAIR ? 2 * (pid % 32) + (j & 1) : id % FA_BKV;
-                if (kv0 + vk >= nkv) vreg[j] = u32x4{0, 0, 0, 0};
-            }
-        }
+    auto store_tile = [&](int buf) {
 #pragma unroll
         for (int j = 0; j < (KDMA ? 0 : LPT); ++j) {
             const int id = tid + NT * j;
             const int kk = id / C8, kc = id % C8;
             *reinterpret_cast<u32x4*>(&sK[buf][kk * KS + kc * 8]) = kreg[j];
         }
-        if (VPAIR) {
+        if (KDMA) {
+        } else if (VPAIR) {
 #pragma unroll
             for (int j = 0; j < LPT; j += 2) {
                 const int pid = tid + NT * (j >> 1);
@@ -222,6 +222,31 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void fattn_kernel(const F
             }
         }
     };
+    // K and V tiles by LDS DMA (buffer_load ... lds): wavefront w fills bytes
+    // [1024 (w KDI + j), +1024) of a tile with instruction j, lane i writing 16 bytes at
+    // + 16 i, i.e. slot s of row r; it loads chunk s ^ kswz(r) (K) or s ^ vswz(r) (V) of key
+    // kv0 + r.  Keys past nkv lie past the end of the buffer resource and read as zero.
+    constexpr int KDI = KDMA ? FA_BKV * D * 2 / 1024 / (NT / 64) : 1;
+    const v4i krsrc = make_rsrc(kb, (int64_t)nkv * p.k_nb1);
+    const v4i vrsrc = make_rsrc(vb, (int64_t)nkv * p.v_nb1);
+    auto dma_k = [&](int kv0, int buf) {
+#pragma unroll
+        for (int j = 0; j < KDI; ++j) {
+            const int base = (w * KDI + j) << 10, byte = base + 16 * lane;
+            const int r = byte / (2 * D), s = (byte % (2 * D)) / 16;
+            dma_b128(krsrc, reinterpret_cast<const char*>(sK[buf]) + base,
+                     (kv0 + r) * (int)p.k_nb1 + 16 * (s ^ kswz<D>(r)));
+        }
+    };
+    auto dma_v = [&](int kv0, int buf) {
+#pragma unroll
+        for (int j = 0; j < KDI; ++j) {
+            const int base = (w * KDI + j) << 10, byte = base + 16 * lane;
+            const int r = byte / (2 * D), s = (byte % (2 * D)) / 16;
+            dma_b128(vrsrc, reinterpret_cast<const char*>(sV[buf]) + base,
+                     (kv0 + r) * (int)p.v_nb1 + 16 * (s ^ vswz(r)));
+        }
+    };
 
     v16f O[NDB];
 #pragma unroll
@@ -232,95 +257,114 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void fattn_kernel(const F
     float m_run = -__builtin_inff(), l_run = 0.0f;
     const float c = p.c;
 
-    // One LDS-only barrier per tile: it publishes tile t (stored at the end of tile
-    // t - 1) and frees the other buffer (read by tile t - 1).  After tile t's compute,
-    // tile t + 1 goes from the registers (loaded during tile t) into that buffer and
-    // tile t + 2's loads are issued, so each load has a whole tile to land.
-    const int ntile = (nkv + FA_BKV - 1) / FA_BKV;
-    if (NBUF == 1 && ntile > 1) return;  // one buffer holds one tile (the launcher's condition)
-    if (KDMA) dma_k(0, 0);
-    load_tile(0);
-    store_tile(0, 0);
-    if (ntile > 1) load_tile(FA_BKV);
-    for (int t = 0; t < ntile; ++t) {
-        const int kv0 = t * FA_BKV, cb = NBUF == 1 ? 0 : (t & 1);
-        if (KDMA) {  // tile t's K DMA precedes tile t + 1's LPT V loads (when issued)
-            if (t + 1 < ntile) wait_vmcnt<LPT>();
-            else wait_vmcnt<0>();
-        }
-        lds_barrier();
-        if (KDMA && t + 1 < ntile) dma_k(kv0 + FA_BKV, cb ^ 1);  // buffer cb ^ 1 was freed by the barrier
-
-        // S^T for the two 32-key halves
-        v16f S[2];
+    // S^T of one key tile (K in buffer kbuf) for its two 32-key halves
+    auto score = [&](int kbuf, v16f* S) {
+        S[0] = zf;
+        S[1] = zf;
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-            S[kh] = zf;
+        for (int cc = 0; cc < NC; ++cc) {
+            const v8h bq = QLDS ? __builtin_bit_cast(v8h, sQ[(w * NC + cc) * 64 + lane]) : qf[cc];
 #pragma unroll
-            for (int cc = 0; cc < NC; ++cc) {
+            for (int kh = 0; kh < 2; ++kh) {
                 const int r = 32 * kh + lr, slot = KDMA ? (2 * cc + g) ^ kswz<D>(r) : 2 * cc + g;
-                const v8h a = *reinterpret_cast<const v8h*>(&sK[cb][r * KS + 8 * slot]);
-                S[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[cc], S[kh], 0, 0, 0);
+                const v8h a = *reinterpret_cast<const v8h*>(&sK[kbuf][r * KS + 8 * slot]);
+                S[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bq, S[kh], 0, 0, 0);
             }
         }
-        if (kv0 + FA_BKV > nkv) {  // keys past the end take no weight
+    };
+    // keys kv0 + 64 > nkv of the tile take no weight
+    auto mask = [&](v16f* S, int kv0) {
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key = kv0 + 32 * kh + 8 * (i >> 2) + 4 * g + (i & 3);
+                if (key >= nkv) S[kh][i] = -__builtin_inff();
+            }
+    };
+    // Online softmax of one tile's scores into the fp16 probability pairs P, with the
+    // running max, the row sum and (when the max moved) O updated.
+    // Online softmax of one tile's scores into the fp16 probability pairs P, with the
+    // running max, the lane's part of the row sum and (when the max moved) O updated.
+    // The probabilities are first taken against the running max as it stands; only when
+    // some lane's sum of them exceeds 2^12 (or is not finite: the first tile, whose
+    // running max is -inf) does the wavefront find the tile's max and take them again
+    // against the raised max, rescaling O and the sum.  Every probability is at most its
+    // lane's sum, so P stays below 2^12 (fp16), and most tiles skip the max altogether.
+    // The two lanes of a query pair compute the same max, so they agree on the reference.
+    auto softmax = [&](const v16f* S, uint32_t (*P)[8]) {
+        const h2v ones = {(_Float16)1.0f, (_Float16)1.0f};
+        // probabilities rounded to fp16 in pairs (the PV operand); the row sum adds the same
+        // rounded values (one dot2 per pair), so numerator and denominator agree
+        auto probs = [&](float m) {
+            float ls = 0.0f;
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int key = kv0 + 32 * kh + 8 * (i >> 2) + 4 * g + (i & 3);
-                    if (key >= nkv) S[kh][i] = -__builtin_inff();
+                for (int i = 0; i < 16; i += 2) {
+                    const v2f pp = {__builtin_amdgcn_exp2f(__builtin_fmaf(S[kh][i], c, -m)),
+                                    __builtin_amdgcn_exp2f(__builtin_fmaf(S[kh][i + 1], c, -m))};
+                    const h2v ph = __builtin_convertvector(pp, h2v);
+                    ls = __builtin_amdgcn_fdot2(ph, ones, ls, false);
+                    P[kh][i >> 1] = __builtin_bit_cast(uint32_t, ph);
                 }
-        }
-        float mx = S[0][0];
+            return ls;
+        };
+        float ls = probs(m_run);
+        if (__builtin_amdgcn_ballot_w64(!(ls <= 4096.0f))) {
+            // four independent max chains, then the pair of lanes holding the same query
+            float m4[4];
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, S[kh][i]);
-        mx = xmax32(mx);
-        // the running max moves only when the tile's max exceeds it by more than 8 (in
-        // log2 units): probabilities then stay below 2^8, and the rescale of O is skipped
-        // by the whole wavefront in the tiles where no query's max moved
-        const float m_cand = fmaxf(m_run, mx * c);
-        const bool grow = m_cand > m_run + 8.0f;
-        const float m_new = grow ? m_cand : m_run;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
-        // probabilities rounded to fp16 in pairs (the PV operand); the row sum adds the same
-        // rounded values (one dot2 per pair), so numerator and denominator agree
-        float ls = 0.0f;
-        uint32_t P[2][8];
-        const h2v ones = {(_Float16)1.0f, (_Float16)1.0f};
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-            for (int i = 0; i < 16; i += 2) {
-                const v2f pp = {__builtin_amdgcn_exp2f(__builtin_fmaf(S[kh][i], c, -m_new)),
-                                __builtin_amdgcn_exp2f(__builtin_fmaf(S[kh][i + 1], c, -m_new))};
-                const h2v ph = __builtin_convertvector(pp, h2v);
-                ls = __builtin_amdgcn_fdot2(ph, ones, ls, false);
-                P[kh][i >> 1] = __builtin_bit_cast(uint32_t, ph);
+            for (int j = 0; j < 4; ++j) {
+                const v16f& sv = S[j >> 1];
+                const int o = 8 * (j & 1);
+                m4[j] = fmaxf(fmaxf(fmaxf(sv[o], sv[o + 1]), fmaxf(sv[o + 2], sv[o + 3])),
+                              fmaxf(fmaxf(sv[o + 4], sv[o + 5]), fmaxf(sv[o + 6], sv[o + 7])));
             }
-        ls = xsum32(ls);
-        l_run = l_run * alpha + ls;
-        if (__builtin_amdgcn_ballot_w64(grow)) {
+            const float mx = xmax32(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])));
+            const float m_new = fmaxf(m_run, mx * c);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            ls = probs(m_new);
+            l_run *= alpha;
 #pragma unroll
             for (int db = 0; db < NDB; ++db)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) O[db][e] *= alpha;
         }
-
-        // O^T += V^T P^T over the 64 keys (four 16-key MFMA chunks)
+        l_run += ls;
+    };
+    // O^T += V^T P^T over the 64 keys of V buffer vbuf (four 16-key MFMA chunks)
+    // V^T fragment rows by transposing reads of the DMA-staged V tile: lane (lr, g) of
+    // 16-lane group (lane / 16) addresses key 4g + j (j = (lane % 16) / 4) of an 8-key block,
+    // columns 32 db + 16 ((lane / 16) % 2) + 4q .. +3 (q = lane % 4), and receives column
+    // 32 db + lr of keys 4g .. 4g + 3 of the block
+    int vtoff[NDB];
+    if (KDMA) {
+        const int j = (lane & 15) >> 2, q = lane & 3, rw = 4 * g + j;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+            vtoff[db] = rw * 2 * D + 16 * ((4 * db + 2 * ((lane >> 4) & 1) + (q >> 1)) ^ vswz(rw)) + 8 * (q & 1);
+    }
+    // O^T += V^T P^T over the 64 keys of V buffer vbuf (four 16-key MFMA chunks)
+    auto pv = [&](int vbuf, uint32_t (*P)[8]) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-            const _Float16* vrow = &sV[cb][(32 * db + lr) * VS];
+            const _Float16* vrow = &sV[vbuf][(32 * db + lr) * VS];
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
                     const int k0 = 32 * kh + 16 * hh + 4 * g;
-                    const uint2 lo = *reinterpret_cast<const uint2*>(&vrow[k0]);
-                    const uint2 hi = *reinterpret_cast<const uint2*>(&vrow[k0 + 8]);
+                    uint2 lo, hi;
+                    if (KDMA) {
+                        const char* vt = reinterpret_cast<const char*>(sV[vbuf]) + vtoff[db] + (32 * kh + 16 * hh) * 2 * D;
+                        lo = lds_read_tr16(vt);
+                        hi = lds_read_tr16(vt + 8 * 2 * D);
+                    } else {
+                        lo = *reinterpret_cast<const uint2*>(&vrow[k0]);
+                        hi = *reinterpret_cast<const uint2*>(&vrow[k0 + 8]);
+                    }
                     const v4i av = {(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
                     const v4i bp = {(int)P[kh][4 * hh], (int)P[kh][4 * hh + 1], (int)P[kh][4 * hh + 2],
                                     (int)P[kh][4 * hh + 3]};
@@ -328,12 +372,67 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void fattn_kernel(const F
                                                                   __builtin_bit_cast(v8h, bp), O[db], 0, 0, 0);
                 }
         }
-        if (NBUF == 2 && t + 1 < ntile) {
-            store_tile(cb ^ 1, kv0 + FA_BKV);
-            if (t + 2 < ntile) load_tile(kv0 + 2 * FA_BKV);
+    };
+
+    const int ntile = (nkv + FA_BKV - 1) / FA_BKV;
+    if (NBUF == 1 && ntile > 1) return;  // one buffer holds one tile (the launcher's condition)
+    if constexpr (KDMA) {
+        // Software pipeline, the K tiles one ahead of V: step t issues the score MFMAs of
+        // tile t + 1 and then does the softmax of tile t (scored in step t - 1), so the
+        // matrix core works on the next scores while the VALU works on these, and then the
+        // PV MFMAs of tile t.  One LDS-only barrier per step, after the wait for this
+        // wavefront's DMAs of step t - 1, publishes K(t + 1) and V(t) and frees K buffer
+        // t % 2 (K(t), read in step t - 1) and V buffer (t + 1) % 2 (V(t - 1)), which take
+        // K(t + 2) and V(t + 1) by DMA.  No DMA is left in flight past the last step.
+        v16f SA[2], SB[2];
+        uint32_t P[2][8];
+        dma_k(0, 0);
+        dma_v(0, 0);
+        if (ntile > 1) dma_k(FA_BKV, 1);
+        if (ntile > 1) wait_vmcnt<KDI>();
+        else wait_vmcnt<0>();
+        lds_barrier();
+        score(0, SA);
+        auto step = [&](int t, int cb, v16f* Sc, v16f* Sn) {
+            const int kv0 = t * FA_BKV;
+            wait_vmcnt<0>();
+            lds_barrier();
+            if (t + 2 < ntile) dma_k(kv0 + 2 * FA_BKV, cb);
+            if (t + 1 < ntile) dma_v(kv0 + FA_BKV, cb ^ 1);
+            if (kv0 + FA_BKV > nkv) mask(Sc, kv0);
+            score(cb ^ 1, Sn);  // tile t + 1 (past the last tile: stale LDS, never used)
+            softmax(Sc, P);
+            pv(cb, P);
+        };
+        for (int t = 0; t < ntile; t += 2) {
+            step(t, 0, SA, SB);
+            if (t + 1 < ntile) step(t + 1, 1, SB, SA);
+        }
+    } else {
+        // One LDS-only barrier per tile: it publishes tile t (stored at the end of tile
+        // t - 1) and frees the other buffer (read by tile t - 1).  After tile t's compute,
+        // tile t + 1 goes from the registers (loaded during tile t) into that buffer and
+        // tile t + 2's loads are issued, so each load has a whole tile to land.
+        load_tile(0);
+        store_tile(0);
+        if (ntile > 1) load_tile(FA_BKV);
+        for (int t = 0; t < ntile; ++t) {
+            const int kv0 = t * FA_BKV, cb = NBUF == 1 ? 0 : (t & 1);
+            lds_barrier();
+            v16f S[2];
+            uint32_t P[2][8];
+            score(cb, S);
+            if (kv0 + FA_BKV > nkv) mask(S, kv0);
+            softmax(S, P);
+            pv(cb, P);
+            if (NBUF == 2 && t + 1 < ntile) {
+                store_tile(cb ^ 1);
+                if (t + 2 < ntile) load_tile(kv0 + 2 * FA_BKV);
+            }
         }
     }
 
+    l_run = xsum32(l_run);  // the two lanes of a query summed over different keys
     if (qi < p.nq && p.kv_split > 1) {  // this key range's unnormalised O and (max, sum)
         const int64_t pr = ((int64_t)ks * p.B * p.nh + (int64_t)b * p.nh + h) * p.nq + qi;
         float* orow = p.part + pr * D;
@@ -463,9 +562,11 @@ static void fa_launch_d(const FaArgs& a, bool qf32, bool kvf32, int B, hipStream
     const dim3 grid((unsigned)((items + 7) / 8 * 8));
     bool launched = false;
     if constexpr (D == 64 || D == 128) {
-        // fp16 K rows and bases on 16 bytes, key offsets within the 32-bit buffer offset
+        // fp16 K and V rows and bases on 16 bytes, key offsets within the 32-bit buffer offset
         const bool kdma = !kvf32 && reinterpret_cast<uintptr_t>(a.k) % 16 == 0 && a.k_nb1 % 16 == 0 &&
-                          a.k_nb2 % 16 == 0 && a.k_nb3 % 16 == 0 && (int64_t)(a.nkv + FA_BKV) * a.k_nb1 < INT32_MAX;
+                          a.k_nb2 % 16 == 0 && a.k_nb3 % 16 == 0 && (int64_t)(a.nkv + FA_BKV) * a.k_nb1 < INT32_MAX &&
+                          reinterpret_cast<uintptr_t>(a.v) % 16 == 0 && a.v_nb1 % 16 == 0 && a.v_nb2 % 16 == 0 &&
+                          a.v_nb3 % 16 == 0 && (int64_t)(a.nkv + FA_BKV) * a.v_nb1 < INT32_MAX;
         if (kdma) {
             if (qf32) fattn_kernel<D, true, false, true><<<grid, FA_NT, 0, st>>>(a);
             else fattn_kernel<D, false, false, true><<<grid, FA_NT, 0, st>>>(a);
