@@ -399,6 +399,10 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
                         if (m < M && n < N) p.dots[((int64_t)m * N + n) * p.nbt + blk] = I[i];
                     }
                 }
+                if (s3 >= 0) {  // this unit's share of the refill, as below
+#pragma unroll
+                    for (int i = q * NL / NU; i < (q + 1) * NL / NU; ++i) dma_one(i, s3, lb3);
+                }
                 continue;
             }
             if (Q41 && bk == 0) {
