@@ -328,7 +328,7 @@ mi355_status mul_mat_run(mi355_context* ctx, const mi355_tensor* s0, const mi355
         }
         if (!mmq8_supported(wr, a8)) return fail(ctx, MI355_STATUS_UNSUPPORTED, "mul_mat: operands beyond the int8 kernel");
         MmqSplit sp8{pl.ks, pl.ks > 1 ? reinterpret_cast<float*>(ws + pl.q + pl.d + pl.s + pl.align) : nullptr,
-                     false};
+                     ctx->skinny};
         sp8.cus = ctx->cus;
         const char* kname = s0->type == T_Q8_0 ? "mmq8_q8_0" : s0->type == T_Q4_0 ? "mmq8_q4_0" : "mmq8_q4_1";
         Timed tk(tctx, kname);
@@ -461,7 +461,7 @@ mi355_status mul_mat_act_i8(mi355_context* ctx, const mi355_tensor* s0, const Ac
         st = ensure_ws(ctx, part);
         if (st != MI355_STATUS_SUCCESS) return st;
     }
-    MmqSplit sp{ks, ks > 1 ? static_cast<float*>(ctx->ws) : nullptr, false};
+    MmqSplit sp{ks, ks > 1 ? static_cast<float*>(ctx->ws) : nullptr, ctx->skinny};
     sp.cus = ctx->cus;
     static const char* names[3][3] = {{"mmq8_q8_0", "mmq8_q8_0+residual", "mmq8_q8_0+qkv"},
                                       {"mmq8_q4_0", "mmq8_q4_0+residual", "mmq8_q4_0+qkv"},

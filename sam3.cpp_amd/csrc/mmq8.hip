@@ -731,6 +731,174 @@ int mmq8_ksplit(int64_t M, int64_t N, int64_t K, int cus) {
     return best;
 }
 
+// ---- skinny K (K <= 128, large M: Hiera's stage-1 projections at 65536 tokens)
+// The tiled kernel spends such a GEMM in prologue and epilogue: a 128-row tile has at most
+// two K stages.  Here a wavefront owns 32 activation rows and NPW consecutive 32-column
+// n-tiles: its A fragments (at most four blocks) and d_a stay in registers, the weight
+// fragments and d_w of each n-tile come straight from global memory (the weights are a few
+// KB and L2-resident), and each 32 x 32 tile leaves through the wavefront's own LDS staging
+// as float4 row segments into the same epilogue as the tiled kernel (epi4).  No barriers and
+// no LDS sharing between wavefronts, so small workgroups fill the CUs.  The arithmetic is
+// the tiled kernel's, in its order: per stage (two blocks, the second a zero block past K
+// for odd block counts) Q4_1's offset MFMA, then per block the isum MFMA, the d_a (x) d_w
+// MFMA and acc = fma(float(isum), S, acc), so the results are bit-identical (float(isum)
+// by conversion here, which frees the tiled kernel's bias registers; both are exact).
+// npw n-tiles per wavefront, sized by the host for about four wavefronts per SIMD.
+namespace {
+constexpr int SK8_TP = 36;   // staging row pitch (floats): 32 columns + 4
+constexpr int SK8_WPS = 4;   // wavefronts per SIMD the registers allow
+}  // namespace
+
+template <int WT, int EPI>
+__global__ __launch_bounds__(256, SK8_WPS) void mmq8_skinny_kernel(const Mmq8Args p, const MmqEpi e, int npw) {
+    constexpr bool Q41 = WT == T_Q4_1;
+    __shared__ __attribute__((aligned(16))) float stg_all[4][32 * SK8_TP];
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lr = lane & 31, g = lane >> 5;
+    const int M = p.M, N = p.N, ntn = (N + 31) / 32, ngr = (ntn + npw - 1) / npw;
+    const int gw = blockIdx.x * 4 + w;  // this wavefront's task: (m-tile, group of n-tiles)
+    if (gw >= ((M + 31) / 32) * ngr) return;
+    const int mt = gw / ngr, j0 = (gw - mt * ngr) * npw, j1 = min(j0 + npw, ntn);
+    const int m0 = 32 * mt, nstg = (p.K / QK + 1) / 2;  // stages of two blocks (at most 2)
+    float* stg = stg_all[w];
+
+    // A fragments (bytes 32 b + 16 g of row m0 + lr), d_a in k-slot b % 2 of the scale MFMA's
+    // A operand, Q4_1's Q8_1 sums (dword s = blocks 2s, 2s + 1); blocks past K are zero
+    const int ma = m0 + lr;
+    const bool mv = ma < M;
+    v4i af[4];
+    v2i da[4];
+    int sa[2] = {0, 0};
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const bool in = mv && b < 2 * nstg && 32 * b < p.K;
+        af[b] = in ? *reinterpret_cast<const v4i*>(p.A + (int64_t)ma * p.a_s1 + 32 * b + 16 * g) : v4i{0, 0, 0, 0};
+        const uint32_t dd = mv && b < 2 * nstg ? ((b & 1) ? p.Adh : p.Adl)[(int64_t)ma * p.nst + (b >> 1)] : 0u;
+        da[b] = v2i{(int)dd, 0};
+    }
+    if (Q41) {
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+            if (mv && st < nstg) sa[st] = (int)reinterpret_cast<const uint32_t*>(p.As)[(int64_t)ma * p.nst + st];
+    }
+    // the epilogue rows of this lane: 8 q + lane / 8 of the m-tile, q < 4; their residual
+    // destinations or (qkv) windows and tokens, fixed for all n-tiles
+    const int rl = lane >> 3, c4 = lane & 7;
+    int rrv[4] = {-1, -1, -1, -1}, bwv[4] = {0, 0, 0, 0}, tnv[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int m = m0 + 8 * q + rl;
+        if (EPI == MMQ_EPI_RESIDUAL && m < M) rrv[q] = map_row32(e.map, rowmap_rcp(e.map), m);
+        if (EPI == MMQ_EPI_QKV && m < M) bwv[q] = div_rcp(m, e.ntok, 1.0 / (double)e.ntok, tnv[q]);
+    }
+    const v16i zi = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const v16f zf = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+
+    for (int j = j0; j < j1; ++j) {
+        const int n = 32 * j + lr;
+        const bool nv = n < N;
+        // weight fragments, d_w (k-slot 0 or 1; lanes 32..63 carry k-slots 4..7 of the scale
+        // MFMA and 8..15 of Q4_1's: zero) and Q4_1's minima of this n-tile
+        v4i wf[4];
+        v2i dw[2];
+        int mw[2] = {0, 0};
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const bool in = nv && b < 2 * nstg && 32 * b < p.K;
+            wf[b] = in ? *reinterpret_cast<const v4i*>(p.W + (int64_t)n * p.w_s1 + 32 * b + 16 * g) : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const bool in = nv && g == 0 && st < nstg;
+            dw[st] = v2i{in ? (int)reinterpret_cast<const uint32_t*>(p.Wd)[(int64_t)n * p.nst + st] : 0, 0};
+            if (Q41) mw[st] = in ? (int)reinterpret_cast<const uint32_t*>(p.Wm)[(int64_t)n * p.nst + st] : 0;
+        }
+        v16f acc = zf;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            if (st >= nstg) break;
+            if (Q41) {
+                const v4i saf = {sa[st], 0, 0, 0}, mwf = {mw[st], 0, 0, 0};
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, saf), __builtin_bit_cast(v8h, mwf),
+                                                             acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int b = 2 * st + h;
+                const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[b], wf[b], zi, 0, 0, 0);
+                const v16f S = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, da[b]),
+                                                                    __builtin_bit_cast(v4h, dw[st]), zf, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[i] = __builtin_fmaf((float)I[i], S[i], acc[i]);
+                __builtin_amdgcn_sched_barrier(0);  // one block's MFMA results live at a time
+            }
+        }
+        // the tile through this wavefront's staging: element i is row 8 (i >> 2) + 4 g + (i & 3)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) stg[(8 * (i >> 2) + 4 * g + (i & 3)) * SK8_TP + lr] = acc[i];
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's LDS writes are done
+        __builtin_amdgcn_wave_barrier();
+        const int nc = 32 * j + 4 * c4;
+        const bool cv = nc < N;  // N % 4 == 0
+        v4f bv = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (EPI != MMQ_EPI_STORE && cv) bv = *reinterpret_cast<const v4f*>(&e.bias[nc]);
+        QkvLane ql{nullptr, 0, 0, false};
+        if (EPI == MMQ_EPI_QKV && cv) {
+            const int E = e.nh * e.hd, which = nc / E, col = nc - which * E;
+            ql.hh = col / e.hd;
+            ql.d = col - ql.hh * e.hd;
+            ql.dst = which == 0 ? e.q : which == 1 ? e.k : e.v;
+            ql.rope = e.rope && which < 2;
+        }
+        // what the stores add (residual rows, RoPE factors), loaded before the stores
+        v4f pvv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            pvv[q] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            const int m = m0 + 8 * q + rl;
+            if (EPI == MMQ_EPI_RESIDUAL && cv && rrv[q] >= 0)
+                pvv[q] = *reinterpret_cast<const v4f*>(&e.res[(int64_t)rrv[q] * N + nc]);
+            if (EPI == MMQ_EPI_QKV && ql.rope && cv && m < M)
+                pvv[q] = *reinterpret_cast<const v4f*>(&e.rope[(int64_t)tnv[q] * e.hd + ql.d]);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int r = 8 * q + rl, m = m0 + r;
+            const v4f v = *reinterpret_cast<const v4f*>(&stg[r * SK8_TP + 4 * c4]);
+            if (m >= M || !cv) continue;
+            epi4<EPI>(reinterpret_cast<char*>(p.D), p.d_nb1, e, N, m, nc, v, bv, rrv[q], ql, bwv[q], tnv[q], pvv[q]);
+        }
+        __builtin_amdgcn_wave_barrier();  // the reads are done before the next tile overwrites
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+    }
+}
+
+// K <= 128 at M >= 4096, no split or inspection, float4 rows: the skinny kernel (true)
+static bool launch8_skinny(const Mmq8Args& a, int wtype, const MmqEpi* e, int cus, hipStream_t st) {
+    const int kind = e ? e->kind : MMQ_EPI_STORE;
+    // as many wavefronts as the CUs hold at once
+    const int64_t mtiles = (a.M + 31) / 32, ntn = (a.N + 31) / 32;
+    const int64_t target = 4LL * SK8_WPS * (cus > 0 ? cus : 256);
+    const int npw = (int)std::max<int64_t>(1, (mtiles * ntn + target - 1) / target);
+    const int64_t waves = mtiles * ((ntn + npw - 1) / npw);
+    const dim3 grid((unsigned)((waves + 3) / 4));
+    MmqEpi none{};
+    const MmqEpi& ee = e ? *e : none;
+#define SK8(WT)                                                                                           \
+    do {                                                                                                  \
+        if (kind == MMQ_EPI_STORE) mmq8_skinny_kernel<WT, MMQ_EPI_STORE><<<grid, 256, 0, st>>>(a, none, npw);  \
+        else if (kind == MMQ_EPI_RESIDUAL) mmq8_skinny_kernel<WT, MMQ_EPI_RESIDUAL><<<grid, 256, 0, st>>>(a, ee, npw); \
+        else mmq8_skinny_kernel<WT, MMQ_EPI_QKV><<<grid, 256, 0, st>>>(a, ee, npw);                            \
+    } while (0)
+    switch (wtype) {
+        case T_Q8_0: SK8(T_Q8_0); break;
+        case T_Q4_0: SK8(T_Q4_0); break;
+        default: SK8(T_Q4_1); break;
+    }
+#undef SK8
+    return true;
+}
+
 template <int WT, int TM>
 static void launch8_t(const Mmq8Args& a, const MmqEpi* e, hipStream_t st) {
     const int TT = a.tiles_m * a.tiles_n * a.ksplit;
@@ -811,6 +979,14 @@ hipError_t launch_mmq8(const WRep& w, const ActI8& a, const MatD& d, const MmqEp
     p.d_v4 = N % 4 == 0 && p.d_nb1 % 16 == 0 && (reinterpret_cast<uintptr_t>(p.D) & 15) == 0;
     if (epi && epi->kind != MMQ_EPI_STORE && !split) p.d_v4 = 1;
     if (!split && !dots && (!epi || epi->kind == MMQ_EPI_STORE) && !d.data) return hipErrorInvalidValue;
+    const LnArgs* ln = epi && epi->kind == MMQ_EPI_RESIDUAL ? epi->ln_next : nullptr;
+    if (!split && !dots && sp.skinny && a.K <= 128 && a.M >= 4096 && N % 4 == 0 &&
+        ((epi && epi->kind != MMQ_EPI_STORE) || p.d_v4)) {
+        launch8_skinny(p, w.type, epi, sp.cus, st);
+        const hipError_t e1 = hipGetLastError();
+        if (e1 != hipSuccess) return e1;
+        return ln ? launch_layer_norm(*ln, st) : hipSuccess;
+    }
     switch (w.type * 2 + (TMv == 64 ? 1 : 0)) {
         case T_Q8_0 * 2: launch8_t<T_Q8_0, 128>(p, epi, st); break;
         case T_Q8_0 * 2 + 1: launch8_t<T_Q8_0, 64>(p, epi, st); break;
@@ -821,7 +997,6 @@ hipError_t launch_mmq8(const WRep& w, const ActI8& a, const MatD& d, const MmqEp
     }
     hipError_t e0 = hipGetLastError();
     if (e0 != hipSuccess) return e0;
-    const LnArgs* ln = epi && epi->kind == MMQ_EPI_RESIDUAL ? epi->ln_next : nullptr;
     if (split) {
         // a 1024-wide residual into its own rows: the reduction and the next LayerNorm in one pass
         if (ln && N == 1024 && sp.ks <= 4 && epi->map.kind == ROWMAP_IDENTITY && epi->res == epi->out &&

@@ -79,6 +79,31 @@ def test_route_bit_identical(mi, ctx, orc, route, tname, M, N, K):
     assert e <= 1e-5, f"rel err {e:.3e}"
 
 
+@pytest.mark.parametrize("route", ["int8", "prepared"])
+@pytest.mark.parametrize("tname", ["q8_0", "q4_0", "q4_1"])
+@pytest.mark.parametrize("M,N,K", [(65536, 288, 96), (5000, 100, 64), (4097, 36, 128), (8192, 384, 32),
+                                   (16384, 192, 96), (4096, 576, 96), (4100, 33, 96)])
+def test_route_skinny_bit_identical(mi, ctx, orc, route, tname, M, N, K):
+    """K <= 128 at M >= 4096 on the int8 routes runs on the skinny int8 kernel (N % 4 == 0;
+    N = 33 stays tiled): bit-identical to the tiled int8 kernel (the skinny switch off) and
+    to the fp16 route, ragged M and N included."""
+    t = orc.NAME_TYPE[tname]
+    print(f"{route} skinny {tname} M={M} N={N} K={K}", flush=True)
+    w = orc.normal(N * K, seed=N + K, stream=1, std=0.02).reshape(N, K)
+    x = orc.normal(M * K, seed=N + K, stream=2).reshape(M, K)
+    wq = orc.quantize_weights(t, w)
+    got = _run(mi, ctx, wq, t, K, N, x, route)
+    ctx.set_skinny(False)
+    try:
+        tiled = _run(mi, ctx, wq, t, K, N, x, route)
+    finally:
+        ctx.set_skinny(True)
+    ref16 = _run(mi, ctx, wq, t, K, N, x, "f16")
+    assert torch.isfinite(got).all()
+    assert torch.equal(got, tiled), f"max diff {(got - tiled).abs().max().item():.3e}"
+    assert torch.equal(got, ref16), f"max diff {(got - ref16).abs().max().item():.3e}"
+
+
 @pytest.mark.parametrize("route", ROUTES)
 @pytest.mark.parametrize("tname", ["q8_0", "q4_0", "q4_1"])
 @pytest.mark.parametrize("K", [96, 1024])
