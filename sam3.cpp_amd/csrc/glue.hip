@@ -295,9 +295,12 @@ __global__ __launch_bounds__(256) void bias_act_i8_kernel(const float* __restric
     }
     for (; t < total; t += step) {
         const int r = t / hb, j = t - r * hb;
-        const int tn = t + step;
+        // the next half-block's loads, issued unconditionally (the last iteration reloads its own
+        // half-block): the compiler then counts them, and its waits for this iteration's data
+        // leave them in flight (a conditional load would make it wait for them too)
+        const int tn = t + step < total ? t + step : t;
         v4f hn[4], bn[4];
-        if (tn < total) {
+        {
             const int rn = tn / hb, jn = tn - rn * hb;
             const float* hr = h + (int64_t)rn * n + 16 * jn;
 #pragma unroll
