@@ -86,10 +86,14 @@ __device__ __forceinline__ float xsum32(float x) {
 template <int D>
 __device__ __forceinline__ int kswz(int r) { return D == 64 ? ((r & 7) ^ ((r >> 3) & 1)) : (r & 15); }
 // V row slot of 16-byte chunk c in row r of an unpadded fp16 V tile (DMA staging): slot
-// c ^ vswz(r), vswz a permutation of 0..7 over any 8 aligned rows whose first four values
-// also reach both halves of the slots, so the transposing reads of 4 or 8 consecutive rows
-// spread over all banks
-__device__ __forceinline__ int vswz(int r) { return ((r & 1) << 2) | ((r >> 1) & 3); }
+// c ^ vswz(r).  A transposing read of the PV operand takes 64 bytes (4 chunks 4 db .. +3)
+// from each of 4 consecutive rows per half-wavefront; the 64 banks of 4 bytes then hold each
+// byte once when the 4 rows' chunks land in distinct 64-byte quarters of a 256-byte bank
+// line: D = 64 (128-byte rows: odd rows are the upper bank half) moves rows 2, 3 (mod 4) to
+// the other half of their row's slots and rows 4..7 (mod 8) by one chunk; D = 128 (256-byte
+// rows) moves row r by 4 (r % 4) chunks.
+template <int D>
+__device__ __forceinline__ int vswz(int r) { return D == 64 ? (((r & 2) << 1) | ((r >> 2) & 1)) : ((r & 3) << 2); }
 
 // 4 fp16 of LDS by the transposing read of gfx950 (ds_read_b64_tr_b16): within each group
 // of 16 lanes, lane i receives element i % 4 of the 8 bytes addressed by lanes i / 4,
@@ -244,7 +248,7 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void fattn_kernel(const F
             const int base = (w * KDI + j) << 10, byte = base + 16 * lane;
             const int r = byte / (2 * D), s = (byte % (2 * D)) / 16;
             dma_b128(vrsrc, reinterpret_cast<const char*>(sV[buf]) + base,
-                     (kv0 + r) * (int)p.v_nb1 + 16 * (s ^ vswz(r)));
+                     (kv0 + r) * (int)p.v_nb1 + 16 * (s ^ vswz<D>(r)));
         }
     };
 
@@ -344,7 +348,7 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void fattn_kernel(const F
         const int j = (lane & 15) >> 2, q = lane & 3, rw = 4 * g + j;
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
-            vtoff[db] = rw * 2 * D + 16 * ((4 * db + 2 * ((lane >> 4) & 1) + (q >> 1)) ^ vswz(rw)) + 8 * (q & 1);
+            vtoff[db] = rw * 2 * D + 16 * ((4 * db + 2 * ((lane >> 4) & 1) + (q >> 1)) ^ vswz<D>(rw)) + 8 * (q & 1);
     }
     // O^T += V^T P^T over the 64 keys of V buffer vbuf (four 16-key MFMA chunks)
     auto pv = [&](int vbuf, uint32_t (*P)[8]) {
