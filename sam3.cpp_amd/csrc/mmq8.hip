@@ -504,7 +504,10 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
                 }
         return;
     }
-    constexpr int TP = 68;                  // staging row pitch (floats): 64 columns + 4
+    // staging rows of 64 floats (256 bytes, one line of the 64 4-byte LDS banks); rows with bit 2
+    // set hold their columns rotated by 32, so a write pass (lanes 0..31 row R, lanes 32..63 row
+    // R + 4) covers all 64 banks, and a read (16 lanes per row) sweeps one row
+    constexpr int TP = 64;
     constexpr int RP = TM == 128 ? 32 : 16;  // rows per staging pass: two wavefronts per stage buffer
     constexpr int NP = 32 / RP;              // passes per 32-row m-tile
     static_assert(2 * RP * TP * 4 <= (int)sizeof(St), "epilogue staging exceeds a stage buffer");
@@ -532,7 +535,7 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
         for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
             for (int i = 16 * h / NP; i < 16 * (h + 1) / NP; ++i)
-                stg[(8 * (i >> 2) + 4 * g + (i & 3) - RP * h) * TP + 32 * nt + lr] = acc[mt][nt][i];
+                stg[(8 * (i >> 2) + 4 * g + (i & 3) - RP * h) * TP + ((32 * nt + lr + 32 * g) & 63)] = acc[mt][nt][i];
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's LDS writes are done
         __builtin_amdgcn_wave_barrier();
         // the pass's rows from the row table, and what their stores add, loaded before the stores
@@ -563,7 +566,7 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
             for (int j = 0; j < CH; ++j) {
                 const int r = (c0 + j) * 4 + (lane >> 4);
                 const int m = m0 + WMR * wm + 32 * mt + RP * h + r;
-                const v4f v = *reinterpret_cast<const v4f*>(&stg[r * TP + 4 * c4]);
+                const v4f v = *reinterpret_cast<const v4f*>(&stg[r * TP + ((4 * c4 + 32 * ((r >> 2) & 1)) & 63)]);
                 if (m >= M || !cv) continue;
                 epi4<EPI>(Dz, p.d_nb1, e, N, m, nc, v, bv, rrv[j], ql, bwv[j], tnv[j], pvv[j]);
             }
