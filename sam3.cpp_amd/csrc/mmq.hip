@@ -520,7 +520,9 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
     if (EPI == MMQ_EPI_STORE) {
         char* Dz = reinterpret_cast<char*>(p.D) + (int64_t)i12 * p.d_nb2 + (int64_t)i13 * p.d_nb3 + split * p.d_split;
         if (p.d_v4) {  // row-major through LDS: float4 stores, whole 512-byte row segments
-            constexpr int TP = BN + 4, CPR = BN / 4, IT = 64 * CPR / NT;
+            // 128-float rows (two lines of the 64 4-byte banks), columns of rows with bit 2 set
+            // rotated by 32: a write (lanes 0..31 row R, lanes 32..63 row R + 4) hits 64 banks
+            constexpr int TP = BN, CPR = BN / 4, IT = 64 * CPR / NT;
             float* t0 = reinterpret_cast<float*>(&st0);
             float* t1 = reinterpret_cast<float*>(&st1);
             const int c = tid % CPR, nc = n0 + 4 * c;
@@ -530,15 +532,15 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int r = 8 * (i >> 2) + 4 * g + (i & 3);
-                    t0[r * TP + wrow] = acc[2 * half][i];
-                    t1[r * TP + wrow] = acc[2 * half + 1][i];
+                    t0[r * TP + ((wrow + 32 * g) & (BN - 1))] = acc[2 * half][i];
+                    t1[r * TP + ((wrow + 32 * g) & (BN - 1))] = acc[2 * half + 1][i];
                 }
                 __syncthreads();
 #pragma unroll
                 for (int it = 0; it < IT; ++it) {
                     const int r = it * (NT / CPR) + tid / CPR, m = m0 + half * 64 + r;
                     if (m >= M || nc >= N) continue;
-                    const v4f v = *reinterpret_cast<const v4f*>(&(it < IT / 2 ? t0 : t1)[(r & 31) * TP + 4 * c]);
+                    const v4f v = *reinterpret_cast<const v4f*>(&(it < IT / 2 ? t0 : t1)[(r & 31) * TP + ((4 * c + 32 * ((r >> 2) & 1)) & (BN - 1))]);
                     *reinterpret_cast<v4f*>(Dz + (int64_t)m * p.d_nb1 + (int64_t)nc * 4) = v;
                 }
             }
@@ -557,7 +559,7 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
     // at a time (32 in st0, 32 in st1), is rewritten row-major so that each
     // thread then owns 4 consecutive columns (float4 loads and stores).
     // u = dst + bias, each add rounded to fp32 as ggml's ADD nodes.
-    constexpr int TP = BN + 4;                // row pitch (floats)
+    constexpr int TP = BN;                    // row pitch (floats), rows with bit 2 set rotated by 32
     constexpr int CPR = BN / 4;               // float4 chunks per row
     constexpr int IT = 64 * CPR / NT;         // rows per thread per half
     static_assert(32 * TP * 4 <= (int)sizeof(St), "epilogue tile exceeds a stage buffer");
@@ -572,8 +574,8 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int r = 8 * (i >> 2) + 4 * g + (i & 3);
-            t0[r * TP + wrow] = acc[2 * half][i];
-            t1[r * TP + wrow] = acc[2 * half + 1][i];
+            t0[r * TP + ((wrow + 32 * g) & (BN - 1))] = acc[2 * half][i];
+            t1[r * TP + ((wrow + 32 * g) & (BN - 1))] = acc[2 * half + 1][i];
         }
         __syncthreads();
         if (EPI == MMQ_EPI_QKV) {
@@ -583,7 +585,7 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
             for (int it = 0; it < IT; ++it) {
                 const int r = it * (NT / CPR) + tid / CPR, m = m0 + half * 64 + r;
                 if (m >= M || !cv) continue;
-                const v4f uv = *reinterpret_cast<const v4f*>(&(it < IT / 2 ? t0 : t1)[(r & 31) * TP + 4 * c]) + bv;
+                const v4f uv = *reinterpret_cast<const v4f*>(&(it < IT / 2 ? t0 : t1)[(r & 31) * TP + ((4 * c + 32 * ((r >> 2) & 1)) & (BN - 1))]) + bv;
                 float u0 = uv[0], u1 = uv[1], u2 = uv[2], u3 = uv[3];
                 const int bw = m / e.ntok, n = m - bw * e.ntok;
                 if (which < 2 && e.rope) {
@@ -611,7 +613,7 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     const int it = i0 + k, r = it * (NT / CPR) + tid / CPR;
-                    const v4f v = *reinterpret_cast<const v4f*>(&(it < IT / 2 ? t0 : t1)[(r & 31) * TP + 4 * c]);
+                    const v4f v = *reinterpret_cast<const v4f*>(&(it < IT / 2 ? t0 : t1)[(r & 31) * TP + ((4 * c + 32 * ((r >> 2) & 1)) & (BN - 1))]);
                     if (rr[k] >= 0) *reinterpret_cast<v4f*>(&e.out[(int64_t)rr[k] * N + nc]) = xs[k] + (v + bv);
                 }
             }
