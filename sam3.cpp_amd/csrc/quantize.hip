@@ -203,8 +203,9 @@ __global__ __launch_bounds__(256) void quantize_q4_kernel(const char* __restrict
 // 32-element block: quants as fp16 integers (exact) [rows][K], scale and Q8_1
 // sum as the fp16 values ggml stores, [rows][dp] (dp = block count rounded up
 // to even; the padding slot is written as zero).  A wavefront covers 64
-// consecutive blocks of the flattened [rows][nb] grid, so loads (128 B per
-// thread), quant stores (64 B per thread) and scale stores are contiguous.
+// consecutive blocks of the flattened [rows][nb] grid.  Flat 16-byte aligned F32
+// rows take quantize_chunks_kernel (below) instead; this kernel serves strided,
+// unaligned and F16 sources and quant row pitches wider than K.
 // I8: quants as int8 [rows][q_s1 bytes] (the int8-MFMA operand) instead of fp16 [rows][ne0].
 // rnb = 1 / (blocks per row) when the rows lie at a fixed pitch nb1 and nblocks plus a row's
 // blocks stay below 2^31: row and block then come from div_rcp, not from 64-bit divisions
@@ -297,22 +298,163 @@ __global__ __launch_bounds__(256) void quantize_mmq_kernel(const char* __restric
 }
 
 // Flat F32 rows (row r at src + r * nb1, elements contiguous, base and nb1 16-byte aligned) ->
-// F16 rows of `pitch` halves, 8 elements per thread (two 16-byte loads, one 16-byte store) with
-// the row from div_rcp; ne0 % 8 == 0, pitch == ne0.
+// the MUL_MAT operand (o: the int8 or fp16-quant layout, quant rows of K = ne0), the same
+// from_float as quantize_mmq_kernel.  The grid walks 4-value chunks of the flattened
+// [rows][K / 4] grid: a workgroup owns CH_U * 256 consecutive chunks, thread t chunks
+// base + 256 u + t, so every load and store instruction of a wavefront covers 1 KB (loads) or
+// 256 / 512 bytes (quants) of consecutive addresses, and all CH_U 16-byte loads are issued
+// before the first block is reduced.  The 8 lanes of a 32-value block (consecutive chunks,
+// consecutive lanes) reduce it by DPP (act_store_chunk); K % 32 == 0 makes the bounds test
+// uniform over each such group.
+// MODE (ACT_Q8, ACT_Q8S, ACT_I8 or ACT_I8S) replaces o.mode, so the operand layout is fixed
+// at compile time.  DENSE: rows back to back (nb1 = 4 K) and an even block count per row
+// (dp = K / 32, no padding slot), so chunk i's values, quants and block i / 8's scale slots
+// all follow from i without a division.
+constexpr int CH_U = 4;
+template <int MODE>
+__device__ __forceinline__ void dense_chunk(const ActOut& o, int i, v4f x) {
+    float amax = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+    amax = group_max<8>(amax);
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    const int q0 = (int)rintf(x[0] * id), q1 = (int)rintf(x[1] * id);
+    const int q2 = (int)rintf(x[2] * id), q3 = (int)rintf(x[3] * id);
+    int isum = 0;
+    if (act_has_sums(MODE)) isum = group_sum_i<8>(q0 + q1 + q2 + q3);
+    const int g = i >> 3;  // the block: row * (K / 32) + block in the row
+    if ((i & 7) == 0) {
+        if (MODE >= ACT_I8) {  // dword g / 2 of dl (even g: low half) or dh (odd g: high half)
+            if ((g & 1) == 0) reinterpret_cast<uint32_t*>(o.d)[g >> 1] = (uint32_t)f2h(d);
+            else o.dh[g >> 1] = (uint32_t)f2h(d) << 16;
+        } else {
+            o.d[g] = f2h(d);
+        }
+        if (act_has_sums(MODE)) o.s[g] = f2h(d * (float)isum);
+    }
+    if (MODE >= ACT_I8) {
+        reinterpret_cast<uint32_t*>(o.q)[i] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) |
+                                              ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)(q3 & 0xff) << 24);
+    } else {
+        const uint32_t h0 = (uint32_t)f2h((float)q0) | ((uint32_t)f2h((float)q1) << 16);
+        const uint32_t h1 = (uint32_t)f2h((float)q2) | ((uint32_t)f2h((float)q3) << 16);
+        reinterpret_cast<uint2*>(o.q)[i] = make_uint2(h0, h1);
+    }
+}
+// Dense rows, two lanes per 32-value block: lane 2j + e holds values 16 e .. 16 e + 15 of
+// its block (half i of the flattened grid, 64 bytes: four 16-byte loads), the pair's max by
+// one DPP swap (act_store_half16's arithmetic), 16 quant bytes (or 16 halves) per lane.  A
+// block's division pair is done by two lanes instead of eight, a quarter of the VALU work of
+// the chunk form per byte.
+constexpr int HF_U = 2;
+template <int MODE>
+__device__ __forceinline__ void dense_half(const ActOut& o, int i, const v4f (&xv)[4]) {
+    float x[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) x[j] = xv[j >> 2][j & 3];
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) amax = fmaxf(amax, fabsf(x[j]));
+    amax = fmaxf(amax, lane_swap_f<1>(amax));  // quad_perm [1, 0, 3, 2]: the block's other half
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    int q[16], isum = 0;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        q[j] = (int)rintf(x[j] * id);
+        isum += q[j];
+    }
+    if (act_has_sums(MODE)) isum += lane_swap<1>(isum);
+    const int g = i >> 1;  // the block: row * (K / 32) + block in the row
+    if ((i & 1) == 0) {
+        if (MODE >= ACT_I8) {  // dword g / 2 of dl (even g: low half) or dh (odd g: high half)
+            if ((g & 1) == 0) reinterpret_cast<uint32_t*>(o.d)[g >> 1] = (uint32_t)f2h(d);
+            else o.dh[g >> 1] = (uint32_t)f2h(d) << 16;
+        } else {
+            o.d[g] = f2h(d);
+        }
+        if (act_has_sums(MODE)) o.s[g] = f2h(d * (float)isum);
+    }
+    if (MODE >= ACT_I8) {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            w[j] = (uint32_t)(q[4 * j] & 0xff) | ((uint32_t)(q[4 * j + 1] & 0xff) << 8) |
+                   ((uint32_t)(q[4 * j + 2] & 0xff) << 16) | ((uint32_t)(q[4 * j + 3] & 0xff) << 24);
+        reinterpret_cast<uint4*>(o.q)[i] = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+        uint32_t hw[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hw[j] = (uint32_t)f2h((float)q[2 * j]) | ((uint32_t)f2h((float)q[2 * j + 1]) << 16);
+        uint4* dst = reinterpret_cast<uint4*>(o.q) + 2 * (int64_t)i;
+        dst[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        dst[1] = make_uint4(hw[4], hw[5], hw[6], hw[7]);
+    }
+}
+// thread t of workgroup b: halves (b HF_U + u) 256 + t, u < HF_U (nh halves, nh even)
+template <int MODE>
+__global__ __launch_bounds__(256) void quantize_halves_kernel(const char* __restrict__ src, int nh, ActOut o) {
+    o.mode = MODE;
+    const int i0 = blockIdx.x * (256 * HF_U) + threadIdx.x;
+    v4f x[HF_U][4];
+#pragma unroll
+    for (int u = 0; u < HF_U; ++u) {
+        const v4f* p = reinterpret_cast<const v4f*>(src + (int64_t)min(i0 + 256 * u, nh - 1) * 64);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[u][j] = p[j];
+    }
+#pragma unroll
+    for (int u = 0; u < HF_U; ++u) {
+        if (i0 + 256 * u >= nh) break;
+        dense_half<MODE>(o, i0 + 256 * u, x[u]);
+    }
+}
+template <int MODE, bool DENSE>
+__global__ __launch_bounds__(256) void quantize_chunks_kernel(const char* __restrict__ src, int64_t nb1, int cpr,
+                                                              int nch, double rcpr, ActOut o, int64_t K) {
+    o.mode = MODE;
+    const int i0 = blockIdx.x * (256 * CH_U) + threadIdx.x;
+    v4f x[CH_U];
+    int row[CH_U], c[CH_U];
+#pragma unroll
+    for (int u = 0; u < CH_U; ++u) {
+        const int i = min(i0 + 256 * u, nch - 1);  // past the end: a valid chunk, loaded and dropped
+        if (DENSE) {
+            x[u] = *reinterpret_cast<const v4f*>(src + (int64_t)i * 16);
+        } else {
+            row[u] = div_rcp(i, cpr, rcpr, c[u]);
+            x[u] = *reinterpret_cast<const v4f*>(src + (int64_t)row[u] * nb1 + (int64_t)c[u] * 16);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < CH_U; ++u) {
+        const int i = i0 + 256 * u;
+        if (i >= nch) break;
+        if (DENSE) dense_chunk<MODE>(o, i, x[u]);
+        else act_store_chunk(o, row[u], K, c[u], x[u]);
+    }
+}
+// Flat F32 rows (as above) -> contiguous F16 rows of ne0 halves (pitch == ne0, ne0 % 4 == 0):
+// chunk i (4 values) of the flattened grid to halves 4i .. 4i + 3, CH_U chunks per thread
+// at a stride of 256 chunks, so a wavefront's loads cover 1 KB and its stores 512 bytes of
+// consecutive addresses, all loads issued before the first conversion.
 __global__ __launch_bounds__(256) void convert_f16_flat_kernel(const char* __restrict__ src, int64_t nb1, int cpr,
-                                                               int nchunks, double rcpr, uint16_t* __restrict__ dst) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= nchunks) return;
-    int k;
-    const int r = div_rcp(i, cpr, rcpr, k);
-    const v4f* p = reinterpret_cast<const v4f*>(src + (int64_t)r * nb1 + (int64_t)k * 32);
-    const v4f a = p[0], b = p[1];
-    uint4 o;
-    o.x = (uint32_t)f2h(a[0]) | ((uint32_t)f2h(a[1]) << 16);
-    o.y = (uint32_t)f2h(a[2]) | ((uint32_t)f2h(a[3]) << 16);
-    o.z = (uint32_t)f2h(b[0]) | ((uint32_t)f2h(b[1]) << 16);
-    o.w = (uint32_t)f2h(b[2]) | ((uint32_t)f2h(b[3]) << 16);
-    *reinterpret_cast<uint4*>(dst + (int64_t)i * 8) = o;
+                                                               int nch, double rcpr, uint16_t* __restrict__ dst) {
+    const int i0 = blockIdx.x * (256 * CH_U) + threadIdx.x;
+    v4f x[CH_U];
+#pragma unroll
+    for (int u = 0; u < CH_U; ++u) {
+        int k;
+        const int r = div_rcp(min(i0 + 256 * u, nch - 1), cpr, rcpr, k);
+        x[u] = *reinterpret_cast<const v4f*>(src + (int64_t)r * nb1 + (int64_t)k * 16);
+    }
+#pragma unroll
+    for (int u = 0; u < CH_U; ++u) {
+        const int i = i0 + 256 * u;
+        if (i >= nch) break;
+        const uint32_t h0 = (uint32_t)f2h(x[u][0]) | ((uint32_t)f2h(x[u][1]) << 16);
+        const uint32_t h1 = (uint32_t)f2h(x[u][2]) | ((uint32_t)f2h(x[u][3]) << 16);
+        *reinterpret_cast<uint2*>(dst + (int64_t)i * 4) = make_uint2(h0, h1);
+    }
 }
 
 // dst rows of `pitch` halves; columns ne0..pitch are zero
@@ -345,6 +487,27 @@ static bool flat_f32(const SrcView& s, int64_t n) {
     return s.type == T_F32 && s.nb[0] == 4 && flat && s.ne[0] >= QK && ((reinterpret_cast<uintptr_t>(s.data) | (uintptr_t)s.nb[1]) & 15) == 0 &&
            n + s.ne[0] < ((int64_t)1 << 31) && s.ne[1] * s.ne[2] * s.ne[3] * s.nb[1] < ((int64_t)1 << 40);
 }
+
+// the chunk kernels' layout: flat_f32 rows, n chunks of 4 values, and the last workgroup's
+// chunk indices below 2^31
+static bool chunk_path(const SrcView& s, int64_t n) {
+    return flat_f32(s, n) && n + 256 * CH_U < ((int64_t)1 << 31);
+}
+static dim3 chunk_grid(int64_t n) { return dim3((unsigned)((n + 256 * CH_U - 1) / (256 * CH_U))); }
+// the chunk kernel for the operand mode and layout
+template <int MODE>
+static void launch_chunks(const SrcView& src, const ActOut& o, int64_t nch, hipStream_t st) {
+    const int64_t K = src.ne[0], cpr = K / 4;
+    const bool dense = src.nb[1] == 4 * K && K % 64 == 0 && o.dp == K / 32;
+    if (dense) {
+        const int64_t nh = nch / 4;
+        quantize_halves_kernel<MODE><<<(unsigned)((nh + 256 * HF_U - 1) / (256 * HF_U)), 256, 0, st>>>(src.data, (int)nh, o);
+        return;
+    }
+    quantize_chunks_kernel<MODE, false><<<chunk_grid(nch), 256, 0, st>>>(src.data, src.nb[1], (int)cpr, (int)nch,
+                                                                         1.0 / (double)cpr, o, K);
+}
+
 
 static RowAddr row_addr(const SrcView& s) {
     RowAddr ra;
@@ -388,6 +551,12 @@ hipError_t launch_quantize_mmq(const SrcView& src, bool with_sum, int64_t dp, ui
     const int64_t rows = src.ne[1] * src.ne[2] * src.ne[3];
     const int64_t nblocks = rows * (src.ne[0] / QK);
     if (nblocks == 0) return hipSuccess;
+    if (chunk_path(src, nblocks * 8)) {
+        const ActOut o{with_sum ? ACT_Q8S : ACT_Q8, nullptr, q, d, s, dp};
+        if (with_sum) launch_chunks<ACT_Q8S>(src, o, nblocks * 8, st);
+        else launch_chunks<ACT_Q8>(src, o, nblocks * 8, st);
+        return hipGetLastError();
+    }
     const dim3 grid((unsigned)((nblocks + 255) / 256));
     const RowAddr ra = row_addr(src);
     if (with_sum)
@@ -406,6 +575,13 @@ hipError_t launch_quantize_mmq_i8(const SrcView& src, bool with_sum, int64_t s1,
     if (nblocks == 0) return hipSuccess;
     if (s1 < src.ne[0] || s1 % 16 != 0) return hipErrorInvalidValue;
     uint16_t* qq = reinterpret_cast<uint16_t*>(q);
+    if (s1 == src.ne[0] && chunk_path(src, nblocks * 8)) {
+        uint32_t* dl = reinterpret_cast<uint32_t*>(d);
+        const ActOut o{with_sum ? ACT_I8S : ACT_I8, nullptr, qq, d, s, dp, dl + rows * (dp / 2)};
+        if (with_sum) launch_chunks<ACT_I8S>(src, o, nblocks * 8, st);
+        else launch_chunks<ACT_I8>(src, o, nblocks * 8, st);
+        return hipGetLastError();
+    }
     const dim3 grid((unsigned)((nblocks + 255) / 256));
     const RowAddr ra = row_addr(src);
     if (with_sum)
@@ -421,10 +597,10 @@ hipError_t launch_convert_f16(const SrcView& src, uint16_t* dst, int64_t pitch, 
     if (pitch < src.ne[0]) return hipErrorInvalidValue;
     const int64_t n = pitch * src.ne[1] * src.ne[2] * src.ne[3];
     if (n == 0) return hipSuccess;
-    if (pitch == src.ne[0] && src.ne[0] % 8 == 0 && flat_f32(src, n / 8) && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
-        const int64_t cpr = src.ne[0] / 8, nch = n / 8;
-        convert_f16_flat_kernel<<<(unsigned)((nch + 255) / 256), 256, 0, st>>>(src.data, src.nb[1], (int)cpr, (int)nch,
-                                                                               1.0 / (double)cpr, dst);
+    if (pitch == src.ne[0] && src.ne[0] % 4 == 0 && chunk_path(src, n / 4) && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
+        const int64_t cpr = src.ne[0] / 4, nch = n / 4;
+        convert_f16_flat_kernel<<<chunk_grid(nch), 256, 0, st>>>(src.data, src.nb[1], (int)cpr, (int)nch,
+                                                                 1.0 / (double)cpr, dst);
         return hipGetLastError();
     }
     const dim3 grid((unsigned)((n + 255) / 256));
