@@ -375,6 +375,24 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
     if (nstage > 2) dma_stage(2, lbuf[2]);
     wait_dma(min(nstage - 1, 2));
     __syncthreads();  // also publishes the zero words
+    // 64-row residual epilogue: the lane's eight residual float4 (two staging passes of four
+    // rows, as the epilogue reads them) are loaded here, so their latency passes under the K
+    // loop instead of being paid once per staging pass after it (32 VGPRs; the tile's rows
+    // are in rtab since the barrier above; each element is read and later written by this
+    // lane only, so an in-place residual is safe)
+    constexpr bool PRE = EPI == MMQ_EPI_RESIDUAL && TM == 64;
+    int rr_pre[PRE ? 8 : 1];
+    v4f pv_pre[PRE ? 8 : 1];
+    if (PRE) {
+        const int nc = n0 + 64 * wn + 4 * (lane & 15);
+#pragma unroll
+        for (int q = 0; q < (PRE ? 8 : 1); ++q) {
+            const int tr = WMR * wm + 16 * (q >> 2) + 4 * (q & 3) + (lane >> 4);  // pass q / 4, row group q % 4
+            rr_pre[q] = nc < N ? rtab[tr] : -1;
+            pv_pre[q] = rr_pre[q] >= 0 ? *reinterpret_cast<const v4f*>(&e.res[(int64_t)rr_pre[q] * N + nc])
+                                       : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
     load_blk(st0, 0, f0);
     load_blk(st0, 1, f1);
     load_dw(st0, dw);
@@ -557,7 +575,10 @@ __global__ __launch_bounds__(NT8, 2) void mmq8_kernel(const Mmq8Args p, const Mm
                     tnv[j] = rtab[TM + tr];
                     if (ql.rope && cv && m0 + tr < M) pvv[j] = *reinterpret_cast<const v4f*>(&e.rope[(int64_t)tnv[j] * e.hd + ql.d]);
                 }
-                if (EPI == MMQ_EPI_RESIDUAL) {
+                if (EPI == MMQ_EPI_RESIDUAL && PRE) {
+                    rrv[j] = rr_pre[PRE ? (mp * 4 + c0 + j) & 7 : 0];
+                    pvv[j] = pv_pre[PRE ? (mp * 4 + c0 + j) & 7 : 0];
+                } else if (EPI == MMQ_EPI_RESIDUAL) {
                     rrv[j] = cv ? rtab[tr] : -1;
                     if (rrv[j] >= 0) pvv[j] = *reinterpret_cast<const v4f*>(&e.res[(int64_t)rrv[j] * N + nc]);
                 }
