@@ -507,6 +507,25 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
         }
     };
 
+    // F16 weights, residual epilogue: the thread's sixteen residual float4 (the epilogue's rows
+    // and columns below) are loaded before the first stage's DMA, so their latency passes
+    // under the K loop instead of being paid per group of rows after it (80 VGPRs, which the
+    // quantized types' fragments leave no room for).  Issued ahead of the stage DMAs they
+    // complete before stage 0 by the in-order vmcnt, so the K loop's waits are unchanged;
+    // each element is read and later written by this thread only (in place is safe).
+    constexpr bool PRE = EPI == MMQ_EPI_RESIDUAL && WT == T_F16;
+    int rr_pre[PRE ? 16 : 1];
+    v4f xs_pre[PRE ? 16 : 1];
+    if (PRE) {
+        const int nc = n0 + 4 * (tid % (BN / 4));
+#pragma unroll
+        for (int q = 0; q < (PRE ? 16 : 1); ++q) {
+            const int m = m0 + (q >> 3) * 64 + (q & 7) * (NT / (BN / 4)) + tid / (BN / 4);
+            rr_pre[q] = m < M && nc < N ? map_row32(e.map, m) : -1;
+            xs_pre[q] = rr_pre[q] >= 0 ? *reinterpret_cast<const v4f*>(&e.res[(int64_t)rr_pre[q] * N + nc])
+                                       : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
     dma_stage(0, st0);
     if (nstage > 1) dma_stage(1, st1);
     for (int s = 0; s < nstage; s += 3) {
@@ -605,6 +624,11 @@ __global__ __launch_bounds__(NT, 2) void mmq_kernel(const MmqArgs p, const MmqEp
                 v4f xs[4];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
+                    if (PRE) {
+                        rr[k] = rr_pre[PRE ? half * 8 + i0 + k : 0];
+                        xs[k] = xs_pre[PRE ? half * 8 + i0 + k : 0];
+                        continue;
+                    }
                     const int m = m0 + half * 64 + (i0 + k) * (NT / CPR) + tid / CPR;
                     rr[k] = m < M && cv ? map_row32(e.map, m) : -1;
                     xs[k] = rr[k] >= 0 ? *reinterpret_cast<const v4f*>(&e.res[(int64_t)rr[k] * N + nc])
