@@ -141,6 +141,12 @@ __device__ __forceinline__ double lane_swap_d(double v) {
     return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
 }
 
+// LDS staging of a 32x32 fp32 MFMA tile in 1024 floats: rows 2k and 2k + 1 share the 64
+// floats (one line of the 64 4-byte banks) at 64 k, row r in half (r ^ r >> 2) & 1, so a write
+// of one accumulator element (lanes 0..31 row R, lanes 32..63 row R + 4) and each 16-lane
+// quarter of a float4 row read (rows 2k, 2k + 1) cover all 64 banks.
+__device__ __forceinline__ int tile32_row(int r) { return 64 * (r >> 1) + 32 * ((r ^ (r >> 2)) & 1); }
+
 // Butterfly max / integer sum across `width` consecutive aligned lanes (a power of two
 // <= 64); exact, so the lane order does not matter.
 template <int width>

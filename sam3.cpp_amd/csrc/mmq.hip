@@ -962,18 +962,18 @@ __global__ __launch_bounds__(256, 2) void mmq_skinny_kernel(const SkinnyArgs p) 
                 }
             }
         }
-        // 32x32 tiles through this wavefront's staging area: rows of 32 floats go out as
-        // eight float4 (one 128-byte line per row)
+        // 32x32 tiles through this wavefront's staging area (tile32_row): rows of 32 floats go
+        // out as eight float4 (one 128-byte line per row)
         const int rr = lane >> 3, cc = 4 * (lane & 7), nc = 32 * j + cc;
 #pragma unroll
         for (int mt = 0; mt < SMT; ++mt) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) stg[(8 * (i >> 2) + 4 * g + (i & 3)) * 32 + lr] = acc[mt][i];
+            for (int i = 0; i < 16; ++i) stg[tile32_row(8 * (i >> 2) + 4 * g + (i & 3)) + lr] = acc[mt][i];
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int m = m0 + mt * 32 + 8 * q + rr;
-                const v4f val = *reinterpret_cast<const v4f*>(&stg[(8 * q + rr) * 32 + cc]);
+                const v4f val = *reinterpret_cast<const v4f*>(&stg[tile32_row(8 * q + rr) + cc]);
                 if (m < M) {
                     float* dst = reinterpret_cast<float*>(reinterpret_cast<char*>(p.D) + (int64_t)m * p.d_nb1) + nc;
                     if (v4 && nc + 4 <= N) {

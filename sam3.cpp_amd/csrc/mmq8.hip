@@ -769,14 +769,13 @@ int mmq8_ksplit(int64_t M, int64_t N, int64_t K, int cus) {
 // by conversion here, which frees the tiled kernel's bias registers; both are exact).
 // npw n-tiles per wavefront, sized by the host for about four wavefronts per SIMD.
 namespace {
-constexpr int SK8_TP = 36;   // staging row pitch (floats): 32 columns + 4
 constexpr int SK8_WPS = 4;   // wavefronts per SIMD the registers allow
 }  // namespace
 
 template <int WT, int EPI>
 __global__ __launch_bounds__(256, SK8_WPS) void mmq8_skinny_kernel(const Mmq8Args p, const MmqEpi e, int npw) {
     constexpr bool Q41 = WT == T_Q4_1;
-    __shared__ __attribute__((aligned(16))) float stg_all[4][32 * SK8_TP];
+    __shared__ __attribute__((aligned(16))) float stg_all[4][32 * 32];
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lr = lane & 31, g = lane >> 5;
     const int M = p.M, N = p.N, ntn = (N + 31) / 32, ngr = (ntn + npw - 1) / npw;
@@ -859,7 +858,7 @@ __global__ __launch_bounds__(256, SK8_WPS) void mmq8_skinny_kernel(const Mmq8Arg
         }
         // the tile through this wavefront's staging: element i is row 8 (i >> 2) + 4 g + (i & 3)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) stg[(8 * (i >> 2) + 4 * g + (i & 3)) * SK8_TP + lr] = acc[i];
+        for (int i = 0; i < 16; ++i) stg[tile32_row(8 * (i >> 2) + 4 * g + (i & 3)) + lr] = acc[i];
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wavefront's LDS writes are done
         __builtin_amdgcn_wave_barrier();
         const int nc = 32 * j + 4 * c4;
@@ -888,7 +887,7 @@ __global__ __launch_bounds__(256, SK8_WPS) void mmq8_skinny_kernel(const Mmq8Arg
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int r = 8 * q + rl, m = m0 + r;
-            const v4f v = *reinterpret_cast<const v4f*>(&stg[r * SK8_TP + 4 * c4]);
+            const v4f v = *reinterpret_cast<const v4f*>(&stg[tile32_row(r) + 4 * c4]);
             if (m >= M || !cv) continue;
             epi4<EPI>(reinterpret_cast<char*>(p.D), p.d_nb1, e, N, m, nc, v, bv, rrv[q], ql, bwv[q], tnv[q], pvv[q]);
         }
