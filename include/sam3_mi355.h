@@ -519,8 +519,12 @@ mi355_status mi355_context_set_fusion(mi355_context* ctx, int enable);
  * activation rows (SAM2 Hiera's stage-1 projections, K = 96) run on a kernel
  * that keeps the whole weight matrix in LDS and streams the activation rows;
  * it computes every output with the tiled kernel's instruction sequence, so
- * both give the same bits.  Off routes them to the tiled kernel (for
- * comparisons).  The int8 route serves these shapes with 64-row tiles. */
+ * both give the same bits.  On the int8 route (prepared weights, and Q8_0 /
+ * Q4_0 under MI355_MMQ_AUTO) the same shapes (N % 4 == 0, no K split) run on
+ * an int8 skinny kernel that keeps each wavefront's activation fragments in
+ * registers and reads the small weight matrix from L2, again bit-identical to
+ * the tiled int8 kernel.  Off routes both to the tiled kernels (for
+ * comparisons). */
 mi355_status mi355_context_set_skinny(mi355_context* ctx, int enable);
 
 /* The kernel behind 2-D MUL_MATs with Q8_0 / Q4_0 / Q4_1 weights in the
