@@ -50,8 +50,11 @@ __device__ __forceinline__ const float* ln_addend(const LnArgs& a, int64_t r) {
 
 // ln_group_kernel at E = 1024: one wavefront per row, lane l holding the 16 consecutive
 // values 16l .. 16l + 15 (half a 32-block), so the operand's blocks are quantized by lane
-// pairs (act_store_half16) instead of groups of eight lanes
-__global__ __launch_bounds__(256) void ln1024_kernel(const LnArgs a) {
+// pairs (act_store_half16) instead of groups of eight lanes.  MODE >= 0 fixes the output
+// mode at compile time (the int8 and F16 operands of the encoders), -1 reads a.out.mode.
+template <int MODE>
+__global__ __launch_bounds__(256) void ln1024_kernel(LnArgs a) {
+    if (MODE >= 0) a.out.mode = MODE;
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= a.rows) return;
     const int l = threadIdx.x & 63;
@@ -79,10 +82,11 @@ __global__ __launch_bounds__(256) void ln1024_kernel(const LnArgs a) {
 // p_{ks-1}) + bias) with mmq_reduce_kernel's adds in its order, written back, then that row's
 // LayerNorm into a.out as ln1024_kernel computes it (a.x is this x, no addend): the bits of
 // the two passes, without reading x back.
-template <int KS>
+template <int KS, int MODE>
 __global__ __launch_bounds__(256) void reduce_residual_ln1024_kernel(const float* __restrict__ part,
                                                                      const float* __restrict__ bias, float* x,
-                                                                     const LnArgs a) {
+                                                                     LnArgs a) {
+    if (MODE >= 0) a.out.mode = MODE;
     const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= a.rows) return;
     const int l = threadIdx.x & 63;
@@ -399,9 +403,12 @@ hipError_t launch_reduce_residual_ln1024(const float* part, int ks, const float*
     if (a.rows <= 0) return hipSuccess;
     if (a.E != 1024 || a.x != x || a.add || ks < 2 || ks > 4 || !part || !bias) return hipErrorInvalidValue;
     const unsigned g = blocks_for(a.rows, 4);
-    if (ks == 2) reduce_residual_ln1024_kernel<2><<<g, 256, 0, st>>>(part, bias, x, a);
-    else if (ks == 3) reduce_residual_ln1024_kernel<3><<<g, 256, 0, st>>>(part, bias, x, a);
-    else reduce_residual_ln1024_kernel<4><<<g, 256, 0, st>>>(part, bias, x, a);
+    const int m = a.out.mode;
+    if (ks == 3 && m == ACT_I8) reduce_residual_ln1024_kernel<3, ACT_I8><<<g, 256, 0, st>>>(part, bias, x, a);
+    else if (ks == 3 && m == ACT_F16) reduce_residual_ln1024_kernel<3, ACT_F16><<<g, 256, 0, st>>>(part, bias, x, a);
+    else if (ks == 2) reduce_residual_ln1024_kernel<2, -1><<<g, 256, 0, st>>>(part, bias, x, a);
+    else if (ks == 3) reduce_residual_ln1024_kernel<3, -1><<<g, 256, 0, st>>>(part, bias, x, a);
+    else reduce_residual_ln1024_kernel<4, -1><<<g, 256, 0, st>>>(part, bias, x, a);
     return hipGetLastError();
 }
 
@@ -409,7 +416,10 @@ hipError_t launch_layer_norm(const LnArgs& a, hipStream_t st) {
     if (a.rows <= 0) return hipSuccess;
     if (a.E % 64 != 0 || a.E > 2048) return hipErrorInvalidValue;
     if (a.E == 1024) {
-        ln1024_kernel<<<blocks_for(a.rows, 4), 256, 0, st>>>(a);
+        const unsigned g = blocks_for(a.rows, 4);
+        if (a.out.mode == ACT_I8) ln1024_kernel<ACT_I8><<<g, 256, 0, st>>>(a);
+        else if (a.out.mode == ACT_F16) ln1024_kernel<ACT_F16><<<g, 256, 0, st>>>(a);
+        else ln1024_kernel<-1><<<g, 256, 0, st>>>(a);
         return hipGetLastError();
     }
     int G, V;  // E % 64 == 0: G >= 16, so each 32-block's 8 lanes share a row
