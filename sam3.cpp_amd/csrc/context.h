@@ -30,8 +30,10 @@ struct mi355_context {
     std::string last_error;
     // encoder runners: producer passes write the next MUL_MAT's operand
     bool fuse = true;
-    // fp16-route MUL_MATs (F16 weights, ggml-layout Q4_1 under MI355_MMQ_AUTO, MI355_MMQ_F16)
-    // with K <= 128 at large M take the skinny kernel; the int8 route has none
+    // quantized 2-D MUL_MATs with K <= 128 over at least 4096 rows take a skinny kernel: the
+    // fp16 route's (ggml-layout Q4_1 under MI355_MMQ_AUTO, any quantized type under
+    // MI355_MMQ_F16) or the int8 route's (prepared weights, Q8_0 / Q4_0 under AUTO; N % 4 == 0,
+    // no K split); F16 weights stay on the tiled kernel
     bool skinny = true;
     // kernel of 2-D MUL_MATs with block-quantized weights (MI355_MMQ_*)
     int mmq_kernel = MI355_MMQ_AUTO;

@@ -5,7 +5,9 @@ for bit.  Each weight type runs three calls in a row on the shared scratch,
 each smaller than the one before (a split-K GEMM, a skinny K = 96 GEMM, a
 small ragged one), so a later call must not read what an earlier call left;
 and an operand set that needs more scratch than the array holds is
-rejected on the host."""
+rejected on the host.  The K = 96 call reaches the int8 skinny kernel for
+Q8_0 / Q4_0 (the int8 route under MI355_MMQ_AUTO), the fp16 route's skinny
+kernel for Q4_1, and the tiled fp16 kernel for F16."""
 import numpy as np
 import pytest
 import torch
