@@ -22,8 +22,10 @@ __device__ __forceinline__ double wave_sum_dh(double v) {
 // ggml_norm(eps) -> mul(w) -> add(b) over rows of C, G lanes per row (C =
 // 4*G*V), float4 loads.  ws > 0: output rows in window order (padding rows
 // zero) and, when out_img is set, the same rows also in image order.
-template <int V>
-__global__ __launch_bounds__(256) void hiera_ln_group_kernel(const HieraLnArgs a, int G) {
+// MODE >= 0: the output mode of out (and out_img when used) fixed at compile time
+template <int V, int MODE = -1>
+__global__ __launch_bounds__(256) void hiera_ln_group_kernel(HieraLnArgs a, int G) {
+    if (MODE >= 0) a.out.mode = a.out_img.mode = MODE;
     const int64_t r = (int64_t)blockIdx.x * (256 / G) + threadIdx.x / G;
     if (r >= a.rows_out) return;
     const int l = threadIdx.x & (G - 1), C = a.C;
@@ -329,7 +331,15 @@ hipError_t launch_hiera_ln(const HieraLnArgs& a, hipStream_t st) {
     switch (V) {
         case 1: hiera_ln_group_kernel<1><<<nb, 256, 0, st>>>(a, G); break;
         case 2: hiera_ln_group_kernel<2><<<nb, 256, 0, st>>>(a, G); break;
-        case 3: hiera_ln_group_kernel<3><<<nb, 256, 0, st>>>(a, G); break;
+        case 3: {
+            // the encoders' operands (int8 or F16), out_img unused or in the same mode
+            const int m = a.out.mode;
+            const bool one = !(a.ws > 0 && (a.out_img.y || a.out_img.q)) || a.out_img.mode == m;
+            if (one && m == ACT_I8) hiera_ln_group_kernel<3, ACT_I8><<<nb, 256, 0, st>>>(a, G);
+            else if (one && m == ACT_F16) hiera_ln_group_kernel<3, ACT_F16><<<nb, 256, 0, st>>>(a, G);
+            else hiera_ln_group_kernel<3><<<nb, 256, 0, st>>>(a, G);
+            break;
+        }
         case 4: hiera_ln_group_kernel<4><<<nb, 256, 0, st>>>(a, G); break;
         case 5: hiera_ln_group_kernel<5><<<nb, 256, 0, st>>>(a, G); break;
         case 6: hiera_ln_group_kernel<6><<<nb, 256, 0, st>>>(a, G); break;
