@@ -281,9 +281,10 @@ __global__ __launch_bounds__(256) void bias_gelu_act_kernel(const float* __restr
 // ACT 0: gelu_erf (ggml_gelu_erf); 1: gelu_tanh_table (ggml_gelu, fp16-table semantics).
 // total = rows * n / 16 half-blocks (< 2^30, even since n % 32 == 0), lanes 2k and 2k+1
 // hold the two halves of one block and run the same iterations.
-template <int ACT>
+template <int ACT, int MODE = -1>  // MODE >= 0: o.mode fixed at compile time
 __global__ __launch_bounds__(256) void bias_act_i8_kernel(const float* __restrict__ h, const float* __restrict__ b,
-                                                          int rows, int n, const ActOut o) {
+                                                          int rows, int n, ActOut o) {
+    if (MODE >= 0) o.mode = MODE;
     const int hb = n / 16, total = rows * hb, step = (int)(gridDim.x * blockDim.x);
     int t = (int)(blockIdx.x * blockDim.x + threadIdx.x);
     if (t >= total) return;
@@ -357,7 +358,9 @@ hipError_t launch_bias_act_i8(int act, const float* h, const float* b, int64_t r
     // about four half-blocks per thread, but at least 1024 workgroups while there is work for them
     const int64_t wgs = (total + 255) / 256;
     const unsigned grid = (unsigned)std::max<int64_t>(std::min<int64_t>(wgs, 1024), (wgs + 3) / 4);
-    if (act == 0) bias_act_i8_kernel<0><<<grid, 256, 0, st>>>(h, b, (int)rows, n, o);
+    if (act == 0 && o.mode == ACT_I8) bias_act_i8_kernel<0, ACT_I8><<<grid, 256, 0, st>>>(h, b, (int)rows, n, o);
+    else if (act == 0) bias_act_i8_kernel<0><<<grid, 256, 0, st>>>(h, b, (int)rows, n, o);
+    else if (o.mode == ACT_I8) bias_act_i8_kernel<1, ACT_I8><<<grid, 256, 0, st>>>(h, b, (int)rows, n, o);
     else bias_act_i8_kernel<1><<<grid, 256, 0, st>>>(h, b, (int)rows, n, o);
     return hipGetLastError();
 }
