@@ -222,6 +222,153 @@ __global__ __launch_bounds__(256, 2) void conv_f16_kernel(const float* __restric
     }
 }
 
+// conv_f16_kernel's implicit GEMM with its operands staged by LDS DMA (buffer_load ... lds):
+// per 32-deep K step the fp32 map rows (128 bytes of one tap's channel slice per output
+// pixel, zero by the buffer's range check outside the image or past M) and the fp16 weight
+// rows (64 bytes), two stage buffers (48 KB: three workgroups per CU; three buffers filled
+// two stages ahead left two per CU and measured slower), no staging registers.  The
+// map is rounded to fp16 (RNE, f2h) as the MFMA fragments are read from LDS: the operands,
+// products and accumulation order of conv_f16_kernel, so the same bits.
+// LDS rows: map rows of 8 chunks of 16 bytes, chunk c of row r in slot c ^ ((r >> 1) & 7),
+// so the 16 rows of a ds_read_b128 quarter (rows of two parities) cover all 64 banks;
+// weight rows as conv_f16_kernel's (csw<4>).
+namespace {
+struct ConvDmaStage {
+    float A[CT * 32];     // 128 map rows x 32 channels, fp32
+    uint16_t B[CT * 32];  // 128 weight rows x 32 K, fp16
+};
+constexpr int CONV_OOB = 0x7ffffff0;
+constexpr int CONV_NB = 2;  // stage buffers  // a buffer offset past every operand the launcher admits
+__device__ __forceinline__ int aswz(int r) { return (r >> 1) & 7; }
+}  // namespace
+
+template <int TAPS, int NB>
+__global__ __launch_bounds__(256, NB == 3 ? 2 : 3) void conv_f16_dma_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
+                                                              const float* __restrict__ bias, int H, int W, int C, int N,
+                                                              int gelu, float* __restrict__ y) {
+    constexpr int NL = 6;  // DMA instructions per wavefront and stage: 4 map, 2 weight
+    __shared__ __attribute__((aligned(16))) ConvDmaStage sb[NB];
+    const int M = H * W, K = TAPS == 9 ? 9 * C : C, cps = C / 32;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wv & 1, wn = wv >> 1;
+    const int lr = lane & 31, g = lane >> 5;
+    // XCD-aware tile order (each XCD a contiguous band of tiles)
+    const int tiles_n = (N + CT - 1) / CT, tiles = ((M + CT - 1) / CT) * tiles_n;
+    const int per_xcd = (tiles + 7) / 8;
+    const int tl = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tl >= tiles) return;
+    const int m0 = (tl / tiles_n) * CT, n0 = (tl % tiles_n) * CT;
+
+    // map DMA instruction j of wavefront wv: tile rows 8 (4 wv + j) + lane / 8, LDS slot lane % 8,
+    // global chunk slot ^ aswz(row); weight instruction j: rows 16 (2 wv + j) + lane / 4, slot lane % 4
+    const v4i xr = make_rsrc(x, (int64_t)M * C * 4), wr = make_rsrc(w, (int64_t)N * K * 2);
+    int py[4], px[4], ach[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = 8 * (4 * wv + j) + (lane >> 3), p = m0 + row;
+        py[j] = p < M ? p / W : -(1 << 20);  // past M: every tap lands outside the image
+        px[j] = p < M ? p - (p / W) * W : 0;
+        ach[j] = (((lane & 7) ^ aswz(row)) << 4);
+    }
+    int woff[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int row = 16 * (2 * wv + j) + (lane >> 2), n = n0 + row;
+        woff[j] = n < N ? n * K * 2 + (((lane & 3) ^ csw<4>(row)) << 4) : CONV_OOB;
+    }
+    uint32_t lb[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) lb[i] = (uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(&sb[i]));
+    auto dma = [&](int s, uint32_t base) __attribute__((always_inline)) {
+        const int tap = TAPS == 9 ? s / cps : 0, c0 = (s - tap * cps) * 32;
+        const int dy = TAPS == 9 ? tap / 3 - 1 : 0, dx = TAPS == 9 ? tap % 3 - 1 : 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int iy = py[j] + dy, ix = px[j] + dx;
+            const bool in = iy >= 0 && iy < H && ix >= 0 && ix < W;
+            const int off = in ? ((iy * W + ix) * C + c0) * 4 + ach[j] : CONV_OOB;
+            dma_b128_so(xr, base + (uint32_t)offsetof(ConvDmaStage, A) + 1024u * (4 * wv + j), off, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            dma_b128_so(wr, base + (uint32_t)offsetof(ConvDmaStage, B) + 1024u * (2 * wv + j), woff[j], s * 64);
+    };
+
+    const v16f zf = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    v16f acc[2][2] = {{zf, zf}, {zf, zf}};
+    auto compute = [&](const ConvDmaStage& b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            v8h a[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int ra = wm * 64 + i * 32 + lr, rb = wn * 64 + i * 32 + lr;
+                const int c = 4 * kk + 2 * g;  // the lane's 8 channels: chunks c, c + 1 of its map row
+                const v4f lo = *reinterpret_cast<const v4f*>(&b.A[ra * 32 + ((c ^ aswz(ra)) << 2)]);
+                const v4f hi = *reinterpret_cast<const v4f*>(&b.A[ra * 32 + (((c + 1) ^ aswz(ra)) << 2)]);
+                const uint4 q = {(uint32_t)f2h(lo[0]) | ((uint32_t)f2h(lo[1]) << 16), (uint32_t)f2h(lo[2]) | ((uint32_t)f2h(lo[3]) << 16),
+                                 (uint32_t)f2h(hi[0]) | ((uint32_t)f2h(hi[1]) << 16), (uint32_t)f2h(hi[2]) | ((uint32_t)f2h(hi[3]) << 16)};
+                a[i] = __builtin_bit_cast(v8h, q);
+                bf[i] = *reinterpret_cast<const v8h*>(&b.B[rb * 32 + (((2 * kk + g) ^ csw<4>(rb)) << 3)]);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    const int nst = K / 32;
+    // NB buffers filled NB - 1 stages ahead
+    dma(0, lb[0]);
+    if (nst > 1) dma(1, lb[1]);
+    if (NB == 3 && nst > 2) dma(2, lb[NB - 1]);
+    if (NB == 3 && nst > 2) wait_vmcnt<2 * NL>();
+    else if (nst > 1) wait_vmcnt<NL>();
+    else wait_vmcnt<0>();
+    __syncthreads();
+    for (int s = 0; s < nst; ++s) {
+        const int cb = s % NB;
+        compute(sb[cb]);
+        if (s + 1 < nst) {
+            if (NB == 3 && s + 2 < nst) wait_vmcnt<NL>();  // stage s + 1 has landed (s + 2 may be in flight)
+            else wait_vmcnt<0>();
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // and stage s's buffer is read
+            if (s + NB < nst) dma(s + NB, lb[cb]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn * 64 + j * 32 + lr;
+        if (n >= N) continue;
+        if (TAPS == 4) {
+            const int Cout = N >> 2, t = n / Cout, co = n - t * Cout;
+            const float bv = bias[co];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (m >= M) continue;
+                    const int qy = m / W, qx = m - (m / W) * W;
+                    const int64_t pix = (int64_t)(2 * qy + (t >> 1)) * (2 * W) + 2 * qx + (t & 1);
+                    const float sv = acc[i][j][r] + bv;
+                    y[pix * Cout + co] = gelu ? gelu_erf(sv) : sv;
+                }
+        } else {
+            const float bv = bias[n];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (m < M) y[(int64_t)m * N + n] = acc[i][j][r] + bv;
+                }
+        }
+    }
+}
+
 // y[r][c] += b[c], four channels per thread (C % 4 == 0)
 __global__ __launch_bounds__(256) void bias_rows_kernel(float* __restrict__ y, const float* __restrict__ b, int64_t rows,
                                                         int C) {
@@ -296,6 +443,13 @@ hipError_t launch_conv_f16(int taps, const float* x, const uint16_t* w, const fl
     const int tiles = (int)(((M + CT - 1) / CT) * ((N + CT - 1) / CT));
     const unsigned grid = (unsigned)((tiles + 7) / 8 * 8);
     const int gl = gelu ? 1 : 0;
+    // operands the DMA kernel's 32-bit buffer offsets reach (with the out-of-range offset above)
+    if ((int64_t)M * C * 4 < CONV_OOB - 4096 && (int64_t)N * (taps == 9 ? 9 : 1) * C * 2 < CONV_OOB - 4096) {
+        if (taps == 9) conv_f16_dma_kernel<9, CONV_NB><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
+        else if (taps == 4) conv_f16_dma_kernel<4, CONV_NB><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
+        else conv_f16_dma_kernel<1, CONV_NB><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
+        return hipGetLastError();
+    }
     // K step 32: a 64-deep step (64 KB of LDS, two workgroups per CU) measured slower
     if (taps == 9)
         conv_f16_kernel<9, 32><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
