@@ -340,14 +340,16 @@ __device__ __forceinline__ void dense_chunk(const ActOut& o, int i, v4f x) {
         reinterpret_cast<uint2*>(o.q)[i] = make_uint2(h0, h1);
     }
 }
-// Dense rows, two lanes per 32-value block: lane 2j + e holds values 16 e .. 16 e + 15 of
-// its block (half i of the flattened grid, 64 bytes: four 16-byte loads), the pair's max by
+// Rows back to back, two lanes per 32-value block: lane 2j + e holds values 16 e .. 16 e + 15
+// of its block (half i of the flattened grid, 64 bytes: four 16-byte loads), the pair's max by
 // one DPP swap (act_store_half16's arithmetic), 16 quant bytes (or 16 halves) per lane.  A
 // block's division pair is done by two lanes instead of eight, a quarter of the VALU work of
-// the chunk form per byte.
+// the chunk form per byte.  DENSE (an even block count per row, no padding slot): the scale
+// slots follow from the flat block index; otherwise the row and block come from div_rcp
+// (rnb = 1 / blocks per row) and act_store_scale writes the slots and the padding.
 constexpr int HF_U = 2;
-template <int MODE>
-__device__ __forceinline__ void dense_half(const ActOut& o, int i, const v4f (&xv)[4]) {
+template <int MODE, bool DENSE>
+__device__ __forceinline__ void dense_half(const ActOut& o, int i, const v4f (&xv)[4], int nbpr, double rnb, int64_t K) {
     float x[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) x[j] = xv[j >> 2][j & 3];
@@ -365,7 +367,11 @@ __device__ __forceinline__ void dense_half(const ActOut& o, int i, const v4f (&x
     }
     if (act_has_sums(MODE)) isum += lane_swap<1>(isum);
     const int g = i >> 1;  // the block: row * (K / 32) + block in the row
-    if ((i & 1) == 0) {
+    if (!DENSE && (i & 1) == 0) {
+        int b;
+        const int r = div_rcp(g, nbpr, rnb, b);
+        act_store_scale(o, r, K, b, d, isum);
+    } else if ((i & 1) == 0) {
         if (MODE >= ACT_I8) {  // dword g / 2 of dl (even g: low half) or dh (odd g: high half)
             if ((g & 1) == 0) reinterpret_cast<uint32_t*>(o.d)[g >> 1] = (uint32_t)f2h(d);
             else o.dh[g >> 1] = (uint32_t)f2h(d) << 16;
@@ -391,8 +397,9 @@ __device__ __forceinline__ void dense_half(const ActOut& o, int i, const v4f (&x
     }
 }
 // thread t of workgroup b: halves (b HF_U + u) 256 + t, u < HF_U (nh halves, nh even)
-template <int MODE>
-__global__ __launch_bounds__(256) void quantize_halves_kernel(const char* __restrict__ src, int nh, ActOut o) {
+template <int MODE, bool DENSE>
+__global__ __launch_bounds__(256) void quantize_halves_kernel(const char* __restrict__ src, int nh, ActOut o, int nbpr,
+                                                              double rnb, int64_t K) {
     o.mode = MODE;
     const int i0 = blockIdx.x * (256 * HF_U) + threadIdx.x;
     v4f x[HF_U][4];
@@ -405,7 +412,7 @@ __global__ __launch_bounds__(256) void quantize_halves_kernel(const char* __rest
 #pragma unroll
     for (int u = 0; u < HF_U; ++u) {
         if (i0 + 256 * u >= nh) break;
-        dense_half<MODE>(o, i0 + 256 * u, x[u]);
+        dense_half<MODE, DENSE>(o, i0 + 256 * u, x[u], nbpr, rnb, K);
     }
 }
 template <int MODE, bool DENSE>
@@ -498,10 +505,14 @@ static dim3 chunk_grid(int64_t n) { return dim3((unsigned)((n + 256 * CH_U - 1) 
 template <int MODE>
 static void launch_chunks(const SrcView& src, const ActOut& o, int64_t nch, hipStream_t st) {
     const int64_t K = src.ne[0], cpr = K / 4;
-    const bool dense = src.nb[1] == 4 * K && K % 64 == 0 && o.dp == K / 32;
-    if (dense) {
-        const int64_t nh = nch / 4;
-        quantize_halves_kernel<MODE><<<(unsigned)((nh + 256 * HF_U - 1) / (256 * HF_U)), 256, 0, st>>>(src.data, (int)nh, o);
+    if (src.nb[1] == 4 * K) {  // rows back to back: the two-lane form
+        const int64_t nh = nch / 4, nbpr = K / 32;
+        const dim3 grid((unsigned)((nh + 256 * HF_U - 1) / (256 * HF_U)));
+        if (K % 64 == 0 && o.dp == K / 32)
+            quantize_halves_kernel<MODE, true><<<grid, 256, 0, st>>>(src.data, (int)nh, o, (int)nbpr, 0.0, K);
+        else
+            quantize_halves_kernel<MODE, false><<<grid, 256, 0, st>>>(src.data, (int)nh, o, (int)nbpr,
+                                                                      1.0 / (double)nbpr, K);
         return;
     }
     quantize_chunks_kernel<MODE, false><<<chunk_grid(nch), 256, 0, st>>>(src.data, src.nb[1], (int)cpr, (int)nch,
