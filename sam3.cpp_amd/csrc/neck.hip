@@ -1,8 +1,9 @@
 // SAM3 SimpleFPN neck kernels (sam3_build_neck_graph, sam3.cpp:3867-3925) on
-// token-major activations [H*W][C] (ggml [C, W, H]).  conv_f16_kernel is the
-// fp16-MFMA implicit GEMM of the F16-kernel convolutions (3x3, 1x1 and the
-// 2x2 / stride-2 conv-transpose with its scatter, bias and GELU in the
-// epilogue); F32-kernel convolutions run on gemm_f32.hip.  The rest are
+// token-major activations [H*W][C] (ggml [C, W, H]).  conv_f16_dma_kernel (and
+// conv_f16_kernel, its register-staged form for operands beyond 32-bit buffer
+// offsets) is the fp16-MFMA implicit GEMM of the F16-kernel convolutions (3x3,
+// 1x1 and the 2x2 / stride-2 conv-transpose with its scatter, bias and GELU in
+// the epilogue); F32-kernel convolutions run on gemm_f32.hip.  The rest are
 // HBM-bound passes: the conv-transpose kernel repack + F16 cast, the 3x3
 // kernel repacks for the implicit GEMMs, and, for maps the implicit GEMMs do
 // not take, im2col, the conv-transpose scatter and bias adds; the 2x2
