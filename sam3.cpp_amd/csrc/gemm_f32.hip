@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const GemmF32Args p) {
 }
 
 template <bool CONV>
-__global__ __launch_bounds__(256, 2) void gemm_f32_tiled_kernel(const GemmF32Args p) {
+__global__ __launch_bounds__(256, 2) void gemm_f32_tiled_kernel(const GemmF32Args p, int ksplit, int sps) {
     __shared__ __attribute__((aligned(16))) float sA[2][TM * TP];
     __shared__ __attribute__((aligned(16))) float sB[2][TN * TP];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -81,10 +81,13 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_tiled_kernel(const GemmF32Arg
     // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs, so
     // workgroup b works tile (b % 8) * per_xcd + b / 8 and each XCD walks a contiguous
     // band of tiles (the n-tiles of one m-tile share its activation rows in one L2)
+    // band of tiles. With a K split, the split is the slowest index: workgroup slot
+    // (split, tile), its K range stages [split * sps, (split + 1) * sps)
     const int tiles_n = (p.N + TN - 1) / TN, tiles = ((p.M + TM - 1) / TM) * tiles_n;
-    const int per_xcd = (tiles + 7) / 8;
-    const int tl = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    if (tl >= tiles) return;
+    const int TT = tiles * ksplit, per_xcd = (TT + 7) / 8;
+    const int tls = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tls >= TT) return;
+    const int split = tls / tiles, tl = tls - split * tiles;
     const int m0 = (tl / tiles_n) * TM, n0 = (tl % tiles_n) * TN;
     const int z = blockIdx.y, i12 = z % p.ne12, i13 = z / p.ne12;
     const char* Wb = reinterpret_cast<const char*>(p.W) + (int64_t)(i12 / p.r2) * p.w_nb2 + (int64_t)(i13 / p.r3) * p.w_nb3;
@@ -141,13 +144,14 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_tiled_kernel(const GemmF32Arg
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const int nst = (p.K + TK - 1) / TK;
-    load(0);
+    const int kb = split * sps * TK;
+    const int nst = min((p.K - kb + TK - 1) / TK, sps);
+    load(kb);
     park(0);
     __syncthreads();
     for (int s = 0; s < nst; ++s) {
         const int buf = s & 1;
-        if (s + 1 < nst) load((s + 1) * TK);
+        if (s + 1 < nst) load(kb + (s + 1) * TK);
         v4f av[2][4], bv[2][4];  // this lane's 16 k values of its row (k-slot g), per tile
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -171,6 +175,22 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_tiled_kernel(const GemmF32Arg
         __syncthreads();
     }
 
+    if (ksplit > 1) {  // this split's partial sums, no bias: part [split][M][N]
+        float* P = p.part + (int64_t)split * p.M * p.N;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = n0 + wn * 64 + j * 32 + lr;
+            if (n >= p.N) continue;
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (m < p.M) P[(int64_t)m * p.N + n] = acc[i][j][r];
+                }
+        }
+        return;
+    }
     char* D = reinterpret_cast<char*>(p.D) + (int64_t)i12 * p.d_nb2 + (int64_t)i13 * p.d_nb3;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -187,27 +207,248 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_tiled_kernel(const GemmF32Arg
     }
 }
 
+// The tiled kernel with its operands staged by LDS DMA (buffer_load ... lds) into NB stage
+// buffers of 32 K values (A and B rows of 128 bytes, 32 KB per stage), filled NB - 1 stages
+// ahead, so no registers stage anything and no branch guards a load: rows past M or N,
+// taps outside the image and the chunks of a last partial stage past K get an offset past
+// the buffer's records, which reads zero. Rows hold chunk c (k values 4c .. 4c + 3) in slot
+// c ^ fswz(r), so the 16 rows of a ds_read_b128 quarter (two parities of eight rows) cover
+// the 64 banks. Lane group g of a fragment read takes chunks 2q + g (q < 4), and MFMA step
+// (q, e) pairs k = 8q + e (lanes 0..31) with 8q + 4 + e (lanes 32..63) in A and B alike:
+// every k of the stage once, in fp32 products and fp32 accumulation as before (the k order
+// inside a stage differs from the tiled kernel's, so sums may differ in the last bits).
+namespace {
+constexpr int F32_OOB = 0x7ffffff0;  // a buffer offset past every operand the launcher admits
+__device__ __forceinline__ int fswz(int r) { return (r >> 1) & 7; }
+struct F32Stage {
+    float A[TM * TK];
+    float B[TN * TK];
+};
+}  // namespace
+
+template <bool CONV, int NB>
+__global__ __launch_bounds__(256, NB == 2 ? 2 : 1) void gemm_f32_dma_kernel(const GemmF32Args p, int ksplit, int sps) {
+    constexpr int NL = 8;  // DMA instructions per wavefront and stage: 4 A, 4 B
+    __shared__ __attribute__((aligned(16))) F32Stage sb[NB];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wv & 1, wn = wv >> 1;
+    const int lr = lane & 31, g = lane >> 5;
+    // XCD-aware order with the K split as the slowest index, as the tiled kernel
+    const int M = p.M, N = p.N, K = p.K;
+    const int tiles_n = (N + TN - 1) / TN, tiles = ((M + TM - 1) / TM) * tiles_n;
+    const int TT = tiles * ksplit, per_xcd = (TT + 7) / 8;
+    const int tls = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tls >= TT) return;
+    const int split = tls / tiles, tl = tls - split * tiles;
+    const int m0 = (tl / tiles_n) * TM, n0 = (tl % tiles_n) * TN;
+    const int z = blockIdx.y, i12 = z % p.ne12, i13 = z / p.ne12;
+    const char* Wb = reinterpret_cast<const char*>(p.W) + (int64_t)(i12 / p.r2) * p.w_nb2 + (int64_t)(i13 / p.r3) * p.w_nb3;
+    const char* Xb = reinterpret_cast<const char*>(p.X) + (int64_t)i12 * p.x_nb2 + (int64_t)i13 * p.x_nb3;
+    const int kb = split * sps * TK;
+    const int nst = min((K - kb + TK - 1) / TK, sps);
+
+    // DMA instruction j (< 4) of wavefront wv: tile rows 8 (4 wv + j) + lane / 8 of A and of B,
+    // LDS slot lane % 8, global chunk slot ^ fswz(row)
+    const v4i xr = make_rsrc(Xb, CONV ? (int64_t)M * p.C * 4 : (int64_t)(M - 1) * p.x_nb1 + 4LL * K);
+    const v4i wr = make_rsrc(Wb, (int64_t)(N - 1) * p.w_nb1 + 4LL * K);
+    int ach[4], aoff[4], boff[4], py[4], px[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = 8 * (4 * wv + j) + (lane >> 3), m = m0 + row, n = n0 + row;
+        ach[j] = (lane & 7) ^ fswz(row);  // the chunk this lane loads
+        py[j] = px[j] = 0;
+        if (CONV) {
+            py[j] = m < M ? m / p.Wd : -(1 << 20);  // past M: every tap lands outside the image
+            px[j] = m < M ? m - (m / p.Wd) * p.Wd : 0;
+        }
+        aoff[j] = m < M ? (int)((int64_t)m * p.x_nb1) + 16 * ach[j] : F32_OOB;
+        boff[j] = n < N ? (int)((int64_t)n * p.w_nb1) + 16 * ach[j] : F32_OOB;
+    }
+    uint32_t lb[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) lb[i] = (uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(&sb[i]));
+    auto dma = [&](int s, uint32_t base) __attribute__((always_inline)) {
+        const int k0 = kb + s * TK;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool kin = k0 + 4 * ach[j] < K;  // false only in a last partial stage
+            int off;
+            if (CONV) {
+                const int tap = k0 / p.C, c0 = k0 - tap * p.C;
+                const int iy = py[j] + tap / 3 - 1, ix = px[j] + tap % 3 - 1;
+                const bool in = iy >= 0 && iy < p.H && ix >= 0 && ix < p.Wd;
+                off = in ? ((iy * p.Wd + ix) * p.C + c0) * 4 + 16 * ach[j] : F32_OOB;
+            } else {
+                off = aoff[j] != F32_OOB && kin ? aoff[j] + 4 * k0 : F32_OOB;
+            }
+            dma_b128_so(xr, base + (uint32_t)offsetof(F32Stage, A) + 1024u * (4 * wv + j), off, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool kin = k0 + 4 * ach[j] < K;
+            const int off = boff[j] != F32_OOB && kin ? boff[j] + 4 * k0 : F32_OOB;
+            dma_b128_so(wr, base + (uint32_t)offsetof(F32Stage, B) + 1024u * (4 * wv + j), off, 0);
+        }
+    };
+
+    const v16f zf = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    v16f acc[2][2] = {{zf, zf}, {zf, zf}};
+    auto compute = [&](const F32Stage& b) __attribute__((always_inline)) {
+        v4f av[4][2], bv[4][2];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int ra = wm * 64 + i * 32 + lr, rb = wn * 64 + i * 32 + lr, c = 2 * q + g;
+                av[q][i] = *reinterpret_cast<const v4f*>(&b.A[ra * TK + ((c ^ fswz(ra)) << 2)]);
+                bv[q][i] = *reinterpret_cast<const v4f*>(&b.B[rb * TK + ((c ^ fswz(rb)) << 2)]);
+            }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][i][e], bv[q][j][e], acc[i][j], 0, 0, 0);
+    };
+
+    // NB buffers filled NB - 1 stages ahead
+    dma(0, lb[0]);
+    if (nst > 1) dma(1, lb[1]);
+    if (NB == 3 && nst > 2) dma(2, lb[NB - 1]);
+    if (NB == 3 && nst > 2) wait_vmcnt<2 * NL>();
+    else if (nst > 1) wait_vmcnt<NL>();
+    else wait_vmcnt<0>();
+    __syncthreads();
+    for (int s = 0; s < nst; ++s) {
+        const int cb = s % NB;
+        compute(sb[cb]);
+        if (s + 1 < nst) {
+            if (NB == 3 && s + 2 < nst) wait_vmcnt<NL>();  // stage s + 1 has landed (s + 2 may be in flight)
+            else wait_vmcnt<0>();
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // and stage s's buffer is read
+            if (s + NB < nst) dma(s + NB, lb[cb]);
+        }
+    }
+
+    if (ksplit > 1) {  // this split's partial sums, no bias: part [split][M][N]
+        float* P = p.part + (int64_t)split * M * N;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = n0 + wn * 64 + j * 32 + lr;
+            if (n >= N) continue;
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (m < M) P[(int64_t)m * N + n] = acc[i][j][r];
+                }
+        }
+        return;
+    }
+    char* D = reinterpret_cast<char*>(p.D) + (int64_t)i12 * p.d_nb2 + (int64_t)i13 * p.d_nb3;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn * 64 + j * 32 + lr;
+        if (n >= N) continue;
+        const float bn = p.bias ? p.bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                if (m < M) *reinterpret_cast<float*>(D + (int64_t)m * p.d_nb1 + 4LL * n) = acc[i][j][r] + bn;
+            }
+    }
+}
+
+// D = bias + part[0] + part[1] + ... (in split order) over an M x N tile set, float4 columns
+__global__ __launch_bounds__(256) void gemm_f32_split_reduce_kernel(const float* __restrict__ part, int S, int M, int N,
+                                                                    const float* __restrict__ bias, float* D,
+                                                                    int64_t d_nb1) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int n4 = N / 4;
+    if (t >= (int64_t)M * n4) return;
+    const int64_t m = t / n4;
+    const int c = (int)(t - m * n4) * 4;
+    const int64_t plane = (int64_t)M * N;
+    v4f v = *reinterpret_cast<const v4f*>(part + m * N + c);
+    for (int s = 1; s < S; ++s) v = v + *reinterpret_cast<const v4f*>(part + s * plane + m * N + c);
+    if (bias) v = v + *reinterpret_cast<const v4f*>(bias + c);
+    *reinterpret_cast<v4f*>(reinterpret_cast<char*>(D) + m * d_nb1 + 4LL * c) = v;
+}
+
+namespace {
+// operand extents (bytes) the DMA kernel's 32-bit buffer offsets reach, with room for the
+// out-of-range offset
+bool dma_ok(int64_t x_bytes, int64_t w_bytes) { return x_bytes < F32_OOB - 4096 && w_bytes < F32_OOB - 4096; }
+constexpr int F32_NB = 2;  // stage buffers of the DMA kernel
+// the fp32 MFMA kernels split grids below two tiles per CU; one 32-deep stage of a
+// 128 x 128 tile takes about 2.5 us alone on a CU
+int f32_ksplit(int64_t M, int64_t N, int64_t K) {
+    const int64_t tiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
+    return gemm_ksplit(tiles, 512, M, N, (K + TK - 1) / TK, 2.5);
+}
+}  // namespace
+
+size_t gemm_f32_part_bytes(int64_t M, int64_t N, int64_t K) {
+    const int S = f32_ksplit(M, N, K);
+    return S > 1 ? (size_t)S * (size_t)M * (size_t)N * 4 : 0;
+}
+
+hipError_t launch_split_reduce(const float* part, int S, int M, int N, const float* bias, float* D, int64_t d_nb1,
+                               hipStream_t st) {
+    if (N % 4 != 0 || S < 1) return hipErrorInvalidValue;
+    const int64_t n = (int64_t)M * (N / 4);
+    if (n > 0) gemm_f32_split_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(part, S, M, N, bias, D, d_nb1);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm_f32(const GemmF32Args& a, int Z, hipStream_t st) {
     if (a.M <= 0 || a.N <= 0 || Z <= 0) return hipSuccess;
+    const int tiles = ((a.M + TM - 1) / TM) * ((a.N + TN - 1) / TN);
+    // the K split (partials in a.part, then the reduce pass), when the caller gave room for it
+    int S = 1, sps = (a.K + TK - 1) / TK;
+    if (a.part && Z == 1) {
+        const int s = f32_ksplit(a.M, a.N, a.K);
+        if (s > 1 && (size_t)s * (size_t)a.M * (size_t)a.N * 4 <= a.part_bytes) {
+            S = s;
+            sps = (sps + S - 1) / S;
+        }
+    }
+    auto reduce = [&]() -> hipError_t {
+        const hipError_t e = hipGetLastError();
+        if (S == 1 || e != hipSuccess) return e;
+        return launch_split_reduce(a.part, S, a.M, a.N, a.bias, a.D, a.d_nb1, st);
+    };
     if (a.conv) {
         if (a.C % TK != 0 || a.K != 9 * a.C || (int64_t)a.H * a.Wd != a.M || Z != 1 ||
             (reinterpret_cast<uintptr_t>(a.X) & 15) || (reinterpret_cast<uintptr_t>(a.W) & 15) || (a.w_nb1 & 15))
             return hipErrorInvalidValue;
-        const int tiles = ((a.M + TM - 1) / TM) * ((a.N + TN - 1) / TN);
-        gemm_f32_tiled_kernel<true><<<dim3((unsigned)((tiles + 7) / 8 * 8), 1), 256, 0, st>>>(a);
-        return hipGetLastError();
+        if (dma_ok((int64_t)a.M * a.C * 4, (int64_t)(a.N - 1) * a.w_nb1 + 4LL * a.K))
+            gemm_f32_dma_kernel<true, F32_NB><<<dim3((unsigned)((tiles * S + 7) / 8 * 8), 1), 256, 0, st>>>(a, S, sps);
+        else
+            gemm_f32_tiled_kernel<true><<<dim3((unsigned)((tiles * S + 7) / 8 * 8), 1), 256, 0, st>>>(a, S, sps);
+        return reduce();
     }
     const bool tiled = a.K % 4 == 0 &&
                        ((reinterpret_cast<uintptr_t>(a.X) | reinterpret_cast<uintptr_t>(a.W) | (uintptr_t)a.x_nb1 |
                          (uintptr_t)a.x_nb2 | (uintptr_t)a.x_nb3 | (uintptr_t)a.w_nb1 | (uintptr_t)a.w_nb2 |
                          (uintptr_t)a.w_nb3) & 15) == 0;
     if (tiled) {
-        const int tiles = ((a.M + TM - 1) / TM) * ((a.N + TN - 1) / TN);
-        gemm_f32_tiled_kernel<false><<<dim3((unsigned)((tiles + 7) / 8 * 8), (unsigned)Z), 256, 0, st>>>(a);
-    } else {
-        const dim3 grid((unsigned)((a.M + GT - 1) / GT), (unsigned)((a.N + GT - 1) / GT), (unsigned)Z);
-        gemm_f32_kernel<<<grid, 256, 0, st>>>(a);
+        // the DMA kernel's 32-bit buffer offsets must reach every operand of every batch
+        if (dma_ok((int64_t)(a.M - 1) * a.x_nb1 + 4LL * a.K, (int64_t)(a.N - 1) * a.w_nb1 + 4LL * a.K))
+            gemm_f32_dma_kernel<false, F32_NB><<<dim3((unsigned)((tiles * S + 7) / 8 * 8), (unsigned)Z), 256, 0, st>>>(a, S, sps);
+        else
+            gemm_f32_tiled_kernel<false><<<dim3((unsigned)((tiles * S + 7) / 8 * 8), (unsigned)Z), 256, 0, st>>>(a, S, sps);
+        return reduce();
     }
+    const dim3 grid((unsigned)((a.M + GT - 1) / GT), (unsigned)((a.N + GT - 1) / GT), (unsigned)Z);
+    gemm_f32_kernel<<<grid, 256, 0, st>>>(a);
     return hipGetLastError();
 }
 

@@ -226,8 +226,41 @@ struct GemmF32Args {
     // implicit 3x3 / stride 1 / pad 1 convolution: X is a token-major map [H*Wd][C], row m
     // of the GEMM is output pixel m, and K = 9*C runs (tap, channel) with W rows in that order
     int conv = 0, H = 0, Wd = 0, C = 0;
+    // K split for grids too small to fill the device (Z == 1 only): when part is given, the
+    // launch may split K into ranges whose fp32 partial sums go to part [split][M][N] (at most
+    // part_bytes) and are then added in split order, with the bias, by a reduce pass
+    float* part = nullptr;
+    size_t part_bytes = 0;
 };
 hipError_t launch_gemm_f32(const GemmF32Args& a, int Z, hipStream_t st);
+// partial-sum bytes launch_gemm_f32 uses for an M x N x K tiled GEMM (0: no K split)
+size_t gemm_f32_part_bytes(int64_t M, int64_t N, int64_t K);
+// D[m][n] = bias[n] + part[0][m][n] + ... + part[S - 1][m][n], added in split order
+// (float4 columns: N % 4 == 0; D row pitch d_nb1 bytes; bias may be null)
+hipError_t launch_split_reduce(const float* part, int S, int M, int N, const float* bias, float* D, int64_t d_nb1,
+                               hipStream_t st);
+
+// K split count of a GEMM of `tiles` 128 x 128 output tiles and nst K stages: grids of `full`
+// tiles or more are not split; smaller ones take the S (at most 16, at least four stages per
+// split, no split left empty) that minimises the busiest CU's stage count, ceil(tiles * S /
+// 256) * ceil(nst / S), plus the reduce (a launch and S + 1 passes over M x N floats at
+// 4 TB/s), in units of stage_us, one stage's time alone on a CU
+inline int gemm_ksplit(int64_t tiles, int64_t full, int64_t M, int64_t N, int64_t nst, double stage_us) {
+    if (tiles >= full || N % 4 != 0) return 1;
+    double best = (double)((tiles + 255) / 256) * (double)nst;
+    int bs = 1;
+    for (int S = 2; S <= 16 && nst >= 4 * S; ++S) {
+        const int64_t sps = (nst + S - 1) / S;
+        if ((nst + sps - 1) / sps != S) continue;
+        const double red = (3.0 + (double)(S + 1) * (double)M * (double)N * 4.0 / 4.0e6) / stage_us;
+        const double c = (double)((tiles * S + 255) / 256) * (double)sps + red;
+        if (c < best) {
+            best = c;
+            bs = S;
+        }
+    }
+    return bs;
+}
 
 // ---- SAM3 ViT glue (rows of E contiguous floats)
 struct LnArgs {
@@ -318,9 +351,14 @@ hipError_t launch_conv3x3_pack(const float* w, int Cin, int Cout, float* out, hi
 hipError_t launch_conv3x3_pack_f16(const uint16_t* w, int Cin, int Cout, uint16_t* out, hipStream_t st);
 // taps: 9 (3x3, kernel packed by launch_conv3x3_pack_f16), 1 (1x1, the kernel as
 // stored) or 4 (2x2 / stride-2 conv-transpose, kernel packed by launch_deconv_pack,
-// N = 4 * Cout, y the 2x map, GELU-erf after the bias if gelu)
+// N = 4 * Cout, y the 2x map, GELU-erf after the bias if gelu). Taps 1 and 9 may split K
+// into ranges whose partial sums go to part [split][M][N] (at most part_bytes; none without
+// part) and are added, with the bias, by launch_split_reduce.
 hipError_t launch_conv_f16(int taps, const float* x, const uint16_t* w, const float* bias, int H, int W, int C, int N,
-                           bool gelu, float* y, hipStream_t st);
+                           bool gelu, float* y, hipStream_t st, float* part = nullptr, size_t part_bytes = 0);
+// partial-sum bytes launch_conv_f16 uses for taps 1 or 9 over M pixels, C input and N output
+// channels (0: no K split)
+size_t conv_f16_part_bytes(int taps, int64_t M, int64_t C, int64_t N);
 hipError_t launch_bias_rows(float* y, const float* b, int64_t rows, int C, hipStream_t st);
 hipError_t launch_maxpool2(const float* x, int H, int W, int C, float* y, hipStream_t st);
 hipError_t launch_hiera_pos_embed(const float* bkg, int E, int bh, int bw, const float* win, int ws, int H, int W,

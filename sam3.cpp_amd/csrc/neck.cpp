@@ -67,11 +67,16 @@ size_t deconv_scratch(int64_t P, int64_t Cin, int64_t Cout) {
 // the implicit-GEMM kernels take maps whose rows are 16-byte aligned with Cin % 32 == 0
 bool implicit_ok(const float* x, int64_t Cin) { return (reinterpret_cast<uintptr_t>(x) & 15) == 0 && Cin % 32 == 0; }
 // implicit 3x3: the kernel repacked to (tap, channel) rows; otherwise the im2col
-// columns in the kernel's type (x_aligned: the map's rows are 16-byte aligned)
+// columns in the kernel's type (x_aligned: the map's rows are 16-byte aligned). The
+// implicit-GEMM kernels' K-split partial sums follow (1x1 and 3x3).
 size_t conv_scratch(int64_t P, int64_t Cin, int64_t Cout, int k, int wtype, bool x_aligned) {
-    if (k == 1) return 0;
+    const bool implicit = x_aligned && Cin % 32 == 0;
+    const size_t part = wtype == T_F32 ? gemm_f32_part_bytes(P, Cout, (int64_t)k * k * Cin)
+                        : implicit     ? conv_f16_part_bytes(k * k, P, Cin, Cout)
+                                       : 0;
+    if (k == 1) return part;
     const int64_t es = wtype == T_F32 ? 4 : 2;
-    if (x_aligned && Cin % 32 == 0) return align_up((size_t)(9 * Cin * Cout * es));
+    if (x_aligned && Cin % 32 == 0) return align_up((size_t)(9 * Cin * Cout * es)) + part;
     return align_up((size_t)(P * 9 * Cin * es));
 }
 
@@ -131,6 +136,9 @@ mi355_status conv(mi355_context* ctx, const mi355_tensor* w, const float* b, con
         }
         GemmF32Args g;
         g.W = k == 3 ? reinterpret_cast<const float*>(scratch) : static_cast<const float*>(w->data);
+        // the K split's partial sums follow the repacked kernel
+        g.part = reinterpret_cast<float*>(scratch + (k == 3 ? align_up((size_t)(K * Cout * 4)) : 0));
+        g.part_bytes = gemm_f32_part_bytes(P, Cout, K);
         g.w_nb1 = 4 * K;
         g.w_nb2 = g.w_nb3 = 4 * K * Cout;
         g.X = x;
@@ -162,8 +170,11 @@ mi355_status conv(mi355_context* ctx, const mi355_tensor* w, const float* b, con
             if (st != MI355_STATUS_SUCCESS) return st;
         }
         const uint16_t* wk = k == 3 ? reinterpret_cast<const uint16_t*>(scratch) : static_cast<const uint16_t*>(w->data);
+        // the K split's partial sums follow the repacked kernel
+        float* part = reinterpret_cast<float*>(scratch + (k == 3 ? align_up((size_t)(K * Cout * 2)) : 0));
         Timed t(ctx, k == 3 ? "neck_conv3x3_f16" : "neck_conv1x1_f16");
-        return hip_check(ctx, t.done(launch_conv_f16(k * k, x, wk, b, H, W, Cin, Cout, false, y, ctx->stream)),
+        return hip_check(ctx, t.done(launch_conv_f16(k * k, x, wk, b, H, W, Cin, Cout, false, y, ctx->stream, part,
+                                                     conv_f16_part_bytes(k * k, P, Cin, Cout))),
                          "conv_f16 launch");
     }
     const mi355_tensor s0 = dev_t(w->data, w->type, K, Cout), d = dev_t(y, T_F32, Cout, P);
@@ -215,18 +226,22 @@ bool neck_plan(int E, int G, const mi355_neck_scale* s, NeckPlan* pl) {
     mapb(16 * G2, s[0].conv1x1_w->ne[3]);
     scr(deconv_scratch(G2, E, C1));
     scr(deconv_scratch(4 * G2, C1, D0));
+    scr(conv_scratch(16 * G2, s[0].conv1x1_w->ne[2], s[0].conv1x1_w->ne[3], 1, s[0].conv1x1_w->type, true));
     scr(conv_scratch(16 * G2, s[0].conv3x3_w->ne[2], s[0].conv3x3_w->ne[3], 3, s[0].conv3x3_w->type, true));
     // scale 1: deconv E->C1 (2G), 1x1, 3x3
     const int64_t C1b = s[1].deconv1_w->ne[2];
     mapb(4 * G2, C1b);
     mapb(4 * G2, s[1].conv1x1_w->ne[3]);
     scr(deconv_scratch(G2, E, C1b));
+    scr(conv_scratch(4 * G2, s[1].conv1x1_w->ne[2], s[1].conv1x1_w->ne[3], 1, s[1].conv1x1_w->type, true));
     scr(conv_scratch(4 * G2, s[1].conv3x3_w->ne[2], s[1].conv3x3_w->ne[3], 3, s[1].conv3x3_w->type, true));
     // scale 2: 1x1, 3x3 at G; scale 3: pool, 1x1, 3x3 at G/2
     mapb(G2, s[2].conv1x1_w->ne[3]);
+    scr(conv_scratch(G2, s[2].conv1x1_w->ne[2], s[2].conv1x1_w->ne[3], 1, s[2].conv1x1_w->type, true));
     scr(conv_scratch(G2, s[2].conv3x3_w->ne[2], s[2].conv3x3_w->ne[3], 3, s[2].conv3x3_w->type, true));
     mapb(G2 / 4, E);
     mapb(G2 / 4, s[3].conv1x1_w->ne[3]);
+    scr(conv_scratch(G2 / 4, s[3].conv1x1_w->ne[2], s[3].conv1x1_w->ne[3], 1, s[3].conv1x1_w->type, true));
     scr(conv_scratch(G2 / 4, s[3].conv3x3_w->ne[2], s[3].conv3x3_w->ne[3], 3, s[3].conv3x3_w->type, true));
     return true;
 }
@@ -255,7 +270,7 @@ mi355_status mi355_neck_conv(mi355_context* ctx, const mi355_tensor* w, const fl
     (void)hipSetDevice(ctx->device);
     char* scr = nullptr;
     const int k = (int)w->ne[0];
-    const size_t sb = k == 3 ? conv_scratch((int64_t)H * W, w->ne[2], w->ne[3], 3, w->type, implicit_ok(x, w->ne[2])) : 0;
+    const size_t sb = conv_scratch((int64_t)H * W, w->ne[2], w->ne[3], k, w->type, implicit_ok(x, w->ne[2]));
     mi355_status st = scratch_for(ctx, sb, &scr);
     if (st != MI355_STATUS_SUCCESS) return st;
     return conv(ctx, w, b, x, H, W, y, scr);

@@ -246,7 +246,8 @@ __device__ __forceinline__ int aswz(int r) { return (r >> 1) & 7; }
 template <int TAPS, int NB>
 __global__ __launch_bounds__(256, NB == 3 ? 2 : 3) void conv_f16_dma_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
                                                               const float* __restrict__ bias, int H, int W, int C, int N,
-                                                              int gelu, float* __restrict__ y) {
+                                                              int gelu, float* __restrict__ y, int ksplit, int sps,
+                                                              float* __restrict__ part) {
     constexpr int NL = 6;  // DMA instructions per wavefront and stage: 4 map, 2 weight
     __shared__ __attribute__((aligned(16))) ConvDmaStage sb[NB];
     const int M = H * W, K = TAPS == 9 ? 9 * C : C, cps = C / 32;
@@ -254,11 +255,13 @@ __global__ __launch_bounds__(256, NB == 3 ? 2 : 3) void conv_f16_dma_kernel(cons
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wv & 1, wn = wv >> 1;
     const int lr = lane & 31, g = lane >> 5;
-    // XCD-aware tile order (each XCD a contiguous band of tiles)
+    // XCD-aware tile order (each XCD a contiguous band of tiles); with a K split (taps 1 and
+    // 9) the split is the slowest index: slot (split, tile) runs stages [split * sps, + sps)
     const int tiles_n = (N + CT - 1) / CT, tiles = ((M + CT - 1) / CT) * tiles_n;
-    const int per_xcd = (tiles + 7) / 8;
-    const int tl = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    if (tl >= tiles) return;
+    const int TT = tiles * ksplit, per_xcd = (TT + 7) / 8;
+    const int tls = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (tls >= TT) return;
+    const int split = tls / tiles, tl = tls - split * tiles;
     const int m0 = (tl / tiles_n) * CT, n0 = (tl % tiles_n) * CT;
 
     // map DMA instruction j of wavefront wv: tile rows 8 (4 wv + j) + lane / 8, LDS slot lane % 8,
@@ -320,11 +323,11 @@ __global__ __launch_bounds__(256, NB == 3 ? 2 : 3) void conv_f16_dma_kernel(cons
         }
     };
 
-    const int nst = K / 32;
+    const int s0 = split * sps, nst = min(K / 32 - s0, sps);  // this split's first stage and stage count
     // NB buffers filled NB - 1 stages ahead
-    dma(0, lb[0]);
-    if (nst > 1) dma(1, lb[1]);
-    if (NB == 3 && nst > 2) dma(2, lb[NB - 1]);
+    dma(s0, lb[0]);
+    if (nst > 1) dma(s0 + 1, lb[1]);
+    if (NB == 3 && nst > 2) dma(s0 + 2, lb[NB - 1]);
     if (NB == 3 && nst > 2) wait_vmcnt<2 * NL>();
     else if (nst > 1) wait_vmcnt<NL>();
     else wait_vmcnt<0>();
@@ -336,8 +339,24 @@ __global__ __launch_bounds__(256, NB == 3 ? 2 : 3) void conv_f16_dma_kernel(cons
             if (NB == 3 && s + 2 < nst) wait_vmcnt<NL>();  // stage s + 1 has landed (s + 2 may be in flight)
             else wait_vmcnt<0>();
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // and stage s's buffer is read
-            if (s + NB < nst) dma(s + NB, lb[cb]);
+            if (s + NB < nst) dma(s0 + s + NB, lb[cb]);
         }
+    }
+    if (TAPS != 4 && ksplit > 1) {  // this split's partial sums, no bias: part [split][M][N]
+        float* P = part + (int64_t)split * M * N;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = n0 + wn * 64 + j * 32 + lr;
+            if (n >= N) continue;
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (m < M) P[(int64_t)m * N + n] = acc[i][j][r];
+                }
+        }
+        return;
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -434,8 +453,27 @@ hipError_t launch_conv3x3_pack_f16(const uint16_t* w, int Cin, int Cout, uint16_
     return hipGetLastError();
 }
 
+namespace {
+// operands the DMA kernel's 32-bit buffer offsets reach (with the out-of-range offset above)
+bool conv_dma_ok(int taps, int64_t M, int64_t C, int64_t N) {
+    return M * C * 4 < CONV_OOB - 4096 && N * (taps == 9 ? 9 : 1) * C * 2 < CONV_OOB - 4096;
+}
+// K split of the DMA kernel (taps 1 and 9): grids below one tile per CU; one 32-deep stage of
+// a tile takes about 0.9 us alone on a CU
+int conv_f16_ksplit(int taps, int64_t M, int64_t C, int64_t N) {
+    if (taps == 4 || !conv_dma_ok(taps, M, C, N)) return 1;
+    const int64_t tiles = ((M + CT - 1) / CT) * ((N + CT - 1) / CT);
+    return gemm_ksplit(tiles, 256, M, N, (taps == 9 ? 9 : 1) * C / 32, 0.9);
+}
+}  // namespace
+
+size_t conv_f16_part_bytes(int taps, int64_t M, int64_t C, int64_t N) {
+    const int S = conv_f16_ksplit(taps, M, C, N);
+    return S > 1 ? (size_t)S * (size_t)M * (size_t)N * 4 : 0;
+}
+
 hipError_t launch_conv_f16(int taps, const float* x, const uint16_t* w, const float* bias, int H, int W, int C, int N,
-                           bool gelu, float* y, hipStream_t st) {
+                           bool gelu, float* y, hipStream_t st, float* part, size_t part_bytes) {
     if ((taps != 1 && taps != 4 && taps != 9) || C % 32 != 0 || (reinterpret_cast<uintptr_t>(x) & 15) ||
         (reinterpret_cast<uintptr_t>(w) & 15) || (taps == 4 && N % 4 != 0))
         return hipErrorInvalidValue;
@@ -444,12 +482,18 @@ hipError_t launch_conv_f16(int taps, const float* x, const uint16_t* w, const fl
     const int tiles = (int)(((M + CT - 1) / CT) * ((N + CT - 1) / CT));
     const unsigned grid = (unsigned)((tiles + 7) / 8 * 8);
     const int gl = gelu ? 1 : 0;
-    // operands the DMA kernel's 32-bit buffer offsets reach (with the out-of-range offset above)
-    if ((int64_t)M * C * 4 < CONV_OOB - 4096 && (int64_t)N * (taps == 9 ? 9 : 1) * C * 2 < CONV_OOB - 4096) {
-        if (taps == 9) conv_f16_dma_kernel<9, CONV_NB><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
-        else if (taps == 4) conv_f16_dma_kernel<4, CONV_NB><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
-        else conv_f16_dma_kernel<1, CONV_NB><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
-        return hipGetLastError();
+    if (conv_dma_ok(taps, M, C, N)) {
+        // the K split, when the caller gave room for its partial sums
+        int S = part ? conv_f16_ksplit(taps, M, C, N) : 1;
+        if ((size_t)S * (size_t)M * (size_t)N * 4 > part_bytes) S = 1;
+        const int nst = (taps == 9 ? 9 : 1) * C / 32, sps = (nst + S - 1) / S;
+        const unsigned gs = (unsigned)((tiles * S + 7) / 8 * 8);
+        if (taps == 9) conv_f16_dma_kernel<9, CONV_NB><<<gs, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, S, sps, part);
+        else if (taps == 4) conv_f16_dma_kernel<4, CONV_NB><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, 1, nst, nullptr);
+        else conv_f16_dma_kernel<1, CONV_NB><<<gs, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, S, sps, part);
+        const hipError_t e = hipGetLastError();
+        if (S == 1 || e != hipSuccess) return e;
+        return launch_split_reduce(part, S, (int)M, N, bias, y, 4LL * N, st);
     }
     // K step 32: a 64-deep step (64 KB of LDS, two workgroups per CU) measured slower
     if (taps == 9)
