@@ -21,6 +21,13 @@
 // lies within one tap, so each A row is one 128-byte segment of the pixel the
 // tap reaches, or zeros outside the image.  No im2col buffer exists.
 //
+// gemm_f32_dma_kernel is the same GEMM with both operands staged by LDS DMA
+// (two 32 KB stage buffers, no staging registers); it serves every operand its
+// 32-bit buffer offsets reach, the register-staged kernel the rest.  Grids of
+// fewer than two tiles per CU may split K (gemm_ksplit): fp32 partial sums per
+// range into caller scratch, added in split order with the bias by
+// gemm_f32_split_reduce_kernel.
+//
 // The 64 x 64 scalar-load kernel remains for rows that are not 16-byte
 // aligned or K not a multiple of 4.
 #include "common.cuh"

@@ -3,7 +3,9 @@
 // conv_f16_kernel, its register-staged form for operands beyond 32-bit buffer
 // offsets) is the fp16-MFMA implicit GEMM of the F16-kernel convolutions (3x3,
 // 1x1 and the 2x2 / stride-2 conv-transpose with its scatter, bias and GELU in
-// the epilogue); F32-kernel convolutions run on gemm_f32.hip.  The rest are
+// the epilogue; the 3x3 and 1x1 split K on grids smaller than the CU count, the
+// partial sums added by gemm_f32.hip's reduce); F32-kernel convolutions run on
+// gemm_f32.hip.  The rest are
 // HBM-bound passes: the conv-transpose kernel repack + F16 cast, the 3x3
 // kernel repacks for the implicit GEMMs, and, for maps the implicit GEMMs do
 // not take, im2col, the conv-transpose scatter and bias adds; the 2x2
