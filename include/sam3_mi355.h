@@ -353,6 +353,13 @@ size_t mi355_hiera_workspace_size(const mi355_hiera_hparams* hp);
  * x_out must not overlap x. */
 mi355_status mi355_hiera_block_forward(mi355_context* ctx, const mi355_hiera_hparams* hp, int block_index,
                                        const mi355_hiera_block* blk, const float* x, int spatial, float* x_out);
+/* x = conv2d(image, patch_w, stride 4, pad 3) + patch_b + pos_embed, the patch
+ * embedding mi355_hiera_encode starts from (sam3.cpp:4473-4494: ggml_conv_2d =
+ * im2col + F32 mul_mat, + bias, + pos_embed): image device F32 [3][img][img],
+ * patch_w [7, 7, 3, E] F32 or F16, patch_b [E], pos_embed and x [S0*S0][E]
+ * token-major (S0 = img/4). */
+mi355_status mi355_hiera_prefix(mi355_context* ctx, const mi355_hiera_hparams* hp, const float* image,
+                                const mi355_tensor* patch_w, const float* patch_b, const float* pos_embed, float* x);
 /* The whole backbone: image device F32 [3][img][img]; patch_w [7, 7, 3, E]
  * F32 or F16, patch_b [E], pos_embed [S0*S0][E] (S0 = img/4).  stage_out[s]
  * (device [S_s*S_s][C_s], or NULL) receive the output of each stage's last

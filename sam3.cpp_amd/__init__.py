@@ -166,6 +166,7 @@ def lib():
         "mi355_hiera_block_info_get": (I, [C.POINTER(HieraHparams), I, C.POINTER(HieraBlockInfo)]),
         "mi355_hiera_workspace_size": (SZ, [C.POINTER(HieraHparams)]),
         "mi355_hiera_block_forward": (I, [P, C.POINTER(HieraHparams), I, C.POINTER(HieraBlock), P, I, P]),
+        "mi355_hiera_prefix": (I, [P, C.POINTER(HieraHparams), P, T, P, P, P]),
         "mi355_hiera_encode": (I, [P, C.POINTER(HieraHparams), P, T, P, P, C.POINTER(HieraBlock), I,
                                    C.POINTER(P)]),
         "mi355_context_set_fusion": (I, [P, I]),
@@ -505,6 +506,9 @@ class Context:
     # ---- SAM2 Hiera encoder
     def hiera_block_forward(self, hp: HieraHparams, index: int, blk: HieraBlock, x, spatial: int, x_out):
         self._check(self.L.mi355_hiera_block_forward(self.h, C.byref(hp), index, C.byref(blk), x, spatial, x_out))
+
+    def hiera_prefix(self, hp: HieraHparams, image, patch_w: Tensor, patch_b, pos, x):
+        self._check(self.L.mi355_hiera_prefix(self.h, C.byref(hp), image, C.byref(patch_w), patch_b, pos, x))
 
     def hiera_encode(self, hp: HieraHparams, image, patch_w: Tensor, patch_b, pos, blocks, stage_out=None):
         arr = (HieraBlock * len(blocks))(*blocks)

@@ -70,10 +70,20 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const GemmF32Args p) {
     char* D = reinterpret_cast<char*>(p.D) + (int64_t)i12 * p.d_nb2 + (int64_t)i13 * p.d_nb3;
     const int n = n0 + wn * 32 + lr;
     const float bn = p.bias && n < p.N ? p.bias[n] : 0.0f;
+    float ad[16];  // the addend, loaded before the first store (as the tiled kernels)
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int m = m0 + wm * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-        if (m < p.M && n < p.N) *reinterpret_cast<float*>(D + (int64_t)m * p.d_nb1 + 4LL * n) = acc[i] + bn;
+        ad[i] = p.add && m < p.M && n < p.N ? p.add[(int64_t)m * p.N + n] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int m = m0 + wm * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
+        if (m < p.M && n < p.N) {
+            float v = acc[i] + bn;
+            if (p.add) v = v + ad[i];
+            *reinterpret_cast<float*>(D + (int64_t)m * p.d_nb1 + 4LL * n) = v;
+        }
     }
 }
 
@@ -199,6 +209,21 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_tiled_kernel(const GemmF32Arg
         return;
     }
     char* D = reinterpret_cast<char*>(p.D) + (int64_t)i12 * p.d_nb2 + (int64_t)i13 * p.d_nb3;
+    // the addend's values, all loaded before the first store (D may alias it, so loads
+    // interleaved with the stores would each wait for the one before)
+    float ad[2][2][16];
+    if (p.add) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int n = n0 + wn * 64 + j * 32 + lr;
+                    const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    ad[j][i][r] = m < p.M && n < p.N ? p.add[(int64_t)m * p.N + n] : 0.0f;
+                }
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int n = n0 + wn * 64 + j * 32 + lr;
@@ -209,7 +234,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_tiled_kernel(const GemmF32Arg
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                if (m < p.M) *reinterpret_cast<float*>(D + (int64_t)m * p.d_nb1 + 4LL * n) = acc[i][j][r] + bn;
+                if (m < p.M) {
+                    float v = acc[i][j][r] + bn;
+                    if (p.add) v = v + ad[j][i][r];
+                    *reinterpret_cast<float*>(D + (int64_t)m * p.d_nb1 + 4LL * n) = v;
+                }
             }
     }
 }
@@ -358,6 +387,21 @@ __global__ __launch_bounds__(256, NB == 2 ? 2 : 1) void gemm_f32_dma_kernel(cons
         return;
     }
     char* D = reinterpret_cast<char*>(p.D) + (int64_t)i12 * p.d_nb2 + (int64_t)i13 * p.d_nb3;
+    // the addend's values, all loaded before the first store (D may alias it, so loads
+    // interleaved with the stores would each wait for the one before)
+    float ad[2][2][16];
+    if (p.add) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int n = n0 + wn * 64 + j * 32 + lr;
+                    const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+                    ad[j][i][r] = m < M && n < N ? p.add[(int64_t)m * N + n] : 0.0f;
+                }
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int n = n0 + wn * 64 + j * 32 + lr;
@@ -368,7 +412,11 @@ __global__ __launch_bounds__(256, NB == 2 ? 2 : 1) void gemm_f32_dma_kernel(cons
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                if (m < M) *reinterpret_cast<float*>(D + (int64_t)m * p.d_nb1 + 4LL * n) = acc[i][j][r] + bn;
+                if (m < M) {
+                    float v = acc[i][j][r] + bn;
+                    if (p.add) v = v + ad[j][i][r];
+                    *reinterpret_cast<float*>(D + (int64_t)m * p.d_nb1 + 4LL * n) = v;
+                }
             }
     }
 }
@@ -417,10 +465,11 @@ hipError_t launch_split_reduce(const float* part, int S, int M, int N, const flo
 
 hipError_t launch_gemm_f32(const GemmF32Args& a, int Z, hipStream_t st) {
     if (a.M <= 0 || a.N <= 0 || Z <= 0) return hipSuccess;
+    if (a.add && Z != 1) return hipErrorInvalidValue;
     const int tiles = ((a.M + TM - 1) / TM) * ((a.N + TN - 1) / TN);
     // the K split (partials in a.part, then the reduce pass), when the caller gave room for it
     int S = 1, sps = (a.K + TK - 1) / TK;
-    if (a.part && Z == 1) {
+    if (a.part && Z == 1 && !a.add) {
         const int s = f32_ksplit(a.M, a.N, a.K);
         if (s > 1 && (size_t)s * (size_t)a.M * (size_t)a.N * 4 <= a.part_bytes) {
             S = s;

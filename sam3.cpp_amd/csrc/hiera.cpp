@@ -185,6 +185,11 @@ mi355_status check_hp(mi355_context* ctx, const mi355_hiera_hparams* hp, std::ve
     return MI355_STATUS_SUCCESS;
 }
 
+// The patch embedding's 147 im2col columns (c, ky, kx) and weight rows at a zero-padded
+// pitch of 148 floats: the fp32 MFMA GEMM then takes them in whole 16-byte chunks (the zero
+// column adds exact zeros to every sum)
+constexpr int PATCH_KP = 148;
+
 Sizes all_sizes(const mi355_hiera_hparams* hp, const std::vector<Info>& infos) {
     Sizes z;
     int S = hp->img_size / 4;
@@ -193,8 +198,8 @@ Sizes all_sizes(const mi355_hiera_hparams* hp, const std::vector<Info>& infos) {
         if (b.qs) S /= 2;
     }
     const size_t S0 = (size_t)(hp->img_size / 4);
-    z.cols = S0 * S0 * 147 * 4;
-    z.w32 = (size_t)147 * hp->embed_dim * 4;
+    z.cols = S0 * S0 * PATCH_KP * 4;
+    z.w32 = (size_t)PATCH_KP * hp->embed_dim * 4;
     z.x = std::max(z.x, S0 * S0 * (size_t)hp->embed_dim * 4);
     return z;
 }
@@ -463,6 +468,54 @@ mi355_status run_block(mi355_context* ctx, const mi355_hiera_hparams* hp, const 
     return MI355_STATUS_SUCCESS;
 }
 
+mi355_status check_patch(mi355_context* ctx, const mi355_hiera_hparams* hp, const mi355_tensor* patch_w,
+                         const char* what) {
+    const int E = hp->embed_dim;
+    if (patch_w->ne[0] != 7 || patch_w->ne[1] != 7 || patch_w->ne[2] != 3 || patch_w->ne[3] != E ||
+        !(patch_w->type == T_F32 || patch_w->type == T_F16) || !patch_w->data)
+        return fail(ctx, MI355_STATUS_INVALID_ARG, "%s: patch weight must be F32/F16 [7, 7, 3, E]", what);
+    if (patch_w->nb[0] != (patch_w->type == T_F32 ? 4 : 2) || patch_w->nb[3] != patch_w->nb[0] * 147)
+        return fail(ctx, MI355_STATUS_UNSUPPORTED, "%s: patch weight must be contiguous", what);
+    return MI355_STATUS_SUCCESS;
+}
+
+// patch embedding (sam3.cpp:4473-4494): ggml_conv_2d(w, img, 4, 4, 3, 3, 1, 1) = im2col +
+// F32 mul_mat, + bias, + pos_embed -> x [S0*S0][E]. With F16 weights the image columns are
+// rounded to fp16 (ggml's F16 im2col) and the weights widened: the F16 kernel's products
+// are exact in fp32. Bias and pos_embed are added in the GEMM's epilogue in the reference's
+// order, (conv + b) + pe.
+mi355_status patch_embed(mi355_context* ctx, const mi355_hiera_hparams* hp, const float* image,
+                         const mi355_tensor* patch_w, const float* patch_b, const float* pos_embed, const Bufs& b,
+                         float* x) {
+    const int E = hp->embed_dim, IMG = hp->img_size, S0 = IMG / 4;
+    hipStream_t st = ctx->stream;
+    const bool w16 = patch_w->type == T_F16;
+    {
+        Timed t(ctx, "im2col");
+        TRY(hip_check(ctx, t.done(launch_im2col_pad(image, b.cols, 3, IMG, IMG, 7, 7, 4, 3, S0, S0, PATCH_KP, w16, st)),
+                      "im2col launch"));
+    }
+    TRY(hip_check(ctx, launch_pad_rows_f32(patch_w->data, w16, E, 147, PATCH_KP, b.w32, st), "patch weight pad"));
+    GemmF32Args g;
+    g.W = b.w32;
+    g.w_nb1 = 4LL * PATCH_KP;
+    g.w_nb2 = g.w_nb3 = g.w_nb1 * E;
+    g.X = b.cols;
+    g.x_nb1 = 4LL * PATCH_KP;
+    g.x_nb2 = g.x_nb3 = g.x_nb1 * S0 * S0;
+    g.D = x;
+    g.d_nb1 = 4LL * E;
+    g.d_nb2 = g.d_nb3 = g.d_nb1 * S0 * S0;
+    g.M = S0 * S0;
+    g.N = E;
+    g.K = PATCH_KP;
+    g.ne12 = g.r2 = g.r3 = 1;
+    g.bias = patch_b;
+    g.add = pos_embed;
+    Timed t(ctx, "gemm_f32");
+    return hip_check(ctx, t.done(launch_gemm_f32(g, 1, st)), "gemm_f32 launch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -528,6 +581,19 @@ mi355_status mi355_hiera_block_forward(mi355_context* ctx, const mi355_hiera_hpa
     return run_block(ctx, hp, bi, blk, x, spatial, x_out, b);
 }
 
+mi355_status mi355_hiera_prefix(mi355_context* ctx, const mi355_hiera_hparams* hp, const float* image,
+                                const mi355_tensor* patch_w, const float* patch_b, const float* pos_embed, float* x) {
+    std::vector<Info> infos;
+    TRY(check_hp(ctx, hp, infos));
+    if (!image || !patch_w || !patch_b || !pos_embed || !x) return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera_prefix: null pointer");
+    TRY(check_patch(ctx, hp, patch_w, "hiera_prefix"));
+    if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "hiera_prefix: null context");
+    (void)hipSetDevice(ctx->device);
+    Bufs b;
+    TRY(get_bufs(ctx, hp, infos, &b));
+    return patch_embed(ctx, hp, image, patch_w, patch_b, pos_embed, b, x);
+}
+
 mi355_status mi355_hiera_encode(mi355_context* ctx, const mi355_hiera_hparams* hp, const float* image,
                                 const mi355_tensor* patch_w, const float* patch_b, const float* pos_embed,
                                 const mi355_hiera_block* blocks, int n_blocks, float* const stage_out[4]) {
@@ -538,38 +604,14 @@ mi355_status mi355_hiera_encode(mi355_context* ctx, const mi355_hiera_hparams* h
     if (n_blocks != (int)infos.size())
         return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera_encode: %d blocks given, the stage table has %d", n_blocks,
                     (int)infos.size());
-    const int E = hp->embed_dim, IMG = hp->img_size, S0 = IMG / 4;
-    if (patch_w->ne[0] != 7 || patch_w->ne[1] != 7 || patch_w->ne[2] != 3 || patch_w->ne[3] != E ||
-        !(patch_w->type == T_F32 || patch_w->type == T_F16) || !patch_w->data)
-        return fail(ctx, MI355_STATUS_INVALID_ARG, "hiera_encode: patch weight must be F32/F16 [7, 7, 3, E]");
-    if (patch_w->nb[0] != (patch_w->type == T_F32 ? 4 : 2) || patch_w->nb[3] != patch_w->nb[0] * 147)
-        return fail(ctx, MI355_STATUS_UNSUPPORTED, "hiera_encode: patch weight must be contiguous");
+    TRY(check_patch(ctx, hp, patch_w, "hiera_encode"));
     if (!ctx) return fail(nullptr, MI355_STATUS_INVALID_ARG, "hiera_encode: null context");
     (void)hipSetDevice(ctx->device);
     Bufs b;
     TRY(get_bufs(ctx, hp, infos, &b));
     hipStream_t st = ctx->stream;
-    // patch embedding: ggml_conv_2d(w, img, 4, 4, 3, 3, 1, 1) = im2col + mul_mat, + bias, + pos_embed
-    const bool w16 = patch_w->type == T_F16;
-    {
-        Timed t(ctx, "im2col");
-        TRY(hip_check(ctx, t.done(launch_im2col_pad(image, b.cols, 3, IMG, IMG, 7, 7, 4, 3, S0, S0, w16, st)),
-                      "im2col launch"));
-    }
-    const float* w32 = static_cast<const float*>(patch_w->data);
-    if (w16) {  // the F16 kernel's products are exact in fp32: F32 GEMM over fp16-valued operands
-        TRY(hip_check(ctx, launch_f16_to_f32(patch_w->data, b.w32, 147LL * E, st), "f16_to_f32 launch"));
-        w32 = b.w32;
-    }
-    {
-        const mi355_tensor w = tensor_on(w32, T_F32, 147, E), cols = tensor_on(b.cols, T_F32, 147, (int64_t)S0 * S0),
-                           out = tensor_on(b.x0, T_F32, E, (int64_t)S0 * S0);
-        TRY(mi355_mul_mat(ctx, &w, &cols, &out));
-    }
-    {
-        Timed t(ctx, "bias_add_pe");
-        TRY(hip_check(ctx, t.done(launch_bias_add_pe(b.x0, patch_b, pos_embed, (int64_t)S0 * S0, E, st)), "bias_pe launch"));
-    }
+    const int S0 = hp->img_size / 4;
+    TRY(patch_embed(ctx, hp, image, patch_w, patch_b, pos_embed, b, b.x0));
     float* cur = b.x0;
     float* nxt = b.x1;
     int S = S0, stage = 0;

@@ -268,29 +268,33 @@ __global__ __launch_bounds__(256) void bias_gelu_tanh_act_kernel(const float* __
 }
 
 // conv2d columns with stride / zero padding: cols[m][k], m = oy*OW + ox,
-// k = (c*KH + ky)*KW + kx; optionally rounded to fp16 (F16 kernels, ggml_im2col F16).
-// Grid-stride over the n = OH OW K elements (a workgroup per 256 elements spent its time
-// in dispatch); rc = {1/K, 1/(KH KW), 1/KW, 1/OW} when n plus the grid stays below 2^31:
-// the indices then come from div_rcp instead of 64- and 32-bit divisions; else rc.k = 0.
+// k = (c*KH + ky)*KW + kx, rows of pitch kp >= K = C*KH*KW floats with the columns past K
+// zero (a pitch the fp32 GEMM's 16-byte chunks take whole); optionally rounded to fp16
+// (F16 kernels, ggml_im2col F16). Grid-stride over the n = OH OW K elements, consecutive
+// threads on consecutive columns so the stores coalesce (a thread per kernel row writing
+// KW columns was slower: 47 against 32 us at 1024^2); rc = {1/K, 1/(KH KW), 1/KW, 1/OW}
+// when n plus the grid stays below 2^31: the indices then come from div_rcp instead of
+// 64- and 32-bit divisions; else rc.k = 0.
 struct Im2colRcp {
     double k, kk, kw, ow;
 };
 __global__ __launch_bounds__(256) void im2col_pad_kernel(const float* __restrict__ img, float* __restrict__ cols, int C,
                                                          int Hin, int Win, int KH, int KW, int stride, int pad, int OH,
-                                                         int OW, int round16, Im2colRcp rc) {
+                                                         int OW, int kp, int round16, Im2colRcp rc) {
     const int K = C * KH * KW;
     const int64_t n = (int64_t)OH * OW * K, step = (int64_t)gridDim.x * blockDim.x;
     for (int64_t tix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; tix < n; tix += step) {
         int k, kx, ky, c, ox, oy;
+        int64_t m;
         if (rc.k != 0.0) {
             int r;
-            const int m = div_rcp((int)tix, K, rc.k, k);
+            m = div_rcp((int)tix, K, rc.k, k);
             c = div_rcp(k, KH * KW, rc.kk, r);
             ky = div_rcp(r, KW, rc.kw, kx);
-            oy = div_rcp(m, OW, rc.ow, ox);
+            oy = div_rcp((int)m, OW, rc.ow, ox);
         } else {
             k = (int)(tix % K);
-            const int64_t m = tix / K;
+            m = tix / K;
             kx = k % KW;
             ky = (k / KW) % KH;
             c = k / (KW * KH);
@@ -300,22 +304,23 @@ __global__ __launch_bounds__(256) void im2col_pad_kernel(const float* __restrict
         const int y = oy * stride - pad + ky, xx = ox * stride - pad + kx;
         float v = (y >= 0 && y < Hin && xx >= 0 && xx < Win) ? img[((int64_t)c * Hin + y) * Win + xx] : 0.0f;
         if (round16) v = h2f(f2h(v));
-        cols[tix] = v;
+        cols[m * kp + k] = v;
+        if (k == K - 1)
+            for (int j = K; j < kp; ++j) cols[m * kp + j] = 0.0f;
     }
 }
 
-// x = (conv + b) + pe over rows of C (patch embedding bias, then pos_embed)
-__global__ __launch_bounds__(256) void bias_add_pe_kernel(float* __restrict__ x, const float* __restrict__ b,
-                                                          const float* __restrict__ pe, int64_t rows, int C) {
-    const int64_t tix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (tix >= rows * C) return;
-    const float u = x[tix] + b[tix % C];
-    x[tix] = u + pe[tix];
-}
-
-__global__ __launch_bounds__(256) void f16_to_f32_kernel(const uint16_t* __restrict__ s, float* __restrict__ d, int64_t n) {
-    const int64_t tix = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (tix < n) d[tix] = h2f(s[tix]);
+// dst[r][k] = src[r][k] (F32, or F16 widened) for k < K, 0 for K <= k < kp: a weight
+// matrix at the zero-padded pitch of the im2col columns
+__global__ __launch_bounds__(256) void pad_rows_f32_kernel(const void* __restrict__ src, int f16, int64_t rows, int K,
+                                                           int kp, float* __restrict__ dst) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= rows * kp) return;
+    const int64_t r = t / kp;
+    const int k = (int)(t - r * kp);
+    float v = 0.0f;
+    if (k < K) v = f16 ? h2f(static_cast<const uint16_t*>(src)[r * K + k]) : static_cast<const float*>(src)[r * K + k];
+    dst[t] = v;
 }
 
 static unsigned nblk(int64_t n) { return (unsigned)((n + 255) / 256); }
@@ -387,19 +392,16 @@ hipError_t launch_bias_gelu_tanh_act(const float* h, const float* b, int64_t row
     return hipGetLastError();
 }
 hipError_t launch_im2col_pad(const float* img, float* cols, int C, int Hin, int Win, int KH, int KW, int stride, int pad,
-                             int OH, int OW, bool round16, hipStream_t st) {
+                             int OH, int OW, int kp, bool round16, hipStream_t st) {
     const int64_t K = (int64_t)C * KH * KW, n = (int64_t)OH * OW * K;
     if (n <= 0) return hipSuccess;
+    if (kp < K) return hipErrorInvalidValue;
     // about eight elements per thread
     const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>(nblk(n), (nblk(n) + 7) / 8));
     Im2colRcp rc{0.0, 0.0, 0.0, 0.0};
     if (n + (int64_t)grid * 256 < ((int64_t)1 << 31) && K > 0 && OW > 0)
         rc = Im2colRcp{1.0 / (double)K, 1.0 / (double)(KH * KW), 1.0 / (double)KW, 1.0 / (double)OW};
-    im2col_pad_kernel<<<grid, 256, 0, st>>>(img, cols, C, Hin, Win, KH, KW, stride, pad, OH, OW, round16 ? 1 : 0, rc);
-    return hipGetLastError();
-}
-hipError_t launch_bias_add_pe(float* x, const float* b, const float* pe, int64_t rows, int C, hipStream_t st) {
-    if (rows * C > 0) bias_add_pe_kernel<<<nblk(rows * C), 256, 0, st>>>(x, b, pe, rows, C);
+    im2col_pad_kernel<<<grid, 256, 0, st>>>(img, cols, C, Hin, Win, KH, KW, stride, pad, OH, OW, kp, round16 ? 1 : 0, rc);
     return hipGetLastError();
 }
 // sam2_compute_pos_embed (sam3.cpp:4076-4157): Keys cubic convolution
@@ -454,8 +456,9 @@ hipError_t launch_hiera_pos_embed(const float* bkg, int E, int bh, int bw, const
     if (n > 0) hiera_pos_embed_kernel<<<nblk(n), 256, 0, st>>>(bkg, E, bh, bw, win, ws, H, W, out);
     return hipGetLastError();
 }
-hipError_t launch_f16_to_f32(const void* s, float* d, int64_t n, hipStream_t st) {
-    if (n > 0) f16_to_f32_kernel<<<nblk(n), 256, 0, st>>>(static_cast<const uint16_t*>(s), d, n);
+hipError_t launch_pad_rows_f32(const void* src, bool f16, int64_t rows, int K, int kp, float* dst, hipStream_t st) {
+    if (kp < K) return hipErrorInvalidValue;
+    if (rows * kp > 0) pad_rows_f32_kernel<<<nblk(rows * kp), 256, 0, st>>>(src, f16 ? 1 : 0, rows, K, kp, dst);
     return hipGetLastError();
 }
 

@@ -226,6 +226,8 @@ struct GemmF32Args {
     // implicit 3x3 / stride 1 / pad 1 convolution: X is a token-major map [H*Wd][C], row m
     // of the GEMM is output pixel m, and K = 9*C runs (tap, channel) with W rows in that order
     int conv = 0, H = 0, Wd = 0, C = 0;
+    // optional addend [M][N] (row pitch N floats, Z == 1), added after the bias: D = (acc + bias) + add
+    const float* add = nullptr;
     // K split for grids too small to fill the device (Z == 1 only): when part is given, the
     // launch may split K into ranges whose fp32 partial sums go to part [split][M][N] (at most
     // part_bytes) and are then added in split order, with the bias, by a reduce pass
@@ -338,10 +340,11 @@ hipError_t launch_hiera_proj_residual(float* x, const float* shortcut, const flo
 hipError_t launch_bias_gelu_tanh(float* h, const float* b, int64_t rows, int n, hipStream_t st);
 hipError_t launch_bias_gelu_tanh_act(const float* h, const float* b, int64_t rows, int n, const ActOut& o,
                                      hipStream_t st);
+// conv2d columns cols[m][k] at row pitch kp >= C*KH*KW, zero past K (see im2col_pad_kernel)
 hipError_t launch_im2col_pad(const float* img, float* cols, int C, int Hin, int Win, int KH, int KW, int stride, int pad,
-                             int OH, int OW, bool round16, hipStream_t st);
-hipError_t launch_bias_add_pe(float* x, const float* b, const float* pe, int64_t rows, int C, hipStream_t st);
-hipError_t launch_f16_to_f32(const void* s, float* d, int64_t n, hipStream_t st);
+                             int OH, int OW, int kp, bool round16, hipStream_t st);
+// rows x K F32 (or F16, widened) -> rows x kp F32, zero past K
+hipError_t launch_pad_rows_f32(const void* src, bool f16, int64_t rows, int K, int kp, float* dst, hipStream_t st);
 // SimpleFPN neck passes (neck.hip); activations token-major [H*W][C]
 hipError_t launch_deconv_pack(const void* w, int wtype, int Cin, int Cout, uint16_t* out, hipStream_t st);
 hipError_t launch_deconv_scatter(const float* D, const float* b, int H, int W, int Cout, bool gelu, float* y,

@@ -100,6 +100,44 @@ def _patch_ref(orc, img, pw, pb, pe, E):
     return ((conv + pb).astype(np.float32) + pe).astype(np.float32)
 
 
+@pytest.mark.parametrize("img_size,wtype", [(128, "f32"), (1024, "f32"), (128, "f16")])
+def test_hiera_prefix(mi, ctx, orc, img_size, wtype):
+    """The patch embedding alone (mi355_hiera_prefix) against the oracle's im2col + F32
+    mul_mat + bias + pos_embed: |gpu - ref| <= 1e-5 * (sum|w x| + |b| + |pe|) + 4 ulp, on
+    every row (128^2) or 256 sampled rows (1024^2); with F16 weights the image columns are
+    rounded to fp16 first, as ggml's F16 im2col does."""
+    hp = mi.hiera_tiny(img_size)
+    E, S0 = 96, img_size // 4
+    img = orc.uniform(3 * img_size * img_size, 13, 1).reshape(3, img_size, img_size)
+    pw = orc.normal(E * 147, 13, 2, std=0.05).reshape(E, 3, 7, 7)
+    if wtype == "f16":
+        pw = pw.astype(np.float16).astype(np.float32)
+    pb = orc.normal(E, 13, 3) * np.float32(0.05)
+    pe = (orc.normal(S0 * S0 * E, 13, 4) * np.float32(0.02)).reshape(S0 * S0, E)
+    wd = dev(pw.astype(np.float16).view(np.uint16)) if wtype == "f16" else dev(pw)
+    wt = mi.from_torch(wd, mi.F16 if wtype == "f16" else mi.F32, [7, 7, 3, E])
+    imgd, pbd, ped = dev(img), dev(pb), dev(pe)
+    x = torch.full((S0 * S0, E), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.hiera_prefix(hp, _p(imgd), wt, _p(pbd), _p(ped), _p(x))
+    ctx.synchronize()
+    got = x.cpu().numpy()
+    rng = np.random.default_rng(img_size)
+    rows = np.arange(S0 * S0) if S0 * S0 <= 1024 else np.unique(np.concatenate([[0, S0 * S0 - 1], rng.choice(S0 * S0, 254, replace=False)]))
+    src = img.astype(np.float16).astype(np.float32) if wtype == "f16" else img
+    pad = np.pad(src, ((0, 0), (3, 3), (3, 3)))
+    cols = np.empty((len(rows), 147), dtype=np.float64)
+    for i, m in enumerate(rows):
+        oy, ox = divmod(int(m), S0)
+        cols[i] = pad[:, oy * 4:oy * 4 + 7, ox * 4:ox * 4 + 7].reshape(-1)
+    w2 = pw.reshape(E, 147).astype(np.float64)
+    ref = (cols @ w2.T + pb.astype(np.float64)) + pe[rows].astype(np.float64)
+    absterm = np.abs(cols) @ np.abs(w2.T) + np.abs(pb) + np.abs(pe[rows])
+    tol = 1e-5 * absterm + 4 * np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+    err = np.abs(got[rows].astype(np.float64) - ref)
+    assert np.isfinite(got).all()
+    assert (err <= tol).all(), float((err / tol).max())
+
+
 def test_hiera_encode_patch_and_stages(mi, ctx, orc):
     """Whole backbone at 128x128 (Q4_0): every stage output is finite and a
     second run reproduces it bit for bit; the stage-0 output (block 0 on the
