@@ -457,7 +457,9 @@ size_t gemm_f32_part_bytes(int64_t M, int64_t N, int64_t K) {
 
 hipError_t launch_split_reduce(const float* part, int S, int M, int N, const float* bias, float* D, int64_t d_nb1,
                                hipStream_t st) {
-    if (N % 4 != 0 || S < 1) return hipErrorInvalidValue;
+    if (N % 4 != 0 || S < 1 || ((reinterpret_cast<uintptr_t>(part) | reinterpret_cast<uintptr_t>(bias) |
+                                 reinterpret_cast<uintptr_t>(D) | (uintptr_t)d_nb1) & 15))
+        return hipErrorInvalidValue;
     const int64_t n = (int64_t)M * (N / 4);
     if (n > 0) gemm_f32_split_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(part, S, M, N, bias, D, d_nb1);
     return hipGetLastError();
@@ -469,7 +471,10 @@ hipError_t launch_gemm_f32(const GemmF32Args& a, int Z, hipStream_t st) {
     const int tiles = ((a.M + TM - 1) / TM) * ((a.N + TN - 1) / TN);
     // the K split (partials in a.part, then the reduce pass), when the caller gave room for it
     int S = 1, sps = (a.K + TK - 1) / TK;
-    if (a.part && Z == 1 && !a.add) {
+    // (the reduce stores float4 rows: D and its row pitch on 16 bytes, N % 4 == 0)
+    const bool d16 = ((reinterpret_cast<uintptr_t>(a.D) | (uintptr_t)a.d_nb1 | reinterpret_cast<uintptr_t>(a.part) |
+                       reinterpret_cast<uintptr_t>(a.bias)) & 15) == 0;
+    if (a.part && Z == 1 && !a.add && d16) {
         const int s = f32_ksplit(a.M, a.N, a.K);
         if (s > 1 && (size_t)s * (size_t)a.M * (size_t)a.N * 4 <= a.part_bytes) {
             S = s;

@@ -486,7 +486,10 @@ hipError_t launch_conv_f16(int taps, const float* x, const uint16_t* w, const fl
     const int gl = gelu ? 1 : 0;
     if (conv_dma_ok(taps, M, C, N)) {
         // the K split, when the caller gave room for its partial sums
-        int S = part ? conv_f16_ksplit(taps, M, C, N) : 1;
+        // (the reduce stores float4 rows: y and part on 16 bytes; N % 4 == 0 in the split choice)
+        const bool y16 = ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(part) |
+                           reinterpret_cast<uintptr_t>(bias)) & 15) == 0;
+        int S = part && y16 ? conv_f16_ksplit(taps, M, C, N) : 1;
         if ((size_t)S * (size_t)M * (size_t)N * 4 > part_bytes) S = 1;
         const int nst = (taps == 9 ? 9 : 1) * C / 32, sps = (nst + S - 1) / S;
         const unsigned gs = (unsigned)((tiles * S + 7) / 8 * 8);

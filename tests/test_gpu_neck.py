@@ -113,6 +113,31 @@ def test_neck_conv(mi, ctx, orc, wtype, k, Cin, Cout, H, W):
 
 
 @pytest.mark.parametrize("wtype", ["f32", "f16"])
+@pytest.mark.parametrize("k", [1, 3])
+def test_neck_conv_split_unaligned_out(mi, ctx, orc, wtype, k):
+    """A grid small enough for the K split (one 128-pixel tile, K = 9 * 256): with the output
+    and bias 16-byte aligned the partial sums and the reduce run, with both offset by 4 bytes
+    the single-pass kernel does; both within the per-op bar."""
+    rng = np.random.default_rng(40 + k)
+    t = mi.F16 if wtype == "f16" else mi.F32
+    Cin, Cout, H, W = 256, 64, 6, 7
+    w = rand(rng, (Cout, Cin, k, k), 0.05)
+    if t == mi.F16:
+        w = neck.f16r(w)
+    b, x = rand(rng, Cout, 0.1), rand(rng, (H * W, Cin))
+    wt = kernel_tensor(mi, w, t, [k, k, Cin, Cout])
+    xd = dev(x)
+    for off in (0, 1):
+        bbuf = torch.zeros(Cout + 4, dtype=torch.float32, device="cuda")
+        bbuf[off:off + Cout] = torch.from_numpy(b).cuda()
+        ybuf = torch.full((H * W * Cout + 4,), float("nan"), dtype=torch.float32, device="cuda")
+        ctx.neck_conv(wt, bbuf.data_ptr() + 4 * off, xd.data_ptr(), H, W, ybuf.data_ptr() + 4 * off)
+        ctx.synchronize()
+        got = ybuf[off:off + H * W * Cout].cpu().numpy().reshape(H * W, Cout)
+        check_conv(got, w, t, b, x, H, W)
+
+
+@pytest.mark.parametrize("wtype", ["f32", "f16"])
 def test_neck_conv3x3_unaligned_map(mi, orc, wtype):
     """A 3x3 over a map whose rows are not 16-byte aligned takes im2col + MUL_MAT;
     its scratch is sized for the columns (P * 9 * Cin), not for the repacked
