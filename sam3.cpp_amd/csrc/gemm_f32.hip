@@ -422,9 +422,10 @@ __global__ __launch_bounds__(256, NB == 2 ? 2 : 1) void gemm_f32_dma_kernel(cons
 }
 
 // D = bias + part[0] + part[1] + ... (in split order) over an M x N tile set, float4 columns
+// (f16out: D holds fp16, the sums rounded RNE)
 __global__ __launch_bounds__(256) void gemm_f32_split_reduce_kernel(const float* __restrict__ part, int S, int M, int N,
                                                                     const float* __restrict__ bias, float* D,
-                                                                    int64_t d_nb1) {
+                                                                    int64_t d_nb1, int f16out) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int n4 = N / 4;
     if (t >= (int64_t)M * n4) return;
@@ -434,7 +435,13 @@ __global__ __launch_bounds__(256) void gemm_f32_split_reduce_kernel(const float*
     v4f v = *reinterpret_cast<const v4f*>(part + m * N + c);
     for (int s = 1; s < S; ++s) v = v + *reinterpret_cast<const v4f*>(part + s * plane + m * N + c);
     if (bias) v = v + *reinterpret_cast<const v4f*>(bias + c);
-    *reinterpret_cast<v4f*>(reinterpret_cast<char*>(D) + m * d_nb1 + 4LL * c) = v;
+    if (f16out) {
+        const uint32_t h0 = (uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16);
+        const uint32_t h1 = (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16);
+        *reinterpret_cast<uint2*>(reinterpret_cast<char*>(D) + m * d_nb1 + 2LL * c) = make_uint2(h0, h1);
+    } else {
+        *reinterpret_cast<v4f*>(reinterpret_cast<char*>(D) + m * d_nb1 + 4LL * c) = v;
+    }
 }
 
 namespace {
@@ -456,12 +463,13 @@ size_t gemm_f32_part_bytes(int64_t M, int64_t N, int64_t K) {
 }
 
 hipError_t launch_split_reduce(const float* part, int S, int M, int N, const float* bias, float* D, int64_t d_nb1,
-                               hipStream_t st) {
+                               hipStream_t st, bool f16out) {
     if (N % 4 != 0 || S < 1 || ((reinterpret_cast<uintptr_t>(part) | reinterpret_cast<uintptr_t>(bias) |
                                  reinterpret_cast<uintptr_t>(D) | (uintptr_t)d_nb1) & 15))
         return hipErrorInvalidValue;
     const int64_t n = (int64_t)M * (N / 4);
-    if (n > 0) gemm_f32_split_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(part, S, M, N, bias, D, d_nb1);
+    if (n > 0)
+        gemm_f32_split_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(part, S, M, N, bias, D, d_nb1, f16out ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -238,9 +238,10 @@ hipError_t launch_gemm_f32(const GemmF32Args& a, int Z, hipStream_t st);
 // partial-sum bytes launch_gemm_f32 uses for an M x N x K tiled GEMM (0: no K split)
 size_t gemm_f32_part_bytes(int64_t M, int64_t N, int64_t K);
 // D[m][n] = bias[n] + part[0][m][n] + ... + part[S - 1][m][n], added in split order
-// (float4 columns: N % 4 == 0; D row pitch d_nb1 bytes; bias may be null)
+// (float4 columns: N % 4 == 0; D row pitch d_nb1 bytes; bias may be null; f16out: D holds
+// fp16, the sums rounded RNE)
 hipError_t launch_split_reduce(const float* part, int S, int M, int N, const float* bias, float* D, int64_t d_nb1,
-                               hipStream_t st);
+                               hipStream_t st, bool f16out = false);
 
 // K split count of a GEMM of `tiles` 128 x 128 output tiles and nst K stages: grids of `full`
 // tiles or more are not split; smaller ones take the S (at most 16, at least four stages per
@@ -357,8 +358,11 @@ hipError_t launch_conv3x3_pack_f16(const uint16_t* w, int Cin, int Cout, uint16_
 // N = 4 * Cout, y the 2x map, GELU-erf after the bias if gelu). Taps 1 and 9 may split K
 // into ranges whose partial sums go to part [split][M][N] (at most part_bytes; none without
 // part) and are added, with the bias, by launch_split_reduce.
-hipError_t launch_conv_f16(int taps, const float* x, const uint16_t* w, const float* bias, int H, int W, int C, int N,
-                           bool gelu, float* y, hipStream_t st, float* part = nullptr, size_t part_bytes = 0);
+// x16 / y16: the map in / out is fp16 (the f32 values rounded RNE, which the kernel's own rounding
+// of an F32 map gives: the same products), for maps only these kernels read.
+hipError_t launch_conv_f16(int taps, const void* x, bool x16, const uint16_t* w, const float* bias, int H, int W, int C,
+                           int N, bool gelu, void* y, bool y16, hipStream_t st, float* part = nullptr,
+                           size_t part_bytes = 0);
 // partial-sum bytes launch_conv_f16 uses for taps 1 or 9 over M pixels, C input and N output
 // channels (0: no K split)
 size_t conv_f16_part_bytes(int taps, int64_t M, int64_t C, int64_t N);

@@ -82,8 +82,11 @@ size_t conv_scratch(int64_t P, int64_t Cin, int64_t Cout, int k, int wtype, bool
 
 // conv_transpose_2d_p0(kernel [2, 2, Cout, Cin], stride 2) + bias (+ GELU):
 // x [H*W][Cin] -> y [(2H)*(2W)][Cout]
-mi355_status deconv(mi355_context* ctx, const mi355_tensor* w, const float* b, const float* x, int H, int W, bool gelu,
-                    float* y, char* scratch) {
+// (x16 / y16: fp16 maps, the fused neck's intermediates; F16 kernels on the implicit path only)
+mi355_status deconv(mi355_context* ctx, const mi355_tensor* w, const float* b, const void* xv, int H, int W, bool gelu,
+                    void* yv, char* scratch, bool x16 = false, bool y16 = false) {
+    const float* x = static_cast<const float*>(xv);
+    float* y = static_cast<float*>(yv);
     mi355_status st = check_kernel(ctx, w, b, 2, "neck_deconv");
     if (st != MI355_STATUS_SUCCESS) return st;
     const int Cout = (int)w->ne[2], Cin = (int)w->ne[3];
@@ -99,9 +102,10 @@ mi355_status deconv(mi355_context* ctx, const mi355_tensor* w, const float* b, c
     if (implicit_ok(x, Cin)) {
         // one fp16-MFMA GEMM whose epilogue adds the bias (+ GELU) and scatters to the 2x map
         Timed t(ctx, "neck_deconv_f16");
-        return hip_check(ctx, t.done(launch_conv_f16(4, x, packed, b, H, W, Cin, 4 * Cout, gelu, y, ctx->stream)),
+        return hip_check(ctx, t.done(launch_conv_f16(4, x, x16, packed, b, H, W, Cin, 4 * Cout, gelu, y, y16, ctx->stream)),
                          "deconv_f16 launch");
     }
+    if (x16 || y16) return fail(ctx, MI355_STATUS_FAILED, "neck_deconv: fp16 maps off the implicit path");
     const mi355_tensor s0 = dev_t(packed, T_F16, Cin, 4LL * Cout), s1 = dev_t(x, T_F32, Cin, P),
                        d = dev_t(D, T_F32, 4LL * Cout, P);
     st = mi355_mul_mat(ctx, &s0, &s1, &d);
@@ -111,8 +115,10 @@ mi355_status deconv(mi355_context* ctx, const mi355_tensor* w, const float* b, c
 }
 
 // conv_2d_sk_p0 (1x1) or conv_2d_s1_ph (3x3) + bias: x [H*W][Cin] -> y [H*W][Cout]
-mi355_status conv(mi355_context* ctx, const mi355_tensor* w, const float* b, const float* x, int H, int W, float* y,
-                  char* scratch) {
+mi355_status conv(mi355_context* ctx, const mi355_tensor* w, const float* b, const void* xv, int H, int W, void* yv,
+                  char* scratch, bool x16 = false, bool y16 = false) {
+    const float* x = static_cast<const float*>(xv);
+    float* y = static_cast<float*>(yv);
     if (!w) return fail(ctx, MI355_STATUS_INVALID_ARG, "neck_conv: null kernel");
     const int k = (int)w->ne[0];
     if (k != 1 && k != 3) return fail(ctx, MI355_STATUS_UNSUPPORTED, "neck_conv: kernel size %d (1 or 3)", k);
@@ -126,6 +132,9 @@ mi355_status conv(mi355_context* ctx, const mi355_tensor* w, const float* b, con
     // rows; maps whose rows are not 16-byte aligned (or a 3x3 with Cin % 32 != 0) take
     // im2col + MUL_MAT below
     const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && Cin % 4 == 0;
+    if ((x16 || y16) && !(w->type == T_F16 && implicit_ok(x, Cin) &&
+                          (k == 3 || (reinterpret_cast<uintptr_t>(w->data) & 15) == 0)))
+        return fail(ctx, MI355_STATUS_FAILED, "neck_conv: fp16 maps off the implicit F16 path");
     if (w->type == T_F32 && aligned && (k == 1 || implicit_ok(x, Cin))) {
         if (k == 3) {
             Timed t(ctx, "neck_conv3x3_pack");
@@ -173,8 +182,8 @@ mi355_status conv(mi355_context* ctx, const mi355_tensor* w, const float* b, con
         // the K split's partial sums follow the repacked kernel
         float* part = reinterpret_cast<float*>(scratch + (k == 3 ? align_up((size_t)(K * Cout * 2)) : 0));
         Timed t(ctx, k == 3 ? "neck_conv3x3_f16" : "neck_conv1x1_f16");
-        return hip_check(ctx, t.done(launch_conv_f16(k * k, x, wk, b, H, W, Cin, Cout, false, y, ctx->stream, part,
-                                                     conv_f16_part_bytes(k * k, P, Cin, Cout))),
+        return hip_check(ctx, t.done(launch_conv_f16(k * k, x, x16, wk, b, H, W, Cin, Cout, false, y, y16, ctx->stream,
+                                                     part, conv_f16_part_bytes(k * k, P, Cin, Cout))),
                          "conv_f16 launch");
     }
     const mi355_tensor s0 = dev_t(w->data, w->type, K, Cout), d = dev_t(y, T_F32, Cout, P);
@@ -203,6 +212,21 @@ mi355_status scratch_for(mi355_context* ctx, size_t bytes, char** p) {
     mi355_status st = ensure_buffer(ctx, &ctx->neck, &ctx->neck_size, std::max<size_t>(bytes, 256));
     *p = static_cast<char*>(ctx->neck);
     return st;
+}
+
+// The fused neck keeps its intermediate maps in fp16 when every kernel is F16 and every
+// convolution takes the implicit path (16-byte aligned F32 input, channel counts % 32 == 0,
+// 1x1 kernels on 16 bytes)
+bool fp16_maps(const float* x, int E, const mi355_neck_scale* s) {
+    auto f16 = [](const mi355_tensor* t) { return t->type == T_F16; };
+    auto a16 = [](const mi355_tensor* t) { return (reinterpret_cast<uintptr_t>(t->data) & 15) == 0; };
+    if (!implicit_ok(x, E)) return false;
+    for (int i = 0; i < 4; ++i) {
+        if (!f16(s[i].conv1x1_w) || !f16(s[i].conv3x3_w) || !a16(s[i].conv1x1_w)) return false;
+        if (s[i].conv1x1_w->ne[2] % 32 != 0 || s[i].conv3x3_w->ne[2] % 32 != 0) return false;
+        if (i < 2 && (!f16(s[i].deconv1_w) || s[i].deconv1_w->ne[3] % 32 != 0)) return false;
+    }
+    return f16(s[0].deconv2_w) && s[0].deconv2_w->ne[3] % 32 == 0;
 }
 
 // Buffer plan of the whole neck: two map buffers plus the largest op scratch.
@@ -318,22 +342,26 @@ mi355_status mi355_sam3_neck(mi355_context* ctx, const float* x, int E, int G, c
         st = (e);                                  \
         if (st != MI355_STATUS_SUCCESS) return st; \
     } while (0)
+    // F16 kernels throughout, on the implicit path: the maps between two convolutions are
+    // stored as fp16, the values each consumer rounds its F32 input to (the same bits out);
+    // the F32 ViT output, the pool output and the four outputs stay F32
+    const bool h = fp16_maps(x, E, s);
     // scale 0 (4x): deconv + GELU, deconv, 1x1, 3x3
-    TRY(deconv(ctx, s[0].deconv1_w, s[0].deconv1_b, x, G, G, true, A, scr));
-    TRY(deconv(ctx, s[0].deconv2_w, s[0].deconv2_b, A, 2 * G, 2 * G, false, B, scr));
-    TRY(conv(ctx, s[0].conv1x1_w, s[0].conv1x1_b, B, 4 * G, 4 * G, A, scr));
-    TRY(conv(ctx, s[0].conv3x3_w, s[0].conv3x3_b, A, 4 * G, 4 * G, out[0], scr));
+    TRY(deconv(ctx, s[0].deconv1_w, s[0].deconv1_b, x, G, G, true, A, scr, false, h));
+    TRY(deconv(ctx, s[0].deconv2_w, s[0].deconv2_b, A, 2 * G, 2 * G, false, B, scr, h, h));
+    TRY(conv(ctx, s[0].conv1x1_w, s[0].conv1x1_b, B, 4 * G, 4 * G, A, scr, h, h));
+    TRY(conv(ctx, s[0].conv3x3_w, s[0].conv3x3_b, A, 4 * G, 4 * G, out[0], scr, h, false));
     // scale 1 (2x): deconv, 1x1, 3x3
-    TRY(deconv(ctx, s[1].deconv1_w, s[1].deconv1_b, x, G, G, false, A, scr));
-    TRY(conv(ctx, s[1].conv1x1_w, s[1].conv1x1_b, A, 2 * G, 2 * G, B, scr));
-    TRY(conv(ctx, s[1].conv3x3_w, s[1].conv3x3_b, B, 2 * G, 2 * G, out[1], scr));
+    TRY(deconv(ctx, s[1].deconv1_w, s[1].deconv1_b, x, G, G, false, A, scr, false, h));
+    TRY(conv(ctx, s[1].conv1x1_w, s[1].conv1x1_b, A, 2 * G, 2 * G, B, scr, h, h));
+    TRY(conv(ctx, s[1].conv3x3_w, s[1].conv3x3_b, B, 2 * G, 2 * G, out[1], scr, h, false));
     // scale 2 (1x): 1x1, 3x3
-    TRY(conv(ctx, s[2].conv1x1_w, s[2].conv1x1_b, x, G, G, A, scr));
-    TRY(conv(ctx, s[2].conv3x3_w, s[2].conv3x3_b, A, G, G, out[2], scr));
+    TRY(conv(ctx, s[2].conv1x1_w, s[2].conv1x1_b, x, G, G, A, scr, false, h));
+    TRY(conv(ctx, s[2].conv3x3_w, s[2].conv3x3_b, A, G, G, out[2], scr, h, false));
     // scale 3 (0.5x): max-pool, 1x1, 3x3
     TRY(pool(ctx, x, G, G, E, B));
-    TRY(conv(ctx, s[3].conv1x1_w, s[3].conv1x1_b, B, G / 2, G / 2, A, scr));
-    TRY(conv(ctx, s[3].conv3x3_w, s[3].conv3x3_b, A, G / 2, G / 2, out[3], scr));
+    TRY(conv(ctx, s[3].conv1x1_w, s[3].conv1x1_b, B, G / 2, G / 2, A, scr, false, h));
+    TRY(conv(ctx, s[3].conv3x3_w, s[3].conv3x3_b, A, G / 2, G / 2, out[3], scr, h, false));
 #undef TRY
     return MI355_STATUS_SUCCESS;
 }

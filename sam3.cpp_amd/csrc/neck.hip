@@ -245,12 +245,16 @@ constexpr int CONV_NB = 2;  // stage buffers  // a buffer offset past every oper
 __device__ __forceinline__ int aswz(int r) { return (r >> 1) & 7; }
 }  // namespace
 
-template <int TAPS, int NB>
-__global__ __launch_bounds__(256, NB == 3 ? 2 : 3) void conv_f16_dma_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
+// AH: the map is fp16 already (a producer of this file rounded it, RNE): its rows are 64 bytes
+// per stage, staged and read as the weights are, with no conversion. OH: the output is fp16
+// (the f32 result rounded, RNE), for a map only another of these kernels reads.
+template <int TAPS, int NB, bool AH = false, bool OH = false>
+__global__ __launch_bounds__(256, NB == 3 ? 2 : 3) void conv_f16_dma_kernel(const void* __restrict__ xv, const uint16_t* __restrict__ w,
                                                               const float* __restrict__ bias, int H, int W, int C, int N,
-                                                              int gelu, float* __restrict__ y, int ksplit, int sps,
+                                                              int gelu, void* __restrict__ yv, int ksplit, int sps,
                                                               float* __restrict__ part) {
-    constexpr int NL = 6;  // DMA instructions per wavefront and stage: 4 map, 2 weight
+    constexpr int NL = AH ? 4 : 6;  // DMA instructions per wavefront and stage: 4 (fp16: 2) map, 2 weight
+    constexpr int NA = AH ? 2 : 4;  // map DMA instructions per wavefront and stage
     __shared__ __attribute__((aligned(16))) ConvDmaStage sb[NB];
     const int M = H * W, K = TAPS == 9 ? 9 * C : C, cps = C / 32;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -267,15 +271,17 @@ __global__ __launch_bounds__(256, NB == 3 ? 2 : 3) void conv_f16_dma_kernel(cons
     const int m0 = (tl / tiles_n) * CT, n0 = (tl % tiles_n) * CT;
 
     // map DMA instruction j of wavefront wv: tile rows 8 (4 wv + j) + lane / 8, LDS slot lane % 8,
-    // global chunk slot ^ aswz(row); weight instruction j: rows 16 (2 wv + j) + lane / 4, slot lane % 4
-    const v4i xr = make_rsrc(x, (int64_t)M * C * 4), wr = make_rsrc(w, (int64_t)N * K * 2);
-    int py[4], px[4], ach[4];
+    // global chunk slot ^ aswz(row) (fp16 map: rows 16 (2 wv + j) + lane / 4, slot lane % 4, as
+    // the weights); weight instruction j: rows 16 (2 wv + j) + lane / 4, slot lane % 4
+    constexpr int XES = AH ? 2 : 4;  // map element bytes
+    const v4i xr = make_rsrc(xv, (int64_t)M * C * XES), wr = make_rsrc(w, (int64_t)N * K * 2);
+    int py[NA], px[NA], ach[NA];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int row = 8 * (4 * wv + j) + (lane >> 3), p = m0 + row;
+    for (int j = 0; j < NA; ++j) {
+        const int row = AH ? 16 * (2 * wv + j) + (lane >> 2) : 8 * (4 * wv + j) + (lane >> 3), p = m0 + row;
         py[j] = p < M ? p / W : -(1 << 20);  // past M: every tap lands outside the image
         px[j] = p < M ? p - (p / W) * W : 0;
-        ach[j] = (((lane & 7) ^ aswz(row)) << 4);
+        ach[j] = AH ? (((lane & 3) ^ csw<4>(row)) << 4) : (((lane & 7) ^ aswz(row)) << 4);
     }
     int woff[2];
 #pragma unroll
@@ -290,11 +296,11 @@ __global__ __launch_bounds__(256, NB == 3 ? 2 : 3) void conv_f16_dma_kernel(cons
         const int tap = TAPS == 9 ? s / cps : 0, c0 = (s - tap * cps) * 32;
         const int dy = TAPS == 9 ? tap / 3 - 1 : 0, dx = TAPS == 9 ? tap % 3 - 1 : 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NA; ++j) {
             const int iy = py[j] + dy, ix = px[j] + dx;
             const bool in = iy >= 0 && iy < H && ix >= 0 && ix < W;
-            const int off = in ? ((iy * W + ix) * C + c0) * 4 + ach[j] : CONV_OOB;
-            dma_b128_so(xr, base + (uint32_t)offsetof(ConvDmaStage, A) + 1024u * (4 * wv + j), off, 0);
+            const int off = in ? ((iy * W + ix) * C + c0) * XES + ach[j] : CONV_OOB;
+            dma_b128_so(xr, base + (uint32_t)offsetof(ConvDmaStage, A) + 1024u * (NA * wv + j), off, 0);
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j)
@@ -310,12 +316,17 @@ __global__ __launch_bounds__(256, NB == 3 ? 2 : 3) void conv_f16_dma_kernel(cons
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int ra = wm * 64 + i * 32 + lr, rb = wn * 64 + i * 32 + lr;
-                const int c = 4 * kk + 2 * g;  // the lane's 8 channels: chunks c, c + 1 of its map row
-                const v4f lo = *reinterpret_cast<const v4f*>(&b.A[ra * 32 + ((c ^ aswz(ra)) << 2)]);
-                const v4f hi = *reinterpret_cast<const v4f*>(&b.A[ra * 32 + (((c + 1) ^ aswz(ra)) << 2)]);
-                const uint4 q = {(uint32_t)f2h(lo[0]) | ((uint32_t)f2h(lo[1]) << 16), (uint32_t)f2h(lo[2]) | ((uint32_t)f2h(lo[3]) << 16),
-                                 (uint32_t)f2h(hi[0]) | ((uint32_t)f2h(hi[1]) << 16), (uint32_t)f2h(hi[2]) | ((uint32_t)f2h(hi[3]) << 16)};
-                a[i] = __builtin_bit_cast(v8h, q);
+                if (AH) {
+                    const uint16_t* ah = reinterpret_cast<const uint16_t*>(b.A);
+                    a[i] = *reinterpret_cast<const v8h*>(&ah[ra * 32 + (((2 * kk + g) ^ csw<4>(ra)) << 3)]);
+                } else {
+                    const int c = 4 * kk + 2 * g;  // the lane's 8 channels: chunks c, c + 1 of its map row
+                    const v4f lo = *reinterpret_cast<const v4f*>(&b.A[ra * 32 + ((c ^ aswz(ra)) << 2)]);
+                    const v4f hi = *reinterpret_cast<const v4f*>(&b.A[ra * 32 + (((c + 1) ^ aswz(ra)) << 2)]);
+                    const uint4 q = {(uint32_t)f2h(lo[0]) | ((uint32_t)f2h(lo[1]) << 16), (uint32_t)f2h(lo[2]) | ((uint32_t)f2h(lo[3]) << 16),
+                                     (uint32_t)f2h(hi[0]) | ((uint32_t)f2h(hi[1]) << 16), (uint32_t)f2h(hi[2]) | ((uint32_t)f2h(hi[3]) << 16)};
+                    a[i] = __builtin_bit_cast(v8h, q);
+                }
                 bf[i] = *reinterpret_cast<const v8h*>(&b.B[rb * 32 + (((2 * kk + g) ^ csw<4>(rb)) << 3)]);
             }
 #pragma unroll
@@ -376,7 +387,9 @@ __global__ __launch_bounds__(256, NB == 3 ? 2 : 3) void conv_f16_dma_kernel(cons
                     const int qy = m / W, qx = m - (m / W) * W;
                     const int64_t pix = (int64_t)(2 * qy + (t >> 1)) * (2 * W) + 2 * qx + (t & 1);
                     const float sv = acc[i][j][r] + bv;
-                    y[pix * Cout + co] = gelu ? gelu_erf(sv) : sv;
+                    const float o = gelu ? gelu_erf(sv) : sv;
+                    if (OH) static_cast<uint16_t*>(yv)[pix * Cout + co] = f2h(o);
+                    else static_cast<float*>(yv)[pix * Cout + co] = o;
                 }
         } else {
             const float bv = bias[n];
@@ -385,7 +398,10 @@ __global__ __launch_bounds__(256, NB == 3 ? 2 : 3) void conv_f16_dma_kernel(cons
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                    if (m < M) y[(int64_t)m * N + n] = acc[i][j][r] + bv;
+                    if (m >= M) continue;
+                    const float o = acc[i][j][r] + bv;
+                    if (OH) static_cast<uint16_t*>(yv)[(int64_t)m * N + n] = f2h(o);
+                    else static_cast<float*>(yv)[(int64_t)m * N + n] = o;
                 }
         }
     }
@@ -474,8 +490,8 @@ size_t conv_f16_part_bytes(int taps, int64_t M, int64_t C, int64_t N) {
     return S > 1 ? (size_t)S * (size_t)M * (size_t)N * 4 : 0;
 }
 
-hipError_t launch_conv_f16(int taps, const float* x, const uint16_t* w, const float* bias, int H, int W, int C, int N,
-                           bool gelu, float* y, hipStream_t st, float* part, size_t part_bytes) {
+hipError_t launch_conv_f16(int taps, const void* x, bool x16, const uint16_t* w, const float* bias, int H, int W, int C,
+                           int N, bool gelu, void* y, bool y16, hipStream_t st, float* part, size_t part_bytes) {
     if ((taps != 1 && taps != 4 && taps != 9) || C % 32 != 0 || (reinterpret_cast<uintptr_t>(x) & 15) ||
         (reinterpret_cast<uintptr_t>(w) & 15) || (taps == 4 && N % 4 != 0))
         return hipErrorInvalidValue;
@@ -487,26 +503,39 @@ hipError_t launch_conv_f16(int taps, const float* x, const uint16_t* w, const fl
     if (conv_dma_ok(taps, M, C, N)) {
         // the K split, when the caller gave room for its partial sums
         // (the reduce stores float4 rows: y and part on 16 bytes; N % 4 == 0 in the split choice)
-        const bool y16 = ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(part) |
+        const bool a16 = ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(part) |
                            reinterpret_cast<uintptr_t>(bias)) & 15) == 0;
-        int S = part && y16 ? conv_f16_ksplit(taps, M, C, N) : 1;
+        int S = part && a16 ? conv_f16_ksplit(taps, M, C, N) : 1;
         if ((size_t)S * (size_t)M * (size_t)N * 4 > part_bytes) S = 1;
         const int nst = (taps == 9 ? 9 : 1) * C / 32, sps = (nst + S - 1) / S;
         const unsigned gs = (unsigned)((tiles * S + 7) / 8 * 8);
-        if (taps == 9) conv_f16_dma_kernel<9, CONV_NB><<<gs, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, S, sps, part);
-        else if (taps == 4) conv_f16_dma_kernel<4, CONV_NB><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, 1, nst, nullptr);
-        else conv_f16_dma_kernel<1, CONV_NB><<<gs, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, S, sps, part);
+        // the map formats the neck uses: F32 in and out (the per-op entry points), and in the
+        // fused neck fp16 intermediates (a 3x3 reads one and writes a neck output; a
+        // conv-transpose or 1x1 reads the ViT output, the pool output or one, and writes one)
+        const int f = (x16 ? 2 : 0) + (y16 ? 1 : 0);
+        if (taps == 9 && f == 0) conv_f16_dma_kernel<9, CONV_NB><<<gs, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, S, sps, part);
+        else if (taps == 9 && f == 2) conv_f16_dma_kernel<9, CONV_NB, true, false><<<gs, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, S, sps, part);
+        else if (taps == 4 && f == 0) conv_f16_dma_kernel<4, CONV_NB><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, 1, nst, nullptr);
+        else if (taps == 4 && f == 1) conv_f16_dma_kernel<4, CONV_NB, false, true><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, 1, nst, nullptr);
+        else if (taps == 4 && f == 3) conv_f16_dma_kernel<4, CONV_NB, true, true><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, 1, nst, nullptr);
+        else if (taps == 1 && f == 0) conv_f16_dma_kernel<1, CONV_NB><<<gs, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, S, sps, part);
+        else if (taps == 1 && f == 1) conv_f16_dma_kernel<1, CONV_NB, false, true><<<gs, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, S, sps, part);
+        else if (taps == 1 && f == 3) conv_f16_dma_kernel<1, CONV_NB, true, true><<<gs, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, S, sps, part);
+        else return hipErrorInvalidValue;
         const hipError_t e = hipGetLastError();
         if (S == 1 || e != hipSuccess) return e;
-        return launch_split_reduce(part, S, (int)M, N, bias, y, 4LL * N, st);
+        return launch_split_reduce(part, S, (int)M, N, bias, static_cast<float*>(y), (y16 ? 2LL : 4LL) * N, st, y16);
     }
     // K step 32: a 64-deep step (64 KB of LDS, two workgroups per CU) measured slower
+    if (x16 || y16) return hipErrorInvalidValue;  // fp16 maps: the DMA kernel only
+    const float* xf = static_cast<const float*>(x);
+    float* yf = static_cast<float*>(y);
     if (taps == 9)
-        conv_f16_kernel<9, 32><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
+        conv_f16_kernel<9, 32><<<grid, 256, 0, st>>>(xf, w, bias, H, W, C, N, gl, yf);
     else if (taps == 4)
-        conv_f16_kernel<4, 32><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
+        conv_f16_kernel<4, 32><<<grid, 256, 0, st>>>(xf, w, bias, H, W, C, N, gl, yf);
     else
-        conv_f16_kernel<1, 32><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y);
+        conv_f16_kernel<1, 32><<<grid, 256, 0, st>>>(xf, w, bias, H, W, C, N, gl, yf);
     return hipGetLastError();
 }
 
