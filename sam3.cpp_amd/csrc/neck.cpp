@@ -346,9 +346,13 @@ mi355_status mi355_sam3_neck(mi355_context* ctx, const float* x, int E, int G, c
     // stored as fp16, the values each consumer rounds its F32 input to (the same bits out);
     // the F32 ViT output, the pool output and the four outputs stay F32
     const bool h = fp16_maps(x, E, s);
+    // the conv-transposes run F16 kernels whatever the weight type (ggml casts their kernels
+    // and inputs to F16), so scale 0's first one hands the second an fp16 map whenever both
+    // take the implicit path
+    const bool hd = h || (implicit_ok(x, E) && s[0].deconv1_w->ne[2] % 32 == 0);
     // scale 0 (4x): deconv + GELU, deconv, 1x1, 3x3
-    TRY(deconv(ctx, s[0].deconv1_w, s[0].deconv1_b, x, G, G, true, A, scr, false, h));
-    TRY(deconv(ctx, s[0].deconv2_w, s[0].deconv2_b, A, 2 * G, 2 * G, false, B, scr, h, h));
+    TRY(deconv(ctx, s[0].deconv1_w, s[0].deconv1_b, x, G, G, true, A, scr, false, hd));
+    TRY(deconv(ctx, s[0].deconv2_w, s[0].deconv2_b, A, 2 * G, 2 * G, false, B, scr, hd, h));
     TRY(conv(ctx, s[0].conv1x1_w, s[0].conv1x1_b, B, 4 * G, 4 * G, A, scr, h, h));
     TRY(conv(ctx, s[0].conv3x3_w, s[0].conv3x3_b, A, 4 * G, 4 * G, out[0], scr, h, false));
     // scale 1 (2x): deconv, 1x1, 3x3

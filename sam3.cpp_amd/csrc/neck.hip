@@ -511,13 +511,15 @@ hipError_t launch_conv_f16(int taps, const void* x, bool x16, const uint16_t* w,
         const unsigned gs = (unsigned)((tiles * S + 7) / 8 * 8);
         // the map formats the neck uses: F32 in and out (the per-op entry points), and in the
         // fused neck fp16 intermediates (a 3x3 reads one and writes a neck output; a
-        // conv-transpose or 1x1 reads the ViT output, the pool output or one, and writes one)
+        // conv-transpose or 1x1 reads the ViT output, the pool output or one, and writes one;
+        // with F32 convolution kernels scale 0's second conv-transpose reads one, writes F32)
         const int f = (x16 ? 2 : 0) + (y16 ? 1 : 0);
         if (taps == 9 && f == 0) conv_f16_dma_kernel<9, CONV_NB><<<gs, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, S, sps, part);
         else if (taps == 9 && f == 2) conv_f16_dma_kernel<9, CONV_NB, true, false><<<gs, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, S, sps, part);
         else if (taps == 4 && f == 0) conv_f16_dma_kernel<4, CONV_NB><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, 1, nst, nullptr);
         else if (taps == 4 && f == 1) conv_f16_dma_kernel<4, CONV_NB, false, true><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, 1, nst, nullptr);
         else if (taps == 4 && f == 3) conv_f16_dma_kernel<4, CONV_NB, true, true><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, 1, nst, nullptr);
+        else if (taps == 4 && f == 2) conv_f16_dma_kernel<4, CONV_NB, true, false><<<grid, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, 1, nst, nullptr);
         else if (taps == 1 && f == 0) conv_f16_dma_kernel<1, CONV_NB><<<gs, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, S, sps, part);
         else if (taps == 1 && f == 1) conv_f16_dma_kernel<1, CONV_NB, false, true><<<gs, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, S, sps, part);
         else if (taps == 1 && f == 3) conv_f16_dma_kernel<1, CONV_NB, true, true><<<gs, 256, 0, st>>>(x, w, bias, H, W, C, N, gl, y, S, sps, part);
