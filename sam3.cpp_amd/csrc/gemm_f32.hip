@@ -255,17 +255,29 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_tiled_kernel(const GemmF32Arg
 // inside a stage differs from the tiled kernel's, so sums may differ in the last bits).
 namespace {
 constexpr int F32_OOB = 0x7ffffff0;  // a buffer offset past every operand the launcher admits
-__device__ __forceinline__ int fswz(int r) { return (r >> 1) & 7; }
+// LDS slot of chunk c of tile row r (16-byte chunks, KD / 4 to a row): c ^ fswz<KD>(r). At KD = 32
+// two 128-byte rows share a 256-byte bank line, at KD = 16 four 64-byte rows: the 16 rows of
+// a ds_read_b128 quarter then cover the 64 banks
+template <int KD>
+__device__ __forceinline__ int fswz(int r) { return KD == 32 ? (r >> 1) & 7 : (r >> 2) & 3; }
+template <int KD>
 struct F32Stage {
-    float A[TM * TK];
-    float B[TN * TK];
+    float A[TM * KD];
+    float B[TN * KD];
 };
 }  // namespace
 
-template <bool CONV, int NB>
-__global__ __launch_bounds__(256, NB == 2 ? 2 : 1) void gemm_f32_dma_kernel(const GemmF32Args p, int ksplit, int sps) {
-    constexpr int NL = 8;  // DMA instructions per wavefront and stage: 4 A, 4 B
-    __shared__ __attribute__((aligned(16))) F32Stage sb[NB];
+// KD: K values per stage (32 or 16); NB stage buffers, up to NB - 1 stages in flight past the
+// one computed. sps counts 32-deep stages (the launcher's unit) whatever KD.
+template <bool CONV, int KD, int NB>
+__global__ __launch_bounds__(256, NB * KD * 2 * 128 * 4 <= 54 * 1024 ? 3 : (NB * KD * 2 * 128 * 4 <= 80 * 1024 ? 2 : 1))
+void gemm_f32_dma_kernel(const GemmF32Args p, int ksplit, int sps) {
+    using Stage = F32Stage<KD>;
+    constexpr int CH = KD / 4;        // 16-byte chunks per tile row
+    constexpr int RPI = 64 / CH;      // tile rows per DMA instruction (1 KB)
+    constexpr int NI = TM / RPI / 4;  // DMA instructions per wavefront and operand
+    constexpr int NL = 2 * NI;        // per wavefront and stage
+    __shared__ __attribute__((aligned(16))) Stage sb[NB];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wv & 1, wn = wv >> 1;
@@ -282,17 +294,17 @@ __global__ __launch_bounds__(256, NB == 2 ? 2 : 1) void gemm_f32_dma_kernel(cons
     const char* Wb = reinterpret_cast<const char*>(p.W) + (int64_t)(i12 / p.r2) * p.w_nb2 + (int64_t)(i13 / p.r3) * p.w_nb3;
     const char* Xb = reinterpret_cast<const char*>(p.X) + (int64_t)i12 * p.x_nb2 + (int64_t)i13 * p.x_nb3;
     const int kb = split * sps * TK;
-    const int nst = min((K - kb + TK - 1) / TK, sps);
+    const int nst = min((K - kb + KD - 1) / KD, sps * (TK / KD));
 
-    // DMA instruction j (< 4) of wavefront wv: tile rows 8 (4 wv + j) + lane / 8 of A and of B,
-    // LDS slot lane % 8, global chunk slot ^ fswz(row)
+    // DMA instruction j (< NI) of wavefront wv: tile rows RPI (NI wv + j) + lane / CH of A and of
+    // B, LDS slot lane % CH, global chunk slot ^ fswz(row)
     const v4i xr = make_rsrc(Xb, CONV ? (int64_t)M * p.C * 4 : (int64_t)(M - 1) * p.x_nb1 + 4LL * K);
     const v4i wr = make_rsrc(Wb, (int64_t)(N - 1) * p.w_nb1 + 4LL * K);
-    int ach[4], aoff[4], boff[4], py[4], px[4];
+    int ach[NI], aoff[NI], boff[NI], py[NI], px[NI];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int row = 8 * (4 * wv + j) + (lane >> 3), m = m0 + row, n = n0 + row;
-        ach[j] = (lane & 7) ^ fswz(row);  // the chunk this lane loads
+    for (int j = 0; j < NI; ++j) {
+        const int row = RPI * (NI * wv + j) + lane / CH, m = m0 + row, n = n0 + row;
+        ach[j] = (lane % CH) ^ fswz<KD>(row);  // the chunk this lane loads
         py[j] = px[j] = 0;
         if (CONV) {
             py[j] = m < M ? m / p.Wd : -(1 << 20);  // past M: every tap lands outside the image
@@ -305,9 +317,9 @@ __global__ __launch_bounds__(256, NB == 2 ? 2 : 1) void gemm_f32_dma_kernel(cons
 #pragma unroll
     for (int i = 0; i < NB; ++i) lb[i] = (uint32_t)__builtin_amdgcn_readfirstlane(lds_addr(&sb[i]));
     auto dma = [&](int s, uint32_t base) __attribute__((always_inline)) {
-        const int k0 = kb + s * TK;
+        const int k0 = kb + s * KD;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NI; ++j) {
             const bool kin = k0 + 4 * ach[j] < K;  // false only in a last partial stage
             int off;
             if (CONV) {
@@ -318,30 +330,37 @@ __global__ __launch_bounds__(256, NB == 2 ? 2 : 1) void gemm_f32_dma_kernel(cons
             } else {
                 off = aoff[j] != F32_OOB && kin ? aoff[j] + 4 * k0 : F32_OOB;
             }
-            dma_b128_so(xr, base + (uint32_t)offsetof(F32Stage, A) + 1024u * (4 * wv + j), off, 0);
+            dma_b128_so(xr, base + (uint32_t)offsetof(Stage, A) + 1024u * (NI * wv + j), off, 0);
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NI; ++j) {
             const bool kin = k0 + 4 * ach[j] < K;
             const int off = boff[j] != F32_OOB && kin ? boff[j] + 4 * k0 : F32_OOB;
-            dma_b128_so(wr, base + (uint32_t)offsetof(F32Stage, B) + 1024u * (4 * wv + j), off, 0);
+            dma_b128_so(wr, base + (uint32_t)offsetof(Stage, B) + 1024u * (NI * wv + j), off, 0);
         }
+    };
+    // wait until this wavefront's DMA of all but the last `later` stages issued has landed
+    auto wait_stages = [&](int later) __attribute__((always_inline)) {
+        if (later >= 3) wait_vmcnt<3 * NL>();
+        else if (later == 2) wait_vmcnt<2 * NL>();
+        else if (later == 1) wait_vmcnt<NL>();
+        else wait_vmcnt<0>();
     };
 
     const v16f zf = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     v16f acc[2][2] = {{zf, zf}, {zf, zf}};
-    auto compute = [&](const F32Stage& b) __attribute__((always_inline)) {
-        v4f av[4][2], bv[4][2];
+    auto compute = [&](const Stage& b) __attribute__((always_inline)) {
+        v4f av[CH / 2][2], bv[CH / 2][2];
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+        for (int q = 0; q < CH / 2; ++q)
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int ra = wm * 64 + i * 32 + lr, rb = wn * 64 + i * 32 + lr, c = 2 * q + g;
-                av[q][i] = *reinterpret_cast<const v4f*>(&b.A[ra * TK + ((c ^ fswz(ra)) << 2)]);
-                bv[q][i] = *reinterpret_cast<const v4f*>(&b.B[rb * TK + ((c ^ fswz(rb)) << 2)]);
+                av[q][i] = *reinterpret_cast<const v4f*>(&b.A[ra * KD + ((c ^ fswz<KD>(ra)) << 2)]);
+                bv[q][i] = *reinterpret_cast<const v4f*>(&b.B[rb * KD + ((c ^ fswz<KD>(rb)) << 2)]);
             }
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+        for (int q = 0; q < CH / 2; ++q)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -351,20 +370,17 @@ __global__ __launch_bounds__(256, NB == 2 ? 2 : 1) void gemm_f32_dma_kernel(cons
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q][i][e], bv[q][j][e], acc[i][j], 0, 0, 0);
     };
 
-    // NB buffers filled NB - 1 stages ahead
-    dma(0, lb[0]);
-    if (nst > 1) dma(1, lb[1]);
-    if (NB == 3 && nst > 2) dma(2, lb[NB - 1]);
-    if (NB == 3 && nst > 2) wait_vmcnt<2 * NL>();
-    else if (nst > 1) wait_vmcnt<NL>();
-    else wait_vmcnt<0>();
+    // all NB buffers filled up front; stage s + NB refills stage s's buffer once it is read
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+        if (i < nst) dma(i, lb[i]);
+    wait_stages(min(nst, NB) - 1);
     __syncthreads();
     for (int s = 0; s < nst; ++s) {
         const int cb = s % NB;
         compute(sb[cb]);
         if (s + 1 < nst) {
-            if (NB == 3 && s + 2 < nst) wait_vmcnt<NL>();  // stage s + 1 has landed (s + 2 may be in flight)
-            else wait_vmcnt<0>();
+            wait_stages(min(nst - 1, s + NB - 1) - (s + 1));  // stage s + 1 has landed
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // and stage s's buffer is read
             if (s + NB < nst) dma(s + NB, lb[cb]);
         }
@@ -448,7 +464,7 @@ namespace {
 // operand extents (bytes) the DMA kernel's 32-bit buffer offsets reach, with room for the
 // out-of-range offset
 bool dma_ok(int64_t x_bytes, int64_t w_bytes) { return x_bytes < F32_OOB - 4096 && w_bytes < F32_OOB - 4096; }
-constexpr int F32_NB = 2;  // stage buffers of the DMA kernel
+constexpr int F32_KD = 32, F32_NB = 2;  // K per stage and stage buffers of the DMA kernel
 // the fp32 MFMA kernels split grids below two tiles per CU; one 32-deep stage of a
 // 128 x 128 tile takes about 2.5 us alone on a CU
 int f32_ksplit(int64_t M, int64_t N, int64_t K) {
@@ -499,7 +515,7 @@ hipError_t launch_gemm_f32(const GemmF32Args& a, int Z, hipStream_t st) {
             (reinterpret_cast<uintptr_t>(a.X) & 15) || (reinterpret_cast<uintptr_t>(a.W) & 15) || (a.w_nb1 & 15))
             return hipErrorInvalidValue;
         if (dma_ok((int64_t)a.M * a.C * 4, (int64_t)(a.N - 1) * a.w_nb1 + 4LL * a.K))
-            gemm_f32_dma_kernel<true, F32_NB><<<dim3((unsigned)((tiles * S + 7) / 8 * 8), 1), 256, 0, st>>>(a, S, sps);
+            gemm_f32_dma_kernel<true, F32_KD, F32_NB><<<dim3((unsigned)((tiles * S + 7) / 8 * 8), 1), 256, 0, st>>>(a, S, sps);
         else
             gemm_f32_tiled_kernel<true><<<dim3((unsigned)((tiles * S + 7) / 8 * 8), 1), 256, 0, st>>>(a, S, sps);
         return reduce();
@@ -511,7 +527,7 @@ hipError_t launch_gemm_f32(const GemmF32Args& a, int Z, hipStream_t st) {
     if (tiled) {
         // the DMA kernel's 32-bit buffer offsets must reach every operand of every batch
         if (dma_ok((int64_t)(a.M - 1) * a.x_nb1 + 4LL * a.K, (int64_t)(a.N - 1) * a.w_nb1 + 4LL * a.K))
-            gemm_f32_dma_kernel<false, F32_NB><<<dim3((unsigned)((tiles * S + 7) / 8 * 8), (unsigned)Z), 256, 0, st>>>(a, S, sps);
+            gemm_f32_dma_kernel<false, F32_KD, F32_NB><<<dim3((unsigned)((tiles * S + 7) / 8 * 8), (unsigned)Z), 256, 0, st>>>(a, S, sps);
         else
             gemm_f32_tiled_kernel<false><<<dim3((unsigned)((tiles * S + 7) / 8 * 8), (unsigned)Z), 256, 0, st>>>(a, S, sps);
         return reduce();
