@@ -28,7 +28,7 @@
 // banks (no bank conflicts in rocprofv3's counters).  Two K / V^T buffers:
 // after tile t's MFMAs tile t + 1 goes from registers into the free buffer
 // and tile t + 2's global loads are issued, with one LDS-only barrier per
-// tile.  An fp16 K with D = 64 or 128 (16-byte aligned rows) skips the
+// tile.  An fp16 K with D = 64, 96 or 128 (16-byte aligned rows) skips the
 // registers: right after the barrier that frees its buffer, tile t + 1's K
 // is copied by LDS DMA (buffer_load ... lds) into unpadded rows whose 16-byte
 // chunks are XOR-swizzled by row, and the next barrier waits for it with an
@@ -83,17 +83,22 @@ __device__ __forceinline__ float xsum32(float x) {
 
 // K row slot of 16-byte chunk c in row r of an unpadded fp16 K tile (DMA staging):
 // the 32-row fragment reads of one chunk then fall in distinct bank quads
+// (D = 96: 192-byte rows, four to three bank lines; (r >> 2) & 3 keeps a chunk inside its
+// aligned group of four, so the twelve slots stay twelve)
 template <int D>
-__device__ __forceinline__ int kswz(int r) { return D == 64 ? ((r & 7) ^ ((r >> 3) & 1)) : (r & 15); }
+__device__ __forceinline__ int kswz(int r) { return D == 64 ? ((r & 7) ^ ((r >> 3) & 1)) : D == 96 ? ((r >> 2) & 3) : (r & 15); }
 // V row slot of 16-byte chunk c in row r of an unpadded fp16 V tile (DMA staging): slot
 // c ^ vswz(r).  A transposing read of the PV operand takes 64 bytes (4 chunks 4 db .. +3)
 // from each of 4 consecutive rows per half-wavefront; the 64 banks of 4 bytes then hold each
 // byte once when the 4 rows' chunks land in distinct 64-byte quarters of a 256-byte bank
 // line: D = 64 (128-byte rows: odd rows are the upper bank half) moves rows 2, 3 (mod 4) to
 // the other half of their row's slots and rows 4..7 (mod 8) by one chunk; D = 128 (256-byte
-// rows) moves row r by 4 (r % 4) chunks.
+// rows) moves row r by 4 (r % 4) chunks; D = 96 (192-byte rows) needs none: the 4 rows start
+// at 0, 192, 384 and 576 bytes, so their 64-byte pieces fall in distinct quarters already.
+// (The transposing reads add whole 8-row blocks to a swizzled row offset, so vswz may
+// depend on r % 8 only.)
 template <int D>
-__device__ __forceinline__ int vswz(int r) { return D == 64 ? (((r & 2) << 1) | ((r >> 2) & 1)) : ((r & 3) << 2); }
+__device__ __forceinline__ int vswz(int r) { return D == 64 ? (((r & 2) << 1) | ((r >> 2) & 1)) : D == 96 ? 0 : ((r & 3) << 2); }
 
 // 4 fp16 of LDS by the transposing read of gfx950 (ds_read_b64_tr_b16): within each group
 // of 16 lanes, lane i receives element i % 4 of the 8 bytes addressed by lanes i / 4,
@@ -112,7 +117,7 @@ __device__ __forceinline__ uint2 lds_read_tr16(const void* a) {
 // is software-pipelined; otherwise they pass through registers.
 template <int D, bool QF32, bool KVF32, bool KDMA, int NW = 4, int NBUF = 2>
 __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void fattn_kernel(const FaArgs p) {
-    static_assert(!KDMA || (!KVF32 && (D == 64 || D == 128)), "K/V DMA staging: fp16 K and V, D = 64 or 128");
+    static_assert(!KDMA || (!KVF32 && (D == 64 || D == 96 || D == 128)), "K/V DMA staging: fp16 K and V, D = 64, 96 or 128");
     static_assert((NW == 4 && NBUF == 2) || (!KDMA && NBUF == 1 && (NW == 1 || NW == 2)), "workgroup shape");
     constexpr int NT = 64 * NW, BQ = 32 * NW;  // threads and queries per workgroup
     constexpr int KS = KDMA ? D : D + 8;  // K tile row stride (halves)
@@ -565,28 +570,29 @@ static void fa_launch_d(const FaArgs& a, bool qf32, bool kvf32, int B, hipStream
     const int64_t items = (int64_t)((a.nq + FA_BQ - 1) / FA_BQ) * a.nh * B * a.kv_split;
     const dim3 grid((unsigned)((items + 7) / 8 * 8));
     bool launched = false;
-    if constexpr (D == 64 || D == 128) {
-        // fp16 K and V rows and bases on 16 bytes, key offsets within the 32-bit buffer offset
-        const bool kdma = !kvf32 && reinterpret_cast<uintptr_t>(a.k) % 16 == 0 && a.k_nb1 % 16 == 0 &&
-                          a.k_nb2 % 16 == 0 && a.k_nb3 % 16 == 0 && (int64_t)(a.nkv + FA_BKV) * a.k_nb1 < INT32_MAX &&
-                          reinterpret_cast<uintptr_t>(a.v) % 16 == 0 && a.v_nb1 % 16 == 0 && a.v_nb2 % 16 == 0 &&
-                          a.v_nb3 % 16 == 0 && (int64_t)(a.nkv + FA_BKV) * a.v_nb1 < INT32_MAX;
-        if (kdma) {
-            if (qf32) fattn_kernel<D, true, false, true><<<grid, FA_NT, 0, st>>>(a);
-            else fattn_kernel<D, false, false, true><<<grid, FA_NT, 0, st>>>(a);
-            launched = true;
-        }
-    }
     // windows of at most one key tile and 64 queries, fp16 operands, no key split: one or two
-    // wavefronts per workgroup and one K/V buffer
+    // wavefronts per workgroup and one K/V buffer (taken before the DMA path, which would
+    // give such a window four wavefronts and two buffers)
     const int nw = a.nq <= 32 ? 1 : 2;
-    const bool small = !launched && !qf32 && !kvf32 && a.kv_split == 1 && a.nkv <= FA_BKV && a.nq <= 64;
+    const bool small = !qf32 && !kvf32 && a.kv_split == 1 && a.nkv <= FA_BKV && a.nq <= 64;
     if (small) {
         const int64_t sitems = (int64_t)((a.nq + 32 * nw - 1) / (32 * nw)) * a.nh * B;
         const dim3 sgrid((unsigned)((sitems + 7) / 8 * 8));
         if (nw == 1) fattn_kernel<D, false, false, false, 1, 1><<<sgrid, 64, 0, st>>>(a);
         else fattn_kernel<D, false, false, false, 2, 1><<<sgrid, 128, 0, st>>>(a);
         launched = true;
+    }
+    if constexpr (D == 64 || D == 96 || D == 128) {
+        // fp16 K and V rows and bases on 16 bytes, key offsets within the 32-bit buffer offset
+        const bool kdma = !kvf32 && reinterpret_cast<uintptr_t>(a.k) % 16 == 0 && a.k_nb1 % 16 == 0 &&
+                          a.k_nb2 % 16 == 0 && a.k_nb3 % 16 == 0 && (int64_t)(a.nkv + FA_BKV) * a.k_nb1 < INT32_MAX &&
+                          reinterpret_cast<uintptr_t>(a.v) % 16 == 0 && a.v_nb1 % 16 == 0 && a.v_nb2 % 16 == 0 &&
+                          a.v_nb3 % 16 == 0 && (int64_t)(a.nkv + FA_BKV) * a.v_nb1 < INT32_MAX;
+        if (!launched && kdma) {
+            if (qf32) fattn_kernel<D, true, false, true><<<grid, FA_NT, 0, st>>>(a);
+            else fattn_kernel<D, false, false, true><<<grid, FA_NT, 0, st>>>(a);
+            launched = true;
+        }
     }
     if (launched) {
     } else if (qf32 && kvf32) fattn_kernel<D, true, true, false><<<grid, FA_NT, 0, st>>>(a);

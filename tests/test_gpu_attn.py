@@ -149,7 +149,7 @@ def test_flash_attn_mixed_types_and_scale(mi, ctx, orc):
         _check(orc, got, _f16(q), kh, vh, scale, orc.F16)
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 96, 128])
 def test_flash_attn_k_row_strides(mi, ctx, orc, D):
     """F16 K rows inside wider rows (padding filled with NaN, never read): a row
     stride of 3D halves keeps 16-byte rows (K staged by LDS DMA), D + 2 does not
@@ -166,7 +166,7 @@ def test_flash_attn_k_row_strides(mi, ctx, orc, D):
         assert np.array_equal(got, ref), f"row stride {W}"
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 96, 128])
 def test_flash_attn_k_row_strides_steady_state(mi, ctx, orc, D):
     """The same strided K through the staging loop's steady state: 2048 queries
     x 16 heads fill 256 workgroups, so the keys are not split over workgroups
